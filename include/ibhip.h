@@ -1,0 +1,140 @@
+/*
+ * ibhip.h -- C ABI of libinferbit_amd (libibhip.so): MI355X (gfx950) kernels
+ * for libinferbit's decode-time quantized matvec path.
+ *
+ * Plain C types only: pointers, sizes, ints.  Two layers:
+ *
+ *  1. Device entry points (ibh_*): operands are DEVICE pointers, launches go
+ *     on `stream` (a hipStream_t passed as void*, NULL = the library's
+ *     stream for the current device).  They return INFERBIT_* style codes
+ *     (0 ok, negative error) and leave a message for ibh_last_error().
+ *     They never allocate unless the comment says so.
+ *
+ *  2. Dispatch-table entries (ib_init_kernels_hip): the exact signatures of
+ *     the reference's `ib_kernels` table (src/inferbit_internal.h:199-277),
+ *     taking HOST pointers, so a reference build can swap its CPU kernels
+ *     for these without touching its callers.  Weight pointers that fall in
+ *     a region registered with ibh_register_host_weights() are served from
+ *     the resident device copy; other pointers are uploaded per call.
+ *
+ * Reference paths (file:line) are relative to the libinferbit repository.
+ */
+#ifndef IBHIP_H
+#define IBHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Error codes: same values as include/inferbit.h:43-49. */
+#define IBH_OK              0
+#define IBH_ERROR_LOAD     -1
+#define IBH_ERROR_FORMAT   -2
+#define IBH_ERROR_MEMORY   -3
+#define IBH_ERROR_CONTEXT  -4
+#define IBH_ERROR_PARAM    -5
+#define IBH_ERROR_INTERNAL -6
+
+/* Scale operand encodings.  IBF stores per-row weight scales as fp16
+ * (src/quantize.c:104-106); the dispatch table passes fp32
+ * (src/forward.c:152-156). */
+#define IBH_SCALE_F16 0
+#define IBH_SCALE_F32 1
+
+/* ── runtime ───────────────────────────────────────────────── */
+
+/* Selects `device`, creates the library stream for it.  Idempotent.
+ * Replaces nothing in the reference (it has no device); the reference's
+ * ibf_load (src/ibf_loader.c:539-543) is where it would be called. */
+int         ibh_init(int device);
+/* Last error message of the calling thread, cleared on read (NULL if none);
+ * same convention as inferbit_last_error (src/error.c:17-21). */
+const char* ibh_last_error(void);
+const char* ibh_version(void);
+void*       ibh_default_stream(void);
+int         ibh_synchronize(void* stream);
+int         ibh_device_malloc(void** dptr, size_t bytes);
+int         ibh_device_free(void* dptr);
+int         ibh_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream);
+int         ibh_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream);
+int         ibh_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
+
+/* ── quantized matvec, device pointers ─────────────────────── */
+
+/* out[M] = scales[i] * sum_j dequant(W[i, j]) * x[j], bits 8 / 4 / 2,
+ * fp32 activations.  W row-major packed as the IBF v1 file stores it:
+ * int8 [M][N]; int4 [M][N/2] (byte k = col 2k low nibble, 2k+1 high nibble,
+ * biased by 8); int2 [M][N/4] (codes 0/1/2 = -1/0/+1, col 4k+i at bits 2i).
+ * Replaces ib_parallel_matmul (src/threading.c:244-258) and the table
+ * entries matmul_int8/int4/int2 (src/kernels/scalar.c:9-41,
+ * src/kernels/ternary.c:20-46, src/kernels/avx2.c:17-149).
+ * fp32 accumulation; summation order differs from the CPU's. */
+int ibh_matmul(float* out, const void* w, const void* scales, int scale_kind,
+               const float* x, int M, int N, int bits, void* stream);
+
+/* Per-128-group int8 activation quantization, bit-identical to
+ * ib_quantize_input_int8_g128 (src/threading.c:401-432).  q[N], s[ceil(N/128)]. */
+int ibh_quantize_act_g128(const float* x, int8_t* q, float* s, int N, void* stream);
+
+/* INT4 weights x INT8 activations with 128-group activation scales,
+ * bit-identical to the x86 kernel (src/kernels/avx2.c:285-352): exact int32
+ * group dots, groups folded in order with an fp32 FMA, times the row scale.
+ * Replaces ib_parallel_matmul_w4a8 (src/threading.c:283-294). */
+int ibh_matmul_w4a8(float* out, const void* w, const void* scales, int scale_kind,
+                    const int8_t* qx, const float* sa, int M, int N, void* stream);
+
+/* ib_quantize_input_int8_g128 + ib_parallel_matmul_w4a8 as tensor_matmul
+ * issues them for INT4 tensors (src/forward.c:158-172).  `qx_ws` (N bytes)
+ * and `sa_ws` (ceil(N/128) floats) are caller-provided device workspace. */
+int ibh_matmul_w4a8_x(float* out, const void* w, const void* scales, int scale_kind,
+                      const float* x, int M, int N, int8_t* qx_ws, float* sa_ws, void* stream);
+
+/* Batched forms, out[b*M_stride + i] (src/inferbit_internal.h:242-276).
+ * ibh_matmul_w4a8_batch is bit-identical to the x86 build's scalar kernel
+ * (src/kernels/scalar.c:86-124: per-group multiply and add rounded apart);
+ * ibh_matmul_int8_batch follows src/kernels/scalar.c:70-84 within fp32
+ * tolerance.  B <= 32 (IB_BATCH_MAX, src/inferbit_internal.h:287). */
+int ibh_matmul_w4a8_batch(float* out, const void* w, const void* scales, int scale_kind,
+                          const int8_t* qx, const float* sa, int M, int N, int B,
+                          int M_stride, void* stream);
+int ibh_matmul_int8_batch(float* out, const void* w, const void* scales, int scale_kind,
+                          const float* x, int M, int N, int B, int M_stride, void* stream);
+
+/* ── dispatch-table boundary (host pointers) ───────────────── */
+
+/* Layout-identical mirror of the reference's `ib_kernels`
+ * (src/inferbit_internal.h:199-277); a reference build passes &ib_kern. */
+typedef struct {
+    void (*matmul_int4)(float*, const void*, const float*, const float*, int, int);
+    void (*matmul_int8)(float*, const void*, const float*, const float*, int, int);
+    void (*matmul_int2)(float*, const void*, const float*, const float*, int, int);
+    void (*rmsnorm)(float*, const float*, const float*, float, int);
+    void (*rope)(float*, float*, int, int, float);
+    void (*softmax)(float*, int);
+    void (*silu_mul)(float*, const float*, const float*, int);
+    void (*matmul_w4a8)(float*, const void*, const float*, const int8_t*, const float*, int, int);
+    void (*matmul_w4a8_batch)(float*, const void*, const float*, const int8_t*, const float*,
+                              int, int, int, int);
+    void (*matmul_int8_batch)(float*, const void*, const float*, const float*, int, int, int, int);
+} ibh_kernels;
+
+/* Registers the GPU matmul entries into `kern`, mirroring
+ * ib_init_kernels_avx2 (src/kernels/avx2.c:356-364).  Elementwise entries
+ * (rmsnorm, rope, softmax, silu_mul) are left as they are.  Call after
+ * every ib_init_kernels (src/ibf_loader.c:539-540 re-initialises the
+ * table on each load). */
+void ib_init_kernels_hip(ibh_kernels* kern);
+
+/* Uploads [host_base, host_base+bytes) once (e.g. the model's mmap'd
+ * weight_data, src/ibf_loader.c:500) and serves table calls whose weight
+ * pointer falls inside it from the device copy.  Returns the device base. */
+int  ibh_register_host_weights(const void* host_base, size_t bytes, void** dev_base);
+void ibh_unregister_host_weights(const void* host_base);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* IBHIP_H */

@@ -1,0 +1,674 @@
+/*
+ * ib_oracle.c -- CPU restatement of libinferbit's decode-time quantized
+ * matvec path.  TEST INFRASTRUCTURE ONLY (see ib_oracle.h): the checker for
+ * the HIP library, never part of the product.
+ *
+ * Build: gcc -std=gnu11 -O2 -ffp-contract=off (oracle/Makefile).  With
+ * contraction off, every a*b+c below is two roundings unless written as
+ * fmaf(), which marks the places where the x86 reference build (avx2.c and
+ * pq_decode.c compiled with -mavx2 -mfma, gnu11 => -ffp-contract=fast)
+ * fuses the multiply-add.  Sources without -mfma (scalar.c, ternary.c,
+ * forward.c, threading.c, quantize.c) cannot fuse on x86-64 and are
+ * restated with separate roundings.
+ */
+#include "ib_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ── fp16 ───────────────────────────────────────────────────── */
+
+/* IEEE binary16 -> binary32, exact.  forward.c:38-70 (same result as
+ * pq_decode.c:263-288 and quantize.c:16-30). */
+float or_fp16_to_fp32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    int e = (h >> 10) & 0x1f;
+    uint32_t m = h & 0x3ffu;
+    uint32_t bits;
+    if (e == 0x1f) {
+        bits = sign | 0x7f800000u | (m << 13);
+    } else if (e == 0) {
+        if (m == 0) {
+            bits = sign;
+        } else {                       /* subnormal: renormalise */
+            int shift = 0;
+            while (!(m & 0x400u)) { m <<= 1; shift++; }
+            m &= 0x3ffu;
+            bits = sign | ((uint32_t)(113 - shift) << 23) | (m << 13);
+        }
+    } else {
+        bits = sign | ((uint32_t)(e + 112) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* Truncating fp32 -> fp16 used for per-row weight scales: the mantissa is
+ * cut (no rounding), exponents below the fp16 normal range give a signed
+ * zero, overflow gives infinity.  quantize.c:32-41. */
+uint16_t or_fp32_to_fp16_trunc(float f) {
+    uint32_t b;
+    memcpy(&b, &f, 4);
+    uint16_t sign = (uint16_t)((b >> 16) & 0x8000u);
+    int e = (int)((b >> 23) & 0xff) - 112;          /* rebias 127 -> 15 */
+    if (e <= 0) return sign;
+    if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+    return (uint16_t)(sign | (e << 10) | ((b & 0x7fffffu) >> 13));
+}
+
+/* Round-to-nearest-even fp32 -> fp16 with subnormals.  pq_decode.c:305-337. */
+uint16_t or_fp32_to_fp16_rne(float f) {
+    uint32_t b;
+    memcpy(&b, &f, 4);
+    uint32_t sign = (b >> 16) & 0x8000u;
+    int e = (int)((b >> 23) & 0xff) - 112;
+    uint32_t m = b & 0x7fffffu;
+    if (e >= 31) {                                   /* inf / nan / overflow */
+        return (uint16_t)(sign | 0x7c00u | (((b >> 23) & 0xff) == 0xff && m ? 0x200u : 0u));
+    }
+    if (e <= 0) {
+        if (e < -10) return (uint16_t)sign;
+        m = (m | 0x800000u) >> (1 - e);
+        uint32_t rest = m & 0x1fffu, keep = m >> 13;
+        if (rest > 0x1000u || (rest == 0x1000u && (keep & 1u))) keep++;
+        return (uint16_t)(sign | keep);
+    }
+    uint32_t rest = m & 0x1fffu, keep = m >> 13;
+    if (rest > 0x1000u || (rest == 0x1000u && (keep & 1u))) keep++;
+    if (keep == 0x400u) {                            /* mantissa carried out */
+        keep = 0;
+        e++;
+        if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+    }
+    return (uint16_t)(sign | ((uint32_t)e << 10) | keep);
+}
+
+/* ── weight quantizers (F32 source) ─────────────────────────── */
+
+static float row_absmax(const float* r, int n) {
+    float mx = 0.0f;
+    for (int c = 0; c < n; c++) { float a = fabsf(r[c]); if (a > mx) mx = a; }
+    return mx;
+}
+
+/* quantize.c:75-115: per-row scale = absmax/127 floored at 6.104e-05,
+ * stored as truncated fp16; q = roundf(w * (1/scale)) clamped to +-127. */
+void or_quantize_int8(int8_t* w, uint16_t* s, const float* src, int rows, int cols) {
+    for (int r = 0; r < rows; r++) {
+        const float* row = src + (size_t)r * cols;
+        float sc = row_absmax(row, cols) / 127.0f;
+        if (sc < 6.104e-05f) sc = 6.104e-05f;
+        float inv = 1.0f / sc;
+        s[r] = or_fp32_to_fp16_trunc(sc);
+        for (int c = 0; c < cols; c++) {
+            int q = (int)roundf(row[c] * inv);
+            q = q < -127 ? -127 : (q > 127 ? 127 : q);
+            w[(size_t)r * cols + c] = (int8_t)q;
+        }
+    }
+}
+
+/* quantize.c:119-165: scale = absmax/7; values clamped to +-7 and stored
+ * biased by 8; byte k of a row holds column 2k in bits 0-3 and column 2k+1
+ * in bits 4-7. */
+void or_quantize_int4(uint8_t* w, uint16_t* s, const float* src, int rows, int cols) {
+    int rb = cols / 2;
+    for (int r = 0; r < rows; r++) {
+        const float* row = src + (size_t)r * cols;
+        float sc = row_absmax(row, cols) / 7.0f;
+        if (sc < 6.104e-05f) sc = 6.104e-05f;
+        float inv = 1.0f / sc;
+        s[r] = or_fp32_to_fp16_trunc(sc);
+        for (int c = 0; c < cols; c += 2) {
+            int q0 = (int)roundf(row[c] * inv);
+            int q1 = (c + 1 < cols) ? (int)roundf(row[c + 1] * inv) : 0;
+            q0 = q0 < -7 ? -7 : (q0 > 7 ? 7 : q0);
+            q1 = q1 < -7 ? -7 : (q1 > 7 ? 7 : q1);
+            if (c / 2 < rb)
+                w[(size_t)r * rb + c / 2] = (uint8_t)(((q0 + 8) & 0xf) | (((q1 + 8) & 0xf) << 4));
+        }
+    }
+}
+
+/* quantize.c:169-239: ternary (TWN) quantizer.  threshold = 0.7*mean|w|;
+ * scale = mean of the |w| above threshold; codes 0/1/2 for -1/0/+1, four
+ * per byte starting at bit 0. */
+void or_quantize_int2(uint8_t* w, uint16_t* s, const float* src, int rows, int cols) {
+    int rb = cols / 4;
+    for (int r = 0; r < rows; r++) {
+        const float* row = src + (size_t)r * cols;
+        float sum_abs = 0.0f;
+        for (int c = 0; c < cols; c++) sum_abs += fabsf(row[c]);
+        float mean_abs = sum_abs / (float)cols;
+        float th = 0.7f * mean_abs;
+        float kept = 0.0f;
+        int nk = 0;
+        for (int c = 0; c < cols; c++) {
+            if (fabsf(row[c]) > th) { kept += fabsf(row[c]); nk++; }
+        }
+        float sc = nk > 0 ? kept / (float)nk : (mean_abs > 0 ? mean_abs : 6.104e-05f);
+        if (sc < 6.104e-05f) sc = 6.104e-05f;
+        s[r] = or_fp32_to_fp16_trunc(sc);
+        for (int c = 0; c < cols; c += 4) {
+            unsigned byte = 0;
+            for (int k = 0; k < 4 && c + k < cols; k++) {
+                float v = row[c + k];
+                unsigned code = v > th ? 2u : (v < -th ? 0u : 1u);
+                byte |= code << (2 * k);
+            }
+            if (c / 4 < rb) w[(size_t)r * rb + c / 4] = (uint8_t)byte;
+        }
+    }
+}
+
+/* threading.c:401-432: per-128-group symmetric int8 quantization of the
+ * activation.  scale = absmax/127 (groups with absmax < 1e-10 get scale
+ * 1e-10 and zero codes); q = (int)(v*inv +- 0.5) truncated toward zero,
+ * clamped to +-127.  The multiply and the add round separately. */
+int or_quantize_act_g128(const float* x, int8_t* q, float* s, int N) {
+    int g = 0;
+    for (int b = 0; b < N; b += 128, g++) {
+        int e = b + 128 < N ? b + 128 : N;
+        float mx = 0.0f;
+        for (int i = b; i < e; i++) { float a = x[i] < 0 ? -x[i] : x[i]; if (a > mx) mx = a; }
+        if (mx < 1e-10f) {
+            s[g] = 1e-10f;
+            for (int i = b; i < e; i++) q[i] = 0;
+            continue;
+        }
+        float sc = mx / 127.0f;
+        float inv = 1.0f / sc;
+        s[g] = sc;
+        for (int i = b; i < e; i++) {
+            float t = x[i] * inv;
+            int v = (int)(t + (x[i] >= 0 ? 0.5f : -0.5f));
+            v = v < -127 ? -127 : (v > 127 ? 127 : v);
+            q[i] = (int8_t)v;
+        }
+    }
+    return g;
+}
+
+/* ── matvec ─────────────────────────────────────────────────── */
+
+/* Horizontal reduction of the two 8-lane AVX2 accumulators:
+ * (acc0+acc1) lane-wise, fold upper 128 bits onto lower, then two hadds.
+ * avx2.c:52-59 / :121-128. */
+static float avx2_fold(const float a0[8], const float a1[8]) {
+    float s8[8], s4[4];
+    for (int l = 0; l < 8; l++) s8[l] = a0[l] + a1[l];
+    for (int l = 0; l < 4; l++) s4[l] = s8[l] + s8[l + 4];
+    float h0 = s4[0] + s4[1], h1 = s4[2] + s4[3];
+    return h0 + h1;
+}
+
+static inline float w4(const uint8_t* row, int j) {
+    uint8_t b = row[j >> 1];
+    return (float)((int)((j & 1) ? (b >> 4) : (b & 0xf)) - 8);
+}
+
+/* order 0: scalar.c:29-41 (serial sum, mul then add).
+ * order 1: avx2.c:17-68 (two 8-lane FMA accumulators over 16-column
+ * blocks, avx2_fold, then a serial FMA tail). */
+void or_matmul_int8(float* out, const int8_t* w, const float* sc, const float* x,
+                    int M, int N, int order) {
+    for (int i = 0; i < M; i++) {
+        const int8_t* row = w + (size_t)i * N;
+        float r;
+        if (order == 0) {
+            r = 0.0f;
+            for (int j = 0; j < N; j++) r = r + (float)row[j] * x[j];
+        } else {
+            float a0[8] = {0}, a1[8] = {0};
+            int j = 0;
+            for (; j + 15 < N; j += 16)
+                for (int l = 0; l < 8; l++) {
+                    a0[l] = fmaf((float)row[j + l], x[j + l], a0[l]);
+                    a1[l] = fmaf((float)row[j + 8 + l], x[j + 8 + l], a1[l]);
+                }
+            r = avx2_fold(a0, a1);
+            for (; j < N; j++) r = fmaf((float)row[j], x[j], r);
+        }
+        out[i] = r * sc[i];
+    }
+}
+
+/* order 0: scalar.c:9-27.  order 1: avx2.c:72-149 (same lane structure as
+ * the int8 kernel; the tail walks column pairs). */
+void or_matmul_int4(float* out, const uint8_t* w, const float* sc, const float* x,
+                    int M, int N, int order) {
+    for (int i = 0; i < M; i++) {
+        const uint8_t* row = w + (size_t)i * (N / 2);
+        float r;
+        if (order == 0) {
+            r = 0.0f;
+            for (int j = 0; j < N; j++) r = r + w4(row, j) * x[j];
+        } else {
+            float a0[8] = {0}, a1[8] = {0};
+            int j = 0;
+            for (; j + 15 < N; j += 16)
+                for (int l = 0; l < 8; l++) {
+                    a0[l] = fmaf(w4(row, j + l), x[j + l], a0[l]);
+                    a1[l] = fmaf(w4(row, j + 8 + l), x[j + 8 + l], a1[l]);
+                }
+            r = avx2_fold(a0, a1);
+            for (; j < N; j++) r = fmaf(w4(row, j), x[j], r);
+        }
+        out[i] = r * sc[i];
+    }
+}
+
+/* ternary.c:20-46 (the x86 registration, :162-168, always picks this
+ * scalar kernel).  Codes 0/1/2(/3) decode to -1/0/+1(/+2). */
+void or_matmul_int2(float* out, const uint8_t* w, const float* sc, const float* x, int M, int N) {
+    for (int i = 0; i < M; i++) {
+        const uint8_t* row = w + (size_t)i * (N / 4);
+        float r = 0.0f;
+        for (int j = 0; j < N; j++) {
+            int code = (row[j >> 2] >> (2 * (j & 3))) & 3;
+            r = r + (float)(code - 1) * x[j];
+        }
+        out[i] = r * sc[i];
+    }
+}
+
+/* Exact int32 dot of one 128-column group (or the shorter tail group). */
+static int32_t w4a8_group(const uint8_t* row, const int8_t* qx, int j0, int j1) {
+    int32_t s = 0;
+    for (int j = j0; j < j1; j++) {
+        uint8_t b = row[j >> 1];
+        int v = (int)((j & 1) ? (b >> 4) : (b & 0xf)) - 8;
+        s += v * (int32_t)qx[j];
+    }
+    return s;
+}
+
+/* order 1: avx2.c:285-352 -- groups g = 0..G-1 in order,
+ * row_acc = fma((float)isum_g, sa[g], row_acc); out = row_acc * sw.
+ * order 0: scalar.c:43-68 -- same with the multiply and add rounded apart. */
+void or_matmul_w4a8(float* out, const uint8_t* w, const float* sw, const int8_t* qx,
+                    const float* sa, int M, int N, int order) {
+    for (int i = 0; i < M; i++) {
+        const uint8_t* row = w + (size_t)i * (N / 2);
+        float acc = 0.0f;
+        int g = 0;
+        for (int j = 0; j < N; j += 128, g++) {
+            int e = j + 128 < N ? j + 128 : N;
+            float f = (float)w4a8_group(row, qx, j, e);
+            acc = order ? fmaf(f, sa[g], acc) : acc + f * sa[g];
+        }
+        out[i] = acc * sw[i];
+    }
+}
+
+/* scalar.c:70-84 (x86 keeps the scalar batched kernel: avx2.c:356-364 does
+ * not override it).  out[b*M_stride + i]. */
+void or_matmul_int8_batch(float* out, const int8_t* w, const float* sw, const float* x,
+                          int M, int N, int B, int M_stride) {
+    for (int i = 0; i < M; i++) {
+        const int8_t* row = w + (size_t)i * N;
+        for (int b = 0; b < B; b++) {
+            const float* xb = x + (size_t)b * N;
+            float r = 0.0f;
+            for (int j = 0; j < N; j++) r = r + (float)row[j] * xb[j];
+            out[(size_t)b * M_stride + i] = r * sw[i];
+        }
+    }
+}
+
+/* scalar.c:86-124: per batch column b, groups accumulate
+ * row_acc[b] = row_acc[b] + (float)isum * sa[b*groups + g] (two roundings). */
+void or_matmul_w4a8_batch(float* out, const uint8_t* w, const float* sw, const int8_t* qx,
+                          const float* sa, int M, int N, int B, int M_stride) {
+    int groups = (N + 127) / 128;
+    for (int i = 0; i < M; i++) {
+        const uint8_t* row = w + (size_t)i * (N / 2);
+        for (int b = 0; b < B; b++) {
+            const int8_t* qb = qx + (size_t)b * N;
+            float acc = 0.0f;
+            int g = 0;
+            for (int j = 0; j < N; j += 128, g++) {
+                int e = j + 128 < N ? j + 128 : N;
+                acc = acc + (float)w4a8_group(row, qb, j, e) * sa[(size_t)b * groups + g];
+            }
+            out[(size_t)b * M_stride + i] = acc * sw[i];
+        }
+    }
+}
+
+/* ── KV cache + attention ───────────────────────────────────── */
+
+/* forward.c:352-413.  Layout per layer: K and V rows [capacity][row] with
+ * row = kv_dim fp32 (bits 16/32), kv_dim int8 (bits 8) or (kv_dim+1)/2
+ * packed bytes (bits 4, head h at byte h*((head_dim+1)/2)); scales fp32
+ * [capacity][n_kv].  int8: scale = max|.|/127 floored at 1e-8, q =
+ * roundf(v*(1/scale)) clamped +-127.  int4: /7, clamp +-7, biased by 8,
+ * low nibble = even dim. */
+void or_kv_write(void* kdata, void* vdata, float* kscales, float* vscales, int pos,
+                 const float* k, const float* v, int n_kv, int hd, int bits) {
+    int kv_dim = n_kv * hd;
+    if (bits >= 16) {
+        memcpy((float*)kdata + (size_t)pos * kv_dim, k, (size_t)kv_dim * 4);
+        memcpy((float*)vdata + (size_t)pos * kv_dim, v, (size_t)kv_dim * 4);
+        return;
+    }
+    for (int side = 0; side < 2; side++) {
+        const float* src = side ? v : k;
+        void* dst = side ? vdata : kdata;
+        float* scl = side ? vscales : kscales;
+        for (int h = 0; h < n_kv; h++) {
+            const float* x = src + (size_t)h * hd;
+            float mx = row_absmax(x, hd);
+            float qmax = bits == 8 ? 127.0f : 7.0f;
+            float sc = mx / qmax;
+            if (sc < 1e-8f) sc = 1e-8f;
+            scl[(size_t)pos * n_kv + h] = sc;
+            float inv = 1.0f / sc;
+            if (bits == 8) {
+                int8_t* d = (int8_t*)dst + (size_t)pos * kv_dim + (size_t)h * hd;
+                for (int i = 0; i < hd; i++) {
+                    int q = (int)roundf(x[i] * inv);
+                    d[i] = (int8_t)(q < -127 ? -127 : (q > 127 ? 127 : q));
+                }
+            } else {
+                size_t rowb = (size_t)(kv_dim + 1) / 2;
+                uint8_t* d = (uint8_t*)dst + (size_t)pos * rowb + (size_t)h * ((hd + 1) / 2);
+                for (int i = 0; i < hd; i += 2) {
+                    int q0 = (int)roundf(x[i] * inv);
+                    int q1 = i + 1 < hd ? (int)roundf(x[i + 1] * inv) : 0;
+                    q0 = q0 < -7 ? -7 : (q0 > 7 ? 7 : q0);
+                    q1 = q1 < -7 ? -7 : (q1 > 7 ? 7 : q1);
+                    d[i / 2] = (uint8_t)(((q0 + 8) & 0xf) | (((q1 + 8) & 0xf) << 4));
+                }
+            }
+        }
+    }
+}
+
+/* forward.c:415-445: dequantized head row = (float)code * scale. */
+static void kv_read(float* o, const void* data, const float* scales, int t, int h,
+                    int n_kv, int hd, int bits) {
+    int kv_dim = n_kv * hd;
+    if (bits >= 16) {
+        memcpy(o, (const float*)data + (size_t)t * kv_dim + (size_t)h * hd, (size_t)hd * 4);
+        return;
+    }
+    float sc = scales[(size_t)t * n_kv + h];
+    if (bits == 8) {
+        const int8_t* r = (const int8_t*)data + (size_t)t * kv_dim + (size_t)h * hd;
+        for (int d = 0; d < hd; d++) o[d] = (float)r[d] * sc;
+    } else {
+        const uint8_t* r = (const uint8_t*)data + (size_t)t * ((kv_dim + 1) / 2) + (size_t)h * ((hd + 1) / 2);
+        for (int d = 0; d < hd; d++) {
+            uint8_t b = r[d >> 1];
+            o[d] = (float)((int)((d & 1) ? (b >> 4) : (b & 0xf)) - 8) * sc;
+        }
+    }
+}
+
+/* avx2.c:192-229: max, then e_i = expf(x_i - max) summed serially, then
+ * every e_i multiplied by 1/sum.  Lane-parallel max and the vector multiply
+ * give the same values as this serial form. */
+void or_softmax(float* d, int n) {
+    float mx = d[0];
+    for (int i = 1; i < n; i++) if (d[i] > mx) mx = d[i];
+    float s = 0.0f;
+    for (int i = 0; i < n; i++) { d[i] = expf(d[i] - mx); s = s + d[i]; }
+    float inv = 1.0f / s;
+    for (int i = 0; i < n; i++) d[i] = d[i] * inv;
+}
+
+/* forward.c:449-504 for all heads of one layer at position pos (the cache
+ * already holds positions 0..pos).  Head h reads KV head h/(n_heads/n_kv);
+ * score_t = (q.k_t) * (1/sqrtf(hd)) with a serial dot; softmax; out =
+ * sum_t a_t * v_t accumulated serially in t.  att_scratch holds pos+1
+ * floats. */
+void or_attn_decode(float* out, float* att, const float* q,
+                    const void* kdata, const void* vdata, const float* ks, const float* vs,
+                    int pos, int n_heads, int n_kv, int hd, int bits) {
+    float tmp[1024];
+    float scale = 1.0f / sqrtf((float)hd);
+    int grp = n_heads / n_kv;
+    for (int h = 0; h < n_heads; h++) {
+        const float* qh = q + (size_t)h * hd;
+        int kh = h / grp;
+        for (int t = 0; t <= pos; t++) {
+            kv_read(tmp, kdata, ks, t, kh, n_kv, hd, bits);
+            float s = 0.0f;
+            for (int d = 0; d < hd; d++) s = s + qh[d] * tmp[d];
+            att[t] = s * scale;
+        }
+        or_softmax(att, pos + 1);
+        float* oh = out + (size_t)h * hd;
+        for (int d = 0; d < hd; d++) oh[d] = 0.0f;
+        for (int t = 0; t <= pos; t++) {
+            kv_read(tmp, vdata, vs, t, kh, n_kv, hd, bits);
+            float a = att[t];
+            for (int d = 0; d < hd; d++) oh[d] = oh[d] + a * tmp[d];
+        }
+    }
+}
+
+/* ── decode-layer helpers ───────────────────────────────────── */
+
+/* avx2.c:153-188: sum of squares in 8 FMA lanes + fold + FMA tail;
+ * scale = 1/sqrtf(ss/N + eps); out = (x*scale)*w. */
+void or_rmsnorm(float* out, const float* x, const float* w, float eps, int N) {
+    float a[8] = {0};
+    int i = 0;
+    for (; i + 7 < N; i += 8)
+        for (int l = 0; l < 8; l++) a[l] = fmaf(x[i + l], x[i + l], a[l]);
+    float s4[4];
+    for (int l = 0; l < 4; l++) s4[l] = a[l] + a[l + 4];
+    float ss = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+    for (; i < N; i++) ss = fmaf(x[i], x[i], ss);
+    float sc = 1.0f / sqrtf(ss / (float)N + eps);
+    for (int j = 0; j < N; j++) out[j] = (x[j] * sc) * w[j];
+}
+
+/* scalar.c:140-157: pairs (2i, 2i+1) rotated by pos * theta^(-2i/hd). */
+void or_rope(float* q, float* k, int hd, int pos, float theta) {
+    for (int i = 0; i < hd; i += 2) {
+        float freq = 1.0f / powf(theta, (float)i / (float)hd);
+        float ang = (float)pos * freq;
+        float c = cosf(ang), s = sinf(ang);
+        float q0 = q[i], q1 = q[i + 1];
+        q[i] = q0 * c - q1 * s;
+        q[i + 1] = q0 * s + q1 * c;
+        float k0 = k[i], k1 = k[i + 1];
+        k[i] = k0 * c - k1 * s;
+        k[i + 1] = k0 * s + k1 * c;
+    }
+}
+
+/* avx2.c:233-251: silu(g) = g / (1 + expf(-g)); out = silu * u. */
+void or_silu_mul(float* out, const float* g, const float* u, int N) {
+    for (int i = 0; i < N; i++) {
+        float x = g[i];
+        out[i] = (x / (1.0f + expf(-x))) * u[i];
+    }
+}
+
+/* ── product quantization ───────────────────────────────────── */
+
+static int pq_l2_at(const or_pq_tensor* t, const uint8_t* row, int c) {
+    int K2 = t->K_l2 > 0 ? t->K_l2 : t->K;
+    if (K2 == 16) { uint8_t b = row[c >> 1]; return (c & 1) ? (b >> 4) : (b & 0xf); }
+    if (t->l2_idx_bytes == 2) { uint16_t v; memcpy(&v, row + 2 * c, 2); return v; }
+    return row[c];
+}
+
+static size_t pq_l2_stride(const or_pq_tensor* t) {
+    int K2 = t->K_l2 > 0 ? t->K_l2 : t->K;
+    if (K2 == 16) return (size_t)(t->C + 1) / 2;
+    return (size_t)t->C * (t->l2_idx_bytes == 2 ? 2 : 1);
+}
+
+static int* pq_inner_cols(const or_pq_tensor* t) {
+    int* ic = (int*)malloc(sizeof(int) * (size_t)(t->N - t->n_outlier));
+    uint8_t* mk = (uint8_t*)calloc((size_t)t->N, 1);
+    for (int i = 0; i < t->n_outlier; i++) mk[t->ocols[i]] = 1;
+    int k = 0;
+    for (int j = 0; j < t->N; j++) if (!mk[j]) ic[k++] = j;
+    free(mk);
+    return ic;
+}
+
+/* pq_decode.c:1103-1196: W[r, col] = fp16_rne(codebook value (+ L2
+ * residual) * row_scale) widened back to fp32; outlier columns =
+ * fp16_rne(sidecar * col_scale). */
+int or_pq_reconstruct(const or_pq_tensor* t, float* out) {
+    int M = t->M, N = t->N, G = t->G, C = t->C, hf = G / 2;
+    int* ic = pq_inner_cols(t);
+    size_t l2s = pq_l2_stride(t);
+    memset(out, 0, sizeof(float) * (size_t)M * N);
+    for (int r = 0; r < M; r++) {
+        float sc = or_fp16_to_fp32(t->row_scale[r]);
+        for (int c = 0; c < C; c++) {
+            for (int side = 0; side < 2; side++) {
+                const uint16_t* cb1 = side ? t->cb1r : t->cb1l;
+                const uint16_t* cb2 = side ? t->cb2r : t->cb2l;
+                const uint8_t* i1 = side ? t->i1r : t->i1l;
+                const uint8_t* i2 = side ? t->i2r : t->i2l;
+                int k1 = i1[(size_t)r * C + c];
+                int k2 = t->n_levels == 2 ? pq_l2_at(t, i2 + (size_t)r * l2s, c) : 0;
+                for (int k = 0; k < hf; k++) {
+                    float v = or_fp16_to_fp32(cb1[(size_t)k1 * hf + k]);
+                    if (t->n_levels == 2) v = v + or_fp16_to_fp32(cb2[(size_t)k2 * hf + k]);
+                    out[(size_t)r * N + ic[c * G + side * hf + k]] =
+                        or_fp16_to_fp32(or_fp32_to_fp16_rne(v * sc));
+                }
+            }
+        }
+    }
+    for (int j = 0; j < t->n_outlier; j++) {
+        float os = or_fp16_to_fp32(t->oscale[j]);
+        for (int r = 0; r < M; r++)
+            out[(size_t)r * N + t->ocols[j]] = or_fp16_to_fp32(
+                or_fp32_to_fp16_rne((float)t->oside[(size_t)r * t->n_outlier + j] * os));
+    }
+    free(ic);
+    return 0;
+}
+
+/* Table entry sum_i cb[i]*x[i] (pq_decode.c:1621-1659).  The x86 build
+ * vectorizes the products of the first half&~3 terms (separately rounded
+ * multiplies, then an in-order serial add); leftover terms are fused. */
+static float pq_dot(const uint16_t* cb, const float* x, int hf) {
+    float s = 0.0f;
+    int v = hf & ~3, i = 0;
+    for (; i < v; i++) s = s + or_fp16_to_fp32(cb[i]) * x[i];
+    for (; i < hf; i++) s = fmaf(or_fp16_to_fp32(cb[i]), x[i], s);
+    return s;
+}
+
+/* pq_decode.c:1233-1421 apply_outliers as x86 runs it: for n_outlier >= 32
+ * the AVX2 form (x*col_scale quantized to int8 with one meta scale
+ * maxabs/127, exact int32 row dots, out += (float)dot * meta as an FMA);
+ * below 32 the scalar form out[r] = fma((float)side*col_scale, x[col], out[r])
+ * walking outlier columns in order. */
+static void pq_outliers(const or_pq_tensor* t, const float* x, float* out) {
+    int no = t->n_outlier, M = t->M;
+    if (no <= 0) return;
+    if (no >= 32) {
+        float* xq = (float*)malloc(sizeof(float) * (size_t)no);
+        int8_t* qq = (int8_t*)malloc((size_t)no);
+        float mx = 0.0f;
+        for (int j = 0; j < no; j++) {
+            xq[j] = x[t->ocols[j]] * or_fp16_to_fp32(t->oscale[j]);
+            float a = xq[j] < 0 ? -xq[j] : xq[j];
+            if (a > mx) mx = a;
+        }
+        float meta = mx > 0.0f ? mx / 127.0f : 1.0f;
+        float inv = 1.0f / meta;
+        for (int j = 0; j < no; j++) {
+            float sv = xq[j] * inv;
+            int v = (int)(sv >= 0 ? sv + 0.5f : sv - 0.5f);
+            qq[j] = (int8_t)(v > 127 ? 127 : (v < -128 ? -128 : v));
+        }
+        for (int r = 0; r < M; r++) {
+            int32_t s = 0;
+            for (int j = 0; j < no; j++) s += (int32_t)t->oside[(size_t)r * no + j] * qq[j];
+            out[r] = fmaf((float)s, meta, out[r]);
+        }
+        free(xq);
+        free(qq);
+        return;
+    }
+    for (int j = 0; j < no; j++) {
+        float os = or_fp16_to_fp32(t->oscale[j]);
+        float xj = x[t->ocols[j]];
+        for (int r = 0; r < M; r++)
+            out[r] = fmaf((float)t->oside[(size_t)r * no + j] * os, xj, out[r]);
+    }
+}
+
+/* pq_decode.c:1504-1686 (ib_pq_matmul_fp32 -> matmul_impl):
+ *   chunk skipping: chunks whose max|x| over their G inner columns is below
+ *   1% of the global max|x| are left out of both table build and gather;
+ *   tables T[c][k] = sum_i cb[k][i] * x[inner col] (pq_dot);
+ *   gather acc = acc + (TL1 + TR1) (+ (TL2 + TR2)) over chunks in order,
+ *   out[r] = acc * row_scale[r]; then outliers. */
+int or_pq_matmul(const or_pq_tensor* t, const float* x, float* out) {
+    int M = t->M, G = t->G, C = t->C, K = t->K, hf = G / 2;
+    int K2 = t->K_l2 > 0 ? t->K_l2 : K;
+    int two = t->n_levels == 2;
+    int* ic = pq_inner_cols(t);
+    size_t l2s = pq_l2_stride(t);
+    int n_inner = t->N - t->n_outlier;
+
+    float gmax = 0.0f;
+    for (int j = 0; j < n_inner; j++) { float a = x[ic[j]]; a = a < 0 ? -a : a; if (a > gmax) gmax = a; }
+    uint8_t* active = (uint8_t*)malloc((size_t)C);
+    float th = gmax * 0.01f;
+    for (int c = 0; c < C; c++) {
+        float cm = 0.0f;
+        for (int i = 0; i < G; i++) { float a = x[ic[c * G + i]]; a = a < 0 ? -a : a; if (a > cm) cm = a; }
+        active[c] = (gmax > 0.0f) ? (cm >= th) : 1;
+    }
+
+    float* T1 = (float*)calloc((size_t)C * K * 2, sizeof(float));
+    float* T2 = two ? (float*)calloc((size_t)C * K2 * 2, sizeof(float)) : NULL;
+    for (int c = 0; c < C; c++) {
+        if (!active[c]) continue;
+        for (int side = 0; side < 2; side++) {
+            const float* xs = NULL;
+            float xv[64];
+            for (int i = 0; i < hf; i++) xv[i] = x[ic[c * G + side * hf + i]];
+            xs = xv;
+            const uint16_t* cb1 = side ? t->cb1r : t->cb1l;
+            for (int k = 0; k < K; k++) {
+                float s = 0.0f;
+                s = pq_dot(cb1 + (size_t)k * hf, xs, hf);
+                T1[((size_t)c * K + k) * 2 + side] = s;
+            }
+            if (two) {
+                const uint16_t* cb2 = side ? t->cb2r : t->cb2l;
+                for (int k = 0; k < K2; k++) {
+                    float s = 0.0f;
+                    s = pq_dot(cb2 + (size_t)k * hf, xs, hf);
+                    T2[((size_t)c * K2 + k) * 2 + side] = s;
+                }
+            }
+        }
+    }
+    for (int r = 0; r < M; r++) {
+        float acc = 0.0f;
+        for (int c = 0; c < C; c++) {
+            if (!active[c]) continue;
+            int kl = t->i1l[(size_t)r * C + c], kr = t->i1r[(size_t)r * C + c];
+            acc = acc + (T1[((size_t)c * K + kl) * 2] + T1[((size_t)c * K + kr) * 2 + 1]);
+            if (two) {
+                int ml = pq_l2_at(t, t->i2l + (size_t)r * l2s, c);
+                int mr = pq_l2_at(t, t->i2r + (size_t)r * l2s, c);
+                acc = acc + (T2[((size_t)c * K2 + ml) * 2] + T2[((size_t)c * K2 + mr) * 2 + 1]);
+            }
+        }
+        out[r] = acc * or_fp16_to_fp32(t->row_scale[r]);
+    }
+    pq_outliers(t, x, out);
+    free(ic); free(active); free(T1); free(T2);
+    return 0;
+}

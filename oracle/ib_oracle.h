@@ -1,0 +1,87 @@
+/*
+ * ib_oracle.h -- CPU restatement of libinferbit's decode-time quantized
+ * matvec path.  TEST INFRASTRUCTURE ONLY: imported by tests/, by
+ * __graft_entry__.smoke() and by bench.py's cpu_baseline leg, always as the
+ * checker, never as the thing measured or shipped.  The product library
+ * (libinferbit_amd) never links or calls this code.
+ *
+ * Every function names the reference file:line whose behaviour it restates
+ * (paths relative to the reference repository root).  Floating-point
+ * operation order is reproduced where the reference fixes it, so that the
+ * compiled reference (oracle/_ref) and this restatement agree bit for bit;
+ * the file is compiled with -ffp-contract=off and uses fmaf() exactly where
+ * the reference build contracts a multiply-add (avx2.c is built with
+ * -mavx2 -mfma in GNU C mode, CMakeLists.txt:80-84).
+ *
+ * Parity pins (tests/test_oracle_*.py): every function is checked against
+ * golden vectors written by the compiled reference (tests/golden/) and
+ * against closed forms (one-hot inputs, single-position attention, uniform
+ * keys, K=1 codebooks).  No function here is "parity unpinned".
+ */
+#ifndef IB_ORACLE_H
+#define IB_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* fp16 helpers */
+float    or_fp16_to_fp32(uint16_t h);          /* forward.c:38-70            */
+uint16_t or_fp32_to_fp16_trunc(float f);       /* quantize.c:32-41           */
+uint16_t or_fp32_to_fp16_rne(float f);         /* pq_decode.c:305-337        */
+
+/* weight producers (F32 source only) */
+void or_quantize_int8(int8_t* w, uint16_t* s, const float* src, int rows, int cols);  /* quantize.c:75-115  */
+void or_quantize_int4(uint8_t* w, uint16_t* s, const float* src, int rows, int cols); /* quantize.c:119-165 */
+void or_quantize_int2(uint8_t* w, uint16_t* s, const float* src, int rows, int cols); /* quantize.c:169-239 */
+
+/* activation quantizer for W4A8, returns number of groups */
+int or_quantize_act_g128(const float* x, int8_t* q, float* s, int N);                 /* threading.c:401-432 */
+
+/* matvec entries; order = 0 scalar.c order, 1 avx2.c order (what x86 runs) */
+void or_matmul_int8(float* out, const int8_t* w, const float* sc, const float* x, int M, int N, int order);
+void or_matmul_int4(float* out, const uint8_t* w, const float* sc, const float* x, int M, int N, int order);
+void or_matmul_int2(float* out, const uint8_t* w, const float* sc, const float* x, int M, int N);
+void or_matmul_w4a8(float* out, const uint8_t* w, const float* sw, const int8_t* qx, const float* sa,
+                    int M, int N, int order);
+void or_matmul_int8_batch(float* out, const int8_t* w, const float* sw, const float* x,
+                          int M, int N, int B, int M_stride);
+void or_matmul_w4a8_batch(float* out, const uint8_t* w, const float* sw, const int8_t* qx,
+                          const float* sa, int M, int N, int B, int M_stride);
+
+/* KV cache row write / attention decode (one layer, one position) */
+void or_kv_write(void* kdata, void* vdata, float* kscales, float* vscales, int pos,
+                 const float* k, const float* v, int n_kv, int head_dim, int kv_bits);
+void or_attn_decode(float* out, float* att_scratch, const float* q,
+                    const void* kdata, const void* vdata, const float* kscales, const float* vscales,
+                    int pos, int n_heads, int n_kv, int head_dim, int kv_bits);
+void or_softmax(float* d, int n);     /* avx2.c:192-229 (scalar-equivalent result) */
+
+/* decode-layer helpers (forward.c layer loop) */
+void or_rmsnorm(float* out, const float* x, const float* w, float eps, int N);  /* avx2.c:153-188 */
+void or_rope(float* q, float* k, int head_dim, int pos, float theta);          /* scalar.c:140-157 */
+void or_silu_mul(float* out, const float* g, const float* u, int N);           /* avx2.c:233-251 */
+
+/* product-quantized LUT matvec (pq_decode.h:39-87 tensor layout) */
+typedef struct {
+    int M, N, G, K, K_l2, n_levels, n_outlier, C;
+    int l2_idx_bytes;              /* 1 or 2 */
+    const uint16_t *cb1l, *cb1r, *cb2l, *cb2r;   /* fp16 [K][G/2], [K_l2][G/2] */
+    const uint8_t  *i1l, *i1r;                   /* [M][C] */
+    const uint8_t  *i2l, *i2r;                   /* [M][l2 stride] */
+    const uint16_t *row_scale;                   /* fp16 [M] */
+    const int32_t  *ocols;                       /* [n_outlier] */
+    const int8_t   *oside;                       /* [M][n_outlier] */
+    const uint16_t *oscale;                      /* fp16 [n_outlier] */
+} or_pq_tensor;
+
+int or_pq_matmul(const or_pq_tensor* t, const float* x, float* out);      /* pq_decode.c:1504-1686 */
+int or_pq_reconstruct(const or_pq_tensor* t, float* out);                /* pq_decode.c:1103-1196 */
+
+#ifdef __cplusplus
+}
+#endif
+#endif
