@@ -1,0 +1,212 @@
+#!/usr/bin/env python3
+"""Benchmark of the headline workload on one MI355X.
+
+Workload: INT4 matvec at the Mistral-7B MLP shape,
+W 14336x4096 packed int4 with per-row fp16 scales (quantize.c semantics),
+x fp32 N(0,1), batch 1 -- ib_parallel_matmul(bits=4) / ib_kern.matmul_int4.
+One step = one GEMV over one weight copy.  16 distinct weight copies
+(~470 MB) are used round-robin so the 256 MB Infinity Cache cannot serve
+repeated reads; inputs are resident in HBM before timing starts.
+
+value = algorithmic bytes per call / average kernel time, in GB/s
+(W + 2M fp16 scales + 4N x + 4M y = 29,462,528 B per call).
+Extra lines in the same JSON: the W4A8 decode form of the same tensor, the
+other matvec configs, the batch sweep, the roofline object, and the CPU
+baseline (the reference library compiled from source, timed on this host).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import subprocess
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+COPIES = 16
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=2000)
+    p.add_argument("--warmup", type=int, default=200)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--quick", action="store_true", help="headline only (for profiling runs)")
+    return p.parse_args()
+
+
+def matvec_bytes(M, N, bits, w4a8=False):
+    wb = M * N * bits // 8
+    xb = (N + 4 * ((N + 127) // 128)) if w4a8 else 4 * N
+    return wb + 2 * M + xb + 4 * M
+
+
+def make_weights(oracle, bits, M, N, seed):
+    """Quantize N(0,0.02) rows with the quantize.c rules.  To keep host time
+    bounded, 256 distinct rows are quantized and tiled to M rows."""
+    rng = np.random.default_rng(seed)
+    base = (rng.standard_normal((min(256, M), N)) * 0.02).astype(np.float32)
+    w, s = oracle.quantize(bits, base)
+    reps = (M + w.shape[0] - 1) // w.shape[0]
+    return np.tile(w, (reps, 1))[:M], np.tile(s, reps)[:M]
+
+
+def time_launches(torch, launch, steps, warmup):
+    """Average device time per launch.  The launches are captured into a HIP
+    graph (one node per weight copy) and the graph is replayed, so the
+    timed region holds back-to-back kernels with no host launch gaps; HIP
+    events on the replay stream bracket the whole timed region."""
+    for i in range(COPIES):
+        launch(i)                                   # eager warmup, also validates
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    with torch.cuda.stream(cap):
+        with torch.cuda.graph(g, stream=cap):
+            for i in range(COPIES):
+                launch(i)
+    torch.cuda.synchronize()
+    reps = max(1, steps // COPIES)
+    for _ in range(max(1, warmup // COPIES)):
+        g.replay()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(reps):
+        g.replay()
+    e1.record(st)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / (reps * COPIES) * 1e-3   # seconds per launch
+
+
+def gemv_case(torch, L, oracle, bits, M, N, steps, warmup, w4a8=False, seed=0):
+    w, s = make_weights(oracle, bits, M, N, seed)
+    wd = torch.from_numpy(w.view(np.uint8).copy()).cuda()
+    copies = [wd] + [wd.clone() for _ in range(COPIES - 1)]
+    sd = torch.from_numpy(s.view(np.int16).copy()).cuda()
+    x = torch.randn(N, generator=torch.Generator().manual_seed(seed + 1)).cuda()
+    y = torch.empty(M, device="cuda")
+    if w4a8:
+        q = torch.empty(N, dtype=torch.int8, device="cuda")
+        sa = torch.empty((N + 127) // 128, device="cuda")
+        L.ops.quantize_input_int8_g128(x, q, sa, N)
+
+        def launch(i):
+            L.ops.parallel_matmul_w4a8(y, copies[i % COPIES], sd, q, sa, M, N)
+    else:
+        def launch(i):
+            L.ops.parallel_matmul(y, copies[i % COPIES], sd, x, M, N, bits)
+    t = time_launches(torch, launch, steps, warmup)
+    del copies
+    nbytes = matvec_bytes(M, N, bits, w4a8)
+    return {"M": M, "N": N, "bits": bits, "w4a8": w4a8, "us": round(t * 1e6, 3),
+            "bytes": nbytes, "GBps": round(nbytes / t / 1e9, 1),
+            "frac_hbm": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
+
+
+def batch_case(torch, L, oracle, B, steps, warmup):
+    M, N = 14336, 4096
+    w, s = make_weights(oracle, 4, M, N, 3)
+    wd = torch.from_numpy(w.copy()).cuda()
+    copies = [wd] + [wd.clone() for _ in range(COPIES - 1)]
+    sd = torch.from_numpy(s.view(np.int16).copy()).cuda()
+    qx = torch.randint(-127, 128, (B, N), dtype=torch.int8).cuda()
+    sa = (torch.rand(B, N // 128) * 0.02 + 0.001).cuda()
+    y = torch.empty(B * M, device="cuda")
+
+    def launch(i):
+        L.ops.matmul_w4a8_batch(y, copies[i % COPIES], sd, qx, sa, M, N, B, M)
+    t = time_launches(torch, launch, steps, warmup)
+    nbytes = M * N // 2 + 2 * M + B * (N + 4 * (N // 128)) + 4 * B * M
+    return {"B": B, "us": round(t * 1e6, 3), "GBps": round(nbytes / t / 1e9, 1)}
+
+
+def cpu_baseline():
+    """The reference library compiled from its own sources (oracle/_ref),
+    ib_parallel_matmul INT4 14336x4096 with the x86 AVX2 table, timed on
+    this host's cores over rotating weight copies."""
+    exe = os.path.join(ROOT, "oracle", "_ref", "ref_harness")
+    if not os.path.exists(exe):
+        return None
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    cores = max(1, min(cores, 16))
+    iters, copies = 800, 8
+    r = subprocess.run([exe, "gemv", "4", "14336", "4096", str(cores), str(iters), str(copies)],
+                       capture_output=True, text=True, timeout=300)
+    if r.returncode != 0:
+        return None
+    d = json.loads(r.stdout.strip().splitlines()[-1])
+    nbytes = matvec_bytes(14336, 4096, 4)
+    return {"value": round(nbytes / d["median_s"] / 1e9, 2), "unit": "GB/s", "cores": cores,
+            "kind": "reference",
+            "sample": f"{iters} calls of ib_parallel_matmul(bits=4) 14336x4096 ({d['simd']}), "
+                      f"{copies} rotating weight copies, median per call {d['median_s'] * 1e6:.0f} us"}
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {a.gpus}); "
+              "multi-GPU sharding is design-only.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import libinferbit_amd as L
+    from oracle import pyoracle as oracle
+
+    L.ops.init(0)
+    print("bench: headline INT4 GEMV 14336x4096", file=sys.stderr, flush=True)
+    head = gemv_case(torch, L, oracle, 4, 14336, 4096, a.steps, a.warmup)
+    extra = {}
+    if not a.quick:
+        for name, (bits, M, N, w4a8) in {
+            "int4_4096x14336": (4, 4096, 14336, False),
+            "w4a8_14336x4096": (4, 14336, 4096, True),
+            "w4a8_4096x14336": (4, 4096, 14336, True),
+            "int8_2048x2048": (8, 2048, 2048, False),
+            "int8_14336x4096": (8, 14336, 4096, False),
+            "int2_14336x4096": (2, 14336, 4096, False),
+        }.items():
+            print(f"bench: {name}", file=sys.stderr, flush=True)
+            extra[name] = gemv_case(torch, L, oracle, bits, M, N, a.steps, a.warmup, w4a8)
+        extra["w4a8_batch_sweep_14336x4096"] = [batch_case(torch, L, oracle, B, max(200, a.steps // 4), 20)
+                                                for B in (1, 2, 4, 8)]
+    cpu = None if a.no_cpu else cpu_baseline()
+    out = {
+        "metric": "quantized GEMV HBM GB/s (% of peak) + decode tok/s, Mistral-7B-shape INT4, 1 GPU",
+        "value": head["GBps"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(head["us"] / 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4xf32",
+        "data": "synthetic: W N(0,0.02) quantized with quantize.c rules (256 distinct rows tiled), x N(0,1)",
+        "config": {"workload": "INT4 matvec 14336x4096 batch 1 (matmul_int4), 16 rotating weight copies",
+                   "M": 14336, "N": 4096, "batch": 1, "bits": 4},
+        "roofline": {"bound": "hbm", "achieved": head["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": head["frac_hbm"], "traffic": None,
+                     "kernel": "gemv_mfma_f32<4,...>", "bytes_per_launch": head["bytes"],
+                     "us_per_launch": head["us"]},
+        "cpu_baseline": cpu,
+        "decode_tok_s": None,
+        "extra": extra,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,73 @@
+"""ctypes loader for libibhip.so with the signatures of include/ibhip.h."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "_build", "libibhip.so")
+_lib = None
+
+P = C.c_void_p
+I = C.c_int
+SZ = C.c_size_t
+
+# name -> (restype, argtypes); must match include/ibhip.h
+SIGNATURES = {
+    "ibh_init": (I, [I]),
+    "ibh_last_error": (C.c_char_p, []),
+    "ibh_version": (C.c_char_p, []),
+    "ibh_default_stream": (P, []),
+    "ibh_synchronize": (I, [P]),
+    "ibh_device_malloc": (I, [C.POINTER(P), SZ]),
+    "ibh_device_free": (I, [P]),
+    "ibh_memcpy_h2d": (I, [P, P, SZ, P]),
+    "ibh_memcpy_d2h": (I, [P, P, SZ, P]),
+    "ibh_memcpy_d2d": (I, [P, P, SZ, P]),
+    "ibh_matmul": (I, [P, P, P, I, P, I, I, I, P]),
+    "ibh_quantize_act_g128": (I, [P, P, P, I, P]),
+    "ibh_matmul_w4a8": (I, [P, P, P, I, P, P, I, I, P]),
+    "ibh_matmul_w4a8_x": (I, [P, P, P, I, P, I, I, P, P, P]),
+    "ibh_matmul_w4a8_batch": (I, [P, P, P, I, P, P, I, I, I, I, P]),
+    "ibh_matmul_int8_batch": (I, [P, P, P, I, P, I, I, I, I, P]),
+    "ib_init_kernels_hip": (None, [P]),
+    "ibh_register_host_weights": (I, [P, SZ, C.POINTER(P)]),
+    "ibh_unregister_host_weights": (None, [P]),
+}
+
+
+class IbhError(RuntimeError):
+    def __init__(self, code: int, where: str):
+        msg = lib().ibh_last_error()
+        super().__init__(f"{where} failed with code {code}: {msg.decode() if msg else 'no message'}")
+        self.code = code
+
+
+def lib_path() -> str:
+    return _LIB_PATH
+
+
+def loaded() -> bool:
+    return _lib is not None
+
+
+def lib():
+    """Load libibhip.so; raise if it has not been built (no fallback)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            raise RuntimeError(
+                f"libinferbit_amd: {_LIB_PATH} is missing -- build it with "
+                "`python -m libinferbit_amd.build` (hipcc, gfx950). There is no CPU fallback.")
+        L = C.CDLL(_LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc: int, where: str) -> None:
+    if rc != 0:
+        raise IbhError(rc, where)

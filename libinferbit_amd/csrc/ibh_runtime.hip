@@ -1,0 +1,335 @@
+// ibh_runtime.hip -- device/stream/error runtime of libibhip and the
+// host-pointer dispatch-table entries (ib_init_kernels_hip).
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <vector>
+
+#include "ibh_common.h"
+
+// ── errors (same convention as src/error.c:7-21 of the reference) ─────────
+static thread_local char g_err[512];
+static thread_local int g_err_set = 0;
+
+extern "C" void ibh_set_error(const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    g_err_set = 1;
+}
+
+extern "C" const char* ibh_last_error(void) {
+    if (!g_err_set) return nullptr;
+    g_err_set = 0;
+    return g_err;
+}
+
+extern "C" const char* ibh_version(void) { return "libinferbit_amd 0.1.0 (gfx950)"; }
+
+// ── per-device state ───────────────────────────────────────────────────────
+namespace {
+constexpr int kMaxDev = 16;
+struct DevState {
+    bool ready = false;
+    hipStream_t stream = nullptr;
+    void* ws = nullptr;          // library workspace (activation operand staging)
+    size_t ws_bytes = 0;
+};
+constexpr size_t kDefaultWorkspace = 4u << 20;
+DevState g_dev[kMaxDev];
+std::mutex g_mu;
+
+int current_device() {
+    int d = 0;
+    if (hipGetDevice(&d) != hipSuccess) return -1;
+    return d;
+}
+}  // namespace
+
+extern "C" int ibh_init(int device) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    int n = 0;
+    IBH_HIP(hipGetDeviceCount(&n), "ibh_init: hipGetDeviceCount");
+    if (device < 0 || device >= n || device >= kMaxDev) {
+        ibh_set_error("ibh_init: device %d out of range (%d visible)", device, n);
+        return IBH_ERROR_PARAM;
+    }
+    IBH_HIP(hipSetDevice(device), "ibh_init: hipSetDevice");
+    DevState& s = g_dev[device];
+    if (!s.ready) {
+        IBH_HIP(hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking), "ibh_init: hipStreamCreate");
+        if (hipMalloc(&s.ws, kDefaultWorkspace) != hipSuccess) {
+            ibh_set_error("ibh_init: cannot allocate the %zu-byte workspace", kDefaultWorkspace);
+            return IBH_ERROR_MEMORY;
+        }
+        s.ws_bytes = kDefaultWorkspace;
+        s.ready = true;
+    }
+    return IBH_OK;
+}
+
+// Per-device workspace allocated by ibh_init (fixed size, so calls can be
+// captured in HIP graphs).  Shared by every call on the device: calls that
+// use it must not overlap in time (one stream, or stream-ordered).
+void* ibh_workspace(size_t bytes) {
+    const int d = current_device();
+    if (d < 0 || d >= kMaxDev) return nullptr;
+    if (!g_dev[d].ready && ibh_init(d) != IBH_OK) return nullptr;
+    return bytes <= g_dev[d].ws_bytes ? g_dev[d].ws : nullptr;
+}
+
+hipStream_t ibh_resolve_stream(void* s) {
+    if (s) return (hipStream_t)s;
+    const int d = current_device();
+    if (d < 0 || d >= kMaxDev) return nullptr;
+    if (!g_dev[d].ready) ibh_init(d);
+    return g_dev[d].stream;
+}
+
+extern "C" void* ibh_default_stream(void) { return (void*)ibh_resolve_stream(nullptr); }
+
+extern "C" int ibh_synchronize(void* stream) {
+    IBH_HIP(hipStreamSynchronize(ibh_resolve_stream(stream)), "ibh_synchronize");
+    return IBH_OK;
+}
+
+extern "C" int ibh_device_malloc(void** dptr, size_t bytes) {
+    if (!dptr) {
+        ibh_set_error("ibh_device_malloc: null out-pointer");
+        return IBH_ERROR_PARAM;
+    }
+    if (hipMalloc(dptr, bytes ? bytes : 1) != hipSuccess) {
+        ibh_set_error("ibh_device_malloc: out of device memory (%zu bytes)", bytes);
+        *dptr = nullptr;
+        return IBH_ERROR_MEMORY;
+    }
+    return IBH_OK;
+}
+
+extern "C" int ibh_device_free(void* dptr) {
+    if (dptr) IBH_HIP(hipFree(dptr), "ibh_device_free");
+    return IBH_OK;
+}
+
+static int copy(void* dst, const void* src, size_t n, hipMemcpyKind k, void* stream, const char* who) {
+    if (!n) return IBH_OK;
+    hipStream_t st = ibh_resolve_stream(stream);
+    IBH_HIP(hipMemcpyAsync(dst, src, n, k, st), who);
+    if (k == hipMemcpyDeviceToHost) IBH_HIP(hipStreamSynchronize(st), who);
+    return IBH_OK;
+}
+extern "C" int ibh_memcpy_h2d(void* d, const void* s, size_t n, void* st) {
+    return copy(d, s, n, hipMemcpyHostToDevice, st, "ibh_memcpy_h2d");
+}
+extern "C" int ibh_memcpy_d2h(void* d, const void* s, size_t n, void* st) {
+    return copy(d, s, n, hipMemcpyDeviceToHost, st, "ibh_memcpy_d2h");
+}
+extern "C" int ibh_memcpy_d2d(void* d, const void* s, size_t n, void* st) {
+    return copy(d, s, n, hipMemcpyDeviceToDevice, st, "ibh_memcpy_d2d");
+}
+
+// ── host-pointer dispatch table ────────────────────────────────────────────
+//
+// The reference calls its table from CPU code with host pointers
+// (src/threading.c:220-258).  Registered weight regions are uploaded once;
+// activations, scales and outputs are staged through a grow-only device
+// workspace.  Table entries return void like the reference's; a failure is
+// reported on stderr and through ibh_last_error(), and the output is left
+// NaN-filled so it cannot pass for a result.
+namespace {
+struct Region {
+    const uint8_t* host;
+    size_t bytes;
+    uint8_t* dev;
+};
+std::vector<Region> g_regions;
+std::mutex g_tab_mu;
+uint8_t* g_ws = nullptr;
+size_t g_ws_bytes = 0;
+
+const uint8_t* lookup(const void* hp, size_t need) {
+    const uint8_t* p = (const uint8_t*)hp;
+    for (const Region& r : g_regions)
+        if (p >= r.host && p + need <= r.host + r.bytes) return r.dev + (p - r.host);
+    return nullptr;
+}
+
+uint8_t* workspace(size_t bytes) {
+    if (bytes <= g_ws_bytes) return g_ws;
+    if (g_ws) (void)hipFree(g_ws);
+    g_ws = nullptr;
+    g_ws_bytes = 0;
+    size_t want = bytes + (bytes >> 2) + 4096;
+    if (hipMalloc((void**)&g_ws, want) != hipSuccess) return nullptr;
+    g_ws_bytes = want;
+    return g_ws;
+}
+
+size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+void fail(float* out, size_t n, const char* who) {
+    const char* e = ibh_last_error();
+    fprintf(stderr, "libinferbit_amd: %s failed: %s\n", who, e ? e : "unknown error");
+    ibh_set_error("%s failed: %s", who, e ? e : "unknown error");
+    for (size_t i = 0; i < n; i++) out[i] = __builtin_nanf("");
+}
+
+// Stage host operands, run `launch(device pointers...)`, copy `out` back.
+struct Staged {
+    uint8_t* base = nullptr;
+    size_t off = 0;
+    uint8_t* put(const void* h, size_t n, hipStream_t st) {
+        uint8_t* d = base + off;
+        off += al256(n);
+        if (h && n) (void)hipMemcpyAsync(d, h, n, hipMemcpyHostToDevice, st);
+        return d;
+    }
+};
+
+int tab_weight(const void* w, size_t wbytes, Staged& S, hipStream_t st, const uint8_t** dw) {
+    *dw = lookup(w, wbytes);
+    if (!*dw) *dw = S.put(w, wbytes, st);
+    return IBH_OK;
+}
+
+size_t wbytes_of(int bits, int M, int N) {
+    return (size_t)M * (bits == 8 ? (size_t)N : (bits == 4 ? (size_t)N / 2 : (size_t)N / 4));
+}
+
+void tab_matmul(float* out, const void* w, const float* sc, const float* x, int M, int N, int bits) {
+    std::lock_guard<std::mutex> lk(g_tab_mu);
+    hipStream_t st = ibh_resolve_stream(nullptr);
+    const size_t wb = wbytes_of(bits, M, N);
+    const bool resident = lookup(w, wb) != nullptr;
+    Staged S;
+    S.base = workspace(al256(4 * (size_t)M) * 2 + al256(4 * (size_t)N) + (resident ? 0 : al256(wb)));
+    if (!S.base) { ibh_set_error("out of device memory"); fail(out, M, "matmul table entry"); return; }
+    const uint8_t* dw;
+    tab_weight(w, wb, S, st, &dw);
+    float* dsc = (float*)S.put(sc, 4 * (size_t)M, st);
+    float* dx = (float*)S.put(x, 4 * (size_t)N, st);
+    float* dout = (float*)S.put(nullptr, 4 * (size_t)M, st);
+    int rc = ibh_matmul(dout, dw, dsc, IBH_SCALE_F32, dx, M, N, bits, st);
+    if (rc == IBH_OK && hipMemcpyAsync(out, dout, 4 * (size_t)M, hipMemcpyDeviceToHost, st) == hipSuccess &&
+        hipStreamSynchronize(st) == hipSuccess)
+        return;
+    if (rc == IBH_OK) ibh_set_error("device copy failed");
+    fail(out, M, "matmul table entry");
+}
+
+void hip_int8(float* o, const void* w, const float* s, const float* x, int M, int N) { tab_matmul(o, w, s, x, M, N, 8); }
+void hip_int4(float* o, const void* w, const float* s, const float* x, int M, int N) { tab_matmul(o, w, s, x, M, N, 4); }
+void hip_int2(float* o, const void* w, const float* s, const float* x, int M, int N) { tab_matmul(o, w, s, x, M, N, 2); }
+
+void tab_w4a8(float* out, const void* w, const float* sw, const int8_t* qx, const float* sa, int M, int N,
+              int B, int M_stride, bool fused) {
+    std::lock_guard<std::mutex> lk(g_tab_mu);
+    hipStream_t st = ibh_resolve_stream(nullptr);
+    const size_t wb = (size_t)M * (N / 2);
+    const bool resident = lookup(w, wb) != nullptr;
+    const int G = (N + 127) / 128;
+    // The output keeps rows this slice does not own (M_stride > M): copy the
+    // whole strided region in and out so they are preserved.
+    const size_t ob = 4 * ((size_t)(B - 1) * M_stride + M);
+    Staged S;
+    S.base = workspace(al256(4 * (size_t)M) + al256((size_t)B * N) + al256(4 * (size_t)B * G) + al256(ob) +
+                       (resident ? 0 : al256(wb)));
+    if (!S.base) { ibh_set_error("out of device memory"); fail(out, ob / 4, "w4a8 table entry"); return; }
+    const uint8_t* dw;
+    tab_weight(w, wb, S, st, &dw);
+    float* dsw = (float*)S.put(sw, 4 * (size_t)M, st);
+    int8_t* dq = (int8_t*)S.put(qx, (size_t)B * N, st);
+    float* dsa = (float*)S.put(sa, 4 * (size_t)B * G, st);
+    float* dout = (float*)S.put(out, ob, st);
+    int rc = fused ? ibh_matmul_w4a8(dout, dw, dsw, IBH_SCALE_F32, dq, dsa, M, N, st)
+                   : ibh_matmul_w4a8_batch(dout, dw, dsw, IBH_SCALE_F32, dq, dsa, M, N, B,
+                                                             M_stride, st);
+    if (rc == IBH_OK && hipMemcpyAsync(out, dout, ob, hipMemcpyDeviceToHost, st) == hipSuccess &&
+        hipStreamSynchronize(st) == hipSuccess)
+        return;
+    if (rc == IBH_OK) ibh_set_error("device copy failed");
+    fail(out, ob / 4, "w4a8 table entry");
+}
+
+// The single-row W4A8 entry is the x86 AVX2 kernel (fused fold); the batched
+// entry is the scalar kernel (unfused fold), also at B == 1.
+void hip_w4a8(float* out, const void* w, const float* sw, const int8_t* qx, const float* sa, int M, int N) {
+    tab_w4a8(out, w, sw, qx, sa, M, N, 1, M, true);
+}
+void hip_w4a8_batch(float* out, const void* w, const float* sw, const int8_t* qx, const float* sa, int M,
+                    int N, int B, int M_stride) {
+    tab_w4a8(out, w, sw, qx, sa, M, N, B, M_stride, false);
+}
+
+void hip_int8_batch(float* out, const void* w, const float* sw, const float* x, int M, int N, int B,
+                    int M_stride) {
+    std::lock_guard<std::mutex> lk(g_tab_mu);
+    hipStream_t st = ibh_resolve_stream(nullptr);
+    const size_t wb = (size_t)M * N;
+    const bool resident = lookup(w, wb) != nullptr;
+    const size_t ob = 4 * ((size_t)(B - 1) * M_stride + M);
+    Staged S;
+    S.base = workspace(al256(4 * (size_t)M) + al256(4 * (size_t)B * N) + al256(ob) + (resident ? 0 : al256(wb)));
+    if (!S.base) { ibh_set_error("out of device memory"); fail(out, ob / 4, "int8 batch table entry"); return; }
+    const uint8_t* dw;
+    tab_weight(w, wb, S, st, &dw);
+    float* dsw = (float*)S.put(sw, 4 * (size_t)M, st);
+    float* dx = (float*)S.put(x, 4 * (size_t)B * N, st);
+    float* dout = (float*)S.put(out, ob, st);
+    int rc = ibh_matmul_int8_batch(dout, dw, dsw, IBH_SCALE_F32, dx, M, N, B, M_stride, st);
+    if (rc == IBH_OK && hipMemcpyAsync(out, dout, ob, hipMemcpyDeviceToHost, st) == hipSuccess &&
+        hipStreamSynchronize(st) == hipSuccess)
+        return;
+    if (rc == IBH_OK) ibh_set_error("device copy failed");
+    fail(out, ob / 4, "int8 batch table entry");
+}
+}  // namespace
+
+extern "C" void ib_init_kernels_hip(ibh_kernels* k) {
+    if (!k) return;
+    k->matmul_int8 = hip_int8;
+    k->matmul_int4 = hip_int4;
+    k->matmul_int2 = hip_int2;
+    k->matmul_w4a8 = hip_w4a8;
+    k->matmul_w4a8_batch = hip_w4a8_batch;
+    k->matmul_int8_batch = hip_int8_batch;
+}
+
+extern "C" int ibh_register_host_weights(const void* host_base, size_t bytes, void** dev_base) {
+    if (!host_base || !bytes) {
+        ibh_set_error("ibh_register_host_weights: empty region");
+        return IBH_ERROR_PARAM;
+    }
+    std::lock_guard<std::mutex> lk(g_tab_mu);
+    for (const Region& r : g_regions)
+        if (r.host == host_base && r.bytes == bytes) {
+            if (dev_base) *dev_base = r.dev;
+            return IBH_OK;
+        }
+    uint8_t* d = nullptr;
+    if (hipMalloc((void**)&d, bytes) != hipSuccess) {
+        ibh_set_error("ibh_register_host_weights: out of device memory (%zu bytes)", bytes);
+        return IBH_ERROR_MEMORY;
+    }
+    if (hipMemcpy(d, host_base, bytes, hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipFree(d);
+        ibh_set_error("ibh_register_host_weights: upload failed");
+        return IBH_ERROR_INTERNAL;
+    }
+    g_regions.push_back({(const uint8_t*)host_base, bytes, d});
+    if (dev_base) *dev_base = d;
+    return IBH_OK;
+}
+
+extern "C" void ibh_unregister_host_weights(const void* host_base) {
+    std::lock_guard<std::mutex> lk(g_tab_mu);
+    for (size_t i = 0; i < g_regions.size(); i++)
+        if (g_regions[i].host == host_base) {
+            (void)hipFree(g_regions[i].dev);
+            g_regions.erase(g_regions.begin() + (long)i);
+            return;
+        }
+}

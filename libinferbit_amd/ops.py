@@ -1,0 +1,76 @@
+"""Host-side mirror of the reference's matvec operator entry points.
+
+Names and argument meaning follow the reference (src/threading.c,
+src/kernels/scalar.c, src/inferbit_internal.h:199-277): ``out`` first, then
+weights, scales, activations, then sizes.  Operands are torch tensors
+resident on the GPU; work is enqueued on torch's current stream so
+torch.cuda events time it.  Errors raise IbhError (the library's negative
+INFERBIT_ERROR_* code plus its message).
+"""
+from __future__ import annotations
+
+import torch
+
+from ._lib import check, lib
+
+SCALE_F16, SCALE_F32 = 0, 1
+
+
+def _ptr(t: torch.Tensor):
+    if not t.is_cuda:
+        raise ValueError("libinferbit_amd ops take GPU tensors")
+    if not t.is_contiguous():
+        raise ValueError("operand must be contiguous")
+    return t.data_ptr()
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _scale_kind(s: torch.Tensor) -> int:
+    if s.dtype in (torch.float16, torch.int16, torch.uint16):
+        return SCALE_F16
+    if s.dtype == torch.float32:
+        return SCALE_F32
+    raise TypeError(f"scales must be fp16 bits or fp32, got {s.dtype}")
+
+
+def init(device: int = 0) -> None:
+    check(lib().ibh_init(device), "ibh_init")
+
+
+def parallel_matmul(out, w, scales, x, M: int, N: int, bits: int) -> None:
+    """ib_parallel_matmul (src/threading.c:244-258): out[M] = W[M,N] x[N] * scales."""
+    check(lib().ibh_matmul(_ptr(out), _ptr(w), _ptr(scales), _scale_kind(scales), _ptr(x), M, N, bits,
+                           _stream()), "ibh_matmul")
+
+
+def quantize_input_int8_g128(x, q, s, N: int) -> int:
+    """ib_quantize_input_int8_g128 (src/threading.c:401-432); returns the group count."""
+    check(lib().ibh_quantize_act_g128(_ptr(x), _ptr(q), _ptr(s), N, _stream()), "ibh_quantize_act_g128")
+    return (N + 127) // 128
+
+
+def parallel_matmul_w4a8(out, w, scales_w, qx, scales_a, M: int, N: int) -> None:
+    """ib_parallel_matmul_w4a8 (src/threading.c:283-294), x86 AVX2 kernel semantics."""
+    check(lib().ibh_matmul_w4a8(_ptr(out), _ptr(w), _ptr(scales_w), _scale_kind(scales_w), _ptr(qx),
+                                _ptr(scales_a), M, N, _stream()), "ibh_matmul_w4a8")
+
+
+def matmul_w4a8_x(out, w, scales_w, x, M: int, N: int, qx_ws, sa_ws) -> None:
+    """tensor_matmul's INT4 branch (src/forward.c:158-172): quantize x, then W4A8."""
+    check(lib().ibh_matmul_w4a8_x(_ptr(out), _ptr(w), _ptr(scales_w), _scale_kind(scales_w), _ptr(x), M, N,
+                                  _ptr(qx_ws), _ptr(sa_ws), _stream()), "ibh_matmul_w4a8_x")
+
+
+def matmul_w4a8_batch(out, w, scales_w, qx, scales_a, M: int, N: int, B: int, M_stride: int) -> None:
+    """ib_kern.matmul_w4a8_batch (src/kernels/scalar.c:86-124)."""
+    check(lib().ibh_matmul_w4a8_batch(_ptr(out), _ptr(w), _ptr(scales_w), _scale_kind(scales_w), _ptr(qx),
+                                      _ptr(scales_a), M, N, B, M_stride, _stream()), "ibh_matmul_w4a8_batch")
+
+
+def matmul_int8_batch(out, w, scales_w, x, M: int, N: int, B: int, M_stride: int) -> None:
+    """ib_kern.matmul_int8_batch (src/kernels/scalar.c:70-84)."""
+    check(lib().ibh_matmul_int8_batch(_ptr(out), _ptr(w), _ptr(scales_w), _scale_kind(scales_w), _ptr(x), M,
+                                      N, B, M_stride, _stream()), "ibh_matmul_int8_batch")

@@ -1,0 +1,167 @@
+"""Writes the golden vectors in this directory from the REFERENCE library.
+
+The reference library is compiled from the reference sources by
+``make -C oracle ref`` (oracle/_ref/libinferbit_ref.so); this script calls its
+exported entry points through ctypes (oracle/refbind.py) on seeded inputs and
+stores inputs and outputs as .npz fixtures (data only).  Run from the repo
+root:  python tests/golden/gen_golden.py
+
+Contents (every array is what the reference produced, except the inputs):
+  quant.npz    ib_quantize_int{8,4,2} on fp32 W            (src/quantize.c)
+  matvec.npz   ib_kern.matmul_int{8,4,2}, x86 (avx2) and scalar tables
+  w4a8.npz     ib_quantize_input_int8_g128 + matmul_w4a8 (avx2/scalar)
+  batch.npz    matmul_int8_batch / matmul_w4a8_batch with M_stride > M
+  pq.npz       ib_pq_matmul_fp32 / ib_pq_reconstruct_fp32 on small tensors
+"""
+from __future__ import annotations
+
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
+
+from oracle import refbind as R  # noqa: E402
+
+SHAPES = [(64, 256), (37, 200), (16, 4100), (8, 4096)]
+
+
+def f16bits(a):
+    return np.asarray(a, np.float16).view(np.uint16)
+
+
+def fp16_to_f32(h):
+    return np.asarray(h, np.uint16).view(np.float16).astype(np.float32)
+
+
+def gen_quant_matvec(out):
+    rng = np.random.default_rng(20240601)
+    q, mv, w4 = {}, {}, {}
+    avx, sca = R.kernels(R.IB_SIMD_AVX2), R.kernels(R.IB_SIMD_NONE)
+    for (M, N) in SHAPES:
+        tag = f"{M}x{N}"
+        W = (rng.standard_normal((M, N)) * 0.02).astype(np.float32)
+        W[0, :] = 0.0                                  # all-zero row: scale floor
+        W[1, 5] = 3.0                                  # outlier row
+        x = rng.standard_normal(N).astype(np.float32)
+        q[f"W_{tag}"] = W
+        mv[f"x_{tag}"] = x
+        for bits in (8, 4, 2):
+            if bits == 2 and N % 4:
+                continue
+            w, s = R.quantize(bits, W)
+            q[f"w{bits}_{tag}"], q[f"s{bits}_{tag}"] = w, s
+            sc = fp16_to_f32(s)
+            mv[f"y{bits}_avx2_{tag}"] = R.matmul(avx, bits, w, sc, x)
+            mv[f"y{bits}_scalar_{tag}"] = R.matmul(sca, bits, w, sc, x)
+        qx, sa = R.quantize_act(x)
+        w4[f"qx_{tag}"], w4[f"sa_{tag}"] = qx, sa
+        wq, s = q[f"w4_{tag}"], q[f"s4_{tag}"]
+        w4[f"y_avx2_{tag}"] = R.matmul_w4a8(avx, wq, fp16_to_f32(s), qx, sa)
+        w4[f"y_scalar_{tag}"] = R.matmul_w4a8(sca, wq, fp16_to_f32(s), qx, sa)
+    # activation-quantizer edge cases: zero group, tiny group, ties at .5
+    xe = np.zeros(300, np.float32)
+    xe[128:256] = 1e-12
+    xe[256:] = np.linspace(-1, 1, 44, dtype=np.float32)
+    xe[260] = 127.0 / 254.0
+    qx, sa = R.quantize_act(xe)
+    w4["x_edge"], w4["qx_edge"], w4["sa_edge"] = xe, qx, sa
+    np.savez_compressed(os.path.join(out, "quant.npz"), **q)
+    np.savez_compressed(os.path.join(out, "matvec.npz"), **mv)
+    np.savez_compressed(os.path.join(out, "w4a8.npz"), **w4)
+
+
+def gen_batch(out):
+    rng = np.random.default_rng(7)
+    tab = R.kernels(R.IB_SIMD_AVX2)
+    d = {}
+    for (M, N) in [(48, 256), (33, 384)]:
+        W = (rng.standard_normal((M, N)) * 0.02).astype(np.float32)
+        w8, s8 = R.quantize(8, W)
+        w4, s4 = R.quantize(4, W)
+        for B in (1, 2, 5, 8):
+            tag = f"{M}x{N}_b{B}"
+            X = rng.standard_normal((B, N)).astype(np.float32)
+            QS = [R.quantize_act(X[b]) for b in range(B)]
+            QX = np.stack([a for a, _ in QS])
+            SA = np.stack([b for _, b in QS])
+            ms = M + 3
+            d[f"X_{tag}"], d[f"QX_{tag}"], d[f"SA_{tag}"] = X, QX, SA
+            d[f"y8_{tag}"] = R.matmul_int8_batch(tab, w8, fp16_to_f32(s8), X, ms)
+            d[f"y4_{tag}"] = R.matmul_w4a8_batch(tab, w4, fp16_to_f32(s4), QX, SA, ms)
+        d[f"w8_{M}x{N}"], d[f"s8_{M}x{N}"] = w8, s8
+        d[f"w4_{M}x{N}"], d[f"s4_{M}x{N}"] = w4, s4
+    np.savez_compressed(os.path.join(out, "batch.npz"), **d)
+
+
+def make_pq(rng, M, Cc, G, K, nl, K2, no, l2b=1):
+    N = Cc * G + no
+    h = G // 2
+    t = dict(M=M, N=N, G=G, K=K, n_levels=nl, n_outlier=no, C=Cc, K_l2=K2 if nl == 2 else 0, l2_idx_bytes=l2b)
+    t["cb1l"] = f16bits(rng.standard_normal((K, h)) * 0.02)
+    t["cb1r"] = f16bits(rng.standard_normal((K, h)) * 0.02)
+    t["i1l"] = rng.integers(0, K, (M, Cc), dtype=np.uint8)
+    t["i1r"] = rng.integers(0, K, (M, Cc), dtype=np.uint8)
+    t["row_scale"] = f16bits(1 + 0.1 * rng.standard_normal(M))
+    if nl == 2:
+        t["cb2l"] = f16bits(rng.standard_normal((K2, h)) * 0.005)
+        t["cb2r"] = f16bits(rng.standard_normal((K2, h)) * 0.005)
+        if K2 == 16:
+            st = (Cc + 1) // 2
+            t["i2l"] = rng.integers(0, 256, (M, st), dtype=np.uint8)
+            t["i2r"] = rng.integers(0, 256, (M, st), dtype=np.uint8)
+        elif l2b == 2:
+            t["i2l"] = rng.integers(0, K2, (M, Cc), dtype=np.uint16).view(np.uint8)
+            t["i2r"] = rng.integers(0, K2, (M, Cc), dtype=np.uint16).view(np.uint8)
+        else:
+            t["i2l"] = rng.integers(0, K2, (M, Cc), dtype=np.uint8)
+            t["i2r"] = rng.integers(0, K2, (M, Cc), dtype=np.uint8)
+    if no:
+        t["ocols"] = np.sort(rng.choice(N, no, replace=False)).astype(np.int32)
+        t["oside"] = rng.integers(-127, 128, (M, no), dtype=np.int8)
+        t["oscale"] = f16bits(np.abs(rng.standard_normal(no)) * 0.01 + 0.001)
+    return t
+
+
+PQ_CASES = {
+    "l1": (64, 16, 16, 256, 1, 0, 0),
+    "l2p16": (33, 20, 16, 256, 2, 16, 0),
+    "l2u8": (40, 12, 16, 64, 2, 256, 0),
+    "l2u16": (40, 12, 8, 256, 2, 512, 0, 2),
+    "out8": (48, 16, 16, 256, 1, 0, 8),
+    "out40": (48, 16, 16, 256, 1, 0, 40),
+}
+
+
+def gen_pq(out):
+    rng = np.random.default_rng(99)
+    d = {}
+    for name, args in PQ_CASES.items():
+        t = make_pq(rng, *args)
+        x = rng.standard_normal(t["N"]).astype(np.float32)
+        xs = x.copy()
+        xs[: t["N"] // 2] *= 1e-4                    # chunk-skipping case
+        for k, v in t.items():
+            d[f"{name}.{k}"] = np.asarray(v)
+        d[f"{name}.x"], d[f"{name}.xs"] = x, xs
+        d[f"{name}.y"] = R.pq_matmul(t, x)
+        d[f"{name}.ys"] = R.pq_matmul(t, xs)
+        d[f"{name}.W"] = R.pq_reconstruct(t)
+    np.savez_compressed(os.path.join(out, "pq.npz"), **d)
+
+
+def main():
+    if not R.available():
+        sys.exit("oracle/_ref/libinferbit_ref.so missing: run `make -C oracle ref` first")
+    gen_quant_matvec(HERE)
+    gen_batch(HERE)
+    gen_pq(HERE)
+    for f in sorted(os.listdir(HERE)):
+        if f.endswith(".npz"):
+            print(f, os.path.getsize(os.path.join(HERE, f)))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,242 @@
+"""The C restatement (oracle/ib_oracle.c) against the golden vectors the
+compiled reference wrote (tests/golden/gen_golden.py), bit for bit, and
+against closed forms that do not depend on the reference at all."""
+import numpy as np
+import pytest
+
+from conftest import load_golden, pq_case
+
+SHAPES = ["64x256", "37x200", "16x4100", "8x4096"]
+
+
+def f16(h):
+    return np.asarray(h, np.uint16).view(np.float16).astype(np.float32)
+
+
+def same_bits(a, b):
+    a, b = np.asarray(a), np.asarray(b)
+    assert a.shape == b.shape and a.dtype == b.dtype
+    assert np.array_equal(a.view(np.uint8), b.view(np.uint8))
+
+
+@pytest.mark.parametrize("tag", SHAPES)
+@pytest.mark.parametrize("bits", [8, 4, 2])
+def test_quantizers_match_reference(oracle_lib, tag, bits):
+    q = load_golden("quant.npz")
+    if f"w{bits}_{tag}" not in q.files:
+        pytest.skip("shape not a whole number of bytes at this width")
+    w, s = oracle_lib.quantize(bits, q[f"W_{tag}"])
+    same_bits(w, q[f"w{bits}_{tag}"])
+    same_bits(s, q[f"s{bits}_{tag}"])
+
+
+@pytest.mark.parametrize("tag", SHAPES)
+@pytest.mark.parametrize("bits", [8, 4, 2])
+@pytest.mark.parametrize("order", ["avx2", "scalar"])
+def test_matvec_matches_reference(oracle_lib, tag, bits, order):
+    q, mv = load_golden("quant.npz"), load_golden("matvec.npz")
+    if f"w{bits}_{tag}" not in q.files:
+        pytest.skip("shape not a whole number of bytes at this width")
+    y = oracle_lib.matmul(bits, q[f"w{bits}_{tag}"], f16(q[f"s{bits}_{tag}"]), mv[f"x_{tag}"],
+                          order=1 if order == "avx2" else 0)
+    same_bits(y, mv[f"y{bits}_{order}_{tag}"])
+
+
+@pytest.mark.parametrize("tag", SHAPES)
+def test_w4a8_matches_reference(oracle_lib, tag):
+    q, mv, g = load_golden("quant.npz"), load_golden("matvec.npz"), load_golden("w4a8.npz")
+    qx, sa = oracle_lib.quantize_act(mv[f"x_{tag}"])
+    same_bits(qx, g[f"qx_{tag}"])
+    same_bits(sa, g[f"sa_{tag}"])
+    for order, name in ((1, "avx2"), (0, "scalar")):
+        y = oracle_lib.matmul_w4a8(q[f"w4_{tag}"], f16(q[f"s4_{tag}"]), qx, sa, order)
+        same_bits(y, g[f"y_{name}_{tag}"])
+
+
+def test_act_quantizer_edges(oracle_lib):
+    g = load_golden("w4a8.npz")
+    qx, sa = oracle_lib.quantize_act(g["x_edge"])
+    same_bits(qx, g["qx_edge"])
+    same_bits(sa, g["sa_edge"])
+    assert sa[0] == np.float32(1e-10) and not qx[:128].any()
+
+
+@pytest.mark.parametrize("MN", ["48x256", "33x384"])
+@pytest.mark.parametrize("B", [1, 2, 5, 8])
+def test_batched_match_reference(oracle_lib, MN, B):
+    d = load_golden("batch.npz")
+    tag = f"{MN}_b{B}"
+    M = int(MN.split("x")[0])
+    y8 = oracle_lib.matmul_int8_batch(d[f"w8_{MN}"], f16(d[f"s8_{MN}"]), d[f"X_{tag}"], M + 3)
+    same_bits(y8, d[f"y8_{tag}"])
+    y4 = oracle_lib.matmul_w4a8_batch(d[f"w4_{MN}"], f16(d[f"s4_{MN}"]), d[f"QX_{tag}"], d[f"SA_{tag}"], M + 3)
+    same_bits(y4, d[f"y4_{tag}"])
+
+
+@pytest.mark.parametrize("name", ["l1", "l2p16", "l2u8", "l2u16", "out8", "out40"])
+def test_pq_matches_reference(oracle_lib, name):
+    d = load_golden("pq.npz")
+    t = pq_case(d, name)
+    same_bits(oracle_lib.pq_matmul(t, t["x"]), t["y"])
+    same_bits(oracle_lib.pq_matmul(t, t["xs"]), t["ys"])
+    same_bits(oracle_lib.pq_reconstruct(t), t["W"])
+
+
+# ── closed forms (independent of the reference build) ─────────────────────
+
+@pytest.mark.parametrize("bits", [8, 4, 2])
+def test_one_hot_picks_code_times_scale(oracle_lib, bits):
+    rng = np.random.default_rng(3)
+    M, N = 9, 64
+    W = (rng.standard_normal((M, N)) * 0.02).astype(np.float32)
+    w, s = oracle_lib.quantize(bits, W)
+    sc = f16(s)
+    for j in (0, 1, 2, 3, 17, N - 1):
+        x = np.zeros(N, np.float32)
+        x[j] = 1.0
+        y = oracle_lib.matmul(bits, w, sc, x, order=1)
+        if bits == 8:
+            code = w[:, j].astype(np.float32)
+        elif bits == 4:
+            code = ((w[:, j // 2] >> (4 * (j % 2))) & 15).astype(np.float32) - 8
+        else:
+            code = ((w[:, j // 4] >> (2 * (j % 4))) & 3).astype(np.float32) - 1
+        np.testing.assert_array_equal(y, code * sc)
+
+
+def test_quantizer_roundtrip_bound(oracle_lib):
+    rng = np.random.default_rng(5)
+    W = (rng.standard_normal((16, 128)) * 0.02).astype(np.float32)
+    for bits, qmax in ((8, 127), (4, 7)):
+        w, s = oracle_lib.quantize(bits, W)
+        sc = f16(s)
+        if bits == 4:
+            lo, hi = (w & 15).astype(np.int32) - 8, (w >> 4).astype(np.int32) - 8
+            codes = np.stack([lo, hi], -1).reshape(16, 128)
+        else:
+            codes = w.astype(np.int32)
+        assert np.abs(codes).max() <= qmax
+        deq = codes * sc[:, None]
+        # the scale is truncated toward zero, so the error bound is one step
+        assert np.all(np.abs(deq - W) <= sc[:, None] * 1.0001 + 1e-7)
+
+
+def test_w4a8_on_int8_grid_is_exact(oracle_lib):
+    """With x already on the int8 grid of its group scale, W4A8 equals the
+    exact integer dot times scales (single group so no fold rounding)."""
+    rng = np.random.default_rng(11)
+    M, N = 7, 128
+    w = rng.integers(0, 256, (M, N // 2), dtype=np.uint8)
+    q = rng.integers(-127, 128, N).astype(np.int8)
+    sa = np.array([0.5], np.float32)
+    sw = np.ones(M, np.float32)
+    y = oracle_lib.matmul_w4a8(w, sw, q, sa, 1)
+    codes = np.stack([(w & 15).astype(np.int64) - 8, (w >> 4).astype(np.int64) - 8], -1).reshape(M, N)
+    np.testing.assert_array_equal(y, (codes @ q.astype(np.int64)).astype(np.float32) * 0.5)
+
+
+def test_attention_single_position_returns_v0(oracle_lib):
+    rng = np.random.default_rng(2)
+    n_heads, n_kv, hd = 8, 2, 16
+    for bits in (32, 8, 4):
+        cache = oracle_lib.kv_alloc(bits, 4, n_kv, hd)
+        k = rng.standard_normal(n_kv * hd).astype(np.float32)
+        v = rng.standard_normal(n_kv * hd).astype(np.float32)
+        oracle_lib.kv_write(cache, 0, k, v, n_kv, hd, bits)
+        q = rng.standard_normal(n_heads * hd).astype(np.float32)
+        out = oracle_lib.attn_decode(q, cache, 0, n_heads, n_kv, hd, bits)
+        # softmax of one score is exactly 1, so out = dequantized v
+        if bits == 32:
+            vd = v
+        else:
+            sc = cache[3][:n_kv]
+            if bits == 8:
+                codes = cache[1][: n_kv * hd].view(np.int8).astype(np.float32)
+            else:
+                b = cache[1][: n_kv * hd // 2]
+                codes = np.stack([(b & 15).astype(np.float32) - 8, (b >> 4).astype(np.float32) - 8], -1).ravel()
+            vd = (codes.reshape(n_kv, hd) * sc[:, None]).ravel().astype(np.float32)
+        for h in range(n_heads):
+            kh = h // (n_heads // n_kv)
+            np.testing.assert_array_equal(out[h * hd:(h + 1) * hd], vd[kh * hd:(kh + 1) * hd])
+
+
+def test_attention_identical_keys_is_mean_of_values(oracle_lib):
+    rng = np.random.default_rng(4)
+    n_heads, n_kv, hd, T = 4, 4, 32, 9
+    cache = oracle_lib.kv_alloc(32, T, n_kv, hd)
+    k = rng.standard_normal(n_kv * hd).astype(np.float32)
+    V = rng.standard_normal((T, n_kv * hd)).astype(np.float32)
+    for t in range(T):
+        oracle_lib.kv_write(cache, t, k, V[t], n_kv, hd, 32)
+    q = rng.standard_normal(n_heads * hd).astype(np.float32)
+    out = oracle_lib.attn_decode(q, cache, T - 1, n_heads, n_kv, hd, 32)
+    np.testing.assert_allclose(out, V.mean(0), rtol=1e-5, atol=1e-6)
+
+
+def test_attention_matches_fp64_softmax(oracle_lib):
+    rng = np.random.default_rng(6)
+    n_heads, n_kv, hd, T = 8, 2, 64, 37
+    cache = oracle_lib.kv_alloc(32, T, n_kv, hd)
+    K = rng.standard_normal((T, n_kv * hd)).astype(np.float32)
+    V = rng.standard_normal((T, n_kv * hd)).astype(np.float32)
+    for t in range(T):
+        oracle_lib.kv_write(cache, t, K[t], V[t], n_kv, hd, 32)
+    q = rng.standard_normal(n_heads * hd).astype(np.float32)
+    out = oracle_lib.attn_decode(q, cache, T - 1, n_heads, n_kv, hd, 32)
+    ref = np.zeros(n_heads * hd)
+    for h in range(n_heads):
+        kh = h // (n_heads // n_kv)
+        s = K[:, kh * hd:(kh + 1) * hd].astype(np.float64) @ q[h * hd:(h + 1) * hd] / np.sqrt(hd)
+        a = np.exp(s - s.max())
+        a /= a.sum()
+        ref[h * hd:(h + 1) * hd] = a @ V[:, kh * hd:(kh + 1) * hd]
+    np.testing.assert_allclose(out, ref, rtol=1e-4, atol=1e-5)
+
+
+def test_kv_int8_quantization_rule(oracle_lib):
+    hd, n_kv = 8, 1
+    cache = oracle_lib.kv_alloc(8, 1, n_kv, hd)
+    k = np.array([1, -2, 0.5, 0, 127, -127, 63.5, -63.5], np.float32)
+    oracle_lib.kv_write(cache, 0, k, k, n_kv, hd, 8)
+    assert cache[2][0] == np.float32(1.0)
+    np.testing.assert_array_equal(cache[0][:8].view(np.int8), [1, -2, 1, 0, 127, -127, 64, -64])
+
+
+def test_pq_one_hot_codebook_closed_form(oracle_lib):
+    """K=1 codebooks of all ones: every row equals row_scale * sum(x)."""
+    M, Cc, G = 5, 4, 8
+    N = Cc * G
+    one = np.full((1, G // 2), 1.0, np.float16).view(np.uint16)
+    t = dict(M=M, N=N, G=G, K=1, n_levels=1, n_outlier=0, C=Cc, cb1l=one, cb1r=one,
+             i1l=np.zeros((M, Cc), np.uint8), i1r=np.zeros((M, Cc), np.uint8),
+             row_scale=np.array([1, 2, 0.5, 4, -1], np.float16).view(np.uint16))
+    x = np.arange(N, dtype=np.float32) / 8
+    y = oracle_lib.pq_matmul(t, x)
+    np.testing.assert_allclose(y, np.array([1, 2, 0.5, 4, -1]) * x.sum(), rtol=1e-6)
+
+
+def test_pq_matches_materialized_fp64(oracle_lib):
+    d = load_golden("pq.npz")
+    for name in ("l1", "l2u8", "out8"):
+        t = pq_case(d, name)
+        W = oracle_lib.pq_reconstruct(t).astype(np.float64)
+        y = oracle_lib.pq_matmul(t, t["x"])
+        ref = W @ t["x"].astype(np.float64)
+        # reconstruct rounds weights to fp16; the LUT path keeps fp32
+        assert np.abs(y - ref).max() <= 2e-3 * np.abs(ref).max()
+
+
+def test_fp16_conversions(oracle_lib):
+    import ctypes
+    L = oracle_lib.lib()
+    for h in (0x0000, 0x8000, 0x0001, 0x03ff, 0x0400, 0x3c00, 0x7bff, 0x7c00, 0xfc00, 0xc000):
+        assert np.float32(L.or_fp16_to_fp32(h)).tobytes() == np.array([h], np.uint16).view(
+            np.float16).astype(np.float32).tobytes()
+    for f in (1.0, -2.5, 65504.0, 1e-3, 3.14159, 6.1e-5, 1e-8, 70000.0):
+        assert L.or_fp32_to_fp16_rne(ctypes.c_float(f)) == int(np.array([f], np.float32).astype(
+            np.float16).view(np.uint16)[0])
+        # truncation never rounds up in magnitude
+        t = L.or_fp32_to_fp16_trunc(ctypes.c_float(f))
+        tv = np.array([t], np.uint16).view(np.float16).astype(np.float32)[0]
+        assert abs(tv) <= abs(np.float32(f)) or np.isinf(tv)
