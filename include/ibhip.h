@@ -103,6 +103,28 @@ int ibh_matmul_w4a8_batch(float* out, const void* w, const void* scales, int sca
 int ibh_matmul_int8_batch(float* out, const void* w, const void* scales, int scale_kind,
                           const float* x, int M, int N, int B, int M_stride, void* stream);
 
+/* ── KV cache and attention decode, device pointers ────────── */
+
+/* Quantises K and V of one position into the cache, bit-identical to
+ * kv_cache_write (src/forward.c:352-413).  Layout per layer as
+ * ib_kv_cache (src/inferbit_internal.h:101-109): rows [capacity][row]
+ * with row = 4*kv_dim bytes (kv_bits 32 or 16: fp32 copy), kv_dim int8
+ * (kv_bits 8) or (kv_dim+1)/2 packed nibbles (kv_bits 4, head h at byte
+ * h*((head_dim+1)/2)); scales fp32 [capacity][n_kv] (bits 8/4 only). */
+int ibh_kv_write(void* kdata, void* vdata, float* kscales, float* vscales, int pos,
+                 const float* k, const float* v, int n_kv, int head_dim, int kv_bits, void* stream);
+
+/* Attention of one query position over cache positions 0..pos for all
+ * heads of a layer: ib_attn_head_task (src/forward.c:449-504) for every
+ * head.  q/out [n_heads*head_dim]; head h reads KV head h/(n_heads/n_kv).
+ * `ws` (>= ibh_attn_workspace_bytes(n_heads, head_dim, pos+1) bytes) holds
+ * per-chunk partials; NULL uses the library workspace.  head_dim <= 256,
+ * n_heads/n_kv <= 8. */
+size_t ibh_attn_workspace_bytes(int n_heads, int head_dim, int n_pos);
+int ibh_attn_decode(float* out, const float* q, const void* kdata, const void* vdata,
+                    const float* kscales, const float* vscales, int pos, int n_heads, int n_kv,
+                    int head_dim, int kv_bits, void* ws, size_t ws_bytes, void* stream);
+
 /* ── dispatch-table boundary (host pointers) ───────────────── */
 
 /* Layout-identical mirror of the reference's `ib_kernels`

@@ -30,6 +30,9 @@ SIGNATURES = {
     "ibh_matmul_w4a8_x": (I, [P, P, P, I, P, I, I, P, P, P]),
     "ibh_matmul_w4a8_batch": (I, [P, P, P, I, P, P, I, I, I, I, P]),
     "ibh_matmul_int8_batch": (I, [P, P, P, I, P, I, I, I, I, P]),
+    "ibh_kv_write": (I, [P, P, P, P, I, P, P, I, I, I, P]),
+    "ibh_attn_workspace_bytes": (SZ, [I, I, I]),
+    "ibh_attn_decode": (I, [P, P, P, P, P, P, I, I, I, I, I, P, SZ, P]),
     "ib_init_kernels_hip": (None, [P]),
     "ibh_register_host_weights": (I, [P, SZ, C.POINTER(P)]),
     "ibh_unregister_host_weights": (None, [P]),

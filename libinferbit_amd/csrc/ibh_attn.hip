@@ -1,0 +1,277 @@
+// ibh_attn.hip -- KV-cache write and single-token attention decode (gfx950).
+//
+// Cache layout is the reference's (src/inferbit_internal.h:101-109,
+// src/forward.c:352-445), kept in device memory:
+//   rows [capacity][row_bytes], row_bytes = 4*kv_dim (bits >= 16),
+//   kv_dim (bits 8) or (kv_dim+1)/2 (bits 4, head h at byte h*((hd+1)/2),
+//   low nibble = even dim, +8 bias); scales fp32 [capacity][n_kv].
+//
+// Decode attention is split over the cache length (flash-decoding): block
+// (kv head, chunk of CT positions) reads each K/V row of its chunk once for
+// all the query heads that share the KV head (GQA), computes the chunk's
+// scores, its max, its exp-sum and its unnormalised value sum; a second
+// kernel merges the chunks with the usual log-sum-exp rescaling.  Scores
+// follow forward.c:463-504 (dot of q with the dequantised key, times
+// 1/sqrtf(hd)); exponentials use expf.  Results differ from the CPU only by
+// fp32 summation order.
+#include "ibh_common.h"
+
+using namespace ibh;
+
+namespace {
+
+constexpr int kChunk = 32;       // positions per block
+constexpr int kMaxChunks = 4096; // positions <= kChunk * kMaxChunks
+constexpr int kMaxHd = 256;      // forward.c:466 limits head_dim to 256
+constexpr int kMaxGroup = 8;     // query heads per KV head
+
+// ── KV write (forward.c:352-413) ─────────────────────────────────────────────
+// One wavefront per (K or V, kv head): absmax, scale = max/qmax floored at
+// 1e-8, q = roundf(x * (1/scale)) clamped -- the same operation sequence as
+// the reference, so codes and scales are bit-identical.
+__global__ __launch_bounds__(256) void kv_write_kernel(uint8_t* __restrict__ kd, uint8_t* __restrict__ vd,
+                                                       float* __restrict__ ks, float* __restrict__ vs,
+                                                       const float* __restrict__ k, const float* __restrict__ v,
+                                                       int pos, int n_kv, int hd, int bits) {
+    const int lane = threadIdx.x & 63;
+    const int id = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (id >= 2 * n_kv) return;
+    const int side = id / n_kv, h = id - side * n_kv;
+    const float* src = (side ? v : k) + (size_t)h * hd;
+    uint8_t* dst = side ? vd : kd;
+    float* scl = side ? vs : ks;
+    const int kv_dim = n_kv * hd;
+    if (bits >= 16) {
+        float* row = (float*)dst + (size_t)pos * kv_dim + (size_t)h * hd;
+        for (int d = lane; d < hd; d += 64) row[d] = src[d];
+        return;
+    }
+    float mx = 0.f;
+    for (int d = lane; d < hd; d += 64) mx = fmaxf(mx, fabsf(src[d]));
+    mx = wave_max(mx);
+    float sc = mx / (bits == 8 ? 127.0f : 7.0f);
+    if (sc < 1e-8f) sc = 1e-8f;
+    const float inv = 1.0f / sc;
+    if (lane == 0) scl[(size_t)pos * n_kv + h] = sc;
+    if (bits == 8) {
+        int8_t* row = (int8_t*)dst + (size_t)pos * kv_dim + (size_t)h * hd;
+        for (int d = lane; d < hd; d += 64) {
+            int q = (int)roundf(src[d] * inv);
+            row[d] = (int8_t)(q < -127 ? -127 : (q > 127 ? 127 : q));
+        }
+    } else {
+        uint8_t* row = dst + (size_t)pos * ((kv_dim + 1) / 2) + (size_t)h * ((hd + 1) / 2);
+        for (int i = 2 * lane; i < hd; i += 128) {
+            int q0 = (int)roundf(src[i] * inv);
+            int q1 = i + 1 < hd ? (int)roundf(src[i + 1] * inv) : 0;
+            q0 = q0 < -7 ? -7 : (q0 > 7 ? 7 : q0);
+            q1 = q1 < -7 ? -7 : (q1 > 7 ? 7 : q1);
+            row[i / 2] = (uint8_t)(((q0 + 8) & 0xf) | (((q1 + 8) & 0xf) << 4));
+        }
+    }
+}
+
+// Dequantised element d of head h in cache row t (forward.c:415-445).
+template <int BITS>
+__device__ __forceinline__ float kv_elem(const uint8_t* row, int h, int d, int hd, float scale) {
+    if constexpr (BITS >= 16) {
+        return ((const float*)row)[(size_t)h * hd + d];
+    } else if constexpr (BITS == 8) {
+        return (float)((const int8_t*)row)[(size_t)h * hd + d] * scale;
+    } else {
+        const uint8_t b = row[(size_t)h * ((hd + 1) / 2) + (d >> 1)];
+        return (float)((int)((d & 1) ? (b >> 4) : (b & 0xf)) - 8) * scale;
+    }
+}
+
+// ── attention, partial over one chunk ────────────────────────────────────────
+// Block (kv head kh, chunk c), 256 threads.  The chunk's K rows of head kh
+// are dequantised into LDS (coalesced reads), scores for every query head of
+// the group are computed from LDS, then the chunk max / exp-sum, then the V
+// rows replace K in LDS and threads (d, t-slice) accumulate p_t * v_t[d].
+template <int BITS, int GRP>
+__global__ __launch_bounds__(256) void attn_partial(float* __restrict__ part, const float* __restrict__ q,
+                                                    const uint8_t* __restrict__ kd, const uint8_t* __restrict__ vd,
+                                                    const float* __restrict__ ks, const float* __restrict__ vs,
+                                                    int T, int n_heads, int n_kv, int hd, float scale, int nchunks) {
+    constexpr int CT = kChunk;
+    __shared__ float qs[GRP * kMaxHd];
+    __shared__ float kv[CT * (kMaxHd + 1)];
+    __shared__ float sc[GRP][CT];
+    __shared__ float red[GRP][2];
+    __shared__ float oacc[4][GRP * 64];
+    const int kh = blockIdx.x, c = blockIdx.y;
+    const int grp = n_heads / n_kv;
+    const int t0 = c * CT, tn = min(CT, T - t0);
+    const int kv_dim = n_kv * hd;
+    const int ld = hd + 1;
+    const size_t row_bytes = BITS >= 16 ? (size_t)4 * kv_dim : (BITS == 8 ? (size_t)kv_dim : (size_t)(kv_dim + 1) / 2);
+    for (int i = threadIdx.x; i < grp * hd; i += 256) qs[i] = q[(size_t)kh * grp * hd + i];
+    // K chunk -> LDS
+    for (int i = threadIdx.x; i < tn * hd; i += 256) {
+        const int t = i / hd, d = i - t * hd;
+        const float s_ = BITS >= 16 ? 1.f : ks[(size_t)(t0 + t) * n_kv + kh];
+        kv[t * ld + d] = kv_elem<BITS>(kd + (size_t)(t0 + t) * row_bytes, kh, d, hd, s_);
+    }
+    __syncthreads();
+
+    // scores: thread per (position, head)
+    for (int idx = threadIdx.x; idx < tn * grp; idx += 256) {
+        const int t = idx % tn, g = idx / tn;
+        const float* qh = qs + g * hd;
+        const float* kr = kv + t * ld;
+        float s_ = 0.f;
+        for (int d = 0; d < hd; d++) s_ = fmaf(qh[d], kr[d], s_);
+        sc[g][t] = s_ * scale;
+    }
+    __syncthreads();
+
+    // chunk max and exp-sum per head
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int g = wave; g < grp; g += 4) {
+        float m = -INFINITY;
+        for (int t = lane; t < tn; t += 64) m = fmaxf(m, sc[g][t]);
+        m = wave_max(m);
+        float l = 0.f;
+        for (int t = lane; t < tn; t += 64) {
+            const float p = expf(sc[g][t] - m);
+            sc[g][t] = p;
+            l += p;
+        }
+        l = wave_sum(l);
+        if (lane == 0) { red[g][0] = m; red[g][1] = l; }
+    }
+    // V chunk -> LDS (K no longer needed)
+    for (int i = threadIdx.x; i < tn * hd; i += 256) {
+        const int t = i / hd, d = i - t * hd;
+        const float s_ = BITS >= 16 ? 1.f : vs[(size_t)(t0 + t) * n_kv + kh];
+        kv[t * ld + d] = kv_elem<BITS>(vd + (size_t)(t0 + t) * row_bytes, kh, d, hd, s_);
+    }
+    __syncthreads();
+
+    // o[g][d] = sum_t p[g][t] * v_t[d]; thread = (d in a 64-slot, t-slice of 4)
+    const int ds = threadIdx.x & 63, ts = threadIdx.x >> 6;
+    for (int d0 = 0; d0 < hd; d0 += 64) {
+        const int d = d0 + ds;
+        float acc[GRP];
+#pragma unroll
+        for (int g = 0; g < GRP; g++) acc[g] = 0.f;
+        if (d < hd) {
+            for (int t = ts; t < tn; t += 4) {
+                const float vv = kv[t * ld + d];
+#pragma unroll
+                for (int g = 0; g < GRP; g++)
+                    if (g < grp) acc[g] = fmaf(sc[g][t], vv, acc[g]);
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < GRP; g++) oacc[ts][g * 64 + ds] = acc[g];
+        __syncthreads();
+        for (int i = threadIdx.x; i < grp * 64; i += 256) {
+            const int g = i / 64, dd = i & 63;
+            if (d0 + dd < hd) {
+                const float o = (oacc[0][i] + oacc[1][i]) + (oacc[2][i] + oacc[3][i]);
+                const int h = kh * grp + g;
+                float* pp = part + ((size_t)h * nchunks + c) * (hd + 2);
+                pp[2 + d0 + dd] = o;
+                if (d0 + dd == 0) { pp[0] = red[g][0]; pp[1] = red[g][1]; }
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// ── merge chunks: out[h] = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c ──────
+__global__ __launch_bounds__(256) void attn_combine(float* __restrict__ out, const float* __restrict__ part,
+                                                    int n_heads, int hd, int nchunks) {
+    const int h = blockIdx.x;
+    const float* ph = part + (size_t)h * nchunks * (hd + 2);
+    __shared__ float w[kMaxChunks];
+    __shared__ float denom_s;
+    float M = -INFINITY;
+    for (int c = 0; c < nchunks; c++) M = fmaxf(M, ph[(size_t)c * (hd + 2)]);
+    for (int c = threadIdx.x; c < nchunks; c += 256) w[c] = expf(ph[(size_t)c * (hd + 2)] - M);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float l = 0.f;
+        for (int c = 0; c < nchunks; c++) l = fmaf(w[c], ph[(size_t)c * (hd + 2) + 1], l);
+        denom_s = l;
+    }
+    __syncthreads();
+    const float inv = 1.0f / denom_s;
+    for (int d = threadIdx.x; d < hd; d += 256) {
+        float o = 0.f;
+        for (int c = 0; c < nchunks; c++) o = fmaf(w[c], ph[(size_t)c * (hd + 2) + 2 + d], o);
+        out[(size_t)h * hd + d] = o * inv;
+    }
+}
+
+}  // namespace
+
+void* ibh_workspace(size_t bytes);
+
+extern "C" int ibh_kv_write(void* kdata, void* vdata, float* kscales, float* vscales, int pos, const float* k,
+                            const float* v, int n_kv, int head_dim, int kv_bits, void* stream) {
+    if (!kdata || !vdata || !k || !v || pos < 0 || n_kv <= 0 || head_dim <= 0 ||
+        (kv_bits != 32 && kv_bits != 16 && kv_bits != 8 && kv_bits != 4) ||
+        (kv_bits < 16 && (!kscales || !vscales))) {
+        ibh_set_error("ibh_kv_write: invalid arguments (pos=%d n_kv=%d head_dim=%d bits=%d)", pos, n_kv, head_dim,
+                      kv_bits);
+        return IBH_ERROR_PARAM;
+    }
+    const int waves = 2 * n_kv;
+    kv_write_kernel<<<(waves + 3) / 4, 256, 0, ibh_resolve_stream(stream)>>>(
+        (uint8_t*)kdata, (uint8_t*)vdata, kscales, vscales, k, v, pos, n_kv, head_dim, kv_bits);
+    IBH_CHECK_LAUNCH("ibh_kv_write");
+    return IBH_OK;
+}
+
+extern "C" size_t ibh_attn_workspace_bytes(int n_heads, int head_dim, int n_pos) {
+    const int nchunks = (n_pos + kChunk - 1) / kChunk;
+    return (size_t)n_heads * nchunks * (head_dim + 2) * sizeof(float);
+}
+
+extern "C" int ibh_attn_decode(float* out, const float* q, const void* kdata, const void* vdata,
+                               const float* kscales, const float* vscales, int pos, int n_heads, int n_kv,
+                               int head_dim, int kv_bits, void* ws, size_t ws_bytes, void* stream) {
+    if (!out || !q || !kdata || !vdata || pos < 0 || n_heads <= 0 || n_kv <= 0 || n_heads % n_kv ||
+        n_heads / n_kv > kMaxGroup || head_dim <= 0 || head_dim > kMaxHd ||
+        (kv_bits != 32 && kv_bits != 16 && kv_bits != 8 && kv_bits != 4) ||
+        (kv_bits < 16 && (!kscales || !vscales))) {
+        ibh_set_error("ibh_attn_decode: invalid arguments (pos=%d heads=%d/%d head_dim=%d bits=%d)", pos, n_heads,
+                      n_kv, head_dim, kv_bits);
+        return IBH_ERROR_PARAM;
+    }
+    const int T = pos + 1;
+    const int nchunks = (T + kChunk - 1) / kChunk;
+    if (nchunks > kMaxChunks) {
+        ibh_set_error("ibh_attn_decode: %d positions exceed the supported %d", T, kChunk * kMaxChunks);
+        return IBH_ERROR_CONTEXT;
+    }
+    const size_t need = ibh_attn_workspace_bytes(n_heads, head_dim, T);
+    if (!ws) {
+        ws = ibh_workspace(need);
+        ws_bytes = ws ? need : 0;
+    }
+    if (!ws || ws_bytes < need) {
+        ibh_set_error("ibh_attn_decode: workspace of %zu bytes needed", need);
+        return IBH_ERROR_MEMORY;
+    }
+    hipStream_t st = ibh_resolve_stream(stream);
+    const float scale = 1.0f / sqrtf((float)head_dim);
+    float* part = (float*)ws;
+    dim3 grid(n_kv, nchunks);
+    const uint8_t* K = (const uint8_t*)kdata;
+    const uint8_t* V = (const uint8_t*)vdata;
+    const int grp = n_heads / n_kv;
+#define IBH_AP(B_, G_) attn_partial<B_, G_><<<grid, 256, 0, st>>>(part, q, K, V, kscales, vscales, T, n_heads, n_kv, head_dim, scale, nchunks)
+#define IBH_APG(B_) do { if (grp <= 1) IBH_AP(B_, 1); else if (grp <= 2) IBH_AP(B_, 2); else if (grp <= 4) IBH_AP(B_, 4); \
+                         else IBH_AP(B_, 8); } while (0)
+    if (kv_bits >= 16) IBH_APG(32); else if (kv_bits == 8) IBH_APG(8); else IBH_APG(4);
+#undef IBH_AP
+#undef IBH_APG
+    IBH_CHECK_LAUNCH("ibh_attn_decode (partial)");
+    attn_combine<<<n_heads, 256, 0, st>>>(out, part, n_heads, head_dim, nchunks);
+    IBH_CHECK_LAUNCH("ibh_attn_decode (combine)");
+    return IBH_OK;
+}

@@ -405,20 +405,20 @@ int launch_matmul(float* out, const void* w, const void* scales, const float* x,
     const int cpu = bits == 8 ? 16 : (bits == 4 ? 32 : 64);
     const bool fast = N % cpu == 0 && aligned16(w) && aligned16(x);
     const int path = gemv_path();
-    void* ws = (path == 0 || path == 7) ? ibh_workspace(ibh_digits_bytes(N, bits)) : nullptr;
-    if ((path == 0 || path == 7) && ws &&
-        ibh_launch_gemv_rows_b(out, w, scales, KIND, x, nullptr, nullptr, M, N, bits, ws, st)) {
+    void* ws = path == 7 ? ibh_workspace(ibh_digits_bytes(N, bits)) : nullptr;
+    if ((path == 0 || path == 2) && ibh_launch_gemv_mfma(out, w, scales, KIND, x, M, N, bits, st)) {
+        // 16-row tile matrix-core path (default: fastest measured for fp32 activations)
+    } else if (path == 7 && ws &&
+               ibh_launch_gemv_rows_b(out, w, scales, KIND, x, nullptr, nullptr, M, N, bits, ws, st)) {
         // digit-plane prep + row-owning integer matrix-core GEMV
     } else if (path == 6 && ibh_launch_gemv_rows_i8(out, w, scales, KIND, x, nullptr, nullptr, M, N, bits, st)) {
-        // row-owning integer matrix-core path
+        // row-owning integer matrix-core path, per-block digit prologue
     } else if (path == 5 && ibh_launch_gemv_rows(out, w, scales, KIND, x, M, N, bits, st)) {
-        // row-owning matrix-core path
+        // row-owning f16 matrix-core path
     } else if (path == 4 && ibh_launch_gemv_i8_stream(out, w, scales, KIND, x, nullptr, nullptr, M, N, bits, st)) {
-        // integer matrix-core streaming path
+        // persistent streaming integer matrix-core path
     } else if (path == 1 && ibh_launch_gemv_stream(out, w, scales, KIND, x, M, N, bits, st)) {
-        // streaming matrix-core path
-    } else if (path == 2 && ibh_launch_gemv_mfma(out, w, scales, KIND, x, M, N, bits, st)) {
-        // matrix-core path
+        // persistent streaming f16 matrix-core path
     } else if (fast) {
         const int blocks = (M + R * kWavesPerBlock - 1) / (R * kWavesPerBlock);
         if (bits == 8) gemv_f32_fast<8, KIND, R><<<blocks, kBlock, 0, st>>>(out, W, scales, x, M, N);

@@ -82,7 +82,35 @@ __device__ __forceinline__ int seg_of(int lane) {
 }
 
 constexpr int kMaxWaves = 16;
+constexpr int kMaxWavesB = 8;       // gemv_rows_b blocks (<= 512 threads: room for 256 VGPRs)
 constexpr int kMaxRowsPerBlock = 32;
+
+// Sum of the diagonal lanes' values (lanes 0-3, 20-23, 40-43, 60-63 hold
+// D[i][i]; every other lane passes 0): quad sums with DPP, then the four
+// quad sums read into scalars.  Uniform result, no LDS round trip.
+__device__ __forceinline__ float diag_sum(float v) {
+    int b = __builtin_bit_cast(int, v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(b, 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+    b = __builtin_bit_cast(int, v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(b, 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+    b = __builtin_bit_cast(int, v);
+    const float q0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+    const float q1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 20));
+    const float q2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 40));
+    const float q3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 60));
+    return (q0 + q1) + (q2 + q3);
+}
+
+// Rows per wavefront for fp32 activations (IBH_ROWS_R=4|8 overrides).
+int ibh_rows_r() {
+    static int r = -1;
+    if (r < 0) {
+        const char* e = getenv("IBH_ROWS_R");
+        r = e ? atoi(e) : 8;
+        if (r != 4 && r != 8) r = 8;
+    }
+    return r;
+}
 
 // Row groups per block (IBH_ROWS_WR overrides, for tuning).
 int ibh_rows_wr() {
@@ -396,7 +424,7 @@ __global__ __launch_bounds__(256) void x_to_digits(const float* __restrict__ x, 
 }
 
 template <int BITS, int KIND, bool W4A8, int R, int SPW>
-__global__ __launch_bounds__(1024) void gemv_rows_b(float* __restrict__ y,
+__global__ __launch_bounds__(512) void gemv_rows_b(float* __restrict__ y,
                                                     const uint8_t* __restrict__ W,
                                                     const void* __restrict__ sc,
                                                     const uint4* __restrict__ xb,
@@ -418,8 +446,10 @@ __global__ __launch_bounds__(1024) void gemv_rows_b(float* __restrict__ y,
     const int row0 = blockIdx.x * RB + wr * R;
     const size_t rb = (size_t)N * BITS / 8;
     const int G = (N + 127) / 128;
-    float* sa_s = (float*)smem;                            // [G]      (W4A8)
-    float* gsum = sa_s + G;                                // [RB][G]  (W4A8)
+    const int Gp = (G + 3) & ~3;                           // padded LDS row stride
+    float* gsum = (float*)smem;                            // [RB][Gp]      (W4A8)
+    float* sa_s_all = gsum + (size_t)RB * Gp;              // [waves][Gp]   (W4A8)
+    float* sa_s = sa_s_all + (size_t)(threadIdx.x >> 6) * Gp;
     const int segl = seg_of<W4A8>(lane);
 
     // ---- small operands first: they are waited for before the weights -------
@@ -427,7 +457,8 @@ __global__ __launch_bounds__(1024) void gemv_rows_b(float* __restrict__ y,
     if (threadIdx.x < RB) rowscale = load_scale<KIND>(sc, min(blockIdx.x * RB + (int)threadIdx.x, M - 1));
     StepHeader sh[SPW];
     if constexpr (W4A8) {
-        for (int g = threadIdx.x; g < G; g += blockDim.x) sa_s[g] = sa[g];
+        // each wavefront stages its own copy of sa (no block barrier needed)
+        for (int g = lane; g < G; g += 64) sa_s[g] = sa[g];
     } else {
 #pragma unroll
         for (int j = 0; j < SPW; j++) sh[j] = hdr[min(wk * SPW + j, S - 1)];
@@ -499,7 +530,7 @@ __global__ __launch_bounds__(1024) void gemv_rows_b(float* __restrict__ y,
             const int g = 16 * s + (lane & 15);
             if (live[j] && diag && g < G) {
 #pragma unroll
-                for (int r = 0; r < R; r++) gsum[(size_t)(wr * R + r) * G + g] = (float)(dval(acc[r][0]) >> 4);
+                for (int r = 0; r < R; r++) gsum[(size_t)(wr * R + r) * Gp + g] = (float)(dval(acc[r][0]) >> 4);
             }
         } else {
             const float st = live[j] ? sh[j].scale : 0.f;
@@ -513,11 +544,19 @@ __global__ __launch_bounds__(1024) void gemv_rows_b(float* __restrict__ y,
 
     // ---- combine ------------------------------------------------------------------
     if constexpr (W4A8) {
-        __syncthreads();
-        const int t = threadIdx.x;
-        const int row = blockIdx.x * RB + t;
-        if (t < RB && row < M) {
-            const float* gp = gsum + (size_t)t * G;
+        // every group of the block's rows is in gsum; fold in group order
+        if (KW == 1) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        } else {
+            __syncthreads();
+        }
+        const int fr = KW == 1 ? wr * R + lane : (int)threadIdx.x;     // local row folded by this thread
+        const bool folder = KW == 1 ? lane < R : threadIdx.x < RB;
+        const int row = blockIdx.x * RB + fr;
+        if (folder && row < M) {
+            const float* gp = gsum + (size_t)fr * Gp;
             float f = 0.f;
             int g = 0;
             for (; g + 4 <= G; g += 4) {
@@ -525,23 +564,35 @@ __global__ __launch_bounds__(1024) void gemv_rows_b(float* __restrict__ y,
                 f = fmaf(a4.x, s4.x, f); f = fmaf(a4.y, s4.y, f); f = fmaf(a4.z, s4.z, f); f = fmaf(a4.w, s4.w, f);
             }
             for (; g < G; g++) f = fmaf(gp[g], sa_s[g], f);
-            y[row] = f * rowscale;
+            const float rs = KW == 1 ? load_scale<KIND>(sc, row) : rowscale;
+            y[row] = f * rs;
         }
     } else {
+        float tot[R];
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            const float v = wave_sum(accf[r]);
-            if (lane == 0) part[wave][r] = v - corr;
-        }
-        __syncthreads();
-        const int t = threadIdx.x;
-        if (t < RB) {
-            const int w_r = t / R, r = t - w_r * R;
-            const int row = blockIdx.x * RB + t;
-            if (row < M) {
-                float v = 0.f;
-                for (int k = 0; k < KW; k++) v += part[w_r * KW + k][r];
-                y[row] = v * rowscale;
+        for (int r = 0; r < R; r++) tot[r] = diag_sum(diag ? accf[r] : 0.f) - corr;
+        if (KW == 1) {
+            if (lane < R && row0 + lane < M) {
+                float v = tot[0];
+#pragma unroll
+                for (int r = 1; r < R; r++) v = lane == r ? tot[r] : v;
+                y[row0 + lane] = v * load_scale<KIND>(sc, row0 + lane);
+            }
+        } else {
+            if (lane == 0) {
+#pragma unroll
+                for (int r = 0; r < R; r++) part[wave][r] = tot[r];
+            }
+            __syncthreads();
+            const int t = threadIdx.x;
+            if (t < RB) {
+                const int w_r = t / R, r = t - w_r * R;
+                const int row = blockIdx.x * RB + t;
+                if (row < M) {
+                    float v = 0.f;
+                    for (int k = 0; k < KW; k++) v += part[w_r * KW + k][r];
+                    y[row] = v * rowscale;
+                }
             }
         }
     }
@@ -570,13 +621,14 @@ int ibh_launch_gemv_rows_b(float* out, const void* w, const void* scales, int ki
     const int S = (int)((rb + 1023) / 1024);
     const int spw = S == 1 ? 1 : 2;
     const int KW = (S + spw - 1) / spw;
-    constexpr int R = 4;
+    const int R = w4a8 ? 4 : ibh_rows_r();
     int WR = ibh_rows_wr();
-    while (WR > 1 && WR * KW > kMaxWaves) WR >>= 1;
-    if (WR * KW > kMaxWaves) return 0;
+    while (WR > 1 && WR * KW > kMaxWavesB) WR >>= 1;
+    if (WR * KW > kMaxWavesB) return 0;
     const int nthreads = 64 * WR * KW;
     const int G = (N + 127) / 128;
-    const size_t lds = w4a8 ? (size_t)(G + WR * R * G) * 4 : 0;
+    const int Gp = (G + 3) & ~3;
+    const size_t lds = w4a8 ? (size_t)(WR * KW * Gp + WR * R * Gp) * 4 : 0;
     if (lds > 64 * 1024) return 0;
     const int blocks = (M + WR * R - 1) / (WR * R);
     const uint8_t* W = (const uint8_t*)w;
@@ -589,9 +641,10 @@ int ibh_launch_gemv_rows_b(float* out, const void* w, const void* scales, int ki
         else if (bits == 4) x_to_digits<4><<<pb, 256, 0, st>>>(x, xb, hdr, N, S);
         else x_to_digits<2><<<pb, 256, 0, st>>>(x, xb, hdr, N, S);
     }
-#define IBH_RB(B_, K_, Q_, SP_) \
-    gemv_rows_b<B_, K_, Q_, R, SP_><<<blocks, nthreads, lds, st>>>(out, W, scales, xb, hdr, qx, sa, M, N, S, WR, KW)
-#define IBH_RBS(B_, K_, Q_) do { if (spw == 2) IBH_RB(B_, K_, Q_, 2); else IBH_RB(B_, K_, Q_, 1); } while (0)
+#define IBH_RB(B_, K_, Q_, R_, SP_) \
+    gemv_rows_b<B_, K_, Q_, R_, SP_><<<blocks, nthreads, lds, st>>>(out, W, scales, xb, hdr, qx, sa, M, N, S, WR, KW)
+#define IBH_RBR(B_, K_, Q_, R_) do { if (spw == 2) IBH_RB(B_, K_, Q_, R_, 2); else IBH_RB(B_, K_, Q_, R_, 1); } while (0)
+#define IBH_RBS(B_, K_, Q_) do { if (R == 8 && !Q_) IBH_RBR(B_, K_, Q_, 8); else IBH_RBR(B_, K_, Q_, 4); } while (0)
     if (w4a8) {
         if (kind == IBH_SCALE_F16) IBH_RBS(4, IBH_SCALE_F16, true); else IBH_RBS(4, IBH_SCALE_F32, true);
     } else if (kind == IBH_SCALE_F16) {
@@ -601,5 +654,6 @@ int ibh_launch_gemv_rows_b(float* out, const void* w, const void* scales, int ki
     }
 #undef IBH_RB
 #undef IBH_RBS
+#undef IBH_RBR
     return 1;
 }

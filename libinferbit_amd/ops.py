@@ -74,3 +74,20 @@ def matmul_int8_batch(out, w, scales_w, x, M: int, N: int, B: int, M_stride: int
     """ib_kern.matmul_int8_batch (src/kernels/scalar.c:70-84)."""
     check(lib().ibh_matmul_int8_batch(_ptr(out), _ptr(w), _ptr(scales_w), _scale_kind(scales_w), _ptr(x), M,
                                       N, B, M_stride, _stream()), "ibh_matmul_int8_batch")
+
+
+def _optptr(t):
+    return None if t is None else _ptr(t)
+
+
+def kv_cache_write(kdata, vdata, kscales, vscales, pos: int, k, v, n_kv: int, head_dim: int, kv_bits: int) -> None:
+    """kv_cache_write (src/forward.c:352-413) into device cache tensors."""
+    check(lib().ibh_kv_write(_ptr(kdata), _ptr(vdata), _optptr(kscales), _optptr(vscales), pos, _ptr(k), _ptr(v),
+                             n_kv, head_dim, kv_bits, _stream()), "ibh_kv_write")
+
+
+def attn_decode(out, q, kdata, vdata, kscales, vscales, pos: int, n_heads: int, n_kv: int, head_dim: int,
+                kv_bits: int) -> None:
+    """ib_attn_head_task for all heads of a layer (src/forward.c:449-504)."""
+    check(lib().ibh_attn_decode(_ptr(out), _ptr(q), _ptr(kdata), _ptr(vdata), _optptr(kscales), _optptr(vscales),
+                                pos, n_heads, n_kv, head_dim, kv_bits, None, 0, _stream()), "ibh_attn_decode")
