@@ -125,6 +125,33 @@ int ibh_attn_decode(float* out, const float* q, const void* kdata, const void* v
                     const float* kscales, const float* vscales, int pos, int n_heads, int n_kv,
                     int head_dim, int kv_bits, void* ws, size_t ws_bytes, void* stream);
 
+/* ── product-quantised LUT matvec, device pointers ─────────── */
+
+/* Device-resident mirror of ib_pq_tensor (src/pq_decode.h:39-87): same
+ * fields and array layouts, pointers into device memory.  inner_cols (the
+ * N - n_outlier non-outlier columns in increasing order, which
+ * matmul_impl rebuilds on every call at src/pq_decode.c:1538-1546) is
+ * computed once at upload; it may be NULL when n_outlier == 0. */
+typedef struct {
+    int M, N, G, K, K_l2, n_levels, n_outlier, C, l2_idx_bytes;
+    const uint16_t *codebook_l1_l, *codebook_l1_r, *codebook_l2_l, *codebook_l2_r;
+    const uint8_t *indices_l1_l, *indices_l1_r, *indices_l2_l, *indices_l2_r;
+    const uint16_t* row_scale;
+    const int32_t* outlier_cols;
+    const int8_t* outlier_sidecar;
+    const uint16_t* outlier_scale;
+    const int32_t* inner_cols;
+} ibh_pq_tensor;
+
+/* out[M] = W x for a PQ tensor, replacing ib_pq_matmul_fp32 /
+ * ib_pq_matmul_fp32_threaded (src/pq_decode.c:1684-1810): same chunk
+ * skipping rule, tables, gather and outlier sidecar; fp32 summation order
+ * differs.  Returns 0 / negative like the reference (plus a message).
+ * `ws` >= ibh_pq_workspace_bytes(t) bytes, NULL = library workspace. */
+size_t ibh_pq_workspace_bytes(const ibh_pq_tensor* t);
+int    ibh_pq_matmul(const ibh_pq_tensor* t, const float* x, float* out, void* ws,
+                     size_t ws_bytes, void* stream);
+
 /* ── dispatch-table boundary (host pointers) ───────────────── */
 
 /* Layout-identical mirror of the reference's `ib_kernels`

@@ -33,6 +33,8 @@ SIGNATURES = {
     "ibh_kv_write": (I, [P, P, P, P, I, P, P, I, I, I, P]),
     "ibh_attn_workspace_bytes": (SZ, [I, I, I]),
     "ibh_attn_decode": (I, [P, P, P, P, P, P, I, I, I, I, I, P, SZ, P]),
+    "ibh_pq_workspace_bytes": (SZ, [P]),
+    "ibh_pq_matmul": (I, [P, P, P, P, SZ, P]),
     "ib_init_kernels_hip": (None, [P]),
     "ibh_register_host_weights": (I, [P, SZ, C.POINTER(P)]),
     "ibh_unregister_host_weights": (None, [P]),
@@ -74,3 +76,11 @@ def lib():
 def check(rc: int, where: str) -> None:
     if rc != 0:
         raise IbhError(rc, where)
+
+
+class PqTensor(C.Structure):
+    """ibh_pq_tensor (include/ibhip.h)."""
+    _fields_ = [(n, I) for n in ("M", "N", "G", "K", "K_l2", "n_levels", "n_outlier", "C", "l2_idx_bytes")] + \
+               [(n, P) for n in ("codebook_l1_l", "codebook_l1_r", "codebook_l2_l", "codebook_l2_r",
+                                 "indices_l1_l", "indices_l1_r", "indices_l2_l", "indices_l2_r", "row_scale",
+                                 "outlier_cols", "outlier_sidecar", "outlier_scale", "inner_cols")]

@@ -1,0 +1,258 @@
+// ibh_pq.hip -- product-quantised (PQ) LUT matvec, ib_pq_matmul_fp32
+// (src/pq_decode.c:1504-1686) on gfx950.
+//
+// Tensor layout is the reference's (src/pq_decode.h:39-87), uploaded as is:
+// fp16 codebooks [K][G/2] per side (one L and one R codebook shared by all
+// chunks, plus the level-2 pair), uint8 indices [M][C] per side (level-2:
+// uint8, uint16 or 4-bit packed), fp16 row scales, outlier sidecar.
+//
+// out[r] = row_scale[r] * sum_c (T_L[c][iL[r,c]] + T_R[c][iR[r,c]] (+ L2))
+//          + outlier terms,
+// T_side[c][k] = codebook_side[k] . x[inner columns of chunk c, that side].
+//
+// Kernel 1 (slab): block (row tile, chunk slab).  Every block finds the
+// global max|x| over the inner columns (chunk-skipping rule of
+// pq_decode.c:1569-1616: chunks whose max|x| is below 1% of it are left out),
+// builds the slab's tables in LDS (CS chunks x K entries x 2 sides, the
+// table entries in the reference's operation order), then each thread walks
+// its rows: CS index bytes per side from one 16-byte load, 2*CS LDS gathers.
+// The per-slab partial sums go to a workspace.
+// Kernel 2 (reduce): sums the slabs in order, applies the row scale and the
+// outlier sidecar (the x86 rules of pq_decode.c:1233-1421: int8-quantised
+// dot for >= 32 outliers, fp32 otherwise).
+// The chunk sum is associated slab by slab instead of strictly serially, so
+// results differ from the CPU by fp32 rounding only.
+#include "ibh_common.h"
+
+using namespace ibh;
+
+namespace {
+
+constexpr int kRowsPerBlock = 512;    // rows of one slab block (2 per thread)
+constexpr int kThreads = 256;
+
+struct PqDev {
+    int M, N, G, K, K2, n_levels, n_outlier, C, l2_idx_bytes;
+    const uint16_t *cb1l, *cb1r, *cb2l, *cb2r;
+    const uint8_t *i1l, *i1r, *i2l, *i2r;
+    const uint16_t* row_scale;
+    const int32_t* ocols;
+    const int8_t* oside;
+    const uint16_t* oscale;
+    const int32_t* inner;    // inner (non-outlier) columns, null when n_outlier == 0
+};
+
+__device__ __forceinline__ int inner_col(const PqDev& t, int j) { return t.inner ? t.inner[j] : j; }
+
+__device__ __forceinline__ int l2_at(const PqDev& t, const uint8_t* row, int c) {
+    if (t.K2 == 16) { const uint8_t b = row[c >> 1]; return (c & 1) ? (b >> 4) : (b & 0xf); }
+    if (t.l2_idx_bytes == 2) return ((const uint16_t*)row)[c];
+    return row[c];
+}
+
+__device__ __forceinline__ size_t l2_stride(const PqDev& t) {
+    if (t.K2 == 16) return (size_t)(t.C + 1) / 2;
+    return (size_t)t.C * (t.l2_idx_bytes == 2 ? 2 : 1);
+}
+
+// sum_i cb[i] * x[i]: products of the first hf&~3 terms rounded then added
+// in order, remaining terms fused (the x86 build's evaluation of
+// pq_decode.c:1621-1659).
+__device__ __forceinline__ float table_entry(const uint16_t* cb, const float* xv, int hf) {
+    float s = 0.f;
+    const int v = hf & ~3;
+    int i = 0;
+    for (; i < v; i++) s = s + f16_to_f32(cb[i]) * xv[i];
+    for (; i < hf; i++) s = fmaf(f16_to_f32(cb[i]), xv[i], s);
+    return s;
+}
+
+template <bool TWO>
+__global__ __launch_bounds__(kThreads) void pq_slab(PqDev t, const float* __restrict__ x,
+                                                    float* __restrict__ part, int CS) {
+    extern __shared__ __align__(16) float sm[];
+    __shared__ float red[kThreads / 64];
+    __shared__ int act_s[64];
+    const int K = t.K, K2 = t.K2, G = t.G, hf = G / 2, C = t.C;
+    float* T1 = sm;                                   // [CS][2][K]
+    float* T2 = T1 + (size_t)CS * 2 * K;              // [CS][2][K2]  (TWO)
+    float* xs = TWO ? T2 + (size_t)CS * 2 * K2 : T2;  // [CS][G]
+    const int c0 = blockIdx.y * CS;
+    const int cn = min(CS, C - c0);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n_inner = t.N - t.n_outlier;
+
+    // global max |x| over the inner columns
+    float mx = 0.f;
+    for (int j = threadIdx.x; j < n_inner; j += kThreads) mx = fmaxf(mx, fabsf(x[inner_col(t, j)]));
+    mx = wave_max(mx);
+    if (lane == 0) red[wave] = mx;
+    // this slab's activations
+    for (int i = threadIdx.x; i < cn * G; i += kThreads) xs[i] = x[inner_col(t, c0 * G + i)];
+    __syncthreads();
+    float gmax = 0.f;
+    for (int w = 0; w < kThreads / 64; w++) gmax = fmaxf(gmax, red[w]);
+    const float th = gmax * 0.01f;
+    if (threadIdx.x < cn) {
+        float cm = 0.f;
+        for (int i = 0; i < G; i++) cm = fmaxf(cm, fabsf(xs[threadIdx.x * G + i]));
+        act_s[threadIdx.x] = gmax > 0.f ? (cm >= th) : 1;
+    }
+    // tables
+    for (int e = threadIdx.x; e < cn * 2 * K; e += kThreads) {
+        const int c = e / (2 * K), side = (e / K) & 1, k = e % K;
+        const uint16_t* cb = (side ? t.cb1r : t.cb1l) + (size_t)k * hf;
+        T1[e] = table_entry(cb, xs + c * G + side * hf, hf);
+    }
+    if (TWO) {
+        for (int e = threadIdx.x; e < cn * 2 * K2; e += kThreads) {
+            const int c = e / (2 * K2), side = (e / K2) & 1, k = e % K2;
+            const uint16_t* cb = (side ? t.cb2r : t.cb2l) + (size_t)k * hf;
+            T2[e] = table_entry(cb, xs + c * G + side * hf, hf);
+        }
+    }
+    __syncthreads();
+
+    // gather: rows of this tile
+    const size_t l2s = TWO ? l2_stride(t) : 0;
+    for (int rr = threadIdx.x; rr < kRowsPerBlock; rr += kThreads) {
+        const int r = blockIdx.x * kRowsPerBlock + rr;
+        if (r >= t.M) break;
+        const uint8_t* il = t.i1l + (size_t)r * C + c0;
+        const uint8_t* ir = t.i1r + (size_t)r * C + c0;
+        const uint8_t* i2l = TWO ? t.i2l + (size_t)r * l2s : nullptr;
+        const uint8_t* i2r = TWO ? t.i2r + (size_t)r * l2s : nullptr;
+        float acc = 0.f;
+        for (int c = 0; c < cn; c++) {
+            if (!act_s[c]) continue;
+            const float* tc = T1 + (size_t)c * 2 * K;
+            acc = acc + (tc[il[c]] + tc[K + ir[c]]);
+            if (TWO) {
+                const float* t2 = T2 + (size_t)c * 2 * K2;
+                acc = acc + (t2[l2_at(t, i2l, c0 + c)] + t2[K2 + l2_at(t, i2r, c0 + c)]);
+            }
+        }
+        part[(size_t)blockIdx.y * t.M + r] = acc;
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void pq_reduce(PqDev t, const float* __restrict__ x,
+                                                      const float* __restrict__ part, int nslabs,
+                                                      float* __restrict__ out) {
+    __shared__ int8_t qq_s[1024];
+    __shared__ float meta_s;
+    const int no = t.n_outlier;
+    const bool quant = no >= 32;
+    if (quant) {
+        // x * col_scale quantised with one meta scale (pq_decode.c:274-301)
+        if (threadIdx.x == 0) {
+            float mx = 0.f;
+            for (int j = 0; j < no; j++) {
+                const float v = x[t.ocols[j]] * f16_to_f32(t.oscale[j]);
+                const float a = v < 0 ? -v : v;
+                if (a > mx) mx = a;
+            }
+            meta_s = mx > 0.f ? mx / 127.0f : 1.0f;
+        }
+        __syncthreads();
+        const float inv = 1.0f / meta_s;
+        for (int j = threadIdx.x; j < no; j += kThreads) {
+            const float sv = (x[t.ocols[j]] * f16_to_f32(t.oscale[j])) * inv;
+            const int v = (int)(sv >= 0 ? sv + 0.5f : sv - 0.5f);
+            qq_s[j] = (int8_t)(v > 127 ? 127 : (v < -128 ? -128 : v));
+        }
+        __syncthreads();
+    }
+    const int r = blockIdx.x * kThreads + threadIdx.x;
+    if (r >= t.M) return;
+    float acc = 0.f;
+    for (int s = 0; s < nslabs; s++) acc += part[(size_t)s * t.M + r];
+    float y = acc * f16_to_f32(t.row_scale[r]);
+    if (no > 0) {
+        const int8_t* side = t.oside + (size_t)r * no;
+        if (quant) {
+            int32_t sum = 0;
+            for (int j = 0; j < no; j++) sum += (int32_t)side[j] * (int32_t)qq_s[j];
+            y = fmaf((float)sum, meta_s, y);
+        } else {
+            for (int j = 0; j < no; j++)
+                y = fmaf((float)side[j] * f16_to_f32(t.oscale[j]), x[t.ocols[j]], y);
+        }
+    }
+    out[r] = y;
+}
+
+}  // namespace
+
+void* ibh_workspace(size_t bytes);
+
+typedef ibh_pq_tensor ibh_pq_tensor_abi;
+
+static int pq_geometry(const ibh_pq_tensor_abi* t, int* CS, int* nslabs, size_t* lds, size_t* ws_need) {
+    const bool two = t->n_levels == 2;
+    const int K2 = t->K_l2 > 0 ? t->K_l2 : t->K;
+    int cs = 16;
+    auto need = [&](int c) { return (size_t)c * 2 * t->K * 4 + (two ? (size_t)c * 2 * K2 * 4 : 0) + (size_t)c * t->G * 4; };
+    while (cs > 1 && need(cs) > 60 * 1024) cs >>= 1;
+    if (need(cs) > 60 * 1024) return IBH_ERROR_PARAM;
+    *CS = cs;
+    *nslabs = (t->C + cs - 1) / cs;
+    *lds = need(cs);
+    *ws_need = (size_t)(*nslabs) * t->M * sizeof(float);
+    return IBH_OK;
+}
+
+extern "C" size_t ibh_pq_workspace_bytes(const ibh_pq_tensor_abi* t) {
+    int cs, ns;
+    size_t lds, need;
+    return t && pq_geometry(t, &cs, &ns, &lds, &need) == IBH_OK ? need : 0;
+}
+
+extern "C" int ibh_pq_matmul(const ibh_pq_tensor_abi* t, const float* x, float* out, void* ws, size_t ws_bytes,
+                             void* stream) {
+    if (!t || !x || !out || t->M <= 0 || t->C <= 0 || t->G <= 0 || t->G % 2 || t->K <= 0 || t->K > 65536 ||
+        !t->codebook_l1_l || !t->codebook_l1_r || !t->indices_l1_l || !t->indices_l1_r || !t->row_scale ||
+        t->N != t->C * t->G + t->n_outlier || t->n_outlier < 0 || t->n_outlier > 1024 ||
+        (t->n_outlier > 0 && (!t->outlier_cols || !t->outlier_sidecar || !t->outlier_scale || !t->inner_cols)) ||
+        (t->n_levels == 2 && (!t->codebook_l2_l || !t->codebook_l2_r || !t->indices_l2_l || !t->indices_l2_r)) ||
+        (t->n_levels != 1 && t->n_levels != 2)) {
+        ibh_set_error("ibh_pq_matmul: invalid tensor");
+        return IBH_ERROR_PARAM;
+    }
+    if (t->K > 256 && t->n_levels == 1) {
+        // level-1 indices are uint8 (pq_decode.h:59-60)
+        ibh_set_error("ibh_pq_matmul: K=%d exceeds uint8 level-1 indices", t->K);
+        return IBH_ERROR_PARAM;
+    }
+    int CS, nslabs;
+    size_t lds, need;
+    if (pq_geometry(t, &CS, &nslabs, &lds, &need) != IBH_OK) {
+        ibh_set_error("ibh_pq_matmul: codebooks too large for the LDS tables");
+        return IBH_ERROR_PARAM;
+    }
+    if (!ws) {
+        ws = ibh_workspace(need);
+        ws_bytes = ws ? need : 0;
+    }
+    if (!ws || ws_bytes < need) {
+        ibh_set_error("ibh_pq_matmul: workspace of %zu bytes needed", need);
+        return IBH_ERROR_MEMORY;
+    }
+    PqDev d;
+    d.M = t->M; d.N = t->N; d.G = t->G; d.K = t->K; d.K2 = t->K_l2 > 0 ? t->K_l2 : t->K;
+    d.n_levels = t->n_levels; d.n_outlier = t->n_outlier; d.C = t->C;
+    d.l2_idx_bytes = t->l2_idx_bytes > 0 ? t->l2_idx_bytes : 1;
+    d.cb1l = t->codebook_l1_l; d.cb1r = t->codebook_l1_r; d.cb2l = t->codebook_l2_l; d.cb2r = t->codebook_l2_r;
+    d.i1l = t->indices_l1_l; d.i1r = t->indices_l1_r; d.i2l = t->indices_l2_l; d.i2r = t->indices_l2_r;
+    d.row_scale = t->row_scale; d.ocols = t->outlier_cols; d.oside = t->outlier_sidecar;
+    d.oscale = t->outlier_scale; d.inner = t->n_outlier > 0 ? t->inner_cols : nullptr;
+    hipStream_t st = ibh_resolve_stream(stream);
+    float* part = (float*)ws;
+    dim3 grid((t->M + kRowsPerBlock - 1) / kRowsPerBlock, nslabs);
+    if (t->n_levels == 2) pq_slab<true><<<grid, kThreads, lds, st>>>(d, x, part, CS);
+    else pq_slab<false><<<grid, kThreads, lds, st>>>(d, x, part, CS);
+    IBH_CHECK_LAUNCH("ibh_pq_matmul (slab)");
+    pq_reduce<<<(t->M + kThreads - 1) / kThreads, kThreads, 0, st>>>(d, x, part, nslabs, out);
+    IBH_CHECK_LAUNCH("ibh_pq_matmul (reduce)");
+    return IBH_OK;
+}

@@ -11,7 +11,11 @@ from __future__ import annotations
 
 import torch
 
-from ._lib import check, lib
+import ctypes
+
+import numpy as np
+
+from ._lib import PqTensor, check, lib
 
 SCALE_F16, SCALE_F32 = 0, 1
 
@@ -91,3 +95,44 @@ def attn_decode(out, q, kdata, vdata, kscales, vscales, pos: int, n_heads: int, 
     """ib_attn_head_task for all heads of a layer (src/forward.c:449-504)."""
     check(lib().ibh_attn_decode(_ptr(out), _ptr(q), _ptr(kdata), _ptr(vdata), _optptr(kscales), _optptr(vscales),
                                 pos, n_heads, n_kv, head_dim, kv_bits, None, 0, _stream()), "ibh_attn_decode")
+
+
+class PqDeviceTensor:
+    """A PQ tensor (ib_pq_tensor layout, src/pq_decode.h:39-87) uploaded to the
+    GPU once.  `t` maps the reference field names used by the oracle
+    (cb1l, cb1r, cb2l, cb2r, i1l, i1r, i2l, i2r, row_scale, ocols, oside,
+    oscale) and sizes (M, N, G, K, K_l2, n_levels, n_outlier, C,
+    l2_idx_bytes) to numpy arrays / ints."""
+
+    _MAP = {"cb1l": "codebook_l1_l", "cb1r": "codebook_l1_r", "cb2l": "codebook_l2_l", "cb2r": "codebook_l2_r",
+            "i1l": "indices_l1_l", "i1r": "indices_l1_r", "i2l": "indices_l2_l", "i2r": "indices_l2_r",
+            "row_scale": "row_scale", "ocols": "outlier_cols", "oside": "outlier_sidecar",
+            "oscale": "outlier_scale"}
+
+    def __init__(self, t: dict):
+        import torch
+        self.keep = []
+        s = PqTensor()
+        for n in ("M", "N", "G", "K", "n_levels", "n_outlier", "C"):
+            setattr(s, n, int(t[n]))
+        s.K_l2 = int(t.get("K_l2", 0))
+        s.l2_idx_bytes = int(t.get("l2_idx_bytes", 1))
+        for k, f in self._MAP.items():
+            a = t.get(k)
+            if a is not None:
+                d = torch.from_numpy(np.ascontiguousarray(a).view(np.uint8).reshape(-1).copy()).cuda()
+                self.keep.append(d)
+                setattr(s, f, d.data_ptr())
+        if s.n_outlier > 0:
+            mask = np.ones(s.N, bool)
+            mask[np.asarray(t["ocols"])] = False
+            inner = np.nonzero(mask)[0].astype(np.int32)
+            d = torch.from_numpy(inner.view(np.uint8).copy()).cuda()
+            self.keep.append(d)
+            s.inner_cols = d.data_ptr()
+        self.s = s
+        self.M = s.M
+
+    def matmul(self, x, out) -> None:
+        """ib_pq_matmul_fp32 (src/pq_decode.c:1684)."""
+        check(lib().ibh_pq_matmul(ctypes.byref(self.s), _ptr(x), _ptr(out), None, 0, _stream()), "ibh_pq_matmul")
