@@ -129,6 +129,26 @@ def batch_case(torch, L, oracle, B, steps, warmup):
     return {"B": B, "us": round(t * 1e6, 3), "GBps": round(nbytes / t / 1e9, 1)}
 
 
+def pq_case(torch, L, steps, warmup):
+    """PQ LUT matvec at BASELINE configs[5]: M=4096, N=14336, G=16, K=256,
+    one level, no outliers (ib_pq_matmul_fp32).  Bytes = both index planes
+    + codebooks + row scales + x + y."""
+    sys.path.insert(0, os.path.join(ROOT, "tests", "golden"))
+    from gen_golden import make_pq
+    M, Cc, G, K = 4096, 896, 16, 256
+    t = make_pq(np.random.default_rng(9), M, Cc, G, K, 1, 0, 0)
+    devs = [L.ops.PqDeviceTensor(t) for _ in range(COPIES)]
+    x = torch.randn(t["N"], generator=torch.Generator().manual_seed(2)).cuda()
+    y = torch.empty(M, device="cuda")
+
+    def launch(i):
+        devs[i % COPIES].matmul(x, y)
+    tm = time_launches(torch, launch, steps, warmup)
+    nbytes = 2 * M * Cc + 2 * 2 * K * (G // 2) + 2 * M + 4 * t["N"] + 4 * M
+    return {"M": M, "N": t["N"], "G": G, "K": K, "us": round(tm * 1e6, 3), "bytes": nbytes,
+            "GBps": round(nbytes / tm / 1e9, 1)}
+
+
 def cpu_baseline():
     """The reference library compiled from its own sources (oracle/_ref),
     ib_parallel_matmul INT4 14336x4096 with the x86 AVX2 table, timed on
@@ -181,6 +201,8 @@ def main():
             extra[name] = gemv_case(torch, L, oracle, bits, M, N, a.steps, a.warmup, w4a8)
         extra["w4a8_batch_sweep_14336x4096"] = [batch_case(torch, L, oracle, B, max(200, a.steps // 4), 20)
                                                 for B in (1, 2, 4, 8)]
+        print("bench: pq_4096x14336", file=sys.stderr, flush=True)
+        extra["pq_4096x14336_G16_K256"] = pq_case(torch, L, max(200, a.steps // 4), 20)
     cpu = None if a.no_cpu else cpu_baseline()
     out = {
         "metric": "quantized GEMV HBM GB/s (% of peak) + decode tok/s, Mistral-7B-shape INT4, 1 GPU",
