@@ -152,6 +152,51 @@ size_t ibh_pq_workspace_bytes(const ibh_pq_tensor* t);
 int    ibh_pq_matmul(const ibh_pq_tensor* t, const float* x, float* out, void* ws,
                      size_t ws_bytes, void* stream);
 
+/* ── device-resident decode (forward_single_ex + greedy generate) ── */
+
+/* Opaque model: an IBF v1 file (src/ibf_loader.c:300-546) whose weight region
+ * lives in HBM unchanged, device KV caches (ib_kv_cache layouts), and one
+ * captured HIP graph per decode position.  Twins of the public API in
+ * include/inferbit.h: inferbit_load / inferbit_free / inferbit_forward /
+ * inferbit_generate (temperature 0) / inferbit_kv_length / _kv_clear /
+ * _kv_truncate.  Host pointers; calls block until the result is on the host.
+ * The matvec routing follows tensor_matmul (src/forward.c:144-185, IB_W4A8
+ * honoured).  Logits differ from the CPU by fp32 summation order. */
+typedef struct ibh_model ibh_model;
+int  ibh_model_load(const char* path, int context_length, ibh_model** out);
+void ibh_model_free(ibh_model* model);
+/* dims[12] = layers, hidden, heads, kv_heads, head_dim, intermediate, vocab,
+ * max_context_length, kv_bits, kv capacity, eos_token_id, usable positions */
+int  ibh_model_dims(const ibh_model* model, int* dims);
+int  ibh_model_forward(ibh_model* model, const int32_t* tokens, int num_tokens, float* logits,
+                       int vocab_size);
+/* Returns the number of tokens written (stops after end-of-sequence, as
+ * src/generate.c:283-297) or a negative error code. */
+int  ibh_model_generate_greedy(ibh_model* model, const int32_t* input_tokens, int num_input_tokens,
+                               int32_t* out_tokens, int max_out_tokens);
+int  ibh_model_kv_length(const ibh_model* model);
+int  ibh_model_kv_clear(ibh_model* model);
+int  ibh_model_kv_truncate(ibh_model* model, int length);
+/* Appends n_pos positions to every layer's cache through the kv_cache_write
+ * quantisation (src/forward.c:352-413); k, v host fp32 [layers][n_pos][kv_dim].
+ * No reference counterpart: it stands in for n_pos earlier decode steps. */
+int  ibh_model_kv_prefill(ibh_model* model, const float* k, const float* v, int n_pos);
+/* Enqueues n more greedy steps continuing the current token stream, without
+ * waiting (throughput measurement); ibh_model_synchronize waits. */
+int  ibh_model_decode_steps(ibh_model* model, int n);
+int  ibh_model_synchronize(ibh_model* model);
+
+/* ── host-side producers of the packed formats (no device work) ── */
+
+/* ib_quantize_int8 / _int4 / _int2 (src/quantize.c:75-239) on fp32 rows:
+ * packed bytes as in ibh_matmul, truncated fp16 scales.  Bit-identical. */
+size_t ibh_packed_row_bytes(int bits, int cols);
+int    ibh_quantize_rows(int bits, const float* w, int rows, int cols, void* out, uint16_t* scales);
+/* Seeded synthetic data: out[i] = std * N(0,1) for stream indices
+ * first..first+n-1 (counter-based, thread-count independent).  No reference
+ * counterpart (the reference converts real checkpoints). */
+int    ibh_fill_normal(float* out, size_t n, uint64_t seed, uint64_t first, float std);
+
 /* ── dispatch-table boundary (host pointers) ───────────────── */
 
 /* Layout-identical mirror of the reference's `ib_kernels`

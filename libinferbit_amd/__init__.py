@@ -9,6 +9,6 @@ a hand-written HIP kernel from libibhip.so.  There is no CPU fallback: if
 the library is not built, ``lib()`` raises.
 """
 from ._lib import IbhError, lib, lib_path, loaded  # noqa: F401
-from . import ops  # noqa: F401
+from . import ibf, model, ops  # noqa: F401
 
-__all__ = ["lib", "lib_path", "loaded", "IbhError", "ops"]
+__all__ = ["lib", "lib_path", "loaded", "IbhError", "ops", "ibf", "model"]

@@ -35,6 +35,20 @@ SIGNATURES = {
     "ibh_attn_decode": (I, [P, P, P, P, P, P, I, I, I, I, I, P, SZ, P]),
     "ibh_pq_workspace_bytes": (SZ, [P]),
     "ibh_pq_matmul": (I, [P, P, P, P, SZ, P]),
+    "ibh_model_load": (I, [C.c_char_p, I, P]),
+    "ibh_model_free": (None, [P]),
+    "ibh_model_dims": (I, [P, P]),
+    "ibh_model_forward": (I, [P, P, I, P, I]),
+    "ibh_model_generate_greedy": (I, [P, P, I, P, I]),
+    "ibh_model_kv_length": (I, [P]),
+    "ibh_model_kv_clear": (I, [P]),
+    "ibh_model_kv_truncate": (I, [P, I]),
+    "ibh_model_kv_prefill": (I, [P, P, P, I]),
+    "ibh_model_decode_steps": (I, [P, I]),
+    "ibh_model_synchronize": (I, [P]),
+    "ibh_packed_row_bytes": (SZ, [I, I]),
+    "ibh_quantize_rows": (I, [I, P, I, I, P, P]),
+    "ibh_fill_normal": (I, [P, SZ, C.c_uint64, C.c_uint64, C.c_float]),
     "ib_init_kernels_hip": (None, [P]),
     "ibh_register_host_weights": (I, [P, SZ, C.POINTER(P)]),
     "ibh_unregister_host_weights": (None, [P]),

@@ -32,7 +32,13 @@ constexpr int kMaxGroup = 8;     // query heads per KV head
 __global__ __launch_bounds__(256) void kv_write_kernel(uint8_t* __restrict__ kd, uint8_t* __restrict__ vd,
                                                        float* __restrict__ ks, float* __restrict__ vs,
                                                        const float* __restrict__ k, const float* __restrict__ v,
-                                                       int pos, int n_kv, int hd, int bits) {
+                                                       int pos, const int* __restrict__ dpos, int n_kv, int hd,
+                                                       int bits) {
+    if (dpos) pos = *dpos;
+    // blockIdx.y: position offset of a multi-position write (KV prefill)
+    pos += blockIdx.y;
+    k += (size_t)blockIdx.y * n_kv * hd;
+    v += (size_t)blockIdx.y * n_kv * hd;
     const int lane = threadIdx.x & 63;
     const int id = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (id >= 2 * n_kv) return;
@@ -93,8 +99,11 @@ template <int BITS, int GRP>
 __global__ __launch_bounds__(256) void attn_partial(float* __restrict__ part, const float* __restrict__ q,
                                                     const uint8_t* __restrict__ kd, const uint8_t* __restrict__ vd,
                                                     const float* __restrict__ ks, const float* __restrict__ vs,
-                                                    int T, int n_heads, int n_kv, int hd, float scale, int nchunks) {
+                                                    int T, const int* __restrict__ dpos, int n_heads, int n_kv,
+                                                    int hd, float scale, int nchunks) {
     constexpr int CT = kChunk;
+    if (dpos) T = *dpos + 1;           // position read on the device (graph replay)
+    if ((int)blockIdx.y * CT >= T) return;
     __shared__ float qs[GRP * kMaxHd];
     __shared__ float kv[CT * (kMaxHd + 1)];
     __shared__ float sc[GRP][CT];
@@ -183,9 +192,12 @@ __global__ __launch_bounds__(256) void attn_partial(float* __restrict__ part, co
 
 // ── merge chunks: out[h] = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c ──────
 __global__ __launch_bounds__(256) void attn_combine(float* __restrict__ out, const float* __restrict__ part,
-                                                    int n_heads, int hd, int nchunks) {
+                                                    int T, const int* __restrict__ dpos, int n_heads, int hd,
+                                                    int nstride) {
     const int h = blockIdx.x;
-    const float* ph = part + (size_t)h * nchunks * (hd + 2);
+    if (dpos) T = *dpos + 1;
+    const int nchunks = (T + kChunk - 1) / kChunk;
+    const float* ph = part + (size_t)h * nstride * (hd + 2);
     __shared__ float w[kMaxChunks];
     __shared__ float denom_s;
     float M = -INFINITY;
@@ -210,9 +222,13 @@ __global__ __launch_bounds__(256) void attn_combine(float* __restrict__ out, con
 
 void* ibh_workspace(size_t bytes);
 
-extern "C" int ibh_kv_write(void* kdata, void* vdata, float* kscales, float* vscales, int pos, const float* k,
-                            const float* v, int n_kv, int head_dim, int kv_bits, void* stream) {
-    if (!kdata || !vdata || !k || !v || pos < 0 || n_kv <= 0 || head_dim <= 0 ||
+// Launchers shared with the decode engine.  `dpos` (device int, may be NULL)
+// overrides `pos` at kernel run time so a captured graph can be replayed for
+// successive positions; `max_pos` bounds it and sizes the grid.
+int ibh_launch_kv_write(void* kdata, void* vdata, float* kscales, float* vscales, int pos, const int* dpos,
+                        const float* k, const float* v, int n_kv, int head_dim, int kv_bits, int npos,
+                        hipStream_t st) {
+    if (!kdata || !vdata || !k || !v || pos < 0 || n_kv <= 0 || head_dim <= 0 || npos <= 0 || npos > 65535 ||
         (kv_bits != 32 && kv_bits != 16 && kv_bits != 8 && kv_bits != 4) ||
         (kv_bits < 16 && (!kscales || !vscales))) {
         ibh_set_error("ibh_kv_write: invalid arguments (pos=%d n_kv=%d head_dim=%d bits=%d)", pos, n_kv, head_dim,
@@ -220,8 +236,8 @@ extern "C" int ibh_kv_write(void* kdata, void* vdata, float* kscales, float* vsc
         return IBH_ERROR_PARAM;
     }
     const int waves = 2 * n_kv;
-    kv_write_kernel<<<(waves + 3) / 4, 256, 0, ibh_resolve_stream(stream)>>>(
-        (uint8_t*)kdata, (uint8_t*)vdata, kscales, vscales, k, v, pos, n_kv, head_dim, kv_bits);
+    kv_write_kernel<<<dim3((waves + 3) / 4, npos), 256, 0, st>>>((uint8_t*)kdata, (uint8_t*)vdata, kscales, vscales, k, v, pos,
+                                                     dpos, n_kv, head_dim, kv_bits);
     IBH_CHECK_LAUNCH("ibh_kv_write");
     return IBH_OK;
 }
@@ -231,11 +247,11 @@ extern "C" size_t ibh_attn_workspace_bytes(int n_heads, int head_dim, int n_pos)
     return (size_t)n_heads * nchunks * (head_dim + 2) * sizeof(float);
 }
 
-extern "C" int ibh_attn_decode(float* out, const float* q, const void* kdata, const void* vdata,
-                               const float* kscales, const float* vscales, int pos, int n_heads, int n_kv,
-                               int head_dim, int kv_bits, void* ws, size_t ws_bytes, void* stream) {
-    if (!out || !q || !kdata || !vdata || pos < 0 || n_heads <= 0 || n_kv <= 0 || n_heads % n_kv ||
-        n_heads / n_kv > kMaxGroup || head_dim <= 0 || head_dim > kMaxHd ||
+int ibh_launch_attn(float* out, const float* q, const void* kdata, const void* vdata, const float* kscales,
+                    const float* vscales, int pos, const int* dpos, int max_pos, int n_heads, int n_kv,
+                    int head_dim, int kv_bits, void* ws, size_t ws_bytes, hipStream_t st) {
+    if (!out || !q || !kdata || !vdata || pos < 0 || max_pos < pos || n_heads <= 0 || n_kv <= 0 ||
+        n_heads % n_kv || n_heads / n_kv > kMaxGroup || head_dim <= 0 || head_dim > kMaxHd ||
         (kv_bits != 32 && kv_bits != 16 && kv_bits != 8 && kv_bits != 4) ||
         (kv_bits < 16 && (!kscales || !vscales))) {
         ibh_set_error("ibh_attn_decode: invalid arguments (pos=%d heads=%d/%d head_dim=%d bits=%d)", pos, n_heads,
@@ -243,12 +259,12 @@ extern "C" int ibh_attn_decode(float* out, const float* q, const void* kdata, co
         return IBH_ERROR_PARAM;
     }
     const int T = pos + 1;
-    const int nchunks = (T + kChunk - 1) / kChunk;
+    const int nchunks = (max_pos + 1 + kChunk - 1) / kChunk;
     if (nchunks > kMaxChunks) {
-        ibh_set_error("ibh_attn_decode: %d positions exceed the supported %d", T, kChunk * kMaxChunks);
+        ibh_set_error("ibh_attn_decode: %d positions exceed the supported %d", max_pos + 1, kChunk * kMaxChunks);
         return IBH_ERROR_CONTEXT;
     }
-    const size_t need = ibh_attn_workspace_bytes(n_heads, head_dim, T);
+    const size_t need = ibh_attn_workspace_bytes(n_heads, head_dim, max_pos + 1);
     if (!ws) {
         ws = ibh_workspace(need);
         ws_bytes = ws ? need : 0;
@@ -257,21 +273,33 @@ extern "C" int ibh_attn_decode(float* out, const float* q, const void* kdata, co
         ibh_set_error("ibh_attn_decode: workspace of %zu bytes needed", need);
         return IBH_ERROR_MEMORY;
     }
-    hipStream_t st = ibh_resolve_stream(stream);
     const float scale = 1.0f / sqrtf((float)head_dim);
     float* part = (float*)ws;
     dim3 grid(n_kv, nchunks);
     const uint8_t* K = (const uint8_t*)kdata;
     const uint8_t* V = (const uint8_t*)vdata;
     const int grp = n_heads / n_kv;
-#define IBH_AP(B_, G_) attn_partial<B_, G_><<<grid, 256, 0, st>>>(part, q, K, V, kscales, vscales, T, n_heads, n_kv, head_dim, scale, nchunks)
+#define IBH_AP(B_, G_) attn_partial<B_, G_><<<grid, 256, 0, st>>>(part, q, K, V, kscales, vscales, T, dpos, n_heads, n_kv, head_dim, scale, nchunks)
 #define IBH_APG(B_) do { if (grp <= 1) IBH_AP(B_, 1); else if (grp <= 2) IBH_AP(B_, 2); else if (grp <= 4) IBH_AP(B_, 4); \
                          else IBH_AP(B_, 8); } while (0)
     if (kv_bits >= 16) IBH_APG(32); else if (kv_bits == 8) IBH_APG(8); else IBH_APG(4);
 #undef IBH_AP
 #undef IBH_APG
     IBH_CHECK_LAUNCH("ibh_attn_decode (partial)");
-    attn_combine<<<n_heads, 256, 0, st>>>(out, part, n_heads, head_dim, nchunks);
+    attn_combine<<<n_heads, 256, 0, st>>>(out, part, T, dpos, n_heads, head_dim, nchunks);
     IBH_CHECK_LAUNCH("ibh_attn_decode (combine)");
     return IBH_OK;
+}
+
+extern "C" int ibh_kv_write(void* kdata, void* vdata, float* kscales, float* vscales, int pos, const float* k,
+                            const float* v, int n_kv, int head_dim, int kv_bits, void* stream) {
+    return ibh_launch_kv_write(kdata, vdata, kscales, vscales, pos, nullptr, k, v, n_kv, head_dim, kv_bits, 1,
+                               ibh_resolve_stream(stream));
+}
+
+extern "C" int ibh_attn_decode(float* out, const float* q, const void* kdata, const void* vdata,
+                               const float* kscales, const float* vscales, int pos, int n_heads, int n_kv,
+                               int head_dim, int kv_bits, void* ws, size_t ws_bytes, void* stream) {
+    return ibh_launch_attn(out, q, kdata, vdata, kscales, vscales, pos, nullptr, pos, n_heads, n_kv, head_dim,
+                           kv_bits, ws, ws_bytes, ibh_resolve_stream(stream));
 }

@@ -1,0 +1,903 @@
+// ibh_decode.hip -- device-resident single-token decode of an IBF v1 model
+// (src/forward.c:519-664 forward_single_ex, src/generate.c:243-300 greedy
+// inferbit_generate) on gfx950.
+//
+// Load: the IBF file (src/ibf_loader.c:300-546: 32-byte preamble, JSON
+// header, 64-byte aligned weight region) is parsed on the host and its
+// weight region is copied to HBM once, unchanged; every tensor is then a
+// device pointer at its file offset.  KV caches live in HBM with the
+// ib_kv_cache layouts (rows [capacity][row], scales [capacity][n_kv]).
+//
+// Step: one token through all layers, the final norm, the LM head and the
+// greedy argmax.  The position and the token stream are DEVICE state: the
+// embedding reads tokens[pos], RoPE / KV write / attention read pos, and the
+// argmax kernel appends its token and advances pos.  So one step's launches
+// are captured once into a HIP graph and replayed for every position, with
+// no host round trip per token.  Matmuls use the library's matvec entry
+// points with the reference's routing (tensor_matmul, forward.c:144-185:
+// INT4 tensors through the int8 activation quantizer + W4A8 unless
+// IB_W4A8=0; INT8 / INT2 with fp32 activations).
+#include <fcntl.h>
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "ibh_common.h"
+
+using namespace ibh;
+
+int ibh_launch_kv_write(void* kdata, void* vdata, float* kscales, float* vscales, int pos, const int* dpos,
+                        const float* k, const float* v, int n_kv, int head_dim, int kv_bits, int npos,
+                        hipStream_t st);
+int ibh_launch_attn(float* out, const float* q, const void* kdata, const void* vdata, const float* kscales,
+                    const float* vscales, int pos, const int* dpos, int max_pos, int n_heads, int n_kv,
+                    int head_dim, int kv_bits, void* ws, size_t ws_bytes, hipStream_t st);
+
+namespace {
+
+// ── minimal JSON reader (the IBF header is plain JSON, ibf_loader.c:124-221) ──
+struct JVal {
+    enum Kind { NUL, BOOL, NUM, STR, ARR, OBJ } kind = NUL;
+    double num = 0;
+    bool b = false;
+    std::string str;
+    std::vector<JVal> arr;
+    std::vector<std::pair<std::string, JVal>> obj;
+    const JVal* get(const char* k) const {
+        if (kind != OBJ) return nullptr;
+        for (auto& kv : obj)
+            if (kv.first == k) return &kv.second;
+        return nullptr;
+    }
+};
+
+struct JParser {
+    const char* p;
+    const char* e;
+    bool ok = true;
+    void ws() {
+        while (p < e && (*p == ' ' || *p == '\n' || *p == '\r' || *p == '\t')) p++;
+    }
+    bool lit(const char* s) {
+        const size_t n = strlen(s);
+        if ((size_t)(e - p) >= n && !memcmp(p, s, n)) {
+            p += n;
+            return true;
+        }
+        return false;
+    }
+    std::string string() {
+        std::string s;
+        p++;   // opening quote
+        while (p < e && *p != '"') {
+            if (*p == '\\' && p + 1 < e) {
+                p++;
+                const char c = *p;
+                if (c == 'n') s += '\n';
+                else if (c == 't') s += '\t';
+                else if (c == 'r') s += '\r';
+                else if (c == 'b') s += '\b';
+                else if (c == 'f') s += '\f';
+                else if (c == 'u') { s += '?'; p += (e - p > 4) ? 4 : 0; }
+                else s += c;
+                p++;
+            } else {
+                s += *p++;
+            }
+        }
+        if (p >= e) ok = false;
+        else p++;
+        return s;
+    }
+    JVal value(int depth) {
+        JVal v;
+        ws();
+        if (p >= e || depth > 64) { ok = false; return v; }
+        if (*p == '{') {
+            v.kind = JVal::OBJ;
+            p++;
+            ws();
+            if (p < e && *p == '}') { p++; return v; }
+            while (ok) {
+                ws();
+                if (p >= e || *p != '"') { ok = false; break; }
+                std::string k = string();
+                ws();
+                if (p >= e || *p != ':') { ok = false; break; }
+                p++;
+                v.obj.emplace_back(std::move(k), value(depth + 1));
+                ws();
+                if (p < e && *p == ',') { p++; continue; }
+                if (p < e && *p == '}') { p++; break; }
+                ok = false;
+            }
+        } else if (*p == '[') {
+            v.kind = JVal::ARR;
+            p++;
+            ws();
+            if (p < e && *p == ']') { p++; return v; }
+            while (ok) {
+                v.arr.push_back(value(depth + 1));
+                ws();
+                if (p < e && *p == ',') { p++; continue; }
+                if (p < e && *p == ']') { p++; break; }
+                ok = false;
+            }
+        } else if (*p == '"') {
+            v.kind = JVal::STR;
+            v.str = string();
+        } else if (lit("true")) {
+            v.kind = JVal::BOOL; v.b = true;
+        } else if (lit("false")) {
+            v.kind = JVal::BOOL;
+        } else if (lit("null")) {
+        } else {
+            std::string num;
+            while (p < e && (strchr("+-.eE", *p) || (*p >= '0' && *p <= '9'))) num += *p++;
+            if (num.empty()) { ok = false; return v; }
+            v.kind = JVal::NUM;
+            v.num = strtod(num.c_str(), nullptr);
+        }
+        return v;
+    }
+};
+
+// cJSON's valueint saturates the double to int (ibf_loader.c:41-45 reads it).
+int jint(const JVal* o, const char* k, int def) {
+    const JVal* v = o ? o->get(k) : nullptr;
+    if (!v || v->kind != JVal::NUM) return def;
+    if (v->num >= 2147483647.0) return 2147483647;
+    if (v->num <= -2147483648.0) return (-2147483647 - 1);
+    return (int)v->num;
+}
+double jdbl(const JVal* o, const char* k, double def) {
+    const JVal* v = o ? o->get(k) : nullptr;
+    return v && v->kind == JVal::NUM ? v->num : def;
+}
+size_t jsize(const JVal* o, const char* k, size_t def) {
+    const JVal* v = o ? o->get(k) : nullptr;
+    return v && v->kind == JVal::NUM ? (size_t)v->num : def;
+}
+
+struct TMeta {   // ib_tensor_meta (inferbit_internal.h:69-78)
+    size_t offset = 0, size = 0, scale_offset = 0, scale_size = 0;
+    int bits = 16;
+    bool present = false;
+};
+
+TMeta parse_tensor(const JVal* o) {
+    TMeta t;
+    if (!o || o->kind != JVal::OBJ) return t;
+    t.present = true;
+    t.offset = jsize(o, "offset", 0);
+    t.size = jsize(o, "size", 0);
+    t.bits = jint(o, "bits", 16);
+    t.scale_offset = jsize(o, "scale_offset", 0);
+    t.scale_size = jsize(o, "scale_size", 0);
+    return t;
+}
+
+// ── device tensors and kernels ───────────────────────────────────────────────
+struct DTensor {
+    const uint8_t* w = nullptr;
+    const void* s = nullptr;   // fp16 scales, or the fp32 ones-vector when the tensor has none
+    int skind = IBH_SCALE_F16;
+    int bits = 16;
+};
+
+struct DLayer {
+    DTensor q, k, v, o, gate, up, down;
+    const uint16_t* in_norm = nullptr;
+    const uint16_t* post_norm = nullptr;
+    const uint8_t* mask = nullptr;   // sparsity mask [inter] or null
+    uint8_t* kd = nullptr;
+    uint8_t* vd = nullptr;
+    float* ks = nullptr;
+    float* vs = nullptr;
+};
+
+constexpr int kNormThreads = 1024;
+constexpr int kNormMaxPer = 16;   // hidden <= 16384
+
+// embedding_lookup (forward.c:90-135) of tokens[*pos].
+__global__ void embed_kernel(float* __restrict__ x, const uint8_t* __restrict__ emb, const uint16_t* __restrict__ sc,
+                             int bits, int hidden, const int* __restrict__ tokens, const int* __restrict__ pos) {
+    const int tok = tokens[*pos];
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= hidden) return;
+    if (bits == 8) {
+        const int8_t* row = (const int8_t*)emb + (size_t)tok * hidden;
+        x[i] = sc ? (float)row[i] * f16_to_f32(sc[tok]) : (float)row[i];
+    } else if (bits == 16) {
+        x[i] = f16_to_f32(((const uint16_t*)emb)[(size_t)tok * hidden + i]);
+    } else {   // 4
+        const uint8_t b = emb[(size_t)tok * (hidden / 2) + i / 2];
+        const float s = sc ? f16_to_f32(sc[tok]) : 1.0f;
+        x[i] = (float)((int)((i & 1) ? (b >> 4) & 0xf : b & 0xf) - 8) * s;
+    }
+}
+
+// Residual add fused with rmsnorm_fp16 (forward.c:322-327, kernels rmsnorm):
+//   x += delta (when delta != null);  out = x * (1/sqrtf(mean(x^2) + eps)) * w.
+// One block; out may alias x.
+__global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(float* __restrict__ out, float* x,
+                                                                   const float* __restrict__ delta,
+                                                                   const uint16_t* __restrict__ w, float eps,
+                                                                   int n) {
+    __shared__ float red[kNormThreads / 64];
+    float v[kNormMaxPer];
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < kNormMaxPer; j++) {
+        const int i = threadIdx.x + j * kNormThreads;
+        v[j] = 0.f;
+        if (i < n) {
+            float xv = x[i];
+            if (delta) {
+                xv = xv + delta[i];
+                x[i] = xv;
+            }
+            v[j] = xv;
+            ss = fmaf(xv, xv, ss);
+        }
+    }
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    float tot = 0.f;
+    for (int k = 0; k < kNormThreads / 64; k++) tot += red[k];
+    const float scale = 1.0f / sqrtf(tot / (float)n + eps);
+#pragma unroll
+    for (int j = 0; j < kNormMaxPer; j++) {
+        const int i = threadIdx.x + j * kNormThreads;
+        if (i < n) out[i] = (v[j] * scale) * f16_to_f32(w[i]);
+    }
+}
+
+// RoPE (kernels rope, applied as forward.c:573-589: every Q head, each K head
+// once) from a host-computed cos/sin table [pos][head_dim/2][2].
+__global__ void rope_kernel(float* __restrict__ q, float* __restrict__ k, const float* __restrict__ table,
+                            const int* __restrict__ pos, int n_heads, int n_kv, int hd) {
+    const int half = hd / 2;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (n_heads + n_kv) * half) return;
+    const int h = i / half, j = i - h * half;
+    const float* cs = table + ((size_t)(*pos) * half + j) * 2;
+    const float c = cs[0], s = cs[1];
+    float* p = h < n_heads ? q + (size_t)h * hd : k + (size_t)(h - n_heads) * hd;
+    const float a = p[2 * j], b = p[2 * j + 1];
+    p[2 * j] = a * c - b * s;
+    p[2 * j + 1] = a * s + b * c;
+}
+
+// silu_mul (kernels silu_mul): out = gate / (1 + expf(-gate)) * up; masked rows
+// of a sparse MLP are zero (forward.c:265-270 zeroes them before silu_mul).
+__global__ void silu_mul_kernel(float* __restrict__ out, const float* __restrict__ gate, const float* __restrict__ up,
+                                const uint8_t* __restrict__ mask, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float g = (mask && !mask[i]) ? 0.f : gate[i];
+    const float u = (mask && !mask[i]) ? 0.f : up[i];
+    out[i] = (g / (1.0f + expf(-g))) * u;
+}
+
+// fp16-weight matvec (tensor_matmul's bits == 16 branch, forward.c:174-182:
+// no scales).  One wavefront per row.
+__global__ void matvec_f16_kernel(float* __restrict__ out, const uint16_t* __restrict__ w, const float* __restrict__ x,
+                                  int M, int N) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= M) return;
+    float acc = 0.f;
+    for (int j = lane; j < N; j += 64) acc = fmaf(f16_to_f32(w[(size_t)row * N + j]), x[j], acc);
+    acc = wave_sum(acc);
+    if (lane == 0) out[row] = acc;
+}
+
+// Greedy pick (generate.c:47-57: first index of the maximum), then append the
+// token at pos+1 unless that slot still holds the prompt, and advance pos.
+__global__ __launch_bounds__(1024) void argmax_advance_kernel(const float* __restrict__ logits, int n,
+                                                              int* __restrict__ tokens, int* __restrict__ pos,
+                                                              const int* __restrict__ prompt_end) {
+    __shared__ float bv[16];
+    __shared__ int bi[16];
+    float best = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int i = threadIdx.x; i < n; i += 1024) {
+        const float v = logits[i];   // NaN never wins, like `>` in the reference
+        if ((idx == 0x7fffffff && !(v != v)) || v > best) { best = v; idx = i; }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(best, o, 64);
+        const int oi = __shfl_xor(idx, o, 64);
+        if (ov > best || (ov == best && oi < idx)) { best = ov; idx = oi; }
+    }
+    if ((threadIdx.x & 63) == 0) { bv[threadIdx.x >> 6] = best; bi[threadIdx.x >> 6] = idx; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float b = bv[0];
+        int bidx = bi[0];
+        for (int k = 1; k < 16; k++)
+            if (bv[k] > b || (bv[k] == b && bi[k] < bidx)) { b = bv[k]; bidx = bi[k]; }
+        const float l0 = logits[0];
+        if (bidx == 0x7fffffff || l0 != l0) bidx = 0;   // NaN at index 0 is never beaten in the reference
+        const int p = *pos;
+        if (p + 1 >= *prompt_end) tokens[p + 1] = bidx;
+        *pos = p + 1;
+    }
+}
+
+bool w4a8_enabled() {
+    const char* e = getenv("IB_W4A8");   // forward.c:14-21
+    return !(e && e[0] == '0');
+}
+
+}  // namespace
+
+struct ibh_model {
+    int device = 0;
+    hipStream_t st = nullptr;
+    // header (ib_ibf_header fields the forward pass reads)
+    int n_layers = 0, hidden = 0, n_heads = 0, n_kv = 0, head_dim = 0, inter = 0, vocab = 0, max_ctx = 0;
+    int kv_bits = 8, eos = 2, capacity = 0, max_pos = 0;
+    float theta = 10000.f, eps = 1e-5f;
+    bool w4a8 = true;
+    uint8_t* dweights = nullptr;
+    size_t wbytes = 0;
+    std::vector<DLayer> layers;
+    DTensor emb, head;
+    const uint16_t* out_norm = nullptr;
+    float *x = nullptr, *xb = nullptr, *xb2 = nullptr, *q = nullptr, *k = nullptr, *v = nullptr;
+    float *hb = nullptr, *hb2 = nullptr, *logits = nullptr, *ones = nullptr, *rope = nullptr, *sa = nullptr;
+    int8_t* qx = nullptr;
+    void* attn_ws = nullptr;
+    size_t attn_ws_bytes = 0;
+    int* dstate = nullptr;   // [0] pos, [1] prompt_end, [2..] tokens[capacity + 1]
+    int hpos = 0;
+    hipGraphExec_t exec = nullptr;
+    std::vector<void*> allocs;
+    int* dpos() { return dstate; }
+    int* dprompt_end() { return dstate + 1; }
+    int* dtokens() { return dstate + 2; }
+};
+
+namespace {
+
+int dalloc(ibh_model* m, void** p, size_t bytes) {
+    if (hipMalloc(p, bytes ? bytes : 16) != hipSuccess) {
+        ibh_set_error("ibh_model: device allocation of %zu bytes failed", bytes);
+        return IBH_ERROR_MEMORY;
+    }
+    m->allocs.push_back(*p);
+    return IBH_OK;
+}
+
+void free_model(ibh_model* m) {
+    if (!m) return;
+    if (m->exec) hipGraphExecDestroy(m->exec);
+    if (m->st) hipStreamSynchronize(m->st);
+    for (void* p : m->allocs) hipFree(p);
+    if (m->st) hipStreamDestroy(m->st);
+    delete m;
+}
+
+int mm(ibh_model* m, const DTensor& t, float* out, const float* in, int M, int N) {
+    void* st = (void*)m->st;
+    if (t.bits == 4 && m->w4a8)
+        return ibh_matmul_w4a8_x(out, t.w, t.s, t.skind, in, M, N, m->qx, m->sa, st);
+    if (t.bits == 8 || t.bits == 4 || t.bits == 2) return ibh_matmul(out, t.w, t.s, t.skind, in, M, N, t.bits, st);
+    matvec_f16_kernel<<<(M + 3) / 4, 256, 0, m->st>>>(out, (const uint16_t*)t.w, in, M, N);
+    IBH_CHECK_LAUNCH("ibh_model: fp16 matvec");
+    return IBH_OK;
+}
+
+// One decode position: forward_single_ex(compute_logits=1) + greedy pick.
+int step(ibh_model* m) {
+    const int H = m->hidden, kv_dim = m->n_kv * m->head_dim;
+    int rc;
+    embed_kernel<<<(H + 255) / 256, 256, 0, m->st>>>(m->x, m->emb.w, (const uint16_t*)(m->emb.skind == IBH_SCALE_F16 ? m->emb.s : nullptr),
+                                                     m->emb.bits, H, m->dtokens(), m->dpos());
+    IBH_CHECK_LAUNCH("ibh_model: embedding");
+    for (int l = 0; l < m->n_layers; l++) {
+        DLayer& L = m->layers[l];
+        // residual of the previous layer's MLP folded into this norm
+        add_rmsnorm_kernel<<<1, kNormThreads, 0, m->st>>>(m->xb, m->x, l ? m->xb : nullptr, L.in_norm, m->eps, H);
+        IBH_CHECK_LAUNCH("ibh_model: rmsnorm");
+        if ((rc = mm(m, L.q, m->q, m->xb, H, H)) || (rc = mm(m, L.k, m->k, m->xb, kv_dim, H)) ||
+            (rc = mm(m, L.v, m->v, m->xb, kv_dim, H)))
+            return rc;
+        const int nr = (m->n_heads + m->n_kv) * (m->head_dim / 2);
+        rope_kernel<<<(nr + 255) / 256, 256, 0, m->st>>>(m->q, m->k, m->rope, m->dpos(), m->n_heads, m->n_kv,
+                                                         m->head_dim);
+        IBH_CHECK_LAUNCH("ibh_model: rope");
+        if ((rc = ibh_launch_kv_write(L.kd, L.vd, L.ks, L.vs, 0, m->dpos(), m->k, m->v, m->n_kv, m->head_dim,
+                                      m->kv_bits, 1, m->st)))
+            return rc;
+        if ((rc = ibh_launch_attn(m->xb2, m->q, L.kd, L.vd, L.ks, L.vs, 0, m->dpos(), m->max_pos, m->n_heads,
+                                  m->n_kv, m->head_dim, m->kv_bits, m->attn_ws, m->attn_ws_bytes, m->st)))
+            return rc;
+        if ((rc = mm(m, L.o, m->xb, m->xb2, H, H))) return rc;
+        add_rmsnorm_kernel<<<1, kNormThreads, 0, m->st>>>(m->xb2, m->x, m->xb, L.post_norm, m->eps, H);
+        IBH_CHECK_LAUNCH("ibh_model: rmsnorm");
+        if ((rc = mm(m, L.gate, m->hb, m->xb2, m->inter, H)) || (rc = mm(m, L.up, m->hb2, m->xb2, m->inter, H)))
+            return rc;
+        silu_mul_kernel<<<(m->inter + 255) / 256, 256, 0, m->st>>>(m->hb, m->hb, m->hb2, L.mask, m->inter);
+        IBH_CHECK_LAUNCH("ibh_model: silu_mul");
+        if ((rc = mm(m, L.down, m->xb, m->hb, H, m->inter))) return rc;
+    }
+    add_rmsnorm_kernel<<<1, kNormThreads, 0, m->st>>>(m->x, m->x, m->xb, m->out_norm, m->eps, H);
+    IBH_CHECK_LAUNCH("ibh_model: final rmsnorm");
+    if ((rc = mm(m, m->head, m->logits, m->x, m->vocab, H))) return rc;
+    argmax_advance_kernel<<<1, 1024, 0, m->st>>>(m->logits, m->vocab, m->dtokens(), m->dpos(), m->dprompt_end());
+    IBH_CHECK_LAUNCH("ibh_model: argmax");
+    return IBH_OK;
+}
+
+bool eager_mode() {
+    const char* e = getenv("IBH_DECODE_EAGER");
+    return e && e[0] == '1';
+}
+
+int build_graph(ibh_model* m) {
+    if (m->exec || eager_mode()) return IBH_OK;
+    hipGraph_t g = nullptr;
+    IBH_HIP(hipStreamBeginCapture(m->st, hipStreamCaptureModeThreadLocal), "ibh_model: begin capture");
+    const int rc = step(m);
+    const hipError_t e = hipStreamEndCapture(m->st, &g);
+    if (rc) {
+        if (g) hipGraphDestroy(g);
+        return rc;
+    }
+    if (e != hipSuccess) {
+        ibh_set_error("ibh_model: capture failed: %s", hipGetErrorString(e));
+        return IBH_ERROR_INTERNAL;
+    }
+    const hipError_t ie = hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0);
+    hipGraphDestroy(g);
+    if (ie != hipSuccess) {
+        m->exec = nullptr;
+        ibh_set_error("ibh_model: graph instantiate failed: %s", hipGetErrorString(ie));
+        return IBH_ERROR_INTERNAL;
+    }
+    return IBH_OK;
+}
+
+int run_steps(ibh_model* m, int n) {
+    int rc = build_graph(m);
+    if (rc) return rc;
+    for (int i = 0; i < n; i++) {
+        if (m->exec) {
+            IBH_HIP(hipGraphLaunch(m->exec, m->st), "ibh_model: graph launch");
+        } else if ((rc = step(m))) {
+            return rc;
+        }
+    }
+    m->hpos += n;
+    return IBH_OK;
+}
+
+int set_state(ibh_model* m, int pos, int prompt_end) {
+    const int s[2] = {pos, prompt_end};
+    IBH_HIP(hipMemcpyAsync(m->dstate, s, sizeof s, hipMemcpyHostToDevice, m->st), "ibh_model: state upload");
+    IBH_HIP(hipStreamSynchronize(m->st), "ibh_model: state upload");
+    return IBH_OK;
+}
+
+bool read_all(int fd, void* dst, size_t n, size_t off) {
+    uint8_t* d = (uint8_t*)dst;
+    while (n) {
+        const ssize_t r = pread(fd, d, n > (1u << 30) ? (1u << 30) : n, (off_t)off);
+        if (r <= 0) return false;
+        d += r;
+        off += (size_t)r;
+        n -= (size_t)r;
+    }
+    return true;
+}
+
+int load(ibh_model* m, const char* path, int context_length) {
+    const int fd = open(path, O_RDONLY);
+    if (fd < 0) {
+        ibh_set_error("ibh_model_load: cannot open %s", path);
+        return IBH_ERROR_LOAD;
+    }
+    struct Closer { int fd; ~Closer() { close(fd); } } closer{fd};
+    struct stat sb;
+    if (fstat(fd, &sb) != 0 || sb.st_size < 32) {
+        ibh_set_error("ibh_model_load: %s is too small to be IBF", path);
+        return IBH_ERROR_FORMAT;
+    }
+    const size_t fsize = (size_t)sb.st_size;
+    uint8_t pre[32];
+    if (!read_all(fd, pre, 32, 0) || memcmp(pre, "INFERBIT", 8) != 0) {
+        ibh_set_error("ibh_model_load: invalid IBF magic");
+        return IBH_ERROR_FORMAT;
+    }
+    uint32_t version, hsize;
+    memcpy(&version, pre + 8, 4);
+    memcpy(&hsize, pre + 12, 4);
+    if (version > 1) {
+        ibh_set_error("ibh_model_load: unsupported IBF version %u (max 1)", version);
+        return IBH_ERROR_FORMAT;
+    }
+    if (32 + (size_t)hsize > fsize) {
+        ibh_set_error("ibh_model_load: IBF header size exceeds file size");
+        return IBH_ERROR_FORMAT;
+    }
+    std::string js(hsize, '\0');
+    if (!read_all(fd, &js[0], hsize, 32)) {
+        ibh_set_error("ibh_model_load: cannot read the JSON header");
+        return IBH_ERROR_LOAD;
+    }
+    JParser jp{js.data(), js.data() + js.size()};
+    const JVal root = jp.value(0);
+    if (!jp.ok || root.kind != JVal::OBJ) {
+        ibh_set_error("ibh_model_load: failed to parse IBF JSON header");
+        return IBH_ERROR_FORMAT;
+    }
+    const JVal* arch = root.get("architecture");
+    m->n_layers = jint(arch, "num_layers", 0);
+    m->hidden = jint(arch, "hidden_size", 0);
+    m->n_heads = jint(arch, "num_heads", 0);
+    m->n_kv = jint(arch, "num_kv_heads", m->n_heads);
+    m->head_dim = jint(arch, "head_dim", m->n_heads ? m->hidden / m->n_heads : 0);
+    m->inter = jint(arch, "intermediate_size", 0);
+    m->vocab = jint(arch, "vocab_size", 0);
+    m->max_ctx = jint(arch, "max_context_length", 2048);
+    m->theta = (float)jdbl(arch, "rope_theta", 10000.0);
+    m->eps = (float)jdbl(arch, "norm_epsilon", 1e-5);
+    m->eos = jint(arch, "eos_token_id", 2);
+    const JVal* kv = root.get("kv_cache");
+    m->kv_bits = kv ? jint(kv, "bits", 8) : 0;
+    if (m->n_layers <= 0 || m->hidden <= 0 || m->vocab <= 0) {
+        ibh_set_error("ibh_model_load: IBF header missing required architecture fields");
+        return IBH_ERROR_FORMAT;
+    }
+    if (m->n_heads <= 0 || m->n_kv <= 0 || m->n_heads % m->n_kv || m->head_dim <= 0 || m->head_dim % 2 ||
+        m->head_dim > 256 || m->n_heads / m->n_kv > 8 || m->hidden > kNormThreads * kNormMaxPer ||
+        m->inter <= 0 || m->n_heads * m->head_dim != m->hidden) {
+        ibh_set_error("ibh_model_load: unsupported geometry (hidden=%d heads=%d/%d head_dim=%d inter=%d)", m->hidden,
+                      m->n_heads, m->n_kv, m->head_dim, m->inter);
+        return IBH_ERROR_FORMAT;
+    }
+    if (m->kv_bits != 32 && m->kv_bits != 16 && m->kv_bits != 8 && m->kv_bits != 4) {
+        ibh_set_error("ibh_model_load: unsupported kv_bits=%d", m->kv_bits);
+        return IBH_ERROR_FORMAT;
+    }
+    const JVal* data = root.get("data");
+    size_t woff = (32 + (size_t)hsize + 63) & ~(size_t)63;
+    const size_t wdo = jsize(data, "weight_data_offset", 0);
+    if (wdo > 0) woff = wdo;
+    if (woff > fsize) {
+        ibh_set_error("ibh_model_load: weight data offset beyond end of file");
+        return IBH_ERROR_FORMAT;
+    }
+    size_t wsize = fsize - woff;
+    const size_t wds = jsize(data, "weight_data_size", 0);
+    if (wds > 0 && wds < wsize) wsize = wds;
+    m->wbytes = wsize;
+    m->capacity = context_length > 0 ? context_length : m->max_ctx;
+    // ib_forward bounds positions by max_context_length (forward.c:856-862); the
+    // cache holds `capacity` rows, so positions stop at the smaller of the two.
+    m->max_pos = (m->capacity < m->max_ctx ? m->capacity : m->max_ctx) - 1;
+    if (m->max_pos < 0 || m->max_pos + 1 > 32 * 4096) {
+        ibh_set_error("ibh_model_load: context length %d unsupported", m->max_pos + 1);
+        return IBH_ERROR_PARAM;
+    }
+    m->w4a8 = w4a8_enabled();
+
+    // weights: staged through a pinned buffer, copied once
+    int rc;
+    if ((rc = dalloc(m, (void**)&m->dweights, wsize))) return rc;
+    {
+        const size_t chunk = 64u << 20;
+        void* pin = nullptr;
+        IBH_HIP(hipHostMalloc(&pin, chunk, hipHostMallocDefault), "ibh_model_load: pinned staging");
+        for (size_t o = 0; o < wsize; o += chunk) {
+            const size_t n = wsize - o < chunk ? wsize - o : chunk;
+            if (!read_all(fd, pin, n, woff + o)) {
+                hipHostFree(pin);
+                ibh_set_error("ibh_model_load: short read of the weight data");
+                return IBH_ERROR_LOAD;
+            }
+            if (hipMemcpy(m->dweights + o, pin, n, hipMemcpyHostToDevice) != hipSuccess) {
+                hipHostFree(pin);
+                ibh_set_error("ibh_model_load: weight upload failed");
+                return IBH_ERROR_INTERNAL;
+            }
+        }
+        hipHostFree(pin);
+    }
+    const int maxM = m->vocab > m->inter ? (m->vocab > m->hidden ? m->vocab : m->hidden)
+                                         : (m->inter > m->hidden ? m->inter : m->hidden);
+    if ((rc = dalloc(m, (void**)&m->ones, (size_t)maxM * 4))) return rc;
+    {
+        std::vector<float> ones(maxM, 1.0f);
+        IBH_HIP(hipMemcpy(m->ones, ones.data(), ones.size() * 4, hipMemcpyHostToDevice), "ibh_model_load: ones");
+    }
+    auto bind = [&](const TMeta& t, DTensor& d, const char* name, size_t rows, size_t cols, bool matvec) -> int {
+        if (!t.present) {
+            ibh_set_error("ibh_model_load: tensor %s missing", name);
+            return IBH_ERROR_FORMAT;
+        }
+        const size_t need = t.bits == 8 ? rows * cols : t.bits == 4 ? rows * cols / 2 : t.bits == 2 ? rows * cols / 4
+                          : rows * cols * 2;
+        if ((t.bits != 8 && t.bits != 4 && t.bits != 2 && t.bits != 16) || t.offset + need > wsize ||
+            (!matvec && t.bits == 2)) {
+            ibh_set_error("ibh_model_load: tensor %s: bits=%d / extent out of range", name, t.bits);
+            return IBH_ERROR_FORMAT;
+        }
+        d.w = m->dweights + t.offset;
+        d.bits = t.bits;
+        if (t.scale_offset == 0 && t.scale_size == 0) {   // tensor_scales_raw: no scales -> 1.0
+            d.s = m->ones;
+            d.skind = IBH_SCALE_F32;
+        } else {
+            if (t.scale_offset + rows * 2 > wsize) {
+                ibh_set_error("ibh_model_load: tensor %s: scales out of range", name);
+                return IBH_ERROR_FORMAT;
+            }
+            d.s = m->dweights + t.scale_offset;
+            d.skind = IBH_SCALE_F16;
+        }
+        return IBH_OK;
+    };
+    auto norm = [&](const TMeta& t, const uint16_t** d, const char* name) -> int {
+        if (!t.present || t.offset + (size_t)m->hidden * 2 > wsize) {
+            ibh_set_error("ibh_model_load: norm %s missing or out of range", name);
+            return IBH_ERROR_FORMAT;
+        }
+        *d = (const uint16_t*)(m->dweights + t.offset);
+        return IBH_OK;
+    };
+    const size_t H = m->hidden, KV = (size_t)m->n_kv * m->head_dim, I = m->inter, V = m->vocab;
+    const JVal* layers = root.get("layers");
+    m->layers.resize(m->n_layers);
+    const size_t kv_row = m->kv_bits >= 16 ? KV * 4 : m->kv_bits == 8 ? KV : (KV + 1) / 2;
+    for (int l = 0; l < m->n_layers; l++) {
+        const JVal* lo = layers && layers->kind == JVal::ARR && l < (int)layers->arr.size() ? &layers->arr[l] : nullptr;
+        const JVal* w = lo ? lo->get("weights") : nullptr;
+        DLayer& L = m->layers[l];
+        if ((rc = bind(parse_tensor(w ? w->get("q_proj") : nullptr), L.q, "q_proj", H, H, true)) ||
+            (rc = bind(parse_tensor(w ? w->get("k_proj") : nullptr), L.k, "k_proj", KV, H, true)) ||
+            (rc = bind(parse_tensor(w ? w->get("v_proj") : nullptr), L.v, "v_proj", KV, H, true)) ||
+            (rc = bind(parse_tensor(w ? w->get("o_proj") : nullptr), L.o, "o_proj", H, H, true)) ||
+            (rc = bind(parse_tensor(w ? w->get("gate_proj") : nullptr), L.gate, "gate_proj", I, H, true)) ||
+            (rc = bind(parse_tensor(w ? w->get("up_proj") : nullptr), L.up, "up_proj", I, H, true)) ||
+            (rc = bind(parse_tensor(w ? w->get("down_proj") : nullptr), L.down, "down_proj", H, I, true)) ||
+            (rc = norm(parse_tensor(w ? w->get("input_norm") : nullptr), &L.in_norm, "input_norm")) ||
+            (rc = norm(parse_tensor(w ? w->get("post_attn_norm") : nullptr), &L.post_norm, "post_attn_norm")))
+            return rc;
+        const JVal* sp = lo ? lo->get("sparsity_mask") : nullptr;
+        const size_t moff = jsize(sp, "offset", 0), msz = jsize(sp, "size", 0);
+        if (msz > 0) {
+            if (moff + I > wsize) {
+                ibh_set_error("ibh_model_load: sparsity mask out of range");
+                return IBH_ERROR_FORMAT;
+            }
+            L.mask = m->dweights + moff;
+        }
+        if ((rc = dalloc(m, (void**)&L.kd, kv_row * m->capacity)) ||
+            (rc = dalloc(m, (void**)&L.vd, kv_row * m->capacity)))
+            return rc;
+        if (m->kv_bits < 16) {
+            if ((rc = dalloc(m, (void**)&L.ks, (size_t)m->capacity * m->n_kv * 4)) ||
+                (rc = dalloc(m, (void**)&L.vs, (size_t)m->capacity * m->n_kv * 4)))
+                return rc;
+        }
+    }
+    const JVal* emb = root.get("embeddings");
+    const TMeta et = parse_tensor(emb ? emb->get("token_embedding") : nullptr);
+    if ((rc = bind(et, m->emb, "token_embedding", V, H, false))) return rc;
+    if (et.bits != 8 && et.bits != 4 && et.bits != 16) {
+        ibh_set_error("ibh_model_load: embedding bits=%d unsupported", et.bits);
+        return IBH_ERROR_FORMAT;
+    }
+    const JVal* out = root.get("output");
+    if ((rc = norm(parse_tensor(out ? out->get("norm") : nullptr), &m->out_norm, "output norm")) ||
+        (rc = bind(parse_tensor(out ? out->get("head") : nullptr), m->head, "output head", V, H, true)))
+        return rc;
+
+    // activations and state
+    if ((rc = dalloc(m, (void**)&m->x, H * 4)) || (rc = dalloc(m, (void**)&m->xb, H * 4)) ||
+        (rc = dalloc(m, (void**)&m->xb2, H * 4)) || (rc = dalloc(m, (void**)&m->q, H * 4)) ||
+        (rc = dalloc(m, (void**)&m->k, KV * 4)) || (rc = dalloc(m, (void**)&m->v, KV * 4)) ||
+        (rc = dalloc(m, (void**)&m->hb, I * 4)) || (rc = dalloc(m, (void**)&m->hb2, I * 4)) ||
+        (rc = dalloc(m, (void**)&m->logits, V * 4)) ||
+        (rc = dalloc(m, (void**)&m->qx, (H > I ? H : I) + 64)) ||
+        (rc = dalloc(m, (void**)&m->sa, ((H > I ? H : I) / 128 + 2) * 4)) ||
+        (rc = dalloc(m, (void**)&m->dstate, ((size_t)m->capacity + 3) * 4)))
+        return rc;
+    m->attn_ws_bytes = ibh_attn_workspace_bytes(m->n_heads, m->head_dim, m->max_pos + 1);
+    if ((rc = dalloc(m, &m->attn_ws, m->attn_ws_bytes))) return rc;
+    // RoPE table with the host libm, as the CPU kernel evaluates it
+    // (kernels rope): freq = 1/powf(theta, i/hd), angle = pos*freq.
+    {
+        const int half = m->head_dim / 2;
+        std::vector<float> tab((size_t)(m->max_pos + 1) * half * 2);
+        for (int p = 0; p <= m->max_pos; p++)
+            for (int j = 0; j < half; j++) {
+                const float freq = 1.0f / powf(m->theta, (float)(2 * j) / (float)m->head_dim);
+                const float ang = (float)p * freq;
+                tab[((size_t)p * half + j) * 2] = cosf(ang);
+                tab[((size_t)p * half + j) * 2 + 1] = sinf(ang);
+            }
+        if ((rc = dalloc(m, (void**)&m->rope, tab.size() * 4))) return rc;
+        IBH_HIP(hipMemcpy(m->rope, tab.data(), tab.size() * 4, hipMemcpyHostToDevice), "ibh_model_load: rope");
+    }
+    return set_state(m, 0, 0);
+}
+
+}  // namespace
+
+extern "C" int ibh_model_load(const char* path, int context_length, ibh_model** out) {
+    if (!path || !out) {
+        ibh_set_error("ibh_model_load: null argument");
+        return IBH_ERROR_PARAM;
+    }
+    *out = nullptr;
+    ibh_model* m = new ibh_model();
+    hipGetDevice(&m->device);
+    if (hipStreamCreateWithFlags(&m->st, hipStreamNonBlocking) != hipSuccess) {
+        delete m;
+        ibh_set_error("ibh_model_load: stream creation failed");
+        return IBH_ERROR_INTERNAL;
+    }
+    const int rc = load(m, path, context_length);
+    if (rc) {
+        free_model(m);
+        return rc;
+    }
+    *out = m;
+    return IBH_OK;
+}
+
+extern "C" void ibh_model_free(ibh_model* m) { free_model(m); }
+
+extern "C" int ibh_model_dims(const ibh_model* m, int* d) {
+    if (!m || !d) {
+        ibh_set_error("ibh_model_dims: null argument");
+        return IBH_ERROR_PARAM;
+    }
+    const int v[12] = {m->n_layers, m->hidden, m->n_heads, m->n_kv,     m->head_dim, m->inter,
+                       m->vocab,    m->max_ctx, m->kv_bits, m->capacity, m->eos,     m->max_pos + 1};
+    memcpy(d, v, sizeof v);
+    return IBH_OK;
+}
+
+extern "C" int ibh_model_kv_length(const ibh_model* m) { return m ? m->hpos : 0; }
+
+extern "C" int ibh_model_kv_truncate(ibh_model* m, int length) {
+    if (!m || length < 0 || length > m->hpos) {
+        ibh_set_error("ibh_model_kv_truncate: invalid length");
+        return IBH_ERROR_PARAM;
+    }
+    m->hpos = length;
+    return set_state(m, length, length);
+}
+
+extern "C" int ibh_model_kv_clear(ibh_model* m) { return ibh_model_kv_truncate(m, 0); }
+
+extern "C" int ibh_model_kv_prefill(ibh_model* m, const float* k, const float* v, int n_pos) {
+    if (!m || !k || !v || n_pos <= 0 || m->hpos + n_pos > m->max_pos + 1) {
+        ibh_set_error("ibh_model_kv_prefill: invalid arguments (n_pos=%d, length=%d)", n_pos, m ? m->hpos : 0);
+        return IBH_ERROR_PARAM;
+    }
+    const size_t kv_dim = (size_t)m->n_kv * m->head_dim, per = (size_t)n_pos * kv_dim;
+    float* tmp = nullptr;
+    IBH_HIP(hipMalloc((void**)&tmp, per * 8), "ibh_model_kv_prefill: staging");
+    int rc = IBH_OK;
+    for (int l = 0; l < m->n_layers && !rc; l++) {
+        DLayer& L = m->layers[l];
+        if (hipMemcpy(tmp, k + l * per, per * 4, hipMemcpyHostToDevice) != hipSuccess ||
+            hipMemcpy(tmp + per, v + l * per, per * 4, hipMemcpyHostToDevice) != hipSuccess) {
+            ibh_set_error("ibh_model_kv_prefill: upload failed");
+            rc = IBH_ERROR_INTERNAL;
+            break;
+        }
+        rc = ibh_launch_kv_write(L.kd, L.vd, L.ks, L.vs, m->hpos, nullptr, tmp, tmp + per, m->n_kv, m->head_dim,
+                                 m->kv_bits, n_pos, m->st);
+        if (!rc && hipStreamSynchronize(m->st) != hipSuccess) {
+            ibh_set_error("ibh_model_kv_prefill: kernel failed");
+            rc = IBH_ERROR_INTERNAL;
+        }
+    }
+    hipFree(tmp);
+    if (rc) return rc;
+    m->hpos += n_pos;
+    return set_state(m, m->hpos, m->hpos);
+}
+
+static int check_tokens(const ibh_model* m, const int32_t* t, int n, const char* who) {
+    for (int i = 0; i < n; i++)
+        if (t[i] < 0 || t[i] >= m->vocab) {
+            ibh_set_error("%s: token ID out of range: %d (vocab_size=%d)", who, t[i], m->vocab);
+            return IBH_ERROR_PARAM;
+        }
+    return IBH_OK;
+}
+
+static int put_tokens(ibh_model* m, const int32_t* t, int n) {
+    IBH_HIP(hipMemcpyAsync(m->dtokens() + m->hpos, t, (size_t)n * 4, hipMemcpyHostToDevice, m->st),
+            "ibh_model: token upload");
+    return set_state(m, m->hpos, m->hpos + n);
+}
+
+extern "C" int ibh_model_forward(ibh_model* m, const int32_t* tokens, int n, float* logits, int vocab) {
+    if (!m || !tokens || !logits || n <= 0) {
+        ibh_set_error("ibh_model_forward: invalid arguments");
+        return IBH_ERROR_PARAM;
+    }
+    if (vocab != m->vocab) {
+        ibh_set_error("ibh_model_forward: vocab_size mismatch: %d vs %d", vocab, m->vocab);
+        return IBH_ERROR_PARAM;
+    }
+    if (m->hpos + n > m->max_pos + 1) {
+        ibh_set_error("ibh_model_forward: context length exceeded: %d + %d > %d", m->hpos, n, m->max_pos + 1);
+        return IBH_ERROR_CONTEXT;
+    }
+    int rc;
+    if ((rc = check_tokens(m, tokens, n, "ibh_model_forward")) || (rc = put_tokens(m, tokens, n)) ||
+        (rc = run_steps(m, n)))
+        return rc;
+    IBH_HIP(hipMemcpyAsync(logits, m->logits, (size_t)vocab * 4, hipMemcpyDeviceToHost, m->st),
+            "ibh_model_forward: logits");
+    IBH_HIP(hipStreamSynchronize(m->st), "ibh_model_forward");
+    return IBH_OK;
+}
+
+extern "C" int ibh_model_generate_greedy(ibh_model* m, const int32_t* in, int n_in, int32_t* out, int max_out) {
+    if (!m || !in || !out || n_in <= 0 || max_out <= 0) {
+        ibh_set_error("ibh_model_generate_greedy: invalid arguments");
+        return IBH_ERROR_PARAM;
+    }
+    const int steps = n_in + max_out - 1;
+    if (m->hpos + steps > m->max_pos + 1) {
+        ibh_set_error("ibh_model_generate_greedy: context length exceeded: %d + %d > %d", m->hpos, steps,
+                      m->max_pos + 1);
+        return IBH_ERROR_CONTEXT;
+    }
+    const int start = m->hpos;
+    int rc;
+    if ((rc = check_tokens(m, in, n_in, "ibh_model_generate_greedy")) || (rc = put_tokens(m, in, n_in)) ||
+        (rc = run_steps(m, steps)))
+        return rc;
+    IBH_HIP(hipMemcpyAsync(out, m->dtokens() + start + n_in, (size_t)max_out * 4, hipMemcpyDeviceToHost, m->st),
+            "ibh_model_generate_greedy: tokens");
+    IBH_HIP(hipStreamSynchronize(m->st), "ibh_model_generate_greedy");
+    // the reference stops at the first end-of-sequence token (generate.c:283-297)
+    int n = max_out;
+    for (int i = 0; i < max_out; i++)
+        if (out[i] == m->eos) {
+            n = i + 1;
+            break;
+        }
+    if (n < max_out) {
+        m->hpos = start + n_in + n - 1;
+        if ((rc = set_state(m, m->hpos, m->hpos))) return rc;
+    }
+    return n;
+}
+
+// Decode-throughput aid: `n` further greedy steps from the current state
+// (tokens continue from the last generated one), timed by the caller.
+extern "C" int ibh_model_decode_steps(ibh_model* m, int n) {
+    if (!m || n <= 0 || m->hpos + n > m->max_pos + 1 || m->hpos == 0) {
+        ibh_set_error("ibh_model_decode_steps: invalid step count");
+        return IBH_ERROR_PARAM;
+    }
+    return run_steps(m, n);
+}
+
+extern "C" int ibh_model_synchronize(ibh_model* m) {
+    if (!m) return IBH_ERROR_PARAM;
+    IBH_HIP(hipStreamSynchronize(m->st), "ibh_model_synchronize");
+    return IBH_OK;
+}

@@ -1,0 +1,78 @@
+"""Device-resident decode of an IBF v1 model: twins of the reference's public
+model API (include/inferbit.h: inferbit_load, inferbit_forward,
+inferbit_generate at temperature 0, inferbit_kv_length / _clear / _truncate).
+Host numpy arrays in and out; errors raise IbhError."""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from ._lib import check, lib
+
+DIM_NAMES = ("num_layers", "hidden_size", "num_heads", "num_kv_heads", "head_dim", "intermediate_size",
+             "vocab_size", "max_context_length", "kv_bits", "capacity", "eos_token_id", "positions")
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+class Model:
+    def __init__(self, path: str, context_length: int = 0):
+        """inferbit_load (src/ibf_loader.c:300-546) with the weight region uploaded to HBM."""
+        h = ctypes.c_void_p()
+        check(lib().ibh_model_load(path.encode(), context_length, ctypes.byref(h)), "ibh_model_load")
+        self._h = h
+        d = np.zeros(12, np.int32)
+        check(lib().ibh_model_dims(self._h, _ptr(d)), "ibh_model_dims")
+        self.dims = dict(zip(DIM_NAMES, (int(v) for v in d)))
+
+    def close(self) -> None:
+        if self._h:
+            lib().ibh_model_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def forward(self, tokens) -> np.ndarray:
+        """inferbit_forward (src/generate.c:225-241): logits of the last token."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        out = np.empty(self.dims["vocab_size"], np.float32)
+        check(lib().ibh_model_forward(self._h, _ptr(t), len(t), _ptr(out), len(out)), "ibh_model_forward")
+        return out
+
+    def generate(self, tokens, max_out: int) -> np.ndarray:
+        """inferbit_generate with temperature 0 (src/generate.c:243-300)."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        out = np.empty(max_out, np.int32)
+        n = lib().ibh_model_generate_greedy(self._h, _ptr(t), len(t), _ptr(out), max_out)
+        if n < 0:
+            check(n, "ibh_model_generate_greedy")
+        return out[:n]
+
+    def kv_prefill(self, k: np.ndarray, v: np.ndarray) -> None:
+        """Append positions to every layer's KV cache; k, v fp32 [layers][n_pos][kv_dim]."""
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        assert k.shape == v.shape and k.ndim == 3
+        check(lib().ibh_model_kv_prefill(self._h, _ptr(k), _ptr(v), k.shape[1]), "ibh_model_kv_prefill")
+
+    def kv_length(self) -> int:
+        return lib().ibh_model_kv_length(self._h)
+
+    def kv_clear(self) -> None:
+        check(lib().ibh_model_kv_clear(self._h), "ibh_model_kv_clear")
+
+    def kv_truncate(self, n: int) -> None:
+        check(lib().ibh_model_kv_truncate(self._h, n), "ibh_model_kv_truncate")
+
+    def decode_steps(self, n: int) -> None:
+        check(lib().ibh_model_decode_steps(self._h, n), "ibh_model_decode_steps")
+
+    def synchronize(self) -> None:
+        check(lib().ibh_model_synchronize(self._h), "ibh_model_synchronize")

@@ -1,0 +1,215 @@
+"""GPU decode (device-resident forward + greedy generate) against the
+reference library's CPU decode.
+
+* Small synthetic models: the reference's own `ref_decode` (oracle/_ref,
+  built from the reference sources) runs live on the same file; logits of the
+  prompt must agree to max|d| / max|logit| <= 1e-4 and the greedy token
+  streams must be identical.
+* Benchmark configurations (TinyLlama-1.1B and Mistral-7B shapes): the
+  models are regenerated from their seeds (SHA-256 checked against the
+  fixture) and the GPU token streams must equal the reference's streams
+  recorded in tests/golden/decode.json by tests/golden/gen_decode_golden.py.
+"""
+import hashlib
+import json
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN, ROOT
+
+pytestmark = pytest.mark.gpu
+
+REF_DECODE = os.path.join(ROOT, "oracle", "_ref", "ref_decode")
+MODEL_DIR = os.environ.get("IBH_MODEL_DIR", "/tmp/ibh_models")
+
+
+@pytest.fixture(scope="module")
+def L():
+    import libinferbit_amd as L
+    L.ops.init(0)
+    return L
+
+
+def tiny_cfg(**kw):
+    from libinferbit_amd import ibf
+    c = dict(ibf.TINYLLAMA, num_layers=2, hidden_size=256, num_heads=4, num_kv_heads=2, head_dim=64,
+             intermediate_size=512, vocab_size=1000, max_context_length=160)
+    c.update(kw)
+    return c
+
+
+def ref_run(path, prompt, n_out, tmp, kv=None, env=None):
+    if not os.path.exists(REF_DECODE):
+        pytest.skip("oracle/_ref/ref_decode not built (make -C oracle ref)")
+    pp, lp = str(tmp / "p.i32"), str(tmp / "lg.f32")
+    np.asarray(prompt, np.int32).tofile(pp)
+    cmd = [REF_DECODE, path, "1", "0", str(n_out), pp]
+    if kv is not None:
+        kp = str(tmp / "kv.f32")
+        with open(kp, "wb") as f:
+            f.write(np.ascontiguousarray(kv[0], np.float32).tobytes())
+            f.write(np.ascontiguousarray(kv[1], np.float32).tobytes())
+        cmd += [kp, str(kv[0].shape[1])]
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=300,
+                       env=dict(os.environ, REF_DECODE_LOGITS=lp, **(env or {})))
+    assert r.returncode == 0, r.stderr
+    return json.loads(r.stdout.strip().splitlines()[-1])["tokens"], np.fromfile(lp, np.float32)
+
+
+def relerr(a, b):
+    return float(np.abs(a.astype(np.float64) - b).max() / np.abs(b).max())
+
+
+TINY = {
+    "fp32kv": dict(kv_bits=32),
+    "int8kv": dict(kv_bits=8),
+    "int4kv": dict(kv_bits=4),
+    "mlp_int2": dict(kv_bits=8, bits=dict(gate_proj=2, up_proj=2, down_proj=2, o_proj=8)),
+    "all_int8": dict(kv_bits=8, bits=dict(o_proj=8, gate_proj=8, up_proj=8, down_proj=8)),
+    "int4_emb_head": dict(kv_bits=8, bits=dict(token_embedding=4, head=4)),
+}
+
+
+@pytest.mark.parametrize("name", list(TINY))
+def test_tiny_model_matches_reference(L, tmp_path, name):
+    from libinferbit_amd import ibf
+    from libinferbit_amd.model import Model
+    spec = dict(TINY[name])
+    bits = spec.pop("bits", None)
+    print(f"case decode tiny {name}", flush=True)
+    path = str(tmp_path / "m.ibf")
+    ibf.write_synthetic(path, tiny_cfg(**spec), seed=11, bits=bits)
+    prompt = [5, 17, 300, 42, 999, 0, 7]
+    ref_tokens, ref_logits = ref_run(path, prompt, 40, tmp_path)
+    m = Model(path)
+    logits = m.forward(prompt)
+    assert relerr(logits, ref_logits) <= 1e-4
+    m.kv_clear()
+    got = m.generate(prompt, 40)
+    assert got.tolist() == ref_tokens
+    m.close()
+
+
+def test_tiny_kv_prefill_matches_reference(L, tmp_path):
+    """KV prefilled through the kv_cache_write rule, then decode (the config-4 recipe)."""
+    from libinferbit_amd import ibf
+    from libinferbit_amd.model import Model
+    for kvb in (8, 4):
+        print(f"case decode tiny kv prefill bits={kvb}", flush=True)
+        cfg = tiny_cfg(kv_bits=kvb)
+        path = str(tmp_path / f"m{kvb}.ibf")
+        ibf.write_synthetic(path, cfg, seed=5)
+        shape = (cfg["num_layers"], 100, cfg["num_kv_heads"] * cfg["head_dim"])
+        k = ibf.fill_normal(int(np.prod(shape)), 1).reshape(shape)
+        v = ibf.fill_normal(int(np.prod(shape)), 2).reshape(shape)
+        ref_tokens, ref_logits = ref_run(path, [77], 30, tmp_path, kv=(k, v))
+        m = Model(path)
+        m.kv_prefill(k, v)
+        assert m.kv_length() == 100
+        logits = m.forward([77])
+        assert relerr(logits, ref_logits) <= 1e-4
+        m.kv_truncate(100)
+        assert m.generate([77], 30).tolist() == ref_tokens
+        m.close()
+
+
+def test_w4a8_disabled_matches_reference(L, tmp_path, monkeypatch):
+    """IB_W4A8=0 (forward.c:14-21) routes INT4 tensors through the fp32-activation matvec."""
+    from libinferbit_amd import ibf
+    from libinferbit_amd.model import Model
+    path = str(tmp_path / "m.ibf")
+    ibf.write_synthetic(path, tiny_cfg(kv_bits=8), seed=3)
+    ref_tokens, ref_logits = ref_run(path, [1, 2, 3], 30, tmp_path, env={"IB_W4A8": "0"})
+    monkeypatch.setenv("IB_W4A8", "0")
+    m = Model(path)
+    assert relerr(m.forward([1, 2, 3]), ref_logits) <= 1e-4
+    m.kv_clear()
+    assert m.generate([1, 2, 3], 30).tolist() == ref_tokens
+    m.close()
+
+
+def test_graph_replay_equals_eager(L, tmp_path, monkeypatch):
+    """The captured per-token graph gives bit-identical logits to eager launches,
+    replay after replay."""
+    from libinferbit_amd import ibf
+    from libinferbit_amd.model import Model
+    path = str(tmp_path / "m.ibf")
+    ibf.write_synthetic(path, tiny_cfg(kv_bits=8), seed=4)
+    prompt = list(range(10, 30))
+    g = Model(path)
+    a = [g.forward([t]) for t in prompt]
+    monkeypatch.setenv("IBH_DECODE_EAGER", "1")
+    e = Model(path)
+    b = [e.forward([t]) for t in prompt]
+    for x, y in zip(a, b):
+        np.testing.assert_array_equal(x, y)
+    g.close()
+    e.close()
+
+
+def test_model_api_errors(L, tmp_path):
+    from libinferbit_amd import IbhError, ibf
+    from libinferbit_amd.model import Model
+    path = str(tmp_path / "m.ibf")
+    ibf.write_synthetic(path, tiny_cfg(kv_bits=8, max_context_length=16), seed=4)
+    m = Model(path)
+    with pytest.raises(IbhError):
+        m.forward([1000])                       # token out of range
+    with pytest.raises(IbhError):
+        m.forward(list(range(17)))              # context exceeded
+    m.forward(list(range(16)))
+    assert m.kv_length() == 16
+    with pytest.raises(IbhError):
+        m.forward([1])                          # no room left
+    with pytest.raises(IbhError):
+        m.generate([1], 2)
+    m.close()
+    bad = tmp_path / "bad.ibf"
+    bad.write_bytes(b"NOTANIBF" + bytes(100))
+    with pytest.raises(IbhError):
+        Model(str(bad))
+
+
+def _sha256(path):
+    h = hashlib.sha256()
+    with open(path, "rb") as f:
+        for b in iter(lambda: f.read(1 << 24), b""):
+            h.update(b)
+    return h.hexdigest()
+
+
+def _golden_case(name):
+    p = os.path.join(GOLDEN, "decode.json")
+    if not os.path.exists(p):
+        pytest.skip("tests/golden/decode.json not generated")
+    d = json.load(open(p))
+    if name not in d:
+        pytest.skip(f"no {name} entry in decode.json")
+    return d[name]
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("name", ["tinyllama", "mistral"])
+def test_benchmark_config_tokens_match_reference(L, name):
+    import sys
+    sys.path.insert(0, GOLDEN)
+    import gen_decode_golden as G
+    from libinferbit_amd.model import Model
+    g = _golden_case(name)
+    os.makedirs(MODEL_DIR, exist_ok=True)
+    print(f"case decode {name}: writing model", flush=True)
+    path = G.ensure_model(name, MODEL_DIR)
+    assert _sha256(path) == g["model_sha256"], "synthetic model bytes differ from the fixture's"
+    print(f"case decode {name}: decoding", flush=True)
+    case = G.CASES[name]
+    m = Model(path)
+    if case["kv_pos"]:
+        k, v = G.kv_of(case)
+        m.kv_prefill(k, v)
+        del k, v
+    got = m.generate(np.asarray(g["prompt"], np.int32), g["n_out"])
+    m.close()
+    assert got.tolist() == g["tokens"]
