@@ -365,18 +365,10 @@ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 }  // namespace
 
-int ibh_launch_gemv_rows_b(float* out, const void* w, const void* scales, int kind, const float* x,
-                           const int8_t* qx, const float* sa, int M, int N, int bits, void* ws, hipStream_t st);
-size_t ibh_digits_bytes(int N, int bits);
-void* ibh_workspace(size_t bytes);
-int ibh_launch_gemv_rows_i8(float* out, const void* w, const void* scales, int kind, const float* x,
-                            const int8_t* qx, const float* sa, int M, int N, int bits, hipStream_t st);
-int ibh_launch_gemv_rows(float* out, const void* w, const void* scales, int kind, const float* x, int M,
-                         int N, int bits, hipStream_t st);
-int ibh_launch_gemv_i8_stream(float* out, const void* w, const void* scales, int kind, const float* x,
-                              const int8_t* qx, const float* sa, int M, int N, int bits, hipStream_t st);
-int ibh_launch_gemv_stream(float* out, const void* w, const void* scales, int kind, const float* x, int M,
-                           int N, int bits, hipStream_t st);
+int ibh_launch_rows_w4a8(float* out, const void* w, const void* sw, int kind, const int8_t* qx, const float* sa,
+                         int M, int N, hipStream_t st);
+int ibh_launch_rows_x(float* out, const void* w, const void* scales, int kind, const float* x, int M, int N,
+                      int bits, hipStream_t st);
 int ibh_launch_gemv_mfma(float* out, const void* w, const void* scales, int kind, const float* x, int M,
                          int N, int bits, hipStream_t st);
 int ibh_launch_w4a8_mfma(float* out, const void* w, const void* sw, int kind, const int8_t* qx, const float* sa,
@@ -384,19 +376,9 @@ int ibh_launch_w4a8_mfma(float* out, const void* w, const void* sw, int kind, co
 
 namespace {
 
-// IBH_GEMV_PATH=stream|tile|valu forces one fp32-activation GEMV kernel family
-// (tuning and profiling aid; default: first eligible of stream, tile, valu).
-int gemv_path() {
-    static int path = -1;
-    if (path < 0) {
-        const char* e = getenv("IBH_GEMV_PATH");
-        path = !e ? 0 : (!strcmp(e, "stream") ? 1 : !strcmp(e, "tile") ? 2 : !strcmp(e, "valu") ? 3
-                      : !strcmp(e, "i8") ? 4 : !strcmp(e, "rows") ? 5 : !strcmp(e, "rowsi8") ? 6
-                      : !strcmp(e, "rowsb") ? 7 : 0);
-    }
-    return path;
-}
-
+// Kernel choice for fp32 activations: the row-streaming int8 matrix-core
+// kernel where the shape allows it (int8 / int4, rows of whole 1 KiB steps),
+// else the 16-row tile kernel, else the VALU kernels.
 template <int KIND>
 int launch_matmul(float* out, const void* w, const void* scales, const float* x, int M, int N,
                   int bits, hipStream_t st) {
@@ -404,21 +386,8 @@ int launch_matmul(float* out, const void* w, const void* scales, const float* x,
     constexpr int R = 4;
     const int cpu = bits == 8 ? 16 : (bits == 4 ? 32 : 64);
     const bool fast = N % cpu == 0 && aligned16(w) && aligned16(x);
-    const int path = gemv_path();
-    void* ws = path == 7 ? ibh_workspace(ibh_digits_bytes(N, bits)) : nullptr;
-    if ((path == 0 || path == 2) && ibh_launch_gemv_mfma(out, w, scales, KIND, x, M, N, bits, st)) {
-        // 16-row tile matrix-core path (default: fastest measured for fp32 activations)
-    } else if (path == 7 && ws &&
-               ibh_launch_gemv_rows_b(out, w, scales, KIND, x, nullptr, nullptr, M, N, bits, ws, st)) {
-        // digit-plane prep + row-owning integer matrix-core GEMV
-    } else if (path == 6 && ibh_launch_gemv_rows_i8(out, w, scales, KIND, x, nullptr, nullptr, M, N, bits, st)) {
-        // row-owning integer matrix-core path, per-block digit prologue
-    } else if (path == 5 && ibh_launch_gemv_rows(out, w, scales, KIND, x, M, N, bits, st)) {
-        // row-owning f16 matrix-core path
-    } else if (path == 4 && ibh_launch_gemv_i8_stream(out, w, scales, KIND, x, nullptr, nullptr, M, N, bits, st)) {
-        // persistent streaming integer matrix-core path
-    } else if (path == 1 && ibh_launch_gemv_stream(out, w, scales, KIND, x, M, N, bits, st)) {
-        // persistent streaming f16 matrix-core path
+    if (ibh_launch_rows_x(out, w, scales, KIND, x, M, N, bits, st)) {
+    } else if (ibh_launch_gemv_mfma(out, w, scales, KIND, x, M, N, bits, st)) {
     } else if (fast) {
         const int blocks = (M + R * kWavesPerBlock - 1) / (R * kWavesPerBlock);
         if (bits == 8) gemv_f32_fast<8, KIND, R><<<blocks, kBlock, 0, st>>>(out, W, scales, x, M, N);
@@ -434,22 +403,15 @@ int launch_matmul(float* out, const void* w, const void* scales, const float* x,
     return IBH_OK;
 }
 
+// W4A8: FUSED = the x86 AVX2 kernel's fold (single-vector entry), otherwise
+// the scalar batched kernel's (mul and add rounded apart).
 template <int KIND, bool FUSED>
 int launch_w4a8(float* out, const void* w, const void* sw, const int8_t* qx, const float* sa, int M,
                 int N, int B, int M_stride, hipStream_t st) {
     const uint8_t* W = (const uint8_t*)w;
     const bool fast = N % 32 == 0 && aligned16(w) && aligned16(qx);
-    if (FUSED && B == 1 && M_stride == M && (gemv_path() == 0 || gemv_path() == 7) &&
-        ibh_launch_gemv_rows_b(out, w, sw, KIND, nullptr, qx, sa, M, N, 4, nullptr, st)) {
-        // row-owning integer matrix-core path
-    } else if (FUSED && B == 1 && M_stride == M && gemv_path() == 6 &&
-        ibh_launch_gemv_rows_i8(out, w, sw, KIND, nullptr, qx, sa, M, N, 4, st)) {
-        // row-owning integer matrix-core path
-    } else if (FUSED && B == 1 && M_stride == M && gemv_path() == 4 &&
-        ibh_launch_gemv_i8_stream(out, w, sw, KIND, nullptr, qx, sa, M, N, 4, st)) {
-        // integer matrix-core streaming path
+    if (FUSED && B == 1 && M_stride == M && ibh_launch_rows_w4a8(out, w, sw, KIND, qx, sa, M, N, st)) {
     } else if (ibh_launch_w4a8_mfma(out, w, sw, KIND, qx, sa, M, N, B, M_stride, FUSED, st)) {
-        // matrix-core path
     } else if (fast && B == 1) {
         constexpr int R = 4;
         const int blocks = (M + R * kWavesPerBlock - 1) / (R * kWavesPerBlock);

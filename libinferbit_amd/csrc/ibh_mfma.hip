@@ -411,299 +411,3 @@ int ibh_launch_w4a8_mfma(float* out, const void* w, const void* sw, int kind, co
     }
     return 1;
 }
-
-// ── streaming row-contiguous GEMV (fp32 activations) ──────────────────────
-//
-// Each wavefront streams whole rows: one load instruction moves 1 KiB of a
-// row (lane l reads bytes 16l..16l+15 of the current 1 KiB segment), R rows
-// per step, with the next P steps' loads in flight while the current step
-// is contracted.  The contraction uses the MFMA "diagonal" form: A row i =
-// the 8 codes lane (i, q) holds, B column j = the x values of the columns
-// lane (j, q) covers, so D[i][i] is lane i's partial dot product and the
-// row result is the trace of D (hi and lo x halves accumulate into the same
-// D).  x is split to f16 hi/lo once per block into LDS, laid out so each
-// lane reads its B operands with one conflict-free ds_read_b128 per plane.
-namespace {
-
-template <int BITS, int KIND, int R, int P>
-__global__ __launch_bounds__(256) void gemv_stream(float* __restrict__ y,
-                                                   const uint8_t* __restrict__ W,
-                                                   const void* __restrict__ sc,
-                                                   const float* __restrict__ x,
-                                                   int M, int N, int S) {
-    constexpr int SEGC = Seg<BITS>::kCols;              // columns per lane-load
-    constexpr int NM = Seg<BITS>::kMfma;
-    extern __shared__ __align__(16) unsigned char smem[];
-    const int lane = threadIdx.x & 63;
-    const int nslot = S * NM * 64;                       // uint4 per plane
-    uint4* xh = (uint4*)smem;
-    uint4* xl = xh + nslot;
-    __shared__ float wmax[4];
-
-    // ---- block prologue: x -> f16 hi/lo planes ---------------------------
-    float mx = 0.f;
-    for (int c = threadIdx.x * 4; c < N; c += 1024) {
-        const float4 v = *(const float4*)(x + c);
-        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-    }
-    mx = wave_max(mx);
-    if (lane == 0) wmax[threadIdx.x >> 6] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-    int e = 0;
-    if (mx >= 16384.f) { (void)frexpf(mx, &e); e -= 14; }
-    const float s_in = ldexpf(1.f, -e), s_out = ldexpf(1.f, e);
-    for (int g = threadIdx.x; g < nslot; g += 256) {
-        const int l = g & 63, m = (g >> 6) % NM, s = g / (64 * NM);
-        const int base = (64 * s + l) * SEGC;
-        _Float16 hi[8], lo[8];
-#pragma unroll
-        for (int t = 0; t < 8; t++) {
-            const int c = base + col_of<BITS>(m, t);
-            const float v = c < N ? x[c] * s_in : 0.f;
-            hi[t] = (_Float16)v;
-            lo[t] = (_Float16)(v - (float)hi[t]);
-        }
-        xh[g] = __builtin_bit_cast(uint4, h8_t{hi[0], hi[1], hi[2], hi[3], hi[4], hi[5], hi[6], hi[7]});
-        xl[g] = __builtin_bit_cast(uint4, h8_t{lo[0], lo[1], lo[2], lo[3], lo[4], lo[5], lo[6], lo[7]});
-    }
-    __syncthreads();
-
-    // ---- stream row groups ------------------------------------------------
-    const size_t rb = (size_t)N * BITS / 8;
-    const int RG = (M + R - 1) / R;
-    const int nwaves = gridDim.x * 4;
-    const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int my_rg = gw < RG ? (RG - gw + nwaves - 1) / nwaves : 0;
-    const int nsteps = my_rg * S;
-    const size_t lane_off = 16 * (size_t)lane;
-
-    // step k -> row group gw + (k / S) * nwaves, segment k % S
-    auto issue = [&](int k, uint4 (&buf)[R]) {
-        const int kk = min(k, max(nsteps - 1, 0));
-        const int rg = gw + (kk / S) * nwaves, s = kk % S;
-        const size_t off = min((size_t)s * 1024 + lane_off, rb - 16);
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            const int row = min(rg * R + r, M - 1);
-            buf[r] = ld_stream16(W + (size_t)row * rb + off);
-        }
-    };
-
-    uint4 ring[P][R];
-#pragma unroll
-    for (int p = 0; p < P; p++) issue(p, ring[p]);
-
-    f4_t acc[R];
-#pragma unroll
-    for (int r = 0; r < R; r++) acc[r] = f4_t{0.f, 0.f, 0.f, 0.f};
-    const bool diag = ((lane & 15) >> 2) == (lane >> 4);
-    const int dsel = lane & 3;
-
-    for (int k0 = 0; k0 < nsteps; k0 += P) {
-#pragma unroll
-        for (int p = 0; p < P; p++) {
-            const int k = k0 + p;
-            if (k < nsteps) {
-                const int s = k % S;
-                uint4 cur[R];
-#pragma unroll
-                for (int r = 0; r < R; r++) cur[r] = ring[p][r];
-                issue(k + P, ring[p]);
-#pragma unroll
-                for (int m = 0; m < NM; m++) {
-                    const int g = (s * NM + m) * 64 + lane;
-                    const h8_t bh = __builtin_bit_cast(h8_t, xh[g]);
-                    const h8_t bl = __builtin_bit_cast(h8_t, xl[g]);
-#pragma unroll
-                    for (int r = 0; r < R; r++) {
-                        const h8_t a = make_a<BITS>(cur[r], m);
-                        acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bh, acc[r], 0, 0, 0);
-                        acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bl, acc[r], 0, 0, 0);
-                    }
-                }
-                if (s == S - 1) {                        // row group done: trace of D
-                    const int rg = gw + (k / S) * nwaves;
-#pragma unroll
-                    for (int r = 0; r < R; r++) {
-                        float v = dsel == 0 ? acc[r][0] : dsel == 1 ? acc[r][1] : dsel == 2 ? acc[r][2] : acc[r][3];
-                        v = wave_sum(diag ? v : 0.f);
-                        const int row = rg * R + r;
-                        if (lane == 0 && row < M) y[row] = (v * s_out) * load_scale<KIND>(sc, row);
-                        acc[r] = f4_t{0.f, 0.f, 0.f, 0.f};
-                    }
-                }
-            }
-        }
-    }
-}
-
-}  // namespace
-
-int ibh_launch_gemv_stream(float* out, const void* w, const void* scales, int kind, const float* x, int M,
-                           int N, int bits, hipStream_t st) {
-    const int segc = bits == 8 ? 16 : (bits == 4 ? 32 : 64);
-    const size_t rb = (size_t)N * bits / 8;
-    if (N % segc != 0 || rb < 16 || ((uintptr_t)w & 15) || ((uintptr_t)x & 15) || N % 4) return 0;
-    const int S = (int)((rb + 1023) / 1024);
-    const int NM = segc / 8;
-    const size_t lds = (size_t)S * NM * 64 * 16 * 2;
-    if (lds > 160 * 1024) return 0;
-    constexpr int P = 4;
-    const int R = M >= 8192 ? 4 : 2;
-    const int RG = (M + R - 1) / R;
-    int blocks = (RG + 3) / 4;
-    if (blocks > 1024) blocks = 1024;
-    const uint8_t* W = (const uint8_t*)w;
-#define IBH_GS(B_, K_, R_)                                                                     \
-    do {                                                                                       \
-        if (!set_lds((const void*)gemv_stream<B_, K_, R_, P>, lds)) return 0;                  \
-        gemv_stream<B_, K_, R_, P><<<blocks, 256, lds, st>>>(out, W, scales, x, M, N, S);      \
-    } while (0)
-#define IBH_GS2(B_, K_) do { if (R == 4) IBH_GS(B_, K_, 4); else IBH_GS(B_, K_, 2); } while (0)
-    if (kind == IBH_SCALE_F16) {
-        if (bits == 8) IBH_GS2(8, IBH_SCALE_F16); else if (bits == 4) IBH_GS2(4, IBH_SCALE_F16); else IBH_GS2(2, IBH_SCALE_F16);
-    } else {
-        if (bits == 8) IBH_GS2(8, IBH_SCALE_F32); else if (bits == 4) IBH_GS2(4, IBH_SCALE_F32); else IBH_GS2(2, IBH_SCALE_F32);
-    }
-#undef IBH_GS
-#undef IBH_GS2
-    return 1;
-}
-
-// ── row-owning GEMV (fp32 activations), the default path ──────────────────
-//
-// Memory shape that streams at full HBM rate on MI355X: short-lived
-// wavefronts that each own R whole rows (or, for long rows, one slice of K
-// for R rows) and issue every load up front in straight-line code, one
-// contiguous 1 KiB step of one row per load instruction (lane l reads bytes
-// 16l..16l+15 of the step).  A block is KW wavefronts that split the steps
-// of the same R rows; their partial sums meet in LDS.
-//
-// Math: v_mfma_f32_16x16x32_f16 in diagonal form.  A row i = the codes of
-// the 16-byte segments held by lanes i, i+16, i+32, i+48 (exact f16, as in
-// make_a), B column j = f16 hi/lo split of the x values of lane j's own
-// columns, so trace(D) over the hi and lo products is the fp32 dot product
-// (to ~2^-22 per term).  Each wavefront splits only the x values of its own
-// columns, after scaling by a power of two chosen from its max|x| so that
-// nothing overflows f16.
-namespace {
-
-template <int BITS, int KIND, int R, int SPW>
-__global__ __launch_bounds__(512) void gemv_rows(float* __restrict__ y,
-                                                  const uint8_t* __restrict__ W,
-                                                  const void* __restrict__ sc,
-                                                  const float* __restrict__ x,
-                                                  int M, int N, int S) {
-    constexpr int SEGC = Seg<BITS>::kCols;               // columns per 16-byte segment
-    constexpr int NM = Seg<BITS>::kMfma;
-    constexpr int STEPC = 64 * SEGC;                      // columns per 1 KiB step
-    __shared__ float red[8][R];
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int KW = blockDim.x >> 6;
-    const int row0 = blockIdx.x * R;
-    const size_t rb = (size_t)N * BITS / 8;
-
-    // ---- loads: per step, x slice first, then the R weight segments --------
-    float4 xv[SPW][SEGC / 4];
-    uint4 wv[SPW][R];
-    bool live[SPW];
-#pragma unroll
-    for (int j = 0; j < SPW; j++) {
-        const int s = wave * SPW + j;
-        const size_t off = (size_t)min(s, S - 1) * 1024 + 16 * (size_t)lane;
-        live[j] = s < S && off < rb;
-        const size_t offc = min(off, rb - 16);
-        const float* xp = x + offc / BITS * 8;            // first column of this segment
-#pragma unroll
-        for (int t = 0; t < SEGC / 4; t++) xv[j][t] = ((const float4*)xp)[t];
-#pragma unroll
-        for (int r = 0; r < R; r++) wv[j][r] = ld_stream16(W + (size_t)min(row0 + r, M - 1) * rb + offc);
-    }
-
-    // ---- scale so |x * 2^-e| < 2^14 (f16-safe), split into hi/lo ----------
-    float mx = 0.f;
-#pragma unroll
-    for (int j = 0; j < SPW; j++)
-#pragma unroll
-        for (int t = 0; t < SEGC / 4; t++)
-            if (live[j]) mx = fmaxf(mx, fmaxf(fmaxf(fabsf(xv[j][t].x), fabsf(xv[j][t].y)),
-                                            fmaxf(fabsf(xv[j][t].z), fabsf(xv[j][t].w))));
-    mx = wave_max(mx);
-    int e = 0;
-    if (mx >= 16384.f) { (void)frexpf(mx, &e); e -= 14; }
-    const float s_in = ldexpf(1.f, -e);
-
-    f4_t acc[R];
-#pragma unroll
-    for (int r = 0; r < R; r++) acc[r] = f4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < SPW; j++) {
-        const float* v = (const float*)&xv[j][0];
-#pragma unroll
-        for (int m = 0; m < NM; m++) {
-            _Float16 hi[8], lo[8];
-#pragma unroll
-            for (int t = 0; t < 8; t++) {
-                const float u = live[j] ? v[col_of<BITS>(m, t)] * s_in : 0.f;
-                hi[t] = (_Float16)u;
-                lo[t] = (_Float16)(u - (float)hi[t]);
-            }
-            const h8_t bh = {hi[0], hi[1], hi[2], hi[3], hi[4], hi[5], hi[6], hi[7]};
-            const h8_t bl = {lo[0], lo[1], lo[2], lo[3], lo[4], lo[5], lo[6], lo[7]};
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                const h8_t a = make_a<BITS>(wv[j][r], m);
-                acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bh, acc[r], 0, 0, 0);
-                acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bl, acc[r], 0, 0, 0);
-            }
-        }
-    }
-
-    // ---- trace(D) per row, wavefront partials through LDS -----------------
-    const bool diag = ((lane & 15) >> 2) == (lane >> 4);
-    const int dsel = lane & 3;
-    const float s_out = ldexpf(1.f, e);
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-        float v = dsel == 0 ? acc[r][0] : dsel == 1 ? acc[r][1] : dsel == 2 ? acc[r][2] : acc[r][3];
-        v = wave_sum(diag ? v : 0.f) * s_out;
-        if (lane == 0) red[wave][r] = v;
-    }
-    __syncthreads();
-    if (threadIdx.x < R && row0 + (int)threadIdx.x < M) {
-        float t = 0.f;
-        for (int w = 0; w < KW; w++) t += red[w][threadIdx.x];
-        y[row0 + threadIdx.x] = t * load_scale<KIND>(sc, row0 + threadIdx.x);
-    }
-}
-
-}  // namespace
-
-int ibh_launch_gemv_rows(float* out, const void* w, const void* scales, int kind, const float* x, int M,
-                         int N, int bits, hipStream_t st) {
-    const int segc = bits == 8 ? 16 : (bits == 4 ? 32 : 64);
-    const size_t rb = (size_t)N * bits / 8;
-    if (N % segc != 0 || rb < 16 || ((uintptr_t)w & 15) || ((uintptr_t)x & 15)) return 0;
-    const int S = (int)((rb + 1023) / 1024);
-    // steps per wavefront: 2 when S is even (or S == 1 uses 1), else 1
-    const int spw = (S % 2 == 0 || bits == 2) && S > 1 ? 2 : 1;
-    const int KW = (S + spw - 1) / spw;
-    if (KW > 8) return 0;
-    constexpr int R = 8;
-    const int blocks = (M + R - 1) / R;
-    const uint8_t* W = (const uint8_t*)w;
-#define IBH_GR(B_, K_)                                                                                   \
-    do {                                                                                                 \
-        if (spw == 2) gemv_rows<B_, K_, R, 2><<<blocks, 64 * KW, 0, st>>>(out, W, scales, x, M, N, S);   \
-        else gemv_rows<B_, K_, R, 1><<<blocks, 64 * KW, 0, st>>>(out, W, scales, x, M, N, S);            \
-    } while (0)
-    if (kind == IBH_SCALE_F16) {
-        if (bits == 8) IBH_GR(8, IBH_SCALE_F16); else if (bits == 4) IBH_GR(4, IBH_SCALE_F16); else IBH_GR(2, IBH_SCALE_F16);
-    } else {
-        if (bits == 8) IBH_GR(8, IBH_SCALE_F32); else if (bits == 4) IBH_GR(4, IBH_SCALE_F32); else IBH_GR(2, IBH_SCALE_F32);
-    }
-#undef IBH_GR
-    return 1;
-}
