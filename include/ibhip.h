@@ -165,9 +165,17 @@ int    ibh_pq_matmul(const ibh_pq_tensor* t, const float* x, float* out, void* w
 typedef struct ibh_model ibh_model;
 int  ibh_model_load(const char* path, int context_length, ibh_model** out);
 void ibh_model_free(ibh_model* model);
-/* dims[12] = layers, hidden, heads, kv_heads, head_dim, intermediate, vocab,
- * max_context_length, kv_bits, kv capacity, eos_token_id, usable positions */
+/* dims[13] = layers, hidden, heads, kv_heads, head_dim, intermediate, vocab,
+ * max_context_length, kv_bits, kv capacity, eos_token_id, usable positions,
+ * exact mode (1/0) */
 int  ibh_model_dims(const ibh_model* model, int* dims);
+/* Exact mode (the default; IBH_DECODE_FAST=1 at load turns it off): every
+ * kernel follows the x86 reference's fp32 operation order (AVX2 lane
+ * accumulators, FMA where its build fuses, glibc expf), so logits and token
+ * streams are bit-identical to the CPU's.  Fast mode uses the row-streaming
+ * matrix-core matvecs and split-T attention: logits within fp32 tolerance.
+ * No reference counterpart (the reference has one CPU path). */
+int  ibh_model_set_exact(ibh_model* model, int exact);
 int  ibh_model_forward(ibh_model* model, const int32_t* tokens, int num_tokens, float* logits,
                        int vocab_size);
 /* Returns the number of tokens written (stops after end-of-sequence, as
@@ -187,6 +195,9 @@ int  ibh_model_decode_steps(ibh_model* model, int n);
 int  ibh_model_synchronize(ibh_model* model);
 
 /* ── host-side producers of the packed formats (no device work) ── */
+
+/* The device expf restatement evaluated on the host (checks against libm). */
+void   ibh_expf_host(const float* x, float* y, size_t n);
 
 /* ib_quantize_int8 / _int4 / _int2 (src/quantize.c:75-239) on fp32 rows:
  * packed bytes as in ibh_matmul, truncated fp16 scales.  Bit-identical. */

@@ -40,6 +40,7 @@ SIGNATURES = {
     "ibh_model_dims": (I, [P, P]),
     "ibh_model_forward": (I, [P, P, I, P, I]),
     "ibh_model_generate_greedy": (I, [P, P, I, P, I]),
+    "ibh_model_set_exact": (I, [P, I]),
     "ibh_model_kv_length": (I, [P]),
     "ibh_model_kv_clear": (I, [P]),
     "ibh_model_kv_truncate": (I, [P, I]),
@@ -49,6 +50,7 @@ SIGNATURES = {
     "ibh_packed_row_bytes": (SZ, [I, I]),
     "ibh_quantize_rows": (I, [I, P, I, I, P, P]),
     "ibh_fill_normal": (I, [P, SZ, C.c_uint64, C.c_uint64, C.c_float]),
+    "ibh_expf_host": (None, [P, P, SZ]),
     "ib_init_kernels_hip": (None, [P]),
     "ibh_register_host_weights": (I, [P, SZ, C.POINTER(P)]),
     "ibh_unregister_host_weights": (None, [P]),

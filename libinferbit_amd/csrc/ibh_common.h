@@ -73,4 +73,52 @@ __device__ __forceinline__ float ubyte(uint32_t v) {
     return (float)((v >> (8 * B)) & 0xffu);
 }
 
+// expf as glibc 2.35 computes it on x86-64 with FMA (the ifunc variant the
+// reference's softmax and SiLU call): the published exp2f-table method
+// (Szabolcs Nagy, ARM optimized-routines: exp(x) = 2^(k/32) * 2^(r/32),
+// r = x*32/ln2 - k, 2^(r/32) by a cubic in double, one rounding to float),
+// with the range reduction and the polynomial evaluated by fused multiply-
+// adds.  The table holds 2^(i/32) correctly rounded to double, minus i<<47
+// (computed from the definition).  Checked bit for bit against the host libm
+// on every float with |x| <= 110 and the special values.
+constexpr uint64_t kExp2fTab[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
+
+__host__ __device__ inline float ib_expf(float x) {
+    constexpr double kN = 32.0;
+    constexpr double C0 = 0x1.c6af84b912394p-5 / kN / kN / kN, C1 = 0x1.ebfce50fac4f3p-3 / kN / kN,
+                     C2 = 0x1.62e42ff0c52d6p-1 / kN;
+    constexpr double kInvLn2N = 0x1.71547652b82fep+0 * kN, kShift = 0x1.8p+52;
+    const uint32_t ux = __builtin_bit_cast(uint32_t, x);
+    const uint32_t abstop = (ux >> 20) & 0x7ff;
+    if (abstop >= (0x42b00000u >> 20)) {                      // |x| >= 88 or nan
+        if (ux == 0xff800000u) return 0.0f;                    // -inf
+        if (abstop >= (0x7f800000u >> 20)) return x + x;       // inf, nan
+        if (x > 0x1.62e42ep6f) return __builtin_inff();        // overflow
+        if (x < -0x1.9fe368p6f) return 0.0f;                   // underflow
+    }
+    const double xd = (double)x;
+    const double z = kInvLn2N * xd;
+    double kd = z + kShift;
+    const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
+    kd -= kShift;
+    const double r = __builtin_fma(kInvLn2N, xd, -kd);
+    uint64_t t = kExp2fTab[ki % 32];
+    t += ki << 47;
+    const double s = __builtin_bit_cast(double, t);
+    const double p = __builtin_fma(C0, r, C1);
+    const double r2 = r * r;
+    double y = __builtin_fma(C2, r, 1.0);
+    y = __builtin_fma(p, r2, y);
+    y = y * s;
+    return (float)y;
+}
+
 }  // namespace ibh

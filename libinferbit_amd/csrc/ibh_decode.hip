@@ -40,6 +40,18 @@ int ibh_launch_attn(float* out, const float* q, const void* kdata, const void* v
                     const float* vscales, int pos, const int* dpos, int max_pos, int n_heads, int n_kv,
                     int head_dim, int kv_bits, void* ws, size_t ws_bytes, hipStream_t st);
 
+int ibh_launch_rmsnorm_exact(float* out, float* x, const float* delta, const uint16_t* w, float eps, int n,
+                             hipStream_t st);
+int ibh_launch_matvec_exact(float* y, const void* w, const void* sc, int kind, const float* x, int M, int N, int bits,
+                            const uint8_t* mask, hipStream_t st);
+int ibh_launch_rope_exact(float* q, float* k, const float* table, const int* dpos, int n_heads, int n_kv, int hd,
+                          hipStream_t st);
+int ibh_launch_silu_mul_exact(float* out, const float* g, const float* u, const uint8_t* mask, int n, hipStream_t st);
+size_t ibh_attn_exact_scratch(int n_heads, int max_pos);
+int ibh_launch_attn_exact(float* out, const float* q, const void* kdata, const void* vdata, const float* ks,
+                          const float* vs, const int* dpos, int max_pos, int n_heads, int n_kv, int hd, int kv_bits,
+                          float* att, hipStream_t st);
+
 namespace {
 
 // ── minimal JSON reader (the IBF header is plain JSON, ibf_loader.c:124-221) ──
@@ -197,6 +209,7 @@ struct DLayer {
     const uint16_t* in_norm = nullptr;
     const uint16_t* post_norm = nullptr;
     const uint8_t* mask = nullptr;   // sparsity mask [inter] or null
+    bool mask_sparse = false;        // <= 80 % of the rows active: serial row path (forward.c:273-317)
     uint8_t* kd = nullptr;
     uint8_t* vd = nullptr;
     float* ks = nullptr;
@@ -349,6 +362,8 @@ struct ibh_model {
     int kv_bits = 8, eos = 2, capacity = 0, max_pos = 0;
     float theta = 10000.f, eps = 1e-5f;
     bool w4a8 = true;
+    bool exact = true;               // bit-identical to the x86 reference (default)
+    float* att = nullptr;            // exact attention scores [n_heads][max_pos + 1]
     uint8_t* dweights = nullptr;
     size_t wbytes = 0;
     std::vector<DLayer> layers;
@@ -398,8 +413,55 @@ int mm(ibh_model* m, const DTensor& t, float* out, const float* in, int M, int N
     return IBH_OK;
 }
 
-// One decode position: forward_single_ex(compute_logits=1) + greedy pick.
+// tensor_matmul / tensor_matmul_sparse (forward.c:144-317) with the
+// x86-identical kernels.  `mask` (gate/up only) zeroes inactive rows.
+int mm_exact(ibh_model* m, const DTensor& t, float* out, const float* in, int M, int N, const uint8_t* mask,
+             bool sparse) {
+    if (mask && sparse)
+        return ibh_launch_matvec_exact(out, t.w, t.s, t.skind, in, M, N, t.bits, mask, m->st);
+    if (t.bits == 4 && m->w4a8)
+        return ibh_matmul_w4a8_x(out, t.w, t.s, t.skind, in, M, N, m->qx, m->sa, (void*)m->st);
+    return ibh_launch_matvec_exact(out, t.w, t.s, t.skind, in, M, N, t.bits, nullptr, m->st);
+}
+
+// forward_single_ex(compute_logits=1) + greedy pick, bit-identical to the CPU.
+int step_exact(ibh_model* m) {
+    const int H = m->hidden, kv_dim = m->n_kv * m->head_dim;
+    int rc;
+    embed_kernel<<<(H + 255) / 256, 256, 0, m->st>>>(m->x, m->emb.w, (const uint16_t*)(m->emb.skind == IBH_SCALE_F16 ? m->emb.s : nullptr),
+                                                     m->emb.bits, H, m->dtokens(), m->dpos());
+    IBH_CHECK_LAUNCH("ibh_model: embedding");
+    for (int l = 0; l < m->n_layers; l++) {
+        DLayer& L = m->layers[l];
+        if ((rc = ibh_launch_rmsnorm_exact(m->xb, m->x, l ? m->xb : nullptr, L.in_norm, m->eps, H, m->st)) ||
+            (rc = mm_exact(m, L.q, m->q, m->xb, H, H, nullptr, false)) ||
+            (rc = mm_exact(m, L.k, m->k, m->xb, kv_dim, H, nullptr, false)) ||
+            (rc = mm_exact(m, L.v, m->v, m->xb, kv_dim, H, nullptr, false)) ||
+            (rc = ibh_launch_rope_exact(m->q, m->k, m->rope, m->dpos(), m->n_heads, m->n_kv, m->head_dim, m->st)) ||
+            (rc = ibh_launch_kv_write(L.kd, L.vd, L.ks, L.vs, 0, m->dpos(), m->k, m->v, m->n_kv, m->head_dim,
+                                      m->kv_bits, 1, m->st)) ||
+            (rc = ibh_launch_attn_exact(m->xb2, m->q, L.kd, L.vd, L.ks, L.vs, m->dpos(), m->max_pos, m->n_heads,
+                                        m->n_kv, m->head_dim, m->kv_bits, m->att, m->st)) ||
+            (rc = mm_exact(m, L.o, m->xb, m->xb2, H, H, nullptr, false)) ||
+            (rc = ibh_launch_rmsnorm_exact(m->xb2, m->x, m->xb, L.post_norm, m->eps, H, m->st)) ||
+            (rc = mm_exact(m, L.gate, m->hb, m->xb2, m->inter, H, L.mask, L.mask_sparse)) ||
+            (rc = mm_exact(m, L.up, m->hb2, m->xb2, m->inter, H, L.mask, L.mask_sparse)) ||
+            (rc = ibh_launch_silu_mul_exact(m->hb, m->hb, m->hb2, L.mask, m->inter, m->st)) ||
+            (rc = mm_exact(m, L.down, m->xb, m->hb, H, m->inter, nullptr, false)))
+            return rc;
+    }
+    if ((rc = ibh_launch_rmsnorm_exact(m->x, m->x, m->xb, m->out_norm, m->eps, H, m->st)) ||
+        (rc = mm_exact(m, m->head, m->logits, m->x, m->vocab, H, nullptr, false)))
+        return rc;
+    argmax_advance_kernel<<<1, 1024, 0, m->st>>>(m->logits, m->vocab, m->dtokens(), m->dpos(), m->dprompt_end());
+    IBH_CHECK_LAUNCH("ibh_model: argmax");
+    return IBH_OK;
+}
+
+// One decode position with the fastest kernels (results within fp32
+// tolerance of the CPU): forward_single_ex(compute_logits=1) + greedy pick.
 int step(ibh_model* m) {
+    if (m->exact) return step_exact(m);
     const int H = m->hidden, kv_dim = m->n_kv * m->head_dim;
     int rc;
     embed_kernel<<<(H + 255) / 256, 256, 0, m->st>>>(m->x, m->emb.w, (const uint16_t*)(m->emb.skind == IBH_SCALE_F16 ? m->emb.s : nullptr),
@@ -592,6 +654,11 @@ int load(ibh_model* m, const char* path, int context_length) {
         return IBH_ERROR_PARAM;
     }
     m->w4a8 = w4a8_enabled();
+    {
+        const char* f = getenv("IBH_DECODE_FAST");
+        m->exact = !(f && f[0] == '1');
+        if (m->hidden % 8 || m->hidden > 12288) m->exact = false;   // no x86-order rmsnorm: fast kernels
+    }
 
     // weights: staged through a pinned buffer, copied once
     int rc;
@@ -683,6 +750,11 @@ int load(ibh_model* m, const char* path, int context_length) {
                 return IBH_ERROR_FORMAT;
             }
             L.mask = m->dweights + moff;
+            std::vector<uint8_t> hm(I);
+            IBH_HIP(hipMemcpy(hm.data(), L.mask, I, hipMemcpyDeviceToHost), "ibh_model_load: mask");
+            size_t active = 0;
+            for (uint8_t v : hm) active += v != 0;
+            L.mask_sparse = !(active > I * 4 / 5);
         }
         if ((rc = dalloc(m, (void**)&L.kd, kv_row * m->capacity)) ||
             (rc = dalloc(m, (void**)&L.vd, kv_row * m->capacity)))
@@ -715,6 +787,7 @@ int load(ibh_model* m, const char* path, int context_length) {
         (rc = dalloc(m, (void**)&m->sa, ((H > I ? H : I) / 128 + 2) * 4)) ||
         (rc = dalloc(m, (void**)&m->dstate, ((size_t)m->capacity + 3) * 4)))
         return rc;
+    if ((rc = dalloc(m, (void**)&m->att, ibh_attn_exact_scratch(m->n_heads, m->max_pos)))) return rc;
     m->attn_ws_bytes = ibh_attn_workspace_bytes(m->n_heads, m->head_dim, m->max_pos + 1);
     if ((rc = dalloc(m, &m->attn_ws, m->attn_ws_bytes))) return rc;
     // RoPE table with the host libm, as the CPU kernel evaluates it
@@ -726,8 +799,10 @@ int load(ibh_model* m, const char* path, int context_length) {
             for (int j = 0; j < half; j++) {
                 const float freq = 1.0f / powf(m->theta, (float)(2 * j) / (float)m->head_dim);
                 const float ang = (float)p * freq;
-                tab[((size_t)p * half + j) * 2] = cosf(ang);
-                tab[((size_t)p * half + j) * 2 + 1] = sinf(ang);
+                float sn, cs;
+                sincosf(ang, &sn, &cs);   // the x86 build calls sincosf for cosf + sinf
+                tab[((size_t)p * half + j) * 2] = cs;
+                tab[((size_t)p * half + j) * 2 + 1] = sn;
             }
         if ((rc = dalloc(m, (void**)&m->rope, tab.size() * 4))) return rc;
         IBH_HIP(hipMemcpy(m->rope, tab.data(), tab.size() * 4, hipMemcpyHostToDevice), "ibh_model_load: rope");
@@ -766,9 +841,23 @@ extern "C" int ibh_model_dims(const ibh_model* m, int* d) {
         ibh_set_error("ibh_model_dims: null argument");
         return IBH_ERROR_PARAM;
     }
-    const int v[12] = {m->n_layers, m->hidden, m->n_heads, m->n_kv,     m->head_dim, m->inter,
-                       m->vocab,    m->max_ctx, m->kv_bits, m->capacity, m->eos,     m->max_pos + 1};
+    const int v[13] = {m->n_layers, m->hidden,   m->n_heads, m->n_kv, m->head_dim,    m->inter, m->vocab,
+                       m->max_ctx,  m->kv_bits,  m->capacity, m->eos, m->max_pos + 1, m->exact ? 1 : 0};
     memcpy(d, v, sizeof v);
+    return IBH_OK;
+}
+
+extern "C" int ibh_model_set_exact(ibh_model* m, int exact) {
+    if (!m) return IBH_ERROR_PARAM;
+    if (exact && (m->hidden % 8 || m->hidden > 12288)) {
+        ibh_set_error("ibh_model_set_exact: hidden size %d has no exact kernel (multiple of 8, <= 12288)", m->hidden);
+        return IBH_ERROR_PARAM;
+    }
+    if ((bool)exact != m->exact && m->exec) {
+        hipGraphExecDestroy(m->exec);
+        m->exec = nullptr;
+    }
+    m->exact = exact != 0;
     return IBH_OK;
 }
 

@@ -456,7 +456,7 @@ int ibh_launch_rows_w4a8(float* out, const void* w, const void* sw, int kind, co
                          int M, int N, hipStream_t st) {
     const size_t rb = (size_t)N / 2;
     if (N % 32 != 0 || N < 32 || ((uintptr_t)w & 15) || ((uintptr_t)qx & 15)) return 0;
-    if ((N == 2048 || N == 4096) && ((uintptr_t)sa & 15) == 0) {
+    if ((N == 2048 || N == 4096) && ((uintptr_t)sa & 15) == 0 && !getenv("IBH_TMP_NOWK")) {
         constexpr int R = 4;
         const int blocks = (M + 4 * R - 1) / (4 * R);
         const uint8_t* W = (const uint8_t*)w;

@@ -11,7 +11,7 @@ import numpy as np
 from ._lib import check, lib
 
 DIM_NAMES = ("num_layers", "hidden_size", "num_heads", "num_kv_heads", "head_dim", "intermediate_size",
-             "vocab_size", "max_context_length", "kv_bits", "capacity", "eos_token_id", "positions")
+             "vocab_size", "max_context_length", "kv_bits", "capacity", "eos_token_id", "positions", "exact")
 
 
 def _ptr(a: np.ndarray):
@@ -24,7 +24,7 @@ class Model:
         h = ctypes.c_void_p()
         check(lib().ibh_model_load(path.encode(), context_length, ctypes.byref(h)), "ibh_model_load")
         self._h = h
-        d = np.zeros(12, np.int32)
+        d = np.zeros(13, np.int32)
         check(lib().ibh_model_dims(self._h, _ptr(d)), "ibh_model_dims")
         self.dims = dict(zip(DIM_NAMES, (int(v) for v in d)))
 
@@ -61,6 +61,11 @@ class Model:
         v = np.ascontiguousarray(v, np.float32)
         assert k.shape == v.shape and k.ndim == 3
         check(lib().ibh_model_kv_prefill(self._h, _ptr(k), _ptr(v), k.shape[1]), "ibh_model_kv_prefill")
+
+    def set_exact(self, exact: bool) -> None:
+        """Bit-identical-to-CPU kernels (default) or the fast tolerance-bound ones."""
+        check(lib().ibh_model_set_exact(self._h, int(exact)), "ibh_model_set_exact")
+        self.dims["exact"] = int(exact)
 
     def kv_length(self) -> int:
         return lib().ibh_model_kv_length(self._h)

@@ -672,3 +672,7 @@ int or_pq_matmul(const or_pq_tensor* t, const float* x, float* out) {
     free(ic); free(active); free(T1); free(T2);
     return 0;
 }
+
+void or_expf_batch(const float* x, float* y, size_t n) {
+    for (size_t i = 0; i < n; i++) y[i] = expf(x[i]);
+}

@@ -81,6 +81,10 @@ typedef struct {
 int or_pq_matmul(const or_pq_tensor* t, const float* x, float* out);      /* pq_decode.c:1504-1686 */
 int or_pq_reconstruct(const or_pq_tensor* t, float* out);                /* pq_decode.c:1103-1196 */
 
+/* glibc expf applied elementwise: the libm the reference links
+ * (kernels/avx2.c:213-216, :241-244), called as is. */
+void or_expf_batch(const float* x, float* y, size_t n);
+
 #ifdef __cplusplus
 }
 #endif

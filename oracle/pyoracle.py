@@ -57,6 +57,7 @@ def _declare(L):
         "or_silu_mul": (None, [P, P, P, I]),
         "or_pq_matmul": (I, [P, P, P]),
         "or_pq_reconstruct": (I, [P, P]),
+        "or_expf_batch": (None, [P, P, C.c_size_t]),
     }
     for name, (res, args) in sigs.items():
         f = getattr(L, name)
@@ -239,3 +240,11 @@ def pq_reconstruct(t: dict):
     out = np.zeros((t["M"], t["N"]), np.float32)
     lib().or_pq_reconstruct(C.byref(s), _p(out))
     return out
+
+
+def expf(x):
+    """glibc expf elementwise (the reference's libm)."""
+    x = _c(x, np.float32)
+    y = np.empty_like(x)
+    lib().or_expf_batch(_p(x), _p(y), C.c_size_t(x.size))
+    return y

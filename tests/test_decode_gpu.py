@@ -2,9 +2,9 @@
 reference library's CPU decode.
 
 * Small synthetic models: the reference's own `ref_decode` (oracle/_ref,
-  built from the reference sources) runs live on the same file; logits of the
-  prompt must agree to max|d| / max|logit| <= 1e-4 and the greedy token
-  streams must be identical.
+  built from the reference sources) runs live on the same file.  Exact mode
+  (the default) must give bit-identical logits and identical greedy token
+  streams; fast mode must give logits within max|d| / max|logit| <= 1e-4.
 * Benchmark configurations (TinyLlama-1.1B and Mistral-7B shapes): the
   models are regenerated from their seeds (SHA-256 checked against the
   fixture) and the GPU token streams must equal the reference's streams
@@ -73,6 +73,10 @@ TINY = {
 }
 
 
+def same_bits(a, b):
+    np.testing.assert_array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
+
+
 @pytest.mark.parametrize("name", list(TINY))
 def test_tiny_model_matches_reference(L, tmp_path, name):
     from libinferbit_amd import ibf
@@ -85,11 +89,32 @@ def test_tiny_model_matches_reference(L, tmp_path, name):
     prompt = [5, 17, 300, 42, 999, 0, 7]
     ref_tokens, ref_logits = ref_run(path, prompt, 40, tmp_path)
     m = Model(path)
-    logits = m.forward(prompt)
-    assert relerr(logits, ref_logits) <= 1e-4
+    assert m.dims["exact"] == 1
+    same_bits(m.forward(prompt), ref_logits)
     m.kv_clear()
-    got = m.generate(prompt, 40)
-    assert got.tolist() == ref_tokens
+    assert m.generate(prompt, 40).tolist() == ref_tokens
+    m.kv_clear()
+    m.set_exact(False)
+    assert relerr(m.forward(prompt), ref_logits) <= 1e-4
+    m.close()
+
+
+@pytest.mark.parametrize("hidden,heads,kv", [(2048, 32, 4), (1024, 16, 16), (512, 8, 1)])
+def test_wider_models_bit_exact(L, tmp_path, hidden, heads, kv):
+    """Hidden sizes and GQA groups of the benchmark shapes (hidden 2048 with a
+    group of 8 is TinyLlama's), 3 layers, W4A8 MLP: logits bit-identical."""
+    from libinferbit_amd import ibf
+    from libinferbit_amd.model import Model
+    print(f"case decode wide hidden={hidden} heads={heads}/{kv}", flush=True)
+    path = str(tmp_path / "m.ibf")
+    ibf.write_synthetic(path, tiny_cfg(num_layers=3, hidden_size=hidden, num_heads=heads, num_kv_heads=kv,
+                                       intermediate_size=2816, kv_bits=8), seed=21)
+    prompt = list(range(3, 60, 3))
+    ref_tokens, ref_logits = ref_run(path, prompt, 20, tmp_path)
+    m = Model(path)
+    same_bits(m.forward(prompt), ref_logits)
+    m.kv_clear()
+    assert m.generate(prompt, 20).tolist() == ref_tokens
     m.close()
 
 
@@ -109,8 +134,7 @@ def test_tiny_kv_prefill_matches_reference(L, tmp_path):
         m = Model(path)
         m.kv_prefill(k, v)
         assert m.kv_length() == 100
-        logits = m.forward([77])
-        assert relerr(logits, ref_logits) <= 1e-4
+        same_bits(m.forward([77]), ref_logits)
         m.kv_truncate(100)
         assert m.generate([77], 30).tolist() == ref_tokens
         m.close()
@@ -125,7 +149,7 @@ def test_w4a8_disabled_matches_reference(L, tmp_path, monkeypatch):
     ref_tokens, ref_logits = ref_run(path, [1, 2, 3], 30, tmp_path, env={"IB_W4A8": "0"})
     monkeypatch.setenv("IB_W4A8", "0")
     m = Model(path)
-    assert relerr(m.forward([1, 2, 3]), ref_logits) <= 1e-4
+    same_bits(m.forward([1, 2, 3]), ref_logits)
     m.kv_clear()
     assert m.generate([1, 2, 3], 30).tolist() == ref_tokens
     m.close()
@@ -133,21 +157,25 @@ def test_w4a8_disabled_matches_reference(L, tmp_path, monkeypatch):
 
 def test_graph_replay_equals_eager(L, tmp_path, monkeypatch):
     """The captured per-token graph gives bit-identical logits to eager launches,
-    replay after replay."""
+    replay after replay, in both modes."""
     from libinferbit_amd import ibf
     from libinferbit_amd.model import Model
     path = str(tmp_path / "m.ibf")
     ibf.write_synthetic(path, tiny_cfg(kv_bits=8), seed=4)
     prompt = list(range(10, 30))
-    g = Model(path)
-    a = [g.forward([t]) for t in prompt]
-    monkeypatch.setenv("IBH_DECODE_EAGER", "1")
-    e = Model(path)
-    b = [e.forward([t]) for t in prompt]
-    for x, y in zip(a, b):
-        np.testing.assert_array_equal(x, y)
-    g.close()
-    e.close()
+    for exact in (True, False):
+        monkeypatch.delenv("IBH_DECODE_EAGER", raising=False)
+        g = Model(path)
+        g.set_exact(exact)
+        a = [g.forward([t]) for t in prompt]
+        monkeypatch.setenv("IBH_DECODE_EAGER", "1")
+        e = Model(path)
+        e.set_exact(exact)
+        b = [e.forward([t]) for t in prompt]
+        for x, y in zip(a, b):
+            np.testing.assert_array_equal(x, y)
+        g.close()
+        e.close()
 
 
 def test_model_api_errors(L, tmp_path):

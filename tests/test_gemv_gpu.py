@@ -57,7 +57,8 @@ def test_matvec_golden(ops, tag, bits, scale_f32):
 
 
 @pytest.mark.parametrize("bits", [8, 4, 2])
-@pytest.mark.parametrize("M,N", [(1, 64), (3, 4096), (14336, 4096), (4096, 14336), (2048, 2048), (5, 4160)])
+@pytest.mark.parametrize("M,N", [(1, 64), (3, 4096), (14336, 4096), (4096, 14336), (2048, 2048), (5, 4160),
+                                 (256, 2048), (5632, 2048), (2048, 5632), (1024, 4096), (32000, 2048), (77, 3072)])
 def test_matvec_random_vs_oracle(ops, oracle_lib, bits, M, N):
     print(f"case matvec-rand bits={bits} M={M} N={N}", flush=True)
     rng = np.random.default_rng(M * 7 + N + bits)
@@ -114,7 +115,8 @@ def test_w4a8_golden_bit_exact(ops, tag):
     np.testing.assert_array_equal(out.cpu().numpy().view(np.uint32), g[f"y_avx2_{tag}"].view(np.uint32))
 
 
-@pytest.mark.parametrize("M,N", [(14336, 4096), (4096, 14336), (333, 4096), (64, 160), (7, 128)])
+@pytest.mark.parametrize("M,N", [(14336, 4096), (4096, 14336), (333, 4096), (64, 160), (7, 128), (5632, 2048),
+                                 (2048, 5632), (2048, 2048), (100, 2816), (64, 6144), (13, 2048)])
 def test_w4a8_x_random_bit_exact(ops, oracle_lib, M, N):
     print(f"case w4a8 M={M} N={N}", flush=True)
     rng = np.random.default_rng(M + N)
