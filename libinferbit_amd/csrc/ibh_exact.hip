@@ -32,27 +32,62 @@ namespace {
 constexpr int kExactNormMax = 12288;     // floats of x staged in LDS
 
 // Residual add + rmsnorm_fp16 in the x86 order.  One block; out may alias x.
-__global__ __launch_bounds__(256) void rmsnorm_exact(float* __restrict__ out, float* x, const float* __restrict__ delta,
+// x is staged chain-major (xt[l][k] = x[8k + l]) so each chain thread reads
+// its elements as float4s.
+__global__ __launch_bounds__(256) void rmsnorm_exact(float* out, float* x, const float* __restrict__ delta,
                                                      const uint16_t* __restrict__ w, float eps, int n) {
-    __shared__ float xs[kExactNormMax];
+    __shared__ __align__(16) float xt[kExactNormMax];
     __shared__ float part[8];
     __shared__ float scale_s;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        float v = x[i];
-        if (delta) {
-            v = v + delta[i];
-            x[i] = v;
+    const int n8 = n >> 3;                                // elements per chain (n % 8 == 0)
+    // all loads first (unconditional, clamped), then the stores
+    constexpr int NQ = kExactNormMax / 4 / 256;
+    const int n4 = n >> 2;
+    float4 xv[NQ], dv[NQ];
+#pragma unroll
+    for (int u = 0; u < NQ; u++) {
+        const int i4 = min((int)threadIdx.x + 256 * u, n4 - 1);
+        xv[u] = ((const float4*)x)[i4];
+        dv[u] = delta ? ((const float4*)delta)[i4] : float4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int u = 0; u < NQ; u++) {
+        const int i4 = (int)threadIdx.x + 256 * u;
+        if (i4 < n4) {
+            float4 v = xv[u];
+            if (delta) {
+                v.x = v.x + dv[u].x; v.y = v.y + dv[u].y; v.z = v.z + dv[u].z; v.w = v.w + dv[u].w;
+                ((float4*)x)[i4] = v;
+            }
+            const int i = 4 * i4;
+            xt[((i + 0) & 7) * n8 + ((i + 0) >> 3)] = v.x;
+            xt[((i + 1) & 7) * n8 + ((i + 1) >> 3)] = v.y;
+            xt[((i + 2) & 7) * n8 + ((i + 2) >> 3)] = v.z;
+            xt[((i + 3) & 7) * n8 + ((i + 3) >> 3)] = v.w;
         }
-        xs[i] = v;
     }
     __syncthreads();
-    const int n8 = n & ~7;
     if (threadIdx.x < 8) {
+        const float* c = xt + threadIdx.x * n8;
         float acc = 0.f;
-        const int l = threadIdx.x;
-#pragma unroll 8
-        for (int i = l; i < n8; i += 8) acc = fmaf(xs[i], xs[i], acc);
-        part[l] = acc;
+        int k = 0;
+        if ((n8 & 3) == 0) {
+            for (; k < n8; k += 32) {                       // 32 reads ahead of their fused adds
+                float4 v[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) v[u] = *(const float4*)(c + min(k + 4 * u, n8 - 4));
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    if (k + 4 * u < n8) {
+                        acc = fmaf(v[u].x, v[u].x, acc); acc = fmaf(v[u].y, v[u].y, acc);
+                        acc = fmaf(v[u].z, v[u].z, acc); acc = fmaf(v[u].w, v[u].w, acc);
+                    }
+                }
+            }
+        } else {
+            for (; k < n8; k++) acc = fmaf(c[k], c[k], acc);
+        }
+        part[threadIdx.x] = acc;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -62,7 +97,20 @@ __global__ __launch_bounds__(256) void rmsnorm_exact(float* __restrict__ out, fl
     }
     __syncthreads();
     const float scale = scale_s;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = (xs[i] * scale) * f16_to_f32(w[i]);
+#pragma unroll
+    for (int u = 0; u < NQ; u++) {
+        const int i4 = (int)threadIdx.x + 256 * u;
+        if (i4 < n4) {
+            const int i = 4 * i4;
+            const uint2 wq = ((const uint2*)w)[i4];
+            float4 o;
+            o.x = (xt[((i + 0) & 7) * n8 + ((i + 0) >> 3)] * scale) * f16_to_f32((uint16_t)(wq.x & 0xffff));
+            o.y = (xt[((i + 1) & 7) * n8 + ((i + 1) >> 3)] * scale) * f16_to_f32((uint16_t)(wq.x >> 16));
+            o.z = (xt[((i + 2) & 7) * n8 + ((i + 2) >> 3)] * scale) * f16_to_f32((uint16_t)(wq.y & 0xffff));
+            o.w = (xt[((i + 3) & 7) * n8 + ((i + 3) >> 3)] * scale) * f16_to_f32((uint16_t)(wq.y >> 16));
+            ((float4*)out)[i4] = o;
+        }
+    }
 }
 
 // INT8 / INT4 matvec with fp32 x in the x86 order.  Block = 4 wavefronts x
@@ -77,7 +125,18 @@ __global__ __launch_bounds__(256) void matvec_exact(float* __restrict__ y, const
     extern __shared__ __align__(16) unsigned char smem[];
     float* xs = (float*)smem;                                         // [N]
     int8_t* tile = (int8_t*)(smem + (((size_t)N * 4 + 15) & ~(size_t)15));   // [4 waves][4 rows][256]
-    for (int i = threadIdx.x; i < N; i += 256) xs[i] = x[i];
+    {
+        constexpr int NQ = 16;                                        // N <= 16384
+        const int n4 = N >> 2;
+        float4 v[NQ];
+#pragma unroll
+        for (int u = 0; u < NQ; u++) v[u] = n4 > 0 ? ((const float4*)x)[max(min((int)threadIdx.x + 256 * u, n4 - 1), 0)]
+                                                   : float4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < NQ; u++)
+            if ((int)threadIdx.x + 256 * u < n4) ((float4*)xs)[threadIdx.x + 256 * u] = v[u];
+        for (int i = 4 * n4 + (int)threadIdx.x; i < N; i += 256) xs[i] = x[i];
+    }
     __syncthreads();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane >> 4, c = lane & 15;
@@ -87,52 +146,74 @@ __global__ __launch_bounds__(256) void matvec_exact(float* __restrict__ y, const
     const uint8_t* wr = W + (size_t)rowc * rb;
     int8_t* mytile = tile + (size_t)(wave * 4 + r) * 256;
     const int nb = N / 16;                                            // whole 16-column blocks
+    const int nt = (nb + 15) / 16;                                    // tiles of 16 blocks
     float acc = 0.f;
-    for (int b0 = 0; b0 < nb; b0 += 16) {
-        const int b = b0 + c;
-        int8_t v[16];
-        if (b < nb) {
-            if constexpr (BITS == 8) {
-                if constexpr (ALIGNED) {
-                    const uint4 q = *(const uint4*)(wr + (size_t)b * 16);
-                    __builtin_memcpy(v, &q, 16);
+    for (int g0 = 0; g0 < nt; g0 += 16) {
+        // all of this group's weight loads first (one 16-column block per tile)
+        uint4 buf[16];
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            const int b = min(16 * (g0 + k) + c, nb - 1);             // clamped: unused blocks are never read
+            buf[k] = make_uint4(0, 0, 0, 0);
+            {
+                if constexpr (BITS == 8) {
+                    if constexpr (ALIGNED) buf[k] = *(const uint4*)(wr + (size_t)b * 16);
+                    else {
+                        uint8_t t[16];
+#pragma unroll
+                        for (int e = 0; e < 16; e++) t[e] = wr[(size_t)b * 16 + e];
+                        __builtin_memcpy(&buf[k], t, 16);
+                    }
                 } else {
+                    if constexpr (ALIGNED) {
+                        const uint2 q = *(const uint2*)(wr + (size_t)b * 8);
+                        buf[k].x = q.x; buf[k].y = q.y;
+                    } else {
+                        uint8_t t[8];
 #pragma unroll
-                    for (int k = 0; k < 16; k++) v[k] = (int8_t)wr[(size_t)b * 16 + k];
-                }
-            } else {
-                uint32_t d[2];
-                if constexpr (ALIGNED) {
-                    const uint2 q = *(const uint2*)(wr + (size_t)b * 8);
-                    d[0] = q.x; d[1] = q.y;
-                } else {
-#pragma unroll
-                    for (int k = 0; k < 2; k++)
-                        d[k] = (uint32_t)wr[(size_t)b * 8 + 4 * k] | ((uint32_t)wr[(size_t)b * 8 + 4 * k + 1] << 8) |
-                               ((uint32_t)wr[(size_t)b * 8 + 4 * k + 2] << 16) | ((uint32_t)wr[(size_t)b * 8 + 4 * k + 3] << 24);
-                }
-#pragma unroll
-                for (int k = 0; k < 8; k++) {
-                    const uint32_t byte = (d[k >> 2] >> (8 * (k & 3))) & 0xffu;
-                    v[2 * k] = (int8_t)((int)(byte & 0xf) - 8);
-                    v[2 * k + 1] = (int8_t)((int)(byte >> 4) - 8);
+                        for (int e = 0; e < 8; e++) t[e] = wr[(size_t)b * 8 + e];
+                        __builtin_memcpy(&buf[k], t, 8);
+                    }
                 }
             }
-        } else {
-#pragma unroll
-            for (int k = 0; k < 16; k++) v[k] = 0;
         }
-        uint4 pk;
-        __builtin_memcpy(&pk, v, 16);
-        *(uint4*)(mytile + 16 * c) = pk;
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        const int nj = min(16, nb - b0);
-        for (int j = 0; j < nj; j++) acc = fmaf((float)mytile[16 * j + c], xs[16 * (b0 + j) + c], acc);
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            const int tile = g0 + k;
+            if (tile >= nt) break;
+            int8_t v[16];
+            if constexpr (BITS == 8) {
+                __builtin_memcpy(v, &buf[k], 16);
+            } else {
+                const uint32_t d[2] = {buf[k].x, buf[k].y};
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const uint32_t byte = (d[e >> 2] >> (8 * (e & 3))) & 0xffu;
+                    v[2 * e] = (int8_t)((int)(byte & 0xf) - 8);
+                    v[2 * e + 1] = (int8_t)((int)(byte >> 4) - 8);
+                }
+            }
+            uint4 pk;
+            __builtin_memcpy(&pk, v, 16);
+            *(uint4*)(mytile + 16 * c) = pk;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const int b0 = 16 * tile;
+            const int nj = min(16, nb - b0);
+            float wv[16], xv[16];
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                wv[j] = (float)mytile[16 * j + c];
+                xv[j] = xs[16 * min(b0 + j, nb - 1) + c];
+            }
+#pragma unroll
+            for (int j = 0; j < 16; j++)
+                if (j < nj) acc = fmaf(wv[j], xv[j], acc);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
     }
     // acc0 + acc1 (lane c < 8 gets chain c + 8), then lo + hi, hadd, hadd
     const float s = acc + __shfl_down(acc, 8, 16);
@@ -219,6 +300,130 @@ __device__ __forceinline__ float kv_at(const uint8_t* base, const float* scales,
     }
 }
 
+// 16 consecutive dequantised elements d0..d0+15 of row t, KV head kh.
+template <int BITS>
+__device__ __forceinline__ void kv_row16(float* o, const uint8_t* base, const float* scales, int t, int kh, int d0,
+                                         int hd, int n_kv) {
+    const int kv_dim = n_kv * hd;
+    if constexpr (BITS >= 16) {
+        const float4* p = (const float4*)((const float*)base + (size_t)t * kv_dim + (size_t)kh * hd + d0);
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const float4 v = p[u];
+            o[4 * u] = v.x; o[4 * u + 1] = v.y; o[4 * u + 2] = v.z; o[4 * u + 3] = v.w;
+        }
+    } else if constexpr (BITS == 8) {
+        const uint4 q = *(const uint4*)(base + (size_t)t * kv_dim + (size_t)kh * hd + d0);
+        const float sc = scales[(size_t)t * n_kv + kh];
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int e = 0; e < 16; e++) o[e] = (float)(int8_t)(w[e >> 2] >> (8 * (e & 3))) * sc;
+    } else {
+        const uint8_t* r = base + (size_t)t * ((kv_dim + 1) / 2) + (size_t)kh * ((hd + 1) / 2) + d0 / 2;
+        const float sc = scales[(size_t)t * n_kv + kh];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const uint8_t b = r[e];
+            o[2 * e] = (float)((int)(b & 0xf) - 8) * sc;
+            o[2 * e + 1] = (float)((int)(b >> 4) - 8) * sc;
+        }
+    }
+}
+
+// Raw bytes of kv_row16's elements (loads only, for prefetching): fp32 4 x
+// 16 B, int8 16 B, int4 8 B; plus the row's scale.
+template <int BITS>
+struct KvRaw {
+    uint4 q[BITS >= 16 ? 4 : 1];
+    float sc;
+};
+
+template <int BITS>
+__device__ __forceinline__ void kv_raw16(KvRaw<BITS>& r, const uint8_t* base, const float* scales, int t, int kh,
+                                         int d0, int hd, int n_kv) {
+    const int kv_dim = n_kv * hd;
+    if constexpr (BITS >= 16) {
+        const uint4* p = (const uint4*)((const float*)base + (size_t)t * kv_dim + (size_t)kh * hd + d0);
+#pragma unroll
+        for (int u = 0; u < 4; u++) r.q[u] = p[u];
+        r.sc = 1.f;
+    } else if constexpr (BITS == 8) {
+        r.q[0] = *(const uint4*)(base + (size_t)t * kv_dim + (size_t)kh * hd + d0);
+        r.sc = scales[(size_t)t * n_kv + kh];
+    } else {
+        const uint2 v = *(const uint2*)(base + (size_t)t * ((kv_dim + 1) / 2) + (size_t)kh * ((hd + 1) / 2) + d0 / 2);
+        r.q[0] = make_uint4(v.x, v.y, 0, 0);
+        r.sc = scales[(size_t)t * n_kv + kh];
+    }
+}
+
+template <int BITS>
+__device__ __forceinline__ void kv_deq16(float* o, const KvRaw<BITS>& r) {
+    if constexpr (BITS >= 16) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            o[4 * u] = __builtin_bit_cast(float, r.q[u].x); o[4 * u + 1] = __builtin_bit_cast(float, r.q[u].y);
+            o[4 * u + 2] = __builtin_bit_cast(float, r.q[u].z); o[4 * u + 3] = __builtin_bit_cast(float, r.q[u].w);
+        }
+    } else if constexpr (BITS == 8) {
+        const uint32_t w[4] = {r.q[0].x, r.q[0].y, r.q[0].z, r.q[0].w};
+#pragma unroll
+        for (int e = 0; e < 16; e++) o[e] = (float)(int8_t)(w[e >> 2] >> (8 * (e & 3))) * r.sc;
+    } else {
+        const uint32_t w[2] = {r.q[0].x, r.q[0].y};
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const uint32_t b = (w[e >> 2] >> (8 * (e & 3))) & 0xffu;
+            o[2 * e] = (float)((int)(b & 0xf) - 8) * r.sc;
+            o[2 * e + 1] = (float)((int)(b >> 4) - 8) * r.sc;
+        }
+    }
+}
+
+// Four groups of 4 consecutive elements (rows t[u], columns d[u]..d[u]+3),
+// loads only: fp32 16 B, int8 4 B, int4 2 B per group, plus the rows' scales.
+template <int BITS>
+struct Kv4x4 {
+    uint32_t q[4][BITS >= 16 ? 4 : 1];
+    float sc[4];
+};
+
+template <int BITS>
+__device__ __forceinline__ void kv_raw4x4(Kv4x4<BITS>& r, const uint8_t* base, const float* scales, const int* t,
+                                          const int* d, int kh, int hd, int n_kv) {
+    const int kv_dim = n_kv * hd;
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        if constexpr (BITS >= 16) {
+            const uint4 v = *(const uint4*)((const float*)base + (size_t)t[u] * kv_dim + (size_t)kh * hd + d[u]);
+            r.q[u][0] = v.x; r.q[u][1] = v.y; r.q[u][2] = v.z; r.q[u][3] = v.w;
+            r.sc[u] = 1.f;
+        } else if constexpr (BITS == 8) {
+            r.q[u][0] = *(const uint32_t*)(base + (size_t)t[u] * kv_dim + (size_t)kh * hd + d[u]);
+            r.sc[u] = scales[(size_t)t[u] * n_kv + kh];
+        } else {
+            r.q[u][0] = *(const uint16_t*)(base + (size_t)t[u] * ((kv_dim + 1) / 2) + (size_t)kh * ((hd + 1) / 2) + d[u] / 2);
+            r.sc[u] = scales[(size_t)t[u] * n_kv + kh];
+        }
+    }
+}
+
+template <int BITS>
+__device__ __forceinline__ float4 kv_deq4(const Kv4x4<BITS>& r, int u) {
+    if constexpr (BITS >= 16) {
+        return float4{__builtin_bit_cast(float, r.q[u][0]), __builtin_bit_cast(float, r.q[u][1]),
+                      __builtin_bit_cast(float, r.q[u][2]), __builtin_bit_cast(float, r.q[u][3])};
+    } else if constexpr (BITS == 8) {
+        const uint32_t w = r.q[u][0];
+        return float4{(float)(int8_t)(w & 0xffu) * r.sc[u], (float)(int8_t)((w >> 8) & 0xffu) * r.sc[u],
+                      (float)(int8_t)((w >> 16) & 0xffu) * r.sc[u], (float)(int8_t)(w >> 24) * r.sc[u]};
+    } else {
+        const uint32_t w = r.q[u][0];
+        return float4{(float)((int)(w & 0xf) - 8) * r.sc[u], (float)((int)((w >> 4) & 0xf) - 8) * r.sc[u],
+                      (float)((int)((w >> 8) & 0xf) - 8) * r.sc[u], (float)((int)((w >> 12) & 0xf) - 8) * r.sc[u]};
+    }
+}
+
 // Scores of one head for positions t (one thread each), serial over d.
 template <int BITS>
 __global__ __launch_bounds__(64) void attn_scores_exact(float* __restrict__ att, const float* __restrict__ q,
@@ -235,58 +440,176 @@ __global__ __launch_bounds__(64) void attn_scores_exact(float* __restrict__ att,
     if (t >= T) return;
     const int kh = h / (n_heads / n_kv);
     float score = 0.f;
-    for (int d = 0; d < hd; d++) score = score + qs[d] * kv_at<BITS>(kd, ks, t, kh, d, hd, n_kv);
+    for (int c0 = 0; c0 < hd; c0 += 128) {                 // up to 8 chunks of 16 loaded at once
+        float kv[8][16];
+#pragma unroll
+        for (int u = 0; u < 8; u++) kv_row16<BITS>(kv[u], kd, ks, t, kh, min(c0 + 16 * u, hd - 16), hd, n_kv);
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            if (c0 + 16 * u >= hd) break;
+#pragma unroll
+            for (int e = 0; e < 16; e++) score = score + qs[c0 + 16 * u + e] * kv[u][e];
+        }
+    }
     att[(size_t)h * tstride + t] = score * scale;
 }
 
-// Softmax over the head's scores and the serial output sum (forward.c:480-502).
-// Block per head: max (any order is exact), expf, one thread sums in order,
-// then per chunk of 32 positions the products a_t * v_t[d] are formed by all
-// threads into LDS and the d-lanes add them in position order.
-template <int BITS>
-__global__ __launch_bounds__(256) void attn_softmax_out_exact(float* __restrict__ out, float* __restrict__ att,
+// Softmax over one head's scores and the serial output sum (forward.c:480-502,
+// kernels/avx2.c:192-229).  Block per head, 512 threads:
+//  max (any order is exact); e_t = expf(s_t - max) into LDS; thread 0 sums
+//  e_t in position order; a_t = e_t * (1/sum).  Output: threads [0, hd)
+//  (one per d) add p_t[d] = a_t * v_t[d] in position order; the other threads
+//  produce p for the next chunk of CH positions into a double-buffered LDS
+//  tile, with their V rows loaded kPrefetch chunks ahead.
+constexpr int kAttnThreads = 512;
+
+// Workgroup barrier that orders LDS only: the LDS stores issued before it are
+// complete (lgkmcnt 0) but outstanding global loads stay in flight, which
+// __syncthreads (a release fence: vmcnt 0) would drain at every step.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);                   // lgkmcnt(0), vmcnt/expcnt untouched
+    __builtin_amdgcn_s_barrier();
+}
+constexpr int kPrefetch = 8;
+
+template <int BITS, int HD>
+__global__ __launch_bounds__(512) void attn_softmax_out_exact(float* __restrict__ out, const float* __restrict__ att,
                                                               const uint8_t* __restrict__ vd,
                                                               const float* __restrict__ vs,
                                                               const int* __restrict__ dpos, int n_heads, int n_kv,
-                                                              int hd, int tstride) {
-    constexpr int CH = 32;
-    __shared__ float red[4];
+                                                              int tstride) {
+    extern __shared__ __align__(16) float sm[];
+    __shared__ float red[kAttnThreads / 64];
     __shared__ float inv_s;
-    __shared__ float prod[CH][257];
+    constexpr int hd = HD;
+    constexpr int CH = 4096 / HD;                        // positions per chunk
+    float* pbuf = sm;                                    // [2][CH][hd]
+    float* es = sm + 2 * 4096;                           // [T]
     const int h = blockIdx.x;
     const int T = *dpos + 1;
-    float* a = att + (size_t)h * tstride;
+    const float* a = att + (size_t)h * tstride;
     float mx = -INFINITY;
-    for (int t = threadIdx.x; t < T; t += 256) mx = fmaxf(mx, a[t]);
+    for (int t = threadIdx.x; t < T; t += kAttnThreads) mx = fmaxf(mx, a[t]);
     mx = wave_max(mx);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
     __syncthreads();
-    const float m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    for (int t = threadIdx.x; t < T; t += 256) a[t] = ib_expf(a[t] - m);
+    float m = red[0];
+    for (int w = 1; w < kAttnThreads / 64; w++) m = fmaxf(m, red[w]);
+    for (int t0 = 0; t0 < T; t0 += 4 * kAttnThreads) {
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = a[min(t0 + u * kAttnThreads + (int)threadIdx.x, T - 1)];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int t = t0 + u * kAttnThreads + threadIdx.x;
+            if (t < T) es[t] = ib_expf(v[u] - m);
+        }
+    }
     __syncthreads();
     if (threadIdx.x == 0) {
+        // serial sum in position order; 32 values are read ahead of their adds
+        // serial sum in position order, the next 32 values read while these are added
         float sum = 0.f;
-        for (int t = 0; t < T; t++) sum = sum + a[t];
+        int t = 0;
+        const int T32 = T & ~31;
+        float4 cur[8], nxt[8];
+        if (T32 > 0) {
+#pragma unroll
+            for (int u = 0; u < 8; u++) cur[u] = *(const float4*)(es + 4 * u);
+        }
+        for (; t < T32; t += 32) {
+            const int tn = min(t + 32, T32 - 32);
+#pragma unroll
+            for (int u = 0; u < 8; u++) nxt[u] = *(const float4*)(es + tn + 4 * u);
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                sum = sum + cur[u].x; sum = sum + cur[u].y; sum = sum + cur[u].z; sum = sum + cur[u].w;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) cur[u] = nxt[u];
+        }
+        for (; t < T; t++) sum = sum + es[t];
         inv_s = 1.0f / sum;
     }
     __syncthreads();
     const float inv = inv_s;
-    for (int t = threadIdx.x; t < T; t += 256) a[t] = a[t] * inv;
+    for (int t = threadIdx.x; t < T; t += kAttnThreads) es[t] = es[t] * inv;
     __syncthreads();
+
     const int kh = h / (n_heads / n_kv);
+    const int nch = (T + CH - 1) / CH;
+    constexpr int P = BITS >= 16 ? 4 : kPrefetch;         // chunks of V rows in flight per producer
+    const int nsteps = (nch + P - 1) / P * P;             // barrier steps, the same for every wave
     float o = 0.f;
-    for (int t0 = 0; t0 < T; t0 += CH) {
-        const int tn = min(CH, T - t0);
-        for (int i = threadIdx.x; i < tn * hd; i += 256) {
-            const int tt = i / hd, d = i - tt * hd;
-            prod[tt][d] = a[t0 + tt] * kv_at<BITS>(vd, vs, t0 + tt, kh, d, hd, n_kv);
+    if ((int)threadIdx.x < hd) {
+        // consumers: one lane per d, chunk k lives in buffer k & 1 during step k
+        lds_barrier();                                  // chunk 0 produced
+        for (int k = 0; k < nsteps; k++) {
+            if (k < nch) {
+                const float* src = pbuf + (k & 1) * 4096 + threadIdx.x;
+                float v[CH];
+#pragma unroll
+                for (int e = 0; e < CH; e++) v[e] = src[e * HD];   // immediate LDS offsets
+                if (T - k * CH >= CH) {
+#pragma unroll
+                    for (int e = 0; e < CH; e++) o = o + v[e];
+                } else {
+                    const int tn = T - k * CH;
+                    for (int e = 0; e < tn; e++) o = o + src[e * HD];
+                }
+            }
+            lds_barrier();
         }
-        __syncthreads();
-        if ((int)threadIdx.x < hd)
-            for (int tt = 0; tt < tn; tt++) o = o + prod[tt][threadIdx.x];
-        __syncthreads();
+        out[(size_t)h * hd + threadIdx.x] = o;
+        return;
     }
-    if ((int)threadIdx.x < hd) out[(size_t)h * hd + threadIdx.x] = o;
+    // producers (the first 256 other threads): element group u of thread pid
+    // is flat offset (u * 256 + pid) * 4 of the chunk tile, so each LDS store
+    // instruction covers 1 KiB contiguously.  Branch-free: rows past T are
+    // clamped and their products land in rows nobody reads.
+    const int pid = threadIdx.x - hd;
+    if (pid >= 256) {
+        for (int k = 0; k < nsteps + 1; k++) lds_barrier();
+        return;
+    }
+    int gtt[4], gd[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int flat = (u * 256 + pid) * 4;
+        gtt[u] = flat / HD;
+        gd[u] = flat % HD;
+    }
+    Kv4x4<BITS> pre[P];
+    auto fetch = [&](int k, Kv4x4<BITS>& r) {
+        int t[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) t[u] = min(k * CH + gtt[u], T - 1);
+        kv_raw4x4<BITS>(r, vd, vs, t, gd, kh, HD, n_kv);
+    };
+    auto produce = [&](int k, const Kv4x4<BITS>& r) {
+        float4* dst = (float4*)(pbuf + (k & 1) * 4096);
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const float at = es[min(k * CH + gtt[u], T - 1)];
+            const float4 v = kv_deq4<BITS>(r, u);
+            dst[u * 256 + pid] = float4{at * v.x, at * v.y, at * v.z, at * v.w};
+        }
+    };
+#pragma unroll
+    for (int k = 0; k < P; k++) fetch(k, pre[k]);
+    // ring invariant: entering step k, pre[(k + 1) % P] holds chunk k + 1
+    produce(0, pre[0]);
+    fetch(P, pre[0]);
+    lds_barrier();
+    for (int k0 = 0; k0 < nsteps; k0 += P) {
+#pragma unroll
+        for (int u = 0; u < P; u++) {
+            const int k = k0 + u;
+            produce(k + 1, pre[(u + 1) % P]);
+            fetch(k + 1 + P, pre[(u + 1) % P]);
+            lds_barrier();
+        }
+    }
 }
 
 }  // namespace
@@ -352,12 +675,14 @@ int ibh_launch_silu_mul_exact(float* out, const float* g, const float* u, const 
 size_t ibh_attn_exact_scratch(int n_heads, int max_pos) { return (size_t)n_heads * (max_pos + 1) * sizeof(float); }
 
 // Attention of the current position (read from dpos) over cache rows 0..pos;
-// `att` >= ibh_attn_exact_scratch(n_heads, max_pos) bytes.
+// `att` >= ibh_attn_exact_scratch(n_heads, max_pos) bytes.  head_dim 64, 128
+// or 256; up to 8192 positions.
 int ibh_launch_attn_exact(float* out, const float* q, const void* kdata, const void* vdata, const float* ks,
                           const float* vs, const int* dpos, int max_pos, int n_heads, int n_kv, int hd, int kv_bits,
                           float* att, hipStream_t st) {
-    if (hd > 256 || n_heads % n_kv || (kv_bits != 32 && kv_bits != 16 && kv_bits != 8 && kv_bits != 4)) {
-        ibh_set_error("exact attention: unsupported geometry");
+    if ((hd != 64 && hd != 128 && hd != 256) || n_heads % n_kv || max_pos + 1 > 8192 ||
+        (kv_bits != 32 && kv_bits != 16 && kv_bits != 8 && kv_bits != 4)) {
+        ibh_set_error("exact attention: unsupported geometry (head_dim %d, %d positions)", hd, max_pos + 1);
         return IBH_ERROR_PARAM;
     }
     const float scale = 1.0f / sqrtf((float)hd);
@@ -365,12 +690,15 @@ int ibh_launch_attn_exact(float* out, const float* q, const void* kdata, const v
     dim3 g1(n_heads, (max_pos + 1 + 63) / 64);
     const uint8_t* K = (const uint8_t*)kdata;
     const uint8_t* V = (const uint8_t*)vdata;
+    const size_t lds = (size_t)(2 * 4096 + ((max_pos + 1 + 3) & ~3)) * sizeof(float);
+#define IBH_AO(B_, H_) attn_softmax_out_exact<B_, H_><<<n_heads, kAttnThreads, lds, st>>>(out, att, V, vs, dpos, n_heads, n_kv, tstride)
 #define IBH_AE(B_) do { \
         attn_scores_exact<B_><<<g1, 64, 0, st>>>(att, q, K, ks, dpos, n_heads, n_kv, hd, scale, tstride); \
-        attn_softmax_out_exact<B_><<<n_heads, 256, 0, st>>>(out, att, V, vs, dpos, n_heads, n_kv, hd, tstride); \
+        if (hd == 64) IBH_AO(B_, 64); else if (hd == 128) IBH_AO(B_, 128); else IBH_AO(B_, 256); \
     } while (0)
     if (kv_bits >= 16) IBH_AE(32); else if (kv_bits == 8) IBH_AE(8); else IBH_AE(4);
 #undef IBH_AE
+#undef IBH_AO
     IBH_CHECK_LAUNCH("exact attention");
     return IBH_OK;
 }
