@@ -39,6 +39,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=200)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--quick", action="store_true", help="headline only (for profiling runs)")
+    p.add_argument("--no-decode", action="store_true", help="skip the end-to-end decode legs")
     return p.parse_args()
 
 
@@ -149,6 +150,109 @@ def pq_case(torch, L, steps, warmup):
             "GBps": round(nbytes / tm / 1e9, 1)}
 
 
+def prefill_gemm_case(torch, L, steps, warmup):
+    """INT8 prefill GEMM at BASELINE configs[4]: 512 tokens x 4096 -> 14336
+    (ibh_gemm_int8, matmul_int8_batch semantics), x N(0,1).  One step = one
+    call (digit planes + GEMM).  Algorithmic work 2*B*M*N = 60.13 GFLOP; the
+    int8 matrix cores execute 3x that (three digit planes)."""
+    M, N, B = 14336, 4096, 512
+    rng = np.random.default_rng(11)
+    w = rng.integers(-127, 128, (M, N), dtype=np.int8)
+    sc = (np.abs(rng.standard_normal(M)) * 1e-4 + 1e-4).astype(np.float16).view(np.int16)
+    wd = [torch.from_numpy(w).cuda() for _ in range(4)]
+    sd = torch.from_numpy(sc).cuda()
+    x = torch.randn(B, N, generator=torch.Generator().manual_seed(3)).cuda()
+    y = torch.empty(B * M, device="cuda")
+    ws = torch.empty(L.lib().ibh_gemm_int8_workspace_bytes(N, B), dtype=torch.uint8, device="cuda")
+
+    def launch(i):
+        L.ops.gemm_int8(y, wd[i % 4], sd, x, M, N, B, M, ws)
+    t = time_launches(torch, launch, steps, warmup)
+    flops = 2.0 * B * M * N
+    return {"M": M, "N": N, "B": B, "us": round(t * 1e6, 2), "TFLOPs_algorithmic": round(flops / t / 1e12, 1),
+            "TOPs_int8_executed": round(3 * flops / t / 1e12, 1),
+            "frac_int8_mfma_peak": round(3 * flops / t / 1e12 / 5000.0, 4)}
+
+
+def decode_bytes_per_token(cfg, bits, n_pos):
+    """Algorithmic HBM bytes of one decode step: every packed weight + scales
+    once, the cache rows read by attention, the embedding row, activations
+    ignored (< 0.1 %)."""
+    H, I, V, L = cfg["hidden_size"], cfg["intermediate_size"], cfg["vocab_size"], cfg["num_layers"]
+    KV = cfg["num_kv_heads"] * cfg["head_dim"]
+    per_layer = 0
+    for key, r, c in (("q_proj", H, H), ("k_proj", KV, H), ("v_proj", KV, H), ("o_proj", H, H),
+                      ("gate_proj", I, H), ("up_proj", I, H), ("down_proj", H, I)):
+        per_layer += r * c * bits[key] // 8 + 2 * r
+    kvb = cfg["kv_bits"]
+    row = 4 * KV if kvb >= 16 else (KV if kvb == 8 else (KV + 1) // 2)
+    per_layer += 2 * n_pos * (row + (4 * cfg["num_kv_heads"] if kvb < 16 else 0)) + 4 * H   # K+V rows, 2 norms
+    head = V * H * bits["head"] // 8 + 2 * V
+    return L * per_layer + head + H * bits["token_embedding"] // 8 + 2 * H
+
+
+def decode_case(name, steps, cpu):
+    """Greedy decode tokens/s of a benchmark configuration: the model is
+    regenerated from its seed, loaded (weights to HBM once), the prompt run,
+    then `steps` decode steps are timed (each one HIP-graph replay; the clock
+    covers host enqueue to device completion).  Measured in exact mode (the
+    kernels whose token stream equals the CPU reference's, the headline) and
+    in fast mode (fp32-tolerance kernels)."""
+    sys.path.insert(0, os.path.join(ROOT, "tests", "golden"))
+    import gen_decode_golden as G
+    from libinferbit_amd import ibf
+    from libinferbit_amd.model import Model
+    case = G.CASES[name]
+    workdir = os.environ.get("IBH_MODEL_DIR", "/tmp/ibh_models")
+    os.makedirs(workdir, exist_ok=True)
+    t = time.time()
+    path = G.ensure_model(name, workdir)
+    t_write = time.time() - t
+    out = {"config": case["cfg"]["name"], "model_write_s": round(t_write, 1)}
+    for mode in ("exact", "fast"):
+        m = Model(path)
+        m.set_exact(mode == "exact")
+        if case["kv_pos"]:
+            k, v = G.kv_of(case)
+            m.kv_prefill(k, v)
+            del k, v
+        m.generate(G.prompt_of(case), 8)                  # prompt + warmup steps (graph built here)
+        m.decode_steps(8)
+        m.synchronize()
+        n_pos = m.kv_length() + steps // 2                # mean cache length over the timed steps
+        t0 = time.perf_counter()
+        m.decode_steps(steps)
+        m.synchronize()
+        dt = time.perf_counter() - t0
+        m.close()
+        nbytes = decode_bytes_per_token(case["cfg"], ibf.DEFAULT_BITS, n_pos)
+        tok_s = steps / dt
+        out[mode] = {"tok_s": round(tok_s, 2), "ms_per_token": round(dt / steps * 1e3, 4), "steps": steps,
+                     "kv_positions": n_pos, "bytes_per_token": nbytes, "GBps": round(nbytes * tok_s / 1e9, 1),
+                     "frac_hbm": round(nbytes * tok_s / 1e9 / HBM_PEAK_GBS, 4)}
+    if cpu:
+        out["cpu_baseline"] = cpu_decode(path, case)
+    return out
+
+
+def cpu_decode(path, case, n_out=8):
+    """The reference CPU decode (oracle/_ref/ref_decode) on the same file, a
+    bounded sample of n_out tokens after a 1-token prompt (no KV prefill)."""
+    exe = os.path.join(ROOT, "oracle", "_ref", "ref_decode")
+    if not os.path.exists(exe):
+        return None
+    cores = max(1, min(len(os.sched_getaffinity(0)), 16))
+    pp = path + ".cpu_prompt.i32"
+    np.array([1], np.int32).tofile(pp)
+    r = subprocess.run([exe, path, str(cores), "0", str(n_out), pp], capture_output=True, text=True, timeout=600)
+    if r.returncode != 0:
+        return None
+    d = json.loads(r.stdout.strip().splitlines()[-1])
+    return {"value": round(d["steps"] / d["seconds"], 3), "unit": "tok/s", "cores": cores, "kind": "reference",
+            "sample": f"inferbit_generate greedy, 1-token prompt + {n_out} tokens ({d['steps']} forward steps), "
+                      f"empty KV cache, {d['seconds']:.2f} s"}
+
+
 def cpu_baseline():
     """The reference library compiled from its own sources (oracle/_ref),
     ib_parallel_matmul INT4 14336x4096 with the x86 AVX2 table, timed on
@@ -201,8 +305,15 @@ def main():
             extra[name] = gemv_case(torch, L, oracle, bits, M, N, a.steps, a.warmup, w4a8)
         extra["w4a8_batch_sweep_14336x4096"] = [batch_case(torch, L, oracle, B, max(200, a.steps // 4), 20)
                                                 for B in (1, 2, 4, 8)]
+        print("bench: prefill gemm", file=sys.stderr, flush=True)
+        extra["prefill_gemm_int8_512x4096x14336"] = prefill_gemm_case(torch, L, 64, 8)
         print("bench: pq_4096x14336", file=sys.stderr, flush=True)
         extra["pq_4096x14336_G16_K256"] = pq_case(torch, L, max(200, a.steps // 4), 20)
+    decode = {}
+    if not a.no_decode and not a.quick:
+        for name in ("tinyllama", "mistral"):
+            print(f"bench: decode {name}", file=sys.stderr, flush=True)
+            decode[name] = decode_case(name, 128, cpu=not a.no_cpu and name == "tinyllama")
     cpu = None if a.no_cpu else cpu_baseline()
     out = {
         "metric": "quantized GEMV HBM GB/s (% of peak) + decode tok/s, Mistral-7B-shape INT4, 1 GPU",
@@ -224,7 +335,8 @@ def main():
                      "kernel": "gemv_mfma_f32<4,...>", "bytes_per_launch": head["bytes"],
                      "us_per_launch": head["us"]},
         "cpu_baseline": cpu,
-        "decode_tok_s": None,
+        "decode_tok_s": decode.get("mistral", {}).get("exact", {}).get("tok_s"),
+        "decode": decode,
         "extra": extra,
     }
     print(json.dumps(out), flush=True)

@@ -103,6 +103,17 @@ int ibh_matmul_w4a8_batch(float* out, const void* w, const void* scales, int sca
 int ibh_matmul_int8_batch(float* out, const void* w, const void* scales, int scale_kind,
                           const float* x, int M, int N, int B, int M_stride, void* stream);
 
+/* Multi-token (prefill) INT8 GEMM on the int8 matrix cores:
+ * out[b*M_stride + i] = scales[i] * sum_j W[i][j] * x[b][j] for any B, the
+ * semantics of matmul_int8_batch (src/kernels/scalar.c:70-84) without its
+ * B <= 32 cap (tensor_matmul_batch, src/forward.c:200-246).  x [B][N] fp32
+ * becomes three int8 digit planes per token (|error| <= max|x_b| * 2^-22 per
+ * element), the GEMM is exact int32.  N % 64 == 0; 16-byte aligned w, x.
+ * `ws` >= ibh_gemm_int8_workspace_bytes(N, B) (NULL: library workspace). */
+size_t ibh_gemm_int8_workspace_bytes(int N, int B);
+int ibh_gemm_int8(float* out, const void* w, const void* scales, int scale_kind, const float* x, int M, int N,
+                  int B, int M_stride, void* ws, size_t ws_bytes, void* stream);
+
 /* ── KV cache and attention decode, device pointers ────────── */
 
 /* Quantises K and V of one position into the cache, bit-identical to

@@ -30,6 +30,8 @@ SIGNATURES = {
     "ibh_matmul_w4a8_x": (I, [P, P, P, I, P, I, I, P, P, P]),
     "ibh_matmul_w4a8_batch": (I, [P, P, P, I, P, P, I, I, I, I, P]),
     "ibh_matmul_int8_batch": (I, [P, P, P, I, P, I, I, I, I, P]),
+    "ibh_gemm_int8_workspace_bytes": (SZ, [I, I]),
+    "ibh_gemm_int8": (I, [P, P, P, I, P, I, I, I, I, P, SZ, P]),
     "ibh_kv_write": (I, [P, P, P, P, I, P, P, I, I, I, P]),
     "ibh_attn_workspace_bytes": (SZ, [I, I, I]),
     "ibh_attn_decode": (I, [P, P, P, P, P, P, I, I, I, I, I, P, SZ, P]),

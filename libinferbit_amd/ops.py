@@ -80,6 +80,14 @@ def matmul_int8_batch(out, w, scales_w, x, M: int, N: int, B: int, M_stride: int
                                       N, B, M_stride, _stream()), "ibh_matmul_int8_batch")
 
 
+def gemm_int8(out, w, scales, x, M: int, N: int, B: int, M_stride: int, ws=None) -> None:
+    """Prefill INT8 GEMM, matmul_int8_batch semantics at any B (src/kernels/scalar.c:70-84)."""
+    if ws is None:
+        ws = torch.empty(lib().ibh_gemm_int8_workspace_bytes(N, B), dtype=torch.uint8, device=out.device)
+    check(lib().ibh_gemm_int8(_ptr(out), _ptr(w), _ptr(scales), _scale_kind(scales), _ptr(x), M, N, B, M_stride,
+                              _ptr(ws), ws.numel(), _stream()), "ibh_gemm_int8")
+
+
 def _optptr(t):
     return None if t is None else _ptr(t)
 
