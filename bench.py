@@ -40,7 +40,38 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--quick", action="store_true", help="headline only (for profiling runs)")
     p.add_argument("--no-decode", action="store_true", help="skip the end-to-end decode legs")
+    p.add_argument("--only", choices=["headline", "gemm", "pq", "decode-tinyllama", "decode-mistral"],
+                   help="run one case and print its JSON (for profiler runs)")
+    p.add_argument("--calib-copy", action="store_true",
+                   help="first copy a 64 MiB buffer 8 times (the known-size kernel that scales the "
+                        "FETCH_SIZE / WRITE_SIZE counters in the traffic passes)")
     return p.parse_args()
+
+
+CALIB_BYTES = 64 << 20
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_int4_14336x4096_traffic.json")
+
+
+def calib_copy(torch):
+    """8 device-to-device copies of CALIB_BYTES (torch's elementwise copy
+    kernel): it reads and writes exactly CALIB_BYTES each, which is what the
+    traffic passes divide the counters by."""
+    a = torch.empty(CALIB_BYTES // 4, device="cuda")
+    a.fill_(1.0)
+    b = torch.empty_like(a)
+    for _ in range(8):
+        b.copy_(a)
+    torch.cuda.synchronize()
+
+
+def measured_traffic():
+    """HBM bytes per headline launch from the committed FETCH_SIZE/WRITE_SIZE
+    passes (profiles/), or None when they have not been recorded."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return json.load(f)["traffic_bytes_per_launch"]
+    except (OSError, ValueError, KeyError):
+        return None
 
 
 def matvec_bytes(M, N, bits, w4a8=False):
@@ -289,6 +320,19 @@ def main():
     from oracle import pyoracle as oracle
 
     L.ops.init(0)
+    if a.calib_copy:
+        calib_copy(torch)
+    if a.only:
+        if a.only == "headline":
+            r = gemv_case(torch, L, oracle, 4, 14336, 4096, a.steps, a.warmup)
+        elif a.only == "gemm":
+            r = prefill_gemm_case(torch, L, 64, 8)
+        elif a.only == "pq":
+            r = pq_case(torch, L, max(200, a.steps // 4), 20)
+        else:
+            r = decode_case(a.only.split("-", 1)[1], 128, cpu=False)
+        print(json.dumps({"only": a.only, "result": r}), flush=True)
+        return
     print("bench: headline INT4 GEMV 14336x4096", file=sys.stderr, flush=True)
     head = gemv_case(torch, L, oracle, 4, 14336, 4096, a.steps, a.warmup)
     extra = {}
@@ -331,8 +375,8 @@ def main():
         "config": {"workload": "INT4 matvec 14336x4096 batch 1 (matmul_int4), 16 rotating weight copies",
                    "M": 14336, "N": 4096, "batch": 1, "bits": 4},
         "roofline": {"bound": "hbm", "achieved": head["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": head["frac_hbm"], "traffic": None,
-                     "kernel": "gemv_mfma_f32<4,...>", "bytes_per_launch": head["bytes"],
+                     "frac": head["frac_hbm"], "traffic": measured_traffic(),
+                     "kernel": "gemv_rows_x<4,...>", "bytes_per_launch": head["bytes"],
                      "us_per_launch": head["us"]},
         "cpu_baseline": cpu,
         "decode_tok_s": decode.get("mistral", {}).get("exact", {}).get("tok_s"),
