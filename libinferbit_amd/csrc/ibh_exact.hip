@@ -455,13 +455,19 @@ __global__ __launch_bounds__(64) void attn_scores_exact(float* __restrict__ att,
 }
 
 // Softmax over one head's scores and the serial output sum (forward.c:480-502,
-// kernels/avx2.c:192-229).  Block per head, 512 threads:
+// kernels/avx2.c:192-229).  Block per (head, slice of 64 d), 256 threads:
 //  max (any order is exact); e_t = expf(s_t - max) into LDS; thread 0 sums
-//  e_t in position order; a_t = e_t * (1/sum).  Output: threads [0, hd)
-//  (one per d) add p_t[d] = a_t * v_t[d] in position order; the other threads
-//  produce p for the next chunk of CH positions into a double-buffered LDS
-//  tile, with their V rows loaded kPrefetch chunks ahead.
-constexpr int kAttnThreads = 512;
+//  e_t in position order; a_t = e_t * (1/sum).  Output: wave 0 (one lane per
+//  d of the slice) adds p_t[d] = a_t * v_t[d] in position order; waves 1-3
+//  produce p for the next chunk of kAoCH positions into a double-buffered LDS
+//  tile, with their V rows held kAoP chunks ahead in registers (the loads of
+//  the first chunks are issued before the serial sum).  Every barrier after
+//  those loads orders LDS only, so the prefetched loads stay in flight.
+constexpr int kAoThreads = 256;
+constexpr int kAoD = 64;                                  // d per block = consumer lanes
+constexpr int kAoCH = 48;                                 // positions per chunk: 48*64/4 = 4 float4 per producer
+constexpr int kAoP = 4;                                   // chunks of V rows in flight per producer
+constexpr int kAoTile = kAoCH * kAoD;                     // floats per LDS chunk tile
 
 // Workgroup barrier that orders LDS only: the LDS stores issued before it are
 // complete (lgkmcnt 0) but outstanding global loads stay in flight, which
@@ -470,45 +476,90 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_s_waitcnt(0xC07F);                   // lgkmcnt(0), vmcnt/expcnt untouched
     __builtin_amdgcn_s_barrier();
 }
-constexpr int kPrefetch = 8;
 
 template <int BITS, int HD>
-__global__ __launch_bounds__(512) void attn_softmax_out_exact(float* __restrict__ out, const float* __restrict__ att,
-                                                              const uint8_t* __restrict__ vd,
-                                                              const float* __restrict__ vs,
-                                                              const int* __restrict__ dpos, int n_heads, int n_kv,
-                                                              int tstride) {
+__global__ __launch_bounds__(kAoThreads) void attn_out_exact(float* __restrict__ out, const float* __restrict__ att,
+                                                            const uint8_t* __restrict__ vd,
+                                                            const float* __restrict__ vs,
+                                                            const int* __restrict__ dpos, int n_heads, int n_kv,
+                                                            int tstride, int tcap) {
     extern __shared__ __align__(16) float sm[];
-    __shared__ float red[kAttnThreads / 64];
+    __shared__ float red[kAoThreads / 64];
     __shared__ float inv_s;
-    constexpr int hd = HD;
-    constexpr int CH = 4096 / HD;                        // positions per chunk
-    float* pbuf = sm;                                    // [2][CH][hd]
-    float* es = sm + 2 * 4096;                           // [T]
-    const int h = blockIdx.x;
+    constexpr int NS = HD / kAoD;
+    float* es = sm;                                       // [tcap]
+    float* pbuf = sm + tcap;                              // [2][kAoCH][kAoD]
+    const int h = blockIdx.x / NS, d0 = (blockIdx.x % NS) * kAoD;
+    const int tid = threadIdx.x, wave = tid >> 6;
     const int T = *dpos + 1;
+    const int kh = h / (n_heads / n_kv);
     const float* a = att + (size_t)h * tstride;
-    float mx = -INFINITY;
-    for (int t = threadIdx.x; t < T; t += kAttnThreads) mx = fmaxf(mx, a[t]);
-    mx = wave_max(mx);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
-    __syncthreads();
-    float m = red[0];
-    for (int w = 1; w < kAttnThreads / 64; w++) m = fmaxf(m, red[w]);
-    for (int t0 = 0; t0 < T; t0 += 4 * kAttnThreads) {
-        float v[4];
+
+    // Scores to LDS: every load of the row is issued before any is used (the
+    // scores were just written by another kernel and arrive from a far
+    // cache); then max (any order is exact) and the exponentials in place.
+    // tstride and the row base are multiples of 4 floats.
+    {
+        const float4* a4 = (const float4*)a;
+        const int n4 = (T + 3) >> 2;
+        for (int f0 = 0; f0 < n4; f0 += 8 * kAoThreads) {
+            float4 v[8];
 #pragma unroll
-        for (int u = 0; u < 4; u++) v[u] = a[min(t0 + u * kAttnThreads + (int)threadIdx.x, T - 1)];
+            for (int u = 0; u < 8; u++) v[u] = a4[min(f0 + u * kAoThreads + tid, n4 - 1)];
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int t = t0 + u * kAttnThreads + threadIdx.x;
-            if (t < T) es[t] = ib_expf(v[u] - m);
+            for (int u = 0; u < 8; u++) {
+                const int f = f0 + u * kAoThreads + tid;
+                if (f < n4) ((float4*)es)[f] = v[u];
+            }
         }
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        // serial sum in position order; 32 values are read ahead of their adds
-        // serial sum in position order, the next 32 values read while these are added
+    float mx = -INFINITY;
+    for (int t = tid; t < T; t += kAoThreads) mx = fmaxf(mx, es[t]);
+    mx = wave_max(mx);
+    if ((tid & 63) == 0) red[wave] = mx;
+    __syncthreads();
+    float m = red[0];
+#pragma unroll
+    for (int w = 1; w < kAoThreads / 64; w++) m = fmaxf(m, red[w]);
+    for (int t = tid; t < T; t += kAoThreads) es[t] = ib_expf(es[t] - m);
+    __syncthreads();
+
+    // producer geometry: float4 f = u * 192 + pid of a chunk tile is row
+    // f / 16, columns 4 (f % 16) .. +3 of the slice
+    const int nch = (T + kAoCH - 1) / kAoCH;
+    const int nsteps = (nch + kAoP - 1) / kAoP * kAoP;    // barrier steps, the same for every wave
+    const int pid = tid - 64;
+    int gtt[4], gd[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int f = u * (kAoThreads - 64) + (pid < 0 ? 0 : pid);
+        gtt[u] = f >> 4;
+        gd[u] = d0 + 4 * (f & 15);
+    }
+    Kv4x4<BITS> ring[kAoP];
+    auto fetch = [&](int k, Kv4x4<BITS>& r) {
+        int t[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) t[u] = min(k * kAoCH + gtt[u], T - 1);
+        kv_raw4x4<BITS>(r, vd, vs, t, gd, kh, HD, n_kv);
+    };
+    auto produce = [&](int k, const Kv4x4<BITS>& r) {
+        float4* dst = (float4*)(pbuf + (k & 1) * kAoTile);
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const float at = es[min(k * kAoCH + gtt[u], T - 1)];
+            const float4 v = kv_deq4<BITS>(r, u);
+            dst[u * (kAoThreads - 64) + pid] = float4{at * v.x, at * v.y, at * v.z, at * v.w};
+        }
+    };
+    if (wave > 0) {
+#pragma unroll
+        for (int k = 0; k < kAoP; k++) fetch(k, ring[k]);
+    }
+
+    // serial sum in position order, the next 32 values read while these are added
+    if (tid == 0) {
         float sum = 0.f;
         int t = 0;
         const int T32 = T & ~31;
@@ -531,82 +582,46 @@ __global__ __launch_bounds__(512) void attn_softmax_out_exact(float* __restrict_
         for (; t < T; t++) sum = sum + es[t];
         inv_s = 1.0f / sum;
     }
-    __syncthreads();
+    lds_barrier();
     const float inv = inv_s;
-    for (int t = threadIdx.x; t < T; t += kAttnThreads) es[t] = es[t] * inv;
-    __syncthreads();
+    for (int t = tid; t < T; t += kAoThreads) es[t] = es[t] * inv;
+    lds_barrier();
 
-    const int kh = h / (n_heads / n_kv);
-    const int nch = (T + CH - 1) / CH;
-    constexpr int P = BITS >= 16 ? 4 : kPrefetch;         // chunks of V rows in flight per producer
-    const int nsteps = (nch + P - 1) / P * P;             // barrier steps, the same for every wave
-    float o = 0.f;
-    if ((int)threadIdx.x < hd) {
-        // consumers: one lane per d, chunk k lives in buffer k & 1 during step k
-        lds_barrier();                                  // chunk 0 produced
+    if (wave == 0) {
+        // consumer: lane d of the slice; chunk k lives in buffer k & 1 during step k
+        float o = 0.f;
+        lds_barrier();                                    // chunk 0 produced
         for (int k = 0; k < nsteps; k++) {
             if (k < nch) {
-                const float* src = pbuf + (k & 1) * 4096 + threadIdx.x;
-                float v[CH];
+                const float* src = pbuf + (k & 1) * kAoTile + tid;
+                if (T - k * kAoCH >= kAoCH) {
+                    float v[kAoCH];
 #pragma unroll
-                for (int e = 0; e < CH; e++) v[e] = src[e * HD];   // immediate LDS offsets
-                if (T - k * CH >= CH) {
+                    for (int e = 0; e < kAoCH; e++) v[e] = src[e * kAoD];   // immediate LDS offsets
 #pragma unroll
-                    for (int e = 0; e < CH; e++) o = o + v[e];
+                    for (int e = 0; e < kAoCH; e++) o = o + v[e];
                 } else {
-                    const int tn = T - k * CH;
-                    for (int e = 0; e < tn; e++) o = o + src[e * HD];
+                    const int tn = T - k * kAoCH;
+                    for (int e = 0; e < tn; e++) o = o + src[e * kAoD];
                 }
             }
             lds_barrier();
         }
-        out[(size_t)h * hd + threadIdx.x] = o;
+        out[(size_t)h * HD + d0 + tid] = o;
         return;
     }
-    // producers (the first 256 other threads): element group u of thread pid
-    // is flat offset (u * 256 + pid) * 4 of the chunk tile, so each LDS store
-    // instruction covers 1 KiB contiguously.  Branch-free: rows past T are
-    // clamped and their products land in rows nobody reads.
-    const int pid = threadIdx.x - hd;
-    if (pid >= 256) {
-        for (int k = 0; k < nsteps + 1; k++) lds_barrier();
-        return;
-    }
-    int gtt[4], gd[4];
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-        const int flat = (u * 256 + pid) * 4;
-        gtt[u] = flat / HD;
-        gd[u] = flat % HD;
-    }
-    Kv4x4<BITS> pre[P];
-    auto fetch = [&](int k, Kv4x4<BITS>& r) {
-        int t[4];
-#pragma unroll
-        for (int u = 0; u < 4; u++) t[u] = min(k * CH + gtt[u], T - 1);
-        kv_raw4x4<BITS>(r, vd, vs, t, gd, kh, HD, n_kv);
-    };
-    auto produce = [&](int k, const Kv4x4<BITS>& r) {
-        float4* dst = (float4*)(pbuf + (k & 1) * 4096);
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const float at = es[min(k * CH + gtt[u], T - 1)];
-            const float4 v = kv_deq4<BITS>(r, u);
-            dst[u * 256 + pid] = float4{at * v.x, at * v.y, at * v.z, at * v.w};
-        }
-    };
-#pragma unroll
-    for (int k = 0; k < P; k++) fetch(k, pre[k]);
-    // ring invariant: entering step k, pre[(k + 1) % P] holds chunk k + 1
-    produce(0, pre[0]);
-    fetch(P, pre[0]);
+    // producers: branch-free; rows past T are clamped and their products land
+    // in rows the consumer does not read.  Ring slot j holds the chunk whose
+    // index is j mod kAoP.
+    produce(0, ring[0]);
+    fetch(kAoP, ring[0]);
     lds_barrier();
-    for (int k0 = 0; k0 < nsteps; k0 += P) {
+    for (int k0 = 0; k0 < nsteps; k0 += kAoP) {
 #pragma unroll
-        for (int u = 0; u < P; u++) {
+        for (int u = 0; u < kAoP; u++) {
             const int k = k0 + u;
-            produce(k + 1, pre[(u + 1) % P]);
-            fetch(k + 1 + P, pre[(u + 1) % P]);
+            produce(k + 1, ring[(u + 1) % kAoP]);
+            fetch(k + 1 + kAoP, ring[(u + 1) % kAoP]);
             lds_barrier();
         }
     }
@@ -672,7 +687,7 @@ int ibh_launch_silu_mul_exact(float* out, const float* g, const float* u, const 
     return IBH_OK;
 }
 
-size_t ibh_attn_exact_scratch(int n_heads, int max_pos) { return (size_t)n_heads * (max_pos + 1) * sizeof(float); }
+size_t ibh_attn_exact_scratch(int n_heads, int max_pos) { return (size_t)n_heads * ((max_pos + 1 + 3) & ~3) * sizeof(float); }
 
 // Attention of the current position (read from dpos) over cache rows 0..pos;
 // `att` >= ibh_attn_exact_scratch(n_heads, max_pos) bytes.  head_dim 64, 128
@@ -686,12 +701,13 @@ int ibh_launch_attn_exact(float* out, const float* q, const void* kdata, const v
         return IBH_ERROR_PARAM;
     }
     const float scale = 1.0f / sqrtf((float)hd);
-    const int tstride = max_pos + 1;
+    const int tstride = (max_pos + 1 + 3) & ~3;             // score rows 16-byte aligned
     dim3 g1(n_heads, (max_pos + 1 + 63) / 64);
     const uint8_t* K = (const uint8_t*)kdata;
     const uint8_t* V = (const uint8_t*)vdata;
-    const size_t lds = (size_t)(2 * 4096 + ((max_pos + 1 + 3) & ~3)) * sizeof(float);
-#define IBH_AO(B_, H_) attn_softmax_out_exact<B_, H_><<<n_heads, kAttnThreads, lds, st>>>(out, att, V, vs, dpos, n_heads, n_kv, tstride)
+    const int tcap = (max_pos + 1 + 3) & ~3;
+    const size_t lds = (size_t)(tcap + 2 * kAoTile) * sizeof(float);
+#define IBH_AO(B_, H_) attn_out_exact<B_, H_><<<n_heads * (H_ / kAoD), kAoThreads, lds, st>>>(out, att, V, vs, dpos, n_heads, n_kv, tstride, tcap)
 #define IBH_AE(B_) do { \
         attn_scores_exact<B_><<<g1, 64, 0, st>>>(att, q, K, ks, dpos, n_heads, n_kv, hd, scale, tstride); \
         if (hd == 64) IBH_AO(B_, 64); else if (hd == 128) IBH_AO(B_, 128); else IBH_AO(B_, 256); \
