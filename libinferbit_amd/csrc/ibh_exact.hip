@@ -150,37 +150,37 @@ __global__ __launch_bounds__(256) void matvec_exact(float* __restrict__ y, const
     float acc = 0.f;
     for (int g0 = 0; g0 < nt; g0 += 16) {
         // all of this group's weight loads first (one 16-column block per tile)
-        uint4 buf[16];
+        // (a native vector array and no early exit from the unrolled loop
+        // below keep buf in registers: all 16 loads are in flight together)
+        u32x4_t buf[16];
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             const int b = min(16 * (g0 + k) + c, nb - 1);             // clamped: unused blocks are never read
-            buf[k] = make_uint4(0, 0, 0, 0);
-            {
-                if constexpr (BITS == 8) {
-                    if constexpr (ALIGNED) buf[k] = *(const uint4*)(wr + (size_t)b * 16);
-                    else {
-                        uint8_t t[16];
+            if constexpr (BITS == 8) {
+                if constexpr (ALIGNED) buf[k] = *(const u32x4_t*)(wr + (size_t)b * 16);
+                else {
+                    uint8_t t[16];
 #pragma unroll
-                        for (int e = 0; e < 16; e++) t[e] = wr[(size_t)b * 16 + e];
-                        __builtin_memcpy(&buf[k], t, 16);
-                    }
+                    for (int e = 0; e < 16; e++) t[e] = wr[(size_t)b * 16 + e];
+                    __builtin_memcpy(&buf[k], t, 16);
+                }
+            } else {
+                buf[k] = u32x4_t{0u, 0u, 0u, 0u};
+                if constexpr (ALIGNED) {
+                    const uint2 q = *(const uint2*)(wr + (size_t)b * 8);
+                    buf[k].x = q.x; buf[k].y = q.y;
                 } else {
-                    if constexpr (ALIGNED) {
-                        const uint2 q = *(const uint2*)(wr + (size_t)b * 8);
-                        buf[k].x = q.x; buf[k].y = q.y;
-                    } else {
-                        uint8_t t[8];
+                    uint8_t t[8];
 #pragma unroll
-                        for (int e = 0; e < 8; e++) t[e] = wr[(size_t)b * 8 + e];
-                        __builtin_memcpy(&buf[k], t, 8);
-                    }
+                    for (int e = 0; e < 8; e++) t[e] = wr[(size_t)b * 8 + e];
+                    __builtin_memcpy(&buf[k], t, 8);
                 }
             }
         }
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             const int tile = g0 + k;
-            if (tile >= nt) break;
+            if (tile < nt) {
             int8_t v[16];
             if constexpr (BITS == 8) {
                 __builtin_memcpy(v, &buf[k], 16);
@@ -213,6 +213,7 @@ __global__ __launch_bounds__(256) void matvec_exact(float* __restrict__ y, const
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            }
         }
     }
     // acc0 + acc1 (lane c < 8 gets chain c + 8), then lo + hi, hadd, hadd
