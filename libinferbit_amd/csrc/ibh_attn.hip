@@ -190,6 +190,200 @@ __global__ __launch_bounds__(256) void attn_partial(float* __restrict__ part, co
     }
 }
 
+// ── attention over a chunk, head_dim 64 / 128 / 256 ─────────────────────────
+// Block (kv head kh, chunk c of CT positions), 256 threads, for every query
+// head of the group at once:
+//   1. the chunk's V rows (packed) are loaded into registers first, so they
+//      stream while the scores are computed;
+//   2. scores: thread (position t, d-slice) dots its dequantised K slice with
+//      each query head (q in LDS), the slices are added, times 1/sqrtf(hd);
+//   3. per head: chunk max, p = expf(s - max), l = sum p (wave reductions);
+//   4. V -> LDS (packed) and threads (d, t-slice) accumulate p_t * v_t[d].
+// Output per (head, chunk): m, l and the unnormalised value sum.
+template <int BITS, int HD>
+struct ChunkGeo {
+    static constexpr int CT = BITS >= 16 ? (HD >= 256 ? 32 : (HD >= 128 ? 64 : 128)) : 128;   // positions
+    static constexpr int RB = BITS >= 16 ? 4 * HD : (BITS == 8 ? HD : HD / 2);                // row bytes per head
+    static constexpr int S = 256 / CT;                    // d-slices per position in the score phase
+    static constexpr int DS = HD / S;                     // dims per slice
+    static constexpr int SB = BITS >= 16 ? 4 * DS : (BITS == 8 ? DS : DS / 2);               // bytes per slice
+    static constexpr int NV = CT * RB / 16 / 256;         // 16-byte V pieces per thread
+    static constexpr int TS = 256 / HD;                   // t-slices in the P.V phase
+};
+
+template <int BITS>
+__device__ __forceinline__ float kv_code(const uint8_t* p, int d) {
+    if constexpr (BITS >= 16) return ((const float*)p)[d];
+    else if constexpr (BITS == 8) return (float)((const int8_t*)p)[d];
+    else {
+        const uint8_t b = p[d >> 1];
+        return (float)((int)((d & 1) ? (b >> 4) : (b & 0xf)) - 8);
+    }
+}
+
+template <int BITS, int GRP, int HD>
+__global__ __launch_bounds__(256) void attn_chunk(float* __restrict__ part, const float* __restrict__ q,
+                                                  const uint8_t* __restrict__ kd, const uint8_t* __restrict__ vd,
+                                                  const float* __restrict__ ks, const float* __restrict__ vs, int T,
+                                                  const int* __restrict__ dpos, int n_kv, float scale, int nstride) {
+    using G = ChunkGeo<BITS, HD>;
+    constexpr int CT = G::CT, RB = G::RB;
+    static_assert(G::NV >= 1 && CT * RB % (16 * 256) == 0, "V chunk split");
+    if (dpos) T = *dpos + 1;
+    const int kh = blockIdx.x, c = blockIdx.y, t0 = c * CT;
+    if (t0 >= T) return;
+    const int tn = min(CT, T - t0);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const size_t row_bytes = (size_t)n_kv * RB;
+    __shared__ float qs[GRP][HD];
+    __shared__ float sc[GRP][CT];
+    __shared__ float scr[G::S][GRP][CT];
+    __shared__ __align__(16) uint8_t vsh[CT * RB];
+    __shared__ float vsc[CT];
+    __shared__ float red[GRP][2];
+    __shared__ float oacc[G::TS][GRP][HD];
+
+    // 1. V chunk into registers (rows past T are clamped; never read)
+    u32x4_t vreg[G::NV];
+#pragma unroll
+    for (int u = 0; u < G::NV; u++) {
+        const int f = tid + 256 * u, t = f / (RB / 16), col = f % (RB / 16);
+        vreg[u] = *(const u32x4_t*)(vd + (size_t)(t0 + min(t, tn - 1)) * row_bytes + (size_t)kh * RB + 16 * col);
+    }
+    float vscale = 1.f;
+    if constexpr (BITS < 16) vscale = vs[(size_t)(t0 + min(tid, tn - 1)) * n_kv + kh];
+    for (int i = tid; i < GRP * HD; i += 256) qs[i / HD][i % HD] = q[(size_t)kh * GRP * HD + i];
+
+    // 2. scores
+    {
+        const int t = tid % CT, sl = tid / CT, tc = min(t, tn - 1);
+        const uint8_t* kr = kd + (size_t)(t0 + tc) * row_bytes + (size_t)kh * RB + sl * G::SB;
+        u32x4_t kreg[(G::SB + 15) / 16];
+#pragma unroll
+        for (int u = 0; u < (G::SB + 15) / 16; u++) {
+            if constexpr (G::SB >= 16) kreg[u] = *(const u32x4_t*)(kr + 16 * u);
+            else {
+                const uint2 h2 = *(const uint2*)kr;
+                kreg[u] = u32x4_t{h2.x, h2.y, 0u, 0u};
+            }
+        }
+        const float ksc = BITS >= 16 ? 1.f : ks[(size_t)(t0 + tc) * n_kv + kh];
+        __syncthreads();                                  // qs ready
+        float acc[GRP];
+#pragma unroll
+        for (int g = 0; g < GRP; g++) acc[g] = 0.f;
+        const uint8_t* kb = (const uint8_t*)kreg;
+#pragma unroll
+        for (int d = 0; d < G::DS; d++) {
+            const float kv = kv_code<BITS>(kb, d) * ksc;
+#pragma unroll
+            for (int g = 0; g < GRP; g++) acc[g] = fmaf(qs[g][sl * G::DS + d], kv, acc[g]);
+        }
+#pragma unroll
+        for (int g = 0; g < GRP; g++) scr[sl][g][t] = acc[g];
+    }
+    __syncthreads();
+    for (int i = tid; i < GRP * CT; i += 256) {
+        const int g = i / CT, t = i % CT;
+        float s_ = 0.f;
+#pragma unroll
+        for (int sl = 0; sl < G::S; sl++) s_ += scr[sl][g][t];
+        sc[g][t] = s_ * scale;
+    }
+    __syncthreads();
+
+    // 3. chunk softmax per head
+    for (int g = wave; g < GRP; g += 4) {
+        float m = -INFINITY;
+        for (int t = lane; t < tn; t += 64) m = fmaxf(m, sc[g][t]);
+        m = wave_max(m);
+        float l = 0.f;
+        for (int t = lane; t < CT; t += 64) {
+            const float pv = t < tn ? expf(sc[g][t] - m) : 0.f;
+            sc[g][t] = pv;
+            l += pv;
+        }
+        l = wave_sum(l);
+        if (lane == 0) { red[g][0] = m; red[g][1] = l; }
+    }
+    // 4. V -> LDS, then P.V
+#pragma unroll
+    for (int u = 0; u < G::NV; u++) ((u32x4_t*)vsh)[tid + 256 * u] = vreg[u];
+    if (tid < CT) vsc[tid] = vscale;
+    __syncthreads();
+    {
+        const int d = tid % HD, ts = tid / HD;
+        float acc[GRP];
+#pragma unroll
+        for (int g = 0; g < GRP; g++) acc[g] = 0.f;
+        for (int t = ts; t < tn; t += G::TS) {
+            const float v = kv_code<BITS>(vsh + t * RB, d) * vsc[t];
+#pragma unroll
+            for (int g = 0; g < GRP; g++) acc[g] = fmaf(sc[g][t], v, acc[g]);
+        }
+#pragma unroll
+        for (int g = 0; g < GRP; g++) oacc[ts][g][d] = acc[g];
+    }
+    __syncthreads();
+    for (int i = tid; i < GRP * HD; i += 256) {
+        const int g = i / HD, d = i % HD;
+        float o = 0.f;
+#pragma unroll
+        for (int ts = 0; ts < G::TS; ts++) o += oacc[ts][g][d];
+        float* pp = part + ((size_t)(kh * GRP + g) * nstride + c) * (HD + 2);
+        pp[2 + d] = o;
+        if (d == 0) { pp[0] = red[g][0]; pp[1] = red[g][1]; }
+    }
+}
+
+// Merge of the chunks of one head: out = sum_c w_c o_c / sum_c w_c l_c with
+// w_c = e^(m_c - M); the chunk terms are gathered in parallel.
+template <int HD>
+__global__ __launch_bounds__(256) void attn_merge(float* __restrict__ out, const float* __restrict__ part, int T,
+                                                  const int* __restrict__ dpos, int ct, int nstride) {
+    __shared__ float w[kMaxChunks / 4];
+    __shared__ float lw[kMaxChunks / 4];
+    __shared__ float red[4];
+    __shared__ float tot[2];
+    if (dpos) T = *dpos + 1;
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nch = (T + ct - 1) / ct;
+    const float* ph = part + (size_t)h * nstride * (HD + 2);
+    float m = -INFINITY;
+    for (int c = tid; c < nch; c += 256) {
+        w[c] = ph[(size_t)c * (HD + 2)];
+        lw[c] = ph[(size_t)c * (HD + 2) + 1];
+        m = fmaxf(m, w[c]);
+    }
+    m = wave_max(m);
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float l = 0.f;
+    for (int c = tid; c < nch; c += 256) {
+        const float e = expf(w[c] - M);
+        w[c] = e;
+        l = fmaf(e, lw[c], l);
+    }
+    l = wave_sum(l);
+    __syncthreads();
+    if (lane == 0) red[wave] = l;
+    __syncthreads();
+    const float inv = 1.0f / ((red[0] + red[1]) + (red[2] + red[3]));
+    for (int d = tid; d < HD; d += 256) {
+        float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
+        int c = 0;
+        for (; c + 4 <= nch; c += 4) {
+            const float a0 = ph[(size_t)c * (HD + 2) + 2 + d], a1 = ph[(size_t)(c + 1) * (HD + 2) + 2 + d];
+            const float a2 = ph[(size_t)(c + 2) * (HD + 2) + 2 + d], a3 = ph[(size_t)(c + 3) * (HD + 2) + 2 + d];
+            o0 = fmaf(w[c], a0, o0); o1 = fmaf(w[c + 1], a1, o1);
+            o2 = fmaf(w[c + 2], a2, o2); o3 = fmaf(w[c + 3], a3, o3);
+        }
+        for (; c < nch; c++) o0 = fmaf(w[c], ph[(size_t)c * (HD + 2) + 2 + d], o0);
+        out[(size_t)h * HD + d] = ((o0 + o1) + (o2 + o3)) * inv;
+    }
+}
+
 // ── merge chunks: out[h] = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c ──────
 __global__ __launch_bounds__(256) void attn_combine(float* __restrict__ out, const float* __restrict__ part,
                                                     int T, const int* __restrict__ dpos, int n_heads, int hd,
@@ -275,10 +469,36 @@ int ibh_launch_attn(float* out, const float* q, const void* kdata, const void* v
     }
     const float scale = 1.0f / sqrtf((float)head_dim);
     float* part = (float*)ws;
+    const int grp = n_heads / n_kv;
+    if (head_dim == 64 || head_dim == 128 || head_dim == 256) {
+        const uint8_t* K = (const uint8_t*)kdata;
+        const uint8_t* V = (const uint8_t*)vdata;
+        // chunk length depends on (bits, head_dim) only; the partials' stride
+        // is the chunk count of max_pos + 1 positions
+#define IBH_AC(B_, H_, G_) do { \
+            constexpr int CT = ChunkGeo<B_, H_>::CT; \
+            const int nstride = (max_pos + 1 + CT - 1) / CT; \
+            if (nstride > kMaxChunks / 4) goto generic;         /* merge keeps <= 1024 chunk terms */ \
+            attn_chunk<B_, G_, H_><<<dim3(n_kv, nstride), 256, 0, st>>>(part, q, K, V, kscales, vscales, T, dpos, n_kv, scale, nstride); \
+            IBH_CHECK_LAUNCH("ibh_attn_decode (chunk)"); \
+            attn_merge<H_><<<n_heads, 256, 0, st>>>(out, part, T, dpos, CT, nstride); \
+        } while (0)
+#define IBH_ACG(B_, H_) do { if (grp == 1) IBH_AC(B_, H_, 1); else if (grp == 2) IBH_AC(B_, H_, 2); \
+                             else if (grp == 4) IBH_AC(B_, H_, 4); else if (grp == 8) IBH_AC(B_, H_, 8); \
+                             else goto generic; } while (0)
+#define IBH_ACH(B_) do { if (head_dim == 64) IBH_ACG(B_, 64); else if (head_dim == 128) IBH_ACG(B_, 128); \
+                         else IBH_ACG(B_, 256); } while (0)
+        if (kv_bits >= 16) IBH_ACH(32); else if (kv_bits == 8) IBH_ACH(8); else IBH_ACH(4);
+#undef IBH_AC
+#undef IBH_ACG
+#undef IBH_ACH
+        IBH_CHECK_LAUNCH("ibh_attn_decode (merge)");
+        return IBH_OK;
+    }
+generic:
     dim3 grid(n_kv, nchunks);
     const uint8_t* K = (const uint8_t*)kdata;
     const uint8_t* V = (const uint8_t*)vdata;
-    const int grp = n_heads / n_kv;
 #define IBH_AP(B_, G_) attn_partial<B_, G_><<<grid, 256, 0, st>>>(part, q, K, V, kscales, vscales, T, dpos, n_heads, n_kv, head_dim, scale, nchunks)
 #define IBH_APG(B_) do { if (grp <= 1) IBH_AP(B_, 1); else if (grp <= 2) IBH_AP(B_, 2); else if (grp <= 4) IBH_AP(B_, 4); \
                          else IBH_AP(B_, 8); } while (0)
