@@ -77,6 +77,103 @@ __global__ __launch_bounds__(256) void kv_write_kernel(uint8_t* __restrict__ kd,
     }
 }
 
+// ── RoPE + KV write, one launch (forward.c:322-327, 352-413) ────────────────
+// One wavefront per query head (rotate in place), per key head (rotate, then
+// the cache rule above) and per value head (cache rule).  Lane holds the
+// pairs (2j, 2j+1), j = lane + 64 i.  EXACT rotates with the x86 build's
+// contraction, a' = fma(a, c, -(b s)), b' = fma(a, s, b c); otherwise the
+// plain a c - b s, a s + b c.  The rotated keys go to the cache only.
+template <bool EXACT>
+__global__ __launch_bounds__(256) void rope_kv_write_kernel(uint8_t* __restrict__ kd, uint8_t* __restrict__ vd,
+                                                            float* __restrict__ ks, float* __restrict__ vs,
+                                                            float* __restrict__ q, const float* __restrict__ k,
+                                                            const float* __restrict__ v,
+                                                            const float* __restrict__ table,
+                                                            const int* __restrict__ dpos, int n_heads, int n_kv,
+                                                            int hd, int bits) {
+    constexpr int kMaxPairs = kMaxHd / 2 / 64;
+    const int pos = *dpos;
+    const int lane = threadIdx.x & 63;
+    int id = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (id >= n_heads + 2 * n_kv) return;
+    const int half = hd / 2;
+    float a[kMaxPairs], b[kMaxPairs];
+    const float* src;
+    if (id < n_heads) src = q + (size_t)id * hd;
+    else if (id < n_heads + n_kv) src = k + (size_t)(id - n_heads) * hd;
+    else src = v + (size_t)(id - n_heads - n_kv) * hd;
+#pragma unroll
+    for (int i = 0; i < kMaxPairs; i++) {
+        const int j = lane + 64 * i;
+        a[i] = j < half ? src[2 * j] : 0.f;
+        b[i] = j < half ? src[2 * j + 1] : 0.f;
+    }
+    if (id < n_heads + n_kv) {                            // rotate q and k
+#pragma unroll
+        for (int i = 0; i < kMaxPairs; i++) {
+            const int j = lane + 64 * i;
+            if (j < half) {
+                const float* cs = table + ((size_t)pos * half + j) * 2;
+                const float c = cs[0], sn = cs[1], x0 = a[i], x1 = b[i];
+                if (EXACT) {
+                    a[i] = fmaf(x0, c, -(x1 * sn));
+                    b[i] = fmaf(x0, sn, x1 * c);
+                } else {
+                    a[i] = x0 * c - x1 * sn;
+                    b[i] = x0 * sn + x1 * c;
+                }
+            }
+        }
+    }
+    if (id < n_heads) {
+        float* dst = q + (size_t)id * hd;
+#pragma unroll
+        for (int i = 0; i < kMaxPairs; i++) {
+            const int j = lane + 64 * i;
+            if (j < half) { dst[2 * j] = a[i]; dst[2 * j + 1] = b[i]; }
+        }
+        return;
+    }
+    id -= n_heads;
+    const int side = id / n_kv, h = id - side * n_kv;
+    uint8_t* dst = side ? vd : kd;
+    float* scl = side ? vs : ks;
+    const int kv_dim = n_kv * hd;
+    if (bits >= 16) {
+        float* row = (float*)dst + (size_t)pos * kv_dim + (size_t)h * hd;
+#pragma unroll
+        for (int i = 0; i < kMaxPairs; i++) {
+            const int j = lane + 64 * i;
+            if (j < half) { row[2 * j] = a[i]; row[2 * j + 1] = b[i]; }
+        }
+        return;
+    }
+    float mx = 0.f;
+#pragma unroll
+    for (int i = 0; i < kMaxPairs; i++) mx = fmaxf(mx, fmaxf(fabsf(a[i]), fabsf(b[i])));
+    mx = wave_max(mx);
+    float sc = mx / (bits == 8 ? 127.0f : 7.0f);
+    if (sc < 1e-8f) sc = 1e-8f;
+    const float inv = 1.0f / sc;
+    if (lane == 0) scl[(size_t)pos * n_kv + h] = sc;
+#pragma unroll
+    for (int i = 0; i < kMaxPairs; i++) {
+        const int j = lane + 64 * i;
+        if (j >= half) continue;
+        int q0 = (int)roundf(a[i] * inv), q1 = (int)roundf(b[i] * inv);
+        if (bits == 8) {
+            int8_t* row = (int8_t*)dst + (size_t)pos * kv_dim + (size_t)h * hd;
+            row[2 * j] = (int8_t)(q0 < -127 ? -127 : (q0 > 127 ? 127 : q0));
+            row[2 * j + 1] = (int8_t)(q1 < -127 ? -127 : (q1 > 127 ? 127 : q1));
+        } else {
+            uint8_t* row = dst + (size_t)pos * ((kv_dim + 1) / 2) + (size_t)h * ((hd + 1) / 2);
+            q0 = q0 < -7 ? -7 : (q0 > 7 ? 7 : q0);
+            q1 = q1 < -7 ? -7 : (q1 > 7 ? 7 : q1);
+            row[j] = (uint8_t)(((q0 + 8) & 0xf) | (((q1 + 8) & 0xf) << 4));
+        }
+    }
+}
+
 // Dequantised element d of head h in cache row t (forward.c:415-445).
 template <int BITS>
 __device__ __forceinline__ float kv_elem(const uint8_t* row, int h, int d, int hd, float scale) {
@@ -508,6 +605,29 @@ generic:
     IBH_CHECK_LAUNCH("ibh_attn_decode (partial)");
     attn_combine<<<n_heads, 256, 0, st>>>(out, part, T, dpos, n_heads, head_dim, nchunks);
     IBH_CHECK_LAUNCH("ibh_attn_decode (combine)");
+    return IBH_OK;
+}
+
+// Rotary embedding of q and k at position *dpos plus the cache write of the
+// rotated k and of v, in one launch (head_dim even, <= 256).
+int ibh_launch_rope_kv_write(void* kdata, void* vdata, float* kscales, float* vscales, float* q, const float* k,
+                             const float* v, const float* table, const int* dpos, int n_heads, int n_kv,
+                             int head_dim, int kv_bits, bool exact, hipStream_t st) {
+    if (head_dim % 2 || head_dim > kMaxHd || !dpos ||
+        (kv_bits != 32 && kv_bits != 16 && kv_bits != 8 && kv_bits != 4)) {
+        ibh_set_error("rope + kv write: unsupported geometry (head_dim %d, bits %d)", head_dim, kv_bits);
+        return IBH_ERROR_PARAM;
+    }
+    const int waves = n_heads + 2 * n_kv;
+    if (exact)
+        rope_kv_write_kernel<true><<<(waves + 3) / 4, 256, 0, st>>>((uint8_t*)kdata, (uint8_t*)vdata, kscales, vscales,
+                                                                     q, k, v, table, dpos, n_heads, n_kv, head_dim,
+                                                                     kv_bits);
+    else
+        rope_kv_write_kernel<false><<<(waves + 3) / 4, 256, 0, st>>>((uint8_t*)kdata, (uint8_t*)vdata, kscales, vscales,
+                                                                      q, k, v, table, dpos, n_heads, n_kv, head_dim,
+                                                                      kv_bits);
+    IBH_CHECK_LAUNCH("rope + kv write");
     return IBH_OK;
 }
 

@@ -44,9 +44,12 @@ int ibh_launch_rmsnorm_exact(float* out, float* x, const float* delta, const uin
                              hipStream_t st);
 int ibh_launch_matvec_exact(float* y, const void* w, const void* sc, int kind, const float* x, int M, int N, int bits,
                             const uint8_t* mask, hipStream_t st);
-int ibh_launch_rope_exact(float* q, float* k, const float* table, const int* dpos, int n_heads, int n_kv, int hd,
-                          hipStream_t st);
 int ibh_launch_silu_mul_exact(float* out, const float* g, const float* u, const uint8_t* mask, int n, hipStream_t st);
+int ibh_launch_rope_kv_write(void* kdata, void* vdata, float* kscales, float* vscales, float* q, const float* k,
+                             const float* v, const float* table, const int* dpos, int n_heads, int n_kv,
+                             int head_dim, int kv_bits, bool exact, hipStream_t st);
+int ibh_launch_silu_quant(float* out, const float* gate, const float* up, const uint8_t* mask, int8_t* q, float* s,
+                          int N, bool exact, hipStream_t st);
 size_t ibh_attn_exact_scratch(int n_heads, int max_pos);
 int ibh_launch_attn_exact(float* out, const float* q, const void* kdata, const void* vdata, const float* ks,
                           const float* vs, const int* dpos, int max_pos, int n_heads, int n_kv, int hd, int kv_bits,
@@ -274,22 +277,6 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(float* __rest
     }
 }
 
-// RoPE (kernels rope, applied as forward.c:573-589: every Q head, each K head
-// once) from a host-computed cos/sin table [pos][head_dim/2][2].
-__global__ void rope_kernel(float* __restrict__ q, float* __restrict__ k, const float* __restrict__ table,
-                            const int* __restrict__ pos, int n_heads, int n_kv, int hd) {
-    const int half = hd / 2;
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (n_heads + n_kv) * half) return;
-    const int h = i / half, j = i - h * half;
-    const float* cs = table + ((size_t)(*pos) * half + j) * 2;
-    const float c = cs[0], s = cs[1];
-    float* p = h < n_heads ? q + (size_t)h * hd : k + (size_t)(h - n_heads) * hd;
-    const float a = p[2 * j], b = p[2 * j + 1];
-    p[2 * j] = a * c - b * s;
-    p[2 * j + 1] = a * s + b * c;
-}
-
 // silu_mul (kernels silu_mul): out = gate / (1 + expf(-gate)) * up; masked rows
 // of a sparse MLP are zero (forward.c:265-270 zeroes them before silu_mul).
 __global__ void silu_mul_kernel(float* __restrict__ out, const float* __restrict__ gate, const float* __restrict__ up,
@@ -424,6 +411,43 @@ int mm_exact(ibh_model* m, const DTensor& t, float* out, const float* in, int M,
     return ibh_launch_matvec_exact(out, t.w, t.s, t.skind, in, M, N, t.bits, nullptr, m->st);
 }
 
+// MLP of one layer from the normed input m->xb2 to m->xb (forward.c:250-290).
+// When gate and up are both W4A8 tensors their shared input is quantized once
+// (the reference quantizes the same vector for each, with identical codes);
+// when down is, silu_mul and the quantization of its result run as one
+// kernel.  `exact` selects the x86-order kernels.
+int mlp(ibh_model* m, const DLayer& L, bool exact) {
+    const int H = m->hidden, I = m->inter;
+    void* st = (void*)m->st;
+    const bool sparse = exact && L.mask && L.mask_sparse;
+    int rc;
+    if (!sparse && m->w4a8 && L.gate.bits == 4 && L.up.bits == 4) {
+        if ((rc = ibh_quantize_act_g128(m->xb2, m->qx, m->sa, H, st)) ||
+            (rc = ibh_matmul_w4a8(m->hb, L.gate.w, L.gate.s, L.gate.skind, m->qx, m->sa, I, H, st)) ||
+            (rc = ibh_matmul_w4a8(m->hb2, L.up.w, L.up.s, L.up.skind, m->qx, m->sa, I, H, st)))
+            return rc;
+    } else if (exact) {
+        if ((rc = mm_exact(m, L.gate, m->hb, m->xb2, I, H, L.mask, L.mask_sparse)) ||
+            (rc = mm_exact(m, L.up, m->hb2, m->xb2, I, H, L.mask, L.mask_sparse)))
+            return rc;
+    } else if ((rc = mm(m, L.gate, m->hb, m->xb2, I, H)) || (rc = mm(m, L.up, m->hb2, m->xb2, I, H))) {
+        return rc;
+    }
+    if (m->w4a8 && L.down.bits == 4) {
+        if ((rc = ibh_launch_silu_quant(m->hb, m->hb, m->hb2, L.mask, m->qx, m->sa, I, exact, m->st)) ||
+            (rc = ibh_matmul_w4a8(m->xb, L.down.w, L.down.s, L.down.skind, m->qx, m->sa, H, I, st)))
+            return rc;
+        return IBH_OK;
+    }
+    if (exact) {
+        if ((rc = ibh_launch_silu_mul_exact(m->hb, m->hb, m->hb2, L.mask, I, m->st))) return rc;
+        return mm_exact(m, L.down, m->xb, m->hb, H, I, nullptr, false);
+    }
+    silu_mul_kernel<<<(I + 255) / 256, 256, 0, m->st>>>(m->hb, m->hb, m->hb2, L.mask, I);
+    IBH_CHECK_LAUNCH("ibh_model: silu_mul");
+    return mm(m, L.down, m->xb, m->hb, H, I);
+}
+
 // forward_single_ex(compute_logits=1) + greedy pick, bit-identical to the CPU.
 int step_exact(ibh_model* m) {
     const int H = m->hidden, kv_dim = m->n_kv * m->head_dim;
@@ -437,17 +461,13 @@ int step_exact(ibh_model* m) {
             (rc = mm_exact(m, L.q, m->q, m->xb, H, H, nullptr, false)) ||
             (rc = mm_exact(m, L.k, m->k, m->xb, kv_dim, H, nullptr, false)) ||
             (rc = mm_exact(m, L.v, m->v, m->xb, kv_dim, H, nullptr, false)) ||
-            (rc = ibh_launch_rope_exact(m->q, m->k, m->rope, m->dpos(), m->n_heads, m->n_kv, m->head_dim, m->st)) ||
-            (rc = ibh_launch_kv_write(L.kd, L.vd, L.ks, L.vs, 0, m->dpos(), m->k, m->v, m->n_kv, m->head_dim,
-                                      m->kv_bits, 1, m->st)) ||
+            (rc = ibh_launch_rope_kv_write(L.kd, L.vd, L.ks, L.vs, m->q, m->k, m->v, m->rope, m->dpos(),
+                                           m->n_heads, m->n_kv, m->head_dim, m->kv_bits, true, m->st)) ||
             (rc = ibh_launch_attn_exact(m->xb2, m->q, L.kd, L.vd, L.ks, L.vs, m->dpos(), m->max_pos, m->n_heads,
                                         m->n_kv, m->head_dim, m->kv_bits, m->att, m->st)) ||
             (rc = mm_exact(m, L.o, m->xb, m->xb2, H, H, nullptr, false)) ||
             (rc = ibh_launch_rmsnorm_exact(m->xb2, m->x, m->xb, L.post_norm, m->eps, H, m->st)) ||
-            (rc = mm_exact(m, L.gate, m->hb, m->xb2, m->inter, H, L.mask, L.mask_sparse)) ||
-            (rc = mm_exact(m, L.up, m->hb2, m->xb2, m->inter, H, L.mask, L.mask_sparse)) ||
-            (rc = ibh_launch_silu_mul_exact(m->hb, m->hb, m->hb2, L.mask, m->inter, m->st)) ||
-            (rc = mm_exact(m, L.down, m->xb, m->hb, H, m->inter, nullptr, false)))
+            (rc = mlp(m, L, true)))
             return rc;
     }
     if ((rc = ibh_launch_rmsnorm_exact(m->x, m->x, m->xb, m->out_norm, m->eps, H, m->st)) ||
@@ -475,12 +495,8 @@ int step(ibh_model* m) {
         if ((rc = mm(m, L.q, m->q, m->xb, H, H)) || (rc = mm(m, L.k, m->k, m->xb, kv_dim, H)) ||
             (rc = mm(m, L.v, m->v, m->xb, kv_dim, H)))
             return rc;
-        const int nr = (m->n_heads + m->n_kv) * (m->head_dim / 2);
-        rope_kernel<<<(nr + 255) / 256, 256, 0, m->st>>>(m->q, m->k, m->rope, m->dpos(), m->n_heads, m->n_kv,
-                                                         m->head_dim);
-        IBH_CHECK_LAUNCH("ibh_model: rope");
-        if ((rc = ibh_launch_kv_write(L.kd, L.vd, L.ks, L.vs, 0, m->dpos(), m->k, m->v, m->n_kv, m->head_dim,
-                                      m->kv_bits, 1, m->st)))
+        if ((rc = ibh_launch_rope_kv_write(L.kd, L.vd, L.ks, L.vs, m->q, m->k, m->v, m->rope, m->dpos(), m->n_heads,
+                                           m->n_kv, m->head_dim, m->kv_bits, false, m->st)))
             return rc;
         if ((rc = ibh_launch_attn(m->xb2, m->q, L.kd, L.vd, L.ks, L.vs, 0, m->dpos(), m->max_pos, m->n_heads,
                                   m->n_kv, m->head_dim, m->kv_bits, m->attn_ws, m->attn_ws_bytes, m->st)))
@@ -488,11 +504,7 @@ int step(ibh_model* m) {
         if ((rc = mm(m, L.o, m->xb, m->xb2, H, H))) return rc;
         add_rmsnorm_kernel<<<1, kNormThreads, 0, m->st>>>(m->xb2, m->x, m->xb, L.post_norm, m->eps, H);
         IBH_CHECK_LAUNCH("ibh_model: rmsnorm");
-        if ((rc = mm(m, L.gate, m->hb, m->xb2, m->inter, H)) || (rc = mm(m, L.up, m->hb2, m->xb2, m->inter, H)))
-            return rc;
-        silu_mul_kernel<<<(m->inter + 255) / 256, 256, 0, m->st>>>(m->hb, m->hb, m->hb2, L.mask, m->inter);
-        IBH_CHECK_LAUNCH("ibh_model: silu_mul");
-        if ((rc = mm(m, L.down, m->xb, m->hb, H, m->inter))) return rc;
+        if ((rc = mlp(m, L, false))) return rc;
     }
     add_rmsnorm_kernel<<<1, kNormThreads, 0, m->st>>>(m->x, m->x, m->xb, m->out_norm, m->eps, H);
     IBH_CHECK_LAUNCH("ibh_model: final rmsnorm");

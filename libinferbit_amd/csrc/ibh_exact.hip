@@ -262,21 +262,6 @@ __global__ __launch_bounds__(256) void matvec_serial_exact(float* __restrict__ y
     y[row] = BITS == 16 ? sum : sum * load_scale<KIND>(sc, row);
 }
 
-// RoPE from the host cos/sin table [pos][hd/2][2], x86 FMA forms.
-__global__ void rope_exact(float* __restrict__ q, float* __restrict__ k, const float* __restrict__ table,
-                           const int* __restrict__ pos, int n_heads, int n_kv, int hd) {
-    const int half = hd / 2;
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (n_heads + n_kv) * half) return;
-    const int h = i / half, j = i - h * half;
-    const float* cs = table + ((size_t)(*pos) * half + j) * 2;
-    const float c = cs[0], s = cs[1];
-    float* p = h < n_heads ? q + (size_t)h * hd : k + (size_t)(h - n_heads) * hd;
-    const float a = p[2 * j], b = p[2 * j + 1];
-    p[2 * j] = fmaf(a, c, -(b * s));
-    p[2 * j + 1] = fmaf(a, s, b * c);
-}
-
 __global__ void silu_mul_exact(float* __restrict__ out, const float* __restrict__ gate, const float* __restrict__ up,
                                const uint8_t* __restrict__ mask, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -671,14 +656,6 @@ int ibh_launch_matvec_exact(float* y, const void* w, const void* sc, int kind, c
 #undef IBH_MX
 #undef IBH_MXA
     IBH_CHECK_LAUNCH("exact matvec");
-    return IBH_OK;
-}
-
-int ibh_launch_rope_exact(float* q, float* k, const float* table, const int* dpos, int n_heads, int n_kv, int hd,
-                          hipStream_t st) {
-    const int nr = (n_heads + n_kv) * (hd / 2);
-    rope_exact<<<(nr + 255) / 256, 256, 0, st>>>(q, k, table, dpos, n_heads, n_kv, hd);
-    IBH_CHECK_LAUNCH("exact rope");
     return IBH_OK;
 }
 

@@ -271,17 +271,10 @@ __global__ __launch_bounds__(kBlock) void w4a8_generic(float* __restrict__ y,
 }
 
 // Activation quantizer, one wavefront per 128-group (threading.c:401-432).
-__global__ __launch_bounds__(kBlock) void quant_act_g128(const float* __restrict__ x,
-                                                         int8_t* __restrict__ q,
-                                                         float* __restrict__ s, int N) {
+// Quantization of one 128-group held two elements per lane (threading.c:401-432).
+__device__ __forceinline__ void quant_group(float v0, float v1, int j0, int j1, int end, int g, int8_t* __restrict__ q,
+                                            float* __restrict__ s) {
     const int lane = threadIdx.x & (kWave - 1);
-    const int g = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
-    const int base = g * 128;
-    if (base >= N) return;
-    const int end = min(N, base + 128);
-    const int j0 = base + lane, j1 = base + lane + 64;
-    const float v0 = j0 < end ? x[j0] : 0.f;
-    const float v1 = j1 < end ? x[j1] : 0.f;
     const float mx = wave_max(fmaxf(v0 < 0 ? -v0 : v0, v1 < 0 ? -v1 : v1));
     if (mx < 1e-10f) {
         if (j0 < end) q[j0] = 0;
@@ -299,6 +292,49 @@ __global__ __launch_bounds__(kBlock) void quant_act_g128(const float* __restrict
     if (j0 < end) q[j0] = qz(v0);
     if (j1 < end) q[j1] = qz(v1);
     if (lane == 0) s[g] = scale;
+}
+
+__global__ __launch_bounds__(kBlock) void quant_act_g128(const float* __restrict__ x,
+                                                         int8_t* __restrict__ q,
+                                                         float* __restrict__ s, int N) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int g = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+    const int base = g * 128;
+    if (base >= N) return;
+    const int end = min(N, base + 128);
+    const int j0 = base + lane, j1 = base + lane + 64;
+    const float v0 = j0 < end ? x[j0] : 0.f;
+    const float v1 = j1 < end ? x[j1] : 0.f;
+    quant_group(v0, v1, j0, j1, end, g, q, s);
+}
+
+// silu_mul (out = gate / (1 + expf(-gate)) * up, masked rows zero) and the
+// 128-group quantization of its result, one launch.  EXACT uses the glibc
+// expf restatement (the reference's x86 build), otherwise the device expf.
+template <bool EXACT>
+__global__ __launch_bounds__(kBlock) void silu_quant_g128(float* __restrict__ out, const float* __restrict__ gate,
+                                                          const float* __restrict__ up,
+                                                          const uint8_t* __restrict__ mask,
+                                                          int8_t* __restrict__ q, float* __restrict__ s, int N) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int g = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+    const int base = g * 128;
+    if (base >= N) return;
+    const int end = min(N, base + 128);
+    const int j0 = base + lane, j1 = base + lane + 64;
+    float h[2];
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+        const int j = e ? j1 : j0;
+        h[e] = 0.f;
+        if (j < end) {
+            const bool on = !mask || mask[j];
+            const float gv = on ? gate[j] : 0.f, uv = on ? up[j] : 0.f;
+            h[e] = (gv / (1.0f + (EXACT ? ib_expf(-gv) : expf(-gv)))) * uv;
+            out[j] = h[e];
+        }
+    }
+    quant_group(h[0], h[1], j0, j1, end, g, q, s);
 }
 
 // ── int8 weights x fp32 activations, batched (scalar.c:70-84) ─────────────
@@ -479,6 +515,16 @@ static int w4a8_args_ok(const void* out, const void* w, const void* s, const voi
         return 0;
     }
     return 1;
+}
+
+int ibh_launch_silu_quant(float* out, const float* gate, const float* up, const uint8_t* mask, int8_t* q, float* s,
+                          int N, bool exact, hipStream_t st) {
+    const int G = (N + 127) / 128;
+    const int blocks = (G + kWavesPerBlock - 1) / kWavesPerBlock;
+    if (exact) silu_quant_g128<true><<<blocks, kBlock, 0, st>>>(out, gate, up, mask, q, s, N);
+    else silu_quant_g128<false><<<blocks, kBlock, 0, st>>>(out, gate, up, mask, q, s, N);
+    IBH_CHECK_LAUNCH("silu_mul + quantize");
+    return IBH_OK;
 }
 
 extern "C" int ibh_matmul_w4a8(float* out, const void* w, const void* scales, int scale_kind,
