@@ -121,4 +121,56 @@ __host__ __device__ inline float ib_expf(float x) {
     return (float)y;
 }
 
+// Up to three matrices with the same input length (and activation) in one
+// launch, e.g. q/k/v or gate/up of a decoder layer: blocks [0, b1) serve
+// matrix 0, [b1, b2) matrix 1, [b2, ...) matrix 2.
+struct RowSet {
+    const uint8_t* W[3];
+    const void* sc[3];
+    float* y[3];
+    int M[3];
+    int b1, b2;
+};
+struct RowPick {
+    const uint8_t* W;
+    const void* sc;
+    float* y;
+    int M;
+    int bid;                                                 // block index within its matrix
+};
+__device__ __forceinline__ RowPick pick_rows(const RowSet& s) {
+    const int b = blockIdx.x;
+    if (b >= s.b2) return {s.W[2], s.sc[2], s.y[2], s.M[2], b - s.b2};
+    if (b >= s.b1) return {s.W[1], s.sc[1], s.y[1], s.M[1], b - s.b1};
+    return {s.W[0], s.sc[0], s.y[0], s.M[0], b};
+}
+// Host side: one matrix of a set.
+struct MatDesc {
+    float* out;
+    const void* w;
+    const void* s;
+    int M;
+};
+inline RowSet make_rowset(const MatDesc* d, int n, int rows_per_block) {
+    RowSet r{};
+    int b = 0;
+    for (int i = 0; i < 3; i++) {
+        const MatDesc& m = d[i < n ? i : 0];
+        r.W[i] = (const uint8_t*)m.w;
+        r.sc[i] = m.s;
+        r.y[i] = m.out;
+        r.M[i] = m.M;
+    }
+    b += (d[0].M + rows_per_block - 1) / rows_per_block;
+    r.b1 = n > 1 ? b : 0x7fffffff;
+    if (n > 1) b += (d[1].M + rows_per_block - 1) / rows_per_block;
+    r.b2 = n > 2 ? b : 0x7fffffff;
+    return r;
+}
+inline int rowset_blocks(const MatDesc* d, int n, int rows_per_block) {
+    int b = 0;
+    for (int i = 0; i < n; i++) b += (d[i].M + rows_per_block - 1) / rows_per_block;
+    return b;
+}
+
 }  // namespace ibh

@@ -50,6 +50,11 @@ int ibh_launch_rope_kv_write(void* kdata, void* vdata, float* kscales, float* vs
                              int head_dim, int kv_bits, bool exact, hipStream_t st);
 int ibh_launch_silu_quant(float* out, const float* gate, const float* up, const uint8_t* mask, int8_t* q, float* s,
                           int N, bool exact, hipStream_t st);
+int ibh_launch_rows_w4a8_multi(const MatDesc* d, int n, int kind, const int8_t* qx, const float* sa, int N,
+                               hipStream_t st);
+int ibh_launch_rows_x_multi(const MatDesc* d, int n, int kind, const float* x, int N, int bits, hipStream_t st);
+int ibh_launch_matvec_exact_multi(const MatDesc* d, int n, int kind, const float* x, int N, int bits,
+                                  hipStream_t st);
 size_t ibh_attn_exact_scratch(int n_heads, int max_pos);
 int ibh_launch_attn_exact(float* out, const float* q, const void* kdata, const void* vdata, const float* ks,
                           const float* vs, const int* dpos, int max_pos, int n_heads, int n_kv, int hd, int kv_bits,
@@ -411,6 +416,41 @@ int mm_exact(ibh_model* m, const DTensor& t, float* out, const float* in, int M,
     return ibh_launch_matvec_exact(out, t.w, t.s, t.skind, in, M, N, t.bits, nullptr, m->st);
 }
 
+// q/k/v projections of the normed input m->xb (forward.c:556-572).  When the
+// three tensors have the same format they run as one launch (same kernels,
+// same per-row arithmetic as three separate calls).
+int qkv(ibh_model* m, const DLayer& L, bool exact) {
+    const int H = m->hidden, KV = m->n_kv * m->head_dim;
+    const bool same = L.q.bits == L.k.bits && L.k.bits == L.v.bits && L.q.skind == L.k.skind && L.k.skind == L.v.skind;
+    const MatDesc d[3] = {{m->q, L.q.w, L.q.s, H}, {m->k, L.k.w, L.k.s, KV}, {m->v, L.v.w, L.v.s, KV}};
+    int rc;
+    if (same && L.q.bits == 4 && m->w4a8) {
+        if ((rc = ibh_quantize_act_g128(m->xb, m->qx, m->sa, H, (void*)m->st))) return rc;
+        if (ibh_launch_rows_w4a8_multi(d, 3, L.q.skind, m->qx, m->sa, H, m->st)) {
+            IBH_CHECK_LAUNCH("ibh_model: qkv (w4a8)");
+            return IBH_OK;
+        }
+    } else if (same && exact && L.q.bits == 8) {
+        return ibh_launch_matvec_exact_multi(d, 3, L.q.skind, m->xb, H, 8, m->st);
+    } else if (same && !exact && (L.q.bits == 8 || L.q.bits == 4)) {
+        if (ibh_launch_rows_x_multi(d, 3, L.q.skind, m->xb, H, L.q.bits, m->st)) {
+            IBH_CHECK_LAUNCH("ibh_model: qkv");
+            return IBH_OK;
+        }
+    }
+    if (exact) {
+        if ((rc = mm_exact(m, L.q, m->q, m->xb, H, H, nullptr, false)) ||
+            (rc = mm_exact(m, L.k, m->k, m->xb, KV, H, nullptr, false)) ||
+            (rc = mm_exact(m, L.v, m->v, m->xb, KV, H, nullptr, false)))
+            return rc;
+        return IBH_OK;
+    }
+    if ((rc = mm(m, L.q, m->q, m->xb, H, H)) || (rc = mm(m, L.k, m->k, m->xb, KV, H)) ||
+        (rc = mm(m, L.v, m->v, m->xb, KV, H)))
+        return rc;
+    return IBH_OK;
+}
+
 // MLP of one layer from the normed input m->xb2 to m->xb (forward.c:250-290).
 // When gate and up are both W4A8 tensors their shared input is quantized once
 // (the reference quantizes the same vector for each, with identical codes);
@@ -422,10 +462,14 @@ int mlp(ibh_model* m, const DLayer& L, bool exact) {
     const bool sparse = exact && L.mask && L.mask_sparse;
     int rc;
     if (!sparse && m->w4a8 && L.gate.bits == 4 && L.up.bits == 4) {
-        if ((rc = ibh_quantize_act_g128(m->xb2, m->qx, m->sa, H, st)) ||
-            (rc = ibh_matmul_w4a8(m->hb, L.gate.w, L.gate.s, L.gate.skind, m->qx, m->sa, I, H, st)) ||
-            (rc = ibh_matmul_w4a8(m->hb2, L.up.w, L.up.s, L.up.skind, m->qx, m->sa, I, H, st)))
+        if ((rc = ibh_quantize_act_g128(m->xb2, m->qx, m->sa, H, st))) return rc;
+        const MatDesc d[2] = {{m->hb, L.gate.w, L.gate.s, I}, {m->hb2, L.up.w, L.up.s, I}};
+        if (L.gate.skind == L.up.skind && ibh_launch_rows_w4a8_multi(d, 2, L.gate.skind, m->qx, m->sa, H, m->st)) {
+            IBH_CHECK_LAUNCH("ibh_model: gate/up");
+        } else if ((rc = ibh_matmul_w4a8(m->hb, L.gate.w, L.gate.s, L.gate.skind, m->qx, m->sa, I, H, st)) ||
+                   (rc = ibh_matmul_w4a8(m->hb2, L.up.w, L.up.s, L.up.skind, m->qx, m->sa, I, H, st))) {
             return rc;
+        }
     } else if (exact) {
         if ((rc = mm_exact(m, L.gate, m->hb, m->xb2, I, H, L.mask, L.mask_sparse)) ||
             (rc = mm_exact(m, L.up, m->hb2, m->xb2, I, H, L.mask, L.mask_sparse)))
@@ -458,9 +502,7 @@ int step_exact(ibh_model* m) {
     for (int l = 0; l < m->n_layers; l++) {
         DLayer& L = m->layers[l];
         if ((rc = ibh_launch_rmsnorm_exact(m->xb, m->x, l ? m->xb : nullptr, L.in_norm, m->eps, H, m->st)) ||
-            (rc = mm_exact(m, L.q, m->q, m->xb, H, H, nullptr, false)) ||
-            (rc = mm_exact(m, L.k, m->k, m->xb, kv_dim, H, nullptr, false)) ||
-            (rc = mm_exact(m, L.v, m->v, m->xb, kv_dim, H, nullptr, false)) ||
+            (rc = qkv(m, L, true)) ||
             (rc = ibh_launch_rope_kv_write(L.kd, L.vd, L.ks, L.vs, m->q, m->k, m->v, m->rope, m->dpos(),
                                            m->n_heads, m->n_kv, m->head_dim, m->kv_bits, true, m->st)) ||
             (rc = ibh_launch_attn_exact(m->xb2, m->q, L.kd, L.vd, L.ks, L.vs, m->dpos(), m->max_pos, m->n_heads,
@@ -492,9 +534,7 @@ int step(ibh_model* m) {
         // residual of the previous layer's MLP folded into this norm
         add_rmsnorm_kernel<<<1, kNormThreads, 0, m->st>>>(m->xb, m->x, l ? m->xb : nullptr, L.in_norm, m->eps, H);
         IBH_CHECK_LAUNCH("ibh_model: rmsnorm");
-        if ((rc = mm(m, L.q, m->q, m->xb, H, H)) || (rc = mm(m, L.k, m->k, m->xb, kv_dim, H)) ||
-            (rc = mm(m, L.v, m->v, m->xb, kv_dim, H)))
-            return rc;
+        if ((rc = qkv(m, L, false))) return rc;
         if ((rc = ibh_launch_rope_kv_write(L.kd, L.vd, L.ks, L.vs, m->q, m->k, m->v, m->rope, m->dpos(), m->n_heads,
                                            m->n_kv, m->head_dim, m->kv_bits, false, m->st)))
             return rc;

@@ -119,9 +119,12 @@ __global__ __launch_bounds__(256) void rmsnorm_exact(float* out, float* x, const
 // into a per-wavefront LDS tile as int8, then reads back column c of the 16
 // blocks; x is staged in LDS once per block.
 template <int BITS, int KIND, bool ALIGNED>
-__global__ __launch_bounds__(256) void matvec_exact(float* __restrict__ y, const uint8_t* __restrict__ W,
-                                                    const void* __restrict__ sc, const float* __restrict__ x, int M,
-                                                    int N) {
+__global__ __launch_bounds__(256) void matvec_exact(const RowSet rs, const float* __restrict__ x, int N) {
+    const RowPick P = pick_rows(rs);
+    const uint8_t* __restrict__ W = P.W;
+    const void* __restrict__ sc = P.sc;
+    float* __restrict__ y = P.y;
+    const int M = P.M;
     extern __shared__ __align__(16) unsigned char smem[];
     float* xs = (float*)smem;                                         // [N]
     int8_t* tile = (int8_t*)(smem + (((size_t)N * 4 + 15) & ~(size_t)15));   // [4 waves][4 rows][256]
@@ -140,7 +143,7 @@ __global__ __launch_bounds__(256) void matvec_exact(float* __restrict__ y, const
     __syncthreads();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane >> 4, c = lane & 15;
-    const int row = (blockIdx.x * 4 + wave) * 4 + r;
+    const int row = (P.bid * 4 + wave) * 4 + r;
     const int rowc = min(row, M - 1);
     const size_t rb = (size_t)N * BITS / 8;
     const uint8_t* wr = W + (size_t)rowc * rb;
@@ -626,6 +629,9 @@ int ibh_launch_rmsnorm_exact(float* out, float* x, const float* delta, const uin
     return IBH_OK;
 }
 
+int ibh_launch_matvec_exact_multi(const MatDesc* d, int n, int kind, const float* x, int N, int bits,
+                                  hipStream_t st);
+
 size_t ibh_exact_matvec_lds(int N) { return (((size_t)N * 4 + 15) & ~(size_t)15) + 4 * 4 * 256; }
 
 int ibh_launch_matvec_exact(float* y, const void* w, const void* sc, int kind, const float* x, int M, int N, int bits,
@@ -641,15 +647,26 @@ int ibh_launch_matvec_exact(float* y, const void* w, const void* sc, int kind, c
         IBH_CHECK_LAUNCH("exact matvec (serial)");
         return IBH_OK;
     }
+    const MatDesc d{y, w, sc, M};
+    return ibh_launch_matvec_exact_multi(&d, 1, kind, x, N, bits, st);
+}
+
+// 1-3 matrices with the same N, bits and scale kind sharing x, one launch.
+int ibh_launch_matvec_exact_multi(const MatDesc* d, int n, int kind, const float* x, int N, int bits,
+                                  hipStream_t st) {
     const size_t lds = ibh_exact_matvec_lds(N);
-    if ((bits != 8 && bits != 4) || lds > 64 * 1024 || (bits == 4 && N % 2)) {
+    if ((bits != 8 && bits != 4) || lds > 64 * 1024 || (bits == 4 && N % 2) || n < 1 || n > 3) {
         ibh_set_error("exact matvec: bits=%d N=%d unsupported", bits, N);
         return IBH_ERROR_PARAM;
     }
     const size_t rb = (size_t)N * bits / 8;
-    const bool al = bits == 8 ? (((uintptr_t)w & 15) == 0 && rb % 16 == 0) : (((uintptr_t)w & 7) == 0 && rb % 8 == 0);
-    const int blocks = (M + 15) / 16;
-#define IBH_MX(B_, K_, A_) matvec_exact<B_, K_, A_><<<blocks, 256, lds, st>>>(y, W, sc, x, M, N)
+    bool al = true;
+    for (int i = 0; i < n; i++)
+        al = al && (bits == 8 ? (((uintptr_t)d[i].w & 15) == 0 && rb % 16 == 0)
+                              : (((uintptr_t)d[i].w & 7) == 0 && rb % 8 == 0));
+    const RowSet rs = make_rowset(d, n, 16);
+    const int blocks = rowset_blocks(d, n, 16);
+#define IBH_MX(B_, K_, A_) matvec_exact<B_, K_, A_><<<blocks, 256, lds, st>>>(rs, x, N)
 #define IBH_MXA(B_, K_) do { if (al) IBH_MX(B_, K_, true); else IBH_MX(B_, K_, false); } while (0)
     if (kind == IBH_SCALE_F16) { if (bits == 8) IBH_MXA(8, IBH_SCALE_F16); else IBH_MXA(4, IBH_SCALE_F16); }
     else { if (bits == 8) IBH_MXA(8, IBH_SCALE_F32); else IBH_MXA(4, IBH_SCALE_F32); }

@@ -220,14 +220,18 @@ __global__ __launch_bounds__(512) void gemv_rows_w4a8(float* __restrict__ y, con
 // groups, one or two 1 KiB steps), whole rows per wavefront.  sa lives in
 // registers from the start, group sums pass through LDS once.
 template <int KIND, int R, int GS>
-__global__ __launch_bounds__(256) void gemv_rows_w4a8_k(float* __restrict__ y, const uint8_t* __restrict__ W,
-                                                        const void* __restrict__ sc, const int8_t* __restrict__ qx,
-                                                        const float* __restrict__ sa, int M) {
+__global__ __launch_bounds__(256) void gemv_rows_w4a8_k(const RowSet rs, const int8_t* __restrict__ qx,
+                                                        const float* __restrict__ sa) {
     constexpr int SPW = GS / 16;
     constexpr size_t rb = (size_t)GS * 64;
     __shared__ __align__(16) float gsum[4 * R][GS];
+    const RowPick P = pick_rows(rs);
+    const uint8_t* __restrict__ W = P.W;
+    const void* __restrict__ sc = P.sc;
+    float* __restrict__ y = P.y;
+    const int M = P.M;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int row0 = (blockIdx.x * 4 + wave) * R;
+    const int row0 = (P.bid * 4 + wave) * R;
     const int segl = seg_of<true>(lane);
     float4 sav[GS / 4];
 #pragma unroll
@@ -319,9 +323,13 @@ __device__ __forceinline__ uint32_t digit_byte(float k) { return (uint32_t)(int)
 
 // NXQ: float4 slices of x per thread (N <= 4 * NXQ * blockDim.x).
 template <int BITS, int KIND, int R, int SPW, int NXQ>
-__global__ __launch_bounds__(1024) void gemv_rows_x(float* __restrict__ y, const uint8_t* __restrict__ W,
-                                                    const void* __restrict__ sc, const float* __restrict__ x, int M,
-                                                    int N, int S, int WR, int KW) {
+__global__ __launch_bounds__(1024) void gemv_rows_x(const RowSet rs, const float* __restrict__ x, int N, int S, int WR,
+                                                    int KW) {
+    const RowPick P = pick_rows(rs);
+    const uint8_t* __restrict__ W = P.W;
+    const void* __restrict__ sc = P.sc;
+    float* __restrict__ y = P.y;
+    const int M = P.M;
     constexpr int NA = RGeo<BITS>::kNA;
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ float red[kMaxWaves];
@@ -331,7 +339,7 @@ __global__ __launch_bounds__(1024) void gemv_rows_x(float* __restrict__ y, const
     const int wave = threadIdx.x >> 6;
     const int wr = wave / KW, wk = wave - wr * KW;
     const int RB = WR * R;
-    const int row0 = blockIdx.x * RB + wr * R;
+    const int row0 = P.bid * RB + wr * R;
     const size_t rb = (size_t)N * BITS / 8;
     const int nth = blockDim.x;
 
@@ -439,7 +447,7 @@ __global__ __launch_bounds__(1024) void gemv_rows_x(float* __restrict__ y, const
         const int t = threadIdx.x;
         if (t < RB) {
             const int w_r = t / R, r = t - w_r * R;
-            const int row = blockIdx.x * RB + t;
+            const int row = P.bid * RB + t;
             if (row < M) {
                 float v = 0.f;
                 for (int k = 0; k < KW; k++) v += part[w_r * KW + k][r];
@@ -451,20 +459,31 @@ __global__ __launch_bounds__(1024) void gemv_rows_x(float* __restrict__ y, const
 
 }  // namespace
 
+// W4A8, batch 1, for 1-3 matrices of N = 2048 or 4096 columns sharing qx
+// (one launch).  Returns 1 if launched, 0 if not eligible.
+int ibh_launch_rows_w4a8_multi(const MatDesc* d, int n, int kind, const int8_t* qx, const float* sa, int N,
+                               hipStream_t st) {
+    if ((N != 2048 && N != 4096) || ((uintptr_t)sa & 15) || ((uintptr_t)qx & 15) || n < 1 || n > 3) return 0;
+    for (int i = 0; i < n; i++)
+        if (((uintptr_t)d[i].w & 15) || d[i].M <= 0) return 0;
+    constexpr int R = 4;
+    const RowSet rs = make_rowset(d, n, 4 * R);
+    const int blocks = rowset_blocks(d, n, 4 * R);
+#define IBH_RWK(K_, G_) gemv_rows_w4a8_k<K_, R, G_><<<blocks, 256, 0, st>>>(rs, qx, sa)
+    if (kind == IBH_SCALE_F16) { if (N == 4096) IBH_RWK(IBH_SCALE_F16, 32); else IBH_RWK(IBH_SCALE_F16, 16); }
+    else { if (N == 4096) IBH_RWK(IBH_SCALE_F32, 32); else IBH_RWK(IBH_SCALE_F32, 16); }
+#undef IBH_RWK
+    return 1;
+}
+
 // W4A8, batch 1.  Returns 1 if launched, 0 if the shape is not eligible.
 int ibh_launch_rows_w4a8(float* out, const void* w, const void* sw, int kind, const int8_t* qx, const float* sa,
                          int M, int N, hipStream_t st) {
     const size_t rb = (size_t)N / 2;
     if (N % 32 != 0 || N < 32 || ((uintptr_t)w & 15) || ((uintptr_t)qx & 15)) return 0;
-    if ((N == 2048 || N == 4096) && ((uintptr_t)sa & 15) == 0 && !getenv("IBH_TMP_NOWK")) {
-        constexpr int R = 4;
-        const int blocks = (M + 4 * R - 1) / (4 * R);
-        const uint8_t* W = (const uint8_t*)w;
-#define IBH_RWK(K_, G_) gemv_rows_w4a8_k<K_, R, G_><<<blocks, 256, 0, st>>>(out, W, sw, qx, sa, M)
-        if (kind == IBH_SCALE_F16) { if (N == 4096) IBH_RWK(IBH_SCALE_F16, 32); else IBH_RWK(IBH_SCALE_F16, 16); }
-        else { if (N == 4096) IBH_RWK(IBH_SCALE_F32, 32); else IBH_RWK(IBH_SCALE_F32, 16); }
-#undef IBH_RWK
-        return 1;
+    if ((N == 2048 || N == 4096) && ((uintptr_t)sa & 15) == 0) {
+        const MatDesc d{out, w, sw, M};
+        return ibh_launch_rows_w4a8_multi(&d, 1, kind, qx, sa, N, st);
     }
     const int S = (int)((rb + 1023) / 1024);
     const int spw = S == 1 ? 1 : 2;
@@ -494,26 +513,30 @@ int ibh_launch_rows_w4a8(float* out, const void* w, const void* sw, int kind, co
 
 // fp32 activations, int8 / int4 weights, rows of whole 1 KiB steps.  Returns 1
 // if launched, 0 if the shape is not eligible.
-int ibh_launch_rows_x(float* out, const void* w, const void* scales, int kind, const float* x, int M, int N,
-                      int bits, hipStream_t st) {
+int ibh_launch_rows_x_multi(const MatDesc* d, int n, int kind, const float* x, int N, int bits, hipStream_t st) {
     if (bits != 8 && bits != 4) return 0;
     const size_t rb = (size_t)N * bits / 8;
-    if (rb % 1024 != 0 || ((uintptr_t)w & 15) || ((uintptr_t)x & 15) || N > 131072) return 0;
+    if (rb % 1024 != 0 || ((uintptr_t)x & 15) || N > 131072 || n < 1 || n > 3) return 0;
+    int Mt = 0;
+    for (int i = 0; i < n; i++) {
+        if (((uintptr_t)d[i].w & 15) || d[i].M <= 0) return 0;
+        Mt += d[i].M;
+    }
     const int S = (int)(rb / 1024);
     constexpr int R = 4, SPW = 2;
     const int KW = (S + SPW - 1) / SPW;
     // rows per block: enough blocks to cover the chip twice where possible
     int WR = 8;
-    while (WR > 1 && (WR * KW > kMaxWaves || (M + WR * R - 1) / (WR * R) < 384)) WR >>= 1;
+    while (WR > 1 && (WR * KW > kMaxWaves || (Mt + WR * R - 1) / (WR * R) < 384)) WR >>= 1;
     if (WR * KW > kMaxWaves) return 0;
     const int nthreads = 64 * WR * KW;
     const int nxq = (N / 4 + nthreads - 1) / nthreads;
     if (nxq > 8) return 0;
     const size_t lds = (size_t)S * (bits == 8 ? 1 : 2) * 3 * 64 * 16;
     if (lds > 64 * 1024) return 0;
-    const int blocks = (M + WR * R - 1) / (WR * R);
-    const uint8_t* W = (const uint8_t*)w;
-#define IBH_RX(B_, K_, Q_) gemv_rows_x<B_, K_, R, SPW, Q_><<<blocks, nthreads, lds, st>>>(out, W, scales, x, M, N, S, WR, KW)
+    const RowSet rs = make_rowset(d, n, WR * R);
+    const int blocks = rowset_blocks(d, n, WR * R);
+#define IBH_RX(B_, K_, Q_) gemv_rows_x<B_, K_, R, SPW, Q_><<<blocks, nthreads, lds, st>>>(rs, x, N, S, WR, KW)
 #define IBH_RXQ(B_, K_) do { if (nxq <= 1) IBH_RX(B_, K_, 1); else if (nxq <= 2) IBH_RX(B_, K_, 2); \
                              else if (nxq <= 4) IBH_RX(B_, K_, 4); else IBH_RX(B_, K_, 8); } while (0)
     if (kind == IBH_SCALE_F16) { if (bits == 8) IBH_RXQ(8, IBH_SCALE_F16); else IBH_RXQ(4, IBH_SCALE_F16); }
@@ -521,4 +544,10 @@ int ibh_launch_rows_x(float* out, const void* w, const void* scales, int kind, c
 #undef IBH_RX
 #undef IBH_RXQ
     return 1;
+}
+
+int ibh_launch_rows_x(float* out, const void* w, const void* scales, int kind, const float* x, int M, int N,
+                      int bits, hipStream_t st) {
+    const MatDesc d{out, w, scales, M};
+    return ibh_launch_rows_x_multi(&d, 1, kind, x, N, bits, st);
 }
