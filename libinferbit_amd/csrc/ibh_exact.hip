@@ -369,20 +369,20 @@ __device__ __forceinline__ void kv_deq16(float* o, const KvRaw<BITS>& r) {
     }
 }
 
-// Four groups of 4 consecutive elements (rows t[u], columns d[u]..d[u]+3),
+// NG groups of 4 consecutive elements (rows t[u], columns d[u]..d[u]+3),
 // loads only: fp32 16 B, int8 4 B, int4 2 B per group, plus the rows' scales.
-template <int BITS>
+template <int BITS, int NG>
 struct Kv4x4 {
-    uint32_t q[4][BITS >= 16 ? 4 : 1];
-    float sc[4];
+    uint32_t q[NG][BITS >= 16 ? 4 : 1];
+    float sc[NG];
 };
 
-template <int BITS>
-__device__ __forceinline__ void kv_raw4x4(Kv4x4<BITS>& r, const uint8_t* base, const float* scales, const int* t,
+template <int BITS, int NG>
+__device__ __forceinline__ void kv_raw4x4(Kv4x4<BITS, NG>& r, const uint8_t* base, const float* scales, const int* t,
                                           const int* d, int kh, int hd, int n_kv) {
     const int kv_dim = n_kv * hd;
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
+    for (int u = 0; u < NG; u++) {
         if constexpr (BITS >= 16) {
             const uint4 v = *(const uint4*)((const float*)base + (size_t)t[u] * kv_dim + (size_t)kh * hd + d[u]);
             r.q[u][0] = v.x; r.q[u][1] = v.y; r.q[u][2] = v.z; r.q[u][3] = v.w;
@@ -397,8 +397,8 @@ __device__ __forceinline__ void kv_raw4x4(Kv4x4<BITS>& r, const uint8_t* base, c
     }
 }
 
-template <int BITS>
-__device__ __forceinline__ float4 kv_deq4(const Kv4x4<BITS>& r, int u) {
+template <int BITS, int NG>
+__device__ __forceinline__ float4 kv_deq4(const Kv4x4<BITS, NG>& r, int u) {
     if constexpr (BITS >= 16) {
         return float4{__builtin_bit_cast(float, r.q[u][0]), __builtin_bit_cast(float, r.q[u][1]),
                       __builtin_bit_cast(float, r.q[u][2]), __builtin_bit_cast(float, r.q[u][3])};
@@ -444,17 +444,20 @@ __global__ __launch_bounds__(64) void attn_scores_exact(float* __restrict__ att,
 }
 
 // Softmax over one head's scores and the serial output sum (forward.c:480-502,
-// kernels/avx2.c:192-229).  Block per (head, slice of 64 d), 256 threads:
+// kernels/avx2.c:192-229).  Block per (head, slice of 64 d), 512 threads:
 //  max (any order is exact); e_t = expf(s_t - max) into LDS; thread 0 sums
 //  e_t in position order; a_t = e_t * (1/sum).  Output: wave 0 (one lane per
-//  d of the slice) adds p_t[d] = a_t * v_t[d] in position order; waves 1-3
-//  produce p for the next chunk of kAoCH positions into a double-buffered LDS
-//  tile, with their V rows held kAoP chunks ahead in registers (the loads of
+//  d of the slice) adds p_t[d] = a_t * v_t[d] in position order; waves 1-7
+//  produce p for the chunks of kAoCH positions ahead into a ring of LDS
+//  tiles, with their V rows held kAoP chunks ahead in registers (the loads of
 //  the first chunks are issued before the serial sum).  Every barrier after
 //  those loads orders LDS only, so the prefetched loads stay in flight.
-constexpr int kAoThreads = 256;
+constexpr int kAoThreads = 512;                           // wave 0 consumer, waves 1-7 producers
 constexpr int kAoD = 64;                                  // d per block = consumer lanes
-constexpr int kAoCH = 48;                                 // positions per chunk: 48*64/4 = 4 float4 per producer
+constexpr int kAoProd = kAoThreads - 64;
+constexpr int kAoCH = 56;                                 // positions per chunk: 56*64/4 = 2 float4 per producer
+constexpr int kAoNG = kAoCH * kAoD / 4 / kAoProd;         // float4 groups per producer per chunk
+static_assert(kAoNG * kAoProd * 4 == kAoCH * kAoD, "chunk split");
 constexpr int kAoP = 4;                                   // chunks of V rows in flight per producer
 constexpr int kAoTile = kAoCH * kAoD;                     // floats per LDS chunk tile
 
@@ -466,7 +469,7 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_s_barrier();
 }
 
-template <int BITS, int HD>
+template <int BITS, int HD, int NB>
 __global__ __launch_bounds__(kAoThreads) void attn_out_exact(float* __restrict__ out, const float* __restrict__ att,
                                                             const uint8_t* __restrict__ vd,
                                                             const float* __restrict__ vs,
@@ -477,7 +480,7 @@ __global__ __launch_bounds__(kAoThreads) void attn_out_exact(float* __restrict__
     __shared__ float inv_s;
     constexpr int NS = HD / kAoD;
     float* es = sm;                                       // [tcap]
-    float* pbuf = sm + tcap;                              // [2][kAoCH][kAoD]
+    float* pbuf = sm + tcap;                              // [NB][kAoCH][kAoD]
     const int h = blockIdx.x / NS, d0 = (blockIdx.x % NS) * kAoD;
     const int tid = threadIdx.x, wave = tid >> 6;
     const int T = *dpos + 1;
@@ -514,32 +517,32 @@ __global__ __launch_bounds__(kAoThreads) void attn_out_exact(float* __restrict__
     for (int t = tid; t < T; t += kAoThreads) es[t] = ib_expf(es[t] - m);
     __syncthreads();
 
-    // producer geometry: float4 f = u * 192 + pid of a chunk tile is row
+    // producer geometry: float4 f = u * kAoProd + pid of a chunk tile is row
     // f / 16, columns 4 (f % 16) .. +3 of the slice
     const int nch = (T + kAoCH - 1) / kAoCH;
     const int nsteps = (nch + kAoP - 1) / kAoP * kAoP;    // barrier steps, the same for every wave
     const int pid = tid - 64;
-    int gtt[4], gd[4];
+    int gtt[kAoNG], gd[kAoNG];
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
-        const int f = u * (kAoThreads - 64) + (pid < 0 ? 0 : pid);
+    for (int u = 0; u < kAoNG; u++) {
+        const int f = u * kAoProd + (pid < 0 ? 0 : pid);
         gtt[u] = f >> 4;
         gd[u] = d0 + 4 * (f & 15);
     }
-    Kv4x4<BITS> ring[kAoP];
-    auto fetch = [&](int k, Kv4x4<BITS>& r) {
-        int t[4];
+    Kv4x4<BITS, kAoNG> ring[kAoP];
+    auto fetch = [&](int k, Kv4x4<BITS, kAoNG>& r) {
+        int t[kAoNG];
 #pragma unroll
-        for (int u = 0; u < 4; u++) t[u] = min(k * kAoCH + gtt[u], T - 1);
-        kv_raw4x4<BITS>(r, vd, vs, t, gd, kh, HD, n_kv);
+        for (int u = 0; u < kAoNG; u++) t[u] = min(k * kAoCH + gtt[u], T - 1);
+        kv_raw4x4<BITS, kAoNG>(r, vd, vs, t, gd, kh, HD, n_kv);
     };
-    auto produce = [&](int k, const Kv4x4<BITS>& r) {
-        float4* dst = (float4*)(pbuf + (k & 1) * kAoTile);
+    auto produce = [&](int k, const Kv4x4<BITS, kAoNG>& r) {
+        float4* dst = (float4*)(pbuf + (k % NB) * kAoTile);
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
+        for (int u = 0; u < kAoNG; u++) {
             const float at = es[min(k * kAoCH + gtt[u], T - 1)];
-            const float4 v = kv_deq4<BITS>(r, u);
-            dst[u * (kAoThreads - 64) + pid] = float4{at * v.x, at * v.y, at * v.z, at * v.w};
+            const float4 v = kv_deq4<BITS, kAoNG>(r, u);
+            dst[u * kAoProd + pid] = float4{at * v.x, at * v.y, at * v.z, at * v.w};
         }
     };
     if (wave > 0) {
@@ -577,40 +580,75 @@ __global__ __launch_bounds__(kAoThreads) void attn_out_exact(float* __restrict__
     lds_barrier();
 
     if (wave == 0) {
-        // consumer: lane d of the slice; chunk k lives in buffer k & 1 during step k
+        // consumer: lane d of the slice; chunk k lives in buffer k % NB
         float o = 0.f;
-        lds_barrier();                                    // chunk 0 produced
-        for (int k = 0; k < nsteps; k++) {
-            if (k < nch) {
-                const float* src = pbuf + (k & 1) * kAoTile + tid;
-                if (T - k * kAoCH >= kAoCH) {
-                    float v[kAoCH];
+        lds_barrier();                                    // chunks 0 .. NB-2 produced
+        if constexpr (NB == 2) {
+            for (int k = 0; k < nsteps; k++) {
+                if (k < nch) {
+                    const float* src = pbuf + (k & 1) * kAoTile + tid;
+                    if (T - k * kAoCH >= kAoCH) {
+                        float v[kAoCH];
 #pragma unroll
-                    for (int e = 0; e < kAoCH; e++) v[e] = src[e * kAoD];   // immediate LDS offsets
+                        for (int e = 0; e < kAoCH; e++) v[e] = src[e * kAoD];   // immediate LDS offsets
+#pragma unroll
+                        for (int e = 0; e < kAoCH; e++) o = o + v[e];
+                    } else {
+                        const int tn = T - k * kAoCH;
+                        for (int e = 0; e < tn; e++) o = o + src[e * kAoD];
+                    }
+                }
+                lds_barrier();
+            }
+        } else {
+            // chunk k+1 is read into registers while chunk k is added, so
+            // only the dependent adds are on this wave's path
+            float va[kAoCH], vb[kAoCH];
+            auto rd = [&](int k, float (&v)[kAoCH]) {
+                const float* src = pbuf + (k % NB) * kAoTile + tid;
+#pragma unroll
+                for (int e = 0; e < kAoCH; e++) v[e] = src[e * kAoD];
+            };
+            // full chunks add from registers; the last, partial one is read
+            // again from its buffer (untouched during its own step)
+            auto add = [&](int k, const float (&v)[kAoCH]) {
+                const int tn = T - k * kAoCH;
+                if (tn >= kAoCH) {
 #pragma unroll
                     for (int e = 0; e < kAoCH; e++) o = o + v[e];
-                } else {
-                    const int tn = T - k * kAoCH;
+                } else if (tn > 0) {
+                    const float* src = pbuf + (k % NB) * kAoTile + tid;
                     for (int e = 0; e < tn; e++) o = o + src[e * kAoD];
                 }
+            };
+            rd(0, va);
+            for (int k = 0; k < nsteps; k += 2) {
+                rd(k + 1, vb);
+                add(k, va);
+                lds_barrier();
+                rd(k + 2, va);
+                add(k + 1, vb);
+                lds_barrier();
             }
-            lds_barrier();
         }
         out[(size_t)h * HD + d0 + tid] = o;
         return;
     }
     // producers: branch-free; rows past T are clamped and their products land
     // in rows the consumer does not read.  Ring slot j holds the chunk whose
-    // index is j mod kAoP.
-    produce(0, ring[0]);
-    fetch(kAoP, ring[0]);
+    // index is j mod kAoP; step k produces chunk k + NB - 1.
+#pragma unroll
+    for (int p = 0; p < NB - 1; p++) {
+        produce(p, ring[p]);
+        fetch(kAoP + p, ring[p]);
+    }
     lds_barrier();
     for (int k0 = 0; k0 < nsteps; k0 += kAoP) {
 #pragma unroll
         for (int u = 0; u < kAoP; u++) {
             const int k = k0 + u;
-            produce(k + 1, ring[(u + 1) % kAoP]);
-            fetch(k + 1 + kAoP, ring[(u + 1) % kAoP]);
+            produce(k + NB - 1, ring[(u + NB - 1) % kAoP]);
+            fetch(k + NB - 1 + kAoP, ring[(u + NB - 1) % kAoP]);
             lds_barrier();
         }
     }
@@ -701,8 +739,12 @@ int ibh_launch_attn_exact(float* out, const float* q, const void* kdata, const v
     const uint8_t* K = (const uint8_t*)kdata;
     const uint8_t* V = (const uint8_t*)vdata;
     const int tcap = (max_pos + 1 + 3) & ~3;
-    const size_t lds = (size_t)(tcap + 2 * kAoTile) * sizeof(float);
-#define IBH_AO(B_, H_) attn_out_exact<B_, H_><<<n_heads * (H_ / kAoD), kAoThreads, lds, st>>>(out, att, V, vs, dpos, n_heads, n_kv, tstride, tcap)
+    const bool nb3 = (size_t)(tcap + 3 * kAoTile) * sizeof(float) <= 64 * 1024;
+    const size_t lds = (size_t)(tcap + (nb3 ? 3 : 2) * kAoTile) * sizeof(float);
+#define IBH_AO(B_, H_) do { \
+        if (nb3) attn_out_exact<B_, H_, 3><<<n_heads * (H_ / kAoD), kAoThreads, lds, st>>>(out, att, V, vs, dpos, n_heads, n_kv, tstride, tcap); \
+        else attn_out_exact<B_, H_, 2><<<n_heads * (H_ / kAoD), kAoThreads, lds, st>>>(out, att, V, vs, dpos, n_heads, n_kv, tstride, tcap); \
+    } while (0)
 #define IBH_AE(B_) do { \
         attn_scores_exact<B_><<<g1, 64, 0, st>>>(att, q, K, ks, dpos, n_heads, n_kv, hd, scale, tstride); \
         if (hd == 64) IBH_AO(B_, 64); else if (hd == 128) IBH_AO(B_, 128); else IBH_AO(B_, 256); \
