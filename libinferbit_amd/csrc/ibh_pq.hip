@@ -10,14 +10,15 @@
 //          + outlier terms,
 // T_side[c][k] = codebook_side[k] . x[inner columns of chunk c, that side].
 //
-// Kernel 1 (slab): block (row tile, chunk slab).  Every block finds the
-// global max|x| over the inner columns (chunk-skipping rule of
-// pq_decode.c:1569-1616: chunks whose max|x| is below 1% of it are left out),
-// builds the slab's tables in LDS (CS chunks x K entries x 2 sides, the
-// table entries in the reference's operation order), then each thread walks
-// its rows: CS index bytes per side from one 16-byte load, 2*CS LDS gathers.
-// The per-slab partial sums go to a workspace.
-// Kernel 2 (reduce): sums the slabs in order, applies the row scale and the
+// Kernel 1 (tables): block per chunk: its tables (K entries x 2 sides, in the
+// reference's operation order) and its max|x|, written once to a workspace.
+// Kernel 2 (gather): block (row tile, slab of CS chunks): the global max|x|
+// over the inner columns from the chunk maxima (chunk-skipping rule of
+// pq_decode.c:1569-1616: chunks whose max|x| is below 1% of it are left
+// out), the slab's tables into LDS, then each thread walks its rows: CS index
+// bytes per side from one 16-byte load, 2*CS LDS gathers.  The per-slab
+// partial sums go to the workspace.
+// Kernel 3 (reduce): sums the slabs in order, applies the row scale and the
 // outlier sidecar (the x86 rules of pq_decode.c:1233-1421: int8-quantised
 // dot for >= 32 outliers, fp32 otherwise).
 // The chunk sum is associated slab by slab instead of strictly serially, so
@@ -67,80 +68,41 @@ __device__ __forceinline__ float table_entry(const uint16_t* cb, const float* xv
     return s;
 }
 
+// Tables of one chunk, built once: T1[c][side][k] (and T2) written to global
+// memory with the chunk's max|x| (the skipping rule is applied by the
+// gather, which has every chunk's max).
 template <bool TWO>
-__global__ __launch_bounds__(kThreads) void pq_slab(PqDev t, const float* __restrict__ x,
-                                                    float* __restrict__ part, int CS) {
-    extern __shared__ __align__(16) float sm[];
-    __shared__ float red[kThreads / 64];
-    __shared__ int act_s[64];
-    const int K = t.K, K2 = t.K2, G = t.G, hf = G / 2, C = t.C;
-    float* T1 = sm;                                   // [CS][2][K]
-    float* T2 = T1 + (size_t)CS * 2 * K;              // [CS][2][K2]  (TWO)
-    float* xs = TWO ? T2 + (size_t)CS * 2 * K2 : T2;  // [CS][G]
-    const int c0 = blockIdx.y * CS;
-    const int cn = min(CS, C - c0);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int n_inner = t.N - t.n_outlier;
-
-    // global max |x| over the inner columns
-    float mx = 0.f;
-    for (int j = threadIdx.x; j < n_inner; j += kThreads) mx = fmaxf(mx, fabsf(x[inner_col(t, j)]));
-    mx = wave_max(mx);
-    if (lane == 0) red[wave] = mx;
-    // this slab's activations
-    for (int i = threadIdx.x; i < cn * G; i += kThreads) xs[i] = x[inner_col(t, c0 * G + i)];
+__global__ __launch_bounds__(kThreads) void pq_tables(PqDev t, const float* __restrict__ x, float* __restrict__ tab1,
+                                                      float* __restrict__ tab2, float* __restrict__ cmax) {
+    __shared__ float xs[64];
+    const int K = t.K, K2 = t.K2, G = t.G, hf = G / 2;
+    const int c = blockIdx.x;
+    if (threadIdx.x < G) xs[threadIdx.x] = x[inner_col(t, c * G + threadIdx.x)];
     __syncthreads();
-    float gmax = 0.f;
-    for (int w = 0; w < kThreads / 64; w++) gmax = fmaxf(gmax, red[w]);
-    const float th = gmax * 0.01f;
-    if (threadIdx.x < cn) {
+    if (threadIdx.x == 0) {
         float cm = 0.f;
-        for (int i = 0; i < G; i++) cm = fmaxf(cm, fabsf(xs[threadIdx.x * G + i]));
-        act_s[threadIdx.x] = gmax > 0.f ? (cm >= th) : 1;
+        for (int i = 0; i < G; i++) cm = fmaxf(cm, fabsf(xs[i]));
+        cmax[c] = cm;
     }
-    // tables
-    for (int e = threadIdx.x; e < cn * 2 * K; e += kThreads) {
-        const int c = e / (2 * K), side = (e / K) & 1, k = e % K;
+    for (int e = threadIdx.x; e < 2 * K; e += kThreads) {
+        const int side = e / K, k = e % K;
         const uint16_t* cb = (side ? t.cb1r : t.cb1l) + (size_t)k * hf;
-        T1[e] = table_entry(cb, xs + c * G + side * hf, hf);
+        tab1[(size_t)c * 2 * K + e] = table_entry(cb, xs + side * hf, hf);
     }
     if (TWO) {
-        for (int e = threadIdx.x; e < cn * 2 * K2; e += kThreads) {
-            const int c = e / (2 * K2), side = (e / K2) & 1, k = e % K2;
+        for (int e = threadIdx.x; e < 2 * K2; e += kThreads) {
+            const int side = e / K2, k = e % K2;
             const uint16_t* cb = (side ? t.cb2r : t.cb2l) + (size_t)k * hf;
-            T2[e] = table_entry(cb, xs + c * G + side * hf, hf);
+            tab2[(size_t)c * 2 * K2 + e] = table_entry(cb, xs + side * hf, hf);
         }
-    }
-    __syncthreads();
-
-    // gather: rows of this tile
-    const size_t l2s = TWO ? l2_stride(t) : 0;
-    for (int rr = threadIdx.x; rr < kRowsPerBlock; rr += kThreads) {
-        const int r = blockIdx.x * kRowsPerBlock + rr;
-        if (r >= t.M) break;
-        const uint8_t* il = t.i1l + (size_t)r * C + c0;
-        const uint8_t* ir = t.i1r + (size_t)r * C + c0;
-        const uint8_t* i2l = TWO ? t.i2l + (size_t)r * l2s : nullptr;
-        const uint8_t* i2r = TWO ? t.i2r + (size_t)r * l2s : nullptr;
-        float acc = 0.f;
-        for (int c = 0; c < cn; c++) {
-            if (!act_s[c]) continue;
-            const float* tc = T1 + (size_t)c * 2 * K;
-            acc = acc + (tc[il[c]] + tc[K + ir[c]]);
-            if (TWO) {
-                const float* t2 = T2 + (size_t)c * 2 * K2;
-                acc = acc + (t2[l2_at(t, i2l, c0 + c)] + t2[K2 + l2_at(t, i2r, c0 + c)]);
-            }
-        }
-        part[(size_t)blockIdx.y * t.M + r] = acc;
     }
 }
 
-__global__ __launch_bounds__(kThreads) void pq_reduce(PqDev t, const float* __restrict__ x,
-                                                      const float* __restrict__ part, int nslabs,
-                                                      float* __restrict__ out) {
-    __shared__ int8_t qq_s[1024];
-    __shared__ float meta_s;
+// Rows [r0, r1): the slab partials summed in slab order, the row scale, and
+// the outlier sidecar (the x86 rules of pq_decode.c:1233-1421: int8-quantised
+// dot for >= 32 outliers, fp32 otherwise).  Whole block.
+__device__ void finish_rows(const PqDev& t, const float* __restrict__ x, const float* __restrict__ part, int nslabs,
+                            float* __restrict__ out, int r0, int r1, int8_t* qq_s, float* meta_s) {
     const int no = t.n_outlier;
     const bool quant = no >= 32;
     if (quant) {
@@ -152,10 +114,10 @@ __global__ __launch_bounds__(kThreads) void pq_reduce(PqDev t, const float* __re
                 const float a = v < 0 ? -v : v;
                 if (a > mx) mx = a;
             }
-            meta_s = mx > 0.f ? mx / 127.0f : 1.0f;
+            *meta_s = mx > 0.f ? mx / 127.0f : 1.0f;
         }
         __syncthreads();
-        const float inv = 1.0f / meta_s;
+        const float inv = 1.0f / *meta_s;
         for (int j = threadIdx.x; j < no; j += kThreads) {
             const float sv = (x[t.ocols[j]] * f16_to_f32(t.oscale[j])) * inv;
             const int v = (int)(sv >= 0 ? sv + 0.5f : sv - 0.5f);
@@ -163,23 +125,125 @@ __global__ __launch_bounds__(kThreads) void pq_reduce(PqDev t, const float* __re
         }
         __syncthreads();
     }
-    const int r = blockIdx.x * kThreads + threadIdx.x;
-    if (r >= t.M) return;
-    float acc = 0.f;
-    for (int s = 0; s < nslabs; s++) acc += part[(size_t)s * t.M + r];
-    float y = acc * f16_to_f32(t.row_scale[r]);
-    if (no > 0) {
-        const int8_t* side = t.oside + (size_t)r * no;
-        if (quant) {
-            int32_t sum = 0;
-            for (int j = 0; j < no; j++) sum += (int32_t)side[j] * (int32_t)qq_s[j];
-            y = fmaf((float)sum, meta_s, y);
+    for (int r = r0 + (int)threadIdx.x; r < r1; r += kThreads) {
+        float acc = 0.f;
+        int s = 0;
+        for (; s + 16 <= nslabs; s += 16) {
+            float v[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) v[u] = part[(size_t)(s + u) * t.M + r];
+#pragma unroll
+            for (int u = 0; u < 16; u++) acc += v[u];
+        }
+        for (; s < nslabs; s++) acc += part[(size_t)s * t.M + r];
+        float y = acc * f16_to_f32(t.row_scale[r]);
+        if (no > 0) {
+            const int8_t* side = t.oside + (size_t)r * no;
+            if (quant) {
+                int32_t sum = 0;
+                for (int j = 0; j < no; j++) sum += (int32_t)side[j] * (int32_t)qq_s[j];
+                y = fmaf((float)sum, *meta_s, y);
+            } else {
+                for (int j = 0; j < no; j++)
+                    y = fmaf((float)side[j] * f16_to_f32(t.oscale[j]), x[t.ocols[j]], y);
+            }
+        }
+        out[r] = y;
+    }
+}
+
+// Block (row tile, slab): the slab's tables into LDS, then each thread walks
+// its rows (CS index bytes per side from one 16-byte load, 2 CS gathers).
+template <bool TWO>
+__global__ __launch_bounds__(kThreads) void pq_gather(PqDev t, const float* __restrict__ tab1,
+                                                      const float* __restrict__ tab2, const float* __restrict__ cmax,
+                                                      float* __restrict__ part, int CS) {
+    extern __shared__ __align__(16) float sm[];
+    __shared__ float red[kThreads / 64];
+    __shared__ int act_s[64];
+    const int K = t.K, K2 = t.K2, C = t.C;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float* T1 = sm;                                   // [CS][2][K]
+    float* T2 = T1 + (size_t)CS * 2 * K;              // [CS][2][K2]  (TWO)
+    const int c0 = blockIdx.y * CS;
+    const int cn = min(CS, C - c0);
+    {
+        const int n1 = cn * 2 * K, n2 = TWO ? cn * 2 * K2 : 0;
+        const float* g1 = tab1 + (size_t)c0 * 2 * K;
+        const float* g2 = TWO ? tab2 + (size_t)c0 * 2 * K2 : nullptr;
+        if ((n1 & 3) == 0 && (n2 & 3) == 0 && (((uintptr_t)g1 | (uintptr_t)g2) & 15) == 0) {
+            for (int i = threadIdx.x; i < n1 / 4; i += kThreads) ((float4*)T1)[i] = ((const float4*)g1)[i];
+            for (int i = threadIdx.x; i < n2 / 4; i += kThreads) ((float4*)T2)[i] = ((const float4*)g2)[i];
         } else {
-            for (int j = 0; j < no; j++)
-                y = fmaf((float)side[j] * f16_to_f32(t.oscale[j]), x[t.ocols[j]], y);
+            for (int i = threadIdx.x; i < n1; i += kThreads) T1[i] = g1[i];
+            for (int i = threadIdx.x; i < n2; i += kThreads) T2[i] = g2[i];
         }
     }
-    out[r] = y;
+    // chunk-skipping rule (pq_decode.c:1569-1616): the global max|x| over the
+    // inner columns is the max of the chunk maxima
+    float mx = 0.f;
+    for (int c0_ = 0; c0_ < C; c0_ += 4 * kThreads) {
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = cmax[min(c0_ + u * kThreads + (int)threadIdx.x, C - 1)];
+#pragma unroll
+        for (int u = 0; u < 4; u++) mx = fmaxf(mx, v[u]);
+    }
+    mx = wave_max(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    float gmax = 0.f;
+    for (int w = 0; w < kThreads / 64; w++) gmax = fmaxf(gmax, red[w]);
+    if (threadIdx.x < cn) act_s[threadIdx.x] = gmax > 0.f ? (cmax[c0 + threadIdx.x] >= gmax * 0.01f) : 1;
+    __syncthreads();
+
+    const size_t l2s = TWO ? l2_stride(t) : 0;
+    for (int rr = threadIdx.x; rr < kRowsPerBlock; rr += kThreads) {
+        const int r = blockIdx.x * kRowsPerBlock + rr;
+        if (r >= t.M) break;
+        const uint8_t* il = t.i1l + (size_t)r * C + c0;
+        const uint8_t* ir = t.i1r + (size_t)r * C + c0;
+        const uint8_t* i2l = TWO ? t.i2l + (size_t)r * l2s : nullptr;
+        const uint8_t* i2r = TWO ? t.i2r + (size_t)r * l2s : nullptr;
+        float acc = 0.f;
+        if (cn == 16 && (((uintptr_t)il | (uintptr_t)ir) & 15) == 0) {
+            // a full slab: both index rows in one 16-byte load each
+            const uint4 a4 = *(const uint4*)il, b4 = *(const uint4*)ir;
+            const uint32_t aw[4] = {a4.x, a4.y, a4.z, a4.w}, bw[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+            for (int c = 0; c < 16; c++) {
+                if (!act_s[c]) continue;
+                const float* tc = T1 + (size_t)c * 2 * K;
+                const int a = (aw[c >> 2] >> (8 * (c & 3))) & 0xff, b = (bw[c >> 2] >> (8 * (c & 3))) & 0xff;
+                acc = acc + (tc[a] + tc[K + b]);
+                if (TWO) {
+                    const float* t2 = T2 + (size_t)c * 2 * K2;
+                    acc = acc + (t2[l2_at(t, i2l, c0 + c)] + t2[K2 + l2_at(t, i2r, c0 + c)]);
+                }
+            }
+        } else {
+            for (int c = 0; c < cn; c++) {
+                if (!act_s[c]) continue;
+                const float* tc = T1 + (size_t)c * 2 * K;
+                acc = acc + (tc[il[c]] + tc[K + ir[c]]);
+                if (TWO) {
+                    const float* t2 = T2 + (size_t)c * 2 * K2;
+                    acc = acc + (t2[l2_at(t, i2l, c0 + c)] + t2[K2 + l2_at(t, i2r, c0 + c)]);
+                }
+            }
+        }
+        part[(size_t)blockIdx.y * t.M + r] = acc;
+    }
+}
+
+// Kernel 3: block per 256 rows.
+__global__ __launch_bounds__(kThreads) void pq_reduce(PqDev t, const float* __restrict__ x,
+                                                      const float* __restrict__ part, int nslabs,
+                                                      float* __restrict__ out) {
+    __shared__ int8_t qq_s[1024];
+    __shared__ float meta_s;
+    finish_rows(t, x, part, nslabs, out, blockIdx.x * kThreads, min(t.M, (int)(blockIdx.x + 1) * kThreads), qq_s,
+                &meta_s);
 }
 
 }  // namespace
@@ -188,29 +252,36 @@ void* ibh_workspace(size_t bytes);
 
 typedef ibh_pq_tensor ibh_pq_tensor_abi;
 
-static int pq_geometry(const ibh_pq_tensor_abi* t, int* CS, int* nslabs, size_t* lds, size_t* ws_need) {
+// Slab of CS chunks per table / gather block; workspace = both levels' tables
+// for all chunks, then the per-slab partial sums.
+static int pq_geometry(const ibh_pq_tensor_abi* t, int* CS, int* nslabs, size_t* lds, size_t* ws_need,
+                       size_t* tab1_off, size_t* tab2_off, size_t* part_off) {
     const bool two = t->n_levels == 2;
     const int K2 = t->K_l2 > 0 ? t->K_l2 : t->K;
     int cs = 16;
-    auto need = [&](int c) { return (size_t)c * 2 * t->K * 4 + (two ? (size_t)c * 2 * K2 * 4 : 0) + (size_t)c * t->G * 4; };
+    auto need = [&](int c) { return (size_t)c * 2 * t->K * 4 + (two ? (size_t)c * 2 * K2 * 4 : 0); };
     while (cs > 1 && need(cs) > 60 * 1024) cs >>= 1;
     if (need(cs) > 60 * 1024) return IBH_ERROR_PARAM;
     *CS = cs;
     *nslabs = (t->C + cs - 1) / cs;
     *lds = need(cs);
-    *ws_need = (size_t)(*nslabs) * t->M * sizeof(float);
+    auto al = [](size_t v) { return (v + 255) / 256 * 256; };
+    *tab1_off = 0;
+    *tab2_off = al((size_t)t->C * 2 * t->K * 4);
+    *part_off = *tab2_off + (two ? al((size_t)t->C * 2 * K2 * 4) : 0);
+    *ws_need = *part_off + al((size_t)(*nslabs) * t->M * sizeof(float)) + (size_t)t->C * sizeof(float);
     return IBH_OK;
 }
 
 extern "C" size_t ibh_pq_workspace_bytes(const ibh_pq_tensor_abi* t) {
     int cs, ns;
-    size_t lds, need;
-    return t && pq_geometry(t, &cs, &ns, &lds, &need) == IBH_OK ? need : 0;
+    size_t lds, need, o1, o2, o3;
+    return t && pq_geometry(t, &cs, &ns, &lds, &need, &o1, &o2, &o3) == IBH_OK ? need : 0;
 }
 
 extern "C" int ibh_pq_matmul(const ibh_pq_tensor_abi* t, const float* x, float* out, void* ws, size_t ws_bytes,
                              void* stream) {
-    if (!t || !x || !out || t->M <= 0 || t->C <= 0 || t->G <= 0 || t->G % 2 || t->K <= 0 || t->K > 65536 ||
+    if (!t || !x || !out || t->M <= 0 || t->C <= 0 || t->G <= 0 || t->G % 2 || t->G > 64 || t->K <= 0 || t->K > 65536 ||
         !t->codebook_l1_l || !t->codebook_l1_r || !t->indices_l1_l || !t->indices_l1_r || !t->row_scale ||
         t->N != t->C * t->G + t->n_outlier || t->n_outlier < 0 || t->n_outlier > 1024 ||
         (t->n_outlier > 0 && (!t->outlier_cols || !t->outlier_sidecar || !t->outlier_scale || !t->inner_cols)) ||
@@ -225,8 +296,8 @@ extern "C" int ibh_pq_matmul(const ibh_pq_tensor_abi* t, const float* x, float* 
         return IBH_ERROR_PARAM;
     }
     int CS, nslabs;
-    size_t lds, need;
-    if (pq_geometry(t, &CS, &nslabs, &lds, &need) != IBH_OK) {
+    size_t lds, need, tab1_off, tab2_off, part_off;
+    if (pq_geometry(t, &CS, &nslabs, &lds, &need, &tab1_off, &tab2_off, &part_off) != IBH_OK) {
         ibh_set_error("ibh_pq_matmul: codebooks too large for the LDS tables");
         return IBH_ERROR_PARAM;
     }
@@ -247,11 +318,18 @@ extern "C" int ibh_pq_matmul(const ibh_pq_tensor_abi* t, const float* x, float* 
     d.row_scale = t->row_scale; d.ocols = t->outlier_cols; d.oside = t->outlier_sidecar;
     d.oscale = t->outlier_scale; d.inner = t->n_outlier > 0 ? t->inner_cols : nullptr;
     hipStream_t st = ibh_resolve_stream(stream);
-    float* part = (float*)ws;
+    float* tab1 = (float*)((char*)ws + tab1_off);
+    float* tab2 = (float*)((char*)ws + tab2_off);
+    float* part = (float*)((char*)ws + part_off);
+    const size_t cmax_off = part_off + ((size_t)nslabs * t->M * sizeof(float) + 255) / 256 * 256;
+    float* cmax = (float*)((char*)ws + cmax_off);
+    if (t->n_levels == 2) pq_tables<true><<<t->C, kThreads, 0, st>>>(d, x, tab1, tab2, cmax);
+    else pq_tables<false><<<t->C, kThreads, 0, st>>>(d, x, tab1, tab2, cmax);
+    IBH_CHECK_LAUNCH("ibh_pq_matmul (tables)");
     dim3 grid((t->M + kRowsPerBlock - 1) / kRowsPerBlock, nslabs);
-    if (t->n_levels == 2) pq_slab<true><<<grid, kThreads, lds, st>>>(d, x, part, CS);
-    else pq_slab<false><<<grid, kThreads, lds, st>>>(d, x, part, CS);
-    IBH_CHECK_LAUNCH("ibh_pq_matmul (slab)");
+    if (t->n_levels == 2) pq_gather<true><<<grid, kThreads, lds, st>>>(d, tab1, tab2, cmax, part, CS);
+    else pq_gather<false><<<grid, kThreads, lds, st>>>(d, tab1, tab2, cmax, part, CS);
+    IBH_CHECK_LAUNCH("ibh_pq_matmul (gather)");
     pq_reduce<<<(t->M + kThreads - 1) / kThreads, kThreads, 0, st>>>(d, x, part, nslabs, out);
     IBH_CHECK_LAUNCH("ibh_pq_matmul (reduce)");
     return IBH_OK;
