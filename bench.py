@@ -40,7 +40,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--quick", action="store_true", help="headline only (for profiling runs)")
     p.add_argument("--no-decode", action="store_true", help="skip the end-to-end decode legs")
-    p.add_argument("--only", choices=["headline", "gemm", "pq", "decode-tinyllama", "decode-mistral"],
+    p.add_argument("--only", choices=["headline", "gemm", "pq", "int4g", "decode-tinyllama", "decode-mistral"],
                    help="run one case and print its JSON (for profiler runs)")
     p.add_argument("--calib-copy", action="store_true",
                    help="first copy a 64 MiB buffer 8 times (the known-size kernel that scales the "
@@ -179,6 +179,26 @@ def pq_case(torch, L, steps, warmup):
     nbytes = 2 * M * Cc + 2 * 2 * K * (G // 2) + 2 * M + 4 * t["N"] + 4 * M
     return {"M": M, "N": t["N"], "G": G, "K": K, "us": round(tm * 1e6, 3), "bytes": nbytes,
             "GBps": round(nbytes / tm / 1e9, 1)}
+
+
+def int4g_case(torch, L, M, N, G, K_out, steps, warmup, awq=True):
+    """IBF v5 INT4 group-scale matvec (ib_pq_session_matmul's INT4 backend,
+    ibh_int4g_matmul) with AWQ inv_act and K_out fp16 outliers per row.
+    Bytes = packed nibbles + fp16 group scales + outlier index/value pairs +
+    x + inv_act + y."""
+    sys.path.insert(0, os.path.join(ROOT, "tests", "golden"))
+    from gen_golden import make_int4g
+    t = make_int4g(np.random.default_rng(12), M, N, G, int(awq), K_out)
+    devs = [L.ops.Int4gDeviceTensor(t) for _ in range(COPIES)]
+    x = torch.randn(N, generator=torch.Generator().manual_seed(4)).cuda()
+    y = torch.empty(M, device="cuda")
+
+    def launch(i):
+        devs[i % COPIES].matmul(x, y)
+    tm = time_launches(torch, launch, steps, warmup)
+    nbytes = M * N // 2 + 2 * M * (N // G) + 4 * M * K_out + (8 if awq else 4) * N + 4 * M
+    return {"M": M, "N": N, "G": G, "K_out": K_out, "awq": awq, "us": round(tm * 1e6, 3), "bytes": nbytes,
+            "GBps": round(nbytes / tm / 1e9, 1), "frac_hbm": round(nbytes / tm / 1e9 / HBM_PEAK_GBS, 4)}
 
 
 def prefill_gemm_case(torch, L, steps, warmup):
@@ -329,6 +349,11 @@ def main():
             r = prefill_gemm_case(torch, L, 64, 8)
         elif a.only == "pq":
             r = pq_case(torch, L, max(200, a.steps // 4), 20)
+        elif a.only == "int4g":
+            r = {"14336x4096": int4g_case(torch, L, 14336, 4096, 128, 8, a.steps, a.warmup),
+                 "4096x14336": int4g_case(torch, L, 4096, 14336, 128, 28, a.steps, a.warmup),
+                 "14336x4096_plain": int4g_case(torch, L, 14336, 4096, 128, 0, a.steps, a.warmup, awq=False),
+                 "4096x14336_plain": int4g_case(torch, L, 4096, 14336, 128, 0, a.steps, a.warmup, awq=False)}
         else:
             r = decode_case(a.only.split("-", 1)[1], 128, cpu=False)
         print(json.dumps({"only": a.only, "result": r}), flush=True)
@@ -353,6 +378,9 @@ def main():
         extra["prefill_gemm_int8_512x4096x14336"] = prefill_gemm_case(torch, L, 64, 8)
         print("bench: pq_4096x14336", file=sys.stderr, flush=True)
         extra["pq_4096x14336_G16_K256"] = pq_case(torch, L, max(200, a.steps // 4), 20)
+        print("bench: int4g (IBF v5 INT4 group-scale)", file=sys.stderr, flush=True)
+        extra["int4g_14336x4096_G128_awq_out8"] = int4g_case(torch, L, 14336, 4096, 128, 8, a.steps, a.warmup)
+        extra["int4g_4096x14336_G128_awq_out28"] = int4g_case(torch, L, 4096, 14336, 128, 28, a.steps, a.warmup)
     decode = {}
     if not a.no_decode and not a.quick:
         for name in ("tinyllama", "mistral"):

@@ -163,6 +163,40 @@ size_t ibh_pq_workspace_bytes(const ibh_pq_tensor* t);
 int    ibh_pq_matmul(const ibh_pq_tensor* t, const float* x, float* out, void* ws,
                      size_t ws_bytes, void* stream);
 
+/* ── IBF v5 INT4 group-scale matvec, device pointers ───────── */
+
+/* Device-resident mirror of the PQ session's INT4 tensor (struct
+ * ib_int4_tensor, src/pq_decode.c:3474-3482, detected from the raw tensors
+ * <base>__i4_q / __i4_s / __act_scale / __i4_outl_idx / __i4_outl_val at
+ * src/pq_decode.c:4193-4276), without the name.  q [M][N/2]: column 2k is
+ * the low nibble of byte k, 2k+1 the high one, value nibble - 8; s [M][N/G]
+ * fp16 group scales; inv_act [N] fp32 or NULL; outl_idx / outl_val
+ * [M][K_out] (uint16 column, fp16 value) or NULL with K_out = 0. */
+typedef struct {
+    const uint8_t* q;
+    const uint16_t* s;
+    const float* inv_act;
+    const uint16_t* outl_idx;
+    const uint16_t* outl_val;
+    int M, N, G, K_out;
+} ibh_int4g_tensor;
+
+/* out[M] = W xk, xk = x * inv_act: the INT4 branch of ib_pq_session_matmul
+ * (src/pq_decode.c:4442-4452 -> int4_matmul_fp32_threaded 3905-3953 ->
+ * int4_matmul_rows_skip 3565-3644).  act_sparse_rel is the value the
+ * reference reads from IB_ACT_SPARSE_REL (build_skip_mask 3856-3882):
+ * <= 0 off (the reference's default); > 0 leaves out the groups with
+ * max|xk| <= act_sparse_rel * max|xk|.  G even, N % G == 0.  fp32 sums in a
+ * different order than the CPU's.  `ws` (>= ibh_int4g_workspace_bytes(t),
+ * only used when act_sparse_rel > 0) NULL = library workspace. */
+size_t ibh_int4g_workspace_bytes(const ibh_int4g_tensor* t);
+int    ibh_int4g_matmul(const ibh_int4g_tensor* t, const float* x, float* out, float act_sparse_rel, void* ws,
+                        size_t ws_bytes, void* stream);
+/* ib_pq_session_matmul_batched for an INT4 tensor (src/pq_decode.c:
+ * 4501-4539; the x86 build runs B single calls): x [B][N], out [B][M]. */
+int    ibh_int4g_matmul_batched(const ibh_int4g_tensor* t, int B, const float* x, float* out, float act_sparse_rel,
+                                void* ws, size_t ws_bytes, void* stream);
+
 /* ── device-resident decode (forward_single_ex + greedy generate) ── */
 
 /* Opaque model: an IBF v1 file (src/ibf_loader.c:300-546) whose weight region

@@ -37,6 +37,9 @@ SIGNATURES = {
     "ibh_attn_decode": (I, [P, P, P, P, P, P, I, I, I, I, I, P, SZ, P]),
     "ibh_pq_workspace_bytes": (SZ, [P]),
     "ibh_pq_matmul": (I, [P, P, P, P, SZ, P]),
+    "ibh_int4g_workspace_bytes": (SZ, [P]),
+    "ibh_int4g_matmul": (I, [P, P, P, C.c_float, P, SZ, P]),
+    "ibh_int4g_matmul_batched": (I, [P, I, P, P, C.c_float, P, SZ, P]),
     "ibh_model_load": (I, [C.c_char_p, I, P]),
     "ibh_model_free": (None, [P]),
     "ibh_model_dims": (I, [P, P]),
@@ -102,3 +105,9 @@ class PqTensor(C.Structure):
                [(n, P) for n in ("codebook_l1_l", "codebook_l1_r", "codebook_l2_l", "codebook_l2_r",
                                  "indices_l1_l", "indices_l1_r", "indices_l2_l", "indices_l2_r", "row_scale",
                                  "outlier_cols", "outlier_sidecar", "outlier_scale", "inner_cols")]
+
+
+class Int4gTensor(C.Structure):
+    """ibh_int4g_tensor (include/ibhip.h)."""
+    _fields_ = [(n, P) for n in ("q", "s", "inv_act", "outl_idx", "outl_val")] + \
+               [(n, I) for n in ("M", "N", "G", "K_out")]

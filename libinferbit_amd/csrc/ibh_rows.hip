@@ -291,14 +291,17 @@ __global__ __launch_bounds__(256) void gemv_rows_w4a8_k(const RowSet rs, const i
 // Digit bytes of 4 consecutive columns c..c+3 (c % 4 == 0) of x go to the
 // B operand slots as: int8 one dword; int4 two 16-bit pairs (columns c, c+2
 // are k-slots b, b+1 of one dword, columns c+1, c+3 of the next).
-template <int BITS>
+// GROUPED: the weight segments were loaded in the "group" lane order, so
+// segment seg's operand goes to the slot of lane seg/4 + 16*(seg%4).
+template <int BITS, bool GROUPED = false>
 __device__ __forceinline__ void put_digits(unsigned char* dig, int c, const uint32_t p0, const uint32_t p1,
                                            const uint32_t p2) {
     constexpr int SEGC = RGeo<BITS>::kSegCols;
     constexpr int NA = RGeo<BITS>::kNA;
     const int s = c >> (BITS == 8 ? 10 : 11);             // 1 KiB step
     const int cc = c & (64 * SEGC - 1);
-    const int seg = cc / SEGC, cs = cc % SEGC;
+    const int sg = cc / SEGC, cs = cc % SEGC;
+    const int seg = GROUPED ? (sg >> 2) + 16 * (sg & 3) : sg;
     const uint32_t pl[3] = {p0, p1, p2};
     if constexpr (BITS == 8) {
 #pragma unroll
@@ -457,6 +460,233 @@ __global__ __launch_bounds__(1024) void gemv_rows_x(const RowSet rs, const float
     }
 }
 
+
+// ── group-scaled INT4 rows, fp32 activations (IBF v5 __i4_q / __i4_s) ─────
+// y[m] = sum_g scale[m][g] * sum_{j in g} (nibble - 8) * xk[j]  (+ outliers),
+// xk = x * inv_act when AWQ.  G % 128 == 0: with the "group" lane order D[i][i]
+// of one step is the 128-column block i of that step, which lies inside one
+// scale group, so each step's three digit-plane sums are combined in fp32 and
+// multiplied by their group scale before the next step accumulates.  Rows are
+// whole 16-byte segments (N % 32 == 0); a step past the row end loads zeros.
+template <int NXQ, bool AWQ>
+__global__ __launch_bounds__(1024) void gemv_rows_grp(const uint8_t* __restrict__ W, const uint16_t* __restrict__ sg,
+                                                      const float* __restrict__ x, const float* __restrict__ ia,
+                                                      const float* __restrict__ xo, const uint16_t* __restrict__ oi,
+                                                      const uint16_t* __restrict__ ov, float* __restrict__ y, int M,
+                                                      int N, int G, int K_out, int S, int WR, int KW) {
+    constexpr int R = 4, SPW = 2, NA = 2;
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ float red[kMaxWaves];
+    __shared__ float part[kMaxWaves][R];
+    __shared__ float opart[kMaxWaves][R];
+    uint4* dig = (uint4*)smem;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wr = wave / KW, wk = wave - wr * KW;
+    const int RB = WR * R;
+    const int row0 = blockIdx.x * RB + wr * R;
+    const int rb = N >> 1;
+    const int ng = N / G, gq = G >> 7;
+    const int nth = blockDim.x;
+    const int segl = seg_of<true>(lane);
+
+    // Every load before the weight loads is unconditional (clamped address)
+    // and consumed only after the weight loads are issued, so no wait for
+    // it lands ahead of them.
+    // 1. x and inv_act, coalesced float4 slices
+    // (AWQ is instantiated for NXQ <= 4 only: eight inv_act slices spill)
+    static_assert(!AWQ || NXQ <= 4, "AWQ with NXQ > 4");
+    float4 xv[NXQ], av[AWQ ? NXQ : 1];
+#pragma unroll
+    for (int q = 0; q < NXQ; q++) {
+        const int c = min(4 * ((int)threadIdx.x + q * nth), N - 4);
+        xv[q] = *(const float4*)(x + c);
+        if constexpr (AWQ) av[q] = *(const float4*)(ia + c);
+    }
+    // 1b. outlier sidecar of the wavefront's rows (waves of K-slice 0): up to
+    // 128 (row, k) pairs, two per lane; index and value now, x after the
+    // weight loads are issued.
+    const bool osc = wk == 0 && K_out > 0 && R * K_out <= 128;
+    int ojx[2] = {0, 0}, orr[2] = {-1, -1};
+    uint32_t ovh[2] = {0u, 0u};   // 32-bit: no packing (and no wait) at the branch join
+    if (osc) {
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int idx = min(lane + 64 * u, R * K_out - 1);
+            const int r = idx / K_out;
+            const size_t e = (size_t)min(row0 + r, M - 1) * K_out + (idx - r * K_out);
+            ojx[u] = oi[e];
+            ovh[u] = ov[e];
+            orr[u] = lane + 64 * u < R * K_out ? r : -1;
+        }
+    }
+    // 2. weights (value 0 past the row end) and the diagonal lanes' group scales
+    uint4 wv[SPW][R];
+    float scv[SPW][R];
+#pragma unroll
+    for (int j = 0; j < SPW; j++) {
+        const int s = min(wk * SPW + j, S - 1);
+        const int off = s * 1024 + 16 * segl;
+        const bool ok = off < rb;
+        const int offc = min(off, rb - 16);
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint4 v = ld_stream16(W + (size_t)min(row0 + r, M - 1) * rb + offc);
+            wv[j][r] = ok ? v : make_uint4(0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u);   // nibble 8 = 0
+        }
+        const int g = min((16 * s + (lane & 15)) / gq, ng - 1);
+#pragma unroll
+        for (int r = 0; r < R; r++) scv[j][r] = f16_to_f32(sg[(size_t)min(row0 + r, M - 1) * ng + g]);
+    }
+    // the x values the outliers read (used after the contraction)
+    float oxv[2] = {0.f, 0.f}, oav[2] = {1.f, 1.f};
+    if (osc) {
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            oxv[u] = xo[ojx[u]];
+            if (ia) oav[u] = ia[ojx[u]];
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < NXQ; q++) {
+        const int c = 4 * ((int)threadIdx.x + q * nth);
+        if constexpr (AWQ) {
+            xv[q].x *= av[q].x; xv[q].y *= av[q].y; xv[q].z *= av[q].z; xv[q].w *= av[q].w;
+        }
+        if (c >= N) xv[q] = float4{0.f, 0.f, 0.f, 0.f};
+    }
+    // 3. max|xk|
+    float mx = 0.f;
+#pragma unroll
+    for (int q = 0; q < NXQ; q++)
+        mx = fmaxf(fmaxf(mx, fmaxf(fabsf(xv[q].x), fabsf(xv[q].y))), fmaxf(fabsf(xv[q].z), fabsf(xv[q].w)));
+    mx = wave_max(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    float gm = 0.f;
+    for (int w = 0; w < (nth >> 6); w++) gm = fmaxf(gm, red[w]);
+    const float xs = gm > 0.f ? gm / 127.0f : 1.0f;
+    const float inv = 1.0f / xs;
+    // 4. digit planes -> LDS, in the slots of the group lane order
+#pragma unroll
+    for (int q = 0; q < NXQ; q++) {
+        const int c = 4 * ((int)threadIdx.x + q * nth);
+        if (c < N) {
+            const float vv[4] = {xv[q].x, xv[q].y, xv[q].z, xv[q].w};
+            uint32_t p0 = 0, p1 = 0, p2 = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float v = vv[e] * inv;
+                const float k0 = __builtin_rintf(v);
+                const float r1 = (v - k0) * 128.f;
+                const float k1 = __builtin_rintf(r1);
+                const float k2 = __builtin_rintf((r1 - k1) * 128.f);
+                p0 |= digit_byte(k0) << (8 * e);
+                p1 |= digit_byte(k1) << (8 * e);
+                p2 |= digit_byte(k2) << (8 * e);
+            }
+            put_digits<4, true>((unsigned char*)dig, c, p0, p1, p2);
+        }
+    }
+    __syncthreads();
+
+    // 5. per step: exact int32 block sums, then one scaled fp32 term per block
+    const i4_t zero4 = {0, 0, 0, 0};
+    const bool diag = is_diag(lane);
+    float f[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) f[r] = 0.f;
+#pragma unroll
+    for (int j = 0; j < SPW; j++) {
+        const int s = wk * SPW + j;
+        if (s < S) {
+            i4_t b[NA][3];
+#pragma unroll
+            for (int a = 0; a < NA; a++)
+#pragma unroll
+                for (int p = 0; p < 3; p++) b[a][p] = __builtin_bit_cast(i4_t, dig[((s * NA + a) * 3 + p) * 64 + lane]);
+            // two rows at a time: six independent accumulation chains
+#pragma unroll
+            for (int r0 = 0; r0 < R; r0 += 2) {
+                i4_t acc[2][3];
+#pragma unroll
+                for (int h = 0; h < 2; h++)
+#pragma unroll
+                    for (int p = 0; p < 3; p++) acc[h][p] = zero4;
+#pragma unroll
+                for (int a = 0; a < NA; a++)
+#pragma unroll
+                    for (int h = 0; h < 2; h++) {
+                        const i4_t av = a_operand<4>(wv[j][r0 + h], a);
+#pragma unroll
+                        for (int p = 0; p < 3; p++)
+                            acc[h][p] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b[a][p], acc[h][p], 0, 0, 0);
+                    }
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const float v = (float)diag_val(acc[h][0], lane) + (float)diag_val(acc[h][1], lane) * (1.f / 128.f) +
+                                    (float)diag_val(acc[h][2], lane) * (1.f / 16384.f);
+                    f[r0 + h] = diag ? fmaf(v, scv[j][r0 + h], f[r0 + h]) : 0.f;
+                }
+            }
+        }
+    }
+
+    // 6. combine; the outlier sum of each row (sum_k val_k * xk[idx_k]) is
+    // added last.  Rows with more than 128 / R outliers loop here instead.
+    float tot[R], osum[R], oprod[2];
+#pragma unroll
+    for (int u = 0; u < 2; u++)
+        oprod[u] = orr[u] >= 0 ? f16_to_f32((uint16_t)ovh[u]) * (ia ? oxv[u] * oav[u] : oxv[u]) : 0.f;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        tot[r] = diag_sum(f[r]);
+        osum[r] = osc ? wave_sum((orr[0] == r ? oprod[0] : 0.f) + (orr[1] == r ? oprod[1] : 0.f)) : 0.f;
+    }
+    const float fin = xs * (1.f / 16.f);
+    auto finish = [&](int row, float v, float o) {
+        float acc = v * fin;
+        if (R * K_out > 128) {
+            for (int k = 0; k < K_out; k++) {
+                const int jj = oi[(size_t)row * K_out + k];
+                acc = fmaf(f16_to_f32(ov[(size_t)row * K_out + k]), ia ? xo[jj] * ia[jj] : xo[jj], acc);
+            }
+        } else {
+            acc += o;
+        }
+        y[row] = acc;
+    };
+    if (KW == 1) {
+        if (lane < R && row0 + lane < M) {
+            float v = tot[0], o = osum[0];
+#pragma unroll
+            for (int r = 1; r < R; r++) {
+                v = lane == r ? tot[r] : v;
+                o = lane == r ? osum[r] : o;
+            }
+            finish(row0 + lane, v, o);
+        }
+    } else {
+        if (lane == 0) {
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                part[wave][r] = tot[r];
+                if (wk == 0) opart[wr][r] = osum[r];
+            }
+        }
+        __syncthreads();
+        const int t = threadIdx.x;
+        if (t < RB) {
+            const int w_r = t / R, r = t - w_r * R;
+            const int row = blockIdx.x * RB + t;
+            if (row < M) {
+                float v = 0.f;
+                for (int k = 0; k < KW; k++) v += part[w_r * KW + k][r];
+                finish(row, v, opart[w_r][r]);
+            }
+        }
+    }
+}
 }  // namespace
 
 // W4A8, batch 1, for 1-3 matrices of N = 2048 or 4096 columns sharing qx
@@ -550,4 +780,40 @@ int ibh_launch_rows_x(float* out, const void* w, const void* scales, int kind, c
                       int bits, hipStream_t st) {
     const MatDesc d{out, w, scales, M};
     return ibh_launch_rows_x_multi(&d, 1, kind, x, N, bits, st);
+}
+
+// Group-scaled INT4 rows (gemv_rows_grp).  x: the activation to digitise
+// (inv_act applied in-kernel when awq); xo/ia: what the outlier sidecar reads
+// (xk[j] = xo[j] * ia[j], or xo[j] when ia is NULL).  Returns 1 if launched,
+// 0 if the shape is not eligible.
+int ibh_launch_rows_grp(float* out, const uint8_t* q, const uint16_t* s, const float* x, bool awq, const float* xo,
+                        const float* ia, const uint16_t* oi, const uint16_t* ov, int M, int N, int G, int K_out,
+                        hipStream_t st) {
+    if (N % 32 != 0 || G % 128 != 0 || N % G != 0 || N > 131072 || ((uintptr_t)q & 15) || ((uintptr_t)x & 15) ||
+        (awq && ((uintptr_t)ia & 15)) || M <= 0)
+        return 0;
+    const int rb = N / 2;
+    const int S = (rb + 1023) / 1024;
+    constexpr int R = 4, SPW = 2;
+    const int KW = (S + SPW - 1) / SPW;
+    int WR = 8;
+    while (WR > 1 && (WR * KW > kMaxWaves || (M + WR * R - 1) / (WR * R) < 384)) WR >>= 1;
+    if (WR * KW > kMaxWaves) return 0;
+    // AWQ keeps x and inv_act slices in registers: at most 4 per thread
+    while (awq && (N / 4 + 64 * WR * KW - 1) / (64 * WR * KW) > 4 && 2 * WR * KW <= kMaxWaves) WR *= 2;
+    const int nthreads = 64 * WR * KW;
+    const int nxq = (N / 4 + nthreads - 1) / nthreads;
+    if (nxq > (awq ? 4 : 8)) return 0;
+    const size_t lds = (size_t)S * 2 * 3 * 64 * 16;
+    if (lds > 64 * 1024) return 0;
+    const int blocks = (M + WR * R - 1) / (WR * R);
+#define IBH_RG(Q_, A_) gemv_rows_grp<Q_, A_><<<blocks, nthreads, lds, st>>>(q, s, x, ia, xo, oi, ov, out, M, N, G, K_out, S, WR, KW)
+    if (awq) {
+        if (nxq <= 1) IBH_RG(1, true); else if (nxq <= 2) IBH_RG(2, true); else IBH_RG(4, true);
+    } else {
+        if (nxq <= 1) IBH_RG(1, false); else if (nxq <= 2) IBH_RG(2, false);
+        else if (nxq <= 4) IBH_RG(4, false); else IBH_RG(8, false);
+    }
+#undef IBH_RG
+    return 1;
 }

@@ -15,7 +15,7 @@ import ctypes
 
 import numpy as np
 
-from ._lib import PqTensor, check, lib
+from ._lib import Int4gTensor, PqTensor, check, lib
 
 SCALE_F16, SCALE_F32 = 0, 1
 
@@ -144,3 +144,39 @@ class PqDeviceTensor:
     def matmul(self, x, out) -> None:
         """ib_pq_matmul_fp32 (src/pq_decode.c:1684)."""
         check(lib().ibh_pq_matmul(ctypes.byref(self.s), _ptr(x), _ptr(out), None, 0, _stream()), "ibh_pq_matmul")
+
+
+class Int4gDeviceTensor:
+    """An IBF v5 INT4 group-scale tensor (struct ib_int4_tensor,
+    src/pq_decode.c:3474-3482) uploaded to the GPU once.  `t` maps q
+    (uint8 [M, N/2]), s (fp16 bits [M, N/G]) and the optional inv_act
+    (fp32 [N]), outl_idx / outl_val (uint16 / fp16 bits [M, K_out]) to numpy
+    arrays (None or absent = not present)."""
+
+    def __init__(self, t: dict):
+        self.keep = []
+        s = Int4gTensor()
+        q = np.ascontiguousarray(t["q"], np.uint8)
+        sc = np.ascontiguousarray(t["s"], np.uint16)
+        s.M, s.N = q.shape[0], q.shape[1] * 2
+        s.G = s.N // sc.shape[1]
+        for f in ("q", "s", "inv_act", "outl_idx", "outl_val"):
+            a = t.get(f)
+            if a is not None:
+                d = torch.from_numpy(np.ascontiguousarray(a).view(np.uint8).reshape(-1).copy()).cuda()
+                self.keep.append(d)
+                setattr(s, f, d.data_ptr())
+        s.K_out = 0 if t.get("outl_idx") is None else int(np.asarray(t["outl_idx"]).shape[1])
+        self.s = s
+        self.M, self.N = s.M, s.N
+
+    def matmul(self, x, out, act_sparse_rel: float = 0.0) -> None:
+        """ib_pq_session_matmul on this tensor (src/pq_decode.c:4442-4452)."""
+        check(lib().ibh_int4g_matmul(ctypes.byref(self.s), _ptr(x), _ptr(out), act_sparse_rel, None, 0, _stream()),
+              "ibh_int4g_matmul")
+
+    def matmul_batched(self, x, out, act_sparse_rel: float = 0.0) -> None:
+        """ib_pq_session_matmul_batched (src/pq_decode.c:4501-4539): x [B, N], out [B, M]."""
+        B = x.shape[0]
+        check(lib().ibh_int4g_matmul_batched(ctypes.byref(self.s), B, _ptr(x), _ptr(out), act_sparse_rel, None, 0,
+                                             _stream()), "ibh_int4g_matmul_batched")

@@ -676,3 +676,58 @@ int or_pq_matmul(const or_pq_tensor* t, const float* x, float* out) {
 void or_expf_batch(const float* x, float* y, size_t n) {
     for (size_t i = 0; i < n; i++) y[i] = expf(x[i]);
 }
+
+/* ── IBF v5 INT4 group-scale matvec ─────────────────────────── */
+
+/* ib_pq_session_matmul, INT4 branch (pq_decode.c:4442-4452):
+ *   xk[j] = x[j] * inv_act[j] when inv_act is present (AWQ);
+ *   build_skip_mask (pq_decode.c:3856-3882): with eps > 0, group g is left
+ *   out iff max|xk over g| <= eps * max|xk|;
+ *   int4_matmul_rows_skip (pq_decode.c:3565-3644), x86 (non-NEON) branch:
+ *   per group gacc += lo*x[j] + hi*x[j+1] over nibble pairs (lo = low
+ *   nibble - 8, even column), acc += scale_g * gacc, then the outlier
+ *   sidecar acc += val_k * xk[idx_k].  pq_decode.c is built with -mfma and
+ *   contraction on; the x86 build fuses as: t = hi*x1; u = fma(lo, x0, t);
+ *   gacc = gacc + u; acc = fma(scale, gacc, acc); acc = fma(val, xk, acc). */
+int or_int4g_matmul(const uint8_t* q, const uint16_t* s, const float* inv_act, const uint16_t* outl_idx,
+                    const uint16_t* outl_val, int M, int N, int G, int K_out, const float* x,
+                    float act_sparse_rel, float* out) {
+    if (G <= 0 || G % 2 || N % G) return -1;
+    const int ng = N / G;
+    float* xk = (float*)malloc((size_t)N * sizeof(float));
+    char* skip = (char*)calloc((size_t)ng, 1);
+    if (!xk || !skip) { free(xk); free(skip); return -1; }
+    for (int j = 0; j < N; j++) xk[j] = inv_act ? x[j] * inv_act[j] : x[j];
+    if (act_sparse_rel > 0.0f) {
+        float xmax = 0.0f;
+        for (int j = 0; j < N; j++) { float a = fabsf(xk[j]); if (a > xmax) xmax = a; }
+        float thr = act_sparse_rel * xmax;
+        for (int g = 0; g < ng; g++) {
+            float gm = 0.0f;
+            for (int j = 0; j < G; j++) { float a = fabsf(xk[g * G + j]); if (a > gm) gm = a; }
+            skip[g] = gm <= thr;
+        }
+    }
+    for (int m = 0; m < M; m++) {
+        const uint8_t* qr = q + (size_t)m * (N / 2);
+        const uint16_t* sr = s + (size_t)m * ng;
+        float acc = 0.0f;
+        for (int g = 0; g < ng; g++) {
+            if (skip[g]) continue;
+            const float* xg = xk + g * G;
+            const uint8_t* qg = qr + g * G / 2;
+            float gacc = 0.0f;
+            for (int j = 0; j < G; j += 2) {
+                const int lo = (qg[j / 2] & 15) - 8, hi = (qg[j / 2] >> 4) - 8;
+                const float t = (float)hi * xg[j + 1];
+                gacc = gacc + fmaf((float)lo, xg[j], t);
+            }
+            acc = fmaf(or_fp16_to_fp32(sr[g]), gacc, acc);
+        }
+        for (int k = 0; k < K_out; k++)
+            acc = fmaf(or_fp16_to_fp32(outl_val[(size_t)m * K_out + k]), xk[outl_idx[(size_t)m * K_out + k]], acc);
+        out[m] = acc;
+    }
+    free(xk); free(skip);
+    return 0;
+}

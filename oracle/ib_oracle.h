@@ -85,6 +85,14 @@ int or_pq_reconstruct(const or_pq_tensor* t, float* out);                /* pq_d
  * (kernels/avx2.c:213-216, :241-244), called as is. */
 void or_expf_batch(const float* x, float* y, size_t n);
 
+/* IBF v5 INT4 group-scale matvec: ib_pq_session_matmul for an INT4 tensor
+ * (pq_decode.c:4442-4452 -> 3905-3953 -> 3565-3644), x86 build.
+ * inv_act may be NULL; K_out 0 = no outlier sidecar; act_sparse_rel is
+ * IB_ACT_SPARSE_REL (<= 0: off). */
+int or_int4g_matmul(const uint8_t* q, const uint16_t* s, const float* inv_act, const uint16_t* outl_idx,
+                    const uint16_t* outl_val, int M, int N, int G, int K_out, const float* x,
+                    float act_sparse_rel, float* out);
+
 #ifdef __cplusplus
 }
 #endif

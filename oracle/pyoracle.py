@@ -58,6 +58,7 @@ def _declare(L):
         "or_pq_matmul": (I, [P, P, P]),
         "or_pq_reconstruct": (I, [P, P]),
         "or_expf_batch": (None, [P, P, C.c_size_t]),
+        "or_int4g_matmul": (I, [P, P, P, P, P, I, I, I, I, P, C.c_float, P]),
     }
     for name, (res, args) in sigs.items():
         f = getattr(L, name)
@@ -248,3 +249,24 @@ def expf(x):
     y = np.empty_like(x)
     lib().or_expf_batch(_p(x), _p(y), C.c_size_t(x.size))
     return y
+
+
+def _opt(a, dt):
+    return None if a is None else _c(a, dt)
+
+
+def int4g_matmul(t: dict, x, act_sparse_rel: float = 0.0):
+    """ib_pq_session_matmul on an INT4 group-scale tensor ``t`` (keys q, s,
+    inv_act, outl_idx, outl_val; the optional ones may be None)."""
+    q, s = _c(t["q"], np.uint8), _c(t["s"], np.uint16)
+    M, N = q.shape[0], q.shape[1] * 2
+    G = N // s.shape[1]
+    ia = _opt(t.get("inv_act"), np.float32)
+    oi, ov = _opt(t.get("outl_idx"), np.uint16), _opt(t.get("outl_val"), np.uint16)
+    K = 0 if oi is None else oi.shape[1]
+    x = _c(x, np.float32)
+    out = np.zeros(M, np.float32)
+    rc = lib().or_int4g_matmul(_p(q), _p(s), None if ia is None else _p(ia), None if oi is None else _p(oi),
+                               None if ov is None else _p(ov), M, N, G, K, _p(x), C.c_float(act_sparse_rel), _p(out))
+    assert rc == 0
+    return out

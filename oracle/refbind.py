@@ -19,6 +19,7 @@ import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 REF_LIB = os.path.join(_HERE, "_ref", "libinferbit_ref.so")
+REF_INT4G = os.path.join(_HERE, "_ref", "libref_int4g.so")
 
 P = C.c_void_p
 I = C.c_int
@@ -185,4 +186,29 @@ def pq_reconstruct(t: dict):
     out = np.zeros((t["M"], t["N"]), np.float32)
     rc = lib().ib_pq_reconstruct_fp32(C.byref(s), _p(out))
     assert rc == 0
+    return out
+
+
+_i4 = None
+
+
+def int4g_matmul(t: dict, x):
+    """The reference's INT4 group-scale session matmul (oracle/ref_int4g.c).
+    IB_ACT_SPARSE_REL is read by the reference once per process, so a caller
+    that wants the skip mask sets it before the first call (in a subprocess)."""
+    global _i4
+    if _i4 is None:
+        _i4 = C.CDLL(REF_INT4G)
+        _i4.ref_int4g_matmul.argtypes = [P, P, P, P, P, I, I, I, I, P, P]
+        _i4.ref_int4g_matmul.restype = I
+    q, s = np.ascontiguousarray(t["q"], np.uint8), np.ascontiguousarray(t["s"], np.uint16)
+    M, N = q.shape[0], q.shape[1] * 2
+    G = N // s.shape[1]
+    opt = lambda a, dt: None if a is None else np.ascontiguousarray(a, dt)
+    ia, oi, ov = opt(t.get("inv_act"), np.float32), opt(t.get("outl_idx"), np.uint16), opt(t.get("outl_val"), np.uint16)
+    K = 0 if oi is None else oi.shape[1]
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.zeros(M, np.float32)
+    pp = lambda a: None if a is None else _p(a)
+    assert _i4.ref_int4g_matmul(_p(q), _p(s), pp(ia), pp(oi), pp(ov), M, N, G, K, _p(x), _p(out)) == 0
     return out

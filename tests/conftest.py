@@ -31,6 +31,14 @@ def pq_case(npz, name):
     return t
 
 
+INT4G_KEYS = ("q", "s", "inv_act", "outl_idx", "outl_val", "x", "y", "ys")
+
+
+def int4g_case(npz, name):
+    """An INT4 group-scale tensor dict (+ x, y, ys) from int4g.npz entries 'name.*'."""
+    return {k: (npz[f"{name}.{k}"] if f"{name}.{k}" in npz.files else None) for k in INT4G_KEYS}
+
+
 @pytest.fixture(scope="session")
 def oracle_lib():
     from oracle import pyoracle

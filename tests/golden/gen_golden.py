@@ -12,6 +12,12 @@ Contents (every array is what the reference produced, except the inputs):
   w4a8.npz     ib_quantize_input_int8_g128 + matmul_w4a8 (avx2/scalar)
   batch.npz    matmul_int8_batch / matmul_w4a8_batch with M_stride > M
   pq.npz       ib_pq_matmul_fp32 / ib_pq_reconstruct_fp32 on small tensors
+  int4g.npz    ib_pq_session_matmul on IBF v5 INT4 group-scale tensors
+               (oracle/_ref/libref_int4g.so): y without, ys with the
+               IB_ACT_SPARSE_REL skip mask (set in a child process, since the
+               reference reads it once per process)
+
+  python tests/golden/gen_golden.py int4g   writes int4g.npz only.
 """
 from __future__ import annotations
 
@@ -152,12 +158,82 @@ def gen_pq(out):
     np.savez_compressed(os.path.join(out, "pq.npz"), **d)
 
 
+# name: (M, N, G, AWQ inv_act, outliers per row)
+INT4G_CASES = {
+    "g32": (64, 256, 32, 0, 0),
+    "g128awq": (100, 512, 128, 1, 3),
+    "g64awq": (33, 384, 64, 1, 0),
+    "g128out": (17, 2048, 128, 0, 5),
+    "g96": (5, 96, 96, 1, 2),
+    "g2": (8, 40, 2, 0, 1),
+    "g128big": (48, 4096, 128, 1, 4),
+    "g256": (20, 1536, 256, 1, 2),
+}
+INT4G_SKIP_REL = 1e-2
+
+
+def make_int4g(rng, M, N, G, awq, K):
+    t = dict(q=rng.integers(0, 256, (M, N // 2), dtype=np.uint8),
+             s=f16bits(rng.uniform(0.002, 0.05, (M, N // G))))
+    if awq:
+        t["inv_act"] = np.exp(rng.normal(0, 0.5, N)).astype(np.float32)
+    if K:
+        t["outl_idx"] = np.stack([rng.choice(N, K, replace=False) for _ in range(M)]).astype(np.uint16)
+        t["outl_val"] = f16bits(rng.normal(0, 1, (M, K)))
+    return t
+
+
+def int4g_inputs():
+    rng = np.random.default_rng(4104)
+    d = {}
+    for name, (M, N, G, awq, K) in INT4G_CASES.items():
+        t = make_int4g(rng, M, N, G, awq, K)
+        x = rng.standard_normal(N).astype(np.float32)
+        small = np.repeat(rng.random(N // G) < 0.3, G)         # whole groups near zero
+        x[small] *= 3e-3
+        for k, v in t.items():
+            d[f"{name}.{k}"] = v
+        d[f"{name}.x"] = x
+    return d
+
+
+def int4g_outputs(d):
+    out = {}
+    for name in INT4G_CASES:
+        t = {k[len(name) + 1:]: d[k] for k in d if k.startswith(name + ".")}
+        out[f"{name}.y"] = R.int4g_matmul(t, t["x"])
+    return out
+
+
+def gen_int4g(out):
+    import subprocess
+    import tempfile
+    d = int4g_inputs()
+    d.update(int4g_outputs(d))
+    with tempfile.TemporaryDirectory() as tmp:
+        f = os.path.join(tmp, "skip.npz")
+        subprocess.run([sys.executable, os.path.abspath(__file__), "int4g-skip-child", f], check=True,
+                       env=dict(os.environ, IB_ACT_SPARSE_REL=repr(INT4G_SKIP_REL)))
+        ys = np.load(f)
+        for name in INT4G_CASES:
+            d[f"{name}.ys"] = ys[f"{name}.y"]
+    d["skip_rel"] = np.float32(INT4G_SKIP_REL)
+    np.savez_compressed(os.path.join(out, "int4g.npz"), **d)
+
+
 def main():
+    if len(sys.argv) > 2 and sys.argv[1] == "int4g-skip-child":
+        np.savez(sys.argv[2], **int4g_outputs(int4g_inputs()))
+        return
+    if len(sys.argv) > 1 and sys.argv[1] == "int4g":
+        gen_int4g(HERE)
+        return
     if not R.available():
         sys.exit("oracle/_ref/libinferbit_ref.so missing: run `make -C oracle ref` first")
     gen_quant_matvec(HERE)
     gen_batch(HERE)
     gen_pq(HERE)
+    gen_int4g(HERE)
     for f in sorted(os.listdir(HERE)):
         if f.endswith(".npz"):
             print(f, os.path.getsize(os.path.join(HERE, f)))

@@ -4,7 +4,7 @@ against closed forms that do not depend on the reference at all."""
 import numpy as np
 import pytest
 
-from conftest import load_golden, pq_case
+from conftest import int4g_case, load_golden, pq_case
 
 SHAPES = ["64x256", "37x200", "16x4100", "8x4096"]
 
@@ -240,3 +240,82 @@ def test_fp16_conversions(oracle_lib):
         t = L.or_fp32_to_fp16_trunc(ctypes.c_float(f))
         tv = np.array([t], np.uint16).view(np.float16).astype(np.float32)[0]
         assert abs(tv) <= abs(np.float32(f)) or np.isinf(tv)
+
+
+INT4G = ["g32", "g128awq", "g64awq", "g128out", "g96", "g2", "g128big", "g256"]
+
+
+@pytest.mark.parametrize("name", INT4G)
+def test_int4g_matches_reference(oracle_lib, name):
+    """ib_pq_session_matmul on INT4 group-scale tensors, with and without the
+    IB_ACT_SPARSE_REL skip mask, bit for bit."""
+    d = load_golden("int4g.npz")
+    t = int4g_case(d, name)
+    same_bits(oracle_lib.int4g_matmul(t, t["x"]), t["y"])
+    same_bits(oracle_lib.int4g_matmul(t, t["x"], float(d["skip_rel"])), t["ys"])
+
+
+def _int4g_dense(t):
+    q = np.asarray(t["q"])
+    M, N = q.shape[0], q.shape[1] * 2
+    n = np.empty((M, N), np.float64)
+    n[:, 0::2] = (q & 15).astype(np.float64) - 8
+    n[:, 1::2] = (q >> 4).astype(np.float64) - 8
+    G = N // t["s"].shape[1]
+    W = n * np.repeat(f16(t["s"]).astype(np.float64), G, axis=1)
+    if t.get("outl_idx") is not None:
+        for m in range(M):
+            for k, j in enumerate(t["outl_idx"][m]):
+                W[m, j] += f16(t["outl_val"][m, k])
+    return W
+
+
+@pytest.mark.parametrize("name", INT4G)
+def test_int4g_matches_materialized_fp64(oracle_lib, name):
+    """y = W (x * inv_act) with W[m, j] = (nibble - 8) * scale[m, j // G] plus
+    the outlier values, in fp64: pins the nibble order, the -8 bias, the
+    group index, the AWQ pre-scale and the sidecar independently of the
+    reference."""
+    t = int4g_case(load_golden("int4g.npz"), name)
+    xk = t["x"].astype(np.float64)
+    if t["inv_act"] is not None:
+        xk = xk * t["inv_act"].astype(np.float32).astype(np.float64)
+    ref = _int4g_dense(t) @ xk
+    y = oracle_lib.int4g_matmul(t, t["x"])
+    assert np.abs(y - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
+def test_int4g_skip_mask_drops_whole_groups(oracle_lib):
+    """With the skip mask on, y equals the unmasked matvec over x with the
+    qualifying groups set to zero (and only those): threshold <= is inclusive."""
+    rng = np.random.default_rng(5)
+    M, N, G = 9, 256, 32
+    t = dict(q=rng.integers(0, 256, (M, N // 2), dtype=np.uint8),
+             s=np.asarray(rng.uniform(0.01, 0.1, (M, N // G)), np.float16).view(np.uint16))
+    x = rng.standard_normal(N).astype(np.float32)
+    x[0] = 4.0
+    x[32:64] = 0.0                     # max 0 <= thr: skipped
+    x[64:96] = np.float32(0.5 * 4.0) * np.sign(x[64:96])   # exactly 0.5 * max: skipped at rel 0.5
+    x[96:128] *= 1e-3
+    y = oracle_lib.int4g_matmul(t, x, 0.5)
+    xz = x.copy()
+    gmax = np.abs(x.reshape(-1, G)).max(1)
+    for g in range(N // G):
+        if gmax[g] <= np.float32(0.5) * np.float32(4.0):
+            xz[g * G:(g + 1) * G] = 0
+    assert (gmax <= 2.0).sum() >= 3
+    same_bits(y, oracle_lib.int4g_matmul(t, xz))
+
+
+def test_int4g_live_reference(oracle_lib):
+    """The compiled reference (oracle/_ref/libref_int4g.so), when present,
+    agrees bit for bit on a fresh random tensor with AWQ and outliers."""
+    from oracle import refbind as R
+    import os
+    if not os.path.exists(R.REF_INT4G):
+        pytest.skip("oracle/_ref/libref_int4g.so not built (make -C oracle ref)")
+    from gen_golden import make_int4g
+    rng = np.random.default_rng(77)
+    t = make_int4g(rng, 31, 1024, 128, 1, 6)
+    x = rng.standard_normal(1024).astype(np.float32)
+    same_bits(oracle_lib.int4g_matmul(t, x), R.int4g_matmul(t, x))
