@@ -162,6 +162,12 @@ typedef struct {
 size_t ibh_pq_workspace_bytes(const ibh_pq_tensor* t);
 int    ibh_pq_matmul(const ibh_pq_tensor* t, const float* x, float* out, void* ws,
                      size_t ws_bytes, void* stream);
+/* The PQ session's default variant: ib_pq_matmul_fp32_streaming_cached
+ * (src/pq_decode.c:2927-2998, taken by ib_pq_session_matmul at
+ * 4468-4470): the same tables, gather and outliers over EVERY chunk (no
+ * skipping rule).  G <= 32 as in the reference.  Same workspace. */
+int    ibh_pq_matmul_streaming(const ibh_pq_tensor* t, const float* x, float* out, void* ws,
+                               size_t ws_bytes, void* stream);
 
 /* ── IBF v5 INT4 group-scale matvec, device pointers ───────── */
 

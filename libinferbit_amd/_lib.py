@@ -37,6 +37,7 @@ SIGNATURES = {
     "ibh_attn_decode": (I, [P, P, P, P, P, P, I, I, I, I, I, P, SZ, P]),
     "ibh_pq_workspace_bytes": (SZ, [P]),
     "ibh_pq_matmul": (I, [P, P, P, P, SZ, P]),
+    "ibh_pq_matmul_streaming": (I, [P, P, P, P, SZ, P]),
     "ibh_int4g_workspace_bytes": (SZ, [P]),
     "ibh_int4g_matmul": (I, [P, P, P, C.c_float, P, SZ, P]),
     "ibh_int4g_matmul_batched": (I, [P, I, P, P, C.c_float, P, SZ, P]),

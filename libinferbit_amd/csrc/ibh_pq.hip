@@ -34,6 +34,7 @@ constexpr int kThreads = 256;
 
 struct PqDev {
     int M, N, G, K, K2, n_levels, n_outlier, C, l2_idx_bytes;
+    float skip_frac;         // chunk kept iff its max|x| >= skip_frac * max|x| (0: every chunk)
     const uint16_t *cb1l, *cb1r, *cb2l, *cb2r;
     const uint8_t *i1l, *i1r, *i2l, *i2r;
     const uint16_t* row_scale;
@@ -194,7 +195,7 @@ __global__ __launch_bounds__(kThreads) void pq_gather(PqDev t, const float* __re
     __syncthreads();
     float gmax = 0.f;
     for (int w = 0; w < kThreads / 64; w++) gmax = fmaxf(gmax, red[w]);
-    if (threadIdx.x < cn) act_s[threadIdx.x] = gmax > 0.f ? (cmax[c0 + threadIdx.x] >= gmax * 0.01f) : 1;
+    if (threadIdx.x < cn) act_s[threadIdx.x] = gmax > 0.f ? (cmax[c0 + threadIdx.x] >= gmax * t.skip_frac) : 1;
     __syncthreads();
 
     const size_t l2s = TWO ? l2_stride(t) : 0;
@@ -279,8 +280,25 @@ extern "C" size_t ibh_pq_workspace_bytes(const ibh_pq_tensor_abi* t) {
     return t && pq_geometry(t, &cs, &ns, &lds, &need, &o1, &o2, &o3) == IBH_OK ? need : 0;
 }
 
+static int pq_run(const ibh_pq_tensor_abi* t, const float* x, float* out, void* ws, size_t ws_bytes, void* stream,
+                  float skip_frac);
+
 extern "C" int ibh_pq_matmul(const ibh_pq_tensor_abi* t, const float* x, float* out, void* ws, size_t ws_bytes,
                              void* stream) {
+    return pq_run(t, x, out, ws, ws_bytes, stream, 0.01f);
+}
+
+extern "C" int ibh_pq_matmul_streaming(const ibh_pq_tensor_abi* t, const float* x, float* out, void* ws,
+                                       size_t ws_bytes, void* stream) {
+    if (t && t->G > 32) {
+        ibh_set_error("ibh_pq_matmul_streaming: G=%d > 32 (the reference's chunk buffers hold 16 per side)", t->G);
+        return IBH_ERROR_PARAM;
+    }
+    return pq_run(t, x, out, ws, ws_bytes, stream, 0.0f);
+}
+
+static int pq_run(const ibh_pq_tensor_abi* t, const float* x, float* out, void* ws, size_t ws_bytes, void* stream,
+                  float skip_frac) {
     if (!t || !x || !out || t->M <= 0 || t->C <= 0 || t->G <= 0 || t->G % 2 || t->G > 64 || t->K <= 0 || t->K > 65536 ||
         !t->codebook_l1_l || !t->codebook_l1_r || !t->indices_l1_l || !t->indices_l1_r || !t->row_scale ||
         t->N != t->C * t->G + t->n_outlier || t->n_outlier < 0 || t->n_outlier > 1024 ||
@@ -311,7 +329,7 @@ extern "C" int ibh_pq_matmul(const ibh_pq_tensor_abi* t, const float* x, float* 
     }
     PqDev d;
     d.M = t->M; d.N = t->N; d.G = t->G; d.K = t->K; d.K2 = t->K_l2 > 0 ? t->K_l2 : t->K;
-    d.n_levels = t->n_levels; d.n_outlier = t->n_outlier; d.C = t->C;
+    d.n_levels = t->n_levels; d.n_outlier = t->n_outlier; d.C = t->C; d.skip_frac = skip_frac;
     d.l2_idx_bytes = t->l2_idx_bytes > 0 ? t->l2_idx_bytes : 1;
     d.cb1l = t->codebook_l1_l; d.cb1r = t->codebook_l1_r; d.cb2l = t->codebook_l2_l; d.cb2r = t->codebook_l2_r;
     d.i1l = t->indices_l1_l; d.i1r = t->indices_l1_r; d.i2l = t->indices_l2_l; d.i2r = t->indices_l2_r;

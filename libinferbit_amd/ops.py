@@ -145,6 +145,11 @@ class PqDeviceTensor:
         """ib_pq_matmul_fp32 (src/pq_decode.c:1684)."""
         check(lib().ibh_pq_matmul(ctypes.byref(self.s), _ptr(x), _ptr(out), None, 0, _stream()), "ibh_pq_matmul")
 
+    def matmul_streaming(self, x, out) -> None:
+        """ib_pq_matmul_fp32_streaming_cached (src/pq_decode.c:2987): every chunk."""
+        check(lib().ibh_pq_matmul_streaming(ctypes.byref(self.s), _ptr(x), _ptr(out), None, 0, _stream()),
+              "ibh_pq_matmul_streaming")
+
 
 class Int4gDeviceTensor:
     """An IBF v5 INT4 group-scale tensor (struct ib_int4_tensor,

@@ -673,6 +673,70 @@ int or_pq_matmul(const or_pq_tensor* t, const float* x, float* out) {
     return 0;
 }
 
+/* pq_chunk_dot_table_f32 (pq_decode.c:169-254), x86 AVX2+FMA build, one
+ * entry: half 16 -> eight lanes fma(e[i+8], x[i+8], e[i]*x[i]); half 8 ->
+ * eight products; either folded as (lo + hi) then two horizontal adds,
+ * ((s0+s1) + (s2+s3)).  Other halves run the scalar loop d += e[j]*x[j] as
+ * gcc -O3 -mavx2 -mfma compiled it (read from this build's disassembly):
+ * products of the leading multiple of 4 columns rounded, then added in
+ * order; the last half % 4 columns fused. */
+static float pq_table_entry_avx2(const float* e, const float* x, int half) {
+    float a[8];
+    if (half == 16 || half == 8) {
+        for (int i = 0; i < 8; i++) a[i] = half == 16 ? fmaf(e[i + 8], x[i + 8], e[i] * x[i]) : e[i] * x[i];
+        float s0 = a[0] + a[4], s1 = a[1] + a[5], s2 = a[2] + a[6], s3 = a[3] + a[7];
+        return (s0 + s1) + (s2 + s3);
+    }
+    float d = 0.0f;
+    int j = 0;
+    for (; j < (half & ~3); j++) d = d + e[j] * x[j];
+    for (; j < half; j++) d = fmaf(e[j], x[j], d);
+    return d;
+}
+
+/* streaming_cached_kernel (pq_decode.c:2927-2985): per chunk c the four
+ * K-entry tables over x at the chunk's inner columns, then for every row
+ * out[r] += TL1 + TR1 (+ TL2 + TR2), left to right; out[r] *= row scale;
+ * outlier sidecar as matmul_impl (apply_outliers). */
+int or_pq_matmul_streaming(const or_pq_tensor* t, const float* x, float* out) {
+    int M = t->M, G = t->G, C = t->C, K = t->K, hf = G / 2;
+    if (hf > 16) return -1;
+    int K2 = t->K_l2 > 0 ? t->K_l2 : K;
+    int two = t->n_levels == 2;
+    int* ic = pq_inner_cols(t);
+    size_t l2s = pq_l2_stride(t);
+    float* tab = (float*)malloc(sizeof(float) * (size_t)(2 * K + 2 * K2));
+    float* cb = (float*)malloc(sizeof(float) * (size_t)hf);
+    for (int r = 0; r < M; r++) out[r] = 0.0f;
+    for (int c = 0; c < C; c++) {
+        float xl[16], xr[16];
+        for (int j = 0; j < hf; j++) { xl[j] = x[ic[c * G + j]]; xr[j] = x[ic[c * G + hf + j]]; }
+        for (int lev = 0; lev < (two ? 2 : 1); lev++) {
+            int KK = lev ? K2 : K;
+            for (int side = 0; side < 2; side++) {
+                const uint16_t* cbh = lev ? (side ? t->cb2r : t->cb2l) : (side ? t->cb1r : t->cb1l);
+                float* T = tab + (lev ? 2 * K : 0) + side * KK;
+                for (int k = 0; k < KK; k++) {
+                    for (int j = 0; j < hf; j++) cb[j] = or_fp16_to_fp32(cbh[(size_t)k * hf + j]);
+                    T[k] = pq_table_entry_avx2(cb, side ? xr : xl, hf);
+                }
+            }
+        }
+        for (int r = 0; r < M; r++) {
+            float v = tab[t->i1l[(size_t)r * C + c]] + tab[K + t->i1r[(size_t)r * C + c]];
+            if (two) {
+                v = v + tab[2 * K + pq_l2_at(t, t->i2l + (size_t)r * l2s, c)];
+                v = v + tab[2 * K + K2 + pq_l2_at(t, t->i2r + (size_t)r * l2s, c)];
+            }
+            out[r] = out[r] + v;
+        }
+    }
+    for (int r = 0; r < M; r++) out[r] = out[r] * or_fp16_to_fp32(t->row_scale[r]);
+    pq_outliers(t, x, out);
+    free(ic); free(tab); free(cb);
+    return 0;
+}
+
 void or_expf_batch(const float* x, float* y, size_t n) {
     for (size_t i = 0; i < n; i++) y[i] = expf(x[i]);
 }

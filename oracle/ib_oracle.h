@@ -80,6 +80,10 @@ typedef struct {
 
 int or_pq_matmul(const or_pq_tensor* t, const float* x, float* out);      /* pq_decode.c:1504-1686 */
 int or_pq_reconstruct(const or_pq_tensor* t, float* out);                /* pq_decode.c:1103-1196 */
+/* ib_pq_matmul_fp32_streaming_cached, the PQ session's default variant
+ * (pq_decode.c:2927-2985, tables by pq_chunk_dot_table_f32 169-254):
+ * every chunk, no skipping.  G <= 32. */
+int or_pq_matmul_streaming(const or_pq_tensor* t, const float* x, float* out);
 
 /* glibc expf applied elementwise: the libm the reference links
  * (kernels/avx2.c:213-216, :241-244), called as is. */

@@ -56,6 +56,7 @@ def _declare(L):
         "or_rope": (None, [P, P, I, I, C.c_float]),
         "or_silu_mul": (None, [P, P, P, I]),
         "or_pq_matmul": (I, [P, P, P]),
+        "or_pq_matmul_streaming": (I, [P, P, P]),
         "or_pq_reconstruct": (I, [P, P]),
         "or_expf_batch": (None, [P, P, C.c_size_t]),
         "or_int4g_matmul": (I, [P, P, P, P, P, I, I, I, I, P, C.c_float, P]),
@@ -233,6 +234,15 @@ def pq_matmul(t: dict, x):
     x = _c(x, np.float32)
     out = np.zeros(t["M"], np.float32)
     lib().or_pq_matmul(C.byref(s), _p(x), _p(out))
+    return out
+
+
+def pq_matmul_streaming(t: dict, x):
+    """ib_pq_matmul_fp32_streaming_cached (the session's default PQ variant)."""
+    s, keep = _pq_struct(t)
+    x = _c(x, np.float32)
+    out = np.zeros(t["M"], np.float32)
+    assert lib().or_pq_matmul_streaming(C.byref(s), _p(x), _p(out)) == 0
     return out
 
 

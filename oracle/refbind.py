@@ -78,6 +78,10 @@ def lib():
         _lib.ib_detect_simd.restype = I
         _lib.ib_pq_matmul_fp32.argtypes = [P, P, P]
         _lib.ib_pq_reconstruct_fp32.argtypes = [P, P]
+        _lib.ib_pq_lut_cache_create.argtypes = [P, P]
+        _lib.ib_pq_lut_cache_free.argtypes = [P]
+        _lib.ib_pq_lut_cache_free.restype = None
+        _lib.ib_pq_matmul_fp32_streaming_cached.argtypes = [P, P, P, P]
     return _lib
 
 
@@ -178,6 +182,21 @@ def pq_matmul(t: dict, x):
     out = np.zeros(t["M"], np.float32)
     rc = lib().ib_pq_matmul_fp32(C.byref(s), _p(x), _p(out))
     assert rc == 0
+    return out
+
+
+def pq_matmul_streaming(t: dict, x):
+    """ib_pq_lut_cache_create + ib_pq_matmul_fp32_streaming_cached (the PQ
+    session's default variant, src/pq_decode.c:2987)."""
+    s, keep = _pq(t)
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.zeros(t["M"], np.float32)
+    cache = C.c_void_p()
+    assert lib().ib_pq_lut_cache_create(C.byref(s), C.byref(cache)) == 0
+    try:
+        assert lib().ib_pq_matmul_fp32_streaming_cached(C.byref(s), cache, _p(x), _p(out)) == 0
+    finally:
+        lib().ib_pq_lut_cache_free(cache)
     return out
 
 

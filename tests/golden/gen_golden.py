@@ -12,12 +12,16 @@ Contents (every array is what the reference produced, except the inputs):
   w4a8.npz     ib_quantize_input_int8_g128 + matmul_w4a8 (avx2/scalar)
   batch.npz    matmul_int8_batch / matmul_w4a8_batch with M_stride > M
   pq.npz       ib_pq_matmul_fp32 / ib_pq_reconstruct_fp32 on small tensors
+  pqs.npz      ib_pq_lut_cache_create + ib_pq_matmul_fp32_streaming_cached
+               (the PQ session's default variant) on the pq.npz cases and on
+               G = 4 / 32 cases
   int4g.npz    ib_pq_session_matmul on IBF v5 INT4 group-scale tensors
                (oracle/_ref/libref_int4g.so): y without, ys with the
                IB_ACT_SPARSE_REL skip mask (set in a child process, since the
                reference reads it once per process)
 
-  python tests/golden/gen_golden.py int4g   writes int4g.npz only.
+  python tests/golden/gen_golden.py int4g   writes int4g.npz only;
+  python tests/golden/gen_golden.py pqs     writes pqs.npz only.
 """
 from __future__ import annotations
 
@@ -158,6 +162,33 @@ def gen_pq(out):
     np.savez_compressed(os.path.join(out, "pq.npz"), **d)
 
 
+# cases of pqs.npz beyond pq.npz's: (M, C, G, K, levels, K_l2, outliers)
+PQS_EXTRA = {
+    "g4": (40, 24, 4, 256, 1, 0, 0),
+    "g32": (36, 10, 32, 256, 2, 256, 5),
+    "g4l2": (20, 16, 4, 64, 2, 16, 3),
+}
+
+
+def gen_pqs(out):
+    d = {}
+    pq = np.load(os.path.join(out, "pq.npz"))
+    for name in PQ_CASES:
+        t = {k[len(name) + 1:]: (int(pq[k]) if pq[k].ndim == 0 else pq[k]) for k in pq.files
+             if k.startswith(name + ".")}
+        d[f"{name}.y"] = R.pq_matmul_streaming(t, t["x"])
+        d[f"{name}.ys"] = R.pq_matmul_streaming(t, t["xs"])
+    rng = np.random.default_rng(1234)
+    for name, args in PQS_EXTRA.items():
+        t = make_pq(rng, *args)
+        x = rng.standard_normal(t["N"]).astype(np.float32)
+        for k, v in t.items():
+            d[f"{name}.{k}"] = np.asarray(v)
+        d[f"{name}.x"] = x
+        d[f"{name}.y"] = R.pq_matmul_streaming(t, x)
+    np.savez_compressed(os.path.join(out, "pqs.npz"), **d)
+
+
 # name: (M, N, G, AWQ inv_act, outliers per row)
 INT4G_CASES = {
     "g32": (64, 256, 32, 0, 0),
@@ -228,11 +259,15 @@ def main():
     if len(sys.argv) > 1 and sys.argv[1] == "int4g":
         gen_int4g(HERE)
         return
+    if len(sys.argv) > 1 and sys.argv[1] == "pqs":
+        gen_pqs(HERE)
+        return
     if not R.available():
         sys.exit("oracle/_ref/libinferbit_ref.so missing: run `make -C oracle ref` first")
     gen_quant_matvec(HERE)
     gen_batch(HERE)
     gen_pq(HERE)
+    gen_pqs(HERE)
     gen_int4g(HERE)
     for f in sorted(os.listdir(HERE)):
         if f.endswith(".npz"):

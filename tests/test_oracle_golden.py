@@ -319,3 +319,29 @@ def test_int4g_live_reference(oracle_lib):
     t = make_int4g(rng, 31, 1024, 128, 1, 6)
     x = rng.standard_normal(1024).astype(np.float32)
     same_bits(oracle_lib.int4g_matmul(t, x), R.int4g_matmul(t, x))
+
+
+@pytest.mark.parametrize("name", ["l1", "l2p16", "l2u8", "l2u16", "out8", "out40", "g4", "g32", "g4l2"])
+def test_pq_streaming_matches_reference(oracle_lib, name):
+    """ib_pq_matmul_fp32_streaming_cached (the PQ session's default), bit for bit."""
+    d = load_golden("pqs.npz")
+    src = d if f"{name}.M" in d.files else load_golden("pq.npz")
+    t = pq_case(src, name)
+    same_bits(oracle_lib.pq_matmul_streaming(t, t["x"]), d[f"{name}.y"])
+    if f"{name}.ys" in d.files:
+        same_bits(oracle_lib.pq_matmul_streaming(t, t["xs"]), d[f"{name}.ys"])
+
+
+
+def test_pq_streaming_keeps_every_chunk(oracle_lib):
+    """On x whose first half is scaled by 1e-4 the skipping variant drops
+    those chunks (its result equals the matvec over the second half only)
+    while the streaming variant keeps them (it does not)."""
+    t = pq_case(load_golden("pq.npz"), "l1")
+    xs = t["xs"].copy()
+    half = xs.copy()
+    half[: t["N"] // 2] = 0
+    y_skip, y_half = oracle_lib.pq_matmul(t, xs), oracle_lib.pq_matmul(t, half)
+    np.testing.assert_allclose(y_skip, y_half, rtol=0, atol=1e-6 * np.abs(y_half).max())
+    y_str = oracle_lib.pq_matmul_streaming(t, xs)
+    assert np.abs(y_str - y_half).max() > 1e-6 * np.abs(y_half).max()

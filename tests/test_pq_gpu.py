@@ -51,3 +51,40 @@ def test_pq_zero_input(ops, oracle_lib):
     t = make_pq(np.random.default_rng(1), 64, 16, 16, 256, 1, 0, 8)
     x = np.zeros(t["N"], np.float32)
     np.testing.assert_array_equal(run(ops, t, x), oracle_lib.pq_matmul(t, x))
+
+
+def run_streaming(ops, t, x):
+    d = ops.PqDeviceTensor(t)
+    out = torch.empty(t["M"], device="cuda")
+    d.matmul_streaming(torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda(), out)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("name", ["l1", "l2p16", "l2u8", "l2u16", "out8", "out40", "g4", "g32", "g4l2"])
+def test_pq_streaming_golden(ops, name):
+    """ib_pq_matmul_fp32_streaming_cached (the PQ session's default): no chunk skipping."""
+    print(f"case pq streaming {name}", flush=True)
+    d = load_golden("pqs.npz")
+    src = d if f"{name}.M" in d.files else load_golden("pq.npz")
+    t = pq_case(src, name)
+    assert relerr(run_streaming(ops, t, t["x"]), d[f"{name}.y"]) <= 1e-4
+    if f"{name}.ys" in d.files:
+        assert relerr(run_streaming(ops, t, t["xs"]), d[f"{name}.ys"]) <= 1e-4
+
+
+def test_pq_streaming_mistral_shape(ops, oracle_lib):
+    from gen_golden import make_pq
+    rng = np.random.default_rng(6)
+    t = make_pq(rng, 4096, 896, 16, 256, 1, 0, 0)
+    x = rng.standard_normal(t["N"]).astype(np.float32)
+    x[: t["N"] // 3] *= 1e-3
+    assert relerr(run_streaming(ops, t, x), oracle_lib.pq_matmul_streaming(t, x)) <= 1e-4
+
+
+def test_pq_streaming_rejects_wide_chunks(ops):
+    from gen_golden import make_pq
+    from libinferbit_amd import IbhError
+    t = make_pq(np.random.default_rng(1), 16, 4, 64, 16, 1, 0, 0)
+    with pytest.raises(IbhError):
+        run_streaming(ops, t, np.zeros(t["N"], np.float32))
