@@ -245,6 +245,31 @@ int  ibh_model_kv_prefill(ibh_model* model, const float* k, const float* v, int 
 int  ibh_model_decode_steps(ibh_model* model, int n);
 int  ibh_model_synchronize(ibh_model* model);
 
+/* ib_forward_positions (src/forward.c:904-939 -> forward_batch 682-881):
+ * tokens[0..n) at positions kv_length .. kv_length+n-1 in one batched pass
+ * (the speculative verify step); logits [n][vocab_size] of every position.
+ * n <= 32 (IB_BATCH_MAX).  Projections through the batch kernels of the
+ * reference's routing (tensor_matmul_batch, 200-246); in exact mode the
+ * x86 table's scalar batch kernels, so logits are bit-identical. */
+int  ibh_model_forward_positions(ibh_model* model, const int32_t* tokens, int n, float* logits, int vocab_size);
+
+/* ── greedy speculative decoding (host loop over the calls above) ── */
+
+/* ib_prompt_lookup_search (src/speculative.c:39-67); returns the number of
+ * candidates written to out (<= k). */
+int  ibh_prompt_lookup_search(const int32_t* history, int hist_len, int ngram, int k, int32_t* out);
+/* inferbit_generate at temperature 0 after inferbit_set_prompt_lookup(model,
+ * ngram, k) (src/generate.c:305-409): prefill, then n-gram drafts verified
+ * by ibh_model_forward_positions, rejected positions rolled back.  Returns
+ * the number of tokens written.  ngram or k <= 0: plain greedy. */
+int  ibh_model_generate_lookup(ibh_model* model, const int32_t* input_tokens, int num_input_tokens,
+                               int32_t* out_tokens, int max_out_tokens, int ngram, int k);
+/* inferbit_generate at temperature 0 after inferbit_set_draft_model(model,
+ * draft, draft_k) (src/generate.c:411-520): the draft proposes draft_k tokens
+ * (default 4, at most 32), the main model verifies them in one batched pass. */
+int  ibh_model_generate_draft(ibh_model* model, ibh_model* draft, const int32_t* input_tokens,
+                              int num_input_tokens, int32_t* out_tokens, int max_out_tokens, int draft_k);
+
 /* ── host-side producers of the packed formats (no device work) ── */
 
 /* The device expf restatement evaluated on the host (checks against libm). */

@@ -53,6 +53,10 @@ SIGNATURES = {
     "ibh_model_kv_prefill": (I, [P, P, P, I]),
     "ibh_model_decode_steps": (I, [P, I]),
     "ibh_model_synchronize": (I, [P]),
+    "ibh_model_forward_positions": (I, [P, P, I, P, I]),
+    "ibh_prompt_lookup_search": (I, [P, I, I, I, P]),
+    "ibh_model_generate_lookup": (I, [P, P, I, P, I, I, I]),
+    "ibh_model_generate_draft": (I, [P, P, P, I, P, I, I]),
     "ibh_packed_row_bytes": (SZ, [I, I]),
     "ibh_quantize_rows": (I, [I, P, I, I, P, P]),
     "ibh_fill_normal": (I, [P, SZ, C.c_uint64, C.c_uint64, C.c_float]),

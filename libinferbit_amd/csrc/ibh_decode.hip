@@ -56,6 +56,8 @@ int ibh_launch_rows_x_multi(const MatDesc* d, int n, int kind, const float* x, i
 int ibh_launch_matvec_exact_multi(const MatDesc* d, int n, int kind, const float* x, int N, int bits,
                                   hipStream_t st);
 size_t ibh_attn_exact_scratch(int n_heads, int max_pos);
+int ibh_launch_int8_batch_exact(float* y, const void* w, const void* sc, int kind, const float* x, int M, int N,
+                                int B, int M_stride, hipStream_t st);
 int ibh_launch_attn_exact(float* out, const float* q, const void* kdata, const void* vdata, const float* ks,
                           const float* vs, const int* dpos, int max_pos, int n_heads, int n_kv, int hd, int kv_bits,
                           float* att, hipStream_t st);
@@ -367,6 +369,12 @@ struct ibh_model {
     void* attn_ws = nullptr;
     size_t attn_ws_bytes = 0;
     int* dstate = nullptr;   // [0] pos, [1] prompt_end, [2..] tokens[capacity + 1]
+    // batched positions (forward_positions), allocated on first use for
+    // kMaxBatch slots: activations [slot][dim], positions [slot]
+    float *bx = nullptr, *bxb = nullptr, *bxb2 = nullptr, *bq = nullptr, *bk = nullptr, *bv = nullptr;
+    float *bhb = nullptr, *bhb2 = nullptr, *blogits = nullptr, *bsa = nullptr;
+    int8_t* bqx = nullptr;
+    int* bpos = nullptr;
     int hpos = 0;
     hipGraphExec_t exec = nullptr;
     std::vector<void*> allocs;
@@ -552,6 +560,156 @@ int step(ibh_model* m) {
     argmax_advance_kernel<<<1, 1024, 0, m->st>>>(m->logits, m->vocab, m->dtokens(), m->dpos(), m->dprompt_end());
     IBH_CHECK_LAUNCH("ibh_model: argmax");
     return IBH_OK;
+}
+
+
+// ── batched positions: ib_forward_positions -> forward_batch (forward.c:682-939) ──
+constexpr int kMaxBatch = 32;   // IB_BATCH_MAX (inferbit_internal.h:287)
+
+int alloc_batch(ibh_model* m) {
+    if (m->bx) return IBH_OK;
+    const size_t B = kMaxBatch, H = m->hidden, KV = (size_t)m->n_kv * m->head_dim, I = m->inter, V = m->vocab;
+    const size_t NM = H > I ? H : I;
+    int rc;
+    if ((rc = dalloc(m, (void**)&m->bx, B * H * 4)) || (rc = dalloc(m, (void**)&m->bxb, B * H * 4)) ||
+        (rc = dalloc(m, (void**)&m->bxb2, B * H * 4)) || (rc = dalloc(m, (void**)&m->bq, B * H * 4)) ||
+        (rc = dalloc(m, (void**)&m->bk, B * KV * 4)) || (rc = dalloc(m, (void**)&m->bv, B * KV * 4)) ||
+        (rc = dalloc(m, (void**)&m->bhb, B * I * 4)) || (rc = dalloc(m, (void**)&m->bhb2, B * I * 4)) ||
+        (rc = dalloc(m, (void**)&m->blogits, B * V * 4)) || (rc = dalloc(m, (void**)&m->bqx, B * NM + 64)) ||
+        (rc = dalloc(m, (void**)&m->bsa, B * (NM / 128 + 2) * 4)) || (rc = dalloc(m, (void**)&m->bpos, B * 4)))
+        return rc;
+    return IBH_OK;
+}
+
+// tensor_matmul_batch (forward.c:200-246): INT4 through the per-slot int8
+// activation quantizer + W4A8 batch kernel (unless IB_W4A8=0), INT8 through
+// matmul_int8_batch, everything else one slot at a time.
+int mm_batch(ibh_model* m, const DTensor& t, float* out, const float* in, int M, int N, int B, bool exact) {
+    void* st = (void*)m->st;
+    int rc;
+    if (t.bits == 4 && m->w4a8) {
+        const int G = (N + 127) / 128;
+        for (int b = 0; b < B; b++)
+            if ((rc = ibh_quantize_act_g128(in + (size_t)b * N, m->bqx + (size_t)b * N, m->bsa + (size_t)b * G, N, st)))
+                return rc;
+        return ibh_matmul_w4a8_batch(out, t.w, t.s, t.skind, m->bqx, m->bsa, M, N, B, M, st);
+    }
+    if (t.bits == 8)
+        return exact ? ibh_launch_int8_batch_exact(out, t.w, t.s, t.skind, in, M, N, B, M, m->st)
+                     : ibh_matmul_int8_batch(out, t.w, t.s, t.skind, in, M, N, B, M, st);
+    for (int b = 0; b < B; b++) {
+        float* o = out + (size_t)b * M;
+        const float* x = in + (size_t)b * N;
+        if ((rc = exact ? mm_exact(m, t, o, x, M, N, nullptr, false) : mm(m, t, o, x, M, N))) return rc;
+    }
+    return IBH_OK;
+}
+
+// x[b] += delta[b] (when given); out[b] = rmsnorm_fp16(x[b]) for every slot.
+int norm_batch(ibh_model* m, float* out, float* x, const float* delta, const uint16_t* w, int B, bool exact) {
+    const int H = m->hidden;
+    int rc;
+    for (int b = 0; b < B; b++) {
+        float* o = out + (size_t)b * H;
+        float* xx = x + (size_t)b * H;
+        const float* d = delta ? delta + (size_t)b * H : nullptr;
+        if (exact) {
+            if ((rc = ibh_launch_rmsnorm_exact(o, xx, d, w, m->eps, H, m->st))) return rc;
+        } else {
+            add_rmsnorm_kernel<<<1, kNormThreads, 0, m->st>>>(o, xx, d, w, m->eps, H);
+            IBH_CHECK_LAUNCH("ibh_model: rmsnorm");
+        }
+    }
+    return IBH_OK;
+}
+
+// forward_batch over B slots whose tokens sit at dtokens[pos0 + b] and whose
+// positions are pos0 + b (in bpos): per-position embedding, norms, RoPE, KV
+// write and attention; batched projections; logits of every slot.
+int forward_batch(ibh_model* m, int B) {
+    const int H = m->hidden, KV = m->n_kv * m->head_dim, I = m->inter;
+    const bool exact = m->exact;
+    int rc;
+    const uint16_t* esc = (const uint16_t*)(m->emb.skind == IBH_SCALE_F16 ? m->emb.s : nullptr);
+    for (int b = 0; b < B; b++) {
+        embed_kernel<<<(H + 255) / 256, 256, 0, m->st>>>(m->bx + (size_t)b * H, m->emb.w, esc, m->emb.bits, H,
+                                                         m->dtokens(), m->bpos + b);
+        IBH_CHECK_LAUNCH("ibh_model: embedding");
+    }
+    for (int l = 0; l < m->n_layers; l++) {
+        DLayer& L = m->layers[l];
+        if ((rc = norm_batch(m, m->bxb, m->bx, l ? m->bxb : nullptr, L.in_norm, B, exact)) ||
+            (rc = mm_batch(m, L.q, m->bq, m->bxb, H, H, B, exact)) ||
+            (rc = mm_batch(m, L.k, m->bk, m->bxb, KV, H, B, exact)) ||
+            (rc = mm_batch(m, L.v, m->bv, m->bxb, KV, H, B, exact)))
+            return rc;
+        for (int b = 0; b < B; b++) {
+            float* q = m->bq + (size_t)b * H;
+            float* o = m->bxb2 + (size_t)b * H;
+            if ((rc = ibh_launch_rope_kv_write(L.kd, L.vd, L.ks, L.vs, q, m->bk + (size_t)b * KV, m->bv + (size_t)b * KV,
+                                               m->rope, m->bpos + b, m->n_heads, m->n_kv, m->head_dim, m->kv_bits,
+                                               exact, m->st)))
+                return rc;
+            rc = exact ? ibh_launch_attn_exact(o, q, L.kd, L.vd, L.ks, L.vs, m->bpos + b, m->max_pos, m->n_heads,
+                                               m->n_kv, m->head_dim, m->kv_bits, m->att, m->st)
+                       : ibh_launch_attn(o, q, L.kd, L.vd, L.ks, L.vs, 0, m->bpos + b, m->max_pos, m->n_heads,
+                                         m->n_kv, m->head_dim, m->kv_bits, m->attn_ws, m->attn_ws_bytes, m->st);
+            if (rc) return rc;
+        }
+        if ((rc = mm_batch(m, L.o, m->bxb, m->bxb2, H, H, B, exact)) ||
+            (rc = norm_batch(m, m->bxb2, m->bx, m->bxb, L.post_norm, B, exact)))
+            return rc;
+        if (L.mask) {
+            // a layer with a sparsity mask runs the single-position MLP per
+            // slot (forward.c:803-814)
+            for (int b = 0; b < B; b++) {
+                float* hb = m->bhb + (size_t)b * I;
+                float* hb2 = m->bhb2 + (size_t)b * I;
+                const float* xin = m->bxb2 + (size_t)b * H;
+                float* xo = m->bxb + (size_t)b * H;
+                if (exact) {
+                    if ((rc = mm_exact(m, L.gate, hb, xin, I, H, L.mask, L.mask_sparse)) ||
+                        (rc = mm_exact(m, L.up, hb2, xin, I, H, L.mask, L.mask_sparse)) ||
+                        (rc = ibh_launch_silu_mul_exact(hb, hb, hb2, L.mask, I, m->st)) ||
+                        (rc = mm_exact(m, L.down, xo, hb, H, I, nullptr, false)))
+                        return rc;
+                } else {
+                    if ((rc = mm(m, L.gate, hb, xin, I, H)) || (rc = mm(m, L.up, hb2, xin, I, H))) return rc;
+                    silu_mul_kernel<<<(I + 255) / 256, 256, 0, m->st>>>(hb, hb, hb2, L.mask, I);
+                    IBH_CHECK_LAUNCH("ibh_model: silu_mul");
+                    if ((rc = mm(m, L.down, xo, hb, H, I))) return rc;
+                }
+            }
+        } else {
+            if ((rc = mm_batch(m, L.gate, m->bhb, m->bxb2, I, H, B, exact)) ||
+                (rc = mm_batch(m, L.up, m->bhb2, m->bxb2, I, H, B, exact)))
+                return rc;
+            if (m->w4a8 && L.down.bits == 4) {
+                // silu_mul + the down projection's activation quantizer, fused
+                // per slot as on the single-position path
+                const int G = (I + 127) / 128;
+                for (int b = 0; b < B; b++) {
+                    float* hb = m->bhb + (size_t)b * I;
+                    if ((rc = ibh_launch_silu_quant(hb, hb, m->bhb2 + (size_t)b * I, nullptr, m->bqx + (size_t)b * I,
+                                                    m->bsa + (size_t)b * G, I, exact, m->st)))
+                        return rc;
+                }
+                if ((rc = ibh_matmul_w4a8_batch(m->bxb, L.down.w, L.down.s, L.down.skind, m->bqx, m->bsa, H, I, B, H,
+                                                (void*)m->st)))
+                    return rc;
+                continue;
+            }
+            if (exact) {
+                if ((rc = ibh_launch_silu_mul_exact(m->bhb, m->bhb, m->bhb2, nullptr, B * I, m->st))) return rc;
+            } else {
+                silu_mul_kernel<<<(B * I + 255) / 256, 256, 0, m->st>>>(m->bhb, m->bhb, m->bhb2, nullptr, B * I);
+                IBH_CHECK_LAUNCH("ibh_model: silu_mul");
+            }
+            if ((rc = mm_batch(m, L.down, m->bxb, m->bhb, H, I, B, exact))) return rc;
+        }
+    }
+    if ((rc = norm_batch(m, m->bx, m->bx, m->bxb, m->out_norm, B, exact))) return rc;
+    return mm_batch(m, m->head, m->blogits, m->bx, m->vocab, H, B, exact);
 }
 
 bool eager_mode() {
@@ -992,6 +1150,42 @@ extern "C" int ibh_model_forward(ibh_model* m, const int32_t* tokens, int n, flo
             "ibh_model_forward: logits");
     IBH_HIP(hipStreamSynchronize(m->st), "ibh_model_forward");
     return IBH_OK;
+}
+
+// ib_forward_positions (forward.c:904-939): tokens at positions kv_length ..
+// kv_length + n - 1 in one batched pass, logits of every position.
+extern "C" int ibh_model_forward_positions(ibh_model* m, const int32_t* tokens, int n, float* logits, int vocab) {
+    if (!m || !tokens || !logits || n <= 0) {
+        ibh_set_error("ibh_model_forward_positions: invalid arguments");
+        return IBH_ERROR_PARAM;
+    }
+    if (vocab != m->vocab) {
+        ibh_set_error("ibh_model_forward_positions: vocab_size mismatch: %d vs %d", vocab, m->vocab);
+        return IBH_ERROR_PARAM;
+    }
+    if (m->hpos + n > m->max_pos + 1) {
+        ibh_set_error("ibh_model_forward_positions: context length exceeded: %d + %d > %d", m->hpos, n,
+                      m->max_pos + 1);
+        return IBH_ERROR_CONTEXT;
+    }
+    if (n > kMaxBatch) {
+        ibh_set_error("ibh_model_forward_positions: num_tokens=%d exceeds IB_BATCH_MAX=%d", n, kMaxBatch);
+        return IBH_ERROR_PARAM;
+    }
+    int rc;
+    if ((rc = check_tokens(m, tokens, n, "ibh_model_forward_positions")) || (rc = alloc_batch(m))) return rc;
+    int pos[kMaxBatch];
+    for (int b = 0; b < n; b++) pos[b] = m->hpos + b;
+    IBH_HIP(hipMemcpyAsync(m->dtokens() + m->hpos, tokens, (size_t)n * 4, hipMemcpyHostToDevice, m->st),
+            "ibh_model_forward_positions: tokens");
+    IBH_HIP(hipMemcpyAsync(m->bpos, pos, (size_t)n * 4, hipMemcpyHostToDevice, m->st),
+            "ibh_model_forward_positions: positions");
+    if ((rc = forward_batch(m, n))) return rc;
+    IBH_HIP(hipMemcpyAsync(logits, m->blogits, (size_t)n * vocab * 4, hipMemcpyDeviceToHost, m->st),
+            "ibh_model_forward_positions: logits");
+    IBH_HIP(hipStreamSynchronize(m->st), "ibh_model_forward_positions");
+    m->hpos += n;
+    return set_state(m, m->hpos, m->hpos);
 }
 
 extern "C" int ibh_model_generate_greedy(ibh_model* m, const int32_t* in, int n_in, int32_t* out, int max_out) {

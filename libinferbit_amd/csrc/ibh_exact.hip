@@ -240,14 +240,18 @@ __global__ __launch_bounds__(256) void matvec_exact(const RowSet rs, const float
 
 // One serial mul/add chain per row: the INT2 table kernel
 // (kernels/ternary.c:20-46), the sparse-row path of tensor_matmul_sparse
-// (forward.c:292-317: masked rows are 0) and fp16 weights (forward.c:174-182,
-// no scales).  BITS 16 ignores the scales.
+// (forward.c:292-317: masked rows are 0), fp16 weights (forward.c:174-182,
+// no scales) and the x86 table's matmul_int8_batch (kernels/scalar.c:70-84).
+// BITS 16 ignores the scales.  blockIdx.y is the batch slot: x[b*N], y[b*ys].
 template <int BITS, int KIND>
 __global__ __launch_bounds__(256) void matvec_serial_exact(float* __restrict__ y, const uint8_t* __restrict__ W,
                                                            const void* __restrict__ sc, const float* __restrict__ x,
-                                                           const uint8_t* __restrict__ mask, int M, int N) {
+                                                           const uint8_t* __restrict__ mask, int M, int N,
+                                                           int ys = 0) {
     const int row = blockIdx.x * 256 + threadIdx.x;
     if (row >= M) return;
+    x += (size_t)blockIdx.y * N;
+    y += (size_t)blockIdx.y * ys;
     if (mask && !mask[row]) {
         y[row] = 0.f;
         return;
@@ -711,6 +715,23 @@ int ibh_launch_matvec_exact_multi(const MatDesc* d, int n, int kind, const float
 #undef IBH_MX
 #undef IBH_MXA
     IBH_CHECK_LAUNCH("exact matvec");
+    return IBH_OK;
+}
+
+// matmul_int8_batch of the x86 kernel table (kernels/scalar.c:70-84):
+// out[b*M_stride + i] = (serial sum_j (float)W[i][j] * x[b][j]) * scale[i].
+int ibh_launch_int8_batch_exact(float* y, const void* w, const void* sc, int kind, const float* x, int M, int N,
+                                int B, int M_stride, hipStream_t st) {
+    if (B <= 0 || B > 65535 || M <= 0 || N <= 0) {
+        ibh_set_error("exact int8 batch: bad sizes");
+        return IBH_ERROR_PARAM;
+    }
+    const dim3 grid((M + 255) / 256, B);
+    if (kind == IBH_SCALE_F16)
+        matvec_serial_exact<8, IBH_SCALE_F16><<<grid, 256, 0, st>>>(y, (const uint8_t*)w, sc, x, nullptr, M, N, M_stride);
+    else
+        matvec_serial_exact<8, IBH_SCALE_F32><<<grid, 256, 0, st>>>(y, (const uint8_t*)w, sc, x, nullptr, M, N, M_stride);
+    IBH_CHECK_LAUNCH("exact int8 batch");
     return IBH_OK;
 }
 

@@ -55,6 +55,36 @@ class Model:
             check(n, "ibh_model_generate_greedy")
         return out[:n]
 
+    def forward_positions(self, tokens) -> np.ndarray:
+        """ib_forward_positions (src/forward.c:904-939): logits [n, vocab] of
+        every position of `tokens` (n <= 32) in one batched pass."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        V = self.dims["vocab_size"]
+        out = np.empty((len(t), V), np.float32)
+        check(lib().ibh_model_forward_positions(self._h, _ptr(t), len(t), _ptr(out), V),
+              "ibh_model_forward_positions")
+        return out
+
+    def generate_lookup(self, tokens, max_out: int, ngram: int, k: int) -> np.ndarray:
+        """inferbit_generate at temperature 0 with inferbit_set_prompt_lookup(ngram, k)
+        (src/generate.c:305-409)."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        out = np.empty(max_out, np.int32)
+        n = lib().ibh_model_generate_lookup(self._h, _ptr(t), len(t), _ptr(out), max_out, ngram, k)
+        if n < 0:
+            check(n, "ibh_model_generate_lookup")
+        return out[:n]
+
+    def generate_draft(self, draft: "Model", tokens, max_out: int, draft_k: int = 4) -> np.ndarray:
+        """inferbit_generate at temperature 0 with inferbit_set_draft_model(draft, draft_k)
+        (src/generate.c:411-520)."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        out = np.empty(max_out, np.int32)
+        n = lib().ibh_model_generate_draft(self._h, draft._h, _ptr(t), len(t), _ptr(out), max_out, draft_k)
+        if n < 0:
+            check(n, "ibh_model_generate_draft")
+        return out[:n]
+
     def kv_prefill(self, k: np.ndarray, v: np.ndarray) -> None:
         """Append positions to every layer's KV cache; k, v fp32 [layers][n_pos][kv_dim]."""
         k = np.ascontiguousarray(k, np.float32)

@@ -12,7 +12,14 @@
  * followed by V in the same layout.  Runs inferbit_generate at temperature 0
  * and prints one JSON line: generated tokens, wall seconds, tokens/s.
  * With REF_DECODE_LOGITS=path, the prompt's last-token logits are first
- * written there (fp32, vocab entries) and the cache is rewound. */
+ * written there (fp32, vocab entries) and the cache is rewound.
+ * With REF_POSITIONS=path and REF_POSITIONS_SPLIT=s, the first s prompt
+ * tokens go through inferbit_forward, the rest through ib_forward_positions
+ * (forward.c:904-939, the batched verify step); its per-position logits are
+ * written there and the cache is rewound.
+ * REF_LOOKUP="ngram,k" turns on prompt-lookup speculation
+ * (inferbit_set_prompt_lookup); REF_DRAFT=model.ibf with REF_DRAFT_K=k loads
+ * a draft model for speculative decoding (inferbit_set_draft_model). */
 #include "forward.c"
 
 #include <stdio.h>
@@ -85,6 +92,39 @@ int main(int argc, char** argv) {
         free(lg);
         inferbit_kv_truncate(m, kv0);
     }
+    const char* ppath = getenv("REF_POSITIONS");
+    if (ppath) {
+        const int kv0 = inferbit_kv_length(m), vocab = m->header.vocab_size, np = (int)(pn / 4);
+        const char* se = getenv("REF_POSITIONS_SPLIT");
+        const int split = se ? atoi(se) : 0;
+        if (split < 0 || split >= np) { fprintf(stderr, "bad REF_POSITIONS_SPLIT\n"); return 1; }
+        float* lg = malloc((size_t)vocab * (size_t)np * sizeof(float));
+        if (!lg) return 1;
+        if (split > 0 && inferbit_forward(m, prompt, split, lg, vocab) != INFERBIT_OK) return 1;
+        if (ib_forward_positions(m, prompt + split, np - split, lg) != INFERBIT_OK) {
+            fprintf(stderr, "forward_positions failed: %s\n", inferbit_last_error());
+            return 1;
+        }
+        FILE* lf = fopen(ppath, "wb");
+        if (!lf || fwrite(lg, sizeof(float), (size_t)vocab * (np - split), lf) != (size_t)vocab * (np - split)) return 1;
+        fclose(lf);
+        free(lg);
+        inferbit_kv_truncate(m, kv0);
+    }
+    const char* lk = getenv("REF_LOOKUP");
+    if (lk) {
+        int ng = 0, kk = 0;
+        if (sscanf(lk, "%d,%d", &ng, &kk) != 2) { fprintf(stderr, "bad REF_LOOKUP\n"); return 1; }
+        inferbit_set_prompt_lookup(m, ng, kk);
+    }
+    inferbit_model* draft = NULL;
+    const char* dp = getenv("REF_DRAFT");
+    if (dp) {
+        draft = inferbit_load(dp, cfg);
+        if (!draft) { fprintf(stderr, "draft load failed: %s\n", inferbit_last_error()); return 1; }
+        const char* dk = getenv("REF_DRAFT_K");
+        inferbit_set_draft_model(m, draft, dk ? atoi(dk) : 4);
+    }
     inferbit_sample_params sp = inferbit_default_sample_params();
     sp.temperature = 0.0f;
     int32_t* out = malloc((size_t)n_out * sizeof(int32_t));
@@ -97,6 +137,7 @@ int main(int argc, char** argv) {
     for (int i = 0; i < n; i++) printf("%s%d", i ? ", " : "", out[i]);
     printf("]}\n");
     inferbit_free(m);
+    if (draft) inferbit_free(draft);
     inferbit_config_free(cfg);
     return 0;
 }

@@ -4,6 +4,8 @@ import ctypes
 import os
 import re
 
+import pytest
+
 from conftest import ROOT
 
 
@@ -42,3 +44,30 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
         assert "no CPU fallback" in str(e)
     else:
         raise AssertionError("expected a loud failure")
+
+
+def test_prompt_lookup_search_matches_reference():
+    """ibh_prompt_lookup_search (host code, no GPU) against the compiled
+    reference's ib_prompt_lookup_search on random short histories."""
+    import ctypes
+    import numpy as np
+    from oracle import refbind as R
+    if not R.available():
+        pytest.skip("reference library not built")
+    from libinferbit_amd import _lib
+    ours, theirs = _lib.lib(), R.lib()
+    theirs.ib_prompt_lookup_search.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                               ctypes.c_void_p]
+    rng = np.random.default_rng(0)
+    hits = 0
+    for _ in range(2000):
+        h = rng.integers(0, 4, rng.integers(0, 30)).astype(np.int32)
+        ng, k = int(rng.integers(0, 5)), int(rng.integers(0, 10))
+        a, b = np.full(16, -1, np.int32), np.full(16, -1, np.int32)
+        na = ours.ibh_prompt_lookup_search(h.ctypes.data_as(ctypes.c_void_p), len(h), ng, k,
+                                           a.ctypes.data_as(ctypes.c_void_p))
+        nb = theirs.ib_prompt_lookup_search(h.ctypes.data_as(ctypes.c_void_p), len(h), ng, k,
+                                            b.ctypes.data_as(ctypes.c_void_p))
+        assert na == nb and (a == b).all()
+        hits += na > 0
+    assert hits > 100
