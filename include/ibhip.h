@@ -152,7 +152,23 @@ typedef struct {
     const int8_t* outlier_sidecar;
     const uint16_t* outlier_scale;
     const int32_t* inner_cols;
+    int format;          /* ib_pq_format (pq_decode.h:26-33); 4 = pyramid, used by L2SKIP */
 } ibh_pq_tensor;
+
+#define IBH_PQ_FORMAT_PYRAMID 4
+
+/* ib_pq_policy (src/pq_decode.h:331-343): the PQ session's per-tensor
+ * kernel choice. */
+#define IBH_PQ_VARIANT_STREAMING 0   /* every chunk, full pyramid */
+#define IBH_PQ_VARIANT_L1_ONLY   1   /* level 1 only */
+#define IBH_PQ_VARIANT_L2SKIP    2   /* level-2 pair skipped per (row, chunk) when |l1| > thr * bound */
+#define IBH_PQ_VARIANT_SPARSE    3   /* chunks with every |x| <= act_threshold skipped */
+#define IBH_PQ_VARIANT_INT8      4   /* int8 codebooks and chunk activations */
+typedef struct {
+    int   variant;
+    float skip_threshold;   /* L2SKIP */
+    float act_threshold;    /* SPARSE */
+} ibh_pq_policy;
 
 /* out[M] = W x for a PQ tensor, replacing ib_pq_matmul_fp32 /
  * ib_pq_matmul_fp32_threaded (src/pq_decode.c:1684-1810): same chunk
@@ -168,6 +184,17 @@ int    ibh_pq_matmul(const ibh_pq_tensor* t, const float* x, float* out, void* w
  * skipping rule).  G <= 32 as in the reference.  Same workspace. */
 int    ibh_pq_matmul_streaming(const ibh_pq_tensor* t, const float* x, float* out, void* ws,
                                size_t ws_bytes, void* stream);
+/* ib_pq_session_matmul's dispatch on a PQ tensor's policy
+ * (src/pq_decode.c:4464-4491): STREAMING -> streaming_cached (2927-2998),
+ * L1_ONLY -> ib_pq_matmul_fp32_l1_only (2085-2139), L2SKIP ->
+ * l2skip_cached (3159-3235, cluster bounds of lut_cache_create 2655-2675),
+ * SPARSE -> streaming_sparse (1814-1928), INT8 -> streaming_int8_cached
+ * (2858-2925 after lut_cache_quantize_int8 2766-2812); other values run
+ * STREAMING, as the reference's default branch.  G <= 32.  The skip
+ * decisions compare GPU-rounded tables, so a decision that sits within
+ * fp32 rounding of its threshold may go the other way.  Same workspace. */
+int    ibh_pq_matmul_policy(const ibh_pq_tensor* t, const float* x, float* out, const ibh_pq_policy* policy,
+                            void* ws, size_t ws_bytes, void* stream);
 
 /* ── IBF v5 INT4 group-scale matvec, device pointers ───────── */
 

@@ -38,6 +38,7 @@ SIGNATURES = {
     "ibh_pq_workspace_bytes": (SZ, [P]),
     "ibh_pq_matmul": (I, [P, P, P, P, SZ, P]),
     "ibh_pq_matmul_streaming": (I, [P, P, P, P, SZ, P]),
+    "ibh_pq_matmul_policy": (I, [P, P, P, P, P, SZ, P]),
     "ibh_int4g_workspace_bytes": (SZ, [P]),
     "ibh_int4g_matmul": (I, [P, P, P, C.c_float, P, SZ, P]),
     "ibh_int4g_matmul_batched": (I, [P, I, P, P, C.c_float, P, SZ, P]),
@@ -109,7 +110,13 @@ class PqTensor(C.Structure):
     _fields_ = [(n, I) for n in ("M", "N", "G", "K", "K_l2", "n_levels", "n_outlier", "C", "l2_idx_bytes")] + \
                [(n, P) for n in ("codebook_l1_l", "codebook_l1_r", "codebook_l2_l", "codebook_l2_r",
                                  "indices_l1_l", "indices_l1_r", "indices_l2_l", "indices_l2_r", "row_scale",
-                                 "outlier_cols", "outlier_sidecar", "outlier_scale", "inner_cols")]
+                                 "outlier_cols", "outlier_sidecar", "outlier_scale", "inner_cols")] + \
+               [("format", I)]
+
+
+class PqPolicy(C.Structure):
+    """ibh_pq_policy (include/ibhip.h)."""
+    _fields_ = [("variant", I), ("skip_threshold", C.c_float), ("act_threshold", C.c_float)]
 
 
 class Int4gTensor(C.Structure):

@@ -34,7 +34,17 @@ constexpr int kThreads = 256;
 
 struct PqDev {
     int M, N, G, K, K2, n_levels, n_outlier, C, l2_idx_bytes;
-    float skip_frac;         // chunk kept iff its max|x| >= skip_frac * max|x| (0: every chunk)
+    // chunk selection: 0 every chunk; 1 kept iff max|x_c| >= skip_val * max|x|
+    // (matmul_impl); 2 kept iff max|x_c| > skip_val when skip_val > 0
+    // (streaming_sparse)
+    int skip_mode;
+    float skip_val;
+    int q8;                  // int8 codebooks and chunk activations (streaming_int8_cached)
+    int l2skip;              // per-(row, chunk) level-2 skip (l2skip_cached) with threshold l2_thr
+    float l2_thr;
+    int pyramid;             // per-cluster level-2 norm bound (format 4)
+    const float* cnorm;      // [C][2] |x_L|, |x_R| per chunk (l2skip)
+    const float* c2max;      // [2][n_outer] max level-2 codeword norm per cluster (l2skip)
     const uint16_t *cb1l, *cb1r, *cb2l, *cb2r;
     const uint8_t *i1l, *i1r, *i2l, *i2r;
     const uint16_t* row_scale;
@@ -72,10 +82,34 @@ __device__ __forceinline__ float table_entry(const uint16_t* cb, const float* xv
 // Tables of one chunk, built once: T1[c][side][k] (and T2) written to global
 // memory with the chunk's max|x| (the skipping rule is applied by the
 // gather, which has every chunk's max).
+// Round-half-away int8 code of v * inv, clamped to +-127
+// (pq_quantize_codebook_int8 / pq_quantize_chunk_int8, pq_decode.c:2766-2856).
+__device__ __forceinline__ int q8_code(float v, float inv) {
+    const float u = v * inv;
+    const int q = (int)(u >= 0.0f ? u + 0.5f : u - 0.5f);
+    return q > 127 ? 127 : (q < -127 ? -127 : q);
+}
+
+// int8 table entry (pq_chunk_dot_table_int8, pq_decode.c:2817-2836): the
+// codeword quantised with its own scale, exact int32 dot with the chunk's
+// codes, then (float)dot * cb_scale * x_scale.
+__device__ __forceinline__ float table_entry_q8(const uint16_t* cb, const int8_t* xq, float xsc, int hf) {
+    float m = 0.f;
+    for (int i = 0; i < hf; i++) m = fmaxf(m, fabsf(f16_to_f32(cb[i])));
+    const float cs = m > 0.f ? m / 127.0f : 1.0f;
+    const float inv = 1.0f / cs;
+    int sum = 0;
+    for (int i = 0; i < hf; i++) sum += q8_code(f16_to_f32(cb[i]), inv) * (int)xq[i];
+    return (float)sum * cs * xsc;
+}
+
 template <bool TWO>
 __global__ __launch_bounds__(kThreads) void pq_tables(PqDev t, const float* __restrict__ x, float* __restrict__ tab1,
-                                                      float* __restrict__ tab2, float* __restrict__ cmax) {
+                                                      float* __restrict__ tab2, float* __restrict__ cmax,
+                                                      float* __restrict__ cnorm) {
     __shared__ float xs[64];
+    __shared__ int8_t xq[2][32];
+    __shared__ float xsc[2];
     const int K = t.K, K2 = t.K2, G = t.G, hf = G / 2;
     const int c = blockIdx.x;
     if (threadIdx.x < G) xs[threadIdx.x] = x[inner_col(t, c * G + threadIdx.x)];
@@ -85,17 +119,60 @@ __global__ __launch_bounds__(kThreads) void pq_tables(PqDev t, const float* __re
         for (int i = 0; i < G; i++) cm = fmaxf(cm, fabsf(xs[i]));
         cmax[c] = cm;
     }
+    if (threadIdx.x < 2 && (t.l2skip || t.q8)) {
+        // this side's |x| (l2skip) and int8 codes (q8)
+        const float* v = xs + threadIdx.x * hf;
+        float n2 = 0.f, m = 0.f;
+        for (int i = 0; i < hf; i++) {
+            n2 = fmaf(v[i], v[i], n2);
+            m = fmaxf(m, fabsf(v[i]));
+        }
+        if (t.l2skip) cnorm[2 * c + threadIdx.x] = sqrtf(n2);
+        const float sc = m > 0.f ? m / 127.0f : 1.0f;
+        const float inv = 1.0f / sc;
+        for (int i = 0; i < hf; i++) xq[threadIdx.x][i] = (int8_t)q8_code(v[i], inv);
+        xsc[threadIdx.x] = sc;
+    }
+    if (t.q8) __syncthreads();
     for (int e = threadIdx.x; e < 2 * K; e += kThreads) {
         const int side = e / K, k = e % K;
         const uint16_t* cb = (side ? t.cb1r : t.cb1l) + (size_t)k * hf;
-        tab1[(size_t)c * 2 * K + e] = table_entry(cb, xs + side * hf, hf);
+        tab1[(size_t)c * 2 * K + e] = t.q8 ? table_entry_q8(cb, xq[side], xsc[side], hf) : table_entry(cb, xs + side * hf, hf);
     }
     if (TWO) {
         for (int e = threadIdx.x; e < 2 * K2; e += kThreads) {
             const int side = e / K2, k = e % K2;
             const uint16_t* cb = (side ? t.cb2r : t.cb2l) + (size_t)k * hf;
-            tab2[(size_t)c * 2 * K2 + e] = table_entry(cb, xs + side * hf, hf);
+            tab2[(size_t)c * 2 * K2 + e] =
+                t.q8 ? table_entry_q8(cb, xq[side], xsc[side], hf) : table_entry(cb, xs + side * hf, hf);
         }
+    }
+}
+
+// Max level-2 codeword norm per cluster (ib_pq_lut_cache_create,
+// pq_decode.c:2655-2675): block per cluster; c2max[0][k1] (L), [1][k1] (R).
+__global__ __launch_bounds__(kThreads) void pq_c2max(PqDev t, float* __restrict__ c2max, int n_outer, int k_inner) {
+    __shared__ float red[2][kThreads / 64];
+    const int k1 = blockIdx.x, hf = t.G / 2, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float ml = 0.f, mr = 0.f;
+    for (int k = k1 * k_inner + (int)threadIdx.x; k < (k1 + 1) * k_inner; k += kThreads) {
+        float nl = 0.f, nr = 0.f;
+        for (int j = 0; j < hf; j++) {
+            const float a = f16_to_f32(t.cb2l[(size_t)k * hf + j]), b = f16_to_f32(t.cb2r[(size_t)k * hf + j]);
+            nl = fmaf(a, a, nl);
+            nr = fmaf(b, b, nr);
+        }
+        ml = fmaxf(ml, sqrtf(nl));
+        mr = fmaxf(mr, sqrtf(nr));
+    }
+    ml = wave_max(ml);
+    mr = wave_max(mr);
+    if (lane == 0) { red[0][wave] = ml; red[1][wave] = mr; }
+    __syncthreads();
+    if (threadIdx.x < 2) {
+        float m = 0.f;
+        for (int w = 0; w < kThreads / 64; w++) m = fmaxf(m, red[threadIdx.x][w]);
+        c2max[threadIdx.x * n_outer + k1] = m;
     }
 }
 
@@ -153,6 +230,15 @@ __device__ void finish_rows(const PqDev& t, const float* __restrict__ x, const f
     }
 }
 
+// Level-2 skip of one (row, chunk) (l2skip_cached, pq_decode.c:3203-3214):
+// |l1| > thr * (c2L * |x_L| + c2R * |x_R|), with per-cluster bounds for a
+// pyramid tensor (cluster = the row's level-1 code of that side).
+__device__ __forceinline__ bool l2_skipped(const PqDev& t, float l1, const float (*c2)[256], const float* nrm, int a,
+                                           int b) {
+    const float bound = t.l2_thr * fmaf(c2[0][t.pyramid ? a : 0], nrm[0], c2[1][t.pyramid ? b : 0] * nrm[1]);
+    return fabsf(l1) > bound;
+}
+
 // Block (row tile, slab): the slab's tables into LDS, then each thread walks
 // its rows (CS index bytes per side from one 16-byte load, 2 CS gathers).
 template <bool TWO>
@@ -162,6 +248,8 @@ __global__ __launch_bounds__(kThreads) void pq_gather(PqDev t, const float* __re
     extern __shared__ __align__(16) float sm[];
     __shared__ float red[kThreads / 64];
     __shared__ int act_s[64];
+    __shared__ float nrm_s[64][2];            // l2skip: |x_L|, |x_R| of the slab's chunks
+    __shared__ float c2_s[2][256];            // l2skip: cluster bounds (pyramid: per level-1 code)
     const int K = t.K, K2 = t.K2, C = t.C;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     float* T1 = sm;                                   // [CS][2][K]
@@ -195,7 +283,17 @@ __global__ __launch_bounds__(kThreads) void pq_gather(PqDev t, const float* __re
     __syncthreads();
     float gmax = 0.f;
     for (int w = 0; w < kThreads / 64; w++) gmax = fmaxf(gmax, red[w]);
-    if (threadIdx.x < cn) act_s[threadIdx.x] = gmax > 0.f ? (cmax[c0 + threadIdx.x] >= gmax * t.skip_frac) : 1;
+    if (threadIdx.x < cn) {
+        const float cm = cmax[c0 + threadIdx.x];
+        act_s[threadIdx.x] = t.skip_mode == 1 ? (gmax > 0.f ? cm >= gmax * t.skip_val : 1)
+                           : t.skip_mode == 2 ? (t.skip_val > 0.f ? cm > t.skip_val : 1) : 1;
+    }
+    const bool l2skip = TWO && t.l2skip && t.l2_thr > 0.f;
+    if (l2skip) {
+        const int no = t.pyramid ? K : 1;
+        for (int i = threadIdx.x; i < 2 * no; i += kThreads) c2_s[i / no][i % no] = t.c2max[i];
+        if (threadIdx.x < 2 * cn) nrm_s[threadIdx.x >> 1][threadIdx.x & 1] = t.cnorm[2 * c0 + threadIdx.x];
+    }
     __syncthreads();
 
     const size_t l2s = TWO ? l2_stride(t) : 0;
@@ -216,8 +314,9 @@ __global__ __launch_bounds__(kThreads) void pq_gather(PqDev t, const float* __re
                 if (!act_s[c]) continue;
                 const float* tc = T1 + (size_t)c * 2 * K;
                 const int a = (aw[c >> 2] >> (8 * (c & 3))) & 0xff, b = (bw[c >> 2] >> (8 * (c & 3))) & 0xff;
-                acc = acc + (tc[a] + tc[K + b]);
-                if (TWO) {
+                const float l1 = tc[a] + tc[K + b];
+                acc = acc + l1;
+                if (TWO && !(l2skip && l2_skipped(t, l1, c2_s, nrm_s[c], a, b))) {
                     const float* t2 = T2 + (size_t)c * 2 * K2;
                     acc = acc + (t2[l2_at(t, i2l, c0 + c)] + t2[K2 + l2_at(t, i2r, c0 + c)]);
                 }
@@ -226,8 +325,10 @@ __global__ __launch_bounds__(kThreads) void pq_gather(PqDev t, const float* __re
             for (int c = 0; c < cn; c++) {
                 if (!act_s[c]) continue;
                 const float* tc = T1 + (size_t)c * 2 * K;
-                acc = acc + (tc[il[c]] + tc[K + ir[c]]);
-                if (TWO) {
+                const int a = il[c], b = ir[c];
+                const float l1 = tc[a] + tc[K + b];
+                acc = acc + l1;
+                if (TWO && !(l2skip && l2_skipped(t, l1, c2_s, nrm_s[c], a, b))) {
                     const float* t2 = T2 + (size_t)c * 2 * K2;
                     acc = acc + (t2[l2_at(t, i2l, c0 + c)] + t2[K2 + l2_at(t, i2r, c0 + c)]);
                 }
@@ -253,10 +354,13 @@ void* ibh_workspace(size_t bytes);
 
 typedef ibh_pq_tensor ibh_pq_tensor_abi;
 
-// Slab of CS chunks per table / gather block; workspace = both levels' tables
-// for all chunks, then the per-slab partial sums.
-static int pq_geometry(const ibh_pq_tensor_abi* t, int* CS, int* nslabs, size_t* lds, size_t* ws_need,
-                       size_t* tab1_off, size_t* tab2_off, size_t* part_off) {
+// Workspace: both levels' tables for all chunks, the per-slab partial sums,
+// then the chunk maxima, the chunk norms and the cluster bounds.
+struct PqWs {
+    size_t tab1, tab2, part, cmax, cnorm, c2max, need;
+};
+
+static int pq_geometry(const ibh_pq_tensor_abi* t, int* CS, int* nslabs, size_t* lds, PqWs* w) {
     const bool two = t->n_levels == 2;
     const int K2 = t->K_l2 > 0 ? t->K_l2 : t->K;
     int cs = 16;
@@ -267,85 +371,150 @@ static int pq_geometry(const ibh_pq_tensor_abi* t, int* CS, int* nslabs, size_t*
     *nslabs = (t->C + cs - 1) / cs;
     *lds = need(cs);
     auto al = [](size_t v) { return (v + 255) / 256 * 256; };
-    *tab1_off = 0;
-    *tab2_off = al((size_t)t->C * 2 * t->K * 4);
-    *part_off = *tab2_off + (two ? al((size_t)t->C * 2 * K2 * 4) : 0);
-    *ws_need = *part_off + al((size_t)(*nslabs) * t->M * sizeof(float)) + (size_t)t->C * sizeof(float);
+    w->tab1 = 0;
+    w->tab2 = al((size_t)t->C * 2 * t->K * 4);
+    w->part = w->tab2 + (two ? al((size_t)t->C * 2 * K2 * 4) : 0);
+    w->cmax = w->part + al((size_t)(*nslabs) * t->M * sizeof(float));
+    w->cnorm = w->cmax + al((size_t)t->C * sizeof(float));
+    w->c2max = w->cnorm + al((size_t)t->C * 2 * sizeof(float));
+    w->need = w->c2max + al((size_t)2 * (t->K + 1) * sizeof(float));
     return IBH_OK;
 }
 
 extern "C" size_t ibh_pq_workspace_bytes(const ibh_pq_tensor_abi* t) {
     int cs, ns;
-    size_t lds, need, o1, o2, o3;
-    return t && pq_geometry(t, &cs, &ns, &lds, &need, &o1, &o2, &o3) == IBH_OK ? need : 0;
+    size_t lds;
+    PqWs w;
+    return t && pq_geometry(t, &cs, &ns, &lds, &w) == IBH_OK ? w.need : 0;
 }
 
+namespace {
+struct PqMode {
+    int skip_mode = 1;        // see PqDev
+    float skip_val = 0.01f;
+    bool level2 = true;       // false: level 1 only
+    bool q8 = false;
+    bool l2skip = false;
+    float l2_thr = 0.f;
+};
+}  // namespace
+
 static int pq_run(const ibh_pq_tensor_abi* t, const float* x, float* out, void* ws, size_t ws_bytes, void* stream,
-                  float skip_frac);
+                  const PqMode& md, const char* who);
 
 extern "C" int ibh_pq_matmul(const ibh_pq_tensor_abi* t, const float* x, float* out, void* ws, size_t ws_bytes,
                              void* stream) {
-    return pq_run(t, x, out, ws, ws_bytes, stream, 0.01f);
+    return pq_run(t, x, out, ws, ws_bytes, stream, PqMode{}, "ibh_pq_matmul");
 }
 
 extern "C" int ibh_pq_matmul_streaming(const ibh_pq_tensor_abi* t, const float* x, float* out, void* ws,
                                        size_t ws_bytes, void* stream) {
-    if (t && t->G > 32) {
-        ibh_set_error("ibh_pq_matmul_streaming: G=%d > 32 (the reference's chunk buffers hold 16 per side)", t->G);
+    const ibh_pq_policy p{IBH_PQ_VARIANT_STREAMING, 0.f, 0.f};
+    return ibh_pq_matmul_policy(t, x, out, &p, ws, ws_bytes, stream);
+}
+
+// ib_pq_session_matmul's dispatch on the tensor's policy (pq_decode.c:4468-4491).
+extern "C" int ibh_pq_matmul_policy(const ibh_pq_tensor_abi* t, const float* x, float* out, const ibh_pq_policy* p,
+                                    void* ws, size_t ws_bytes, void* stream) {
+    if (!p) {
+        ibh_set_error("ibh_pq_matmul_policy: null policy");
         return IBH_ERROR_PARAM;
     }
-    return pq_run(t, x, out, ws, ws_bytes, stream, 0.0f);
+    if (t && t->G > 32) {
+        ibh_set_error("ibh_pq_matmul_policy: G=%d > 32 (the reference's chunk buffers hold 16 per side)", t->G);
+        return IBH_ERROR_PARAM;
+    }
+    PqMode md;
+    md.skip_mode = 0;
+    switch (p->variant) {
+    case IBH_PQ_VARIANT_L1_ONLY:
+        md.level2 = false;
+        break;
+    case IBH_PQ_VARIANT_L2SKIP:
+        md.l2skip = true;
+        md.l2_thr = p->skip_threshold;
+        if (t && t->format == IBH_PQ_FORMAT_PYRAMID && t->K > 256) {
+            ibh_set_error("ibh_pq_matmul_policy: pyramid L2SKIP supports K <= 256 (K=%d)", t->K);
+            return IBH_ERROR_PARAM;
+        }
+        break;
+    case IBH_PQ_VARIANT_SPARSE:
+        md.skip_mode = 2;
+        md.skip_val = p->act_threshold;
+        break;
+    case IBH_PQ_VARIANT_INT8:
+        md.q8 = true;
+        break;
+    default:   // STREAMING, and the reference's default branch
+        break;
+    }
+    return pq_run(t, x, out, ws, ws_bytes, stream, md, "ibh_pq_matmul_policy");
 }
 
 static int pq_run(const ibh_pq_tensor_abi* t, const float* x, float* out, void* ws, size_t ws_bytes, void* stream,
-                  float skip_frac) {
+                  const PqMode& md, const char* who) {
     if (!t || !x || !out || t->M <= 0 || t->C <= 0 || t->G <= 0 || t->G % 2 || t->G > 64 || t->K <= 0 || t->K > 65536 ||
         !t->codebook_l1_l || !t->codebook_l1_r || !t->indices_l1_l || !t->indices_l1_r || !t->row_scale ||
         t->N != t->C * t->G + t->n_outlier || t->n_outlier < 0 || t->n_outlier > 1024 ||
         (t->n_outlier > 0 && (!t->outlier_cols || !t->outlier_sidecar || !t->outlier_scale || !t->inner_cols)) ||
         (t->n_levels == 2 && (!t->codebook_l2_l || !t->codebook_l2_r || !t->indices_l2_l || !t->indices_l2_r)) ||
         (t->n_levels != 1 && t->n_levels != 2)) {
-        ibh_set_error("ibh_pq_matmul: invalid tensor");
+        ibh_set_error("%s: invalid tensor", who);
         return IBH_ERROR_PARAM;
     }
     if (t->K > 256 && t->n_levels == 1) {
         // level-1 indices are uint8 (pq_decode.h:59-60)
-        ibh_set_error("ibh_pq_matmul: K=%d exceeds uint8 level-1 indices", t->K);
+        ibh_set_error("%s: K=%d exceeds uint8 level-1 indices", who, t->K);
         return IBH_ERROR_PARAM;
     }
     int CS, nslabs;
-    size_t lds, need, tab1_off, tab2_off, part_off;
-    if (pq_geometry(t, &CS, &nslabs, &lds, &need, &tab1_off, &tab2_off, &part_off) != IBH_OK) {
-        ibh_set_error("ibh_pq_matmul: codebooks too large for the LDS tables");
+    size_t lds;
+    PqWs w;
+    if (pq_geometry(t, &CS, &nslabs, &lds, &w) != IBH_OK) {
+        ibh_set_error("%s: codebooks too large for the LDS tables", who);
         return IBH_ERROR_PARAM;
     }
     if (!ws) {
-        ws = ibh_workspace(need);
-        ws_bytes = ws ? need : 0;
+        ws = ibh_workspace(w.need);
+        ws_bytes = ws ? w.need : 0;
     }
-    if (!ws || ws_bytes < need) {
-        ibh_set_error("ibh_pq_matmul: workspace of %zu bytes needed", need);
+    if (!ws || ws_bytes < w.need) {
+        ibh_set_error("%s: workspace of %zu bytes needed", who, w.need);
         return IBH_ERROR_MEMORY;
     }
+    const bool two = t->n_levels == 2 && md.level2;
     PqDev d;
     d.M = t->M; d.N = t->N; d.G = t->G; d.K = t->K; d.K2 = t->K_l2 > 0 ? t->K_l2 : t->K;
-    d.n_levels = t->n_levels; d.n_outlier = t->n_outlier; d.C = t->C; d.skip_frac = skip_frac;
+    d.n_levels = t->n_levels; d.n_outlier = t->n_outlier; d.C = t->C;
+    d.skip_mode = md.skip_mode; d.skip_val = md.skip_val; d.q8 = md.q8;
+    d.l2skip = two && md.l2skip && md.l2_thr > 0.f; d.l2_thr = md.l2_thr;
+    d.pyramid = t->format == IBH_PQ_FORMAT_PYRAMID;
     d.l2_idx_bytes = t->l2_idx_bytes > 0 ? t->l2_idx_bytes : 1;
     d.cb1l = t->codebook_l1_l; d.cb1r = t->codebook_l1_r; d.cb2l = t->codebook_l2_l; d.cb2r = t->codebook_l2_r;
     d.i1l = t->indices_l1_l; d.i1r = t->indices_l1_r; d.i2l = t->indices_l2_l; d.i2r = t->indices_l2_r;
     d.row_scale = t->row_scale; d.ocols = t->outlier_cols; d.oside = t->outlier_sidecar;
     d.oscale = t->outlier_scale; d.inner = t->n_outlier > 0 ? t->inner_cols : nullptr;
     hipStream_t st = ibh_resolve_stream(stream);
-    float* tab1 = (float*)((char*)ws + tab1_off);
-    float* tab2 = (float*)((char*)ws + tab2_off);
-    float* part = (float*)((char*)ws + part_off);
-    const size_t cmax_off = part_off + ((size_t)nslabs * t->M * sizeof(float) + 255) / 256 * 256;
-    float* cmax = (float*)((char*)ws + cmax_off);
-    if (t->n_levels == 2) pq_tables<true><<<t->C, kThreads, 0, st>>>(d, x, tab1, tab2, cmax);
-    else pq_tables<false><<<t->C, kThreads, 0, st>>>(d, x, tab1, tab2, cmax);
+    char* base = (char*)ws;
+    float* tab1 = (float*)(base + w.tab1);
+    float* tab2 = (float*)(base + w.tab2);
+    float* part = (float*)(base + w.part);
+    float* cmax = (float*)(base + w.cmax);
+    float* cnorm = (float*)(base + w.cnorm);
+    float* c2max = (float*)(base + w.c2max);
+    d.cnorm = cnorm;
+    d.c2max = c2max;
+    if (d.l2skip) {
+        const int n_outer = d.pyramid ? t->K : 1;
+        const int k_inner = d.pyramid ? d.K2 / t->K : d.K2;
+        pq_c2max<<<n_outer, kThreads, 0, st>>>(d, c2max, n_outer, k_inner);
+        IBH_CHECK_LAUNCH("ibh_pq_matmul (cluster bounds)");
+    }
+    if (two) pq_tables<true><<<t->C, kThreads, 0, st>>>(d, x, tab1, tab2, cmax, cnorm);
+    else pq_tables<false><<<t->C, kThreads, 0, st>>>(d, x, tab1, tab2, cmax, cnorm);
     IBH_CHECK_LAUNCH("ibh_pq_matmul (tables)");
     dim3 grid((t->M + kRowsPerBlock - 1) / kRowsPerBlock, nslabs);
-    if (t->n_levels == 2) pq_gather<true><<<grid, kThreads, lds, st>>>(d, tab1, tab2, cmax, part, CS);
+    if (two) pq_gather<true><<<grid, kThreads, lds, st>>>(d, tab1, tab2, cmax, part, CS);
     else pq_gather<false><<<grid, kThreads, lds, st>>>(d, tab1, tab2, cmax, part, CS);
     IBH_CHECK_LAUNCH("ibh_pq_matmul (gather)");
     pq_reduce<<<(t->M + kThreads - 1) / kThreads, kThreads, 0, st>>>(d, x, part, nslabs, out);

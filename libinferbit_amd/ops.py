@@ -15,7 +15,7 @@ import ctypes
 
 import numpy as np
 
-from ._lib import Int4gTensor, PqTensor, check, lib
+from ._lib import Int4gTensor, PqPolicy, PqTensor, check, lib
 
 SCALE_F16, SCALE_F32 = 0, 1
 
@@ -125,6 +125,7 @@ class PqDeviceTensor:
             setattr(s, n, int(t[n]))
         s.K_l2 = int(t.get("K_l2", 0))
         s.l2_idx_bytes = int(t.get("l2_idx_bytes", 1))
+        s.format = int(t.get("format", 0))
         for k, f in self._MAP.items():
             a = t.get(k)
             if a is not None:
@@ -140,15 +141,25 @@ class PqDeviceTensor:
             s.inner_cols = d.data_ptr()
         self.s = s
         self.M = s.M
+        # a workspace of its own (tables, slab partials), allocated once
+        self.ws = torch.empty(max(1, lib().ibh_pq_workspace_bytes(ctypes.byref(s))), dtype=torch.uint8,
+                              device="cuda")
 
     def matmul(self, x, out) -> None:
         """ib_pq_matmul_fp32 (src/pq_decode.c:1684)."""
-        check(lib().ibh_pq_matmul(ctypes.byref(self.s), _ptr(x), _ptr(out), None, 0, _stream()), "ibh_pq_matmul")
+        check(lib().ibh_pq_matmul(ctypes.byref(self.s), _ptr(x), _ptr(out), _ptr(self.ws), self.ws.numel(),
+                                  _stream()), "ibh_pq_matmul")
+
+    def matmul_policy(self, x, out, variant: int, skip_threshold: float = 0.0, act_threshold: float = 0.0) -> None:
+        """ib_pq_session_matmul with an ib_pq_policy (src/pq_decode.c:4464-4491)."""
+        p = PqPolicy(variant, skip_threshold, act_threshold)
+        check(lib().ibh_pq_matmul_policy(ctypes.byref(self.s), _ptr(x), _ptr(out), ctypes.byref(p), _ptr(self.ws),
+                                         self.ws.numel(), _stream()), "ibh_pq_matmul_policy")
 
     def matmul_streaming(self, x, out) -> None:
         """ib_pq_matmul_fp32_streaming_cached (src/pq_decode.c:2987): every chunk."""
-        check(lib().ibh_pq_matmul_streaming(ctypes.byref(self.s), _ptr(x), _ptr(out), None, 0, _stream()),
-              "ibh_pq_matmul_streaming")
+        check(lib().ibh_pq_matmul_streaming(ctypes.byref(self.s), _ptr(x), _ptr(out), _ptr(self.ws),
+                                            self.ws.numel(), _stream()), "ibh_pq_matmul_streaming")
 
 
 class Int4gDeviceTensor:

@@ -737,6 +737,131 @@ int or_pq_matmul_streaming(const or_pq_tensor* t, const float* x, float* out) {
     return 0;
 }
 
+/* pq_quantize_codebook_int8 / pq_quantize_chunk_int8 (pq_decode.c:2766-2791,
+ * 2838-2856): scale = max|v|/127 (1 if 0), codes round half away from zero,
+ * clamped to +-127. */
+static float pq_q8(const float* v, int n, int8_t* q) {
+    float m = 0.0f;
+    for (int j = 0; j < n; j++) { float a = fabsf(v[j]); if (a > m) m = a; }
+    float sc = m > 0.0f ? m / 127.0f : 1.0f;
+    float inv = 1.0f / sc;
+    for (int j = 0; j < n; j++) {
+        float u = v[j] * inv;
+        int qi = (int)(u >= 0.0f ? u + 0.5f : u - 0.5f);
+        if (qi > 127) qi = 127;
+        if (qi < -127) qi = -127;
+        q[j] = (int8_t)qi;
+    }
+    return sc;
+}
+
+/* Per-cluster max L2 codeword norm (ib_pq_lut_cache_create,
+ * pq_decode.c:2655-2675): norms accumulate with fused multiply-adds in the
+ * x86 build, then sqrtf. */
+static void pq_c2max(const or_pq_tensor* t, int pyramid, float* ml_out, float* mr_out) {
+    int K2 = t->K_l2 > 0 ? t->K_l2 : t->K, hf = t->G / 2;
+    int n_outer = (pyramid && t->K > 0) ? t->K : 1;
+    int K_inner = (pyramid && t->K > 0) ? K2 / t->K : K2;
+    for (int k1 = 0; k1 < n_outer; k1++) {
+        float ml = 0.0f, mr = 0.0f;
+        int lo = pyramid ? k1 * K_inner : 0, hi = pyramid ? (k1 + 1) * K_inner : K2;
+        for (int k = lo; k < hi; k++) {
+            float nl = 0.0f, nr = 0.0f;
+            for (int j = 0; j < hf; j++) {
+                float a = or_fp16_to_fp32(t->cb2l[(size_t)k * hf + j]);
+                float b = or_fp16_to_fp32(t->cb2r[(size_t)k * hf + j]);
+                nl = fmaf(a, a, nl);
+                nr = fmaf(b, b, nr);
+            }
+            nl = sqrtf(nl); nr = sqrtf(nr);
+            if (nl > ml) ml = nl;
+            if (nr > mr) mr = nr;
+        }
+        ml_out[k1] = ml;
+        mr_out[k1] = mr;
+    }
+}
+
+int or_pq_matmul_variant(const or_pq_tensor* t, const float* x, float* out, int variant, float skip_threshold,
+                         float act_threshold, int pyramid) {
+    if (variant == 0) return or_pq_matmul_streaming(t, x, out);
+    int M = t->M, G = t->G, C = t->C, K = t->K, hf = G / 2;
+    if (hf > 16 || variant < 1 || variant > 4) return -1;
+    int K2 = t->K_l2 > 0 ? t->K_l2 : K;
+    int two = t->n_levels == 2 && variant != 1;
+    if (variant == 2 && t->n_levels != 2) return or_pq_matmul_streaming(t, x, out);
+    int* ic = pq_inner_cols(t);
+    size_t l2s = pq_l2_stride(t);
+    float* tab = (float*)malloc(sizeof(float) * (size_t)(2 * K + 2 * K2));
+    float* cb = (float*)malloc(sizeof(float) * (size_t)hf);
+    int8_t* cbq = (int8_t*)malloc((size_t)hf);
+    float* c2l = (float*)malloc(sizeof(float) * (size_t)(K + 1));
+    float* c2r = (float*)malloc(sizeof(float) * (size_t)(K + 1));
+    if (variant == 2) pq_c2max(t, pyramid, c2l, c2r);
+    for (int r = 0; r < M; r++) out[r] = 0.0f;
+    for (int c = 0; c < C; c++) {
+        float xl[16], xr[16], nl2 = 0.0f, nr2 = 0.0f;
+        for (int j = 0; j < hf; j++) {
+            xl[j] = x[ic[c * G + j]];
+            xr[j] = x[ic[c * G + hf + j]];
+            nl2 = fmaf(xl[j], xl[j], nl2);
+            nr2 = fmaf(xr[j], xr[j], nr2);
+        }
+        if (variant == 3 && act_threshold > 0.0f) {
+            int small = 1;
+            for (int j = 0; j < hf; j++)
+                if (fabsf(xl[j]) > act_threshold || fabsf(xr[j]) > act_threshold) { small = 0; break; }
+            if (small) continue;
+        }
+        int8_t xq[2][16];
+        float xsc[2] = {0.0f, 0.0f};
+        if (variant == 4) { xsc[0] = pq_q8(xl, hf, xq[0]); xsc[1] = pq_q8(xr, hf, xq[1]); }
+        for (int lev = 0; lev < (two ? 2 : 1); lev++) {
+            int KK = lev ? K2 : K;
+            for (int side = 0; side < 2; side++) {
+                const uint16_t* cbh = lev ? (side ? t->cb2r : t->cb2l) : (side ? t->cb1r : t->cb1l);
+                float* T = tab + (lev ? 2 * K : 0) + side * KK;
+                for (int k = 0; k < KK; k++) {
+                    for (int j = 0; j < hf; j++) cb[j] = or_fp16_to_fp32(cbh[(size_t)k * hf + j]);
+                    if (variant == 4) {
+                        /* pq_chunk_dot_table_int8 (2817-2836): exact int32 dot, then
+                         * (float)s * cb_scale[k] * x_scale left to right */
+                        float cs = pq_q8(cb, hf, cbq);
+                        int32_t sum = 0;
+                        for (int j = 0; j < hf; j++) sum += (int32_t)cbq[j] * (int32_t)xq[side][j];
+                        T[k] = (float)sum * cs * xsc[side];
+                    } else {
+                        T[k] = pq_table_entry_avx2(cb, side ? xr : xl, hf);
+                    }
+                }
+            }
+        }
+        float nl = sqrtf(nl2), nr = sqrtf(nr2);
+        for (int r = 0; r < M; r++) {
+            int a = t->i1l[(size_t)r * C + c], b = t->i1r[(size_t)r * C + c];
+            float l1 = tab[a] + tab[K + b];
+            if (!two) { out[r] = out[r] + l1; continue; }
+            float c2a = tab[2 * K + pq_l2_at(t, t->i2l + (size_t)r * l2s, c)];
+            float c2b = tab[2 * K + K2 + pq_l2_at(t, t->i2r + (size_t)r * l2s, c)];
+            if (variant == 2) {
+                /* v = l1; skip the level-2 pair when |l1| > thr * (c2l*|xL| + c2r*|xR|) */
+                float bound = skip_threshold * fmaf(c2l[pyramid ? a : 0], nl, c2r[pyramid ? b : 0] * nr);
+                float v = l1;
+                if (!(skip_threshold > 0.0f && fabsf(l1) > bound)) v = v + (c2a + c2b);
+                out[r] = out[r] + v;
+            } else if (variant == 3) {
+                out[r] = out[r] + (l1 + (c2a + c2b));
+            } else {
+                out[r] = out[r] + ((l1 + c2a) + c2b);
+            }
+        }
+    }
+    for (int r = 0; r < M; r++) out[r] = out[r] * or_fp16_to_fp32(t->row_scale[r]);
+    pq_outliers(t, x, out);
+    free(ic); free(tab); free(cb); free(cbq); free(c2l); free(c2r);
+    return 0;
+}
+
 void or_expf_batch(const float* x, float* y, size_t n) {
     for (size_t i = 0; i < n; i++) y[i] = expf(x[i]);
 }

@@ -57,6 +57,7 @@ def _declare(L):
         "or_silu_mul": (None, [P, P, P, I]),
         "or_pq_matmul": (I, [P, P, P]),
         "or_pq_matmul_streaming": (I, [P, P, P]),
+        "or_pq_matmul_variant": (I, [P, P, P, I, C.c_float, C.c_float, I]),
         "or_pq_reconstruct": (I, [P, P]),
         "or_expf_batch": (None, [P, P, C.c_size_t]),
         "or_int4g_matmul": (I, [P, P, P, P, P, I, I, I, I, P, C.c_float, P]),
@@ -243,6 +244,17 @@ def pq_matmul_streaming(t: dict, x):
     x = _c(x, np.float32)
     out = np.zeros(t["M"], np.float32)
     assert lib().or_pq_matmul_streaming(C.byref(s), _p(x), _p(out)) == 0
+    return out
+
+
+def pq_matmul_variant(t: dict, x, variant: int, skip_threshold=0.0, act_threshold=0.0):
+    """The PQ session's policy variants (0 streaming, 1 l1-only, 2 l2skip,
+    3 sparse, 4 int8); t["format"] == 4 marks a pyramid tensor."""
+    s, keep = _pq_struct(t)
+    x = _c(x, np.float32)
+    out = np.zeros(t["M"], np.float32)
+    assert lib().or_pq_matmul_variant(C.byref(s), _p(x), _p(out), variant, C.c_float(skip_threshold),
+                                      C.c_float(act_threshold), int(t.get("format", 0) == 4)) == 0
     return out
 
 

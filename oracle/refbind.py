@@ -82,6 +82,11 @@ def lib():
         _lib.ib_pq_lut_cache_free.argtypes = [P]
         _lib.ib_pq_lut_cache_free.restype = None
         _lib.ib_pq_matmul_fp32_streaming_cached.argtypes = [P, P, P, P]
+        _lib.ib_pq_matmul_fp32_l1_only.argtypes = [P, P, P]
+        _lib.ib_pq_matmul_fp32_streaming_sparse.argtypes = [P, P, P, C.c_float]
+        _lib.ib_pq_matmul_fp32_streaming_l2skip_cached.argtypes = [P, P, P, P, C.c_float]
+        _lib.ib_pq_lut_cache_quantize_int8.argtypes = [P]
+        _lib.ib_pq_matmul_fp32_streaming_int8_cached.argtypes = [P, P, P, P]
     return _lib
 
 
@@ -161,7 +166,7 @@ def _pq(t: dict):
         setattr(s, n, int(t[n]))
     s.K_l2 = int(t.get("K_l2", 0))
     s.l2_idx_bytes = int(t.get("l2_idx_bytes", 1))
-    s.format = 1 if t["n_levels"] == 1 else 3
+    s.format = int(t["format"]) if "format" in t else (1 if t["n_levels"] == 1 else 3)
     keep = []
     m = {"cb1l": "codebook_l1_l", "cb1r": "codebook_l1_r", "cb2l": "codebook_l2_l",
          "cb2r": "codebook_l2_r", "i1l": "indices_l1_l", "i1r": "indices_l1_r", "i2l": "indices_l2_l",
@@ -197,6 +202,35 @@ def pq_matmul_streaming(t: dict, x):
         assert lib().ib_pq_matmul_fp32_streaming_cached(C.byref(s), cache, _p(x), _p(out)) == 0
     finally:
         lib().ib_pq_lut_cache_free(cache)
+    return out
+
+
+def pq_matmul_variant(t: dict, x, variant: int, skip_threshold=0.0, act_threshold=0.0):
+    """What ib_pq_session_matmul runs for each ib_pq_policy variant
+    (src/pq_decode.c:4468-4491)."""
+    s, keep = _pq(t)
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.zeros(t["M"], np.float32)
+    L = lib()
+    if variant == 1:
+        assert L.ib_pq_matmul_fp32_l1_only(C.byref(s), _p(x), _p(out)) == 0
+        return out
+    if variant == 3:
+        assert L.ib_pq_matmul_fp32_streaming_sparse(C.byref(s), _p(x), _p(out), C.c_float(act_threshold)) == 0
+        return out
+    cache = C.c_void_p()
+    assert L.ib_pq_lut_cache_create(C.byref(s), C.byref(cache)) == 0
+    try:
+        if variant == 0:
+            assert L.ib_pq_matmul_fp32_streaming_cached(C.byref(s), cache, _p(x), _p(out)) == 0
+        elif variant == 2:
+            assert L.ib_pq_matmul_fp32_streaming_l2skip_cached(C.byref(s), cache, _p(x), _p(out),
+                                                              C.c_float(skip_threshold)) == 0
+        elif variant == 4:
+            assert L.ib_pq_lut_cache_quantize_int8(cache) == 0
+            assert L.ib_pq_matmul_fp32_streaming_int8_cached(C.byref(s), cache, _p(x), _p(out)) == 0
+    finally:
+        L.ib_pq_lut_cache_free(cache)
     return out
 
 

@@ -15,13 +15,17 @@ Contents (every array is what the reference produced, except the inputs):
   pqs.npz      ib_pq_lut_cache_create + ib_pq_matmul_fp32_streaming_cached
                (the PQ session's default variant) on the pq.npz cases and on
                G = 4 / 32 cases
+  pqv.npz      the PQ session's policy variants (l1_only, l2skip_cached,
+               streaming_sparse, streaming_int8_cached) on the pq.npz cases and
+               on pyramid-format tensors
   int4g.npz    ib_pq_session_matmul on IBF v5 INT4 group-scale tensors
                (oracle/_ref/libref_int4g.so): y without, ys with the
                IB_ACT_SPARSE_REL skip mask (set in a child process, since the
                reference reads it once per process)
 
   python tests/golden/gen_golden.py int4g   writes int4g.npz only;
-  python tests/golden/gen_golden.py pqs     writes pqs.npz only.
+  python tests/golden/gen_golden.py pqs     writes pqs.npz only;
+  python tests/golden/gen_golden.py pqv     writes pqv.npz only.
 """
 from __future__ import annotations
 
@@ -189,6 +193,37 @@ def gen_pqs(out):
     np.savez_compressed(os.path.join(out, "pqs.npz"), **d)
 
 
+# (variant, skip_threshold, act_threshold) per policy case of pqv.npz
+PQV_POLICIES = {"l1only": (1, 0.0, 0.0), "l2skip05": (2, 0.5, 0.0), "l2skip5": (2, 5.0, 0.0),
+                "sparse": (3, 0.0, 1e-2), "int8": (4, 0.0, 0.0)}
+# pyramid tensors: (M, C, G, K, levels, K_l2 = K * K_inner, outliers)
+PQV_PYRAMID = {"pyr16": (50, 12, 16, 16, 2, 256, 3), "pyr8": (40, 10, 8, 8, 2, 64, 0)}
+
+
+def gen_pqv(out):
+    d = {}
+    pq = np.load(os.path.join(out, "pq.npz"))
+    cases = {}
+    for name in PQ_CASES:
+        cases[name] = {k[len(name) + 1:]: (int(pq[k]) if pq[k].ndim == 0 else pq[k]) for k in pq.files
+                       if k.startswith(name + ".")}
+    rng = np.random.default_rng(777)
+    for name, args in PQV_PYRAMID.items():
+        t = make_pq(rng, *args)
+        t["format"] = 4
+        t["x"] = rng.standard_normal(t["N"]).astype(np.float32)
+        t["xs"] = t["x"].copy()
+        t["xs"][: t["N"] // 2] *= 1e-3
+        for k, v in t.items():
+            d[f"{name}.{k}"] = np.asarray(v)
+        cases[name] = t
+    for name, t in cases.items():
+        for pol, (v, st, at) in PQV_POLICIES.items():
+            d[f"{name}.{pol}.y"] = R.pq_matmul_variant(t, t["x"], v, st, at)
+            d[f"{name}.{pol}.ys"] = R.pq_matmul_variant(t, t["xs"], v, st, at)
+    np.savez_compressed(os.path.join(out, "pqv.npz"), **d)
+
+
 # name: (M, N, G, AWQ inv_act, outliers per row)
 INT4G_CASES = {
     "g32": (64, 256, 32, 0, 0),
@@ -262,12 +297,16 @@ def main():
     if len(sys.argv) > 1 and sys.argv[1] == "pqs":
         gen_pqs(HERE)
         return
+    if len(sys.argv) > 1 and sys.argv[1] == "pqv":
+        gen_pqv(HERE)
+        return
     if not R.available():
         sys.exit("oracle/_ref/libinferbit_ref.so missing: run `make -C oracle ref` first")
     gen_quant_matvec(HERE)
     gen_batch(HERE)
     gen_pq(HERE)
     gen_pqs(HERE)
+    gen_pqv(HERE)
     gen_int4g(HERE)
     for f in sorted(os.listdir(HERE)):
         if f.endswith(".npz"):

@@ -345,3 +345,41 @@ def test_pq_streaming_keeps_every_chunk(oracle_lib):
     np.testing.assert_allclose(y_skip, y_half, rtol=0, atol=1e-6 * np.abs(y_half).max())
     y_str = oracle_lib.pq_matmul_streaming(t, xs)
     assert np.abs(y_str - y_half).max() > 1e-6 * np.abs(y_half).max()
+
+
+PQV_NAMES = ["l1", "l2p16", "l2u8", "l2u16", "out8", "out40", "pyr16", "pyr8"]
+PQV_POLICIES = {"l1only": (1, 0.0, 0.0), "l2skip05": (2, 0.5, 0.0), "l2skip5": (2, 5.0, 0.0),
+                "sparse": (3, 0.0, 1e-2), "int8": (4, 0.0, 0.0)}
+
+
+def pqv_case(name):
+    d = load_golden("pqv.npz")
+    src = d if f"{name}.M" in d.files else load_golden("pq.npz")
+    return d, pq_case(src, name)
+
+
+@pytest.mark.parametrize("name", PQV_NAMES)
+@pytest.mark.parametrize("pol", list(PQV_POLICIES))
+def test_pq_policy_variants_match_reference(oracle_lib, name, pol):
+    """The PQ session's policy variants, bit for bit against the compiled reference."""
+    d, t = pqv_case(name)
+    v, st, at = PQV_POLICIES[pol]
+    same_bits(oracle_lib.pq_matmul_variant(t, t["x"], v, st, at), d[f"{name}.{pol}.y"])
+    same_bits(oracle_lib.pq_matmul_variant(t, t["xs"], v, st, at), d[f"{name}.{pol}.ys"])
+
+
+def test_pq_policy_variant_properties(oracle_lib):
+    """Closed forms: L1_ONLY equals the streaming result of the tensor with
+    its level 2 removed; L2SKIP at threshold 0 and SPARSE at threshold 0
+    equal STREAMING; INT8 stays within the int8 quantisation error."""
+    d, t = pqv_case("l2u8")
+    x = t["x"]
+    one = {k: v for k, v in t.items() if k not in ("cb2l", "cb2r", "i2l", "i2r")}
+    one["n_levels"], one["K_l2"] = 1, 0
+    same_bits(oracle_lib.pq_matmul_variant(t, x, 1), oracle_lib.pq_matmul_streaming(one, x))
+    ys = oracle_lib.pq_matmul_streaming(t, x)
+    np.testing.assert_allclose(oracle_lib.pq_matmul_variant(t, x, 2, 0.0), ys, rtol=0, atol=1e-6 * np.abs(ys).max())
+    np.testing.assert_allclose(oracle_lib.pq_matmul_variant(t, x, 3, 0.0, 0.0), ys, rtol=0,
+                               atol=1e-6 * np.abs(ys).max())
+    y8 = oracle_lib.pq_matmul_variant(t, x, 4)
+    assert 0 < np.abs(y8 - ys).max() <= 0.05 * np.abs(ys).max()

@@ -88,3 +88,40 @@ def test_pq_streaming_rejects_wide_chunks(ops):
     t = make_pq(np.random.default_rng(1), 16, 4, 64, 16, 1, 0, 0)
     with pytest.raises(IbhError):
         run_streaming(ops, t, np.zeros(t["N"], np.float32))
+
+
+PQV_NAMES = ["l1", "l2p16", "l2u8", "l2u16", "out8", "out40", "pyr16", "pyr8"]
+PQV_POLICIES = {"l1only": (1, 0.0, 0.0), "l2skip05": (2, 0.5, 0.0), "l2skip5": (2, 5.0, 0.0),
+                "sparse": (3, 0.0, 1e-2), "int8": (4, 0.0, 0.0)}
+
+
+def run_policy(ops, t, x, v, st, at):
+    d = ops.PqDeviceTensor(t)
+    out = torch.empty(t["M"], device="cuda")
+    d.matmul_policy(torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda(), out, v, st, at)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("name", PQV_NAMES)
+@pytest.mark.parametrize("pol", list(PQV_POLICIES))
+def test_pq_policy_golden(ops, name, pol):
+    """The PQ session's policy variants against the reference's outputs."""
+    print(f"case pq policy {name} {pol}", flush=True)
+    d = load_golden("pqv.npz")
+    src = d if f"{name}.M" in d.files else load_golden("pq.npz")
+    t = pq_case(src, name)
+    v, st, at = PQV_POLICIES[pol]
+    assert relerr(run_policy(ops, t, t["x"], v, st, at), d[f"{name}.{pol}.y"]) <= 1e-4
+    assert relerr(run_policy(ops, t, t["xs"], v, st, at), d[f"{name}.{pol}.ys"]) <= 1e-4
+
+
+@pytest.mark.parametrize("v,st,at", [(1, 0, 0), (2, 0.5, 0), (3, 0, 1e-3), (4, 0, 0)])
+def test_pq_policy_mistral_shape(ops, oracle_lib, v, st, at):
+    from gen_golden import make_pq
+    print(f"case pq policy mistral v={v}", flush=True)
+    rng = np.random.default_rng(8)
+    t = make_pq(rng, 4096, 896, 16, 256, 2, 256, 0)
+    x = rng.standard_normal(t["N"]).astype(np.float32)
+    x[: t["N"] // 3] *= 1e-4
+    assert relerr(run_policy(ops, t, x, v, st, at), oracle_lib.pq_matmul_variant(t, x, v, st, at)) <= 1e-4
