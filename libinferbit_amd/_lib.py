@@ -39,6 +39,8 @@ SIGNATURES = {
     "ibh_pq_matmul": (I, [P, P, P, P, SZ, P]),
     "ibh_pq_matmul_streaming": (I, [P, P, P, P, SZ, P]),
     "ibh_pq_matmul_policy": (I, [P, P, P, P, P, SZ, P]),
+    "ibh_pq_topk_workspace_bytes": (SZ, [P, I]),
+    "ibh_pq_lm_head_topk": (I, [P, P, I, P, P, P, SZ, P]),
     "ibh_int4g_workspace_bytes": (SZ, [P]),
     "ibh_int4g_matmul": (I, [P, P, P, C.c_float, P, SZ, P]),
     "ibh_int4g_matmul_batched": (I, [P, I, P, P, C.c_float, P, SZ, P]),

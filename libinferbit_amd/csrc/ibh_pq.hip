@@ -348,6 +348,127 @@ __global__ __launch_bounds__(kThreads) void pq_reduce(PqDev t, const float* __re
                 &meta_s);
 }
 
+
+// ── top-K LM head (ib_pq_lm_head_topk, pq_decode.c:2259-2346) ─────────────
+// Order key of a float, descending: smaller key = larger value.
+__device__ __forceinline__ uint32_t desc_key(float v) {
+    const uint32_t f = __float_as_uint(v);
+    const uint32_t u = (f & 0x80000000u) ? ~f : (f | 0x80000000u);
+    return ~u;
+}
+
+constexpr int kSelThreads = 1024;
+
+// The K largest of v[0..M): radix select of the K-th key (4 passes of 8 bits),
+// then every element above it plus the first ties in index order.  One block.
+__global__ __launch_bounds__(kSelThreads) void pq_topk_select(const float* __restrict__ v, int M, int K,
+                                                              int32_t* __restrict__ sel) {
+    __shared__ int hist[256];
+    __shared__ uint32_t s_prefix, s_mask;
+    __shared__ int s_kk, s_nless, s_neq;
+    __shared__ int wcnt[kSelThreads / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid == 0) { s_prefix = 0; s_mask = 0; s_kk = K; s_nless = 0; s_neq = 0; }
+    for (int pass = 0; pass < 4; pass++) {
+        const int shift = 24 - 8 * pass;
+        if (tid < 256) hist[tid] = 0;
+        __syncthreads();
+        const uint32_t prefix = s_prefix, mask = s_mask;
+        for (int i = tid; i < M; i += kSelThreads) {
+            const uint32_t d = desc_key(v[i]);
+            if ((d & mask) == prefix) atomicAdd(&hist[(d >> shift) & 255], 1);
+        }
+        __syncthreads();
+        if (tid == 0) {
+            int cum = 0, b = 0;
+            for (; b < 255; b++) {
+                if (cum + hist[b] >= s_kk) break;
+                cum += hist[b];
+            }
+            s_kk -= cum;
+            s_prefix |= (uint32_t)b << shift;
+            s_mask |= 0xFFu << shift;
+        }
+        __syncthreads();
+    }
+    const uint32_t kth = s_prefix;
+    const int take_eq = s_kk;                     // ties of the K-th key to keep, lowest indices first
+    for (int base = 0; base < M; base += kSelThreads) {
+        const int i = base + tid;
+        const uint32_t d = i < M ? desc_key(v[i]) : 0xFFFFFFFFu;
+        const bool less = i < M && d < kth, eq = i < M && d == kth;
+        if (less) sel[atomicAdd(&s_nless, 1)] = i;
+        const unsigned long long b = __ballot(eq);
+        if (lane == 0) wcnt[wave] = __popcll(b);
+        __syncthreads();
+        int before = s_neq;
+        for (int w = 0; w < wave; w++) before += wcnt[w];
+        const int r = before + __popcll(b & ((1ull << lane) - 1ull));
+        if (eq && r < take_eq) sel[(K - take_eq) + r] = i;
+        __syncthreads();
+        if (tid == 0) {
+            int tot = 0;
+            for (int w = 0; w < kSelThreads / 64; w++) tot += wcnt[w];
+            s_neq += tot;
+        }
+        __syncthreads();
+    }
+}
+
+// Full-pyramid logits of the selected rows (ib_pq_matmul_fp32_subset,
+// pq_decode.c:2145-2250): one wavefront per row, lanes over chunks; the
+// outlier sidecar in fp32.
+__global__ __launch_bounds__(256) void pq_subset_rows(PqDev t, const float* __restrict__ x,
+                                                      const int32_t* __restrict__ rows, int n,
+                                                      float* __restrict__ out) {
+    const int lane = threadIdx.x & 63;
+    const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (i >= n) return;
+    const int r = rows[i], C = t.C, G = t.G, hf = G / 2;
+    const size_t l2s = t.n_levels == 2 ? l2_stride(t) : 0;
+    float acc = 0.f;
+    for (int c = lane; c < C; c += 64) {
+        const uint16_t* el = t.cb1l + (size_t)t.i1l[(size_t)r * C + c] * hf;
+        const uint16_t* er = t.cb1r + (size_t)t.i1r[(size_t)r * C + c] * hf;
+        const uint16_t *e2l = nullptr, *e2r = nullptr;
+        if (t.n_levels == 2) {
+            e2l = t.cb2l + (size_t)l2_at(t, t.i2l + (size_t)r * l2s, c) * hf;
+            e2r = t.cb2r + (size_t)l2_at(t, t.i2r + (size_t)r * l2s, c) * hf;
+        }
+        for (int j = 0; j < hf; j++) {
+            const float xl = x[inner_col(t, c * G + j)], xr = x[inner_col(t, c * G + hf + j)];
+            acc = fmaf(f16_to_f32(el[j]), xl, acc);
+            acc = fmaf(f16_to_f32(er[j]), xr, acc);
+            if (e2l) {
+                acc = fmaf(f16_to_f32(e2l[j]), xl, acc);
+                acc = fmaf(f16_to_f32(e2r[j]), xr, acc);
+            }
+        }
+    }
+    acc = wave_sum(acc) * f16_to_f32(t.row_scale[r]);
+    float o = 0.f;
+    for (int j = lane; j < t.n_outlier; j += 64)
+        o = fmaf((float)t.oside[(size_t)r * t.n_outlier + j] * f16_to_f32(t.oscale[j]), x[t.ocols[j]], o);
+    o = wave_sum(o);
+    if (lane == 0) out[i] = acc + o;
+}
+
+// Descending order of the refined logits (the reference's insertion sort:
+// ties keep their selection order).  One block, K <= 1024.
+__global__ __launch_bounds__(1024) void pq_topk_sort(const float* __restrict__ val, const int32_t* __restrict__ ids,
+                                                     int K, float* __restrict__ out_v, int32_t* __restrict__ out_i) {
+    for (int i = threadIdx.x; i < K; i += 1024) {
+        const float v = val[i];
+        int rank = 0;
+        for (int j = 0; j < K; j++) {
+            const float w = val[j];
+            rank += (w > v) || (w == v && j < i);
+        }
+        out_v[rank] = v;
+        out_i[rank] = ids[i];
+    }
+}
+
 }  // namespace
 
 void* ibh_workspace(size_t bytes);
@@ -519,5 +640,63 @@ static int pq_run(const ibh_pq_tensor_abi* t, const float* x, float* out, void* 
     IBH_CHECK_LAUNCH("ibh_pq_matmul (gather)");
     pq_reduce<<<(t->M + kThreads - 1) / kThreads, kThreads, 0, st>>>(d, x, part, nslabs, out);
     IBH_CHECK_LAUNCH("ibh_pq_matmul (reduce)");
+    return IBH_OK;
+}
+
+// Workspace of ibh_pq_lm_head_topk: the matvec's, then the coarse logits,
+// the selected rows and their refined logits.
+extern "C" size_t ibh_pq_topk_workspace_bytes(const ibh_pq_tensor_abi* t, int k_top) {
+    const size_t base = ibh_pq_workspace_bytes(t);
+    if (!base || k_top <= 0) return 0;
+    auto al = [](size_t v) { return (v + 255) / 256 * 256; };
+    return base + al((size_t)t->M * 4) + 2 * al((size_t)k_top * 4);
+}
+
+extern "C" int ibh_pq_lm_head_topk(const ibh_pq_tensor_abi* t, const float* x, int k_top, float* out_logits,
+                                   int32_t* out_ids, void* ws, size_t ws_bytes, void* stream) {
+    if (!t || !x || !out_logits || !out_ids || k_top <= 0 || k_top > t->M || k_top > 1024) {
+        ibh_set_error("ibh_pq_lm_head_topk: invalid arguments (K_top=%d, M=%d; K_top <= 1024)", k_top, t ? t->M : 0);
+        return IBH_ERROR_PARAM;
+    }
+    const size_t need = ibh_pq_topk_workspace_bytes(t, k_top);
+    if (!need) {
+        ibh_set_error("ibh_pq_lm_head_topk: invalid tensor");
+        return IBH_ERROR_PARAM;
+    }
+    if (!ws) {
+        ws = ibh_workspace(need);
+        ws_bytes = ws ? need : 0;
+    }
+    if (!ws || ws_bytes < need) {
+        ibh_set_error("ibh_pq_lm_head_topk: workspace of %zu bytes needed", need);
+        return IBH_ERROR_MEMORY;
+    }
+    auto al = [](size_t v) { return (v + 255) / 256 * 256; };
+    const size_t base = ibh_pq_workspace_bytes(t);
+    float* coarse = (float*)((char*)ws + base);
+    int32_t* sel = (int32_t*)((char*)coarse + al((size_t)t->M * 4));
+    float* refined = (float*)((char*)sel + al((size_t)k_top * 4));
+    hipStream_t st = ibh_resolve_stream(stream);
+    // 1. level-1 logits of every row (ib_pq_matmul_fp32_l1_only)
+    PqMode md;
+    md.skip_mode = 0;
+    md.level2 = false;
+    int rc = pq_run(t, x, coarse, ws, base, stream, md, "ibh_pq_lm_head_topk");
+    if (rc) return rc;
+    // 2. the K largest, 3. their full-pyramid logits, 4. sorted
+    pq_topk_select<<<1, kSelThreads, 0, st>>>(coarse, t->M, k_top, sel);
+    IBH_CHECK_LAUNCH("ibh_pq_lm_head_topk (select)");
+    PqDev d{};
+    d.M = t->M; d.N = t->N; d.G = t->G; d.K = t->K; d.K2 = t->K_l2 > 0 ? t->K_l2 : t->K;
+    d.n_levels = t->n_levels; d.n_outlier = t->n_outlier; d.C = t->C;
+    d.l2_idx_bytes = t->l2_idx_bytes > 0 ? t->l2_idx_bytes : 1;
+    d.cb1l = t->codebook_l1_l; d.cb1r = t->codebook_l1_r; d.cb2l = t->codebook_l2_l; d.cb2r = t->codebook_l2_r;
+    d.i1l = t->indices_l1_l; d.i1r = t->indices_l1_r; d.i2l = t->indices_l2_l; d.i2r = t->indices_l2_r;
+    d.row_scale = t->row_scale; d.ocols = t->outlier_cols; d.oside = t->outlier_sidecar;
+    d.oscale = t->outlier_scale; d.inner = t->n_outlier > 0 ? t->inner_cols : nullptr;
+    pq_subset_rows<<<(k_top + 3) / 4, 256, 0, st>>>(d, x, sel, k_top, refined);
+    IBH_CHECK_LAUNCH("ibh_pq_lm_head_topk (refine)");
+    pq_topk_sort<<<1, 1024, 0, st>>>(refined, sel, k_top, out_logits, out_ids);
+    IBH_CHECK_LAUNCH("ibh_pq_lm_head_topk (sort)");
     return IBH_OK;
 }

@@ -156,6 +156,16 @@ class PqDeviceTensor:
         check(lib().ibh_pq_matmul_policy(ctypes.byref(self.s), _ptr(x), _ptr(out), ctypes.byref(p), _ptr(self.ws),
                                          self.ws.numel(), _stream()), "ibh_pq_matmul_policy")
 
+    def lm_head_topk(self, x, k_top: int):
+        """ib_pq_lm_head_topk (src/pq_decode.c:2259-2346): (logits [k], ids [k]) on the GPU."""
+        need = lib().ibh_pq_topk_workspace_bytes(ctypes.byref(self.s), k_top)
+        ws = torch.empty(max(1, need), dtype=torch.uint8, device="cuda")
+        lg = torch.empty(k_top, device="cuda")
+        ids = torch.empty(k_top, dtype=torch.int32, device="cuda")
+        check(lib().ibh_pq_lm_head_topk(ctypes.byref(self.s), _ptr(x), k_top, _ptr(lg), _ptr(ids), _ptr(ws), need,
+                                        _stream()), "ibh_pq_lm_head_topk")
+        return lg, ids
+
     def matmul_streaming(self, x, out) -> None:
         """ib_pq_matmul_fp32_streaming_cached (src/pq_decode.c:2987): every chunk."""
         check(lib().ibh_pq_matmul_streaming(ctypes.byref(self.s), _ptr(x), _ptr(out), _ptr(self.ws),

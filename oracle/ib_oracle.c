@@ -862,6 +862,79 @@ int or_pq_matmul_variant(const or_pq_tensor* t, const float* x, float* out, int 
     return 0;
 }
 
+int or_pq_matmul_subset(const or_pq_tensor* t, const float* x, const int32_t* rows, int n_rows, float* out) {
+    int M = t->M, G = t->G, C = t->C, hf = G / 2, two = t->n_levels == 2;
+    for (int i = 0; i < n_rows; i++) if (rows[i] < 0 || rows[i] >= M) return -1;
+    int* ic = pq_inner_cols(t);
+    size_t l2s = pq_l2_stride(t);
+    for (int ri = 0; ri < n_rows; ri++) {
+        int r = rows[ri];
+        float acc = 0.0f;
+        for (int c = 0; c < C; c++) {
+            const uint16_t* el = t->cb1l + (size_t)t->i1l[(size_t)r * C + c] * hf;
+            const uint16_t* er = t->cb1r + (size_t)t->i1r[(size_t)r * C + c] * hf;
+            for (int j = 0; j < hf; j++) {
+                acc = fmaf(or_fp16_to_fp32(el[j]), x[ic[c * G + j]], acc);
+                acc = fmaf(or_fp16_to_fp32(er[j]), x[ic[c * G + hf + j]], acc);
+            }
+            if (two) {
+                const uint16_t* e2l = t->cb2l + (size_t)pq_l2_at(t, t->i2l + (size_t)r * l2s, c) * hf;
+                const uint16_t* e2r = t->cb2r + (size_t)pq_l2_at(t, t->i2r + (size_t)r * l2s, c) * hf;
+                for (int j = 0; j < hf; j++) {
+                    acc = fmaf(or_fp16_to_fp32(e2l[j]), x[ic[c * G + j]], acc);
+                    acc = fmaf(or_fp16_to_fp32(e2r[j]), x[ic[c * G + hf + j]], acc);
+                }
+            }
+        }
+        acc = acc * or_fp16_to_fp32(t->row_scale[r]);
+        for (int j = 0; j < t->n_outlier; j++) {
+            float w = (float)t->oside[(size_t)r * t->n_outlier + j] * or_fp16_to_fp32(t->oscale[j]);
+            acc = fmaf(w, x[t->ocols[j]], acc);
+        }
+        out[ri] = acc;
+    }
+    free(ic);
+    return 0;
+}
+
+static void heap_sift(float* v, int32_t* id, int n, int i) {
+    for (;;) {
+        int l = 2 * i + 1, r = 2 * i + 2, s = i;
+        if (l < n && v[l] < v[s]) s = l;
+        if (r < n && v[r] < v[s]) s = r;
+        if (s == i) return;
+        float tv = v[i]; v[i] = v[s]; v[s] = tv;
+        int32_t ti = id[i]; id[i] = id[s]; id[s] = ti;
+        i = s;
+    }
+}
+
+int or_pq_lm_head_topk(const or_pq_tensor* t, const float* x, int k_top, float* out_logits, int32_t* out_ids) {
+    int M = t->M;
+    if (k_top <= 0 || k_top > M) return -1;
+    float* coarse = (float*)malloc(sizeof(float) * (size_t)M);
+    or_pq_matmul_variant(t, x, coarse, 1, 0.0f, 0.0f, 0);
+    float* tv = (float*)malloc(sizeof(float) * (size_t)k_top);
+    int32_t* ti = (int32_t*)malloc(sizeof(int32_t) * (size_t)k_top);
+    for (int i = 0; i < k_top; i++) { ti[i] = i; tv[i] = coarse[i]; }
+    for (int s = k_top / 2 - 1; s >= 0; s--) heap_sift(tv, ti, k_top, s);
+    for (int j = k_top; j < M; j++)
+        if (coarse[j] > tv[0]) { tv[0] = coarse[j]; ti[0] = j; heap_sift(tv, ti, k_top, 0); }
+    float* ref = (float*)malloc(sizeof(float) * (size_t)k_top);
+    or_pq_matmul_subset(t, x, ti, k_top, ref);
+    for (int i = 1; i < k_top; i++) {
+        float v = ref[i];
+        int32_t id = ti[i];
+        int j = i - 1;
+        while (j >= 0 && ref[j] < v) { ref[j + 1] = ref[j]; ti[j + 1] = ti[j]; j--; }
+        ref[j + 1] = v;
+        ti[j + 1] = id;
+    }
+    for (int i = 0; i < k_top; i++) { out_logits[i] = ref[i]; out_ids[i] = ti[i]; }
+    free(coarse); free(tv); free(ti); free(ref);
+    return 0;
+}
+
 void or_expf_batch(const float* x, float* y, size_t n) {
     for (size_t i = 0; i < n; i++) y[i] = expf(x[i]);
 }

@@ -92,6 +92,12 @@ int or_pq_matmul_streaming(const or_pq_tensor* t, const float* x, float* out);
  * 2766-2812).  G <= 32. */
 int or_pq_matmul_variant(const or_pq_tensor* t, const float* x, float* out, int variant, float skip_threshold,
                          float act_threshold, int pyramid);
+/* ib_pq_matmul_fp32_subset (pq_decode.c:2145-2250): full pyramid for the
+ * listed rows, one serial chain per row. */
+int or_pq_matmul_subset(const or_pq_tensor* t, const float* x, const int32_t* rows, int n_rows, float* out);
+/* ib_pq_lm_head_topk (pq_decode.c:2259-2346): L1-only logits, top-K by a
+ * min-heap, subset refinement, insertion sort descending. */
+int or_pq_lm_head_topk(const or_pq_tensor* t, const float* x, int k_top, float* out_logits, int32_t* out_ids);
 
 /* glibc expf applied elementwise: the libm the reference links
  * (kernels/avx2.c:213-216, :241-244), called as is. */

@@ -58,6 +58,8 @@ def _declare(L):
         "or_pq_matmul": (I, [P, P, P]),
         "or_pq_matmul_streaming": (I, [P, P, P]),
         "or_pq_matmul_variant": (I, [P, P, P, I, C.c_float, C.c_float, I]),
+        "or_pq_matmul_subset": (I, [P, P, P, I, P]),
+        "or_pq_lm_head_topk": (I, [P, P, I, P, P]),
         "or_pq_reconstruct": (I, [P, P]),
         "or_expf_batch": (None, [P, P, C.c_size_t]),
         "or_int4g_matmul": (I, [P, P, P, P, P, I, I, I, I, P, C.c_float, P]),
@@ -256,6 +258,23 @@ def pq_matmul_variant(t: dict, x, variant: int, skip_threshold=0.0, act_threshol
     assert lib().or_pq_matmul_variant(C.byref(s), _p(x), _p(out), variant, C.c_float(skip_threshold),
                                       C.c_float(act_threshold), int(t.get("format", 0) == 4)) == 0
     return out
+
+
+def pq_matmul_subset(t: dict, x, rows):
+    s, keep = _pq_struct(t)
+    x = _c(x, np.float32)
+    rows = _c(rows, np.int32)
+    out = np.zeros(len(rows), np.float32)
+    assert lib().or_pq_matmul_subset(C.byref(s), _p(x), _p(rows), len(rows), _p(out)) == 0
+    return out
+
+
+def pq_lm_head_topk(t: dict, x, k: int):
+    s, keep = _pq_struct(t)
+    x = _c(x, np.float32)
+    lg, ids = np.zeros(k, np.float32), np.zeros(k, np.int32)
+    assert lib().or_pq_lm_head_topk(C.byref(s), _p(x), k, _p(lg), _p(ids)) == 0
+    return lg, ids
 
 
 def pq_reconstruct(t: dict):

@@ -87,6 +87,8 @@ def lib():
         _lib.ib_pq_matmul_fp32_streaming_l2skip_cached.argtypes = [P, P, P, P, C.c_float]
         _lib.ib_pq_lut_cache_quantize_int8.argtypes = [P]
         _lib.ib_pq_matmul_fp32_streaming_int8_cached.argtypes = [P, P, P, P]
+        _lib.ib_pq_matmul_fp32_subset.argtypes = [P, P, P, I, P]
+        _lib.ib_pq_lm_head_topk.argtypes = [P, P, I, P, P]
     return _lib
 
 
@@ -232,6 +234,23 @@ def pq_matmul_variant(t: dict, x, variant: int, skip_threshold=0.0, act_threshol
     finally:
         L.ib_pq_lut_cache_free(cache)
     return out
+
+
+def pq_matmul_subset(t: dict, x, rows):
+    s, keep = _pq(t)
+    x = np.ascontiguousarray(x, np.float32)
+    rows = np.ascontiguousarray(rows, np.int32)
+    out = np.zeros(len(rows), np.float32)
+    assert lib().ib_pq_matmul_fp32_subset(C.byref(s), _p(x), _p(rows), len(rows), _p(out)) == 0
+    return out
+
+
+def pq_lm_head_topk(t: dict, x, k: int):
+    s, keep = _pq(t)
+    x = np.ascontiguousarray(x, np.float32)
+    lg, ids = np.zeros(k, np.float32), np.zeros(k, np.int32)
+    assert lib().ib_pq_lm_head_topk(C.byref(s), _p(x), k, _p(lg), _p(ids)) == 0
+    return lg, ids
 
 
 def pq_reconstruct(t: dict):

@@ -18,6 +18,7 @@ Contents (every array is what the reference produced, except the inputs):
   pqv.npz      the PQ session's policy variants (l1_only, l2skip_cached,
                streaming_sparse, streaming_int8_cached) on the pq.npz cases and
                on pyramid-format tensors
+  pqtopk.npz   ib_pq_lm_head_topk (l1-only logits, top-K, subset refinement)
   int4g.npz    ib_pq_session_matmul on IBF v5 INT4 group-scale tensors
                (oracle/_ref/libref_int4g.so): y without, ys with the
                IB_ACT_SPARSE_REL skip mask (set in a child process, since the
@@ -25,7 +26,8 @@ Contents (every array is what the reference produced, except the inputs):
 
   python tests/golden/gen_golden.py int4g   writes int4g.npz only;
   python tests/golden/gen_golden.py pqs     writes pqs.npz only;
-  python tests/golden/gen_golden.py pqv     writes pqv.npz only.
+  python tests/golden/gen_golden.py pqv     writes pqv.npz only;
+  python tests/golden/gen_golden.py pqtopk  writes pqtopk.npz only.
 """
 from __future__ import annotations
 
@@ -224,6 +226,26 @@ def gen_pqv(out):
     np.savez_compressed(os.path.join(out, "pqv.npz"), **d)
 
 
+# top-K head cases: (M, C, G, K, levels, K_l2, outliers), K_top values
+PQTOPK = {"head1": ((2000, 24, 16, 256, 1, 0, 0), (1, 8, 40)),
+          "head2": ((1500, 16, 16, 64, 2, 256, 6), (3, 64)),
+          "small": ((12, 8, 8, 16, 2, 16, 0), (12,))}
+
+
+def gen_pqtopk(out):
+    d = {}
+    rng = np.random.default_rng(4242)
+    for name, (args, ks) in PQTOPK.items():
+        t = make_pq(rng, *args)
+        t["x"] = rng.standard_normal(t["N"]).astype(np.float32)
+        for k, v in t.items():
+            d[f"{name}.{k}"] = np.asarray(v)
+        for kt in ks:
+            lg, ids = R.pq_lm_head_topk(t, t["x"], kt)
+            d[f"{name}.k{kt}.logits"], d[f"{name}.k{kt}.ids"] = lg, ids
+    np.savez_compressed(os.path.join(out, "pqtopk.npz"), **d)
+
+
 # name: (M, N, G, AWQ inv_act, outliers per row)
 INT4G_CASES = {
     "g32": (64, 256, 32, 0, 0),
@@ -300,6 +322,9 @@ def main():
     if len(sys.argv) > 1 and sys.argv[1] == "pqv":
         gen_pqv(HERE)
         return
+    if len(sys.argv) > 1 and sys.argv[1] == "pqtopk":
+        gen_pqtopk(HERE)
+        return
     if not R.available():
         sys.exit("oracle/_ref/libinferbit_ref.so missing: run `make -C oracle ref` first")
     gen_quant_matvec(HERE)
@@ -307,6 +332,7 @@ def main():
     gen_pq(HERE)
     gen_pqs(HERE)
     gen_pqv(HERE)
+    gen_pqtopk(HERE)
     gen_int4g(HERE)
     for f in sorted(os.listdir(HERE)):
         if f.endswith(".npz"):

@@ -383,3 +383,33 @@ def test_pq_policy_variant_properties(oracle_lib):
                                atol=1e-6 * np.abs(ys).max())
     y8 = oracle_lib.pq_matmul_variant(t, x, 4)
     assert 0 < np.abs(y8 - ys).max() <= 0.05 * np.abs(ys).max()
+
+
+TOPK_CASES = [("head1", 1), ("head1", 8), ("head1", 40), ("head2", 3), ("head2", 64), ("small", 12)]
+
+
+@pytest.mark.parametrize("name,k", TOPK_CASES)
+def test_pq_lm_head_topk_matches_reference(oracle_lib, name, k):
+    d = load_golden("pqtopk.npz")
+    t = pq_case(d, name)
+    lg, ids = oracle_lib.pq_lm_head_topk(t, t["x"], k)
+    same_bits(lg, d[f"{name}.k{k}.logits"])
+    same_bits(ids, d[f"{name}.k{k}.ids"])
+
+
+def test_pq_topk_is_the_subset_of_largest_coarse_logits(oracle_lib):
+    """Properties: the ids are the K largest level-1 logits; the logits are
+    the subset matvec of those ids, sorted descending; K = M returns every
+    row."""
+    d = load_golden("pqtopk.npz")
+    t = pq_case(d, "head2")
+    coarse = oracle_lib.pq_matmul_variant(t, t["x"], 1)
+    lg, ids = oracle_lib.pq_lm_head_topk(t, t["x"], 64)
+    assert set(ids.tolist()) == set(np.argsort(-coarse, kind="stable")[:64].tolist())
+    same_bits(lg, oracle_lib.pq_matmul_subset(t, t["x"], ids))
+    assert (np.diff(lg) <= 0).all()
+    W = oracle_lib.pq_reconstruct(t).astype(np.float64)
+    np.testing.assert_allclose(lg, (W @ t["x"].astype(np.float64))[ids], rtol=0, atol=2e-3 * np.abs(lg).max())
+    small = pq_case(d, "small")
+    lg, ids = oracle_lib.pq_lm_head_topk(small, small["x"], 12)
+    assert sorted(ids.tolist()) == list(range(12))

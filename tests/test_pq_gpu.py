@@ -125,3 +125,29 @@ def test_pq_policy_mistral_shape(ops, oracle_lib, v, st, at):
     x = rng.standard_normal(t["N"]).astype(np.float32)
     x[: t["N"] // 3] *= 1e-4
     assert relerr(run_policy(ops, t, x, v, st, at), oracle_lib.pq_matmul_variant(t, x, v, st, at)) <= 1e-4
+
+
+@pytest.mark.parametrize("name,k", [("head1", 1), ("head1", 8), ("head1", 40), ("head2", 3), ("head2", 64),
+                                    ("small", 12)])
+def test_pq_lm_head_topk_golden(ops, name, k):
+    print(f"case pq topk {name} k={k}", flush=True)
+    d = load_golden("pqtopk.npz")
+    t = pq_case(d, name)
+    lg, ids = ops.PqDeviceTensor(t).lm_head_topk(torch.from_numpy(t["x"]).cuda(), k)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(ids.cpu().numpy(), d[f"{name}.k{k}.ids"])
+    want = d[f"{name}.k{k}.logits"]
+    assert float(np.abs(lg.cpu().numpy().astype(np.float64) - want).max() / np.abs(want).max()) <= 1e-4
+
+
+def test_pq_lm_head_topk_vocab_shape(ops, oracle_lib):
+    """A 32000-row head (Llama vocabulary) over hidden 4096, two levels."""
+    from gen_golden import make_pq
+    rng = np.random.default_rng(12)
+    t = make_pq(rng, 32000, 256, 16, 256, 2, 256, 0)
+    x = rng.standard_normal(t["N"]).astype(np.float32)
+    want_lg, want_ids = oracle_lib.pq_lm_head_topk(t, x, 50)
+    lg, ids = ops.PqDeviceTensor(t).lm_head_topk(torch.from_numpy(x).cuda(), 50)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(ids.cpu().numpy(), want_ids)
+    assert float(np.abs(lg.cpu().numpy().astype(np.float64) - want_lg).max() / np.abs(want_lg).max()) <= 1e-4
