@@ -290,6 +290,28 @@ int  ibh_model_synchronize(ibh_model* model);
  * x86 table's scalar batch kernels, so logits are bit-identical. */
 int  ibh_model_forward_positions(ibh_model* model, const int32_t* tokens, int n, float* logits, int vocab_size);
 
+/* ── sampling (host loop over the calls above) ── */
+
+/* inferbit_sample_params (include/inferbit.h:78-85), same fields and order. */
+typedef struct {
+    float temperature;
+    int   top_k;
+    float top_p;
+    float repeat_penalty;
+    int   max_tokens;
+    int   seed;
+} ibh_sample_params;
+/* inferbit_default_sample_params (src/generate.c:9-18). */
+ibh_sample_params ibh_default_sample_params(void);
+/* inferbit_generate (src/generate.c:243-302): temperature < 0.01 runs the
+ * device greedy loop (ibh_model_generate_greedy); otherwise each position's
+ * logits come back to the host and sample_token (src/generate.c:200-221:
+ * repeat penalty, temperature, top-k, softmax, top-p over the xorshift32
+ * stream seeded as rng_seed does) picks the token.  With exact mode and a
+ * seed >= 0 the token stream equals the CPU's. */
+int  ibh_model_generate(ibh_model* model, const int32_t* input_tokens, int num_input_tokens, int32_t* out_tokens,
+                        int max_out_tokens, const ibh_sample_params* params);
+
 /* ── greedy speculative decoding (host loop over the calls above) ── */
 
 /* ib_prompt_lookup_search (src/speculative.c:39-67); returns the number of

@@ -58,6 +58,8 @@ SIGNATURES = {
     "ibh_model_synchronize": (I, [P]),
     "ibh_model_forward_positions": (I, [P, P, I, P, I]),
     "ibh_prompt_lookup_search": (I, [P, I, I, I, P]),
+    "ibh_model_generate": (I, [P, P, I, P, I, P]),
+    "ibh_default_sample_params": (None, []),   # struct return: restype set below
     "ibh_model_generate_lookup": (I, [P, P, I, P, I, I, I]),
     "ibh_model_generate_draft": (I, [P, P, P, I, P, I, I]),
     "ibh_packed_row_bytes": (SZ, [I, I]),
@@ -98,6 +100,7 @@ def lib():
             f = getattr(L, name)
             f.restype = res
             f.argtypes = args
+        L.ibh_default_sample_params.restype = SampleParams
         _lib = L
     return _lib
 
@@ -125,3 +128,9 @@ class Int4gTensor(C.Structure):
     """ibh_int4g_tensor (include/ibhip.h)."""
     _fields_ = [(n, P) for n in ("q", "s", "inv_act", "outl_idx", "outl_val")] + \
                [(n, I) for n in ("M", "N", "G", "K_out")]
+
+
+class SampleParams(C.Structure):
+    """ibh_sample_params (include/ibhip.h) = inferbit_sample_params."""
+    _fields_ = [("temperature", C.c_float), ("top_k", I), ("top_p", C.c_float), ("repeat_penalty", C.c_float),
+                ("max_tokens", I), ("seed", I)]

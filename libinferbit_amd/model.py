@@ -8,7 +8,7 @@ import ctypes
 
 import numpy as np
 
-from ._lib import check, lib
+from ._lib import SampleParams, check, lib
 
 DIM_NAMES = ("num_layers", "hidden_size", "num_heads", "num_kv_heads", "head_dim", "intermediate_size",
              "vocab_size", "max_context_length", "kv_bits", "capacity", "eos_token_id", "positions", "exact")
@@ -53,6 +53,17 @@ class Model:
         n = lib().ibh_model_generate_greedy(self._h, _ptr(t), len(t), _ptr(out), max_out)
         if n < 0:
             check(n, "ibh_model_generate_greedy")
+        return out[:n]
+
+    def generate_sampled(self, tokens, max_out: int, temperature: float = 1.0, top_k: int = 40, top_p: float = 0.9,
+                         repeat_penalty: float = 1.0, seed: int = -1) -> np.ndarray:
+        """inferbit_generate with sampling parameters (src/generate.c:243-302)."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        out = np.empty(max_out, np.int32)
+        p = SampleParams(temperature, top_k, top_p, repeat_penalty, max_out, seed)
+        n = lib().ibh_model_generate(self._h, _ptr(t), len(t), _ptr(out), max_out, ctypes.byref(p))
+        if n < 0:
+            check(n, "ibh_model_generate")
         return out[:n]
 
     def forward_positions(self, tokens) -> np.ndarray:

@@ -19,7 +19,9 @@
  * written there and the cache is rewound.
  * REF_LOOKUP="ngram,k" turns on prompt-lookup speculation
  * (inferbit_set_prompt_lookup); REF_DRAFT=model.ibf with REF_DRAFT_K=k loads
- * a draft model for speculative decoding (inferbit_set_draft_model). */
+ * a draft model for speculative decoding (inferbit_set_draft_model).
+ * REF_SAMPLE="temperature,top_k,top_p,repeat_penalty,seed" samples with those
+ * parameters instead of greedy decoding. */
 #include "forward.c"
 
 #include <stdio.h>
@@ -127,6 +129,12 @@ int main(int argc, char** argv) {
     }
     inferbit_sample_params sp = inferbit_default_sample_params();
     sp.temperature = 0.0f;
+    /* REF_SAMPLE="temperature,top_k,top_p,repeat_penalty,seed" samples instead */
+    const char* se = getenv("REF_SAMPLE");
+    if (se && sscanf(se, "%f,%d,%f,%f,%d", &sp.temperature, &sp.top_k, &sp.top_p, &sp.repeat_penalty, &sp.seed) != 5) {
+        fprintf(stderr, "bad REF_SAMPLE\n");
+        return 1;
+    }
     int32_t* out = malloc((size_t)n_out * sizeof(int32_t));
     const double t0 = now_s();
     const int n = inferbit_generate(m, prompt, (int)(pn / 4), out, n_out, sp);

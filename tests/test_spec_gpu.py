@@ -152,3 +152,23 @@ def test_draft_model_tokens_match_reference(L, tmp_path, draft_k):
     assert got.tolist() == want
     m.close()
     d.close()
+
+
+SAMPLING = [(0.8, 40, 0.9, 1.0, 7), (1.0, 0, 1.0, 1.3, 123), (1.5, 5, 0.5, 1.1, 0), (0.3, 1000, 0.95, 1.0, 99)]
+
+
+@pytest.mark.parametrize("name", ["w4a8_int8kv", "all_int8"])
+@pytest.mark.parametrize("temp,top_k,top_p,pen,seed", SAMPLING)
+def test_sampled_tokens_match_reference(L, tmp_path, name, temp, top_k, top_p, pen, seed):
+    """inferbit_generate with sampling: same seed, same token stream (exact
+    mode gives the CPU's logits bit for bit; sampling runs the reference's
+    rules on the host)."""
+    from libinferbit_amd.model import Model
+    print(f"case sampled {name} T={temp} k={top_k} p={top_p} pen={pen} seed={seed}", flush=True)
+    path = write(tmp_path, name, seed=17)
+    prompt = [5, 17, 300, 42, 999, 0, 7]
+    want = ref(path, prompt, 48, tmp_path, {"REF_SAMPLE": f"{temp},{top_k},{top_p},{pen},{seed}"})
+    m = Model(path)
+    got = m.generate_sampled(prompt, 48, temp, top_k, top_p, pen, seed)
+    assert got.tolist() == want
+    m.close()
