@@ -40,7 +40,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--quick", action="store_true", help="headline only (for profiling runs)")
     p.add_argument("--no-decode", action="store_true", help="skip the end-to-end decode legs")
-    p.add_argument("--only", choices=["headline", "gemm", "pq", "int4g", "decode-tinyllama", "decode-mistral"],
+    p.add_argument("--only", choices=["headline", "gemm", "pq", "pqpol", "int4g", "verify", "decode-tinyllama",
+                            "decode-mistral"],
                    help="run one case and print its JSON (for profiler runs)")
     p.add_argument("--calib-copy", action="store_true",
                    help="first copy a 64 MiB buffer 8 times (the known-size kernel that scales the "
@@ -201,6 +202,69 @@ def int4g_case(torch, L, M, N, G, K_out, steps, warmup, awq=True):
             "GBps": round(nbytes / tm / 1e9, 1), "frac_hbm": round(nbytes / tm / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def pq_policy_cases(torch, L, steps, warmup):
+    """The PQ session's policy variants (ibh_pq_matmul_policy) at the
+    config-5 FFN shape with two levels (K = K_l2 = 256) and the top-K LM
+    head (ibh_pq_lm_head_topk, K_top = 50) at a 32000 x 4096 head."""
+    sys.path.insert(0, os.path.join(ROOT, "tests", "golden"))
+    from gen_golden import make_pq
+    rng = np.random.default_rng(21)
+    t = make_pq(rng, 4096, 896, 16, 256, 2, 256, 0)
+    devs = [L.ops.PqDeviceTensor(t) for _ in range(4)]
+    x = torch.randn(t["N"], generator=torch.Generator().manual_seed(5)).cuda()
+    x[: t["N"] // 4] *= 1e-4
+    y = torch.empty(4096, device="cuda")
+    out = {}
+    for name, (v, st, at) in {"streaming": (0, 0, 0), "l1_only": (1, 0, 0), "l2skip_0.5": (2, 0.5, 0),
+                              "sparse_1e-3": (3, 0, 1e-3), "int8": (4, 0, 0)}.items():
+        def launch(i, v=v, st=st, at=at):
+            devs[i % 4].matmul_policy(x, y, v, st, at)
+        out[name] = {"us": round(time_launches(torch, launch, steps, warmup) * 1e6, 2)}
+    th = make_pq(rng, 32000, 256, 16, 256, 2, 256, 0)
+    dh = L.ops.PqDeviceTensor(th)
+    xh = torch.randn(th["N"], generator=torch.Generator().manual_seed(6)).cuda()
+    for _ in range(3):
+        dh.lm_head_topk(xh, 50)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(50):
+        dh.lm_head_topk(xh, 50)
+    torch.cuda.synchronize()
+    out["lm_head_topk_32000x4096_k50"] = {"us_per_call_host_clock": round((time.perf_counter() - t0) / 50 * 1e6, 1)}
+    return out
+
+
+def verify_case(steps):
+    """Batched verify (ibh_model_forward_positions) on the TinyLlama
+    configuration: milliseconds for B positions in one pass vs B single
+    decode steps, both modes."""
+    sys.path.insert(0, os.path.join(ROOT, "tests", "golden"))
+    import gen_decode_golden as G
+    from libinferbit_amd.model import Model
+    workdir = os.environ.get("IBH_MODEL_DIR", "/tmp/ibh_models")
+    os.makedirs(workdir, exist_ok=True)
+    path = G.ensure_model("tinyllama", workdir)
+    out = {}
+    for mode in ("exact", "fast"):
+        m = Model(path)
+        m.set_exact(mode == "exact")
+        m.forward(list(range(1, 33)))
+        base = m.kv_length()
+        res = {}
+        for B in (1, 4, 8, 16):
+            toks = list(range(100, 100 + B))
+            m.forward_positions(toks)
+            m.kv_truncate(base)
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                m.forward_positions(toks)
+                m.kv_truncate(base)
+            res[f"B{B}_ms"] = round((time.perf_counter() - t0) / steps * 1e3, 3)
+        m.close()
+        out[mode] = res
+    return out
+
+
 def prefill_gemm_case(torch, L, steps, warmup):
     """INT8 prefill GEMM at BASELINE configs[4]: 512 tokens x 4096 -> 14336
     (ibh_gemm_int8, matmul_int8_batch semantics), x N(0,1).  One step = one
@@ -349,6 +413,10 @@ def main():
             r = prefill_gemm_case(torch, L, 64, 8)
         elif a.only == "pq":
             r = pq_case(torch, L, max(200, a.steps // 4), 20)
+        elif a.only == "pqpol":
+            r = pq_policy_cases(torch, L, max(200, a.steps // 4), 20)
+        elif a.only == "verify":
+            r = verify_case(10)
         elif a.only == "int4g":
             r = {"14336x4096": int4g_case(torch, L, 14336, 4096, 128, 8, a.steps, a.warmup),
                  "4096x14336": int4g_case(torch, L, 4096, 14336, 128, 28, a.steps, a.warmup),
@@ -378,6 +446,8 @@ def main():
         extra["prefill_gemm_int8_512x4096x14336"] = prefill_gemm_case(torch, L, 64, 8)
         print("bench: pq_4096x14336", file=sys.stderr, flush=True)
         extra["pq_4096x14336_G16_K256"] = pq_case(torch, L, max(200, a.steps // 4), 20)
+        print("bench: pq policies + top-K head", file=sys.stderr, flush=True)
+        extra["pq_policies_4096x14336_G16_K256_two_level"] = pq_policy_cases(torch, L, max(200, a.steps // 4), 20)
         print("bench: int4g (IBF v5 INT4 group-scale)", file=sys.stderr, flush=True)
         extra["int4g_14336x4096_G128_awq_out8"] = int4g_case(torch, L, 14336, 4096, 128, 8, a.steps, a.warmup)
         extra["int4g_4096x14336_G128_awq_out28"] = int4g_case(torch, L, 4096, 14336, 128, 28, a.steps, a.warmup)
@@ -386,6 +456,8 @@ def main():
         for name in ("tinyllama", "mistral"):
             print(f"bench: decode {name}", file=sys.stderr, flush=True)
             decode[name] = decode_case(name, 128, cpu=not a.no_cpu and name == "tinyllama")
+        print("bench: batched verify (forward_positions)", file=sys.stderr, flush=True)
+        decode["tinyllama_forward_positions"] = verify_case(10)
     cpu = None if a.no_cpu else cpu_baseline()
     out = {
         "metric": "quantized GEMV HBM GB/s (% of peak) + decode tok/s, Mistral-7B-shape INT4, 1 GPU",

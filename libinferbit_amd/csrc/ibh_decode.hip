@@ -377,6 +377,7 @@ struct ibh_model {
     int* bpos = nullptr;
     int hpos = 0;
     hipGraphExec_t exec = nullptr;
+    hipGraphExec_t bexec[2][33] = {};   // forward_batch graphs per (exact, B)
     std::vector<void*> allocs;
     int* dpos() { return dstate; }
     int* dprompt_end() { return dstate + 1; }
@@ -397,6 +398,9 @@ int dalloc(ibh_model* m, void** p, size_t bytes) {
 void free_model(ibh_model* m) {
     if (!m) return;
     if (m->exec) hipGraphExecDestroy(m->exec);
+    for (auto& row : m->bexec)
+        for (hipGraphExec_t& g : row)
+            if (g) hipGraphExecDestroy(g);
     if (m->st) hipStreamSynchronize(m->st);
     for (void* p : m->allocs) hipFree(p);
     if (m->st) hipStreamDestroy(m->st);
@@ -1180,7 +1184,31 @@ extern "C" int ibh_model_forward_positions(ibh_model* m, const int32_t* tokens, 
             "ibh_model_forward_positions: tokens");
     IBH_HIP(hipMemcpyAsync(m->bpos, pos, (size_t)n * 4, hipMemcpyHostToDevice, m->st),
             "ibh_model_forward_positions: positions");
-    if ((rc = forward_batch(m, n))) return rc;
+    // one captured graph per (mode, B): the positions and tokens are device
+    // state, so the same graph serves every kv_length
+    hipGraphExec_t& ge = m->bexec[m->exact ? 1 : 0][n];
+    if (!ge && !eager_mode()) {
+        hipGraph_t g = nullptr;
+        IBH_HIP(hipStreamBeginCapture(m->st, hipStreamCaptureModeThreadLocal), "ibh_model_forward_positions: capture");
+        rc = forward_batch(m, n);
+        const hipError_t e = hipStreamEndCapture(m->st, &g);
+        if (rc) {
+            if (g) hipGraphDestroy(g);
+            return rc;
+        }
+        if (e != hipSuccess || hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) != hipSuccess) {
+            if (g) hipGraphDestroy(g);
+            ge = nullptr;
+            ibh_set_error("ibh_model_forward_positions: graph capture failed");
+            return IBH_ERROR_INTERNAL;
+        }
+        hipGraphDestroy(g);
+    }
+    if (ge) {
+        IBH_HIP(hipGraphLaunch(ge, m->st), "ibh_model_forward_positions: graph launch");
+    } else if ((rc = forward_batch(m, n))) {
+        return rc;
+    }
     IBH_HIP(hipMemcpyAsync(logits, m->blogits, (size_t)n * vocab * 4, hipMemcpyDeviceToHost, m->st),
             "ibh_model_forward_positions: logits");
     IBH_HIP(hipStreamSynchronize(m->st), "ibh_model_forward_positions");

@@ -243,28 +243,84 @@ __global__ __launch_bounds__(256) void matvec_exact(const RowSet rs, const float
 // (forward.c:292-317: masked rows are 0), fp16 weights (forward.c:174-182,
 // no scales) and the x86 table's matmul_int8_batch (kernels/scalar.c:70-84).
 // BITS 16 ignores the scales.  blockIdx.y is the batch slot: x[b*N], y[b*ys].
+constexpr int kSerTile = 2048;   // x columns staged in LDS per pass
+
+// Weight element e of a 16-byte chunk as float (int8; int4 nibble - 8, low
+// nibble first; int2 code - 1, low bits first; fp16).
+template <int BITS>
+__device__ __forceinline__ float ser_elem(const u32x4_t c, int e) {
+    const uint32_t d = c[e / (32 / BITS)];
+    const int k = e % (32 / BITS);
+    if constexpr (BITS == 8) return (float)(int8_t)(d >> (8 * k));
+    else if constexpr (BITS == 4) return (float)((int)((d >> (4 * k)) & 15u) - 8);
+    else if constexpr (BITS == 2) return (float)((int)((d >> (2 * k)) & 3u) - 1);
+    else return f16_to_f32((uint16_t)(d >> (16 * k)));
+}
+
+// One serial mul/add chain per row: the INT2 table kernel
+// (kernels/ternary.c:20-46), the sparse-row path of tensor_matmul_sparse
+// (forward.c:292-317: masked rows are 0), fp16 weights (forward.c:174-182,
+// no scales) and the x86 table's matmul_int8_batch (kernels/scalar.c:70-84).
+// BITS 16 ignores the scales.  blockIdx.y is the batch slot: x[b*N], y[b*ys].
+// x is staged in LDS a tile at a time (every row of the block reads the same
+// column: a broadcast); each row streams its bytes 16 at a time with the
+// next chunk already in flight.  The chain order is j = 0 .. N-1.
 template <int BITS, int KIND>
 __global__ __launch_bounds__(256) void matvec_serial_exact(float* __restrict__ y, const uint8_t* __restrict__ W,
                                                            const void* __restrict__ sc, const float* __restrict__ x,
                                                            const uint8_t* __restrict__ mask, int M, int N,
                                                            int ys = 0) {
+    __shared__ float xs[kSerTile];
+    constexpr int CPC = 128 / BITS;                       // columns per 16-byte chunk
     const int row = blockIdx.x * 256 + threadIdx.x;
-    if (row >= M) return;
     x += (size_t)blockIdx.y * N;
     y += (size_t)blockIdx.y * ys;
-    if (mask && !mask[row]) {
+    const bool active = row < M && !(mask && !mask[row]);
+    const size_t rb = (size_t)N * BITS / 8;
+    const uint8_t* wr = W + (size_t)min(row, M - 1) * rb;
+    const bool vec = ((rb | (uintptr_t)W) & 15) == 0;
+    float sum = 0.f;
+    for (int j0 = 0; j0 < N; j0 += kSerTile) {
+        const int jn = min(kSerTile, N - j0);
+        __syncthreads();
+        for (int i = threadIdx.x; i < jn; i += 256) xs[i] = x[j0 + i];
+        __syncthreads();
+        if (!active) continue;
+        if (vec) {
+            const u32x4_t* cp = (const u32x4_t*)(wr + (size_t)j0 * BITS / 8);
+            const int full = jn / CPC;
+            u32x4_t cur = full > 0 ? cp[0] : u32x4_t{0u, 0u, 0u, 0u};
+            for (int ci = 0; ci < full; ci++) {
+                const u32x4_t nxt = ci + 1 < full ? cp[ci + 1] : cur;
+#pragma unroll
+                for (int e = 0; e < CPC; e++) sum = sum + ser_elem<BITS>(cur, e) * xs[ci * CPC + e];
+                cur = nxt;
+            }
+            for (int j = full * CPC; j < jn; j++) {
+                const int jj = j0 + j;
+                float wv;
+                if constexpr (BITS == 8) wv = (float)(int8_t)wr[jj];
+                else if constexpr (BITS == 4) wv = (float)((int)((jj & 1) ? (wr[jj / 2] >> 4) : (wr[jj / 2] & 0xf)) - 8);
+                else if constexpr (BITS == 2) wv = (float)((int)((wr[jj / 4] >> (2 * (jj & 3))) & 3) - 1);
+                else wv = f16_to_f32(((const uint16_t*)wr)[jj]);
+                sum = sum + wv * xs[j];
+            }
+        } else {
+            for (int j = 0; j < jn; j++) {
+                const int jj = j0 + j;
+                float wv;
+                if constexpr (BITS == 8) wv = (float)(int8_t)wr[jj];
+                else if constexpr (BITS == 4) wv = (float)((int)((jj & 1) ? (wr[jj / 2] >> 4) : (wr[jj / 2] & 0xf)) - 8);
+                else if constexpr (BITS == 2) wv = (float)((int)((wr[jj / 4] >> (2 * (jj & 3))) & 3) - 1);
+                else wv = f16_to_f32(((const uint16_t*)wr)[jj]);
+                sum = sum + wv * xs[j];
+            }
+        }
+    }
+    if (row >= M) return;
+    if (!active) {
         y[row] = 0.f;
         return;
-    }
-    const uint8_t* wr = W + (size_t)row * ((size_t)N * BITS / 8);
-    float sum = 0.f;
-    for (int j = 0; j < N; j++) {
-        float wv;
-        if constexpr (BITS == 8) wv = (float)(int8_t)wr[j];
-        else if constexpr (BITS == 4) wv = (float)((int)((j & 1) ? (wr[j / 2] >> 4) : (wr[j / 2] & 0xf)) - 8);
-        else if constexpr (BITS == 2) wv = (float)((int)((wr[j / 4] >> (2 * (j & 3))) & 3) - 1);
-        else wv = f16_to_f32(((const uint16_t*)wr)[j]);
-        sum = sum + wv * x[j];
     }
     y[row] = BITS == 16 ? sum : sum * load_scale<KIND>(sc, row);
 }

@@ -172,3 +172,21 @@ def test_sampled_tokens_match_reference(L, tmp_path, name, temp, top_k, top_p, p
     got = m.generate_sampled(prompt, 48, temp, top_k, top_p, pen, seed)
     assert got.tolist() == want
     m.close()
+
+
+def test_forward_positions_graph_equals_eager(L, tmp_path, monkeypatch):
+    """The captured per-B graph gives the eager launches' logits, call after
+    call, at different cache lengths, in both modes."""
+    from libinferbit_amd.model import Model
+    path = write(tmp_path, "w4a8_int8kv", seed=3)
+    for exact in (True, False):
+        monkeypatch.delenv("IBH_DECODE_EAGER", raising=False)
+        g = Model(path)
+        g.set_exact(exact)
+        monkeypatch.setenv("IBH_DECODE_EAGER", "1")
+        e = Model(path)
+        e.set_exact(exact)
+        for chunk in ([5, 6, 7, 8], [9, 10, 11, 12], [1, 2], [3, 4, 5, 6]):
+            np.testing.assert_array_equal(g.forward_positions(chunk), e.forward_positions(chunk))
+        g.close()
+        e.close()
