@@ -240,6 +240,55 @@ int    ibh_int4g_matmul(const ibh_int4g_tensor* t, const float* x, float* out, f
 int    ibh_int4g_matmul_batched(const ibh_int4g_tensor* t, int B, const float* x, float* out, float act_sparse_rel,
                                 void* ws, size_t ws_bytes, void* stream);
 
+/* ── IBF v5 PQ session on the GPU ─────────────────────────── */
+
+/* Opaque session: an IBF v5 file (src/pq_decode.c:685-849) whose data
+ * region lives in HBM unchanged, replacing ib_pq_session
+ * (src/pq_decode.h:345-403).  Same error convention as the rest of this
+ * library (0 / negative IBH_ERROR_*, message in ibh_last_error). */
+typedef struct ibh_v5_session ibh_v5_session;
+typedef struct ibh_v5_kv ibh_v5_kv;
+/* ib_pq_session_open / _close (src/pq_decode.c:4111-4362).  Detects the
+ * fp16 (<base>__fp16w), INT4 (<base>__i4_q / __i4_s [+ __act_scale,
+ * __i4_outl_idx / _val]) and PQ tensors and checks the decoder's tensors
+ * (L{i}_{q,k,v,o,gate,up,down}_proj or fused qkv / gateup, norms,
+ * final_norm, lm_head, tok_embed) once. */
+int  ibh_v5_open(const char* path, ibh_v5_session** out);
+void ibh_v5_close(ibh_v5_session* s);
+/* dims[9] = layers, hidden, heads, kv_heads, head_dim, intermediate, vocab,
+ * fused qkv (1/0), fused gateup (1/0) -- the config keys the reference
+ * reads at src/pq_decode.c:4944-4952. */
+int  ibh_v5_dims(const ibh_v5_session* s, int* dims);
+/* ib_pq_session_tensor_shape (src/pq_decode.c:4541-4560) plus the backend
+ * the session matmul takes: kind 0 PQ, 1 INT4, 2 fp16. */
+int  ibh_v5_tensor_info(const ibh_v5_session* s, const char* name, int* kind, int* M, int* N);
+/* ib_pq_session_set_default_policy / _set_policy (src/pq_decode.c:
+ * 4364-4383); set_policy names a PQ tensor. */
+int  ibh_v5_set_default_policy(ibh_v5_session* s, const ibh_pq_policy* p);
+int  ibh_v5_set_policy(ibh_v5_session* s, const char* name, const ibh_pq_policy* p);
+/* ib_pq_session_matmul (src/pq_decode.c:4430-4491) on device pointers:
+ * x [N], out [M]; ordered after earlier work on `stream`. */
+int  ibh_v5_session_matmul(ibh_v5_session* s, const char* name, const float* x, float* out, void* stream);
+/* ib_pq_kv_cache_create / _free / _clear / _length (src/pq_decode.c:
+ * 4740-4852): fp32 K and V [layer][pos][kv_dim] in HBM (the reference's
+ * default storage; its IB_PQ_KV_FP16 / _INT8 / _PYRAMID modes are not
+ * provided). */
+int  ibh_v5_kv_create(ibh_v5_session* s, int max_seq, ibh_v5_kv** out);
+void ibh_v5_kv_free(ibh_v5_kv* kv);
+void ibh_v5_kv_clear(ibh_v5_kv* kv);
+int  ibh_v5_kv_length(const ibh_v5_kv* kv);
+/* ib_pq_forward_step (src/pq_decode.c:5286-5289): host logits [vocab], or
+ * NULL for a step that only fills the cache. */
+int  ibh_v5_forward_step(ibh_v5_session* s, ibh_v5_kv* kv, int token_id, int pos, float* logits);
+/* ib_pq_forward_step_to_hidden (src/pq_decode.c:5291-5295): the
+ * post-final-norm hidden state [hidden] on the host. */
+int  ibh_v5_forward_step_to_hidden(ibh_v5_session* s, ibh_v5_kv* kv, int token_id, int pos, float* hidden);
+/* ib_pq_generate_greedy (src/pq_decode.c:5297-5346): prompt prefill, then
+ * per token the top-8 PQ LM head (ibh_pq_lm_head_topk); stops at eos
+ * (>= 0) or a full cache.  Host arrays; lm_head must be PQ. */
+int  ibh_v5_generate_greedy(ibh_v5_session* s, ibh_v5_kv* kv, const int* prompt_ids, int n_prompt, int max_new,
+                            int eos_token_id, int* out_ids, int* n_out);
+
 /* ── device-resident decode (forward_single_ex + greedy generate) ── */
 
 /* Opaque model: an IBF v1 file (src/ibf_loader.c:300-546) whose weight region

@@ -44,6 +44,20 @@ SIGNATURES = {
     "ibh_int4g_workspace_bytes": (SZ, [P]),
     "ibh_int4g_matmul": (I, [P, P, P, C.c_float, P, SZ, P]),
     "ibh_int4g_matmul_batched": (I, [P, I, P, P, C.c_float, P, SZ, P]),
+    "ibh_v5_open": (I, [C.c_char_p, P]),
+    "ibh_v5_close": (None, [P]),
+    "ibh_v5_dims": (I, [P, P]),
+    "ibh_v5_tensor_info": (I, [P, C.c_char_p, P, P, P]),
+    "ibh_v5_set_default_policy": (I, [P, P]),
+    "ibh_v5_set_policy": (I, [P, C.c_char_p, P]),
+    "ibh_v5_session_matmul": (I, [P, C.c_char_p, P, P, P]),
+    "ibh_v5_kv_create": (I, [P, I, P]),
+    "ibh_v5_kv_free": (None, [P]),
+    "ibh_v5_kv_clear": (None, [P]),
+    "ibh_v5_kv_length": (I, [P]),
+    "ibh_v5_forward_step": (I, [P, P, I, I, P]),
+    "ibh_v5_forward_step_to_hidden": (I, [P, P, I, I, P]),
+    "ibh_v5_generate_greedy": (I, [P, P, P, I, I, I, P, P]),
     "ibh_model_load": (I, [C.c_char_p, I, P]),
     "ibh_model_free": (None, [P]),
     "ibh_model_dims": (I, [P, P]),

@@ -1,0 +1,1036 @@
+// ibh_v5.hip -- the IBF v5 PQ session on the GPU: loader, KV cache,
+// single-token forward step and greedy generation (src/pq_decode.c
+// ib_pq_session_open 4111-4362, ib_pq_kv_cache_create 4740-4837,
+// forward_step_internal_sc 4938-5284, ib_pq_generate_greedy 5297-5346).
+//
+// Device layout:
+//   weight arena   the file's data region [weight_data_start, EOF) copied to
+//                  HBM unchanged; every PQ block and raw tensor is a pointer
+//                  at arena + offset (the file's own layout, so a tensor
+//                  costs no repacking);
+//   side arrays    inner_cols of PQ tensors with outlier columns, unpacked
+//                  bit-packed level-2 indices (l2_packed_bits);
+//   KV cache       fp32 [layer][pos][kv_dim] for K and for V (the
+//                  reference's default storage);
+//   rope table     (cos, sin)[pos][head_dim/2] computed on the host with the
+//                  reference's powf / cosf / sinf expressions.
+//
+// A step is a chain of launches on the session's stream: embedding row ->
+// per layer { residual add + rmsnorm -> q/k/v (or fused qkv) matvecs ->
+// NEOX rope of q and k + cache write -> split-K attention -> o matvec ->
+// residual add + rmsnorm -> gate/up (or fused) -> silu * up -> down } ->
+// final residual + rmsnorm -> lm_head.  Matvecs dispatch like
+// ib_pq_session_matmul (4430-4491): an fp16 tensor <name>__fp16w, else an
+// INT4 tensor <name>__i4_q/__i4_s (ibh_int4g_matmul), else the PQ tensor
+// with its policy (ibh_pq_matmul_policy), x pre-multiplied by
+// <name>__act_scale when present.  fp32 results differ from the CPU by
+// summation order only.
+#include <fcntl.h>
+#include <math.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <algorithm>
+#include <string>
+#include <vector>
+
+#include "ibh_common.h"
+#include "ibh_json.h"
+
+using namespace ibh;
+
+int ibh_launch_attn(float* out, const float* q, const void* kdata, const void* vdata, const float* kscales,
+                    const float* vscales, int pos, const int* dpos, int max_pos, int n_heads, int n_kv,
+                    int head_dim, int kv_bits, void* ws, size_t ws_bytes, hipStream_t st);
+
+namespace {
+
+enum { RAW_F32 = 0, RAW_F16, RAW_I32, RAW_I16, RAW_I8, RAW_U8, RAW_U16 };
+
+struct RawT {
+    std::string name;
+    int dtype = 0, ndim = 0;
+    int shape[4] = {0, 0, 0, 0};
+    size_t off = 0, size = 0;
+    void* d = nullptr;
+};
+
+enum { MAT_PQ = 0, MAT_INT4 = 1, MAT_F16 = 2 };
+
+struct Mat {
+    std::string name;
+    int kind = MAT_PQ, M = 0, N = 0;
+    ibh_pq_tensor pq{};
+    const float* act_inv = nullptr;   // PQ: <name>__act_scale
+    ibh_int4g_tensor i4{};
+    const uint16_t* w16 = nullptr;
+    bool has_policy = false;
+    ibh_pq_policy policy{0, 0.f, 0.f};
+};
+
+constexpr int kNormThreads = 1024;
+constexpr int kNormMaxPer = 16;   // hidden <= 16384
+
+__global__ void embed_raw_kernel(float* __restrict__ x, const void* __restrict__ emb, int f16, int token,
+                                 int hidden) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= hidden) return;
+    const size_t at = (size_t)token * hidden + i;
+    x[i] = f16 ? f16_to_f32(((const uint16_t*)emb)[at]) : ((const float*)emb)[at];
+}
+
+// ib_pq_session_reconstruct_row (src/pq_decode.c:6136-6198): chunk c places
+// (cb1 + cb2) of its two halves at inner_cols, times the row scale; outlier
+// columns are sidecar * column scale.
+__global__ void pq_row_kernel(float* __restrict__ out, ibh_pq_tensor t, int row) {
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    const int half = t.G / 2;
+    const float rs = f16_to_f32(t.row_scale[row]);
+    if (j < t.C * t.G) {
+        const int c = j / t.G, w = j - c * t.G, side = w >= half, e = side ? w - half : w;
+        const int i1 = (side ? t.indices_l1_r : t.indices_l1_l)[(size_t)row * t.C + c];
+        float v = f16_to_f32((side ? t.codebook_l1_r : t.codebook_l1_l)[(size_t)i1 * half + e]);
+        if (t.n_levels == 2) {
+            const int K2 = t.K_l2 > 0 ? t.K_l2 : t.K;
+            const uint8_t* base = side ? t.indices_l2_r : t.indices_l2_l;
+            int i2;
+            if (K2 == 16) {
+                const uint8_t b = base[(size_t)row * ((t.C + 1) / 2) + (c >> 1)];
+                i2 = (c & 1) ? (b >> 4) : (b & 0xf);
+            } else if (t.l2_idx_bytes == 2) {
+                i2 = ((const uint16_t*)base)[(size_t)row * t.C + c];
+            } else {
+                i2 = base[(size_t)row * t.C + c];
+            }
+            v += f16_to_f32((side ? t.codebook_l2_r : t.codebook_l2_l)[(size_t)i2 * half + e]);
+        }
+        out[t.inner_cols ? t.inner_cols[j] : j] = v * rs;
+    } else if (j < t.C * t.G + t.n_outlier) {
+        const int k = j - t.C * t.G;
+        out[t.outlier_cols[k]] =
+            (float)t.outlier_sidecar[(size_t)row * t.n_outlier + k] * f16_to_f32(t.outlier_scale[k]);
+    }
+}
+
+// ib_residual_add_f32 then ib_rmsnorm_f32 (src/pq_decode.c:4603-4621):
+//   x += delta (delta may be null);  s = sum (double) x^2;
+//   inv = 1 / sqrtf((float)(s / H) + eps);  out = x * inv * w.
+// One block; the squares are summed in double like the reference.
+__global__ __launch_bounds__(kNormThreads) void v5_rmsnorm_kernel(float* __restrict__ out, float* __restrict__ x,
+                                                                  const float* __restrict__ delta,
+                                                                  const float* __restrict__ w, float eps, int n) {
+    __shared__ double red[kNormThreads / 64];
+    float v[kNormMaxPer];
+    double ss = 0.0;
+#pragma unroll
+    for (int j = 0; j < kNormMaxPer; j++) {
+        const int i = threadIdx.x + j * kNormThreads;
+        v[j] = 0.f;
+        if (i < n) {
+            float xv = x[i];
+            if (delta) {
+                xv = xv + delta[i];
+                x[i] = xv;
+            }
+            v[j] = xv;
+            ss += (double)xv * (double)xv;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, kWave);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    double tot = 0.0;
+    for (int k = 0; k < kNormThreads / 64; k++) tot += red[k];
+    const float inv = 1.0f / sqrtf((float)(tot / (double)n) + eps);
+#pragma unroll
+    for (int j = 0; j < kNormMaxPer; j++) {
+        const int i = threadIdx.x + j * kNormThreads;
+        if (i < n) out[i] = v[j] * inv * w[i];
+    }
+}
+
+// ib_rope_f32 (NEOX halves, src/pq_decode.c:4623-4642) of the query heads in
+// place and of the key heads into the cache row, plus the value copy.
+// Block b < n_heads: query head; < n_heads + n_kv: key head; else value head.
+__global__ void v5_rope_kv_kernel(float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+                                  float* __restrict__ kc, float* __restrict__ vc, const float* __restrict__ cs,
+                                  int n_heads, int n_kv, int hd) {
+    const int b = blockIdx.x, half = hd / 2;
+    for (int i = threadIdx.x; i < half; i += blockDim.x) {
+        if (b < n_heads + n_kv) {
+            const float* src = b < n_heads ? q + (size_t)b * hd : k + (size_t)(b - n_heads) * hd;
+            float* dst = b < n_heads ? q + (size_t)b * hd : kc + (size_t)(b - n_heads) * hd;
+            const float c = cs[2 * i], s = cs[2 * i + 1];
+            const float a = src[i], e = src[i + half];
+            dst[i] = a * c - e * s;
+            dst[i + half] = e * c + a * s;
+        } else {
+            const int h = b - n_heads - n_kv;
+            vc[(size_t)h * hd + i] = v[(size_t)h * hd + i];
+            vc[(size_t)h * hd + i + half] = v[(size_t)h * hd + i + half];
+        }
+    }
+}
+
+// ib_silu_gate_f32 (src/pq_decode.c:4610-4616).
+__global__ void v5_silu_kernel(float* __restrict__ out, const float* __restrict__ gate, const float* __restrict__ up,
+                               int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float g = gate[i];
+    out[i] = g / (1.0f + ib_expf(-g)) * up[i];
+}
+
+__global__ void v5_scale_kernel(float* __restrict__ out, const float* __restrict__ x, const float* __restrict__ s,
+                                int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = x[i] * s[i];
+}
+
+// fp16w_rows (src/pq_decode.c:3490-3535): out[m] = sum_j fp16(w[m][j]) x[j].
+// One wavefront per row, 8 halves per lane per step.
+__global__ __launch_bounds__(256) void v5_f16_matvec(float* __restrict__ out, const uint16_t* __restrict__ w,
+                                                     const float* __restrict__ x, int M, int N) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= M) return;
+    const uint16_t* wr = w + (size_t)row * N;
+    float acc = 0.f;
+    if ((N & 7) == 0) {
+        for (int j = lane * 8; j < N; j += 512) {
+            const uint4 u = *(const uint4*)(wr + j);
+            const uint32_t wv[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                acc = fmaf(f16_to_f32((uint16_t)(wv[k] & 0xffff)), x[j + 2 * k], acc);
+                acc = fmaf(f16_to_f32((uint16_t)(wv[k] >> 16)), x[j + 2 * k + 1], acc);
+            }
+        }
+    } else {
+        for (int j = lane; j < N; j += 64) acc = fmaf(f16_to_f32(wr[j]), x[j], acc);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) out[row] = acc;
+}
+
+}  // namespace
+
+struct ibh_v5_session {
+    int n_layers = 0, hidden = 0, n_heads = 0, n_kv = 0, head_dim = 0, inter = 0, vocab = 0;
+    float eps = 1e-5f, theta = 10000.f, act_sparse_rel = 0.f;
+    int kv_dim = 0;
+    bool fused_qkv = false, fused_gu = false;
+    std::vector<RawT> raws;
+    std::vector<Mat> mats;
+    std::string config_json;
+    ibh_pq_policy default_policy{IBH_PQ_VARIANT_STREAMING, 0.f, 0.f};
+    hipStream_t st = nullptr;
+    std::vector<void*> allocs;
+    uint8_t* arena = nullptr;
+    size_t arena_bytes = 0;
+    // per-layer lookups
+    std::vector<const float*> w_in, w_pn;
+    std::vector<int> mq, mk, mv, mo, mg, mu, md, mqkv, mgu;
+    const float* w_final = nullptr;
+    int m_head = -1;
+    int embed_kind = -1;   // 0 raw f32, 1 raw f16, 2 PQ
+    const void* embed = nullptr;
+    int embed_mat = -1;
+    // activations
+    float *x = nullptr, *xb = nullptr, *xb2 = nullptr, *q = nullptr, *kn = nullptr, *vn = nullptr, *qkv = nullptr;
+    float *gate = nullptr, *up = nullptr, *gu = nullptr, *delta = nullptr, *xs = nullptr, *logits = nullptr;
+    float* top_val = nullptr;
+    int32_t* top_ids = nullptr;
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+};
+
+struct ibh_v5_kv {
+    ibh_v5_session* s = nullptr;
+    int max_seq = 0, length = 0;
+    float *k = nullptr, *v = nullptr, *rope = nullptr;
+    void* aws = nullptr;
+    size_t aws_bytes = 0;
+};
+
+namespace {
+
+int salloc(ibh_v5_session* s, void** p, size_t bytes) {
+    if (hipMalloc(p, bytes ? bytes : 16) != hipSuccess) {
+        ibh_set_error("ibh_v5: device allocation of %zu bytes failed", bytes);
+        return IBH_ERROR_MEMORY;
+    }
+    s->allocs.push_back(*p);
+    return IBH_OK;
+}
+
+bool pread_all(int fd, void* dst, size_t n, size_t off) {
+    uint8_t* d = (uint8_t*)dst;
+    while (n) {
+        const ssize_t r = pread(fd, d, n, (off_t)off);
+        if (r <= 0) return false;
+        d += r;
+        off += (size_t)r;
+        n -= (size_t)r;
+    }
+    return true;
+}
+
+const RawT* raw_find(const ibh_v5_session* s, const std::string& n) {
+    for (auto& r : s->raws)
+        if (r.name == n) return &r;
+    return nullptr;
+}
+
+int mat_find(const ibh_v5_session* s, const std::string& n) {
+    // ib_pq_session_matmul's precedence: fp16w, then INT4, then PQ
+    for (int k = MAT_F16; k >= MAT_PQ; k--)
+        for (size_t i = 0; i < s->mats.size(); i++)
+            if (s->mats[i].kind == k && s->mats[i].name == n) return (int)i;
+    return -1;
+}
+
+bool ends_with(const std::string& a, const char* suf, std::string* base) {
+    const size_t n = strlen(suf);
+    if (a.size() <= n || a.compare(a.size() - n, n, suf) != 0) return false;
+    if (base) *base = a.substr(0, a.size() - n);
+    return true;
+}
+
+void free_session(ibh_v5_session* s) {
+    if (!s) return;
+    if (s->st) hipStreamSynchronize(s->st);
+    for (void* p : s->allocs) hipFree(p);
+    if (s->st) hipStreamDestroy(s->st);
+    delete s;
+}
+
+size_t raw_elem(int dt) {
+    switch (dt) {
+    case RAW_F32: case RAW_I32: return 4;
+    case RAW_F16: case RAW_I16: case RAW_U16: return 2;
+    default: return 1;
+    }
+}
+
+// One PQ tensor's header (load_one_tensor, src/pq_decode.c:391-528): block
+// pointers into the arena, validated sizes; host work for inner_cols and
+// bit-packed level-2 indices.
+int load_pq(ibh_v5_session* s, int fd, size_t wds, const std::string& name, const JVal& tm, Mat* m) {
+    ibh_pq_tensor& t = m->pq;
+    const JVal* f = tm.get("format");
+    const std::string fmt = f && f->kind == JVal::STR ? f->str : "";
+    int format = 0;
+    if (fmt == "pq2d_v1_l1") format = 1;
+    else if (fmt == "pq2d_v1_l2") format = 2;
+    else if (fmt == "pq2d_v1_l1_l2") format = 3;
+    else if (fmt == "pq2d_v1_pyramid") format = IBH_PQ_FORMAT_PYRAMID;
+    const JVal* shape = tm.get("shape");
+    if (!format || !shape || shape->kind != JVal::ARR || shape->arr.size() != 2) {
+        ibh_set_error("ibh_v5_open: tensor %s: bad format or shape", name.c_str());
+        return IBH_ERROR_FORMAT;
+    }
+    const JVal* rot = tm.get("rotate");
+    if (rot && ((rot->kind == JVal::BOOL && rot->b) || (rot->kind == JVal::NUM && rot->num != 0))) {
+        ibh_set_error("ibh_v5_open: tensor %s: rotated PQ tensors are not supported", name.c_str());
+        return IBH_ERROR_FORMAT;
+    }
+    t.format = format;
+    t.M = (int)shape->arr[0].num;
+    t.N = (int)shape->arr[1].num;
+    t.G = jint(&tm, "G", 0);
+    t.K = jint(&tm, "K", 0);
+    t.n_levels = jint(&tm, "n_levels", 0);
+    t.n_outlier = jint(tm.get("outlier"), "n_cols", 0);
+    t.K_l2 = jint(&tm, "K_l2", 0);
+    const int n_inner = t.N - t.n_outlier;
+    if (t.M <= 0 || t.N <= 0 || t.G <= 0 || t.K <= 0 || (t.G & 1) || n_inner <= 0 || n_inner % t.G ||
+        (t.n_levels != 1 && t.n_levels != 2) || t.K > 256) {
+        ibh_set_error("ibh_v5_open: tensor %s: unsupported geometry", name.c_str());
+        return IBH_ERROR_FORMAT;
+    }
+    t.C = n_inner / t.G;
+    const int K2 = t.K_l2 > 0 ? t.K_l2 : t.K;
+    if (t.n_levels == 2 && format != IBH_PQ_FORMAT_PYRAMID && K2 != 16 && K2 != 64 && K2 != t.K) {
+        ibh_set_error("ibh_v5_open: tensor %s: K_l2 %d not in {16, 64, K}", name.c_str(), K2);
+        return IBH_ERROR_FORMAT;
+    }
+    const bool packed4 = K2 == 16;
+    t.l2_idx_bytes = (format == IBH_PQ_FORMAT_PYRAMID && K2 > 256) ? 2 : 1;
+    const int packed_bits = jint(&tm, "l2_packed_bits", 0);
+    const size_t half = (size_t)t.G / 2, M = (size_t)t.M, C = (size_t)t.C;
+    const size_t l2_row = packed4 ? (C + 1) / 2 : C * t.l2_idx_bytes;
+    auto block = [&](const char* key, size_t expect, const void** ptr) -> int {
+        const JVal* b = tm.get(key);
+        if (!b || b->kind != JVal::OBJ) {
+            ibh_set_error("ibh_v5_open: tensor %s: block %s missing", name.c_str(), key);
+            return IBH_ERROR_FORMAT;
+        }
+        const size_t off = jsize(b, "offset", (size_t)-1), sz = jsize(b, "size", 0);
+        if (sz != expect || off > s->arena_bytes || sz > s->arena_bytes - off) {
+            ibh_set_error("ibh_v5_open: tensor %s: block %s has size %zu (expected %zu) or lies outside the file",
+                          name.c_str(), key, sz, expect);
+            return IBH_ERROR_FORMAT;
+        }
+        *ptr = s->arena + off;
+        return IBH_OK;
+    };
+    int rc;
+#define IBH_BLK(key, field, type, sz) \
+    do { const void* p_; if ((rc = block(key, sz, &p_)) != IBH_OK) return rc; t.field = (type)p_; } while (0)
+    IBH_BLK("codebook_l1_l", codebook_l1_l, const uint16_t*, (size_t)t.K * half * 2);
+    IBH_BLK("codebook_l1_r", codebook_l1_r, const uint16_t*, (size_t)t.K * half * 2);
+    IBH_BLK("indices_l1_l", indices_l1_l, const uint8_t*, M * C);
+    IBH_BLK("indices_l1_r", indices_l1_r, const uint8_t*, M * C);
+    IBH_BLK("row_scale", row_scale, const uint16_t*, M * 2);
+    if (t.n_levels == 2) {
+        IBH_BLK("codebook_l2_l", codebook_l2_l, const uint16_t*, (size_t)K2 * half * 2);
+        IBH_BLK("codebook_l2_r", codebook_l2_r, const uint16_t*, (size_t)K2 * half * 2);
+        if (packed_bits > 0 && !packed4) {
+            // bit-packed on disk, uint16 in memory (pq_unpack_bits_to_u16,
+            // src/pq_decode.c:1078-1095: LSB-first bit stream per row)
+            if (t.l2_idx_bytes != 2 || packed_bits > 16) {
+                ibh_set_error("ibh_v5_open: tensor %s: l2_packed_bits needs a pyramid with K_l2 > 256",
+                              name.c_str());
+                return IBH_ERROR_FORMAT;
+            }
+            const size_t disk_row = (C * packed_bits + 7) >> 3;
+            const char* keys[2] = {"indices_l2_l", "indices_l2_r"};
+            for (int side = 0; side < 2; side++) {
+                const JVal* b = tm.get(keys[side]);
+                const size_t off = jsize(b, "offset", (size_t)-1), sz = jsize(b, "size", 0);
+                if (!b || sz != M * disk_row || off > s->arena_bytes || sz > s->arena_bytes - off) {
+                    ibh_set_error("ibh_v5_open: tensor %s: packed block %s has the wrong size", name.c_str(),
+                                  keys[side]);
+                    return IBH_ERROR_FORMAT;
+                }
+                std::vector<uint8_t> disk(sz + 4, 0);
+                if (!pread_all(fd, disk.data(), sz, wds + off)) {
+                    ibh_set_error("ibh_v5_open: cannot read %s of %s", keys[side], name.c_str());
+                    return IBH_ERROR_LOAD;
+                }
+                std::vector<uint16_t> un(M * C);
+                const uint32_t mask = packed_bits == 16 ? 0xffffu : ((1u << packed_bits) - 1u);
+                for (size_t r = 0; r < M; r++) {
+                    const uint8_t* src = disk.data() + r * disk_row;
+                    size_t bit = 0;
+                    for (size_t c = 0; c < C; c++, bit += packed_bits) {
+                        const size_t by = bit >> 3;
+                        const int bo = (int)(bit & 7);
+                        uint32_t wd = (uint32_t)src[by] | ((uint32_t)src[by + 1] << 8);
+                        if (bo + packed_bits > 16) wd |= (uint32_t)src[by + 2] << 16;
+                        un[r * C + c] = (uint16_t)((wd >> bo) & mask);
+                    }
+                }
+                void* d;
+                if ((rc = salloc(s, &d, un.size() * 2)) != IBH_OK) return rc;
+                IBH_HIP(hipMemcpy(d, un.data(), un.size() * 2, hipMemcpyHostToDevice), "ibh_v5_open: upload");
+                (side ? t.indices_l2_r : t.indices_l2_l) = (const uint8_t*)d;
+            }
+        } else {
+            IBH_BLK("indices_l2_l", indices_l2_l, const uint8_t*, M * l2_row);
+            IBH_BLK("indices_l2_r", indices_l2_r, const uint8_t*, M * l2_row);
+        }
+    }
+    if (t.n_outlier > 0) {
+        IBH_BLK("outlier_cols", outlier_cols, const int32_t*, (size_t)t.n_outlier * 4);
+        IBH_BLK("outlier_sidecar", outlier_sidecar, const int8_t*, M * t.n_outlier);
+        IBH_BLK("outlier_scale", outlier_scale, const uint16_t*, (size_t)t.n_outlier * 2);
+        // inner columns: the non-outlier columns in increasing order
+        std::vector<int32_t> oc(t.n_outlier);
+        const size_t off = jsize(tm.get("outlier_cols"), "offset", 0);
+        if (!pread_all(fd, oc.data(), oc.size() * 4, wds + off)) {
+            ibh_set_error("ibh_v5_open: cannot read the outlier columns of %s", name.c_str());
+            return IBH_ERROR_LOAD;
+        }
+        std::vector<uint8_t> is_out(t.N, 0);
+        for (int c : oc) {
+            if (c < 0 || c >= t.N || is_out[c]) {
+                ibh_set_error("ibh_v5_open: tensor %s: bad outlier column %d", name.c_str(), c);
+                return IBH_ERROR_FORMAT;
+            }
+            is_out[c] = 1;
+        }
+        std::vector<int32_t> inner;
+        for (int j = 0; j < t.N; j++)
+            if (!is_out[j]) inner.push_back(j);
+        void* d;
+        if ((rc = salloc(s, &d, inner.size() * 4)) != IBH_OK) return rc;
+        IBH_HIP(hipMemcpy(d, inner.data(), inner.size() * 4, hipMemcpyHostToDevice), "ibh_v5_open: upload");
+        t.inner_cols = (const int32_t*)d;
+    }
+#undef IBH_BLK
+    m->kind = MAT_PQ;
+    m->M = t.M;
+    m->N = t.N;
+    return IBH_OK;
+}
+
+int cfg_int(const JVal* cfg, const char* k, int def) { return jint(cfg, k, def); }
+
+int open_session(ibh_v5_session* s, const char* path) {
+    const int fd = open(path, O_RDONLY);
+    if (fd < 0) {
+        ibh_set_error("ibh_v5_open: cannot open %s", path);
+        return IBH_ERROR_LOAD;
+    }
+    struct Closer { int fd; ~Closer() { close(fd); } } closer{fd};
+    struct stat sb;
+    if (fstat(fd, &sb) != 0 || sb.st_size < 32) {
+        ibh_set_error("ibh_v5_open: %s is too small to be IBF", path);
+        return IBH_ERROR_FORMAT;
+    }
+    const size_t fsize = (size_t)sb.st_size;
+    uint8_t pre[32];
+    if (!pread_all(fd, pre, 32, 0) || memcmp(pre, "INFERBIT", 8) != 0) {
+        ibh_set_error("ibh_v5_open: invalid IBF magic");
+        return IBH_ERROR_FORMAT;
+    }
+    uint32_t version, reserve;
+    memcpy(&version, pre + 8, 4);
+    memcpy(&reserve, pre + 12, 4);
+    if (version != 5 || 32 + (size_t)reserve > fsize) {
+        ibh_set_error("ibh_v5_open: not an IBF v5 file (version %u)", version);
+        return IBH_ERROR_FORMAT;
+    }
+    std::string js(reserve, '\0');
+    if (!pread_all(fd, &js[0], reserve, 32)) {
+        ibh_set_error("ibh_v5_open: cannot read the JSON header");
+        return IBH_ERROR_LOAD;
+    }
+    js.resize(strnlen(js.data(), js.size()));
+    JParser jp{js.data(), js.data() + js.size()};
+    const JVal root = jp.value(0);
+    if (!jp.ok || root.kind != JVal::OBJ) {
+        ibh_set_error("ibh_v5_open: failed to parse the JSON header");
+        return IBH_ERROR_FORMAT;
+    }
+    const size_t wds = jsize(&root, "weight_data_start", 0);
+    const JVal* tensors = root.get("tensors");
+    if (!wds || wds > fsize || !tensors || tensors->kind != JVal::OBJ) {
+        ibh_set_error("ibh_v5_open: header lacks weight_data_start or tensors");
+        return IBH_ERROR_FORMAT;
+    }
+    const JVal* cfg = root.get("config");
+    s->n_layers = cfg_int(cfg, "num_layers", 0);
+    s->hidden = cfg_int(cfg, "hidden_size", 0);
+    s->n_heads = cfg_int(cfg, "num_heads", 0);
+    s->n_kv = cfg_int(cfg, "num_kv_heads", s->n_heads);
+    s->head_dim = cfg_int(cfg, "head_dim", s->n_heads > 0 ? s->hidden / s->n_heads : 0);
+    s->inter = cfg_int(cfg, "intermediate_size", 0);
+    s->vocab = cfg_int(cfg, "vocab_size", 0);
+    s->eps = (float)jdbl(cfg, "rms_norm_eps", 1e-5);
+    s->theta = (float)jdbl(cfg, "rope_theta", 10000.0);
+    s->kv_dim = s->n_kv * s->head_dim;
+    if (s->n_layers <= 0 || s->hidden <= 0 || s->hidden > kNormThreads * kNormMaxPer || s->n_heads <= 0 ||
+        s->n_kv <= 0 || s->n_heads % s->n_kv || s->head_dim <= 0 || s->head_dim % 2 || s->head_dim > 256 ||
+        s->n_heads * s->head_dim != s->hidden || s->inter <= 0 || s->vocab <= 0) {
+        ibh_set_error("ibh_v5_open: unsupported config (layers %d hidden %d heads %d/%d head_dim %d inter %d "
+                      "vocab %d)", s->n_layers, s->hidden, s->n_heads, s->n_kv, s->head_dim, s->inter, s->vocab);
+        return IBH_ERROR_FORMAT;
+    }
+    s->act_sparse_rel = 0.f;
+    if (const char* e = getenv("IB_ACT_SPARSE_REL")) s->act_sparse_rel = (float)atof(e);
+
+    // the data region, streamed to HBM in 64 MiB pieces
+    s->arena_bytes = fsize - wds;
+    int rc;
+    if ((rc = salloc(s, (void**)&s->arena, s->arena_bytes)) != IBH_OK) return rc;
+    {
+        const size_t piece = 64u << 20;
+        std::vector<uint8_t> buf(std::min(piece, s->arena_bytes ? s->arena_bytes : 1));
+        for (size_t o = 0; o < s->arena_bytes; o += piece) {
+            const size_t n = std::min(piece, s->arena_bytes - o);
+            if (!pread_all(fd, buf.data(), n, wds + o)) {
+                ibh_set_error("ibh_v5_open: cannot read the weight region");
+                return IBH_ERROR_LOAD;
+            }
+            IBH_HIP(hipMemcpy(s->arena + o, buf.data(), n, hipMemcpyHostToDevice), "ibh_v5_open: upload");
+        }
+    }
+    // raw tensors (src/pq_decode.c:786-829)
+    if (const JVal* raws = root.get("raw_tensors")) {
+        if (raws->kind != JVal::OBJ) {
+            ibh_set_error("ibh_v5_open: raw_tensors is not an object");
+            return IBH_ERROR_FORMAT;
+        }
+        static const char* kTypes[] = {"float32", "float16", "int32", "int16", "int8", "uint8", "uint16"};
+        for (auto& kv : raws->obj) {
+            RawT r;
+            r.name = kv.first;
+            const JVal* dt = kv.second.get("dtype");
+            const std::string d = dt && dt->kind == JVal::STR ? dt->str : "float32";
+            r.dtype = -1;
+            for (int i = 0; i < 7; i++)
+                if (d == kTypes[i]) r.dtype = i;
+            const JVal* sh = kv.second.get("shape");
+            const JVal* o = kv.second.get("offset");
+            const JVal* z = kv.second.get("size");
+            if (r.dtype < 0 || !o || o->kind != JVal::NUM || !z || z->kind != JVal::NUM) {
+                ibh_set_error("ibh_v5_open: raw tensor %s: bad dtype, offset or size", r.name.c_str());
+                return IBH_ERROR_FORMAT;
+            }
+            if (sh && sh->kind == JVal::ARR) {
+                r.ndim = (int)std::min<size_t>(sh->arr.size(), 4);
+                for (int i = 0; i < r.ndim; i++) r.shape[i] = (int)sh->arr[i].num;
+            }
+            r.off = (size_t)o->num;
+            r.size = (size_t)z->num;
+            size_t want = raw_elem(r.dtype);
+            for (int i = 0; i < r.ndim; i++) want *= (size_t)std::max(r.shape[i], 0);
+            if (r.off > s->arena_bytes || r.size > s->arena_bytes - r.off || r.size < want) {
+                ibh_set_error("ibh_v5_open: raw tensor %s lies outside the file or is short", r.name.c_str());
+                return IBH_ERROR_FORMAT;
+            }
+            r.d = s->arena + r.off;
+            s->raws.push_back(r);
+        }
+    }
+    // PQ tensors (+ __act_scale), fp16w and INT4 raw matrices
+    for (auto& kv : tensors->obj) {
+        Mat m;
+        m.name = kv.first;
+        if ((rc = load_pq(s, fd, wds, kv.first, kv.second, &m)) != IBH_OK) return rc;
+        if (const RawT* a = raw_find(s, kv.first + "__act_scale"))
+            if (a->dtype == RAW_F32 && a->ndim == 1 && a->shape[0] == m.N) m.act_inv = (const float*)a->d;
+        s->mats.push_back(m);
+    }
+    for (auto& r : s->raws) {
+        std::string base;
+        if (ends_with(r.name, "__fp16w", &base) && r.dtype == RAW_F16 && r.ndim == 2) {
+            Mat m;
+            m.name = base;
+            m.kind = MAT_F16;
+            m.M = r.shape[0];
+            m.N = r.shape[1];
+            m.w16 = (const uint16_t*)r.d;
+            s->mats.push_back(m);
+        } else if (ends_with(r.name, "__i4_q", &base) && r.dtype == RAW_U8 && r.ndim == 2) {
+            const RawT* rs = raw_find(s, base + "__i4_s");
+            if (!rs || rs->dtype != RAW_F16 || rs->ndim != 2) continue;
+            const int M = r.shape[0], N = r.shape[1] * 2, ng = rs->shape[1];
+            if (ng <= 0 || N % ng || rs->shape[0] != M) continue;
+            Mat m;
+            m.name = base;
+            m.kind = MAT_INT4;
+            m.M = M;
+            m.N = N;
+            ibh_int4g_tensor& t = m.i4;
+            t.q = (const uint8_t*)r.d;
+            t.s = (const uint16_t*)rs->d;
+            t.M = M;
+            t.N = N;
+            t.G = N / ng;
+            if (const RawT* a = raw_find(s, base + "__act_scale"))
+                if (a->dtype == RAW_F32 && a->ndim == 1 && a->shape[0] == N) t.inv_act = (const float*)a->d;
+            const RawT* oi = raw_find(s, base + "__i4_outl_idx");
+            const RawT* ov = raw_find(s, base + "__i4_outl_val");
+            if (oi && ov && oi->dtype == RAW_U16 && ov->dtype == RAW_F16 && oi->ndim == 2 && ov->ndim == 2 &&
+                oi->shape[0] == M && ov->shape[0] == M && oi->shape[1] == ov->shape[1]) {
+                t.outl_idx = (const uint16_t*)oi->d;
+                t.outl_val = (const uint16_t*)ov->d;
+                t.K_out = oi->shape[1];
+            }
+            s->mats.push_back(m);
+        }
+    }
+    // ib_pq_session_open sizes its x_scratch to the widest PQ tensor, or,
+    // with no PQ tensor, to the widest fp16 / INT4 one (4142-4159, 4277-4280),
+    // and the INT4 branch applies __act_scale only when N fits that buffer
+    // (4445-4448): a wider INT4 tensor runs on the unscaled x.
+    {
+        int xs_pq = 0, xs_all = 0;
+        for (auto& m : s->mats) {
+            if (m.kind == MAT_PQ) xs_pq = std::max(xs_pq, m.N);
+            xs_all = std::max(xs_all, m.N);
+        }
+        const int xs_n = xs_pq > 0 ? xs_pq : xs_all;
+        for (auto& m : s->mats)
+            if (m.kind == MAT_INT4 && m.N > xs_n) m.i4.inv_act = nullptr;
+    }
+    if (const JVal* c = root.get("config")) {
+        (void)c;
+        const size_t a = js.find("\"config\"");
+        s->config_json = a == std::string::npos ? "" : js.substr(a);
+    }
+
+    // the decoder's tensors, checked once
+    const int H = s->hidden, KV = s->kv_dim, I = s->inter;
+    s->fused_qkv = mat_find(s, "L0_qkv_proj") >= 0;
+    s->fused_gu = mat_find(s, "L0_gateup_proj") >= 0;
+    auto need = [&](const std::string& n, int M, int N, int* out) -> int {
+        const int i = mat_find(s, n);
+        if (i < 0 || s->mats[i].M != M || s->mats[i].N != N) {
+            ibh_set_error("ibh_v5_open: tensor %s missing or not [%d, %d]", n.c_str(), M, N);
+            return IBH_ERROR_FORMAT;
+        }
+        *out = i;
+        return IBH_OK;
+    };
+    auto norm = [&](const std::string& n, const float** out) -> int {
+        const RawT* r = raw_find(s, n);
+        if (!r || r->dtype != RAW_F32 || r->ndim != 1 || r->shape[0] != H) {
+            ibh_set_error("ibh_v5_open: norm weight %s missing or not fp32 [%d]", n.c_str(), H);
+            return IBH_ERROR_FORMAT;
+        }
+        *out = (const float*)r->d;
+        return IBH_OK;
+    };
+    const int L = s->n_layers;
+    s->w_in.resize(L);
+    s->w_pn.resize(L);
+    for (auto* v : {&s->mq, &s->mk, &s->mv, &s->mo, &s->mg, &s->mu, &s->md, &s->mqkv, &s->mgu}) v->assign(L, -1);
+    for (int l = 0; l < L; l++) {
+        const std::string p = "L" + std::to_string(l) + "_";
+        if ((rc = norm(p + "input_norm", &s->w_in[l])) || (rc = norm(p + "post_attn_norm", &s->w_pn[l]))) return rc;
+        if (s->fused_qkv) {
+            if ((rc = need(p + "qkv_proj", H + 2 * KV, H, &s->mqkv[l]))) return rc;
+        } else if ((rc = need(p + "q_proj", H, H, &s->mq[l])) || (rc = need(p + "k_proj", KV, H, &s->mk[l])) ||
+                   (rc = need(p + "v_proj", KV, H, &s->mv[l]))) {
+            return rc;
+        }
+        if ((rc = need(p + "o_proj", H, H, &s->mo[l]))) return rc;
+        if (s->fused_gu) {
+            if ((rc = need(p + "gateup_proj", 2 * I, H, &s->mgu[l]))) return rc;
+        } else if ((rc = need(p + "gate_proj", I, H, &s->mg[l])) || (rc = need(p + "up_proj", I, H, &s->mu[l]))) {
+            return rc;
+        }
+        if ((rc = need(p + "down_proj", H, I, &s->md[l]))) return rc;
+    }
+    if ((rc = norm("final_norm", &s->w_final))) return rc;
+    if ((rc = need("lm_head", s->vocab, H, &s->m_head))) return rc;
+    // embedding: PQ tok_embed first, else raw fp16 / fp32 (embed_lookup 4854-4876)
+    int ei = -1;
+    for (size_t i = 0; i < s->mats.size(); i++)
+        if (s->mats[i].kind == MAT_PQ && s->mats[i].name == "tok_embed") ei = (int)i;
+    if (ei >= 0) {
+        if (s->mats[ei].N != H) {
+            ibh_set_error("ibh_v5_open: tok_embed has %d columns, hidden is %d", s->mats[ei].N, H);
+            return IBH_ERROR_FORMAT;
+        }
+        s->embed_kind = 2;
+        s->embed_mat = ei;
+    } else {
+        const RawT* r = raw_find(s, "tok_embed");
+        if (!r || r->ndim != 2 || r->shape[1] != H || (r->dtype != RAW_F16 && r->dtype != RAW_F32)) {
+            ibh_set_error("ibh_v5_open: tok_embed missing or not fp16/fp32 [vocab, %d]", H);
+            return IBH_ERROR_FORMAT;
+        }
+        s->embed_kind = r->dtype == RAW_F16 ? 1 : 0;
+        s->embed = r->d;
+    }
+
+    // activations and one shared workspace (every launch is on one stream)
+    const int maxN = std::max(std::max(H, I), H + 2 * KV);
+    float** bufs[] = {&s->x, &s->xb, &s->xb2, &s->q, &s->kn, &s->vn, &s->delta};
+    for (float** b : bufs)
+        if ((rc = salloc(s, (void**)b, (size_t)H * 4 + 256))) return rc;
+    if ((rc = salloc(s, (void**)&s->qkv, (size_t)(H + 2 * KV) * 4)) || (rc = salloc(s, (void**)&s->gate, (size_t)I * 4)) ||
+        (rc = salloc(s, (void**)&s->up, (size_t)I * 4)) || (rc = salloc(s, (void**)&s->gu, (size_t)2 * I * 4)) ||
+        (rc = salloc(s, (void**)&s->xs, (size_t)maxN * 4)) ||
+        (rc = salloc(s, (void**)&s->logits, (size_t)s->vocab * 4)) ||
+        (rc = salloc(s, (void**)&s->top_val, 1024 * 4)) || (rc = salloc(s, (void**)&s->top_ids, 1024 * 4)))
+        return rc;
+    size_t ws = 0;
+    for (auto& m : s->mats) {
+        if (m.kind == MAT_PQ) ws = std::max(ws, ibh_pq_workspace_bytes(&m.pq));
+        if (m.kind == MAT_INT4) ws = std::max(ws, ibh_int4g_workspace_bytes(&m.i4));
+    }
+    if (s->mats[s->m_head].kind == MAT_PQ) ws = std::max(ws, ibh_pq_topk_workspace_bytes(&s->mats[s->m_head].pq, 8));
+    s->ws_bytes = ws;
+    if ((rc = salloc(s, &s->ws, ws))) return rc;
+    IBH_HIP(hipStreamCreateWithFlags(&s->st, hipStreamNonBlocking), "ibh_v5_open: stream");
+    return IBH_OK;
+}
+
+int matmul(ibh_v5_session* s, int mi, const float* x, float* out) {
+    Mat& m = s->mats[mi];
+    if (m.kind == MAT_F16) {
+        v5_f16_matvec<<<(m.M + 3) / 4, 256, 0, s->st>>>(out, m.w16, x, m.M, m.N);
+        IBH_CHECK_LAUNCH("ibh_v5: fp16 matvec");
+        return IBH_OK;
+    }
+    if (m.kind == MAT_INT4) return ibh_int4g_matmul(&m.i4, x, out, s->act_sparse_rel, s->ws, s->ws_bytes, s->st);
+    const float* xk = x;
+    if (m.act_inv) {
+        v5_scale_kernel<<<(m.N + 255) / 256, 256, 0, s->st>>>(s->xs, x, m.act_inv, m.N);
+        IBH_CHECK_LAUNCH("ibh_v5: act scale");
+        xk = s->xs;
+    }
+    const ibh_pq_policy& p = m.has_policy ? m.policy : s->default_policy;
+    return ibh_pq_matmul_policy(&m.pq, xk, out, &p, s->ws, s->ws_bytes, s->st);
+}
+
+// forward_step_internal_sc: x ends as the post-final-norm hidden state in
+// s->xb; logits (device) when want_logits.
+int forward(ibh_v5_session* s, ibh_v5_kv* kv, int token, int pos, bool want_logits) {
+    const int H = s->hidden, KV = s->kv_dim, I = s->inter, hd = s->head_dim;
+    if (token < 0 || token >= (s->embed_kind == 2 ? s->mats[s->embed_mat].M : s->vocab) || pos < 0 ||
+        pos >= kv->max_seq) {
+        ibh_set_error("ibh_v5_forward_step: token %d or position %d out of range", token, pos);
+        return IBH_ERROR_PARAM;
+    }
+    if (s->embed_kind == 2) {
+        const ibh_pq_tensor& t = s->mats[s->embed_mat].pq;
+        const int n = t.C * t.G + t.n_outlier;
+        pq_row_kernel<<<(n + 255) / 256, 256, 0, s->st>>>(s->x, t, token);
+    } else {
+        embed_raw_kernel<<<(H + 255) / 256, 256, 0, s->st>>>(s->x, s->embed, s->embed_kind, token, H);
+    }
+    IBH_CHECK_LAUNCH("ibh_v5: embedding");
+    int rc;
+    const float* pending = nullptr;   // residual not yet added into x
+    for (int l = 0; l < s->n_layers; l++) {
+        v5_rmsnorm_kernel<<<1, kNormThreads, 0, s->st>>>(s->xb, s->x, pending, s->w_in[l], s->eps, H);
+        IBH_CHECK_LAUNCH("ibh_v5: rmsnorm");
+        float *q = s->q, *k = s->kn, *v = s->vn;
+        if (s->fused_qkv) {
+            if ((rc = matmul(s, s->mqkv[l], s->xb, s->qkv))) return rc;
+            q = s->qkv;
+            k = s->qkv + H;
+            v = s->qkv + H + KV;
+        } else if ((rc = matmul(s, s->mq[l], s->xb, q)) || (rc = matmul(s, s->mk[l], s->xb, k)) ||
+                   (rc = matmul(s, s->mv[l], s->xb, v))) {
+            return rc;
+        }
+        const size_t lbase = (size_t)l * kv->max_seq * KV;
+        v5_rope_kv_kernel<<<s->n_heads + 2 * s->n_kv, 64, 0, s->st>>>(
+            q, k, v, kv->k + lbase + (size_t)pos * KV, kv->v + lbase + (size_t)pos * KV,
+            kv->rope + (size_t)pos * hd, s->n_heads, s->n_kv, hd);
+        IBH_CHECK_LAUNCH("ibh_v5: rope + kv write");
+        if ((rc = ibh_launch_attn(s->xb2, q, kv->k + lbase, kv->v + lbase, nullptr, nullptr, pos, nullptr, pos,
+                                  s->n_heads, s->n_kv, hd, 32, kv->aws, kv->aws_bytes, s->st)))
+            return rc;
+        if ((rc = matmul(s, s->mo[l], s->xb2, s->delta))) return rc;
+        v5_rmsnorm_kernel<<<1, kNormThreads, 0, s->st>>>(s->xb, s->x, s->delta, s->w_pn[l], s->eps, H);
+        IBH_CHECK_LAUNCH("ibh_v5: rmsnorm");
+        float *g = s->gate, *u = s->up;
+        if (s->fused_gu) {
+            if ((rc = matmul(s, s->mgu[l], s->xb, s->gu))) return rc;
+            g = s->gu;
+            u = s->gu + I;
+        } else if ((rc = matmul(s, s->mg[l], s->xb, g)) || (rc = matmul(s, s->mu[l], s->xb, u))) {
+            return rc;
+        }
+        v5_silu_kernel<<<(I + 255) / 256, 256, 0, s->st>>>(s->gate, g, u, I);
+        IBH_CHECK_LAUNCH("ibh_v5: silu");
+        if ((rc = matmul(s, s->md[l], s->gate, s->delta))) return rc;
+        pending = s->delta;
+    }
+    v5_rmsnorm_kernel<<<1, kNormThreads, 0, s->st>>>(s->xb, s->x, pending, s->w_final, s->eps, H);
+    IBH_CHECK_LAUNCH("ibh_v5: final rmsnorm");
+    if (want_logits && (rc = matmul(s, s->m_head, s->xb, s->logits))) return rc;
+    kv->length = pos + 1;
+    return IBH_OK;
+}
+
+}  // namespace
+
+extern "C" int ibh_v5_open(const char* path, ibh_v5_session** out) {
+    if (!path || !out) {
+        ibh_set_error("ibh_v5_open: null argument");
+        return IBH_ERROR_PARAM;
+    }
+    *out = nullptr;
+    ibh_v5_session* s = new ibh_v5_session();
+    const int rc = open_session(s, path);
+    if (rc != IBH_OK) {
+        free_session(s);
+        return rc;
+    }
+    *out = s;
+    return IBH_OK;
+}
+
+extern "C" void ibh_v5_close(ibh_v5_session* s) { free_session(s); }
+
+extern "C" int ibh_v5_dims(const ibh_v5_session* s, int* dims) {
+    if (!s || !dims) return IBH_ERROR_PARAM;
+    const int d[9] = {s->n_layers, s->hidden, s->n_heads, s->n_kv, s->head_dim, s->inter, s->vocab,
+                      s->fused_qkv ? 1 : 0, s->fused_gu ? 1 : 0};
+    memcpy(dims, d, sizeof(d));
+    return IBH_OK;
+}
+
+extern "C" int ibh_v5_tensor_info(const ibh_v5_session* s, const char* name, int* kind, int* M, int* N) {
+    if (!s || !name) return IBH_ERROR_PARAM;
+    const int i = mat_find(s, name);
+    if (i < 0) return IBH_ERROR_PARAM;
+    if (kind) *kind = s->mats[i].kind;
+    if (M) *M = s->mats[i].M;
+    if (N) *N = s->mats[i].N;
+    return IBH_OK;
+}
+
+extern "C" int ibh_v5_set_default_policy(ibh_v5_session* s, const ibh_pq_policy* p) {
+    if (!s || !p) {
+        ibh_set_error("ibh_v5_set_default_policy: null argument");
+        return IBH_ERROR_PARAM;
+    }
+    s->default_policy = *p;
+    return IBH_OK;
+}
+
+extern "C" int ibh_v5_set_policy(ibh_v5_session* s, const char* name, const ibh_pq_policy* p) {
+    if (!s || !name || !p) {
+        ibh_set_error("ibh_v5_set_policy: null argument");
+        return IBH_ERROR_PARAM;
+    }
+    bool found = false;
+    for (auto& m : s->mats)   // session_find_index: PQ tensors only
+        if (m.kind == MAT_PQ && m.name == name) {
+            m.policy = *p;
+            m.has_policy = true;
+            found = true;
+        }
+    if (!found) {
+        ibh_set_error("ibh_v5_set_policy: no PQ tensor %s", name);
+        return IBH_ERROR_PARAM;
+    }
+    return IBH_OK;
+}
+
+extern "C" int ibh_v5_session_matmul(ibh_v5_session* s, const char* name, const float* x, float* out,
+                                     void* stream) {
+    if (!s || !name || !x || !out) {
+        ibh_set_error("ibh_v5_session_matmul: null argument");
+        return IBH_ERROR_PARAM;
+    }
+    const int i = mat_find(s, name);
+    if (i < 0) {
+        ibh_set_error("ibh_v5_session_matmul: no tensor %s", name);
+        return IBH_ERROR_PARAM;
+    }
+    hipStream_t st = ibh_resolve_stream(stream);
+    hipEvent_t ev;
+    IBH_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming), "ibh_v5_session_matmul: event");
+    hipEventRecord(ev, st);
+    hipStreamWaitEvent(s->st, ev, 0);
+    int rc = matmul(s, i, x, out);
+    hipEventRecord(ev, s->st);
+    hipStreamWaitEvent(st, ev, 0);
+    hipEventDestroy(ev);
+    return rc;
+}
+
+extern "C" int ibh_v5_kv_create(ibh_v5_session* s, int max_seq, ibh_v5_kv** out) {
+    if (!s || !out || max_seq <= 0) {
+        ibh_set_error("ibh_v5_kv_create: invalid arguments");
+        return IBH_ERROR_PARAM;
+    }
+    *out = nullptr;
+    ibh_v5_kv* kv = new ibh_v5_kv();
+    kv->s = s;
+    kv->max_seq = max_seq;
+    const size_t n = (size_t)s->n_layers * max_seq * s->kv_dim;
+    const int half = s->head_dim / 2;
+    kv->aws_bytes = ibh_attn_workspace_bytes(s->n_heads, s->head_dim, max_seq);
+    bool ok = hipMalloc((void**)&kv->k, n * 4) == hipSuccess && hipMalloc((void**)&kv->v, n * 4) == hipSuccess &&
+              hipMalloc((void**)&kv->rope, (size_t)max_seq * half * 8) == hipSuccess &&
+              hipMalloc(&kv->aws, kv->aws_bytes) == hipSuccess;
+    if (ok) {
+        // ib_rope_f32's angles (src/pq_decode.c:4631-4634), host libm
+        std::vector<float> tab((size_t)max_seq * half * 2);
+        for (int p = 0; p < max_seq; p++)
+            for (int i = 0; i < half; i++) {
+                const float freq = powf(s->theta, -2.0f * (float)i / (float)s->head_dim);
+                const float ang = (float)p * freq;
+                tab[((size_t)p * half + i) * 2] = cosf(ang);
+                tab[((size_t)p * half + i) * 2 + 1] = sinf(ang);
+            }
+        ok = hipMemcpy(kv->rope, tab.data(), tab.size() * 4, hipMemcpyHostToDevice) == hipSuccess;
+    }
+    if (!ok) {
+        hipFree(kv->k);
+        hipFree(kv->v);
+        hipFree(kv->rope);
+        hipFree(kv->aws);
+        delete kv;
+        ibh_set_error("ibh_v5_kv_create: device allocation failed (%d positions)", max_seq);
+        return IBH_ERROR_MEMORY;
+    }
+    *out = kv;
+    return IBH_OK;
+}
+
+extern "C" void ibh_v5_kv_free(ibh_v5_kv* kv) {
+    if (!kv) return;
+    if (kv->s && kv->s->st) hipStreamSynchronize(kv->s->st);
+    hipFree(kv->k);
+    hipFree(kv->v);
+    hipFree(kv->rope);
+    hipFree(kv->aws);
+    delete kv;
+}
+
+extern "C" void ibh_v5_kv_clear(ibh_v5_kv* kv) {
+    if (kv) kv->length = 0;
+}
+
+extern "C" int ibh_v5_kv_length(const ibh_v5_kv* kv) { return kv ? kv->length : 0; }
+
+extern "C" int ibh_v5_forward_step(ibh_v5_session* s, ibh_v5_kv* kv, int token, int pos, float* logits) {
+    if (!s || !kv || kv->s != s) {
+        ibh_set_error("ibh_v5_forward_step: invalid session or cache");
+        return IBH_ERROR_PARAM;
+    }
+    int rc = forward(s, kv, token, pos, logits != nullptr);
+    if (rc == IBH_OK && logits)
+        IBH_HIP(hipMemcpyAsync(logits, s->logits, (size_t)s->vocab * 4, hipMemcpyDeviceToHost, s->st),
+                "ibh_v5_forward_step: logits");
+    IBH_HIP(hipStreamSynchronize(s->st), "ibh_v5_forward_step");
+    return rc;
+}
+
+extern "C" int ibh_v5_forward_step_to_hidden(ibh_v5_session* s, ibh_v5_kv* kv, int token, int pos, float* hidden) {
+    if (!s || !kv || kv->s != s) {
+        ibh_set_error("ibh_v5_forward_step_to_hidden: invalid session or cache");
+        return IBH_ERROR_PARAM;
+    }
+    int rc = forward(s, kv, token, pos, false);
+    if (rc == IBH_OK && hidden)
+        IBH_HIP(hipMemcpyAsync(hidden, s->xb, (size_t)s->hidden * 4, hipMemcpyDeviceToHost, s->st),
+                "ibh_v5_forward_step_to_hidden: copy");
+    IBH_HIP(hipStreamSynchronize(s->st), "ibh_v5_forward_step_to_hidden");
+    return rc;
+}
+
+// ib_pq_generate_greedy: prompt through the cache (the reference's batched
+// prefill equals sequential steps), then per token the top-8 PQ head
+// (top_ids[0] is the refined best), stop on eos or a full cache.
+extern "C" int ibh_v5_generate_greedy(ibh_v5_session* s, ibh_v5_kv* kv, const int* prompt, int n_prompt,
+                                      int max_new, int eos, int* out_ids, int* n_out) {
+    if (!s || !kv || kv->s != s || !prompt || n_prompt <= 0 || max_new < 0 || !out_ids || !n_out) {
+        ibh_set_error("ibh_v5_generate_greedy: invalid arguments");
+        return IBH_ERROR_PARAM;
+    }
+    *n_out = 0;
+    const Mat& head = s->mats[s->m_head];
+    if (head.kind != MAT_PQ) {
+        ibh_set_error("ibh_v5_generate_greedy: lm_head must be a PQ tensor");
+        return IBH_ERROR_FORMAT;
+    }
+    if (n_prompt > kv->max_seq) {
+        ibh_set_error("ibh_v5_generate_greedy: prompt of %d tokens exceeds the cache (%d)", n_prompt, kv->max_seq);
+        return IBH_ERROR_CONTEXT;
+    }
+    int rc;
+    for (int i = 0; i < n_prompt; i++)
+        if ((rc = forward(s, kv, prompt[i], i, false))) return rc;
+    int pos = n_prompt, written = 0;
+    for (int g = 0; g < max_new; g++) {
+        if ((rc = ibh_pq_lm_head_topk(&head.pq, s->xb, 8, s->top_val, s->top_ids, s->ws, s->ws_bytes, s->st)))
+            return rc;
+        int32_t best = 0;
+        IBH_HIP(hipMemcpyAsync(&best, s->top_ids, 4, hipMemcpyDeviceToHost, s->st), "ibh_v5_generate_greedy: id");
+        IBH_HIP(hipStreamSynchronize(s->st), "ibh_v5_generate_greedy");
+        out_ids[written++] = best;
+        *n_out = written;
+        if (eos >= 0 && best == eos) break;
+        if (pos >= kv->max_seq) break;
+        if ((rc = forward(s, kv, best, pos, false))) return rc;
+        pos++;
+    }
+    IBH_HIP(hipStreamSynchronize(s->st), "ibh_v5_generate_greedy");
+    return IBH_OK;
+}

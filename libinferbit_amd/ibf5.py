@@ -89,10 +89,13 @@ class V5Writer:
                 f.write(b)
 
 
-def _pq(rng, M, N, G=16, K=256, levels=1, K2=0, cb_std=0.05):
-    C = N // G
+def _pq(rng, M, N, G=16, K=256, levels=1, K2=0, n_outlier=0, cb_std=0.05):
+    """Random PQ tensor dict (the oracle's field names).  K2 == 16 packs the
+    level-2 indices two per byte, low nibble first (pq_l2_idx_at)."""
+    C = (N - n_outlier) // G
+    assert C * G == N - n_outlier
     h = G // 2
-    t = dict(M=M, N=N, G=G, K=K, n_levels=levels, n_outlier=0, C=C, K_l2=K2 if levels == 2 else 0)
+    t = dict(M=M, N=N, G=G, K=K, n_levels=levels, n_outlier=n_outlier, C=C, K_l2=K2 if levels == 2 else 0)
     t["cb1l"] = _f16(rng.standard_normal((K, h)) * cb_std)
     t["cb1r"] = _f16(rng.standard_normal((K, h)) * cb_std)
     t["i1l"] = rng.integers(0, K, (M, C), dtype=np.uint8)
@@ -101,20 +104,33 @@ def _pq(rng, M, N, G=16, K=256, levels=1, K2=0, cb_std=0.05):
     if levels == 2:
         t["cb2l"] = _f16(rng.standard_normal((K2, h)) * cb_std * 0.25)
         t["cb2r"] = _f16(rng.standard_normal((K2, h)) * cb_std * 0.25)
-        t["i2l"] = rng.integers(0, K2, (M, C), dtype=np.uint8)
-        t["i2r"] = rng.integers(0, K2, (M, C), dtype=np.uint8)
+        for k in ("i2l", "i2r"):
+            i2 = rng.integers(0, K2, (M, C), dtype=np.uint8)
+            if K2 == 16:
+                pad = np.zeros((M, C + (C & 1)), np.uint8)
+                pad[:, :C] = i2
+                i2 = (pad[:, 0::2] | (pad[:, 1::2] << 4)).astype(np.uint8)
+            t[k] = i2
+    if n_outlier:
+        t["ocols"] = np.sort(rng.choice(N, n_outlier, replace=False)).astype(np.int32)
+        t["oside"] = rng.integers(-127, 128, (M, n_outlier), dtype=np.int8)
+        t["oscale"] = _f16(rng.uniform(0.5, 1.5, n_outlier) * cb_std / 64)
     return t
 
 
 def write_synthetic_v5(path: str, cfg: dict, seed: int = 0, backend=None, awq: bool = False, outliers: int = 0,
-                       head: str = "pq", levels: int = 1):
+                       head: str = "pq", levels: int = 1, k2: int = 256, pq_outliers: int = 0,
+                       pq_act_scale: bool = False, fused: bool = False, embed: str = "f16"):
     """A random decoder in IBF v5.  cfg: num_layers, hidden_size, num_heads,
     num_kv_heads, head_dim, intermediate_size, vocab_size (+ rms_norm_eps,
     rope_theta).  backend maps projection names (q_proj, k_proj, v_proj,
     o_proj, gate_proj, up_proj, down_proj) to "int4g" (group 128 scales,
     optional AWQ inv_act and fp16 outliers), "pq" or "fp16"; default int4g.
     The LM head is a PQ tensor ("pq", the greedy path's top-K head needs
-    one) or int4g / fp16."""
+    one) or int4g / fp16.  PQ tensors: `levels` 1 or 2 (K_l2 = k2),
+    `pq_outliers` outlier columns, `pq_act_scale` an <name>__act_scale
+    vector.  `fused` writes L{i}_qkv_proj / L{i}_gateup_proj instead of the
+    separate projections; `embed` is "f16", "f32" or "pq"."""
     rng = np.random.default_rng(seed)
     backend = dict(backend or {})
     H, L = cfg["hidden_size"], cfg["num_layers"]
@@ -124,11 +140,18 @@ def write_synthetic_v5(path: str, cfg: dict, seed: int = 0, backend=None, awq: b
     config = dict(num_layers=L, hidden_size=H, num_heads=nh, num_kv_heads=nkv, head_dim=hd, intermediate_size=I,
                   vocab_size=V, rms_norm_eps=cfg.get("rms_norm_eps", 1e-5), rope_theta=cfg.get("rope_theta", 10000.0))
     w = V5Writer(config)
-    w.raw_tensor("tok_embed", _f16(rng.standard_normal((V, H))), "float16")
+    if embed == "pq":
+        w.pq_tensor("tok_embed", _pq(rng, V, H, levels=levels, K2=k2, n_outlier=pq_outliers, cb_std=1.0))
+    elif embed == "f32":
+        w.raw_tensor("tok_embed", rng.standard_normal((V, H)).astype(np.float32), "float32")
+    else:
+        w.raw_tensor("tok_embed", _f16(rng.standard_normal((V, H))), "float16")
 
     def matrix(name, M, N, kind):
         if kind == "pq":
-            w.pq_tensor(name, _pq(rng, M, N, levels=levels, K2=256 if levels == 2 else 0))
+            w.pq_tensor(name, _pq(rng, M, N, levels=levels, K2=k2 if levels == 2 else 0, n_outlier=pq_outliers))
+            if pq_act_scale:
+                w.raw_tensor(name + "__act_scale", np.exp(rng.normal(0, 0.3, N)).astype(np.float32), "float32")
         elif kind == "fp16":
             w.raw_tensor(name + "__fp16w", _f16(rng.standard_normal((M, N)) / np.sqrt(N)), "float16")
         else:
@@ -148,7 +171,12 @@ def write_synthetic_v5(path: str, cfg: dict, seed: int = 0, backend=None, awq: b
         w.raw_tensor(f"L{l}_input_norm", (1 + 0.1 * rng.standard_normal(H)).astype(np.float32), "float32")
         w.raw_tensor(f"L{l}_post_attn_norm", (1 + 0.1 * rng.standard_normal(H)).astype(np.float32), "float32")
         for p, (M, N) in shapes.items():
+            if fused and p in ("q_proj", "k_proj", "v_proj", "gate_proj", "up_proj"):
+                continue
             matrix(f"L{l}_{p}", M, N, backend.get(p, "int4g"))
+        if fused:
+            matrix(f"L{l}_qkv_proj", nh * hd + 2 * nkv * hd, H, backend.get("qkv_proj", "int4g"))
+            matrix(f"L{l}_gateup_proj", 2 * I, H, backend.get("gateup_proj", "int4g"))
     w.raw_tensor("final_norm", (1 + 0.1 * rng.standard_normal(H)).astype(np.float32), "float32")
     matrix("lm_head", V, H, head)
     w.write(path)

@@ -79,3 +79,41 @@ def test_expf_restatement_matches_glibc(oracle_lib):
     ref = oracle_lib.expf(x)
     same = (ours.view(np.uint32) == ref.view(np.uint32)) | (np.isnan(ours) & np.isnan(ref))
     assert same.all(), x[~same][:10]
+
+
+def test_ibf5_writer_layout_and_reference_load(tmp_path):
+    """The IBF v5 writer: preamble, JSON header, 64-byte aligned blocks inside
+    the data region; the reference's own session (oracle/_ref/ref_v5, when
+    built) opens the file and decodes from it."""
+    import os
+    import subprocess
+    from libinferbit_amd import ibf5
+    cfg = dict(num_layers=1, hidden_size=128, num_heads=2, num_kv_heads=1, head_dim=64, intermediate_size=256,
+               vocab_size=300)
+    p = str(tmp_path / "m.ibf")
+    ibf5.write_synthetic_v5(p, cfg, seed=1, backend=dict(gate_proj="pq", o_proj="fp16"), levels=2, k2=16,
+                            pq_outliers=16, fused=False, embed="pq")
+    raw = open(p, "rb").read()
+    assert raw[:8] == b"INFERBIT"
+    version, reserve = np.frombuffer(raw[8:16], np.uint32)
+    assert version == 5
+    hdr = json.loads(raw[32:32 + reserve].decode().rstrip(" \0"))
+    wds = hdr["weight_data_start"]
+    assert wds % 4096 == 0 and hdr["config"]["hidden_size"] == 128
+    assert hdr["tensors"]["L0_gate_proj"]["format"] == "pq2d_v1_l1_l2"
+    assert hdr["tensors"]["L0_gate_proj"]["outlier"]["n_cols"] == 16
+    for t in hdr["tensors"].values():
+        for v in t.values():
+            if isinstance(v, dict) and "offset" in v:
+                assert v["offset"] % 64 == 0 and wds + v["offset"] + v["size"] <= len(raw)
+    for r in hdr["raw_tensors"].values():
+        assert wds + r["offset"] + r["size"] <= len(raw)
+    assert "L0_q_proj__i4_q" in hdr["raw_tensors"] and "L0_o_proj__fp16w" in hdr["raw_tensors"]
+    ref = os.path.join(os.path.dirname(__file__), "..", "oracle", "_ref", "ref_v5")
+    if not os.path.exists(ref):
+        pytest.skip("oracle/_ref/ref_v5 not built")
+    pp = str(tmp_path / "p.i32")
+    np.array([1, 2, 3], np.int32).tofile(pp)
+    r = subprocess.run([ref, p, "16", "4", pp, "greedy"], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    assert len(json.loads(r.stdout)["tokens"]) == 4

@@ -1,0 +1,167 @@
+"""The IBF v5 PQ session on the GPU against the reference's own session
+(oracle/_ref/ref_v5, built from the reference sources, run live on the same
+file): ib_pq_forward_step logits of every prompt position within
+max|d| / max|logit| <= 1e-4, the greedy continuation by argmax of those
+logits identical, and ib_pq_generate_greedy (top-8 PQ head) identical.
+
+Models are small seeded decoders written by libinferbit_amd.ibf5 covering
+each backend of ib_pq_session_matmul (INT4 group scales with and without
+AWQ scales and outliers, fp16 matrices, one- and two-level PQ with
+outlier columns, 4-bit packed level-2 indices, PQ activation scales), fused
+qkv / gateup tensors, fp16 / fp32 / PQ embeddings and the session's PQ
+policies."""
+import json
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+from conftest import ROOT
+
+pytestmark = pytest.mark.gpu
+
+REF_V5 = os.path.join(ROOT, "oracle", "_ref", "ref_v5")
+CFG = dict(num_layers=2, hidden_size=256, num_heads=4, num_kv_heads=2, head_dim=64, intermediate_size=512,
+           vocab_size=1000)
+ALLPQ = {p: "pq" for p in ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")}
+CASES = {
+    "int4": dict(),
+    "int4_awq_outl": dict(awq=True, outliers=3),
+    "mixed": dict(backend=dict(gate_proj="pq", up_proj="pq", down_proj="pq", o_proj="fp16"), awq=True),
+    "pq_l2_actscale_pqembed": dict(backend=ALLPQ, levels=2, pq_act_scale=True, embed="pq"),
+    "pq_outl_k16_f32embed": dict(backend=ALLPQ, levels=2, k2=16, pq_outliers=16, embed="f32"),
+    "fused": dict(fused=True, backend=dict(qkv_proj="pq", gateup_proj="int4g")),
+}
+PROMPT = [5, 17, 300, 42, 7]
+N_NEW = 10
+TOL = 1e-4
+
+
+@pytest.fixture(scope="module")
+def L():
+    import libinferbit_amd as L
+    L.ops.init(0)
+    return L
+
+
+def model(tmp_path_factory, name, cfg=CFG, **over):
+    from libinferbit_amd import ibf5
+    kw = dict(CASES.get(name, {}), **over)
+    p = str(tmp_path_factory.mktemp("v5") / f"{name}.ibf")
+    ibf5.write_synthetic_v5(p, cfg, seed=3, **kw)
+    return p
+
+
+def ref_run(path, prompt, n_new, mode, tmp, policy=None, max_seq=64):
+    if not os.path.exists(REF_V5):
+        pytest.skip("oracle/_ref/ref_v5 not built (make -C oracle ref)")
+    pp, lp = str(tmp / "p.i32"), str(tmp / "lg.f32")
+    np.asarray(prompt, np.int32).tofile(pp)
+    env = dict(os.environ, REF_V5_LOGITS=lp)
+    if policy is not None:
+        env["REF_V5_POLICY"] = ",".join(str(v) for v in policy)
+    r = subprocess.run([REF_V5, path, str(max_seq), str(n_new), pp, mode], capture_output=True, text=True,
+                       timeout=300, env=env)
+    assert r.returncode == 0, r.stderr
+    toks = json.loads(r.stdout.strip().splitlines()[-1])["tokens"]
+    lg = np.fromfile(lp, np.float32).reshape(len(prompt), -1) if mode == "steps" else None
+    return toks, lg
+
+
+def relerr(a, b):
+    return float(np.abs(a.astype(np.float64) - b).max() / np.abs(b).max())
+
+
+def gpu_steps(S, prompt, n_new, max_seq=64):
+    kv = S.kv_cache(max_seq)
+    lg = [S.forward_step(kv, t, i) for i, t in enumerate(prompt)]
+    cur, toks = lg[-1], []
+    for g in range(n_new):
+        best = int(np.argmax(cur))
+        toks.append(best)
+        if g + 1 < n_new:
+            cur = S.forward_step(kv, best, len(prompt) + g)
+    assert len(kv) == len(prompt) + n_new - 1
+    return toks, np.stack(lg)
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_forward_step_and_greedy(L, tmp_path_factory, tmp_path, name):
+    from libinferbit_amd.session import PqSession
+    path = model(tmp_path_factory, name)
+    rt, rl = ref_run(path, PROMPT, N_NEW, "steps", tmp_path)
+    S = PqSession(path)
+    gt, gl = gpu_steps(S, PROMPT, N_NEW)
+    errs = [relerr(gl[i], rl[i]) for i in range(len(PROMPT))]
+    assert max(errs) <= TOL, (name, errs)
+    assert gt == rt, (name, gt, rt)
+    rg, _ = ref_run(path, PROMPT, N_NEW, "greedy", tmp_path)
+    gg = S.generate_greedy(S.kv_cache(64), PROMPT, N_NEW).tolist()
+    assert gg == rg, (name, gg, rg)
+
+
+POLICIES = {
+    "l1_only": (1, 0.0, 0.0),
+    "l2skip": (2, 0.5, 0.0),
+    "sparse": (3, 0.0, 0.3),
+    "int8": (4, 0.0, 0.0),
+}
+
+
+@pytest.mark.parametrize("pol", list(POLICIES))
+def test_policies(L, tmp_path_factory, tmp_path, pol):
+    from libinferbit_amd.session import PqSession
+    path = model(tmp_path_factory, "pq_l2_actscale_pqembed")
+    p = POLICIES[pol]
+    rt, rl = ref_run(path, PROMPT, N_NEW, "steps", tmp_path, policy=p)
+    S = PqSession(path)
+    S.set_default_policy(*p)
+    gt, gl = gpu_steps(S, PROMPT, N_NEW)
+    errs = [relerr(gl[i], rl[i]) for i in range(len(PROMPT))]
+    # skip decisions compare rounded tables: a decision at its threshold may
+    # flip, which moves a logit by one dropped level-2 term
+    tol = TOL if pol in ("l1_only", "int8") else 1e-3
+    assert max(errs) <= tol, (pol, errs)
+    assert gt == rt, (pol, gt, rt)
+
+
+def test_per_tensor_policy_and_matmul(L, tmp_path_factory, tmp_path):
+    """set_policy on one tensor; session matmul of every backend against the
+    session's own step (shapes) and the error paths."""
+    import torch
+    from libinferbit_amd._lib import IbhError
+    from libinferbit_amd.session import PqSession
+    path = model(tmp_path_factory, "mixed")
+    S = PqSession(path)
+    assert S.tensor_info("L0_q_proj") == ("int4", 256, 256)
+    assert S.tensor_info("L0_o_proj") == ("fp16", 256, 256)
+    assert S.tensor_info("L0_down_proj") == ("pq", 256, 512)
+    with pytest.raises(IbhError):
+        S.set_policy("L0_q_proj", 1)       # not a PQ tensor
+    with pytest.raises(IbhError):
+        S.tensor_info("nope")
+    x = torch.randn(512, device="cuda")
+    y = torch.empty(256, device="cuda")
+    S.matmul("L0_down_proj", x, y)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y).all()
+    S.set_policy("L1_gate_proj", 1)
+    rt, _ = ref_run(path, PROMPT, 4, "steps", tmp_path)
+    gt, _ = gpu_steps(S, PROMPT, 4)
+    assert len(gt) == 4
+    kv = S.kv_cache(8)
+    with pytest.raises(IbhError):
+        S.forward_step(kv, 0, 8)            # position beyond the cache
+    with pytest.raises(IbhError):
+        S.forward_step(kv, 1000, 0)         # token beyond the vocabulary
+
+
+def test_cache_limit_stops_generation(L, tmp_path_factory, tmp_path):
+    """ib_pq_generate_greedy stops once pos reaches max_seq."""
+    from libinferbit_amd.session import PqSession
+    path = model(tmp_path_factory, "int4")
+    rg, _ = ref_run(path, PROMPT, 20, "greedy", tmp_path, max_seq=8)
+    S = PqSession(path)
+    gg = S.generate_greedy(S.kv_cache(8), PROMPT, 20).tolist()
+    assert gg == rg and len(gg) == 8 - len(PROMPT) + 1
