@@ -71,10 +71,21 @@ struct Mat {
 constexpr int kNormThreads = 1024;
 constexpr int kNormMaxPer = 16;   // hidden <= 16384
 
-__global__ void embed_raw_kernel(float* __restrict__ x, const void* __restrict__ emb, int f16, int token,
+// Token and position are read from device memory (tokens[*dpos]) so that a
+// captured step replays for successive positions.  Host entry points check
+// token ranges; generated tokens come from the LM head's rows and are clamped
+// to the embedding's rows here as a guard against a short table.
+__device__ __forceinline__ int cur_token(const int* tokens, const int* dpos, int rows) {
+    const int t = tokens[*dpos];
+    return t < 0 ? 0 : (t >= rows ? rows - 1 : t);
+}
+
+__global__ void embed_raw_kernel(float* __restrict__ x, const void* __restrict__ emb, int f16,
+                                 const int* __restrict__ tokens, const int* __restrict__ dpos, int rows,
                                  int hidden) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= hidden) return;
+    const int token = cur_token(tokens, dpos, rows);
     const size_t at = (size_t)token * hidden + i;
     x[i] = f16 ? f16_to_f32(((const uint16_t*)emb)[at]) : ((const float*)emb)[at];
 }
@@ -82,8 +93,10 @@ __global__ void embed_raw_kernel(float* __restrict__ x, const void* __restrict__
 // ib_pq_session_reconstruct_row (src/pq_decode.c:6136-6198): chunk c places
 // (cb1 + cb2) of its two halves at inner_cols, times the row scale; outlier
 // columns are sidecar * column scale.
-__global__ void pq_row_kernel(float* __restrict__ out, ibh_pq_tensor t, int row) {
+__global__ void pq_row_kernel(float* __restrict__ out, ibh_pq_tensor t, const int* __restrict__ tokens,
+                              const int* __restrict__ dpos) {
     const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    const int row = cur_token(tokens, dpos, t.M);
     const int half = t.G / 2;
     const float rs = f16_to_f32(t.row_scale[row]);
     if (j < t.C * t.G) {
@@ -155,8 +168,11 @@ __global__ __launch_bounds__(kNormThreads) void v5_rmsnorm_kernel(float* __restr
 // Block b < n_heads: query head; < n_heads + n_kv: key head; else value head.
 __global__ void v5_rope_kv_kernel(float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
                                   float* __restrict__ kc, float* __restrict__ vc, const float* __restrict__ cs,
-                                  int n_heads, int n_kv, int hd) {
-    const int b = blockIdx.x, half = hd / 2;
+                                  const int* __restrict__ dpos, int n_heads, int n_kv, int hd) {
+    const int b = blockIdx.x, half = hd / 2, pos = *dpos;
+    kc += (size_t)pos * n_kv * hd;
+    vc += (size_t)pos * n_kv * hd;
+    cs += (size_t)pos * hd;
     for (int i = threadIdx.x; i < half; i += blockDim.x) {
         if (b < n_heads + n_kv) {
             const float* src = b < n_heads ? q + (size_t)b * hd : k + (size_t)(b - n_heads) * hd;
@@ -180,6 +196,18 @@ __global__ void v5_silu_kernel(float* __restrict__ out, const float* __restrict_
     if (i >= n) return;
     const float g = gate[i];
     out[i] = g / (1.0f + ib_expf(-g)) * up[i];
+}
+
+// End of a step: position + 1.
+__global__ void v5_bump_kernel(int* __restrict__ dpos) { *dpos += 1; }
+
+// Greedy pick from the sorted top-K head: out[g] = tokens[pos] = ids[0], g + 1.
+__global__ void v5_advance_kernel(const int32_t* __restrict__ ids, int* __restrict__ tokens,
+                                  int* __restrict__ state, int* __restrict__ out) {
+    const int id = ids[0];
+    out[state[1]] = id;
+    state[1] += 1;
+    tokens[state[0]] = id;
 }
 
 __global__ void v5_scale_kernel(float* __restrict__ out, const float* __restrict__ x, const float* __restrict__ s,
@@ -236,6 +264,7 @@ struct ibh_v5_session {
     int embed_kind = -1;   // 0 raw f32, 1 raw f16, 2 PQ
     const void* embed = nullptr;
     int embed_mat = -1;
+    int embed_rows = 0;
     // activations
     float *x = nullptr, *xb = nullptr, *xb2 = nullptr, *q = nullptr, *kn = nullptr, *vn = nullptr, *qkv = nullptr;
     float *gate = nullptr, *up = nullptr, *gu = nullptr, *delta = nullptr, *xs = nullptr, *logits = nullptr;
@@ -243,6 +272,7 @@ struct ibh_v5_session {
     int32_t* top_ids = nullptr;
     void* ws = nullptr;
     size_t ws_bytes = 0;
+    unsigned epoch = 1;   // bumped by policy changes: captured steps are stale
 };
 
 struct ibh_v5_kv {
@@ -251,6 +281,13 @@ struct ibh_v5_kv {
     float *k = nullptr, *v = nullptr, *rope = nullptr;
     void* aws = nullptr;
     size_t aws_bytes = 0;
+    int* state = nullptr;    // device: [0] position, [1] generated count
+    int* tokens = nullptr;   // device: token at each position [max_seq]
+    int* outs = nullptr;     // device: generated tokens [max_seq + 1]
+    // captured steps (they bake this cache's and the session's pointers and
+    // the policies at capture time): to hidden, to logits, greedy step
+    hipGraphExec_t g_hidden = nullptr, g_logits = nullptr, g_gen = nullptr, g_pick = nullptr;
+    unsigned epoch = 0;
 };
 
 namespace {
@@ -710,6 +747,7 @@ int open_session(ibh_v5_session* s, const char* path) {
         }
         s->embed_kind = 2;
         s->embed_mat = ei;
+        s->embed_rows = s->mats[ei].M;
     } else {
         const RawT* r = raw_find(s, "tok_embed");
         if (!r || r->ndim != 2 || r->shape[1] != H || (r->dtype != RAW_F16 && r->dtype != RAW_F32)) {
@@ -718,6 +756,7 @@ int open_session(ibh_v5_session* s, const char* path) {
         }
         s->embed_kind = r->dtype == RAW_F16 ? 1 : 0;
         s->embed = r->d;
+        s->embed_rows = r->shape[0];
     }
 
     // activations and one shared workspace (every launch is on one stream)
@@ -761,21 +800,20 @@ int matmul(ibh_v5_session* s, int mi, const float* x, float* out) {
     return ibh_pq_matmul_policy(&m.pq, xk, out, &p, s->ws, s->ws_bytes, s->st);
 }
 
-// forward_step_internal_sc: x ends as the post-final-norm hidden state in
-// s->xb; logits (device) when want_logits.
-int forward(ibh_v5_session* s, ibh_v5_kv* kv, int token, int pos, bool want_logits) {
+// forward_step_internal_sc for tokens[*pos] at *pos: ends with the
+// post-final-norm hidden state in s->xb and, when want_logits, the logits in
+// s->logits; then *pos + 1.  Every launch reads the position from device
+// memory, so the chain is captured once and replayed.
+int forward_dev(ibh_v5_session* s, ibh_v5_kv* kv, bool want_logits) {
     const int H = s->hidden, KV = s->kv_dim, I = s->inter, hd = s->head_dim;
-    if (token < 0 || token >= (s->embed_kind == 2 ? s->mats[s->embed_mat].M : s->vocab) || pos < 0 ||
-        pos >= kv->max_seq) {
-        ibh_set_error("ibh_v5_forward_step: token %d or position %d out of range", token, pos);
-        return IBH_ERROR_PARAM;
-    }
+    int* dpos = kv->state;
     if (s->embed_kind == 2) {
         const ibh_pq_tensor& t = s->mats[s->embed_mat].pq;
         const int n = t.C * t.G + t.n_outlier;
-        pq_row_kernel<<<(n + 255) / 256, 256, 0, s->st>>>(s->x, t, token);
+        pq_row_kernel<<<(n + 255) / 256, 256, 0, s->st>>>(s->x, t, kv->tokens, dpos);
     } else {
-        embed_raw_kernel<<<(H + 255) / 256, 256, 0, s->st>>>(s->x, s->embed, s->embed_kind, token, H);
+        embed_raw_kernel<<<(H + 255) / 256, 256, 0, s->st>>>(s->x, s->embed, s->embed_kind, kv->tokens, dpos,
+                                                             s->embed_rows, H);
     }
     IBH_CHECK_LAUNCH("ibh_v5: embedding");
     int rc;
@@ -794,12 +832,11 @@ int forward(ibh_v5_session* s, ibh_v5_kv* kv, int token, int pos, bool want_logi
             return rc;
         }
         const size_t lbase = (size_t)l * kv->max_seq * KV;
-        v5_rope_kv_kernel<<<s->n_heads + 2 * s->n_kv, 64, 0, s->st>>>(
-            q, k, v, kv->k + lbase + (size_t)pos * KV, kv->v + lbase + (size_t)pos * KV,
-            kv->rope + (size_t)pos * hd, s->n_heads, s->n_kv, hd);
+        v5_rope_kv_kernel<<<s->n_heads + 2 * s->n_kv, 64, 0, s->st>>>(q, k, v, kv->k + lbase, kv->v + lbase,
+                                                                       kv->rope, dpos, s->n_heads, s->n_kv, hd);
         IBH_CHECK_LAUNCH("ibh_v5: rope + kv write");
-        if ((rc = ibh_launch_attn(s->xb2, q, kv->k + lbase, kv->v + lbase, nullptr, nullptr, pos, nullptr, pos,
-                                  s->n_heads, s->n_kv, hd, 32, kv->aws, kv->aws_bytes, s->st)))
+        if ((rc = ibh_launch_attn(s->xb2, q, kv->k + lbase, kv->v + lbase, nullptr, nullptr, 0, dpos,
+                                  kv->max_seq - 1, s->n_heads, s->n_kv, hd, 32, kv->aws, kv->aws_bytes, s->st)))
             return rc;
         if ((rc = matmul(s, s->mo[l], s->xb2, s->delta))) return rc;
         v5_rmsnorm_kernel<<<1, kNormThreads, 0, s->st>>>(s->xb, s->x, s->delta, s->w_pn[l], s->eps, H);
@@ -820,7 +857,80 @@ int forward(ibh_v5_session* s, ibh_v5_kv* kv, int token, int pos, bool want_logi
     v5_rmsnorm_kernel<<<1, kNormThreads, 0, s->st>>>(s->xb, s->x, pending, s->w_final, s->eps, H);
     IBH_CHECK_LAUNCH("ibh_v5: final rmsnorm");
     if (want_logits && (rc = matmul(s, s->m_head, s->xb, s->logits))) return rc;
-    kv->length = pos + 1;
+    v5_bump_kernel<<<1, 1, 0, s->st>>>(dpos);
+    IBH_CHECK_LAUNCH("ibh_v5: position");
+    return IBH_OK;
+}
+
+// The greedy pick of ib_pq_generate_greedy: top-8 of the PQ head on s->xb,
+// ids[0] recorded and placed at tokens[*pos].
+int pick_dev(ibh_v5_session* s, ibh_v5_kv* kv) {
+    int rc;
+    if ((rc = ibh_pq_lm_head_topk(&s->mats[s->m_head].pq, s->xb, 8, s->top_val, s->top_ids, s->ws, s->ws_bytes,
+                                  s->st)))
+        return rc;
+    v5_advance_kernel<<<1, 1, 0, s->st>>>(s->top_ids, kv->tokens, kv->state, kv->outs);
+    IBH_CHECK_LAUNCH("ibh_v5: advance");
+    return IBH_OK;
+}
+
+void drop_graphs(ibh_v5_kv* kv) {
+    for (hipGraphExec_t* g : {&kv->g_hidden, &kv->g_logits, &kv->g_gen, &kv->g_pick})
+        if (*g) {
+            hipGraphExecDestroy(*g);
+            *g = nullptr;
+        }
+}
+
+// what: 0 step to hidden, 1 step to logits, 2 pick + step, 3 pick only
+int capture(ibh_v5_session* s, ibh_v5_kv* kv, int what, hipGraphExec_t* out) {
+    IBH_HIP(hipStreamBeginCapture(s->st, hipStreamCaptureModeThreadLocal), "ibh_v5: begin capture");
+    int rc = IBH_OK;
+    if (what >= 2) rc = pick_dev(s, kv);
+    if (rc == IBH_OK && what != 3) rc = forward_dev(s, kv, what == 1);
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture(s->st, &g);
+    if (rc != IBH_OK || e != hipSuccess) {
+        if (g) hipGraphDestroy(g);
+        if (rc == IBH_OK) ibh_set_error("ibh_v5: stream capture failed: %s", hipGetErrorString(e));
+        return rc != IBH_OK ? rc : IBH_ERROR_INTERNAL;
+    }
+    const hipError_t ie = hipGraphInstantiate(out, g, nullptr, nullptr, 0);
+    hipGraphDestroy(g);
+    if (ie != hipSuccess) {
+        *out = nullptr;
+        ibh_set_error("ibh_v5: graph instantiation failed: %s", hipGetErrorString(ie));
+        return IBH_ERROR_INTERNAL;
+    }
+    return IBH_OK;
+}
+
+int run_graph(ibh_v5_session* s, ibh_v5_kv* kv, int what) {
+    if (kv->epoch != s->epoch) {
+        drop_graphs(kv);
+        kv->epoch = s->epoch;
+    }
+    hipGraphExec_t* g = what == 0 ? &kv->g_hidden : what == 1 ? &kv->g_logits : what == 2 ? &kv->g_gen : &kv->g_pick;
+    int rc;
+    if (!*g && (rc = capture(s, kv, what, g))) return rc;
+    IBH_HIP(hipGraphLaunch(*g, s->st), "ibh_v5: graph launch");
+    return IBH_OK;
+}
+
+// Host token at host position: tokens[pos] = token, state = {pos, 0}.
+int set_token_pos(ibh_v5_session* s, ibh_v5_kv* kv, int token, int pos) {
+    const int st[2] = {pos, 0};
+    IBH_HIP(hipMemcpyAsync(kv->tokens + pos, &token, 4, hipMemcpyHostToDevice, s->st), "ibh_v5: token");
+    IBH_HIP(hipMemcpyAsync(kv->state, st, 8, hipMemcpyHostToDevice, s->st), "ibh_v5: position");
+    return IBH_OK;
+}
+
+int check_token_pos(ibh_v5_session* s, ibh_v5_kv* kv, int token, int pos, const char* who) {
+    if (token < 0 || token >= s->embed_rows || pos < 0 || pos >= kv->max_seq) {
+        ibh_set_error("%s: token %d or position %d out of range (%d rows, %d positions)", who, token, pos,
+                      s->embed_rows, kv->max_seq);
+        return IBH_ERROR_PARAM;
+    }
     return IBH_OK;
 }
 
@@ -868,6 +978,7 @@ extern "C" int ibh_v5_set_default_policy(ibh_v5_session* s, const ibh_pq_policy*
         return IBH_ERROR_PARAM;
     }
     s->default_policy = *p;
+    s->epoch++;
     return IBH_OK;
 }
 
@@ -882,6 +993,7 @@ extern "C" int ibh_v5_set_policy(ibh_v5_session* s, const char* name, const ibh_
             m.policy = *p;
             m.has_policy = true;
             found = true;
+            s->epoch++;
         }
     if (!found) {
         ibh_set_error("ibh_v5_set_policy: no PQ tensor %s", name);
@@ -913,6 +1025,8 @@ extern "C" int ibh_v5_session_matmul(ibh_v5_session* s, const char* name, const 
     return rc;
 }
 
+extern "C" void ibh_v5_kv_free(ibh_v5_kv* kv);
+
 extern "C" int ibh_v5_kv_create(ibh_v5_session* s, int max_seq, ibh_v5_kv** out) {
     if (!s || !out || max_seq <= 0) {
         ibh_set_error("ibh_v5_kv_create: invalid arguments");
@@ -927,7 +1041,9 @@ extern "C" int ibh_v5_kv_create(ibh_v5_session* s, int max_seq, ibh_v5_kv** out)
     kv->aws_bytes = ibh_attn_workspace_bytes(s->n_heads, s->head_dim, max_seq);
     bool ok = hipMalloc((void**)&kv->k, n * 4) == hipSuccess && hipMalloc((void**)&kv->v, n * 4) == hipSuccess &&
               hipMalloc((void**)&kv->rope, (size_t)max_seq * half * 8) == hipSuccess &&
-              hipMalloc(&kv->aws, kv->aws_bytes) == hipSuccess;
+              hipMalloc(&kv->aws, kv->aws_bytes) == hipSuccess && hipMalloc((void**)&kv->state, 16) == hipSuccess &&
+              hipMalloc((void**)&kv->tokens, (size_t)max_seq * 4 + 4) == hipSuccess &&
+              hipMalloc((void**)&kv->outs, (size_t)max_seq * 4 + 8) == hipSuccess;
     if (ok) {
         // ib_rope_f32's angles (src/pq_decode.c:4631-4634), host libm
         std::vector<float> tab((size_t)max_seq * half * 2);
@@ -941,14 +1057,11 @@ extern "C" int ibh_v5_kv_create(ibh_v5_session* s, int max_seq, ibh_v5_kv** out)
         ok = hipMemcpy(kv->rope, tab.data(), tab.size() * 4, hipMemcpyHostToDevice) == hipSuccess;
     }
     if (!ok) {
-        hipFree(kv->k);
-        hipFree(kv->v);
-        hipFree(kv->rope);
-        hipFree(kv->aws);
-        delete kv;
+        ibh_v5_kv_free(kv);
         ibh_set_error("ibh_v5_kv_create: device allocation failed (%d positions)", max_seq);
         return IBH_ERROR_MEMORY;
     }
+    kv->epoch = s->epoch;
     *out = kv;
     return IBH_OK;
 }
@@ -956,10 +1069,10 @@ extern "C" int ibh_v5_kv_create(ibh_v5_session* s, int max_seq, ibh_v5_kv** out)
 extern "C" void ibh_v5_kv_free(ibh_v5_kv* kv) {
     if (!kv) return;
     if (kv->s && kv->s->st) hipStreamSynchronize(kv->s->st);
-    hipFree(kv->k);
-    hipFree(kv->v);
-    hipFree(kv->rope);
-    hipFree(kv->aws);
+    drop_graphs(kv);
+    for (void* p : {(void*)kv->k, (void*)kv->v, (void*)kv->rope, kv->aws, (void*)kv->state, (void*)kv->tokens,
+                    (void*)kv->outs})
+        if (p) hipFree(p);
     delete kv;
 }
 
@@ -974,12 +1087,16 @@ extern "C" int ibh_v5_forward_step(ibh_v5_session* s, ibh_v5_kv* kv, int token, 
         ibh_set_error("ibh_v5_forward_step: invalid session or cache");
         return IBH_ERROR_PARAM;
     }
-    int rc = forward(s, kv, token, pos, logits != nullptr);
-    if (rc == IBH_OK && logits)
+    int rc;
+    if ((rc = check_token_pos(s, kv, token, pos, "ibh_v5_forward_step")) || (rc = set_token_pos(s, kv, token, pos)) ||
+        (rc = run_graph(s, kv, logits ? 1 : 0)))
+        return rc;
+    if (logits)
         IBH_HIP(hipMemcpyAsync(logits, s->logits, (size_t)s->vocab * 4, hipMemcpyDeviceToHost, s->st),
                 "ibh_v5_forward_step: logits");
     IBH_HIP(hipStreamSynchronize(s->st), "ibh_v5_forward_step");
-    return rc;
+    kv->length = pos + 1;
+    return IBH_OK;
 }
 
 extern "C" int ibh_v5_forward_step_to_hidden(ibh_v5_session* s, ibh_v5_kv* kv, int token, int pos, float* hidden) {
@@ -987,17 +1104,26 @@ extern "C" int ibh_v5_forward_step_to_hidden(ibh_v5_session* s, ibh_v5_kv* kv, i
         ibh_set_error("ibh_v5_forward_step_to_hidden: invalid session or cache");
         return IBH_ERROR_PARAM;
     }
-    int rc = forward(s, kv, token, pos, false);
-    if (rc == IBH_OK && hidden)
+    int rc;
+    if ((rc = check_token_pos(s, kv, token, pos, "ibh_v5_forward_step_to_hidden")) ||
+        (rc = set_token_pos(s, kv, token, pos)) || (rc = run_graph(s, kv, 0)))
+        return rc;
+    if (hidden)
         IBH_HIP(hipMemcpyAsync(hidden, s->xb, (size_t)s->hidden * 4, hipMemcpyDeviceToHost, s->st),
                 "ibh_v5_forward_step_to_hidden: copy");
     IBH_HIP(hipStreamSynchronize(s->st), "ibh_v5_forward_step_to_hidden");
-    return rc;
+    kv->length = pos + 1;
+    return IBH_OK;
 }
 
-// ib_pq_generate_greedy: prompt through the cache (the reference's batched
-// prefill equals sequential steps), then per token the top-8 PQ head
-// (top_ids[0] is the refined best), stop on eos or a full cache.
+// ib_pq_generate_greedy: the prompt through the cache (the reference's
+// batched prefill equals sequential steps), then per token the top-8 PQ
+// head (ids[0] is the refined best) and a step on it, as replays of
+// captured graphs with the tokens kept on the device.  The reference stops
+// after eos or once the position reaches the cache size; without eos the
+// count is known up front and nothing waits on the host until the end,
+// with eos the loop syncs every 16 tokens and cuts the output at the first
+// eos (steps replayed past it only write cache rows beyond the length).
 extern "C" int ibh_v5_generate_greedy(ibh_v5_session* s, ibh_v5_kv* kv, const int* prompt, int n_prompt,
                                       int max_new, int eos, int* out_ids, int* n_out) {
     if (!s || !kv || kv->s != s || !prompt || n_prompt <= 0 || max_new < 0 || !out_ids || !n_out) {
@@ -1005,8 +1131,7 @@ extern "C" int ibh_v5_generate_greedy(ibh_v5_session* s, ibh_v5_kv* kv, const in
         return IBH_ERROR_PARAM;
     }
     *n_out = 0;
-    const Mat& head = s->mats[s->m_head];
-    if (head.kind != MAT_PQ) {
+    if (s->mats[s->m_head].kind != MAT_PQ) {
         ibh_set_error("ibh_v5_generate_greedy: lm_head must be a PQ tensor");
         return IBH_ERROR_FORMAT;
     }
@@ -1014,23 +1139,46 @@ extern "C" int ibh_v5_generate_greedy(ibh_v5_session* s, ibh_v5_kv* kv, const in
         ibh_set_error("ibh_v5_generate_greedy: prompt of %d tokens exceeds the cache (%d)", n_prompt, kv->max_seq);
         return IBH_ERROR_CONTEXT;
     }
+    for (int i = 0; i < n_prompt; i++)
+        if (prompt[i] < 0 || prompt[i] >= s->embed_rows) {
+            ibh_set_error("ibh_v5_generate_greedy: prompt token %d out of range", prompt[i]);
+            return IBH_ERROR_PARAM;
+        }
+    const int st0[2] = {0, 0};
+    IBH_HIP(hipMemcpyAsync(kv->tokens, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice, s->st),
+            "ibh_v5_generate_greedy: prompt");
+    IBH_HIP(hipMemcpyAsync(kv->state, st0, 8, hipMemcpyHostToDevice, s->st), "ibh_v5_generate_greedy: state");
     int rc;
     for (int i = 0; i < n_prompt; i++)
-        if ((rc = forward(s, kv, prompt[i], i, false))) return rc;
-    int pos = n_prompt, written = 0;
-    for (int g = 0; g < max_new; g++) {
-        if ((rc = ibh_pq_lm_head_topk(&head.pq, s->xb, 8, s->top_val, s->top_ids, s->ws, s->ws_bytes, s->st)))
-            return rc;
-        int32_t best = 0;
-        IBH_HIP(hipMemcpyAsync(&best, s->top_ids, 4, hipMemcpyDeviceToHost, s->st), "ibh_v5_generate_greedy: id");
-        IBH_HIP(hipStreamSynchronize(s->st), "ibh_v5_generate_greedy");
-        out_ids[written++] = best;
-        *n_out = written;
-        if (eos >= 0 && best == eos) break;
-        if (pos >= kv->max_seq) break;
-        if ((rc = forward(s, kv, best, pos, false))) return rc;
-        pos++;
+        if ((rc = run_graph(s, kv, 0))) return rc;
+    const int n_step = std::min(max_new, kv->max_seq - n_prompt);   // tokens followed by a step
+    const int n_tok = std::min(max_new, kv->max_seq - n_prompt + 1);
+    int done = 0, found = -1;
+    while (done < n_step && found < 0) {
+        const int chunk = eos >= 0 ? std::min(16, n_step - done) : n_step - done;
+        for (int i = 0; i < chunk; i++)
+            if ((rc = run_graph(s, kv, 2))) return rc;
+        if (eos >= 0) {
+            IBH_HIP(hipMemcpyAsync(out_ids + done, kv->outs + done, (size_t)chunk * 4, hipMemcpyDeviceToHost, s->st),
+                    "ibh_v5_generate_greedy: ids");
+            IBH_HIP(hipStreamSynchronize(s->st), "ibh_v5_generate_greedy");
+            for (int i = 0; i < chunk && found < 0; i++)
+                if (out_ids[done + i] == eos) found = done + i;
+        }
+        done += chunk;
     }
+    if (found < 0 && n_tok > n_step && (rc = run_graph(s, kv, 3))) return rc;   // last token, no step after it
+    const int total = found >= 0 ? found + 1 : n_tok;
+    if (total > 0)
+        IBH_HIP(hipMemcpyAsync(out_ids, kv->outs, (size_t)total * 4, hipMemcpyDeviceToHost, s->st),
+                "ibh_v5_generate_greedy: ids");
     IBH_HIP(hipStreamSynchronize(s->st), "ibh_v5_generate_greedy");
+    if (found < 0 && n_tok > n_step) {
+        const int last = out_ids[total - 1];
+        if (eos >= 0 && last == eos) found = total - 1;
+    }
+    *n_out = total;
+    // steps taken: every token before the one that stopped the loop
+    kv->length = n_prompt + (found >= 0 ? found : n_step);
     return IBH_OK;
 }

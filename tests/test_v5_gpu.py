@@ -73,8 +73,8 @@ def relerr(a, b):
     return float(np.abs(a.astype(np.float64) - b).max() / np.abs(b).max())
 
 
-def gpu_steps(S, prompt, n_new, max_seq=64):
-    kv = S.kv_cache(max_seq)
+def gpu_steps(S, prompt, n_new, max_seq=64, kv=None):
+    kv = kv or S.kv_cache(max_seq)
     lg = [S.forward_step(kv, t, i) for i, t in enumerate(prompt)]
     cur, toks = lg[-1], []
     for g in range(n_new):
@@ -165,3 +165,39 @@ def test_cache_limit_stops_generation(L, tmp_path_factory, tmp_path):
     S = PqSession(path)
     gg = S.generate_greedy(S.kv_cache(8), PROMPT, 20).tolist()
     assert gg == rg and len(gg) == 8 - len(PROMPT) + 1
+
+
+def test_eos_cut_and_cache_length(L, tmp_path_factory, tmp_path):
+    """Generation stops at the first eos (kept in the output); the cache holds
+    the prompt plus every token before it; a second call on a cleared cache
+    replays the same captured steps to the same tokens."""
+    from libinferbit_amd.session import PqSession
+    path = model(tmp_path_factory, "mixed")
+    rg, _ = ref_run(path, PROMPT, 40, "greedy", tmp_path)
+    S = PqSession(path)
+    kv = S.kv_cache(64)
+    assert S.generate_greedy(kv, PROMPT, 40).tolist() == rg
+    assert len(kv) == len(PROMPT) + 40
+    for cut in (0, 3, 21):
+        eos = rg[cut]
+        first = rg.index(eos)
+        kv.clear()
+        got = S.generate_greedy(kv, PROMPT, 40, eos=eos).tolist()
+        assert got == rg[:first + 1], (cut, got)
+        assert len(kv) == len(PROMPT) + first
+
+
+def test_policy_change_recaptures(L, tmp_path_factory, tmp_path):
+    """A policy change after steps were captured applies to the next step."""
+    from libinferbit_amd.session import PqSession
+    path = model(tmp_path_factory, "pq_l2_actscale_pqembed")
+    S = PqSession(path)
+    kv = S.kv_cache(64)
+    t0, l0 = gpu_steps(S, PROMPT, 3, kv=kv)
+    r0, rl0 = ref_run(path, PROMPT, 3, "steps", tmp_path)
+    assert t0 == r0 and relerr(l0[-1], rl0[-1]) <= TOL
+    S.set_default_policy(1)
+    t1, l1 = gpu_steps(S, PROMPT, 3, kv=kv)
+    r1, rl1 = ref_run(path, PROMPT, 3, "steps", tmp_path, policy=(1, 0.0, 0.0))
+    assert t1 == r1 and relerr(l1[-1], rl1[-1]) <= TOL
+    assert relerr(l1[-1], l0[-1]) > 1e-3      # the level-2 terms are gone
