@@ -40,7 +40,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--quick", action="store_true", help="headline only (for profiling runs)")
     p.add_argument("--no-decode", action="store_true", help="skip the end-to-end decode legs")
-    p.add_argument("--only", choices=["headline", "gemm", "pq", "pqpol", "int4g", "verify", "decode-tinyllama",
+    p.add_argument("--only", choices=["headline", "gemm", "pq", "pqpol", "int4g", "verify", "v5", "decode-tinyllama",
                             "decode-mistral"],
                    help="run one case and print its JSON (for profiler runs)")
     p.add_argument("--calib-copy", action="store_true",
@@ -368,6 +368,82 @@ def cpu_decode(path, case, n_out=8):
                       f"empty KV cache, {d['seconds']:.2f} s"}
 
 
+V5_TINYLLAMA = dict(num_layers=22, hidden_size=2048, num_heads=32, num_kv_heads=4, head_dim=64,
+                    intermediate_size=5632, vocab_size=32000, rope_theta=10000.0)
+
+
+def v5_bytes_per_token(cfg, n_pos, G=128, pq_G=16, pq_K=256):
+    """Algorithmic HBM bytes of one v5 greedy step: INT4 nibbles + fp16 group
+    scales + fp32 AWQ vector of every projection, the PQ head's indices, row
+    scales and codebooks (level-1 logits of every row; the top-8 refinement
+    re-reads 8 rows), the fp32 cache rows attention reads, the fp16
+    embedding row."""
+    H, I, V, L = cfg["hidden_size"], cfg["intermediate_size"], cfg["vocab_size"], cfg["num_layers"]
+    KV = cfg["num_kv_heads"] * cfg["head_dim"]
+    per_layer = 0
+    for r, c in ((H, H), (KV, H), (KV, H), (H, H), (I, H), (I, H), (H, I)):
+        per_layer += r * c // 2 + r * (c // G) * 2 + 4 * c
+    per_layer += 2 * n_pos * 4 * KV + 2 * 4 * H
+    C = H // pq_G
+    head = 2 * V * C + 2 * V + 2 * pq_K * (pq_G // 2) * 2
+    return L * per_layer + head + 2 * H
+
+
+def v5_decode_case(steps, cpu):
+    """IBF v5 session greedy decode (ib_pq_generate_greedy) on a TinyLlama-
+    1.1B-shaped synthetic v5 model: INT4 group-128 projections with AWQ
+    scales, PQ LM head (G 16, K 256), fp16 embedding.  tok/s = steps / (time
+    of prompt + steps - time of the prompt alone), each a full
+    generate call (device-resident loop of captured steps)."""
+    from libinferbit_amd import ibf5
+    from libinferbit_amd.session import PqSession
+    workdir = os.environ.get("IBH_MODEL_DIR", "/tmp/ibh_models")
+    os.makedirs(workdir, exist_ok=True)
+    path = os.path.join(workdir, "v5_tinyllama_int4g_awq.ibf")
+    t = time.time()
+    if not os.path.exists(path):
+        ibf5.write_synthetic_v5(path + ".tmp", V5_TINYLLAMA, seed=7, awq=True)
+        os.replace(path + ".tmp", path)
+    out = {"config": "TinyLlama-1.1B shape, IBF v5 INT4 g128 + AWQ, PQ head", "model_write_s": round(time.time() - t, 1)}
+    S = PqSession(path)
+    kv = S.kv_cache(1024)
+    prompt = list(range(1, 9))
+    S.generate_greedy(kv, prompt, 8)                 # captures the steps
+    kv.clear()
+    t0 = time.perf_counter()
+    S.generate_greedy(kv, prompt, 0)
+    t_pre = time.perf_counter() - t0
+    kv.clear()
+    t0 = time.perf_counter()
+    S.generate_greedy(kv, prompt, steps)
+    t_all = time.perf_counter() - t0
+    dt = t_all - t_pre
+    tok_s = steps / dt
+    nbytes = v5_bytes_per_token(V5_TINYLLAMA, len(prompt) + steps // 2)
+    out["gpu"] = {"tok_s": round(tok_s, 2), "ms_per_token": round(dt / steps * 1e3, 4), "steps": steps,
+                  "prefill_ms": round(t_pre * 1e3, 3), "bytes_per_token": nbytes,
+                  "GBps": round(nbytes * tok_s / 1e9, 1), "frac_hbm": round(nbytes * tok_s / 1e9 / HBM_PEAK_GBS, 4)}
+    kv.close()
+    S.close()
+    if cpu:
+        exe = os.path.join(ROOT, "oracle", "_ref", "ref_v5")
+        if os.path.exists(exe):
+            cores = max(1, min(len(os.sched_getaffinity(0)), 16))
+            pp = path + ".prompt.i32"
+            np.asarray(prompt, np.int32).tofile(pp)
+            n_cpu = 8
+            r = subprocess.run([exe, path, "64", str(n_cpu), pp, "greedy"], capture_output=True, text=True,
+                               timeout=900, env=dict(os.environ, IB_PQ_THREADS=str(cores)))
+            if r.returncode == 0:
+                d = json.loads(r.stdout.strip().splitlines()[-1])
+                cdt = d["seconds"] - d["prefill_seconds"]
+                out["cpu_baseline"] = {"value": round(n_cpu / cdt, 3), "unit": "tok/s", "cores": cores,
+                                       "kind": "reference",
+                                       "sample": f"ib_pq_generate_greedy, 8-token prompt + {n_cpu} tokens, "
+                                                 f"IB_PQ_THREADS={cores}, {cdt:.2f} s after the prompt"}
+    return out
+
+
 def cpu_baseline():
     """The reference library compiled from its own sources (oracle/_ref),
     ib_parallel_matmul INT4 14336x4096 with the x86 AVX2 table, timed on
@@ -415,6 +491,8 @@ def main():
             r = pq_case(torch, L, max(200, a.steps // 4), 20)
         elif a.only == "pqpol":
             r = pq_policy_cases(torch, L, max(200, a.steps // 4), 20)
+        elif a.only == "v5":
+            r = v5_decode_case(256, cpu=not a.no_cpu)
         elif a.only == "verify":
             r = verify_case(10)
         elif a.only == "int4g":
@@ -458,6 +536,8 @@ def main():
             decode[name] = decode_case(name, 128, cpu=not a.no_cpu and name == "tinyllama")
         print("bench: batched verify (forward_positions)", file=sys.stderr, flush=True)
         decode["tinyllama_forward_positions"] = verify_case(10)
+        print("bench: v5 session decode", file=sys.stderr, flush=True)
+        decode["v5_tinyllama_int4g"] = v5_decode_case(256, cpu=not a.no_cpu)
     cpu = None if a.no_cpu else cpu_baseline()
     out = {
         "metric": "quantized GEMV HBM GB/s (% of peak) + decode tok/s, Mistral-7B-shape INT4, 1 GPU",

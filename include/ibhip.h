@@ -199,8 +199,9 @@ int    ibh_pq_matmul_policy(const ibh_pq_tensor* t, const float* x, float* out, 
  * level-1 logits of every row, the K_top largest, their full-pyramid logits
  * (ib_pq_matmul_fp32_subset, 2145-2250), sorted descending.  out_logits /
  * out_ids [K_top] device arrays; K_top <= 1024.  Ties in the level-1 logits
- * keep the lowest row indices (the reference's heap keeps an order-dependent
- * subset of equal values).  `ws` >= ibh_pq_topk_workspace_bytes(t, K_top),
+ * keep the lowest row indices and equal refined logits come in row order
+ * (the reference's heap keeps an order-dependent subset of equal values and
+ * its insertion sort keeps heap order).  `ws` >= ibh_pq_topk_workspace_bytes(t, K_top),
  * NULL = library workspace. */
 size_t ibh_pq_topk_workspace_bytes(const ibh_pq_tensor* t, int k_top);
 int    ibh_pq_lm_head_topk(const ibh_pq_tensor* t, const float* x, int k_top, float* out_logits, int32_t* out_ids,

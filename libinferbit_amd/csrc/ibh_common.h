@@ -144,7 +144,18 @@ __device__ __forceinline__ RowPick pick_rows(const RowSet& s) {
     if (b >= s.b1) return {s.W[1], s.sc[1], s.y[1], s.M[1], b - s.b1};
     return {s.W[0], s.sc[0], s.y[0], s.M[0], b};
 }
+// One group-scaled INT4 matrix of a multi-matrix launch (ibh_rows.hip).
+struct IbhGrpMat {
+    const uint8_t* q;
+    const uint16_t* s;
+    const float* ia;
+    const uint16_t* oi;
+    const uint16_t* ov;
+    float* out;
+    int M, K_out;
+};
 // Host side: one matrix of a set.
+
 struct MatDesc {
     float* out;
     const void* w;

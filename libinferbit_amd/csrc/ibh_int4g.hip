@@ -16,6 +16,8 @@
 
 using namespace ibh;
 
+int ibh_launch_rows_grp_multi(const IbhGrpMat* m, int n, const float* x, bool awq, const float* xo, int N, int G,
+                              hipStream_t st);
 int ibh_launch_rows_grp(float* out, const uint8_t* q, const uint16_t* s, const float* x, bool awq, const float* xo,
                         const float* ia, const uint16_t* oi, const uint16_t* ov, int M, int N, int G, int K_out,
                         hipStream_t st);
@@ -123,6 +125,27 @@ static int int4g_one(const ibh_int4g_tensor* t, const float* x, float* out, floa
     }
     IBH_CHECK_LAUNCH("ibh_int4g_matmul");
     return IBH_OK;
+}
+
+// Up to three INT4 tensors that read the same x (a layer's q/k/v or
+// gate/up), one launch of the matrix-core kernel.  Returns 1 when launched;
+// 0 when the set does not qualify (different N or G, mixed AWQ, a skip mask
+// asked for, or a shape the kernel does not take): nothing was launched
+// and the caller runs the tensors one by one.
+int ibh_int4g_matmul_group(const ibh_int4g_tensor* const* t, float* const* out, int n, const float* x, float rel,
+                           hipStream_t st) {
+    if (n < 1 || n > 3 || rel > 0.f) return 0;
+    const bool awq = t[0]->inv_act != nullptr;
+    IbhGrpMat m[3];
+    for (int i = 0; i < n; i++) {
+        if (t[i]->N != t[0]->N || t[i]->G != t[0]->G || (t[i]->inv_act != nullptr) != awq ||
+            (t[i]->K_out > 0 && (!t[i]->outl_idx || !t[i]->outl_val)))
+            return 0;
+        m[i] = IbhGrpMat{t[i]->q, t[i]->s, t[i]->inv_act, t[i]->outl_idx, t[i]->outl_val, out[i], t[i]->M,
+                         t[i]->K_out};
+    }
+    if (!ibh_launch_rows_grp_multi(m, n, x, awq, x, t[0]->N, t[0]->G, st)) return 0;
+    return hipGetLastError() == hipSuccess ? 1 : -1;
 }
 
 static int int4g_ws_resolve(const ibh_int4g_tensor* t, float rel, void** ws, size_t ws_bytes, const char* who) {

@@ -359,60 +359,108 @@ __device__ __forceinline__ uint32_t desc_key(float v) {
 
 constexpr int kSelThreads = 1024;
 
-// The K largest of v[0..M): radix select of the K-th key (4 passes of 8 bits),
-// then every element above it plus the first ties in index order.  One block.
+// The K largest of v[0..M): radix select of the K-th key (4 passes of 8 bits;
+// per-wavefront histograms, the bin search one wavefront-wide scan), then
+// every element above it plus the first ties of the K-th key in index order;
+// the selection ends sorted by row index.  One block.
 __global__ __launch_bounds__(kSelThreads) void pq_topk_select(const float* __restrict__ v, int M, int K,
                                                               int32_t* __restrict__ sel) {
-    __shared__ int hist[256];
+    constexpr int NW = kSelThreads / 64;
+    __shared__ int hist[NW][256];
+    __shared__ int tot[256];
+    __shared__ int tmp[1024];
     __shared__ uint32_t s_prefix, s_mask;
-    __shared__ int s_kk, s_nless, s_neq;
-    __shared__ int wcnt[kSelThreads / 64];
+    __shared__ int s_kk, s_nless, s_neq, s_eqtot;
+    __shared__ int wcnt[NW];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (tid == 0) { s_prefix = 0; s_mask = 0; s_kk = K; s_nless = 0; s_neq = 0; }
+    if (tid == 0) { s_prefix = 0; s_mask = 0; s_kk = K; s_nless = 0; s_neq = 0; s_eqtot = 0; }
     for (int pass = 0; pass < 4; pass++) {
         const int shift = 24 - 8 * pass;
-        if (tid < 256) hist[tid] = 0;
+        for (int e = tid; e < NW * 256; e += kSelThreads) (&hist[0][0])[e] = 0;
         __syncthreads();
         const uint32_t prefix = s_prefix, mask = s_mask;
         for (int i = tid; i < M; i += kSelThreads) {
             const uint32_t d = desc_key(v[i]);
-            if ((d & mask) == prefix) atomicAdd(&hist[(d >> shift) & 255], 1);
+            if ((d & mask) == prefix) atomicAdd(&hist[wave][(d >> shift) & 255], 1);
         }
         __syncthreads();
-        if (tid == 0) {
-            int cum = 0, b = 0;
-            for (; b < 255; b++) {
-                if (cum + hist[b] >= s_kk) break;
-                cum += hist[b];
+        if (tid < 256) {
+            int c = 0;
+#pragma unroll
+            for (int w = 0; w < NW; w++) c += hist[w][tid];
+            tot[tid] = c;
+        }
+        __syncthreads();
+        if (wave == 0) {
+            // first bin b (<= 255) whose inclusive count reaches kk
+            int c[4], sum = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) { c[j] = tot[4 * lane + j]; sum += c[j]; }
+            int incl = sum;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int n = __shfl_up(incl, o, 64);
+                if (lane >= o) incl += n;
             }
-            s_kk -= cum;
-            s_prefix |= (uint32_t)b << shift;
-            s_mask |= 0xFFu << shift;
+            const int excl = incl - sum, kk = s_kk;
+            const bool last = lane == 63;
+            if ((excl < kk && kk <= incl) || (last && incl < kk)) {
+                int cum = excl, j = 0;
+                for (; j < 3; j++) {
+                    if (cum + c[j] >= kk) break;
+                    cum += c[j];
+                }
+                s_kk = kk - cum;
+                s_prefix = prefix | ((uint32_t)(4 * lane + j) << shift);
+                s_mask = mask | (0xFFu << shift);
+            }
         }
         __syncthreads();
     }
     const uint32_t kth = s_prefix;
     const int take_eq = s_kk;                     // ties of the K-th key to keep, lowest indices first
-    for (int base = 0; base < M; base += kSelThreads) {
-        const int i = base + tid;
-        const uint32_t d = i < M ? desc_key(v[i]) : 0xFFFFFFFFu;
-        const bool less = i < M && d < kth, eq = i < M && d == kth;
-        if (less) sel[atomicAdd(&s_nless, 1)] = i;
-        const unsigned long long b = __ballot(eq);
-        if (lane == 0) wcnt[wave] = __popcll(b);
-        __syncthreads();
-        int before = s_neq;
-        for (int w = 0; w < wave; w++) before += wcnt[w];
-        const int r = before + __popcll(b & ((1ull << lane) - 1ull));
-        if (eq && r < take_eq) sel[(K - take_eq) + r] = i;
-        __syncthreads();
-        if (tid == 0) {
-            int tot = 0;
-            for (int w = 0; w < kSelThreads / 64; w++) tot += wcnt[w];
-            s_neq += tot;
-        }
-        __syncthreads();
+    for (int i = tid; i < M; i += kSelThreads) {
+        const uint32_t d = desc_key(v[i]);
+        if (d < kth) sel[atomicAdd(&s_nless, 1)] = i;
+        else if (d == kth) atomicAdd(&s_eqtot, 1);
     }
+    __syncthreads();
+    if (s_eqtot <= take_eq) {
+        for (int i = tid; i < M; i += kSelThreads)
+            if (desc_key(v[i]) == kth) sel[(K - take_eq) + atomicAdd(&s_neq, 1)] = i;
+    } else {
+        // more ties than places: the lowest indices, in index order
+        for (int base = 0; base < M; base += kSelThreads) {
+            const int i = base + tid;
+            const bool eq = i < M && desc_key(v[i]) == kth;
+            const unsigned long long b = __ballot(eq);
+            if (lane == 0) wcnt[wave] = __popcll(b);
+            __syncthreads();
+            int before = s_neq;
+            for (int w = 0; w < wave; w++) before += wcnt[w];
+            const int r = before + __popcll(b & ((1ull << lane) - 1ull));
+            if (eq && r < take_eq) sel[(K - take_eq) + r] = i;
+            __syncthreads();
+            if (tid == 0) {
+                int t = 0;
+                for (int w = 0; w < NW; w++) t += wcnt[w];
+                s_neq += t;
+            }
+            __syncthreads();
+            if (s_neq >= take_eq) break;
+        }
+    }
+    __syncthreads();
+    // selection order = row index order (K <= 1024, distinct rows)
+    __threadfence_block();
+    for (int i = tid; i < K; i += kSelThreads) {
+        const int r = sel[i];
+        int rank = 0;
+        for (int j = 0; j < K; j++) rank += sel[j] < r;
+        tmp[rank] = r;
+    }
+    __syncthreads();
+    for (int i = tid; i < K; i += kSelThreads) sel[i] = tmp[i];
 }
 
 // Full-pyramid logits of the selected rows (ib_pq_matmul_fp32_subset,
@@ -454,7 +502,7 @@ __global__ __launch_bounds__(256) void pq_subset_rows(PqDev t, const float* __re
 }
 
 // Descending order of the refined logits (the reference's insertion sort:
-// ties keep their selection order).  One block, K <= 1024.
+// ties keep their selection order, here row order).  One block, K <= 1024.
 __global__ __launch_bounds__(1024) void pq_topk_sort(const float* __restrict__ val, const int32_t* __restrict__ ids,
                                                      int K, float* __restrict__ out_v, int32_t* __restrict__ out_i) {
     for (int i = threadIdx.x; i < K; i += 1024) {

@@ -104,6 +104,7 @@ __device__ __forceinline__ float diag_sum(float v) {
 }
 
 constexpr int kMaxWaves = 16;
+constexpr int kGrpSegs = 3;
 
 // ── W4A8 ─────────────────────────────────────────────────────────────────────
 // SAREG: the block folds its rows itself (KW == 1) and G <= 32, so sa is
@@ -468,13 +469,40 @@ __global__ __launch_bounds__(1024) void gemv_rows_x(const RowSet rs, const float
 // scale group, so each step's three digit-plane sums are combined in fp32 and
 // multiplied by their group scale before the next step accumulates.  Rows are
 // whole 16-byte segments (N % 32 == 0); a step past the row end loads zeros.
+//
+// One launch may cover up to kGrpSegs matrices that share x, N and G (the
+// q/k/v or gate/up projections of a layer): segment i owns the blocks from
+// b0[i], its own weights, scales, AWQ vector, outliers and output.
+struct GrpSet {
+    int n;
+    int b0[kGrpSegs];
+    const uint8_t* W[kGrpSegs];
+    const uint16_t* sg[kGrpSegs];
+    const float* ia[kGrpSegs];
+    const uint16_t* oi[kGrpSegs];
+    const uint16_t* ov[kGrpSegs];
+    float* y[kGrpSegs];
+    int M[kGrpSegs];
+    int K_out[kGrpSegs];
+};
+
 template <int NXQ, bool AWQ>
-__global__ __launch_bounds__(1024) void gemv_rows_grp(const uint8_t* __restrict__ W, const uint16_t* __restrict__ sg,
-                                                      const float* __restrict__ x, const float* __restrict__ ia,
-                                                      const float* __restrict__ xo, const uint16_t* __restrict__ oi,
-                                                      const uint16_t* __restrict__ ov, float* __restrict__ y, int M,
-                                                      int N, int G, int K_out, int S, int WR, int KW) {
+__global__ __launch_bounds__(1024) void gemv_rows_grp(const GrpSet gs, const float* __restrict__ x,
+                                                      const float* __restrict__ xo, int N, int G, int S, int WR,
+                                                      int KW) {
     constexpr int R = 4, SPW = 2, NA = 2;
+    int seg = 0;
+#pragma unroll
+    for (int i = 1; i < kGrpSegs; i++)
+        if (i < gs.n && (int)blockIdx.x >= gs.b0[i]) seg = i;
+    const uint8_t* __restrict__ W = gs.W[seg];
+    const uint16_t* __restrict__ sg = gs.sg[seg];
+    const float* __restrict__ ia = gs.ia[seg];
+    const uint16_t* __restrict__ oi = gs.oi[seg];
+    const uint16_t* __restrict__ ov = gs.ov[seg];
+    float* __restrict__ y = gs.y[seg];
+    const int M = gs.M[seg], K_out = gs.K_out[seg];
+    const int bid = (int)blockIdx.x - gs.b0[seg];
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ float red[kMaxWaves];
     __shared__ float part[kMaxWaves][R];
@@ -484,7 +512,7 @@ __global__ __launch_bounds__(1024) void gemv_rows_grp(const uint8_t* __restrict_
     const int wave = threadIdx.x >> 6;
     const int wr = wave / KW, wk = wave - wr * KW;
     const int RB = WR * R;
-    const int row0 = blockIdx.x * RB + wr * R;
+    const int row0 = bid * RB + wr * R;
     const int rb = N >> 1;
     const int ng = N / G, gq = G >> 7;
     const int nth = blockDim.x;
@@ -678,7 +706,7 @@ __global__ __launch_bounds__(1024) void gemv_rows_grp(const uint8_t* __restrict_
         const int t = threadIdx.x;
         if (t < RB) {
             const int w_r = t / R, r = t - w_r * R;
-            const int row = blockIdx.x * RB + t;
+            const int row = bid * RB + t;
             if (row < M) {
                 float v = 0.f;
                 for (int k = 0; k < KW; k++) v += part[w_r * KW + k][r];
@@ -786,28 +814,51 @@ int ibh_launch_rows_x(float* out, const void* w, const void* scales, int kind, c
 // (inv_act applied in-kernel when awq); xo/ia: what the outlier sidecar reads
 // (xk[j] = xo[j] * ia[j], or xo[j] when ia is NULL).  Returns 1 if launched,
 // 0 if the shape is not eligible.
-int ibh_launch_rows_grp(float* out, const uint8_t* q, const uint16_t* s, const float* x, bool awq, const float* xo,
-                        const float* ia, const uint16_t* oi, const uint16_t* ov, int M, int N, int G, int K_out,
-                        hipStream_t st) {
-    if (N % 32 != 0 || G % 128 != 0 || N % G != 0 || N > 131072 || ((uintptr_t)q & 15) || ((uintptr_t)x & 15) ||
-        (awq && ((uintptr_t)ia & 15)) || M <= 0)
+// One or more group-scaled INT4 matrices sharing x, N and G, one launch.
+// awq: x is multiplied by each matrix's inv_act (ia, then required);
+// otherwise ia (may be null) only scales the outlier reads of xo.  Returns 1 if launched, 0 if not
+// eligible (the caller then runs its own path).
+int ibh_launch_rows_grp_multi(const IbhGrpMat* m, int n, const float* x, bool awq, const float* xo, int N, int G,
+                              hipStream_t st) {
+    if (n < 1 || n > kGrpSegs || N % 32 != 0 || G % 128 != 0 || N % G != 0 || N > 131072 || ((uintptr_t)x & 15))
         return 0;
+    int Mtot = 0;
+    for (int i = 0; i < n; i++) {
+        if (((uintptr_t)m[i].q & 15) || (awq && (!m[i].ia || ((uintptr_t)m[i].ia & 15))) || m[i].M <= 0)
+            return 0;
+        Mtot += m[i].M;
+    }
     const int rb = N / 2;
     const int S = (rb + 1023) / 1024;
     constexpr int R = 4, SPW = 2;
     const int KW = (S + SPW - 1) / SPW;
     int WR = 8;
-    while (WR > 1 && (WR * KW > kMaxWaves || (M + WR * R - 1) / (WR * R) < 384)) WR >>= 1;
+    while (WR > 1 && (WR * KW > kMaxWaves || (Mtot + WR * R - 1) / (WR * R) < 384)) WR >>= 1;
     if (WR * KW > kMaxWaves) return 0;
-    // AWQ keeps x and inv_act slices in registers: at most 4 per thread
-    while (awq && (N / 4 + 64 * WR * KW - 1) / (64 * WR * KW) > 4 && 2 * WR * KW <= kMaxWaves) WR *= 2;
+    // x (and inv_act) slices live in registers: at most 8 per thread, 4 with AWQ
+    const int cap = awq ? 4 : 8;
+    while ((N / 4 + 64 * WR * KW - 1) / (64 * WR * KW) > cap && 2 * WR * KW <= kMaxWaves) WR *= 2;
     const int nthreads = 64 * WR * KW;
     const int nxq = (N / 4 + nthreads - 1) / nthreads;
-    if (nxq > (awq ? 4 : 8)) return 0;
+    if (nxq > cap) return 0;
     const size_t lds = (size_t)S * 2 * 3 * 64 * 16;
     if (lds > 64 * 1024) return 0;
-    const int blocks = (M + WR * R - 1) / (WR * R);
-#define IBH_RG(Q_, A_) gemv_rows_grp<Q_, A_><<<blocks, nthreads, lds, st>>>(q, s, x, ia, xo, oi, ov, out, M, N, G, K_out, S, WR, KW)
+    GrpSet gs{};
+    gs.n = n;
+    int blocks = 0;
+    for (int i = 0; i < n; i++) {
+        gs.b0[i] = blocks;
+        gs.W[i] = m[i].q;
+        gs.sg[i] = m[i].s;
+        gs.ia[i] = m[i].ia;
+        gs.oi[i] = m[i].oi;
+        gs.ov[i] = m[i].ov;
+        gs.y[i] = m[i].out;
+        gs.M[i] = m[i].M;
+        gs.K_out[i] = m[i].K_out;
+        blocks += (m[i].M + WR * R - 1) / (WR * R);
+    }
+#define IBH_RG(Q_, A_) gemv_rows_grp<Q_, A_><<<blocks, nthreads, lds, st>>>(gs, x, xo, N, G, S, WR, KW)
     if (awq) {
         if (nxq <= 1) IBH_RG(1, true); else if (nxq <= 2) IBH_RG(2, true); else IBH_RG(4, true);
     } else {
@@ -816,4 +867,11 @@ int ibh_launch_rows_grp(float* out, const uint8_t* q, const uint16_t* s, const f
     }
 #undef IBH_RG
     return 1;
+}
+
+int ibh_launch_rows_grp(float* out, const uint8_t* q, const uint16_t* s, const float* x, bool awq, const float* xo,
+                        const float* ia, const uint16_t* oi, const uint16_t* ov, int M, int N, int G, int K_out,
+                        hipStream_t st) {
+    const IbhGrpMat m{q, s, ia, oi, ov, out, M, K_out};
+    return ibh_launch_rows_grp_multi(&m, 1, x, awq, xo, N, G, st);
 }

@@ -43,6 +43,9 @@ int ibh_launch_attn(float* out, const float* q, const void* kdata, const void* v
                     const float* vscales, int pos, const int* dpos, int max_pos, int n_heads, int n_kv,
                     int head_dim, int kv_bits, void* ws, size_t ws_bytes, hipStream_t st);
 
+int ibh_int4g_matmul_group(const ibh_int4g_tensor* const* t, float* const* out, int n, const float* x, float rel,
+                           hipStream_t st);
+
 namespace {
 
 enum { RAW_F32 = 0, RAW_F16, RAW_I32, RAW_I16, RAW_I8, RAW_U8, RAW_U16 };
@@ -131,7 +134,8 @@ __global__ void pq_row_kernel(float* __restrict__ out, ibh_pq_tensor t, const in
 // One block; the squares are summed in double like the reference.
 __global__ __launch_bounds__(kNormThreads) void v5_rmsnorm_kernel(float* __restrict__ out, float* __restrict__ x,
                                                                   const float* __restrict__ delta,
-                                                                  const float* __restrict__ w, float eps, int n) {
+                                                                  const float* __restrict__ w, float eps, int n,
+                                                                  int* __restrict__ bump) {
     __shared__ double red[kNormThreads / 64];
     float v[kNormMaxPer];
     double ss = 0.0;
@@ -161,6 +165,7 @@ __global__ __launch_bounds__(kNormThreads) void v5_rmsnorm_kernel(float* __restr
         const int i = threadIdx.x + j * kNormThreads;
         if (i < n) out[i] = v[j] * inv * w[i];
     }
+    if (bump && threadIdx.x == 0) *bump += 1;   // end of a step: position + 1
 }
 
 // ib_rope_f32 (NEOX halves, src/pq_decode.c:4623-4642) of the query heads in
@@ -189,6 +194,205 @@ __global__ void v5_rope_kv_kernel(float* __restrict__ q, const float* __restrict
     }
 }
 
+// Decode attention of one position with the rope and the cache write fused
+// in (ib_rope_f32 + the fp32 cache write + the per-head loop of
+// forward_step_internal_sc, src/pq_decode.c:4623-4642, 5011-5251).
+// Grid (kv head, split): split sp owns positions [64 sp, 64 sp + 64) of
+// T = pos + 1 (splits past T exit at once).  Each block rotates its GRP
+// query heads into LDS; the block owning pos rotates the new key, writes key
+// and value rows to the cache and uses them from LDS.  Scores: wavefront w
+// takes the heads g = w mod 4, lane = position; softmax pieces per head in
+// that wavefront.  Value sums: lane = dimension, wavefront w the positions
+// = w mod 4, all heads, then the four wavefronts add up in LDS.  The split's
+// max / exp-sum / value sums go to `part`; the last active block of a kv
+// head to arrive merges the splits (log-sum-exp) into out and re-arms the
+// counter for the next call.  With one active split the block normalises
+// directly.  Exponentials use the hardware exp2 (__expf, a few ulp): the
+// softmax only needs fp32 accuracy here.
+constexpr int kAttnThreads = 256;
+constexpr int kAttnPos = 64;   // positions per split
+
+template <int HD, int GRP>
+__global__ __launch_bounds__(kAttnThreads) void v5_attn_kernel(
+    float* __restrict__ out, const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    float* __restrict__ kc, float* __restrict__ vc, const float* __restrict__ cs, const int* __restrict__ dpos,
+    int n_kv, int NS, float scale, float* __restrict__ part, int* __restrict__ counter) {
+    constexpr int HALF = HD / 2, NW = kAttnThreads / 64, DPL = HD / 64, PPW = kAttnPos / NW;
+    constexpr int KPRE = HD == 64 ? HD / 4 : 1;   // key row held in registers (head_dim 64)
+    __shared__ __align__(16) float qs[GRP][HD];
+    __shared__ __align__(16) float kcur[HD], vcur[HD];
+    __shared__ float pr[GRP][kAttnPos];
+    __shared__ float gmax[GRP], gsum[GRP];
+    __shared__ float vred[NW][GRP][HD];
+    __shared__ int last;
+    const int kvh = blockIdx.x, sp = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int pos = *dpos, T = pos + 1;
+    const int t0 = sp * kAttnPos, t1 = min(T, t0 + kAttnPos);
+    if (t0 >= t1) return;                       // split past T: nothing to do
+    const int nact = (T + kAttnPos - 1) / kAttnPos, np = t1 - t0;
+    const int kv_dim = n_kv * HD;
+    const size_t hoff = (size_t)kvh * HD;
+    // cache reads first (their latency overlaps the rope below): this
+    // lane's key row and this wavefront's value elements
+    const int t = t0 + lane;
+    const bool act = t < t1;
+    float4 kreg[KPRE];
+    if constexpr (HD == 64) {
+        if (act && t != pos) {
+            const float4* kr = (const float4*)(kc + (size_t)t * kv_dim + hoff);
+#pragma unroll
+            for (int i = 0; i < KPRE; i++) kreg[i] = kr[i];
+        }
+    }
+    float vpre[PPW][DPL];
+#pragma unroll
+    for (int j = 0; j < PPW; j++) {
+        const int tt = t0 + wave + NW * j;
+#pragma unroll
+        for (int jj = 0; jj < DPL; jj++)
+            vpre[j][jj] = (tt < t1 && tt != pos) ? vc[(size_t)tt * kv_dim + hoff + lane + 64 * jj] : 0.f;
+    }
+    const float* csp = cs + (size_t)pos * HD;
+    for (int e = tid; e < GRP * HALF; e += kAttnThreads) {
+        const int g = e / HALF, i = e - g * HALF;
+        const float* qh = q + (size_t)(kvh * GRP + g) * HD;
+        const float c = csp[2 * i], sn = csp[2 * i + 1], a = qh[i], b = qh[i + HALF];
+        qs[g][i] = a * c - b * sn;
+        qs[g][i + HALF] = b * c + a * sn;
+    }
+    if (t0 <= pos && pos < t1) {
+        const float* kh = k + hoff;
+        const float* vh = v + hoff;
+        float* krow = kc + (size_t)pos * kv_dim + hoff;
+        float* vrow = vc + (size_t)pos * kv_dim + hoff;
+        for (int i = tid; i < HALF; i += kAttnThreads) {
+            const float c = csp[2 * i], sn = csp[2 * i + 1], a = kh[i], b = kh[i + HALF];
+            const float r0 = a * c - b * sn, r1 = b * c + a * sn;
+            kcur[i] = r0;
+            kcur[i + HALF] = r1;
+            krow[i] = r0;
+            krow[i + HALF] = r1;
+        }
+        for (int i = tid; i < HD; i += kAttnThreads) {
+            vcur[i] = vh[i];
+            vrow[i] = vh[i];
+        }
+    }
+    __syncthreads();
+    // scores: lane = position, wavefront = heads w, w + 4, ...
+    if (wave < GRP) {
+        constexpr int HPW = (GRP + NW - 1) / NW;
+        float sc[HPW];
+#pragma unroll
+        for (int h = 0; h < HPW; h++) sc[h] = 0.f;
+        if (act) {
+            const float* kr = t == pos ? kcur : kc + (size_t)t * kv_dim + hoff;
+#pragma unroll
+            for (int d = 0; d < HD; d += 4) {
+                float4 kk;
+                if constexpr (HD == 64) kk = t == pos ? *(const float4*)(kcur + d) : kreg[d / 4];
+                else kk = *(const float4*)(kr + d);
+#pragma unroll
+                for (int h = 0; h < HPW; h++) {
+                    const int g = wave + NW * h;
+                    if (g < GRP) {
+                        const float4 qq = *(const float4*)(&qs[g][d]);
+                        sc[h] = fmaf(qq.x, kk.x, sc[h]);
+                        sc[h] = fmaf(qq.y, kk.y, sc[h]);
+                        sc[h] = fmaf(qq.z, kk.z, sc[h]);
+                        sc[h] = fmaf(qq.w, kk.w, sc[h]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < HPW; h++) {
+            const int g = wave + NW * h;
+            if (g < GRP) {
+                const float x = act ? sc[h] * scale : -INFINITY;
+                const float m = wave_max(x);
+                const float p = act ? __expf(x - m) : 0.f;
+                pr[g][lane] = p;
+                const float sm = wave_sum(p);
+                if (lane == 0) {
+                    gmax[g] = m;
+                    gsum[g] = sm;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    // value sums: lane = dimension(s), wavefront w = positions w, w + 4, ...
+    float acc[GRP][DPL];
+#pragma unroll
+    for (int g = 0; g < GRP; g++)
+#pragma unroll
+        for (int jj = 0; jj < DPL; jj++) acc[g][jj] = 0.f;
+#pragma unroll
+    for (int j = 0; j < PPW; j++) {
+        const int pi = wave + NW * j;
+        if (pi < np) {
+            float vv[DPL];
+#pragma unroll
+            for (int jj = 0; jj < DPL; jj++) vv[jj] = t0 + pi == pos ? vcur[lane + 64 * jj] : vpre[j][jj];
+#pragma unroll
+            for (int g = 0; g < GRP; g++) {
+                const float p = pr[g][pi];
+#pragma unroll
+                for (int jj = 0; jj < DPL; jj++) acc[g][jj] = fmaf(p, vv[jj], acc[g][jj]);
+            }
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < GRP; g++)
+#pragma unroll
+        for (int jj = 0; jj < DPL; jj++) vred[wave][g][lane + 64 * jj] = acc[g][jj];
+    __syncthreads();
+    if (nact == 1) {   // one split: normalise here
+        for (int e = tid; e < GRP * HD; e += kAttnThreads) {
+            const int g = e / HD, d = e - g * HD;
+            float a = 0.f;
+#pragma unroll
+            for (int w = 0; w < NW; w++) a += vred[w][g][d];
+            out[(size_t)(kvh * GRP + g) * HD + d] = a / gsum[g];
+        }
+        return;
+    }
+    float* pp = part + ((size_t)kvh * NS + sp) * GRP * (HD + 2);
+    for (int e = tid; e < GRP * HD; e += kAttnThreads) {
+        const int g = e / HD, d = e - g * HD;
+        float a = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) a += vred[w][g][d];
+        pp[g * (HD + 2) + 2 + d] = a;
+    }
+    if (tid < GRP) {
+        pp[tid * (HD + 2)] = gmax[tid];
+        pp[tid * (HD + 2) + 1] = gsum[tid];
+    }
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) last = atomicAdd(&counter[kvh], 1) == nact - 1;
+    __syncthreads();
+    if (!last) return;
+    __threadfence();   // acquire: the other splits' partials are visible to plain loads
+    const float* pk = part + (size_t)kvh * NS * GRP * (HD + 2);
+    for (int e = tid; e < GRP * HD; e += kAttnThreads) {
+        const int g = e / HD, d = e - g * HD;
+        float M = -INFINITY;
+        for (int s2 = 0; s2 < nact; s2++) M = fmaxf(M, pk[((size_t)s2 * GRP + g) * (HD + 2)]);
+        float L = 0.f, A = 0.f;
+        for (int s2 = 0; s2 < nact; s2++) {
+            const float* ps = pk + ((size_t)s2 * GRP + g) * (HD + 2);
+            const float w = __expf(ps[0] - M);
+            L = fmaf(ps[1], w, L);
+            A = fmaf(ps[2 + d], w, A);
+        }
+        out[(size_t)(kvh * GRP + g) * HD + d] = A / L;
+    }
+    if (tid == 0) counter[kvh] = 0;
+}
+
 // ib_silu_gate_f32 (src/pq_decode.c:4610-4616).
 __global__ void v5_silu_kernel(float* __restrict__ out, const float* __restrict__ gate, const float* __restrict__ up,
                                int n) {
@@ -197,9 +401,6 @@ __global__ void v5_silu_kernel(float* __restrict__ out, const float* __restrict_
     const float g = gate[i];
     out[i] = g / (1.0f + ib_expf(-g)) * up[i];
 }
-
-// End of a step: position + 1.
-__global__ void v5_bump_kernel(int* __restrict__ dpos) { *dpos += 1; }
 
 // Greedy pick from the sorted top-K head: out[g] = tokens[pos] = ids[0], g + 1.
 __global__ void v5_advance_kernel(const int32_t* __restrict__ ids, int* __restrict__ tokens,
@@ -273,6 +474,7 @@ struct ibh_v5_session {
     void* ws = nullptr;
     size_t ws_bytes = 0;
     unsigned epoch = 1;   // bumped by policy changes: captured steps are stale
+    bool no_group = false;   // IBH_V5_NO_GROUP=1: one launch per matrix
 };
 
 struct ibh_v5_kv {
@@ -284,6 +486,9 @@ struct ibh_v5_kv {
     int* state = nullptr;    // device: [0] position, [1] generated count
     int* tokens = nullptr;   // device: token at each position [max_seq]
     int* outs = nullptr;     // device: generated tokens [max_seq + 1]
+    int ns = 0;              // fused attention: splits per kv head (0 = split-K kernels of ibh_attn)
+    float* apart = nullptr;  // fused attention: split partials [n_kv][ns][group][head_dim + 2]
+    int* acnt = nullptr;     // fused attention: per kv head arrival counters (re-armed by the kernel)
     // captured steps (they bake this cache's and the session's pointers and
     // the policies at capture time): to hidden, to logits, greedy step
     hipGraphExec_t g_hidden = nullptr, g_logits = nullptr, g_gen = nullptr, g_pick = nullptr;
@@ -568,6 +773,7 @@ int open_session(ibh_v5_session* s, const char* path) {
     }
     s->act_sparse_rel = 0.f;
     if (const char* e = getenv("IB_ACT_SPARSE_REL")) s->act_sparse_rel = (float)atof(e);
+    if (const char* e = getenv("IBH_V5_NO_GROUP")) s->no_group = atoi(e) > 0;
 
     // the data region, streamed to HBM in 64 MiB pieces
     s->arena_bytes = fsize - wds;
@@ -800,6 +1006,53 @@ int matmul(ibh_v5_session* s, int mi, const float* x, float* out) {
     return ibh_pq_matmul_policy(&m.pq, xk, out, &p, s->ws, s->ws_bytes, s->st);
 }
 
+constexpr int kAttnMaxSplits = 1024;
+
+bool attn_fused_ok(const ibh_v5_session* s, int max_seq) {
+    const int grp = s->n_heads / s->n_kv;
+    return (s->head_dim == 64 || s->head_dim == 128) && (grp == 1 || grp == 2 || grp == 4 || grp == 8) &&
+           (max_seq + kAttnPos - 1) / kAttnPos <= kAttnMaxSplits && !getenv("IBH_V5_SPLIT_ATTN");
+}
+
+int launch_attn_fused(ibh_v5_session* s, ibh_v5_kv* kv, const float* q, const float* k, const float* v, float* kc,
+                      float* vc) {
+    const int grp = s->n_heads / s->n_kv;
+    const float scale = 1.0f / sqrtf((float)s->head_dim);
+    const dim3 grid(s->n_kv, kv->ns);
+#define IBH_VA(H_, G_) v5_attn_kernel<H_, G_><<<grid, kAttnThreads, 0, s->st>>>(s->xb2, q, k, v, kc, vc, kv->rope, \
+        kv->state, s->n_kv, kv->ns, scale, kv->apart, kv->acnt)
+#define IBH_VAG(H_) do { if (grp == 1) IBH_VA(H_, 1); else if (grp == 2) IBH_VA(H_, 2); \
+                         else if (grp == 4) IBH_VA(H_, 4); else IBH_VA(H_, 8); } while (0)
+    if (s->head_dim == 64) IBH_VAG(64); else IBH_VAG(128);
+#undef IBH_VAG
+#undef IBH_VA
+    IBH_CHECK_LAUNCH("ibh_v5: attention");
+    return IBH_OK;
+}
+
+// Matrices that read the same x (q/k/v, gate/up): one launch when they are
+// all INT4 and the matrix-core kernel takes them, else one by one.
+int matmul_set(ibh_v5_session* s, const int* mi, float* const* out, int n, const float* x) {
+    const ibh_int4g_tensor* t[3];
+    bool all4 = true;
+    for (int i = 0; i < n; i++) {
+        all4 = all4 && s->mats[mi[i]].kind == MAT_INT4;
+        t[i] = &s->mats[mi[i]].i4;
+    }
+    if (all4 && !s->no_group) {
+        const int r = ibh_int4g_matmul_group(t, out, n, x, s->act_sparse_rel, s->st);
+        if (r < 0) {
+            ibh_set_error("ibh_v5: grouped INT4 launch failed");
+            return IBH_ERROR_INTERNAL;
+        }
+        if (r == 1) return IBH_OK;
+    }
+    int rc;
+    for (int i = 0; i < n; i++)
+        if ((rc = matmul(s, mi[i], x, out[i]))) return rc;
+    return IBH_OK;
+}
+
 // forward_step_internal_sc for tokens[*pos] at *pos: ends with the
 // post-final-norm hidden state in s->xb and, when want_logits, the logits in
 // s->logits; then *pos + 1.  Every launch reads the position from device
@@ -819,7 +1072,7 @@ int forward_dev(ibh_v5_session* s, ibh_v5_kv* kv, bool want_logits) {
     int rc;
     const float* pending = nullptr;   // residual not yet added into x
     for (int l = 0; l < s->n_layers; l++) {
-        v5_rmsnorm_kernel<<<1, kNormThreads, 0, s->st>>>(s->xb, s->x, pending, s->w_in[l], s->eps, H);
+        v5_rmsnorm_kernel<<<1, kNormThreads, 0, s->st>>>(s->xb, s->x, pending, s->w_in[l], s->eps, H, nullptr);
         IBH_CHECK_LAUNCH("ibh_v5: rmsnorm");
         float *q = s->q, *k = s->kn, *v = s->vn;
         if (s->fused_qkv) {
@@ -827,38 +1080,43 @@ int forward_dev(ibh_v5_session* s, ibh_v5_kv* kv, bool want_logits) {
             q = s->qkv;
             k = s->qkv + H;
             v = s->qkv + H + KV;
-        } else if ((rc = matmul(s, s->mq[l], s->xb, q)) || (rc = matmul(s, s->mk[l], s->xb, k)) ||
-                   (rc = matmul(s, s->mv[l], s->xb, v))) {
-            return rc;
+        } else {
+            const int mi[3] = {s->mq[l], s->mk[l], s->mv[l]};
+            float* const o[3] = {q, k, v};
+            if ((rc = matmul_set(s, mi, o, 3, s->xb))) return rc;
         }
         const size_t lbase = (size_t)l * kv->max_seq * KV;
-        v5_rope_kv_kernel<<<s->n_heads + 2 * s->n_kv, 64, 0, s->st>>>(q, k, v, kv->k + lbase, kv->v + lbase,
-                                                                       kv->rope, dpos, s->n_heads, s->n_kv, hd);
-        IBH_CHECK_LAUNCH("ibh_v5: rope + kv write");
-        if ((rc = ibh_launch_attn(s->xb2, q, kv->k + lbase, kv->v + lbase, nullptr, nullptr, 0, dpos,
-                                  kv->max_seq - 1, s->n_heads, s->n_kv, hd, 32, kv->aws, kv->aws_bytes, s->st)))
-            return rc;
+        if (kv->ns > 0) {
+            if ((rc = launch_attn_fused(s, kv, q, k, v, kv->k + lbase, kv->v + lbase))) return rc;
+        } else {
+            v5_rope_kv_kernel<<<s->n_heads + 2 * s->n_kv, 64, 0, s->st>>>(q, k, v, kv->k + lbase, kv->v + lbase,
+                                                                           kv->rope, dpos, s->n_heads, s->n_kv, hd);
+            IBH_CHECK_LAUNCH("ibh_v5: rope + kv write");
+            if ((rc = ibh_launch_attn(s->xb2, q, kv->k + lbase, kv->v + lbase, nullptr, nullptr, 0, dpos,
+                                      kv->max_seq - 1, s->n_heads, s->n_kv, hd, 32, kv->aws, kv->aws_bytes, s->st)))
+                return rc;
+        }
         if ((rc = matmul(s, s->mo[l], s->xb2, s->delta))) return rc;
-        v5_rmsnorm_kernel<<<1, kNormThreads, 0, s->st>>>(s->xb, s->x, s->delta, s->w_pn[l], s->eps, H);
+        v5_rmsnorm_kernel<<<1, kNormThreads, 0, s->st>>>(s->xb, s->x, s->delta, s->w_pn[l], s->eps, H, nullptr);
         IBH_CHECK_LAUNCH("ibh_v5: rmsnorm");
         float *g = s->gate, *u = s->up;
         if (s->fused_gu) {
             if ((rc = matmul(s, s->mgu[l], s->xb, s->gu))) return rc;
             g = s->gu;
             u = s->gu + I;
-        } else if ((rc = matmul(s, s->mg[l], s->xb, g)) || (rc = matmul(s, s->mu[l], s->xb, u))) {
-            return rc;
+        } else {
+            const int mi[2] = {s->mg[l], s->mu[l]};
+            float* const o[2] = {g, u};
+            if ((rc = matmul_set(s, mi, o, 2, s->xb))) return rc;
         }
         v5_silu_kernel<<<(I + 255) / 256, 256, 0, s->st>>>(s->gate, g, u, I);
         IBH_CHECK_LAUNCH("ibh_v5: silu");
         if ((rc = matmul(s, s->md[l], s->gate, s->delta))) return rc;
         pending = s->delta;
     }
-    v5_rmsnorm_kernel<<<1, kNormThreads, 0, s->st>>>(s->xb, s->x, pending, s->w_final, s->eps, H);
+    v5_rmsnorm_kernel<<<1, kNormThreads, 0, s->st>>>(s->xb, s->x, pending, s->w_final, s->eps, H, dpos);
     IBH_CHECK_LAUNCH("ibh_v5: final rmsnorm");
     if (want_logits && (rc = matmul(s, s->m_head, s->xb, s->logits))) return rc;
-    v5_bump_kernel<<<1, 1, 0, s->st>>>(dpos);
-    IBH_CHECK_LAUNCH("ibh_v5: position");
     return IBH_OK;
 }
 
@@ -1044,6 +1302,12 @@ extern "C" int ibh_v5_kv_create(ibh_v5_session* s, int max_seq, ibh_v5_kv** out)
               hipMalloc(&kv->aws, kv->aws_bytes) == hipSuccess && hipMalloc((void**)&kv->state, 16) == hipSuccess &&
               hipMalloc((void**)&kv->tokens, (size_t)max_seq * 4 + 4) == hipSuccess &&
               hipMalloc((void**)&kv->outs, (size_t)max_seq * 4 + 8) == hipSuccess;
+    if (ok && attn_fused_ok(s, max_seq)) {
+        kv->ns = (max_seq + kAttnPos - 1) / kAttnPos;
+        const size_t pb = (size_t)s->n_kv * kv->ns * (s->n_heads / s->n_kv) * (s->head_dim + 2) * 4;
+        ok = hipMalloc((void**)&kv->apart, pb) == hipSuccess && hipMalloc((void**)&kv->acnt, 4 * s->n_kv) == hipSuccess &&
+             hipMemset(kv->acnt, 0, 4 * s->n_kv) == hipSuccess;
+    }
     if (ok) {
         // ib_rope_f32's angles (src/pq_decode.c:4631-4634), host libm
         std::vector<float> tab((size_t)max_seq * half * 2);
@@ -1071,7 +1335,7 @@ extern "C" void ibh_v5_kv_free(ibh_v5_kv* kv) {
     if (kv->s && kv->s->st) hipStreamSynchronize(kv->s->st);
     drop_graphs(kv);
     for (void* p : {(void*)kv->k, (void*)kv->v, (void*)kv->rope, kv->aws, (void*)kv->state, (void*)kv->tokens,
-                    (void*)kv->outs})
+                    (void*)kv->outs, (void*)kv->apart, (void*)kv->acnt})
         if (p) hipFree(p);
     delete kv;
 }

@@ -8,12 +8,22 @@
  *                   argmax of ib_pq_forward_step's logits;
  *     MODE greedy : ib_pq_generate_greedy (batched prefill, top-8 PQ head).
  *   $REF_V5_POLICY="variant,skip,act" sets the session default policy.
- * Prints one JSON line with the generated tokens. */
+ *   $IB_PQ_THREADS is the reference's own thread-pool switch.
+ * Prints one JSON line with the generated tokens and, for greedy, the wall
+ * seconds of a prefill-only call (max_new 0) and of the full call. */
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
+#include <time.h>
+
 #include "pq_decode.h"
+
+static double now_s(void) {
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
+}
 
 static void* slurp(const char* path, size_t* n) {
     FILE* f = fopen(path, "rb");
@@ -50,11 +60,21 @@ int main(int argc, char** argv) {
     if (ib_pq_session_tensor_shape(s, "lm_head", &vocab, &hidden) != 0) { fprintf(stderr, "no lm_head\n"); return 1; }
     int* out = (int*)calloc((size_t)n_new + 1, sizeof(int));
     int n_out = 0;
+    double t_pre = 0, t_all = 0;
     if (!strcmp(argv[5], "greedy")) {
+        double t0 = now_s();
+        if (ib_pq_generate_greedy(s, kv, prompt, np, 0, -1, out, &n_out, NULL, NULL) != 0) {
+            fprintf(stderr, "generate failed\n");
+            return 1;
+        }
+        t_pre = now_s() - t0;
+        ib_pq_kv_cache_clear(kv);
+        t0 = now_s();
         if (ib_pq_generate_greedy(s, kv, prompt, np, n_new, -1, out, &n_out, NULL, NULL) != 0) {
             fprintf(stderr, "generate failed\n");
             return 1;
         }
+        t_all = now_s() - t0;
     } else {
         float* lg = (float*)malloc((size_t)vocab * (size_t)(np > 0 ? np : 1) * sizeof(float));
         for (int i = 0; i < np; i++)
@@ -76,6 +96,6 @@ int main(int argc, char** argv) {
     }
     printf("{\"tokens\": [");
     for (int i = 0; i < n_out; i++) printf("%s%d", i ? ", " : "", out[i]);
-    printf("]}\n");
+    printf("], \"prefill_seconds\": %.6f, \"seconds\": %.6f}\n", t_pre, t_all);
     return 0;
 }

@@ -45,10 +45,11 @@ def test_int4g_golden(ops, name):
 
 # (M, N, G, AWQ, outliers per row): Mistral/TinyLlama projection shapes on the
 # matrix-core path (N = 5632 ends inside a 1 KiB step), the any-G fallback
-# (G = 32, 64) and a row too long for the LDS digit planes (N = 24576).
+# (G = 32, 64), a row too long for the LDS digit planes (N = 24576) and
+# rows wide enough that a plain launch needs more waves per row (N = 5632).
 SHAPES = [(14336, 4096, 128, 1, 4), (4096, 14336, 128, 1, 0), (2048, 5632, 128, 1, 2), (5632, 2048, 128, 0, 0),
           (1024, 4096, 256, 1, 3), (512, 20480, 128, 0, 1), (300, 4096, 64, 1, 3), (77, 2048, 32, 0, 0),
-          (64, 24576, 128, 1, 2), (3, 96, 32, 1, 1)]
+          (64, 24576, 128, 1, 2), (3, 96, 32, 1, 1), (2048, 5632, 128, 0, 0), (256, 5632, 128, 0, 3)]
 
 
 @pytest.mark.parametrize("M,N,G,awq,K", SHAPES)

@@ -201,3 +201,52 @@ def test_policy_change_recaptures(L, tmp_path_factory, tmp_path):
     r1, rl1 = ref_run(path, PROMPT, 3, "steps", tmp_path, policy=(1, 0.0, 0.0))
     assert t1 == r1 and relerr(l1[-1], rl1[-1]) <= TOL
     assert relerr(l1[-1], l0[-1]) > 1e-3      # the level-2 terms are gone
+
+
+def test_grouped_int4_launch_matches_single(L, tmp_path_factory, monkeypatch):
+    """q/k/v and gate/up run as one matrix-core launch per set; the per-row
+    arithmetic is that of one launch per matrix, so logits are bit-equal."""
+    from libinferbit_amd.session import PqSession
+    path = model(tmp_path_factory, "int4_awq_outl")
+    S = PqSession(path)
+    _, a = gpu_steps(S, PROMPT, 2)
+    monkeypatch.setenv("IBH_V5_NO_GROUP", "1")
+    S1 = PqSession(path)
+    _, b = gpu_steps(S1, PROMPT, 2)
+    np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("split_env", ["", "1"])
+def test_long_prompt_attention_splits(L, tmp_path_factory, tmp_path, monkeypatch, split_env):
+    """A 300-token prompt in a 600-position cache: the fused attention spreads
+    the positions over three splits merged in-kernel (and, with
+    IBH_V5_SPLIT_ATTN=1, the rope + split-K attention kernels run instead);
+    logits and tokens as the reference's."""
+    from libinferbit_amd.session import PqSession
+    if split_env:
+        monkeypatch.setenv("IBH_V5_SPLIT_ATTN", split_env)
+    path = model(tmp_path_factory, "fused")
+    prompt = [int(t) for t in np.random.default_rng(5).integers(0, CFG["vocab_size"], 300)]
+    rt, rl = ref_run(path, prompt, 6, "steps", tmp_path, max_seq=600)
+    S = PqSession(path)
+    gt, gl = gpu_steps(S, prompt, 6, max_seq=600)
+    errs = [relerr(gl[i], rl[i]) for i in (0, 1, 150, 255, 256, 299)]
+    assert max(errs) <= TOL, errs
+    assert gt == rt
+    rg, _ = ref_run(path, prompt, 12, "greedy", tmp_path, max_seq=600)
+    assert S.generate_greedy(S.kv_cache(600), prompt, 12).tolist() == rg
+
+
+@pytest.mark.parametrize("heads,kv_heads,hd", [(8, 1, 64), (4, 4, 128), (16, 4, 32)])
+def test_head_geometries(L, tmp_path_factory, tmp_path, heads, kv_heads, hd):
+    """Eight query heads per kv head, head_dim 128 without GQA, and
+    head_dim 32 (the rope + split-K attention kernels)."""
+    from libinferbit_amd.session import PqSession
+    cfg = dict(CFG, hidden_size=heads * hd, num_heads=heads, num_kv_heads=kv_heads, head_dim=hd)
+    path = model(tmp_path_factory, f"geo{heads}_{kv_heads}_{hd}", cfg=cfg, backend=dict(o_proj="pq"))
+    prompt = [int(t) for t in np.random.default_rng(heads).integers(0, CFG["vocab_size"], 40)]
+    rt, rl = ref_run(path, prompt, 5, "steps", tmp_path, max_seq=300)
+    S = PqSession(path)
+    gt, gl = gpu_steps(S, prompt, 5, max_seq=300)
+    assert max(relerr(gl[i], rl[i]) for i in range(len(prompt))) <= TOL
+    assert gt == rt
