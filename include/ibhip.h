@@ -289,6 +289,19 @@ int  ibh_v5_forward_step_to_hidden(ibh_v5_session* s, ibh_v5_kv* kv, int token_i
  * (>= 0) or a full cache.  Host arrays; lm_head must be PQ. */
 int  ibh_v5_generate_greedy(ibh_v5_session* s, ibh_v5_kv* kv, const int* prompt_ids, int n_prompt, int max_new,
                             int eos_token_id, int* out_ids, int* n_out);
+/* ib_pq_sample_params (src/pq_decode.h:499-504), same layout. */
+typedef struct {
+    float    temperature;   /* <= 0: argmax */
+    int      top_k;         /* 1..256: the top-K PQ head; otherwise full logits */
+    float    top_p;         /* (0, 1): nucleus prefix */
+    uint32_t seed;          /* 0: the reference's fixed default */
+} ibh_pq_sample_params;
+/* ib_pq_generate_sample (src/pq_decode.c:5480-5561): candidates from the
+ * device (top-K PQ head, or the full logits), the pick on the host with the
+ * reference's xorshift64 stream and softmax / top-p / inverse-CDF rule.
+ * Equal full-vocabulary logits are ordered by token id. */
+int  ibh_v5_generate_sample(ibh_v5_session* s, ibh_v5_kv* kv, const int* prompt_ids, int n_prompt, int max_new,
+                            int eos_token_id, const ibh_pq_sample_params* params, int* out_ids, int* n_out);
 
 /* ── device-resident decode (forward_single_ex + greedy generate) ── */
 

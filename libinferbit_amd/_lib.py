@@ -58,6 +58,7 @@ SIGNATURES = {
     "ibh_v5_forward_step": (I, [P, P, I, I, P]),
     "ibh_v5_forward_step_to_hidden": (I, [P, P, I, I, P]),
     "ibh_v5_generate_greedy": (I, [P, P, P, I, I, I, P, P]),
+    "ibh_v5_generate_sample": (I, [P, P, P, I, I, I, P, P, P]),
     "ibh_model_load": (I, [C.c_char_p, I, P]),
     "ibh_model_free": (None, [P]),
     "ibh_model_dims": (I, [P, P]),
@@ -131,6 +132,11 @@ class PqTensor(C.Structure):
                                  "indices_l1_l", "indices_l1_r", "indices_l2_l", "indices_l2_r", "row_scale",
                                  "outlier_cols", "outlier_sidecar", "outlier_scale", "inner_cols")] + \
                [("format", I)]
+
+
+class PqSampleParams(C.Structure):
+    """ib_pq_sample_params (src/pq_decode.h:499-504)."""
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_int), ("top_p", C.c_float), ("seed", C.c_uint32)]
 
 
 class PqPolicy(C.Structure):

@@ -981,7 +981,7 @@ int open_session(ibh_v5_session* s, const char* path) {
         if (m.kind == MAT_PQ) ws = std::max(ws, ibh_pq_workspace_bytes(&m.pq));
         if (m.kind == MAT_INT4) ws = std::max(ws, ibh_int4g_workspace_bytes(&m.i4));
     }
-    if (s->mats[s->m_head].kind == MAT_PQ) ws = std::max(ws, ibh_pq_topk_workspace_bytes(&s->mats[s->m_head].pq, 8));
+    if (s->mats[s->m_head].kind == MAT_PQ) ws = std::max(ws, ibh_pq_topk_workspace_bytes(&s->mats[s->m_head].pq, 256));
     s->ws_bytes = ws;
     if ((rc = salloc(s, &s->ws, ws))) return rc;
     IBH_HIP(hipStreamCreateWithFlags(&s->st, hipStreamNonBlocking), "ibh_v5_open: stream");
@@ -1444,5 +1444,55 @@ extern "C" int ibh_v5_generate_greedy(ibh_v5_session* s, ibh_v5_kv* kv, const in
     *n_out = total;
     // steps taken: every token before the one that stopped the loop
     kv->length = n_prompt + (found >= 0 ? found : n_step);
+    return IBH_OK;
+}
+
+// ── helpers of ibh_v5_generate_sample (ibh_v5_sample.cpp) ──────────────────
+int ibh_v5_vocab(const ibh_v5_session* s) { return s->vocab; }
+int ibh_v5_kv_capacity(const ibh_v5_kv* kv) { return kv->max_seq; }
+void ibh_v5_kv_set_length(ibh_v5_kv* kv, int n) { kv->length = n; }
+
+int ibh_v5_step_logits(ibh_v5_session* s, ibh_v5_kv* kv, int token, int pos, float* logits) {
+    return ibh_v5_forward_step(s, kv, token, pos, logits);
+}
+
+// first: the prompt through the cache; else one step on `token` at `pos`.
+// Then the top-k PQ head on the hidden state, copied to the host.
+int ibh_v5_step_hidden_topk(ibh_v5_session* s, ibh_v5_kv* kv, int first, const int* prompt, int n_prompt, int token,
+                            int pos, int k_top, float* top_logits, int32_t* top_ids) {
+    if (!s || !kv || kv->s != s) {
+        ibh_set_error("ibh_v5_generate_sample: invalid session or cache");
+        return IBH_ERROR_PARAM;
+    }
+    if (s->mats[s->m_head].kind != MAT_PQ) {
+        ibh_set_error("ibh_v5_generate_sample: top-K sampling needs a PQ lm_head");
+        return IBH_ERROR_FORMAT;
+    }
+    int rc;
+    if (first) {
+        for (int i = 0; i < n_prompt; i++)
+            if (prompt[i] < 0 || prompt[i] >= s->embed_rows) {
+                ibh_set_error("ibh_v5_generate_sample: prompt token %d out of range", prompt[i]);
+                return IBH_ERROR_PARAM;
+            }
+        const int st0[2] = {0, 0};
+        IBH_HIP(hipMemcpyAsync(kv->tokens, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice, s->st),
+                "ibh_v5_generate_sample: prompt");
+        IBH_HIP(hipMemcpyAsync(kv->state, st0, 8, hipMemcpyHostToDevice, s->st), "ibh_v5_generate_sample: state");
+        for (int i = 0; i < n_prompt; i++)
+            if ((rc = run_graph(s, kv, 0))) return rc;
+    } else {
+        if ((rc = check_token_pos(s, kv, token, pos, "ibh_v5_generate_sample")) ||
+            (rc = set_token_pos(s, kv, token, pos)) || (rc = run_graph(s, kv, 0)))
+            return rc;
+    }
+    if ((rc = ibh_pq_lm_head_topk(&s->mats[s->m_head].pq, s->xb, k_top, s->top_val, s->top_ids, s->ws, s->ws_bytes,
+                                  s->st)))
+        return rc;
+    IBH_HIP(hipMemcpyAsync(top_logits, s->top_val, (size_t)k_top * 4, hipMemcpyDeviceToHost, s->st),
+            "ibh_v5_generate_sample: logits");
+    IBH_HIP(hipMemcpyAsync(top_ids, s->top_ids, (size_t)k_top * 4, hipMemcpyDeviceToHost, s->st),
+            "ibh_v5_generate_sample: ids");
+    IBH_HIP(hipStreamSynchronize(s->st), "ibh_v5_generate_sample");
     return IBH_OK;
 }

@@ -10,7 +10,7 @@ import ctypes
 
 import numpy as np
 
-from ._lib import PqPolicy, check, lib
+from ._lib import PqPolicy, PqSampleParams, check, lib
 
 DIM_NAMES = ("num_layers", "hidden_size", "num_heads", "num_kv_heads", "head_dim", "intermediate_size",
              "vocab_size", "fused_qkv", "fused_gateup")
@@ -117,4 +117,15 @@ class PqSession:
         n = ctypes.c_int()
         check(lib().ibh_v5_generate_greedy(self._h, kv._h, _ptr(p), len(p), max_new, eos, _ptr(out),
                                            ctypes.byref(n)), "ibh_v5_generate_greedy")
+        return out[:n.value]
+
+    def generate_sample(self, kv: KvCache, prompt, max_new: int, temperature: float = 1.0, top_k: int = 40,
+                        top_p: float = 0.9, seed: int = 0, eos: int = -1) -> np.ndarray:
+        """ib_pq_generate_sample (src/pq_decode.c:5480-5561)."""
+        p = np.ascontiguousarray(prompt, np.int32)
+        out = np.empty(max(max_new, 1), np.int32)
+        n = ctypes.c_int()
+        sp = PqSampleParams(temperature, top_k, top_p, seed)
+        check(lib().ibh_v5_generate_sample(self._h, kv._h, _ptr(p), len(p), max_new, eos, ctypes.byref(sp),
+                                           _ptr(out), ctypes.byref(n)), "ibh_v5_generate_sample")
         return out[:n.value]

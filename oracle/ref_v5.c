@@ -6,7 +6,9 @@
  *     MODE steps  : ib_pq_forward_step over the prompt (logits of every
  *                   position to $REF_V5_LOGITS), then N_NEW greedy steps by
  *                   argmax of ib_pq_forward_step's logits;
- *     MODE greedy : ib_pq_generate_greedy (batched prefill, top-8 PQ head).
+ *     MODE greedy : ib_pq_generate_greedy (batched prefill, top-8 PQ head);
+ *     MODE sample : ib_pq_generate_sample with $REF_V5_SAMPLE =
+ *                   "temperature,top_k,top_p,seed".
  *   $REF_V5_POLICY="variant,skip,act" sets the session default policy.
  *   $IB_PQ_THREADS is the reference's own thread-pool switch.
  * Prints one JSON line with the generated tokens and, for greedy, the wall
@@ -72,6 +74,16 @@ int main(int argc, char** argv) {
         t0 = now_s();
         if (ib_pq_generate_greedy(s, kv, prompt, np, n_new, -1, out, &n_out, NULL, NULL) != 0) {
             fprintf(stderr, "generate failed\n");
+            return 1;
+        }
+        t_all = now_s() - t0;
+    } else if (!strcmp(argv[5], "sample")) {
+        ib_pq_sample_params sp;
+        const char* se = getenv("REF_V5_SAMPLE");
+        if (!se || sscanf(se, "%f,%d,%f,%u", &sp.temperature, &sp.top_k, &sp.top_p, &sp.seed) != 4) return 2;
+        double t0 = now_s();
+        if (ib_pq_generate_sample(s, kv, prompt, np, n_new, -1, sp, out, &n_out, NULL, NULL) != 0) {
+            fprintf(stderr, "generate_sample failed\n");
             return 1;
         }
         t_all = now_s() - t0;

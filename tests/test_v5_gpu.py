@@ -53,7 +53,7 @@ def model(tmp_path_factory, name, cfg=CFG, **over):
     return p
 
 
-def ref_run(path, prompt, n_new, mode, tmp, policy=None, max_seq=64):
+def ref_run(path, prompt, n_new, mode, tmp, policy=None, max_seq=64, sample=None):
     if not os.path.exists(REF_V5):
         pytest.skip("oracle/_ref/ref_v5 not built (make -C oracle ref)")
     pp, lp = str(tmp / "p.i32"), str(tmp / "lg.f32")
@@ -61,6 +61,8 @@ def ref_run(path, prompt, n_new, mode, tmp, policy=None, max_seq=64):
     env = dict(os.environ, REF_V5_LOGITS=lp)
     if policy is not None:
         env["REF_V5_POLICY"] = ",".join(str(v) for v in policy)
+    if sample is not None:
+        env["REF_V5_SAMPLE"] = ",".join(str(v) for v in sample)
     r = subprocess.run([REF_V5, path, str(max_seq), str(n_new), pp, mode], capture_output=True, text=True,
                        timeout=300, env=env)
     assert r.returncode == 0, r.stderr
@@ -250,3 +252,29 @@ def test_head_geometries(L, tmp_path_factory, tmp_path, heads, kv_heads, hd):
     gt, gl = gpu_steps(S, prompt, 5, max_seq=300)
     assert max(relerr(gl[i], rl[i]) for i in range(len(prompt))) <= TOL
     assert gt == rt
+
+
+SAMPLES = {
+    "topk40_p09": (0.8, 40, 0.9, 7),
+    "topk256_T1": (1.0, 256, 0.0, 123),
+    "topk8_T0": (0.0, 8, 0.9, 5),
+    "full_p09": (0.8, 0, 0.9, 7),
+    "full_T12": (1.2, 0, 0.0, 99),
+    "k300_full": (0.7, 300, 0.95, 0),
+}
+
+
+@pytest.mark.parametrize("name", list(SAMPLES))
+def test_generate_sample(L, tmp_path_factory, tmp_path, name):
+    """ib_pq_generate_sample: the top-K PQ head (0 < top_k <= 256) or the
+    full logits (top_k 0 or > 256), the reference's xorshift64 stream and
+    softmax / top-p / inverse-CDF pick; token streams equal."""
+    from libinferbit_amd.session import PqSession
+    T, k, p, seed = SAMPLES[name]
+    path = model(tmp_path_factory, "mixed")
+    rg, _ = ref_run(path, PROMPT, 24, "sample", tmp_path, sample=(T, k, p, seed))
+    S = PqSession(path)
+    kv = S.kv_cache(64)
+    got = S.generate_sample(kv, PROMPT, 24, temperature=T, top_k=k, top_p=p, seed=seed).tolist()
+    assert got == rg, (name, got, rg)
+    assert len(kv) == len(PROMPT) + 24
