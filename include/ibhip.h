@@ -195,6 +195,15 @@ int    ibh_pq_matmul_streaming(const ibh_pq_tensor* t, const float* x, float* ou
  * fp32 rounding of its threshold may go the other way.  Same workspace. */
 int    ibh_pq_matmul_policy(const ibh_pq_tensor* t, const float* x, float* out, const ibh_pq_policy* policy,
                             void* ws, size_t ws_bytes, void* stream);
+/* ib_pq_matmul_fp32_q8lut (src/pq_decode.c:2340-2561): every chunk's tables
+ * (the matmul_impl entry order) quantised to int8 with one scale per
+ * (chunk, side) -- max|T|/127, round half away, clamp [-128, 127] -- then
+ * the gather, the row scale and the outlier sidecar.  The quantised codes
+ * equal the reference's; the gather sums in another order.  G <= 32; a
+ * two-level tensor needs K_l2 == K with uint8 indices (the reference reads
+ * its level-2 tables that way).  Same workspace as ibh_pq_matmul. */
+int    ibh_pq_matmul_q8lut(const ibh_pq_tensor* t, const float* x, float* out, void* ws, size_t ws_bytes,
+                           void* stream);
 /* ib_pq_lm_head_topk (src/pq_decode.c:2259-2346; session entry 4493-4499):
  * level-1 logits of every row, the K_top largest, their full-pyramid logits
  * (ib_pq_matmul_fp32_subset, 2145-2250), sorted descending.  out_logits /

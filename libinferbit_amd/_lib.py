@@ -39,6 +39,7 @@ SIGNATURES = {
     "ibh_pq_matmul": (I, [P, P, P, P, SZ, P]),
     "ibh_pq_matmul_streaming": (I, [P, P, P, P, SZ, P]),
     "ibh_pq_matmul_policy": (I, [P, P, P, P, P, SZ, P]),
+    "ibh_pq_matmul_q8lut": (I, [P, P, P, P, SZ, P]),
     "ibh_pq_topk_workspace_bytes": (SZ, [P, I]),
     "ibh_pq_lm_head_topk": (I, [P, P, I, P, P, P, SZ, P]),
     "ibh_int4g_workspace_bytes": (SZ, [P]),

@@ -565,7 +565,42 @@ struct PqMode {
     bool q8 = false;
     bool l2skip = false;
     float l2_thr = 0.f;
+    bool tq8 = false;         // tables quantised to int8 per (chunk, side) (q8lut)
 };
+
+// ib_pq_matmul_fp32_q8lut's table quantisation (build_q8_lut,
+// pq_decode.c:2405-2449): per (chunk, side) of each level, sc = max|T|/127
+// (1 if 0), q = (int)(T * (1/sc) +- 0.5) clamped to [-128, 127]; the tables
+// are replaced by q * sc, the terms the reference's gather adds.  Block per
+// chunk, grid.y = level.
+__global__ __launch_bounds__(kThreads) void pq_tq8(float* __restrict__ tab1, float* __restrict__ tab2, int K) {
+    __shared__ float red[kThreads / 64];
+    __shared__ float s_sc;
+    float* tab = (blockIdx.y ? tab2 : tab1) + (size_t)blockIdx.x * 2 * K;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int side = 0; side < 2; side++) {
+        float* T = tab + side * K;
+        float m = 0.f;
+        for (int k = threadIdx.x; k < K; k += kThreads) m = fmaxf(m, fabsf(T[k]));
+        m = wave_max(m);
+        if (lane == 0) red[wave] = m;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float mm = 0.f;
+            for (int w = 0; w < kThreads / 64; w++) mm = fmaxf(mm, red[w]);
+            s_sc = mm > 0.f ? mm / 127.0f : 1.0f;
+        }
+        __syncthreads();
+        const float sc = s_sc, inv = 1.0f / sc;
+        for (int k = threadIdx.x; k < K; k += kThreads) {
+            const float u = T[k] * inv;
+            int q = (int)(u >= 0 ? u + 0.5f : u - 0.5f);
+            q = q > 127 ? 127 : (q < -128 ? -128 : q);
+            T[k] = (float)q * sc;
+        }
+        __syncthreads();
+    }
+}
 }  // namespace
 
 static int pq_run(const ibh_pq_tensor_abi* t, const float* x, float* out, void* ws, size_t ws_bytes, void* stream,
@@ -580,6 +615,23 @@ extern "C" int ibh_pq_matmul_streaming(const ibh_pq_tensor_abi* t, const float* 
                                        size_t ws_bytes, void* stream) {
     const ibh_pq_policy p{IBH_PQ_VARIANT_STREAMING, 0.f, 0.f};
     return ibh_pq_matmul_policy(t, x, out, &p, ws, ws_bytes, stream);
+}
+
+// ib_pq_matmul_fp32_q8lut (pq_decode.c:2451-2561): every chunk, tables in the
+// matmul_impl order quantised to int8 per (chunk, side), gather, row scale,
+// outliers.  Its level-2 tables hold K entries read through uint8 indices,
+// so a level-2 tensor must have K_l2 == K (not 16-packed, not 2-byte).
+extern "C" int ibh_pq_matmul_q8lut(const ibh_pq_tensor_abi* t, const float* x, float* out, void* ws,
+                                   size_t ws_bytes, void* stream) {
+    if (t && (t->G > 32 || (t->n_levels == 2 && ((t->K_l2 > 0 && t->K_l2 != t->K) || t->K == 16 ||
+                                                   t->l2_idx_bytes == 2)))) {
+        ibh_set_error("ibh_pq_matmul_q8lut: needs G <= 32 and, with two levels, K_l2 == K (uint8 indices)");
+        return IBH_ERROR_PARAM;
+    }
+    PqMode md;
+    md.skip_mode = 0;
+    md.tq8 = true;
+    return pq_run(t, x, out, ws, ws_bytes, stream, md, "ibh_pq_matmul_q8lut");
 }
 
 // ib_pq_session_matmul's dispatch on the tensor's policy (pq_decode.c:4468-4491).
@@ -682,6 +734,10 @@ static int pq_run(const ibh_pq_tensor_abi* t, const float* x, float* out, void* 
     if (two) pq_tables<true><<<t->C, kThreads, 0, st>>>(d, x, tab1, tab2, cmax, cnorm);
     else pq_tables<false><<<t->C, kThreads, 0, st>>>(d, x, tab1, tab2, cmax, cnorm);
     IBH_CHECK_LAUNCH("ibh_pq_matmul (tables)");
+    if (md.tq8) {
+        pq_tq8<<<dim3(t->C, two ? 2 : 1), kThreads, 0, st>>>(tab1, tab2, t->K);
+        IBH_CHECK_LAUNCH("ibh_pq_matmul (table quantisation)");
+    }
     dim3 grid((t->M + kRowsPerBlock - 1) / kRowsPerBlock, nslabs);
     if (two) pq_gather<true><<<grid, kThreads, lds, st>>>(d, tab1, tab2, cmax, part, CS);
     else pq_gather<false><<<grid, kThreads, lds, st>>>(d, tab1, tab2, cmax, part, CS);

@@ -810,14 +810,11 @@ int ibh_launch_rows_x(float* out, const void* w, const void* scales, int kind, c
     return ibh_launch_rows_x_multi(&d, 1, kind, x, N, bits, st);
 }
 
-// Group-scaled INT4 rows (gemv_rows_grp).  x: the activation to digitise
-// (inv_act applied in-kernel when awq); xo/ia: what the outlier sidecar reads
-// (xk[j] = xo[j] * ia[j], or xo[j] when ia is NULL).  Returns 1 if launched,
-// 0 if the shape is not eligible.
-// One or more group-scaled INT4 matrices sharing x, N and G, one launch.
-// awq: x is multiplied by each matrix's inv_act (ia, then required);
-// otherwise ia (may be null) only scales the outlier reads of xo.  Returns 1 if launched, 0 if not
-// eligible (the caller then runs its own path).
+// Group-scaled INT4 rows (gemv_rows_grp): one or more matrices sharing x, N
+// and G, one launch.  x: the activation to digitise; awq: x is multiplied by
+// each matrix's inv_act in-kernel (ia then required); xo/ia: what the
+// outlier sidecar reads (xk[j] = xo[j] * ia[j], or xo[j] when ia is NULL).
+// Returns 1 if launched, 0 if not eligible (the caller runs its own path).
 int ibh_launch_rows_grp_multi(const IbhGrpMat* m, int n, const float* x, bool awq, const float* xo, int N, int G,
                               hipStream_t st) {
     if (n < 1 || n > kGrpSegs || N % 32 != 0 || G % 128 != 0 || N % G != 0 || N > 131072 || ((uintptr_t)x & 15))

@@ -156,6 +156,11 @@ class PqDeviceTensor:
         check(lib().ibh_pq_matmul_policy(ctypes.byref(self.s), _ptr(x), _ptr(out), ctypes.byref(p), _ptr(self.ws),
                                          self.ws.numel(), _stream()), "ibh_pq_matmul_policy")
 
+    def matmul_q8lut(self, x, out) -> None:
+        """ib_pq_matmul_fp32_q8lut (src/pq_decode.c:2451-2561)."""
+        check(lib().ibh_pq_matmul_q8lut(ctypes.byref(self.s), _ptr(x), _ptr(out), _ptr(self.ws), self.ws.numel(),
+                                        _stream()), "ibh_pq_matmul_q8lut")
+
     def lm_head_topk(self, x, k_top: int):
         """ib_pq_lm_head_topk (src/pq_decode.c:2259-2346): (logits [k], ids [k]) on the GPU."""
         need = lib().ibh_pq_topk_workspace_bytes(ctypes.byref(self.s), k_top)

@@ -737,6 +737,66 @@ int or_pq_matmul_streaming(const or_pq_tensor* t, const float* x, float* out) {
     return 0;
 }
 
+/* ib_pq_matmul_fp32_q8lut (pq_decode.c:2340-2561): per chunk and side the
+ * K table entries sum_i cb[k][i] * x[inner col] as build_q8_lut's loop
+ * compiles on x86 (pq_dot: the first half&~3 products rounded and added in
+ * order, the rest fused; 2405-2417), quantised with sc = max|T|/127 (1 if
+ * 0), q = (int)(T * (1/sc) +- 0.5) clamped to [-128, 127] (2423-2445); the
+ * gather (pq_q8_gather_rows, 2367-2397) adds per chunk
+ * fma((float)qL, sL, (float)qR * sR) to the row accumulator (level 2 the
+ * same, as a second term), out = acc * row scale, then the outliers.
+ * Level 2 uses K-entry tables and uint8 indices [r * C + c]. */
+int or_pq_matmul_q8lut(const or_pq_tensor* t, const float* x, float* out) {
+    int M = t->M, G = t->G, C = t->C, K = t->K, hf = G / 2;
+    int two = t->n_levels == 2;
+    if (hf > 16) return -1;
+    int* ic = pq_inner_cols(t);
+    int8_t* q = (int8_t*)malloc((size_t)C * K * 2 * (two ? 2 : 1));
+    float* sc = (float*)malloc(sizeof(float) * (size_t)C * 2 * (two ? 2 : 1));
+    float* tmp = (float*)malloc(sizeof(float) * (size_t)K);
+    for (int lev = 0; lev < (two ? 2 : 1); lev++)
+        for (int side = 0; side < 2; side++) {
+            const uint16_t* cb = lev ? (side ? t->cb2r : t->cb2l) : (side ? t->cb1r : t->cb1l);
+            for (int c = 0; c < C; c++) {
+                float xs[16];
+                for (int i = 0; i < hf; i++) xs[i] = x[ic[c * G + side * hf + i]];
+                float mx = 0.0f;
+                for (int k = 0; k < K; k++) {
+                    tmp[k] = pq_dot(cb + (size_t)k * hf, xs, hf);
+                    float a = tmp[k] < 0 ? -tmp[k] : tmp[k];
+                    if (a > mx) mx = a;
+                }
+                float s = mx > 0.0f ? mx / 127.0f : 1.0f;
+                float inv = 1.0f / s;
+                sc[((size_t)lev * C + c) * 2 + side] = s;
+                for (int k = 0; k < K; k++) {
+                    float u = tmp[k] * inv;
+                    int v = (int)(u >= 0 ? u + 0.5f : u - 0.5f);
+                    v = v > 127 ? 127 : (v < -128 ? -128 : v);
+                    q[(((size_t)lev * C + c) * K + k) * 2 + side] = (int8_t)v;
+                }
+            }
+        }
+    for (int r = 0; r < M; r++) {
+        float acc = 0.0f;
+        for (int c = 0; c < C; c++) {
+            for (int lev = 0; lev < (two ? 2 : 1); lev++) {
+                const uint8_t* il = lev ? t->i2l : t->i1l;
+                const uint8_t* ir = lev ? t->i2r : t->i1r;
+                const int8_t* T = q + ((size_t)lev * C + c) * K * 2;
+                const float* S = sc + ((size_t)lev * C + c) * 2;
+                float ql = (float)T[(size_t)il[(size_t)r * C + c] * 2];
+                float qr = (float)T[(size_t)ir[(size_t)r * C + c] * 2 + 1];
+                acc = acc + fmaf(ql, S[0], qr * S[1]);
+            }
+        }
+        out[r] = acc * or_fp16_to_fp32(t->row_scale[r]);
+    }
+    pq_outliers(t, x, out);
+    free(ic); free(q); free(sc); free(tmp);
+    return 0;
+}
+
 /* pq_quantize_codebook_int8 / pq_quantize_chunk_int8 (pq_decode.c:2766-2791,
  * 2838-2856): scale = max|v|/127 (1 if 0), codes round half away from zero,
  * clamped to +-127. */

@@ -84,6 +84,7 @@ int or_pq_reconstruct(const or_pq_tensor* t, float* out);                /* pq_d
  * (pq_decode.c:2927-2985, tables by pq_chunk_dot_table_f32 169-254):
  * every chunk, no skipping.  G <= 32. */
 int or_pq_matmul_streaming(const or_pq_tensor* t, const float* x, float* out);
+int or_pq_matmul_q8lut(const or_pq_tensor* t, const float* x, float* out);
 /* The PQ session's policy variants (ib_pq_policy, pq_decode.h:331-343;
  * dispatch pq_decode.c:4468-4491): 0 STREAMING (streaming_cached), 1 L1_ONLY
  * (ib_pq_matmul_fp32_l1_only, 2085-2139), 2 L2SKIP (l2skip_cached,

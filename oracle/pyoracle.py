@@ -57,6 +57,7 @@ def _declare(L):
         "or_silu_mul": (None, [P, P, P, I]),
         "or_pq_matmul": (I, [P, P, P]),
         "or_pq_matmul_streaming": (I, [P, P, P]),
+        "or_pq_matmul_q8lut": (I, [P, P, P]),
         "or_pq_matmul_variant": (I, [P, P, P, I, C.c_float, C.c_float, I]),
         "or_pq_matmul_subset": (I, [P, P, P, I, P]),
         "or_pq_lm_head_topk": (I, [P, P, I, P, P]),
@@ -246,6 +247,15 @@ def pq_matmul_streaming(t: dict, x):
     x = _c(x, np.float32)
     out = np.zeros(t["M"], np.float32)
     assert lib().or_pq_matmul_streaming(C.byref(s), _p(x), _p(out)) == 0
+    return out
+
+
+def pq_matmul_q8lut(t: dict, x):
+    """ib_pq_matmul_fp32_q8lut (int8-quantised tables)."""
+    s, keep = _pq_struct(t)
+    x = _c(x, np.float32)
+    out = np.zeros(t["M"], np.float32)
+    assert lib().or_pq_matmul_q8lut(C.byref(s), _p(x), _p(out)) == 0
     return out
 
 

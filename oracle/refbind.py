@@ -83,6 +83,7 @@ def lib():
         _lib.ib_pq_lut_cache_free.restype = None
         _lib.ib_pq_matmul_fp32_streaming_cached.argtypes = [P, P, P, P]
         _lib.ib_pq_matmul_fp32_l1_only.argtypes = [P, P, P]
+        _lib.ib_pq_matmul_fp32_q8lut.argtypes = [P, P, P, P]
         _lib.ib_pq_matmul_fp32_streaming_sparse.argtypes = [P, P, P, C.c_float]
         _lib.ib_pq_matmul_fp32_streaming_l2skip_cached.argtypes = [P, P, P, P, C.c_float]
         _lib.ib_pq_lut_cache_quantize_int8.argtypes = [P]
@@ -204,6 +205,15 @@ def pq_matmul_streaming(t: dict, x):
         assert lib().ib_pq_matmul_fp32_streaming_cached(C.byref(s), cache, _p(x), _p(out)) == 0
     finally:
         lib().ib_pq_lut_cache_free(cache)
+    return out
+
+
+def pq_matmul_q8lut(t: dict, x):
+    """ib_pq_matmul_fp32_q8lut, single-threaded (src/pq_decode.c:2451-2561)."""
+    s, keep = _pq(t)
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.zeros(t["M"], np.float32)
+    assert lib().ib_pq_matmul_fp32_q8lut(C.byref(s), _p(x), _p(out), None) == 0
     return out
 
 

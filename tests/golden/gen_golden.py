@@ -19,6 +19,7 @@ Contents (every array is what the reference produced, except the inputs):
                streaming_sparse, streaming_int8_cached) on the pq.npz cases and
                on pyramid-format tensors
   pqtopk.npz   ib_pq_lm_head_topk (l1-only logits, top-K, subset refinement)
+  pqq8.npz     ib_pq_matmul_fp32_q8lut (int8-quantised tables)
   int4g.npz    ib_pq_session_matmul on IBF v5 INT4 group-scale tensors
                (oracle/_ref/libref_int4g.so): y without, ys with the
                IB_ACT_SPARSE_REL skip mask (set in a child process, since the
@@ -27,7 +28,8 @@ Contents (every array is what the reference produced, except the inputs):
   python tests/golden/gen_golden.py int4g   writes int4g.npz only;
   python tests/golden/gen_golden.py pqs     writes pqs.npz only;
   python tests/golden/gen_golden.py pqv     writes pqv.npz only;
-  python tests/golden/gen_golden.py pqtopk  writes pqtopk.npz only.
+  python tests/golden/gen_golden.py pqtopk  writes pqtopk.npz only;
+  python tests/golden/gen_golden.py pqq8    writes pqq8.npz only.
 """
 from __future__ import annotations
 
@@ -309,6 +311,26 @@ def gen_int4g(out):
     np.savez_compressed(os.path.join(out, "int4g.npz"), **d)
 
 
+# q8lut cases: (M, C, G, K, levels, K_l2, outliers); level 2 needs K_l2 == K
+PQQ8 = {"l1": (64, 16, 16, 256, 1, 0, 0), "l2": (40, 12, 16, 256, 2, 256, 0),
+        "out8": (48, 16, 16, 256, 1, 0, 8), "out40l2": (30, 10, 16, 64, 2, 64, 40),
+        "g4": (40, 24, 4, 256, 1, 0, 0), "g32": (36, 10, 32, 256, 1, 0, 5), "g6": (20, 9, 6, 32, 2, 32, 0)}
+
+
+def gen_pqq8(out):
+    d = {}
+    rng = np.random.default_rng(8080)
+    for name, args in PQQ8.items():
+        t = make_pq(rng, *args)
+        x = rng.standard_normal(t["N"]).astype(np.float32)
+        x[rng.integers(0, t["N"], 3)] *= 20.0
+        for k, v in t.items():
+            d[f"{name}.{k}"] = np.asarray(v)
+        d[f"{name}.x"] = x
+        d[f"{name}.y"] = R.pq_matmul_q8lut(t, x)
+    np.savez_compressed(os.path.join(out, "pqq8.npz"), **d)
+
+
 def main():
     if len(sys.argv) > 2 and sys.argv[1] == "int4g-skip-child":
         np.savez(sys.argv[2], **int4g_outputs(int4g_inputs()))
@@ -325,6 +347,9 @@ def main():
     if len(sys.argv) > 1 and sys.argv[1] == "pqtopk":
         gen_pqtopk(HERE)
         return
+    if len(sys.argv) > 1 and sys.argv[1] == "pqq8":
+        gen_pqq8(HERE)
+        return
     if not R.available():
         sys.exit("oracle/_ref/libinferbit_ref.so missing: run `make -C oracle ref` first")
     gen_quant_matvec(HERE)
@@ -333,6 +358,7 @@ def main():
     gen_pqs(HERE)
     gen_pqv(HERE)
     gen_pqtopk(HERE)
+    gen_pqq8(HERE)
     gen_int4g(HERE)
     for f in sorted(os.listdir(HERE)):
         if f.endswith(".npz"):

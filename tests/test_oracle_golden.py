@@ -413,3 +413,48 @@ def test_pq_topk_is_the_subset_of_largest_coarse_logits(oracle_lib):
     small = pq_case(d, "small")
     lg, ids = oracle_lib.pq_lm_head_topk(small, small["x"], 12)
     assert sorted(ids.tolist()) == list(range(12))
+
+
+PQQ8_NAMES = ["l1", "l2", "out8", "out40l2", "g4", "g32", "g6"]
+
+
+@pytest.mark.parametrize("name", PQQ8_NAMES)
+def test_pq_q8lut_matches_reference(oracle_lib, name):
+    """ib_pq_matmul_fp32_q8lut, bit for bit against the reference's outputs."""
+    d = load_golden("pqq8.npz")
+    t = pq_case(d, name)
+    same_bits(oracle_lib.pq_matmul_q8lut(t, t["x"]), d[f"{name}.y"])
+
+
+@pytest.mark.parametrize("name", PQQ8_NAMES)
+def test_pq_q8lut_error_bound(oracle_lib, name):
+    """Independent of the restatement: the int8 tables move each chunk term
+    by at most half a step of its (chunk, side) scale, so
+    |y - W x| <= |row_scale| * sum_c sum_side (max_k |T| / 254) per level
+    (+ fp32 slack), with W x in float64 from the materialised matrix and
+    T in float64 from the codebooks."""
+    d = load_golden("pqq8.npz")
+    t = pq_case(d, name)
+    x = t["x"].astype(np.float64)
+    W = oracle_lib.pq_reconstruct(t).astype(np.float64)
+    y = oracle_lib.pq_matmul_q8lut(t, t["x"]).astype(np.float64)
+    exact = W @ x
+    G, C, hf = t["G"], t["C"], t["G"] // 2
+    mask = np.ones(t["N"], bool)
+    if t["n_outlier"]:
+        mask[np.asarray(t["ocols"])] = False
+    inner = np.nonzero(mask)[0]
+    bound = 0.0
+    for lev in range(t["n_levels"]):
+        for side, key in enumerate(("cb1l", "cb1r") if lev == 0 else ("cb2l", "cb2r")):
+            cb = np.asarray(t[key]).view(np.float16).astype(np.float64).reshape(-1, hf)
+            for c in range(C):
+                xs = x[inner[c * G + side * hf: c * G + side * hf + hf]]
+                bound += np.abs(cb @ xs).max() / 254.0
+    rs = np.abs(np.asarray(t["row_scale"]).view(np.float16).astype(np.float64))
+    slack = 1e-5 * np.abs(exact).max() + 1e-6
+    if t["n_outlier"] >= 32:      # the int8 outlier dot adds its own half step per column
+        oc = np.asarray(t["ocols"])
+        os_ = np.asarray(t["oscale"]).view(np.float16).astype(np.float64)
+        slack += np.abs(t["oside"]).max() * np.abs(x[oc] * os_).max() / 254.0 * t["n_outlier"]
+    assert np.all(np.abs(y - exact) <= rs * bound + slack)

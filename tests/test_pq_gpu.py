@@ -90,6 +90,40 @@ def test_pq_streaming_rejects_wide_chunks(ops):
         run_streaming(ops, t, np.zeros(t["N"], np.float32))
 
 
+def run_q8lut(ops, t, x):
+    d = ops.PqDeviceTensor(t)
+    out = torch.empty(t["M"], device="cuda")
+    d.matmul_q8lut(torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda(), out)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("name", ["l1", "l2", "out8", "out40l2", "g4", "g32", "g6"])
+def test_pq_q8lut_golden(ops, name):
+    """ib_pq_matmul_fp32_q8lut: the int8 codes equal the reference's, the
+    gather sums in another order."""
+    print(f"case pq q8lut {name}", flush=True)
+    d = load_golden("pqq8.npz")
+    t = pq_case(d, name)
+    assert relerr(run_q8lut(ops, t, t["x"]), d[f"{name}.y"]) <= 1e-4
+
+
+def test_pq_q8lut_mistral_shape(ops, oracle_lib):
+    from gen_golden import make_pq
+    rng = np.random.default_rng(61)
+    t = make_pq(rng, 4096, 896, 16, 256, 2, 256, 0)
+    x = rng.standard_normal(t["N"]).astype(np.float32)
+    assert relerr(run_q8lut(ops, t, x), oracle_lib.pq_matmul_q8lut(t, x)) <= 1e-4
+
+
+def test_pq_q8lut_rejects_unreadable_level2(ops):
+    from gen_golden import make_pq
+    from libinferbit_amd import IbhError
+    t = make_pq(np.random.default_rng(2), 16, 4, 16, 64, 2, 256, 0)     # K_l2 != K
+    with pytest.raises(IbhError):
+        run_q8lut(ops, t, np.zeros(t["N"], np.float32))
+
+
 PQV_NAMES = ["l1", "l2p16", "l2u8", "l2u16", "out8", "out40", "pyr16", "pyr8"]
 PQV_POLICIES = {"l1only": (1, 0.0, 0.0), "l2skip05": (2, 0.5, 0.0), "l2skip5": (2, 5.0, 0.0),
                 "sparse": (3, 0.0, 1e-2), "int8": (4, 0.0, 0.0)}
