@@ -280,9 +280,11 @@ int  ibh_v5_set_policy(ibh_v5_session* s, const char* name, const ibh_pq_policy*
  * x [N], out [M]; ordered after earlier work on `stream`. */
 int  ibh_v5_session_matmul(ibh_v5_session* s, const char* name, const float* x, float* out, void* stream);
 /* ib_pq_kv_cache_create / _free / _clear / _length (src/pq_decode.c:
- * 4740-4852): fp32 K and V [layer][pos][kv_dim] in HBM (the reference's
- * default storage; its IB_PQ_KV_FP16 / _INT8 / _PYRAMID modes are not
- * provided). */
+ * 4740-4852): K and V [layer][pos][kv_dim] in HBM, fp32 by default, fp16
+ * with IB_PQ_KV_FP16=1, int8 with one scale per position with
+ * IB_PQ_KV_INT8=1 (read here as the reference reads them).  IB_PQ_KV_PYRAMID
+ * with K/V codebooks in the file is refused (without them: fp32, as the
+ * reference falls back). */
 int  ibh_v5_kv_create(ibh_v5_session* s, int max_seq, ibh_v5_kv** out);
 void ibh_v5_kv_free(ibh_v5_kv* kv);
 void ibh_v5_kv_clear(ibh_v5_kv* kv);

@@ -212,11 +212,46 @@ __global__ void v5_rope_kv_kernel(float* __restrict__ q, const float* __restrict
 constexpr int kAttnThreads = 256;
 constexpr int kAttnPos = 64;   // positions per split
 
-template <int HD, int GRP>
+// Cache storage (ib_pq_kv_cache_create, pq_decode.c:4752-4833): fp32, fp16
+// (IB_PQ_KV_FP16; ib_fp32_to_fp16 rounds to nearest even) or int8
+// (IB_PQ_KV_INT8; one scale per position over the whole kv_dim vector,
+// max(1e-12, max|v|) / 127, codes round half away clamped to +-127;
+// pq_decode.c:5092-5116).
+enum { KV_F32 = 0, KV_F16 = 1, KV_I8 = 2 };
+
+template <int KVT>
+__device__ __forceinline__ float kv_ld(const void* base, size_t i, float sc) {
+    if constexpr (KVT == KV_F32) return ((const float*)base)[i];
+    else if constexpr (KVT == KV_F16) return f16_to_f32(((const uint16_t*)base)[i]);
+    else return (float)((const int8_t*)base)[i] * sc;
+}
+
+template <int KVT>
+__device__ __forceinline__ float4 kv_ld4(const void* base, size_t i, float sc) {
+    if constexpr (KVT == KV_F32) return *(const float4*)((const float*)base + i);
+    else if constexpr (KVT == KV_F16) {
+        const uint2 u = *(const uint2*)((const uint16_t*)base + i);
+        return float4{f16_to_f32((uint16_t)(u.x & 0xffff)), f16_to_f32((uint16_t)(u.x >> 16)),
+                      f16_to_f32((uint16_t)(u.y & 0xffff)), f16_to_f32((uint16_t)(u.y >> 16))};
+    } else {
+        const uint32_t u = *(const uint32_t*)((const int8_t*)base + i);
+        return float4{(float)(int8_t)(u & 0xff) * sc, (float)(int8_t)((u >> 8) & 0xff) * sc,
+                      (float)(int8_t)((u >> 16) & 0xff) * sc, (float)(int8_t)(u >> 24) * sc};
+    }
+}
+
+__device__ __forceinline__ int kv_q8(float v, float inv) {
+    const float u = v * inv;
+    const int q = (int)(u >= 0 ? u + 0.5f : u - 0.5f);
+    return q > 127 ? 127 : (q < -127 ? -127 : q);
+}
+
+template <int HD, int GRP, int KVT>
 __global__ __launch_bounds__(kAttnThreads) void v5_attn_kernel(
     float* __restrict__ out, const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
-    float* __restrict__ kc, float* __restrict__ vc, const float* __restrict__ cs, const int* __restrict__ dpos,
-    int n_kv, int NS, float scale, float* __restrict__ part, int* __restrict__ counter) {
+    void* __restrict__ kc, void* __restrict__ vc, float* __restrict__ ksc, float* __restrict__ vsc,
+    const float* __restrict__ cs, const int* __restrict__ dpos, int n_kv, int NS, float scale,
+    float* __restrict__ part, int* __restrict__ counter) {
     constexpr int HALF = HD / 2, NW = kAttnThreads / 64, DPL = HD / 64, PPW = kAttnPos / NW;
     constexpr int KPRE = HD == 64 ? HD / 4 : 1;   // key row held in registers (head_dim 64)
     __shared__ __align__(16) float qs[GRP][HD];
@@ -236,21 +271,23 @@ __global__ __launch_bounds__(kAttnThreads) void v5_attn_kernel(
     // lane's key row and this wavefront's value elements
     const int t = t0 + lane;
     const bool act = t < t1;
+    const float kst = (KVT == KV_I8 && act && t != pos) ? ksc[t] : 1.f;
     float4 kreg[KPRE];
     if constexpr (HD == 64) {
         if (act && t != pos) {
-            const float4* kr = (const float4*)(kc + (size_t)t * kv_dim + hoff);
 #pragma unroll
-            for (int i = 0; i < KPRE; i++) kreg[i] = kr[i];
+            for (int i = 0; i < KPRE; i++) kreg[i] = kv_ld4<KVT>(kc, (size_t)t * kv_dim + hoff + 4 * i, kst);
         }
     }
     float vpre[PPW][DPL];
 #pragma unroll
     for (int j = 0; j < PPW; j++) {
         const int tt = t0 + wave + NW * j;
+        const bool ok = tt < t1 && tt != pos;
+        const float vst = (KVT == KV_I8 && ok) ? vsc[tt] : 1.f;
 #pragma unroll
         for (int jj = 0; jj < DPL; jj++)
-            vpre[j][jj] = (tt < t1 && tt != pos) ? vc[(size_t)tt * kv_dim + hoff + lane + 64 * jj] : 0.f;
+            vpre[j][jj] = ok ? kv_ld<KVT>(vc, (size_t)tt * kv_dim + hoff + lane + 64 * jj, vst) : 0.f;
     }
     const float* csp = cs + (size_t)pos * HD;
     for (int e = tid; e < GRP * HALF; e += kAttnThreads) {
@@ -263,19 +300,78 @@ __global__ __launch_bounds__(kAttnThreads) void v5_attn_kernel(
     if (t0 <= pos && pos < t1) {
         const float* kh = k + hoff;
         const float* vh = v + hoff;
-        float* krow = kc + (size_t)pos * kv_dim + hoff;
-        float* vrow = vc + (size_t)pos * kv_dim + hoff;
-        for (int i = tid; i < HALF; i += kAttnThreads) {
-            const float c = csp[2 * i], sn = csp[2 * i + 1], a = kh[i], b = kh[i + HALF];
-            const float r0 = a * c - b * sn, r1 = b * c + a * sn;
-            kcur[i] = r0;
-            kcur[i + HALF] = r1;
-            krow[i] = r0;
-            krow[i + HALF] = r1;
-        }
-        for (int i = tid; i < HD; i += kAttnThreads) {
-            vcur[i] = vh[i];
-            vrow[i] = vh[i];
+        const size_t rowo = (size_t)pos * kv_dim + hoff;
+        if constexpr (KVT == KV_I8) {
+            // the position's scales span every kv head: each owner block
+            // rotates all keys to find max|k| (the same value in each block)
+            __shared__ float kred[NW], vred2[NW];
+            float km = 0.f, vm = 0.f;
+            for (int e = tid; e < n_kv * HALF; e += kAttnThreads) {
+                const int h = e / HALF, i = e - h * HALF;
+                const float* kk = k + (size_t)h * HD;
+                const float c = csp[2 * i], sn = csp[2 * i + 1], a = kk[i], b = kk[i + HALF];
+                km = fmaxf(km, fmaxf(fabsf(a * c - b * sn), fabsf(b * c + a * sn)));
+            }
+            for (int e = tid; e < kv_dim; e += kAttnThreads) vm = fmaxf(vm, fabsf(v[e]));
+            km = wave_max(km);
+            vm = wave_max(vm);
+            if (lane == 0) {
+                kred[wave] = km;
+                vred2[wave] = vm;
+            }
+            __syncthreads();
+            float kmax = 1e-12f, vmax = 1e-12f;
+            for (int w = 0; w < NW; w++) {
+                kmax = fmaxf(kmax, kred[w]);
+                vmax = fmaxf(vmax, vred2[w]);
+            }
+            const float ks = kmax / 127.0f, vs = vmax / 127.0f, ki = 1.0f / ks, vi = 1.0f / vs;
+            if (tid == 0) {
+                ksc[pos] = ks;
+                vsc[pos] = vs;
+            }
+            int8_t* krow = (int8_t*)kc + rowo;
+            int8_t* vrow = (int8_t*)vc + rowo;
+            for (int i = tid; i < HALF; i += kAttnThreads) {
+                const float c = csp[2 * i], sn = csp[2 * i + 1], a = kh[i], b = kh[i + HALF];
+                const int q0 = kv_q8(a * c - b * sn, ki), q1 = kv_q8(b * c + a * sn, ki);
+                krow[i] = (int8_t)q0;
+                krow[i + HALF] = (int8_t)q1;
+                kcur[i] = (float)q0 * ks;
+                kcur[i + HALF] = (float)q1 * ks;
+            }
+            for (int i = tid; i < HD; i += kAttnThreads) {
+                const int qv = kv_q8(vh[i], vi);
+                vrow[i] = (int8_t)qv;
+                vcur[i] = (float)qv * vs;
+            }
+        } else {
+            for (int i = tid; i < HALF; i += kAttnThreads) {
+                const float c = csp[2 * i], sn = csp[2 * i + 1], a = kh[i], b = kh[i + HALF];
+                const float r0 = a * c - b * sn, r1 = b * c + a * sn;
+                if constexpr (KVT == KV_F16) {
+                    const _Float16 h0 = (_Float16)r0, h1 = (_Float16)r1;
+                    ((_Float16*)kc)[rowo + i] = h0;
+                    ((_Float16*)kc)[rowo + i + HALF] = h1;
+                    kcur[i] = (float)h0;
+                    kcur[i + HALF] = (float)h1;
+                } else {
+                    ((float*)kc)[rowo + i] = r0;
+                    ((float*)kc)[rowo + i + HALF] = r1;
+                    kcur[i] = r0;
+                    kcur[i + HALF] = r1;
+                }
+            }
+            for (int i = tid; i < HD; i += kAttnThreads) {
+                if constexpr (KVT == KV_F16) {
+                    const _Float16 h = (_Float16)vh[i];
+                    ((_Float16*)vc)[rowo + i] = h;
+                    vcur[i] = (float)h;
+                } else {
+                    ((float*)vc)[rowo + i] = vh[i];
+                    vcur[i] = vh[i];
+                }
+            }
         }
     }
     __syncthreads();
@@ -286,12 +382,12 @@ __global__ __launch_bounds__(kAttnThreads) void v5_attn_kernel(
 #pragma unroll
         for (int h = 0; h < HPW; h++) sc[h] = 0.f;
         if (act) {
-            const float* kr = t == pos ? kcur : kc + (size_t)t * kv_dim + hoff;
 #pragma unroll
             for (int d = 0; d < HD; d += 4) {
                 float4 kk;
-                if constexpr (HD == 64) kk = t == pos ? *(const float4*)(kcur + d) : kreg[d / 4];
-                else kk = *(const float4*)(kr + d);
+                if (t == pos) kk = *(const float4*)(kcur + d);
+                else if constexpr (HD == 64) kk = kreg[d / 4];
+                else kk = kv_ld4<KVT>(kc, (size_t)t * kv_dim + hoff + d, kst);
 #pragma unroll
                 for (int h = 0; h < HPW; h++) {
                     const int g = wave + NW * h;
@@ -480,7 +576,9 @@ struct ibh_v5_session {
 struct ibh_v5_kv {
     ibh_v5_session* s = nullptr;
     int max_seq = 0, length = 0;
-    float *k = nullptr, *v = nullptr, *rope = nullptr;
+    float *k = nullptr, *v = nullptr, *rope = nullptr;   // cache rows (typed by kvt)
+    int kvt = 0;                // storage: 0 fp32, 1 fp16, 2 int8 (+ per-position scales)
+    float *ks = nullptr, *vs = nullptr;   // int8 scales [layer][pos]
     void* aws = nullptr;
     size_t aws_bytes = 0;
     int* state = nullptr;    // device: [0] position, [1] generated count
@@ -1014,17 +1112,25 @@ bool attn_fused_ok(const ibh_v5_session* s, int max_seq) {
            (max_seq + kAttnPos - 1) / kAttnPos <= kAttnMaxSplits && !getenv("IBH_V5_SPLIT_ATTN");
 }
 
-int launch_attn_fused(ibh_v5_session* s, ibh_v5_kv* kv, const float* q, const float* k, const float* v, float* kc,
-                      float* vc) {
+int launch_attn_fused(ibh_v5_session* s, ibh_v5_kv* kv, const float* q, const float* k, const float* v, int layer) {
     const int grp = s->n_heads / s->n_kv;
     const float scale = 1.0f / sqrtf((float)s->head_dim);
     const dim3 grid(s->n_kv, kv->ns);
-#define IBH_VA(H_, G_) v5_attn_kernel<H_, G_><<<grid, kAttnThreads, 0, s->st>>>(s->xb2, q, k, v, kc, vc, kv->rope, \
-        kv->state, s->n_kv, kv->ns, scale, kv->apart, kv->acnt)
-#define IBH_VAG(H_) do { if (grp == 1) IBH_VA(H_, 1); else if (grp == 2) IBH_VA(H_, 2); \
-                         else if (grp == 4) IBH_VA(H_, 4); else IBH_VA(H_, 8); } while (0)
+    const size_t lrow = (size_t)layer * kv->max_seq;
+    const size_t esz = kv->kvt == 0 ? 4 : (kv->kvt == 1 ? 2 : 1);
+    void* kc = (char*)kv->k + lrow * s->kv_dim * esz;
+    void* vc = (char*)kv->v + lrow * s->kv_dim * esz;
+    float* ksc = kv->ks ? kv->ks + lrow : nullptr;
+    float* vsc = kv->vs ? kv->vs + lrow : nullptr;
+#define IBH_VA(H_, G_, T_) v5_attn_kernel<H_, G_, T_><<<grid, kAttnThreads, 0, s->st>>>(s->xb2, q, k, v, kc, vc, \
+        ksc, vsc, kv->rope, kv->state, s->n_kv, kv->ns, scale, kv->apart, kv->acnt)
+#define IBH_VAT(H_, G_) do { if (kv->kvt == 0) IBH_VA(H_, G_, KV_F32); else if (kv->kvt == 1) IBH_VA(H_, G_, KV_F16); \
+                             else IBH_VA(H_, G_, KV_I8); } while (0)
+#define IBH_VAG(H_) do { if (grp == 1) IBH_VAT(H_, 1); else if (grp == 2) IBH_VAT(H_, 2); \
+                         else if (grp == 4) IBH_VAT(H_, 4); else IBH_VAT(H_, 8); } while (0)
     if (s->head_dim == 64) IBH_VAG(64); else IBH_VAG(128);
 #undef IBH_VAG
+#undef IBH_VAT
 #undef IBH_VA
     IBH_CHECK_LAUNCH("ibh_v5: attention");
     return IBH_OK;
@@ -1087,7 +1193,7 @@ int forward_dev(ibh_v5_session* s, ibh_v5_kv* kv, bool want_logits) {
         }
         const size_t lbase = (size_t)l * kv->max_seq * KV;
         if (kv->ns > 0) {
-            if ((rc = launch_attn_fused(s, kv, q, k, v, kv->k + lbase, kv->v + lbase))) return rc;
+            if ((rc = launch_attn_fused(s, kv, q, k, v, l))) return rc;
         } else {
             v5_rope_kv_kernel<<<s->n_heads + 2 * s->n_kv, 64, 0, s->st>>>(q, k, v, kv->k + lbase, kv->v + lbase,
                                                                            kv->rope, dpos, s->n_heads, s->n_kv, hd);
@@ -1297,7 +1403,30 @@ extern "C" int ibh_v5_kv_create(ibh_v5_session* s, int max_seq, ibh_v5_kv** out)
     const size_t n = (size_t)s->n_layers * max_seq * s->kv_dim;
     const int half = s->head_dim / 2;
     kv->aws_bytes = ibh_attn_workspace_bytes(s->n_heads, s->head_dim, max_seq);
-    bool ok = hipMalloc((void**)&kv->k, n * 4) == hipSuccess && hipMalloc((void**)&kv->v, n * 4) == hipSuccess &&
+    // storage selected like ib_pq_kv_cache_create (pq_decode.c:4752-4758):
+    // pyramid > int8 > fp16 > fp32
+    const auto env_on = [](const char* n) { const char* e = getenv(n); return e && atoi(e) > 0; };
+    if (env_on("IB_PQ_KV_PYRAMID")) {
+        // the reference falls back to fp32 when the file has no K codebooks
+        // (4759-4775); product-quantised cache rows are not provided here
+        const RawT* cb = raw_find(s, "K_codebook_L0_l");
+        if (cb && cb->dtype == RAW_F16 && cb->ndim == 2) {
+            delete kv;
+            ibh_set_error("ibh_v5_kv_create: IB_PQ_KV_PYRAMID cache storage is not provided");
+            return IBH_ERROR_PARAM;
+        }
+    }
+    kv->kvt = env_on("IB_PQ_KV_INT8") ? 2 : (env_on("IB_PQ_KV_FP16") ? 1 : 0);
+    if (kv->kvt != 0 && !attn_fused_ok(s, max_seq)) {
+        delete kv;
+        ibh_set_error("ibh_v5_kv_create: fp16 / int8 cache storage needs head_dim 64 or 128 and a group of "
+                      "1, 2, 4 or 8 query heads per kv head");
+        return IBH_ERROR_PARAM;
+    }
+    const size_t esz = kv->kvt == 0 ? 4 : (kv->kvt == 1 ? 2 : 1);
+    bool ok = hipMalloc((void**)&kv->k, n * esz) == hipSuccess && hipMalloc((void**)&kv->v, n * esz) == hipSuccess &&
+              (kv->kvt != 2 || (hipMalloc((void**)&kv->ks, (size_t)s->n_layers * max_seq * 4) == hipSuccess &&
+                                hipMalloc((void**)&kv->vs, (size_t)s->n_layers * max_seq * 4) == hipSuccess)) &&
               hipMalloc((void**)&kv->rope, (size_t)max_seq * half * 8) == hipSuccess &&
               hipMalloc(&kv->aws, kv->aws_bytes) == hipSuccess && hipMalloc((void**)&kv->state, 16) == hipSuccess &&
               hipMalloc((void**)&kv->tokens, (size_t)max_seq * 4 + 4) == hipSuccess &&
@@ -1334,7 +1463,8 @@ extern "C" void ibh_v5_kv_free(ibh_v5_kv* kv) {
     if (!kv) return;
     if (kv->s && kv->s->st) hipStreamSynchronize(kv->s->st);
     drop_graphs(kv);
-    for (void* p : {(void*)kv->k, (void*)kv->v, (void*)kv->rope, kv->aws, (void*)kv->state, (void*)kv->tokens,
+    for (void* p : {(void*)kv->k, (void*)kv->v, (void*)kv->ks, (void*)kv->vs, (void*)kv->rope, kv->aws,
+                    (void*)kv->state, (void*)kv->tokens,
                     (void*)kv->outs, (void*)kv->apart, (void*)kv->acnt})
         if (p) hipFree(p);
     delete kv;

@@ -278,3 +278,34 @@ def test_generate_sample(L, tmp_path_factory, tmp_path, name):
     got = S.generate_sample(kv, PROMPT, 24, temperature=T, top_k=k, top_p=p, seed=seed).tolist()
     assert got == rg, (name, got, rg)
     assert len(kv) == len(PROMPT) + 24
+
+
+@pytest.mark.parametrize("mode", ["IB_PQ_KV_FP16", "IB_PQ_KV_INT8"])
+@pytest.mark.parametrize("name,n_prompt", [("mixed", 5), ("fused", 150)])
+def test_kv_storage_modes(L, tmp_path_factory, tmp_path, monkeypatch, mode, name, n_prompt):
+    """The reference's fp16 and int8 (one scale per position over kv_dim)
+    cache storage, selected by the same environment switches; logits and
+    tokens as the reference's under the same switch."""
+    from libinferbit_amd.session import PqSession
+    monkeypatch.setenv(mode, "1")
+    path = model(tmp_path_factory, name)
+    prompt = PROMPT if n_prompt == 5 else [int(t) for t in np.random.default_rng(9).integers(0, 1000, n_prompt)]
+    rt, rl = ref_run(path, prompt, 6, "steps", tmp_path, max_seq=256)
+    S = PqSession(path)
+    gt, gl = gpu_steps(S, prompt, 6, max_seq=256)
+    assert max(relerr(gl[i], rl[i]) for i in range(len(prompt))) <= TOL
+    assert gt == rt
+    rg, _ = ref_run(path, prompt, 10, "greedy", tmp_path, max_seq=256)
+    assert S.generate_greedy(S.kv_cache(256), prompt, 10).tolist() == rg
+
+
+def test_kv_pyramid_without_codebooks_is_fp32(L, tmp_path_factory, tmp_path, monkeypatch):
+    """IB_PQ_KV_PYRAMID on a file without K/V codebooks: the reference keeps
+    fp32 rows, so does the GPU cache (same logits as without the switch)."""
+    from libinferbit_amd.session import PqSession
+    path = model(tmp_path_factory, "int4")
+    monkeypatch.setenv("IB_PQ_KV_PYRAMID", "1")
+    rt, rl = ref_run(path, PROMPT, 4, "steps", tmp_path)
+    S = PqSession(path)
+    gt, gl = gpu_steps(S, PROMPT, 4)
+    assert gt == rt and max(relerr(gl[i], rl[i]) for i in range(len(PROMPT))) <= TOL
