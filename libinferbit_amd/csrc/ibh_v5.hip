@@ -137,11 +137,16 @@ __global__ __launch_bounds__(kNormThreads) void v5_rmsnorm_kernel(float* __restr
                                                                   const float* __restrict__ w, float eps, int n,
                                                                   int* __restrict__ bump) {
     __shared__ double red[kNormThreads / 64];
-    float v[kNormMaxPer];
+    float v[kNormMaxPer], wv[kNormMaxPer];
     double ss = 0.0;
 #pragma unroll
+    for (int j = 0; j < kNormMaxPer; j++) {   // weights first: off the reduction's critical path
+        const int i = threadIdx.x + j * (int)blockDim.x;
+        wv[j] = i < n ? w[i] : 0.f;
+    }
+#pragma unroll
     for (int j = 0; j < kNormMaxPer; j++) {
-        const int i = threadIdx.x + j * kNormThreads;
+        const int i = threadIdx.x + j * (int)blockDim.x;
         v[j] = 0.f;
         if (i < n) {
             float xv = x[i];
@@ -158,12 +163,12 @@ __global__ __launch_bounds__(kNormThreads) void v5_rmsnorm_kernel(float* __restr
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
     __syncthreads();
     double tot = 0.0;
-    for (int k = 0; k < kNormThreads / 64; k++) tot += red[k];
+    for (int k = 0; k < (int)(blockDim.x >> 6); k++) tot += red[k];
     const float inv = 1.0f / sqrtf((float)(tot / (double)n) + eps);
 #pragma unroll
     for (int j = 0; j < kNormMaxPer; j++) {
-        const int i = threadIdx.x + j * kNormThreads;
-        if (i < n) out[i] = v[j] * inv * w[i];
+        const int i = threadIdx.x + j * (int)blockDim.x;
+        if (i < n) out[i] = v[j] * inv * wv[j];
     }
     if (bump && threadIdx.x == 0) *bump += 1;   // end of a step: position + 1
 }
@@ -1163,6 +1168,10 @@ int matmul_set(ibh_v5_session* s, const int* mi, float* const* out, int n, const
 // post-final-norm hidden state in s->xb and, when want_logits, the logits in
 // s->logits; then *pos + 1.  Every launch reads the position from device
 // memory, so the chain is captured once and replayed.
+// rmsnorm block: 1024 threads (a 256-thread block measured slower at
+// hidden 2048: fewer wavefronts in flight for the same loads)
+int norm_threads(int) { return kNormThreads; }
+
 int forward_dev(ibh_v5_session* s, ibh_v5_kv* kv, bool want_logits) {
     const int H = s->hidden, KV = s->kv_dim, I = s->inter, hd = s->head_dim;
     int* dpos = kv->state;
@@ -1178,7 +1187,7 @@ int forward_dev(ibh_v5_session* s, ibh_v5_kv* kv, bool want_logits) {
     int rc;
     const float* pending = nullptr;   // residual not yet added into x
     for (int l = 0; l < s->n_layers; l++) {
-        v5_rmsnorm_kernel<<<1, kNormThreads, 0, s->st>>>(s->xb, s->x, pending, s->w_in[l], s->eps, H, nullptr);
+        v5_rmsnorm_kernel<<<1, norm_threads(H), 0, s->st>>>(s->xb, s->x, pending, s->w_in[l], s->eps, H, nullptr);
         IBH_CHECK_LAUNCH("ibh_v5: rmsnorm");
         float *q = s->q, *k = s->kn, *v = s->vn;
         if (s->fused_qkv) {
@@ -1203,7 +1212,7 @@ int forward_dev(ibh_v5_session* s, ibh_v5_kv* kv, bool want_logits) {
                 return rc;
         }
         if ((rc = matmul(s, s->mo[l], s->xb2, s->delta))) return rc;
-        v5_rmsnorm_kernel<<<1, kNormThreads, 0, s->st>>>(s->xb, s->x, s->delta, s->w_pn[l], s->eps, H, nullptr);
+        v5_rmsnorm_kernel<<<1, norm_threads(H), 0, s->st>>>(s->xb, s->x, s->delta, s->w_pn[l], s->eps, H, nullptr);
         IBH_CHECK_LAUNCH("ibh_v5: rmsnorm");
         float *g = s->gate, *u = s->up;
         if (s->fused_gu) {
@@ -1220,7 +1229,7 @@ int forward_dev(ibh_v5_session* s, ibh_v5_kv* kv, bool want_logits) {
         if ((rc = matmul(s, s->md[l], s->gate, s->delta))) return rc;
         pending = s->delta;
     }
-    v5_rmsnorm_kernel<<<1, kNormThreads, 0, s->st>>>(s->xb, s->x, pending, s->w_final, s->eps, H, dpos);
+    v5_rmsnorm_kernel<<<1, norm_threads(H), 0, s->st>>>(s->xb, s->x, pending, s->w_final, s->eps, H, dpos);
     IBH_CHECK_LAUNCH("ibh_v5: final rmsnorm");
     if (want_logits && (rc = matmul(s, s->m_head, s->xb, s->logits))) return rc;
     return IBH_OK;
