@@ -120,7 +120,7 @@ def _pq(rng, M, N, G=16, K=256, levels=1, K2=0, n_outlier=0, cb_std=0.05):
 
 def write_synthetic_v5(path: str, cfg: dict, seed: int = 0, backend=None, awq: bool = False, outliers: int = 0,
                        head: str = "pq", levels: int = 1, k2: int = 256, pq_outliers: int = 0,
-                       pq_act_scale: bool = False, fused: bool = False, embed: str = "f16"):
+                       pq_act_scale: bool = False, fused: bool = False, embed: str = "f16", i4_group: int = 0):
     """A random decoder in IBF v5.  cfg: num_layers, hidden_size, num_heads,
     num_kv_heads, head_dim, intermediate_size, vocab_size (+ rms_norm_eps,
     rope_theta).  backend maps projection names (q_proj, k_proj, v_proj,
@@ -130,7 +130,8 @@ def write_synthetic_v5(path: str, cfg: dict, seed: int = 0, backend=None, awq: b
     one) or int4g / fp16.  PQ tensors: `levels` 1 or 2 (K_l2 = k2),
     `pq_outliers` outlier columns, `pq_act_scale` an <name>__act_scale
     vector.  `fused` writes L{i}_qkv_proj / L{i}_gateup_proj instead of the
-    separate projections; `embed` is "f16", "f32" or "pq"."""
+    separate projections; `embed` is "f16", "f32" or "pq"; `i4_group` the
+    INT4 scale group (0: 128 when it divides N, else 32)."""
     rng = np.random.default_rng(seed)
     backend = dict(backend or {})
     H, L = cfg["hidden_size"], cfg["num_layers"]
@@ -155,7 +156,7 @@ def write_synthetic_v5(path: str, cfg: dict, seed: int = 0, backend=None, awq: b
         elif kind == "fp16":
             w.raw_tensor(name + "__fp16w", _f16(rng.standard_normal((M, N)) / np.sqrt(N)), "float16")
         else:
-            G = 128 if N % 128 == 0 else 32
+            G = i4_group or (128 if N % 128 == 0 else 32)
             w.raw_tensor(name + "__i4_q", rng.integers(0, 256, (M, N // 2), dtype=np.uint8), "uint8")
             w.raw_tensor(name + "__i4_s", _f16(rng.uniform(0.5, 1.5, (M, N // G)) / (4 * np.sqrt(N))), "float16")
             if awq:

@@ -309,3 +309,19 @@ def test_kv_pyramid_without_codebooks_is_fp32(L, tmp_path_factory, tmp_path, mon
     S = PqSession(path)
     gt, gl = gpu_steps(S, PROMPT, 4)
     assert gt == rt and max(relerr(gl[i], rl[i]) for i in range(len(PROMPT))) <= TOL
+
+
+def test_long_context_odd_vocab_small_groups(L, tmp_path_factory, tmp_path):
+    """A 1500-token prompt over 24 attention splits, rope_theta 5e5,
+    rms_norm_eps 1e-6, an odd vocabulary and INT4 groups of 64 (the
+    wavefront-per-row INT4 kernel)."""
+    from libinferbit_amd.session import PqSession
+    cfg = dict(CFG, vocab_size=1237, rope_theta=500000.0, rms_norm_eps=1e-6)
+    path = model(tmp_path_factory, "long_g64", cfg=cfg, i4_group=64, awq=True, outliers=2)
+    prompt = [int(t) for t in np.random.default_rng(15).integers(0, 1237, 1500)]
+    rt, rl = ref_run(path, prompt, 4, "steps", tmp_path, max_seq=1600)
+    S = PqSession(path)
+    gt, gl = gpu_steps(S, prompt, 4, max_seq=1600)
+    errs = [relerr(gl[i], rl[i]) for i in (0, 63, 64, 700, 1499)]
+    assert max(errs) <= TOL, errs
+    assert gt == rt
