@@ -215,7 +215,9 @@ __global__ void v5_rope_kv_kernel(float* __restrict__ q, const float* __restrict
 // directly.  Exponentials use the hardware exp2 (__expf, a few ulp): the
 // softmax only needs fp32 accuracy here.
 constexpr int kAttnThreads = 256;
-constexpr int kAttnPos = 64;   // positions per split
+constexpr int kAttnPos = 64;   // positions per tile (one per lane)
+constexpr int kAttnTiles = 1;  // tiles per split, online softmax across them (more
+                               // than one measured slower than split + merge)
 
 // Cache storage (ib_pq_kv_cache_create, pq_decode.c:4752-4833): fp32, fp16
 // (IB_PQ_KV_FP16; ib_fp32_to_fp16 rounds to nearest even) or int8
@@ -259,41 +261,45 @@ __global__ __launch_bounds__(kAttnThreads) void v5_attn_kernel(
     float* __restrict__ part, int* __restrict__ counter) {
     constexpr int HALF = HD / 2, NW = kAttnThreads / 64, DPL = HD / 64, PPW = kAttnPos / NW;
     constexpr int KPRE = HD == 64 ? HD / 4 : 1;   // key row held in registers (head_dim 64)
+    constexpr int SPAN = kAttnPos * kAttnTiles;
     __shared__ __align__(16) float qs[GRP][HD];
     __shared__ __align__(16) float kcur[HD], vcur[HD];
     __shared__ float pr[GRP][kAttnPos];
-    __shared__ float gmax[GRP], gsum[GRP];
+    __shared__ float gmax[GRP], gsum[GRP], galpha[GRP];
     __shared__ float vred[NW][GRP][HD];
     __shared__ int last;
     const int kvh = blockIdx.x, sp = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int pos = *dpos, T = pos + 1;
-    const int t0 = sp * kAttnPos, t1 = min(T, t0 + kAttnPos);
-    if (t0 >= t1) return;                       // split past T: nothing to do
-    const int nact = (T + kAttnPos - 1) / kAttnPos, np = t1 - t0;
+    const int b0 = sp * SPAN, b1 = min(T, b0 + SPAN);
+    if (b0 >= b1) return;                       // split past T: nothing to do
+    const int nact = (T + SPAN - 1) / SPAN;
     const int kv_dim = n_kv * HD;
     const size_t hoff = (size_t)kvh * HD;
-    // cache reads first (their latency overlaps the rope below): this
-    // lane's key row and this wavefront's value elements
-    const int t = t0 + lane;
-    const bool act = t < t1;
-    const float kst = (KVT == KV_I8 && act && t != pos) ? ksc[t] : 1.f;
+    // this lane's key row and this wavefront's value elements of one tile
     float4 kreg[KPRE];
-    if constexpr (HD == 64) {
-        if (act && t != pos) {
-#pragma unroll
-            for (int i = 0; i < KPRE; i++) kreg[i] = kv_ld4<KVT>(kc, (size_t)t * kv_dim + hoff + 4 * i, kst);
-        }
-    }
+    float kst = 1.f;
     float vpre[PPW][DPL];
+    auto fetch = [&](int t0) {
+        const int t1 = min(b1, t0 + kAttnPos), t = t0 + lane;
+        const bool ok = t < t1 && t != pos;
+        kst = (KVT == KV_I8 && ok) ? ksc[t] : 1.f;
+        if constexpr (HD == 64) {
+            if (ok) {
 #pragma unroll
-    for (int j = 0; j < PPW; j++) {
-        const int tt = t0 + wave + NW * j;
-        const bool ok = tt < t1 && tt != pos;
-        const float vst = (KVT == KV_I8 && ok) ? vsc[tt] : 1.f;
+                for (int i = 0; i < KPRE; i++) kreg[i] = kv_ld4<KVT>(kc, (size_t)t * kv_dim + hoff + 4 * i, kst);
+            }
+        }
 #pragma unroll
-        for (int jj = 0; jj < DPL; jj++)
-            vpre[j][jj] = ok ? kv_ld<KVT>(vc, (size_t)tt * kv_dim + hoff + lane + 64 * jj, vst) : 0.f;
-    }
+        for (int j = 0; j < PPW; j++) {
+            const int tt = t0 + wave + NW * j;
+            const bool vok = tt < t1 && tt != pos;
+            const float vst = (KVT == KV_I8 && vok) ? vsc[tt] : 1.f;
+#pragma unroll
+            for (int jj = 0; jj < DPL; jj++)
+                vpre[j][jj] = vok ? kv_ld<KVT>(vc, (size_t)tt * kv_dim + hoff + lane + 64 * jj, vst) : 0.f;
+        }
+    };
+    fetch(b0);   // the first tile's reads overlap the rope below
     const float* csp = cs + (size_t)pos * HD;
     for (int e = tid; e < GRP * HALF; e += kAttnThreads) {
         const int g = e / HALF, i = e - g * HALF;
@@ -302,7 +308,11 @@ __global__ __launch_bounds__(kAttnThreads) void v5_attn_kernel(
         qs[g][i] = a * c - b * sn;
         qs[g][i + HALF] = b * c + a * sn;
     }
-    if (t0 <= pos && pos < t1) {
+    if (tid < GRP) {
+        gmax[tid] = -INFINITY;
+        gsum[tid] = 0.f;
+    }
+    if (b0 <= pos && pos < b1) {
         const float* kh = k + hoff;
         const float* vh = v + hoff;
         const size_t rowo = (size_t)pos * kv_dim + hoff;
@@ -380,69 +390,95 @@ __global__ __launch_bounds__(kAttnThreads) void v5_attn_kernel(
         }
     }
     __syncthreads();
-    // scores: lane = position, wavefront = heads w, w + 4, ...
-    if (wave < GRP) {
-        constexpr int HPW = (GRP + NW - 1) / NW;
-        float sc[HPW];
-#pragma unroll
-        for (int h = 0; h < HPW; h++) sc[h] = 0.f;
-        if (act) {
-#pragma unroll
-            for (int d = 0; d < HD; d += 4) {
-                float4 kk;
-                if (t == pos) kk = *(const float4*)(kcur + d);
-                else if constexpr (HD == 64) kk = kreg[d / 4];
-                else kk = kv_ld4<KVT>(kc, (size_t)t * kv_dim + hoff + d, kst);
-#pragma unroll
-                for (int h = 0; h < HPW; h++) {
-                    const int g = wave + NW * h;
-                    if (g < GRP) {
-                        const float4 qq = *(const float4*)(&qs[g][d]);
-                        sc[h] = fmaf(qq.x, kk.x, sc[h]);
-                        sc[h] = fmaf(qq.y, kk.y, sc[h]);
-                        sc[h] = fmaf(qq.z, kk.z, sc[h]);
-                        sc[h] = fmaf(qq.w, kk.w, sc[h]);
-                    }
-                }
-            }
-        }
-#pragma unroll
-        for (int h = 0; h < HPW; h++) {
-            const int g = wave + NW * h;
-            if (g < GRP) {
-                const float x = act ? sc[h] * scale : -INFINITY;
-                const float m = wave_max(x);
-                const float p = act ? __expf(x - m) : 0.f;
-                pr[g][lane] = p;
-                const float sm = wave_sum(p);
-                if (lane == 0) {
-                    gmax[g] = m;
-                    gsum[g] = sm;
-                }
-            }
-        }
-    }
-    __syncthreads();
-    // value sums: lane = dimension(s), wavefront w = positions w, w + 4, ...
     float acc[GRP][DPL];
 #pragma unroll
     for (int g = 0; g < GRP; g++)
 #pragma unroll
         for (int jj = 0; jj < DPL; jj++) acc[g][jj] = 0.f;
+    for (int t0 = b0; t0 < b1; t0 += kAttnPos) {
+        const int t1 = min(b1, t0 + kAttnPos), np = t1 - t0, t = t0 + lane;
+        const bool act = t < t1;
+        // this tile's registers; the next tile's reads go out now
+        float4 kt[KPRE];
+        float vt[PPW][DPL];
+        const float kstt = kst;
 #pragma unroll
-    for (int j = 0; j < PPW; j++) {
-        const int pi = wave + NW * j;
-        if (pi < np) {
-            float vv[DPL];
+        for (int i = 0; i < KPRE; i++) kt[i] = kreg[i];
 #pragma unroll
-            for (int jj = 0; jj < DPL; jj++) vv[jj] = t0 + pi == pos ? vcur[lane + 64 * jj] : vpre[j][jj];
+        for (int j = 0; j < PPW; j++)
 #pragma unroll
-            for (int g = 0; g < GRP; g++) {
-                const float p = pr[g][pi];
+            for (int jj = 0; jj < DPL; jj++) vt[j][jj] = vpre[j][jj];
+        if (t0 + kAttnPos < b1) fetch(t0 + kAttnPos);
+        // scores: lane = position, wavefront = heads w, w + 4, ...; running
+        // max / exp-sum per head kept by its wavefront
+        if (wave < GRP) {
+            constexpr int HPW = (GRP + NW - 1) / NW;
+            float sc[HPW];
 #pragma unroll
-                for (int jj = 0; jj < DPL; jj++) acc[g][jj] = fmaf(p, vv[jj], acc[g][jj]);
+            for (int h = 0; h < HPW; h++) sc[h] = 0.f;
+            if (act) {
+#pragma unroll
+                for (int d = 0; d < HD; d += 4) {
+                    float4 kk;
+                    if (t == pos) kk = *(const float4*)(kcur + d);
+                    else if constexpr (HD == 64) kk = kt[d / 4];
+                    else kk = kv_ld4<KVT>(kc, (size_t)t * kv_dim + hoff + d, kstt);
+#pragma unroll
+                    for (int h = 0; h < HPW; h++) {
+                        const int g = wave + NW * h;
+                        if (g < GRP) {
+                            const float4 qq = *(const float4*)(&qs[g][d]);
+                            sc[h] = fmaf(qq.x, kk.x, sc[h]);
+                            sc[h] = fmaf(qq.y, kk.y, sc[h]);
+                            sc[h] = fmaf(qq.z, kk.z, sc[h]);
+                            sc[h] = fmaf(qq.w, kk.w, sc[h]);
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int h = 0; h < HPW; h++) {
+                const int g = wave + NW * h;
+                if (g < GRP) {
+                    const float x = act ? sc[h] * scale : -INFINITY;
+                    const float mold = gmax[g];
+                    const float mnew = fmaxf(mold, wave_max(x));
+                    const float p = act ? __expf(x - mnew) : 0.f;
+                    pr[g][lane] = p;
+                    const float sm = wave_sum(p);
+                    if (lane == 0) {
+                        const float al = __expf(mold - mnew);   // 0 on the first tile
+                        galpha[g] = al;
+                        gsum[g] = fmaf(gsum[g], al, sm);
+                        gmax[g] = mnew;
+                    }
+                }
             }
         }
+        __syncthreads();
+        // value sums: lane = dimension(s), wavefront w = positions w, w + 4, ...
+#pragma unroll
+        for (int g = 0; g < GRP; g++) {
+            const float al = galpha[g];
+#pragma unroll
+            for (int jj = 0; jj < DPL; jj++) acc[g][jj] *= al;
+        }
+#pragma unroll
+        for (int j = 0; j < PPW; j++) {
+            const int pi = wave + NW * j;
+            if (pi < np) {
+                float vv[DPL];
+#pragma unroll
+                for (int jj = 0; jj < DPL; jj++) vv[jj] = t0 + pi == pos ? vcur[lane + 64 * jj] : vt[j][jj];
+#pragma unroll
+                for (int g = 0; g < GRP; g++) {
+                    const float p = pr[g][pi];
+#pragma unroll
+                    for (int jj = 0; jj < DPL; jj++) acc[g][jj] = fmaf(p, vv[jj], acc[g][jj]);
+                }
+            }
+        }
+        __syncthreads();   // pr / galpha are rewritten by the next tile
     }
 #pragma unroll
     for (int g = 0; g < GRP; g++)
@@ -1114,7 +1150,7 @@ constexpr int kAttnMaxSplits = 1024;
 bool attn_fused_ok(const ibh_v5_session* s, int max_seq) {
     const int grp = s->n_heads / s->n_kv;
     return (s->head_dim == 64 || s->head_dim == 128) && (grp == 1 || grp == 2 || grp == 4 || grp == 8) &&
-           (max_seq + kAttnPos - 1) / kAttnPos <= kAttnMaxSplits && !getenv("IBH_V5_SPLIT_ATTN");
+           (max_seq + kAttnPos * kAttnTiles - 1) / (kAttnPos * kAttnTiles) <= kAttnMaxSplits && !getenv("IBH_V5_SPLIT_ATTN");
 }
 
 int launch_attn_fused(ibh_v5_session* s, ibh_v5_kv* kv, const float* q, const float* k, const float* v, int layer) {
@@ -1441,7 +1477,7 @@ extern "C" int ibh_v5_kv_create(ibh_v5_session* s, int max_seq, ibh_v5_kv** out)
               hipMalloc((void**)&kv->tokens, (size_t)max_seq * 4 + 4) == hipSuccess &&
               hipMalloc((void**)&kv->outs, (size_t)max_seq * 4 + 8) == hipSuccess;
     if (ok && attn_fused_ok(s, max_seq)) {
-        kv->ns = (max_seq + kAttnPos - 1) / kAttnPos;
+        kv->ns = (max_seq + kAttnPos * kAttnTiles - 1) / (kAttnPos * kAttnTiles);
         const size_t pb = (size_t)s->n_kv * kv->ns * (s->n_heads / s->n_kv) * (s->head_dim + 2) * 4;
         ok = hipMalloc((void**)&kv->apart, pb) == hipSuccess && hipMalloc((void**)&kv->acnt, 4 * s->n_kv) == hipSuccess &&
              hipMemset(kv->acnt, 0, 4 * s->n_kv) == hipSuccess;
