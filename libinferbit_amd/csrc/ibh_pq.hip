@@ -463,6 +463,73 @@ __global__ __launch_bounds__(kSelThreads) void pq_topk_select(const float* __res
     for (int i = tid; i < K; i += kSelThreads) sel[i] = tmp[i];
 }
 
+// Two-pass selection for small K on long vectors: every block of
+// kLocalSpan values keeps its K largest (ties: lowest index) in descending
+// order, then the one-block select runs over the B*K candidates.  The global
+// K largest are among the candidates, and the candidates' order (block,
+// rank) agrees with row order among equal values, so the result equals the
+// one-pass select.
+constexpr int kLocalSpan = 1024, kLocalMaxK = 16;
+
+__global__ __launch_bounds__(256) void pq_topk_local(const float* __restrict__ v, int M, int K,
+                                                     float* __restrict__ cval, int32_t* __restrict__ cidx) {
+    constexpr int PER = kLocalSpan / 256;
+    __shared__ uint32_t wk[4];
+    __shared__ int wi[4];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int base = blockIdx.x * kLocalSpan;
+    uint32_t key[PER];   // descending key: smaller = larger value; taken = 0xFFFFFFFF
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int i = base + threadIdx.x + 256 * j;
+        key[j] = i < M ? desc_key(v[i]) : 0xFFFFFFFFu;
+    }
+    for (int r = 0; r < K; r++) {
+        uint32_t bk = 0xFFFFFFFFu;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int j = 0; j < PER; j++) {
+            const int i = base + threadIdx.x + 256 * j;
+            if (key[j] < bk || (key[j] == bk && i < bi)) { bk = key[j]; bi = i; }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const uint32_t ok = __shfl_xor(bk, o, 64);
+            const int oi = __shfl_xor(bi, o, 64);
+            if (ok < bk || (ok == bk && oi < bi)) { bk = ok; bi = oi; }
+        }
+        if (lane == 0) { wk[wave] = bk; wi[wave] = bi; }
+        __syncthreads();
+        uint32_t k2 = wk[0];
+        int i2 = wi[0];
+        for (int w = 1; w < 4; w++)
+            if (wk[w] < k2 || (wk[w] == k2 && wi[w] < i2)) { k2 = wk[w]; i2 = wi[w]; }
+        if (threadIdx.x == 0) {
+            const bool ok = k2 != 0xFFFFFFFFu;
+            cval[blockIdx.x * K + r] = ok ? v[i2] : -INFINITY;
+            cidx[blockIdx.x * K + r] = ok ? i2 : 0x7fffffff;
+        }
+#pragma unroll
+        for (int j = 0; j < PER; j++)
+            if (base + (int)threadIdx.x + 256 * j == i2) key[j] = 0xFFFFFFFFu;
+        __syncthreads();
+    }
+}
+
+// Candidate positions -> rows, in row order (K <= kLocalMaxK).
+__global__ void pq_topk_rows(const int32_t* __restrict__ selc, const int32_t* __restrict__ cidx, int K,
+                             int32_t* __restrict__ sel) {
+    __shared__ int rows[kLocalMaxK];
+    if (threadIdx.x < K) rows[threadIdx.x] = cidx[selc[threadIdx.x]];
+    __syncthreads();
+    if (threadIdx.x < K) {
+        const int r = rows[threadIdx.x];
+        int rank = 0;
+        for (int j = 0; j < K; j++) rank += rows[j] < r;
+        sel[rank] = r;
+    }
+}
+
 // Full-pyramid logits of the selected rows (ib_pq_matmul_fp32_subset,
 // pq_decode.c:2145-2250): one wavefront per row, lanes over chunks; the
 // outlier sidecar in fp32.
@@ -753,7 +820,8 @@ extern "C" size_t ibh_pq_topk_workspace_bytes(const ibh_pq_tensor_abi* t, int k_
     const size_t base = ibh_pq_workspace_bytes(t);
     if (!base || k_top <= 0) return 0;
     auto al = [](size_t v) { return (v + 255) / 256 * 256; };
-    return base + al((size_t)t->M * 4) + 2 * al((size_t)k_top * 4);
+    const size_t nb = ((size_t)t->M + kLocalSpan - 1) / kLocalSpan;   // two-pass select candidates
+    return base + al((size_t)t->M * 4) + 3 * al((size_t)k_top * 4) + 2 * al(nb * kLocalMaxK * 4);
 }
 
 extern "C" int ibh_pq_lm_head_topk(const ibh_pq_tensor_abi* t, const float* x, int k_top, float* out_logits,
@@ -788,8 +856,21 @@ extern "C" int ibh_pq_lm_head_topk(const ibh_pq_tensor_abi* t, const float* x, i
     int rc = pq_run(t, x, coarse, ws, base, stream, md, "ibh_pq_lm_head_topk");
     if (rc) return rc;
     // 2. the K largest, 3. their full-pyramid logits, 4. sorted
-    pq_topk_select<<<1, kSelThreads, 0, st>>>(coarse, t->M, k_top, sel);
-    IBH_CHECK_LAUNCH("ibh_pq_lm_head_topk (select)");
+    const int nb = (t->M + kLocalSpan - 1) / kLocalSpan;
+    if (k_top <= kLocalMaxK && nb >= 4) {
+        int32_t* selc = (int32_t*)((char*)refined + al((size_t)k_top * 4));
+        float* cval = (float*)((char*)selc + al((size_t)k_top * 4));
+        int32_t* cidx = (int32_t*)((char*)cval + al((size_t)nb * kLocalMaxK * 4));
+        pq_topk_local<<<nb, 256, 0, st>>>(coarse, t->M, k_top, cval, cidx);
+        IBH_CHECK_LAUNCH("ibh_pq_lm_head_topk (local select)");
+        pq_topk_select<<<1, kSelThreads, 0, st>>>(cval, nb * k_top, k_top, selc);
+        IBH_CHECK_LAUNCH("ibh_pq_lm_head_topk (select)");
+        pq_topk_rows<<<1, 64, 0, st>>>(selc, cidx, k_top, sel);
+        IBH_CHECK_LAUNCH("ibh_pq_lm_head_topk (rows)");
+    } else {
+        pq_topk_select<<<1, kSelThreads, 0, st>>>(coarse, t->M, k_top, sel);
+        IBH_CHECK_LAUNCH("ibh_pq_lm_head_topk (select)");
+    }
     PqDev d{};
     d.M = t->M; d.N = t->N; d.G = t->G; d.K = t->K; d.K2 = t->K_l2 > 0 ? t->K_l2 : t->K;
     d.n_levels = t->n_levels; d.n_outlier = t->n_outlier; d.C = t->C;
