@@ -17,7 +17,7 @@
 using namespace ibh;
 
 int ibh_launch_rows_grp_multi(const IbhGrpMat* m, int n, const float* x, bool awq, const float* xo, int N, int G,
-                              hipStream_t st);
+                              hipStream_t st, const float* up);
 int ibh_launch_rows_grp(float* out, const uint8_t* q, const uint16_t* s, const float* x, bool awq, const float* xo,
                         const float* ia, const uint16_t* oi, const uint16_t* ov, int M, int N, int G, int K_out,
                         hipStream_t st);
@@ -144,7 +144,19 @@ int ibh_int4g_matmul_group(const ibh_int4g_tensor* const* t, float* const* out, 
         m[i] = IbhGrpMat{t[i]->q, t[i]->s, t[i]->inv_act, t[i]->outl_idx, t[i]->outl_val, out[i], t[i]->M,
                          t[i]->K_out};
     }
-    if (!ibh_launch_rows_grp_multi(m, n, x, awq, x, t[0]->N, t[0]->G, st)) return 0;
+    if (!ibh_launch_rows_grp_multi(m, n, x, awq, x, t[0]->N, t[0]->G, st, nullptr)) return 0;
+    return hipGetLastError() == hipSuccess ? 1 : -1;
+}
+
+// The MLP's down projection on silu(gate) * up, the activation formed in the
+// matvec's prologue (ib_silu_gate_f32 then the INT4 branch).  Returns 1 when
+// launched; 0 when not eligible (AWQ scales, a skip mask, or a shape the
+// kernel does not take): nothing was launched.
+int ibh_int4g_matmul_silu(const ibh_int4g_tensor* t, const float* gate, const float* up, float* out, float rel,
+                          hipStream_t st) {
+    if (rel > 0.f || t->inv_act || (t->K_out > 0 && (!t->outl_idx || !t->outl_val))) return 0;
+    const IbhGrpMat m{t->q, t->s, nullptr, t->outl_idx, t->outl_val, out, t->M, t->K_out};
+    if (!ibh_launch_rows_grp_multi(&m, 1, gate, false, gate, t->N, t->G, st, up)) return 0;
     return hipGetLastError() == hipSuccess ? 1 : -1;
 }
 

@@ -486,10 +486,17 @@ struct GrpSet {
     int K_out[kGrpSegs];
 };
 
-template <int NXQ, bool AWQ>
+// silu(g) = g / (1 + e^-g) (ib_silu_gate_f32, pq_decode.c:4610-4616; the
+// hardware exp, a few ulp).
+__device__ __forceinline__ float silu_f(float g) { return g / (1.0f + __expf(-g)); }
+
+// MODE 0: xk = x; 1 (AWQ): xk = x * inv_act; 2 (SILU): xk = silu(x) * x2, the
+// MLP's silu(gate) * up fused into the down projection (x = gate, x2 = up).
+template <int NXQ, int MODE>
 __global__ __launch_bounds__(1024) void gemv_rows_grp(const GrpSet gs, const float* __restrict__ x,
-                                                      const float* __restrict__ xo, int N, int G, int S, int WR,
-                                                      int KW) {
+                                                      const float* __restrict__ x2, const float* __restrict__ xo,
+                                                      int N, int G, int S, int WR, int KW) {
+    constexpr bool AWQ = MODE != 0;   // a second float4 stream per slice (inv_act or up)
     constexpr int R = 4, SPW = 2, NA = 2;
     int seg = 0;
 #pragma unroll
@@ -529,7 +536,8 @@ __global__ __launch_bounds__(1024) void gemv_rows_grp(const GrpSet gs, const flo
     for (int q = 0; q < NXQ; q++) {
         const int c = min(4 * ((int)threadIdx.x + q * nth), N - 4);
         xv[q] = *(const float4*)(x + c);
-        if constexpr (AWQ) av[q] = *(const float4*)(ia + c);
+        if constexpr (MODE == 1) av[q] = *(const float4*)(ia + c);
+        if constexpr (MODE == 2) av[q] = *(const float4*)(x2 + c);
     }
     // 1b. outlier sidecar of the wavefront's rows (waves of K-slice 0): up to
     // 128 (row, k) pairs, two per lane; index and value now, x after the
@@ -572,14 +580,19 @@ __global__ __launch_bounds__(1024) void gemv_rows_grp(const GrpSet gs, const flo
 #pragma unroll
         for (int u = 0; u < 2; u++) {
             oxv[u] = xo[ojx[u]];
-            if (ia) oav[u] = ia[ojx[u]];
+            if constexpr (MODE == 2) oav[u] = x2[ojx[u]];
+            else if (ia) oav[u] = ia[ojx[u]];
         }
     }
 #pragma unroll
     for (int q = 0; q < NXQ; q++) {
         const int c = 4 * ((int)threadIdx.x + q * nth);
-        if constexpr (AWQ) {
+        if constexpr (MODE == 1) {
             xv[q].x *= av[q].x; xv[q].y *= av[q].y; xv[q].z *= av[q].z; xv[q].w *= av[q].w;
+        }
+        if constexpr (MODE == 2) {
+            xv[q].x = silu_f(xv[q].x) * av[q].x; xv[q].y = silu_f(xv[q].y) * av[q].y;
+            xv[q].z = silu_f(xv[q].z) * av[q].z; xv[q].w = silu_f(xv[q].w) * av[q].w;
         }
         if (c >= N) xv[q] = float4{0.f, 0.f, 0.f, 0.f};
     }
@@ -665,7 +678,9 @@ __global__ __launch_bounds__(1024) void gemv_rows_grp(const GrpSet gs, const flo
     float tot[R], osum[R], oprod[2];
 #pragma unroll
     for (int u = 0; u < 2; u++)
-        oprod[u] = orr[u] >= 0 ? f16_to_f32((uint16_t)ovh[u]) * (ia ? oxv[u] * oav[u] : oxv[u]) : 0.f;
+        oprod[u] = orr[u] >= 0 ? f16_to_f32((uint16_t)ovh[u]) *
+                                     (MODE == 2 ? silu_f(oxv[u]) * oav[u] : (ia ? oxv[u] * oav[u] : oxv[u]))
+                               : 0.f;
 #pragma unroll
     for (int r = 0; r < R; r++) {
         tot[r] = diag_sum(f[r]);
@@ -677,7 +692,8 @@ __global__ __launch_bounds__(1024) void gemv_rows_grp(const GrpSet gs, const flo
         if (R * K_out > 128) {
             for (int k = 0; k < K_out; k++) {
                 const int jj = oi[(size_t)row * K_out + k];
-                acc = fmaf(f16_to_f32(ov[(size_t)row * K_out + k]), ia ? xo[jj] * ia[jj] : xo[jj], acc);
+                const float xk = MODE == 2 ? silu_f(xo[jj]) * x2[jj] : (ia ? xo[jj] * ia[jj] : xo[jj]);
+                acc = fmaf(f16_to_f32(ov[(size_t)row * K_out + k]), xk, acc);
             }
         } else {
             acc += o;
@@ -814,9 +830,12 @@ int ibh_launch_rows_x(float* out, const void* w, const void* scales, int kind, c
 // and G, one launch.  x: the activation to digitise; awq: x is multiplied by
 // each matrix's inv_act in-kernel (ia then required); xo/ia: what the
 // outlier sidecar reads (xk[j] = xo[j] * ia[j], or xo[j] when ia is NULL).
+// up: x is the MLP gate and xk = silu(x) * up (xo = x then; no AWQ).
 // Returns 1 if launched, 0 if not eligible (the caller runs its own path).
 int ibh_launch_rows_grp_multi(const IbhGrpMat* m, int n, const float* x, bool awq, const float* xo, int N, int G,
-                              hipStream_t st) {
+                              hipStream_t st, const float* up) {
+    // up != null: x is the MLP gate, xk = silu(x) * up (no inv_act then)
+    if (up && (awq || ((uintptr_t)up & 15))) return 0;
     if (n < 1 || n > kGrpSegs || N % 32 != 0 || G % 128 != 0 || N % G != 0 || N > 131072 || ((uintptr_t)x & 15))
         return 0;
     int Mtot = 0;
@@ -833,7 +852,7 @@ int ibh_launch_rows_grp_multi(const IbhGrpMat* m, int n, const float* x, bool aw
     while (WR > 1 && (WR * KW > kMaxWaves || (Mtot + WR * R - 1) / (WR * R) < 384)) WR >>= 1;
     if (WR * KW > kMaxWaves) return 0;
     // x (and inv_act) slices live in registers: at most 8 per thread, 4 with AWQ
-    const int cap = awq ? 4 : 8;
+    const int cap = (awq || up) ? 4 : 8;
     while ((N / 4 + 64 * WR * KW - 1) / (64 * WR * KW) > cap && 2 * WR * KW <= kMaxWaves) WR *= 2;
     const int nthreads = 64 * WR * KW;
     const int nxq = (N / 4 + nthreads - 1) / nthreads;
@@ -855,12 +874,14 @@ int ibh_launch_rows_grp_multi(const IbhGrpMat* m, int n, const float* x, bool aw
         gs.K_out[i] = m[i].K_out;
         blocks += (m[i].M + WR * R - 1) / (WR * R);
     }
-#define IBH_RG(Q_, A_) gemv_rows_grp<Q_, A_><<<blocks, nthreads, lds, st>>>(gs, x, xo, N, G, S, WR, KW)
-    if (awq) {
-        if (nxq <= 1) IBH_RG(1, true); else if (nxq <= 2) IBH_RG(2, true); else IBH_RG(4, true);
+#define IBH_RG(Q_, A_) gemv_rows_grp<Q_, A_><<<blocks, nthreads, lds, st>>>(gs, x, up, xo, N, G, S, WR, KW)
+    if (up) {
+        if (nxq <= 1) IBH_RG(1, 2); else if (nxq <= 2) IBH_RG(2, 2); else IBH_RG(4, 2);
+    } else if (awq) {
+        if (nxq <= 1) IBH_RG(1, 1); else if (nxq <= 2) IBH_RG(2, 1); else IBH_RG(4, 1);
     } else {
-        if (nxq <= 1) IBH_RG(1, false); else if (nxq <= 2) IBH_RG(2, false);
-        else if (nxq <= 4) IBH_RG(4, false); else IBH_RG(8, false);
+        if (nxq <= 1) IBH_RG(1, 0); else if (nxq <= 2) IBH_RG(2, 0);
+        else if (nxq <= 4) IBH_RG(4, 0); else IBH_RG(8, 0);
     }
 #undef IBH_RG
     return 1;
@@ -870,5 +891,5 @@ int ibh_launch_rows_grp(float* out, const uint8_t* q, const uint16_t* s, const f
                         const float* ia, const uint16_t* oi, const uint16_t* ov, int M, int N, int G, int K_out,
                         hipStream_t st) {
     const IbhGrpMat m{q, s, ia, oi, ov, out, M, K_out};
-    return ibh_launch_rows_grp_multi(&m, 1, x, awq, xo, N, G, st);
+    return ibh_launch_rows_grp_multi(&m, 1, x, awq, xo, N, G, st, nullptr);
 }

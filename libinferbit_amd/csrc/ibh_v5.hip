@@ -45,6 +45,8 @@ int ibh_launch_attn(float* out, const float* q, const void* kdata, const void* v
 
 int ibh_int4g_matmul_group(const ibh_int4g_tensor* const* t, float* const* out, int n, const float* x, float rel,
                            hipStream_t st);
+int ibh_int4g_matmul_silu(const ibh_int4g_tensor* t, const float* gate, const float* up, float* out, float rel,
+                          hipStream_t st);
 
 namespace {
 
@@ -611,7 +613,7 @@ struct ibh_v5_session {
     void* ws = nullptr;
     size_t ws_bytes = 0;
     unsigned epoch = 1;   // bumped by policy changes: captured steps are stale
-    bool no_group = false;   // IBH_V5_NO_GROUP=1: one launch per matrix
+    bool no_group = false;   // IBH_V5_NO_GROUP=1: one launch per matrix, silu separate
 };
 
 struct ibh_v5_kv {
@@ -1260,9 +1262,20 @@ int forward_dev(ibh_v5_session* s, ibh_v5_kv* kv, bool want_logits) {
             float* const o[2] = {g, u};
             if ((rc = matmul_set(s, mi, o, 2, s->xb))) return rc;
         }
-        v5_silu_kernel<<<(I + 255) / 256, 256, 0, s->st>>>(s->gate, g, u, I);
-        IBH_CHECK_LAUNCH("ibh_v5: silu");
-        if ((rc = matmul(s, s->md[l], s->gate, s->delta))) return rc;
+        // silu(gate) * up formed inside the INT4 down launch when it can be
+        int fused = 0;
+        if (s->mats[s->md[l]].kind == MAT_INT4 && !s->no_group) {
+            fused = ibh_int4g_matmul_silu(&s->mats[s->md[l]].i4, g, u, s->delta, s->act_sparse_rel, s->st);
+            if (fused < 0) {
+                ibh_set_error("ibh_v5: fused silu + down launch failed");
+                return IBH_ERROR_INTERNAL;
+            }
+        }
+        if (!fused) {
+            v5_silu_kernel<<<(I + 255) / 256, 256, 0, s->st>>>(s->gate, g, u, I);
+            IBH_CHECK_LAUNCH("ibh_v5: silu");
+            if ((rc = matmul(s, s->md[l], s->gate, s->delta))) return rc;
+        }
         pending = s->delta;
     }
     v5_rmsnorm_kernel<<<1, norm_threads(H), 0, s->st>>>(s->xb, s->x, pending, s->w_final, s->eps, H, dpos);

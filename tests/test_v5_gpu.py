@@ -206,8 +206,11 @@ def test_policy_change_recaptures(L, tmp_path_factory, tmp_path):
 
 
 def test_grouped_int4_launch_matches_single(L, tmp_path_factory, monkeypatch):
-    """q/k/v and gate/up run as one matrix-core launch per set; the per-row
-    arithmetic is that of one launch per matrix, so logits are bit-equal."""
+    """q/k/v and gate/up run as one matrix-core launch per set and silu * up
+    is formed inside the down launch; IBH_V5_NO_GROUP=1 runs one launch per
+    matrix and a separate silu.  The per-row arithmetic is the same except
+    the silu exponential (hardware exp in the fused launch, the glibc-exact
+    one in the separate kernel): logits agree to 1e-5."""
     from libinferbit_amd.session import PqSession
     path = model(tmp_path_factory, "int4_awq_outl")
     S = PqSession(path)
@@ -215,7 +218,7 @@ def test_grouped_int4_launch_matches_single(L, tmp_path_factory, monkeypatch):
     monkeypatch.setenv("IBH_V5_NO_GROUP", "1")
     S1 = PqSession(path)
     _, b = gpu_steps(S1, PROMPT, 2)
-    np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert relerr(a, b) <= 1e-5
 
 
 @pytest.mark.parametrize("split_env", ["", "1"])
