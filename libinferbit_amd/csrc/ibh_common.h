@@ -154,6 +154,12 @@ struct IbhGrpMat {
     float* out;
     int M, K_out;
 };
+// Residual add + rmsnorm fused in front of a multi-matrix launch.
+struct IbhGrpNorm {
+    const float* dl;   // residual delta added to x (null: none)
+    float* xr;         // where block 0 writes x + dl (null: not written)
+    float eps;
+};
 // Host side: one matrix of a set.
 
 struct MatDesc {

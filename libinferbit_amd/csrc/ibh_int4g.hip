@@ -17,7 +17,7 @@
 using namespace ibh;
 
 int ibh_launch_rows_grp_multi(const IbhGrpMat* m, int n, const float* x, bool awq, const float* xo, int N, int G,
-                              hipStream_t st, const float* up);
+                              hipStream_t st, const float* up, const IbhGrpNorm* nrm);
 int ibh_launch_rows_grp(float* out, const uint8_t* q, const uint16_t* s, const float* x, bool awq, const float* xo,
                         const float* ia, const uint16_t* oi, const uint16_t* ov, int M, int N, int G, int K_out,
                         hipStream_t st);
@@ -144,7 +144,7 @@ int ibh_int4g_matmul_group(const ibh_int4g_tensor* const* t, float* const* out, 
         m[i] = IbhGrpMat{t[i]->q, t[i]->s, t[i]->inv_act, t[i]->outl_idx, t[i]->outl_val, out[i], t[i]->M,
                          t[i]->K_out};
     }
-    if (!ibh_launch_rows_grp_multi(m, n, x, awq, x, t[0]->N, t[0]->G, st, nullptr)) return 0;
+    if (!ibh_launch_rows_grp_multi(m, n, x, awq, x, t[0]->N, t[0]->G, st, nullptr, nullptr)) return 0;
     return hipGetLastError() == hipSuccess ? 1 : -1;
 }
 
@@ -156,7 +156,27 @@ int ibh_int4g_matmul_silu(const ibh_int4g_tensor* t, const float* gate, const fl
                           hipStream_t st) {
     if (rel > 0.f || t->inv_act || (t->K_out > 0 && (!t->outl_idx || !t->outl_val))) return 0;
     const IbhGrpMat m{t->q, t->s, nullptr, t->outl_idx, t->outl_val, out, t->M, t->K_out};
-    if (!ibh_launch_rows_grp_multi(&m, 1, gate, false, gate, t->N, t->G, st, up)) return 0;
+    if (!ibh_launch_rows_grp_multi(&m, 1, gate, false, gate, t->N, t->G, st, up, nullptr)) return 0;
+    return hipGetLastError() == hipSuccess ? 1 : -1;
+}
+
+// Residual add + rmsnorm + up to three INT4 matrices reading the normed x
+// (a layer's q/k/v or gate/up), one launch: xin = x + dl, xk = (xin * inv) *
+// wia[i] with wia[i] = norm weight * the matrix's AWQ vector (or the norm
+// weight); block 0 writes xin to xr.  Returns 1 when launched, 0 when not
+// eligible (nothing launched), -1 on a launch error.
+int ibh_int4g_matmul_group_norm(const ibh_int4g_tensor* const* t, const float* const* wia, float* const* out, int n,
+                                const float* x, const float* dl, float* xr, float eps, float rel, hipStream_t st) {
+    if (n < 1 || n > 3 || rel > 0.f) return 0;
+    IbhGrpMat m[3];
+    for (int i = 0; i < n; i++) {
+        if (t[i]->N != t[0]->N || t[i]->G != t[0]->G || !wia[i] ||
+            (t[i]->K_out > 0 && (!t[i]->outl_idx || !t[i]->outl_val)))
+            return 0;
+        m[i] = IbhGrpMat{t[i]->q, t[i]->s, wia[i], t[i]->outl_idx, t[i]->outl_val, out[i], t[i]->M, t[i]->K_out};
+    }
+    const IbhGrpNorm nrm{dl, xr, eps};
+    if (!ibh_launch_rows_grp_multi(m, n, x, false, x, t[0]->N, t[0]->G, st, nullptr, &nrm)) return 0;
     return hipGetLastError() == hipSuccess ? 1 : -1;
 }
 

@@ -491,12 +491,20 @@ struct GrpSet {
 __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + __expf(-g)); }
 
 // MODE 0: xk = x; 1 (AWQ): xk = x * inv_act; 2 (SILU): xk = silu(x) * x2, the
-// MLP's silu(gate) * up fused into the down projection (x = gate, x2 = up).
+// MLP's silu(gate) * up fused into the down projection (x = gate, x2 = up);
+// 3 (NORM): the residual add and rmsnorm of the layer fused in front:
+// xin = x + dl (dl may be null), inv = 1 / sqrtf((float)(sum_double xin^2 / N)
+// + eps), xk = (xin * inv) * ia with ia = the norm weight (times the AWQ
+// vector when the matrix has one); block 0 writes xin to xr (the new
+// residual stream) when xr is not null.
 template <int NXQ, int MODE>
 __global__ __launch_bounds__(1024) void gemv_rows_grp(const GrpSet gs, const float* __restrict__ x,
                                                       const float* __restrict__ x2, const float* __restrict__ xo,
-                                                      int N, int G, int S, int WR, int KW) {
-    constexpr bool AWQ = MODE != 0;   // a second float4 stream per slice (inv_act or up)
+                                                      int N, int G, int S, int WR, int KW,
+                                                      const float* __restrict__ dl, float* __restrict__ xr,
+                                                      float eps) {
+    constexpr bool AWQ = MODE != 0;   // a second float4 stream per slice (inv_act, up or norm weight)
+    constexpr bool NORM = MODE == 3;
     constexpr int R = 4, SPW = 2, NA = 2;
     int seg = 0;
 #pragma unroll
@@ -531,12 +539,13 @@ __global__ __launch_bounds__(1024) void gemv_rows_grp(const GrpSet gs, const flo
     // 1. x and inv_act, coalesced float4 slices
     // (AWQ is instantiated for NXQ <= 4 only: eight inv_act slices spill)
     static_assert(!AWQ || NXQ <= 4, "AWQ with NXQ > 4");
-    float4 xv[NXQ], av[AWQ ? NXQ : 1];
+    float4 xv[NXQ], av[AWQ ? NXQ : 1], dv[NORM ? NXQ : 1];
 #pragma unroll
     for (int q = 0; q < NXQ; q++) {
         const int c = min(4 * ((int)threadIdx.x + q * nth), N - 4);
         xv[q] = *(const float4*)(x + c);
-        if constexpr (MODE == 1) av[q] = *(const float4*)(ia + c);
+        if constexpr (MODE == 1 || MODE == 3) av[q] = *(const float4*)(ia + c);
+        if constexpr (NORM) dv[q] = dl ? *(const float4*)(dl + c) : float4{0.f, 0.f, 0.f, 0.f};
         if constexpr (MODE == 2) av[q] = *(const float4*)(x2 + c);
     }
     // 1b. outlier sidecar of the wavefront's rows (waves of K-slice 0): up to
@@ -580,6 +589,9 @@ __global__ __launch_bounds__(1024) void gemv_rows_grp(const GrpSet gs, const flo
 #pragma unroll
         for (int u = 0; u < 2; u++) {
             oxv[u] = xo[ojx[u]];
+            if constexpr (NORM) {
+                if (dl) oxv[u] += dl[ojx[u]];
+            }
             if constexpr (MODE == 2) oav[u] = x2[ojx[u]];
             else if (ia) oav[u] = ia[ojx[u]];
         }
@@ -594,7 +606,32 @@ __global__ __launch_bounds__(1024) void gemv_rows_grp(const GrpSet gs, const flo
             xv[q].x = silu_f(xv[q].x) * av[q].x; xv[q].y = silu_f(xv[q].y) * av[q].y;
             xv[q].z = silu_f(xv[q].z) * av[q].z; xv[q].w = silu_f(xv[q].w) * av[q].w;
         }
+        if constexpr (NORM) {
+            xv[q].x += dv[q].x; xv[q].y += dv[q].y; xv[q].z += dv[q].z; xv[q].w += dv[q].w;
+            if (xr && blockIdx.x == 0 && c < N) *(float4*)(xr + c) = xv[q];
+        }
         if (c >= N) xv[q] = float4{0.f, 0.f, 0.f, 0.f};
+    }
+    float ninv = 1.f;
+    if constexpr (NORM) {
+        __shared__ double redd[kMaxWaves];
+        double ss = 0.0;
+#pragma unroll
+        for (int q = 0; q < NXQ; q++)
+            ss += ((double)xv[q].x * (double)xv[q].x + (double)xv[q].y * (double)xv[q].y) +
+                  ((double)xv[q].z * (double)xv[q].z + (double)xv[q].w * (double)xv[q].w);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        if (lane == 0) redd[wave] = ss;
+        __syncthreads();
+        double tot = 0.0;
+        for (int w = 0; w < (nth >> 6); w++) tot += redd[w];
+        ninv = 1.0f / sqrtf((float)(tot / (double)N) + eps);
+#pragma unroll
+        for (int q = 0; q < NXQ; q++) {
+            xv[q].x = (xv[q].x * ninv) * av[q].x; xv[q].y = (xv[q].y * ninv) * av[q].y;
+            xv[q].z = (xv[q].z * ninv) * av[q].z; xv[q].w = (xv[q].w * ninv) * av[q].w;
+        }
     }
     // 3. max|xk|
     float mx = 0.f;
@@ -679,7 +716,9 @@ __global__ __launch_bounds__(1024) void gemv_rows_grp(const GrpSet gs, const flo
 #pragma unroll
     for (int u = 0; u < 2; u++)
         oprod[u] = orr[u] >= 0 ? f16_to_f32((uint16_t)ovh[u]) *
-                                     (MODE == 2 ? silu_f(oxv[u]) * oav[u] : (ia ? oxv[u] * oav[u] : oxv[u]))
+                                     (MODE == 2 ? silu_f(oxv[u]) * oav[u]
+                                      : NORM    ? (oxv[u] * ninv) * oav[u]
+                                                : (ia ? oxv[u] * oav[u] : oxv[u]))
                                : 0.f;
 #pragma unroll
     for (int r = 0; r < R; r++) {
@@ -692,7 +731,9 @@ __global__ __launch_bounds__(1024) void gemv_rows_grp(const GrpSet gs, const flo
         if (R * K_out > 128) {
             for (int k = 0; k < K_out; k++) {
                 const int jj = oi[(size_t)row * K_out + k];
-                const float xk = MODE == 2 ? silu_f(xo[jj]) * x2[jj] : (ia ? xo[jj] * ia[jj] : xo[jj]);
+                const float xk = MODE == 2 ? silu_f(xo[jj]) * x2[jj]
+                                 : NORM    ? ((xo[jj] + (dl ? dl[jj] : 0.f)) * ninv) * ia[jj]
+                                           : (ia ? xo[jj] * ia[jj] : xo[jj]);
                 acc = fmaf(f16_to_f32(ov[(size_t)row * K_out + k]), xk, acc);
             }
         } else {
@@ -833,9 +874,17 @@ int ibh_launch_rows_x(float* out, const void* w, const void* scales, int kind, c
 // up: x is the MLP gate and xk = silu(x) * up (xo = x then; no AWQ).
 // Returns 1 if launched, 0 if not eligible (the caller runs its own path).
 int ibh_launch_rows_grp_multi(const IbhGrpMat* m, int n, const float* x, bool awq, const float* xo, int N, int G,
-                              hipStream_t st, const float* up) {
-    // up != null: x is the MLP gate, xk = silu(x) * up (no inv_act then)
-    if (up && (awq || ((uintptr_t)up & 15))) return 0;
+                              hipStream_t st, const float* up, const IbhGrpNorm* nrm) {
+    // up != null: x is the MLP gate, xk = silu(x) * up (no inv_act then);
+    // nrm != null: residual add + rmsnorm in front (each matrix's ia = its
+    // norm weight, times its AWQ vector)
+    if (up && (awq || nrm || ((uintptr_t)up & 15))) return 0;
+    if (nrm && (((uintptr_t)nrm->dl & 15) || ((uintptr_t)nrm->xr & 15))) return 0;
+    if (nrm) {
+        for (int i = 0; i < n; i++)
+            if (!m[i].ia || ((uintptr_t)m[i].ia & 15)) return 0;
+        awq = false;
+    }
     if (n < 1 || n > kGrpSegs || N % 32 != 0 || G % 128 != 0 || N % G != 0 || N > 131072 || ((uintptr_t)x & 15))
         return 0;
     int Mtot = 0;
@@ -852,7 +901,7 @@ int ibh_launch_rows_grp_multi(const IbhGrpMat* m, int n, const float* x, bool aw
     while (WR > 1 && (WR * KW > kMaxWaves || (Mtot + WR * R - 1) / (WR * R) < 384)) WR >>= 1;
     if (WR * KW > kMaxWaves) return 0;
     // x (and inv_act) slices live in registers: at most 8 per thread, 4 with AWQ
-    const int cap = (awq || up) ? 4 : 8;
+    const int cap = nrm ? 2 : ((awq || up) ? 4 : 8);
     while ((N / 4 + 64 * WR * KW - 1) / (64 * WR * KW) > cap && 2 * WR * KW <= kMaxWaves) WR *= 2;
     const int nthreads = 64 * WR * KW;
     const int nxq = (N / 4 + nthreads - 1) / nthreads;
@@ -874,8 +923,13 @@ int ibh_launch_rows_grp_multi(const IbhGrpMat* m, int n, const float* x, bool aw
         gs.K_out[i] = m[i].K_out;
         blocks += (m[i].M + WR * R - 1) / (WR * R);
     }
-#define IBH_RG(Q_, A_) gemv_rows_grp<Q_, A_><<<blocks, nthreads, lds, st>>>(gs, x, up, xo, N, G, S, WR, KW)
-    if (up) {
+    const float* ndl = nrm ? nrm->dl : nullptr;
+    float* nxr = nrm ? nrm->xr : nullptr;
+    const float neps = nrm ? nrm->eps : 0.f;
+#define IBH_RG(Q_, A_) gemv_rows_grp<Q_, A_><<<blocks, nthreads, lds, st>>>(gs, x, up, xo, N, G, S, WR, KW, ndl, nxr, neps)
+    if (nrm) {
+        if (nxq <= 1) IBH_RG(1, 3); else IBH_RG(2, 3);
+    } else if (up) {
         if (nxq <= 1) IBH_RG(1, 2); else if (nxq <= 2) IBH_RG(2, 2); else IBH_RG(4, 2);
     } else if (awq) {
         if (nxq <= 1) IBH_RG(1, 1); else if (nxq <= 2) IBH_RG(2, 1); else IBH_RG(4, 1);
@@ -891,5 +945,5 @@ int ibh_launch_rows_grp(float* out, const uint8_t* q, const uint16_t* s, const f
                         const float* ia, const uint16_t* oi, const uint16_t* ov, int M, int N, int G, int K_out,
                         hipStream_t st) {
     const IbhGrpMat m{q, s, ia, oi, ov, out, M, K_out};
-    return ibh_launch_rows_grp_multi(&m, 1, x, awq, xo, N, G, st, nullptr);
+    return ibh_launch_rows_grp_multi(&m, 1, x, awq, xo, N, G, st, nullptr, nullptr);
 }

@@ -31,6 +31,7 @@
 #include <unistd.h>
 
 #include <algorithm>
+#include <array>
 #include <string>
 #include <vector>
 
@@ -47,6 +48,8 @@ int ibh_int4g_matmul_group(const ibh_int4g_tensor* const* t, float* const* out, 
                            hipStream_t st);
 int ibh_int4g_matmul_silu(const ibh_int4g_tensor* t, const float* gate, const float* up, float* out, float rel,
                           hipStream_t st);
+int ibh_int4g_matmul_group_norm(const ibh_int4g_tensor* const* t, const float* const* wia, float* const* out, int n,
+                                const float* x, const float* dl, float* xr, float eps, float rel, hipStream_t st);
 
 namespace {
 
@@ -607,6 +610,10 @@ struct ibh_v5_session {
     int embed_rows = 0;
     // activations
     float *x = nullptr, *xb = nullptr, *xb2 = nullptr, *q = nullptr, *kn = nullptr, *vn = nullptr, *qkv = nullptr;
+    float* xalt = nullptr;   // second residual buffer (norm-fused launches write x + delta there)
+    // norm weight * AWQ vector (or the norm weight) per layer for q/k/v and
+    // gate/up when they are INT4: the norm-fused launches' input scales
+    std::vector<std::array<const float*, 3>> wia_in, wia_pn;
     float *gate = nullptr, *up = nullptr, *gu = nullptr, *delta = nullptr, *xs = nullptr, *logits = nullptr;
     float* top_val = nullptr;
     int32_t* top_ids = nullptr;
@@ -1108,7 +1115,7 @@ int open_session(ibh_v5_session* s, const char* path) {
 
     // activations and one shared workspace (every launch is on one stream)
     const int maxN = std::max(std::max(H, I), H + 2 * KV);
-    float** bufs[] = {&s->x, &s->xb, &s->xb2, &s->q, &s->kn, &s->vn, &s->delta};
+    float** bufs[] = {&s->x, &s->xalt, &s->xb, &s->xb2, &s->q, &s->kn, &s->vn, &s->delta};
     for (float** b : bufs)
         if ((rc = salloc(s, (void**)b, (size_t)H * 4 + 256))) return rc;
     if ((rc = salloc(s, (void**)&s->qkv, (size_t)(H + 2 * KV) * 4)) || (rc = salloc(s, (void**)&s->gate, (size_t)I * 4)) ||
@@ -1125,6 +1132,39 @@ int open_session(ibh_v5_session* s, const char* path) {
     if (s->mats[s->m_head].kind == MAT_PQ) ws = std::max(ws, ibh_pq_topk_workspace_bytes(&s->mats[s->m_head].pq, 256));
     s->ws_bytes = ws;
     if ((rc = salloc(s, &s->ws, ws))) return rc;
+    // inputs of the norm-fused INT4 launches: norm weight (* AWQ vector)
+    s->wia_in.assign(L, {nullptr, nullptr, nullptr});
+    s->wia_pn.assign(L, {nullptr, nullptr, nullptr});
+    {
+        std::vector<float> w(std::max(H, I)), a(std::max(H, I));
+        auto make = [&](const float* wdev, int mi, const float** dst) -> int {
+            const Mat& m = s->mats[mi];
+            if (m.kind != MAT_INT4 || m.N != H) return IBH_OK;
+            IBH_HIP(hipMemcpy(w.data(), wdev, (size_t)H * 4, hipMemcpyDeviceToHost), "ibh_v5_open: norm weight");
+            if (m.i4.inv_act) {
+                IBH_HIP(hipMemcpy(a.data(), m.i4.inv_act, (size_t)H * 4, hipMemcpyDeviceToHost), "ibh_v5_open: act scale");
+                for (int j = 0; j < H; j++) a[j] = w[j] * a[j];
+            } else {
+                for (int j = 0; j < H; j++) a[j] = w[j];
+            }
+            void* d;
+            int r;
+            if ((r = salloc(s, &d, (size_t)H * 4))) return r;
+            IBH_HIP(hipMemcpy(d, a.data(), (size_t)H * 4, hipMemcpyHostToDevice), "ibh_v5_open: upload");
+            *dst = (const float*)d;
+            return IBH_OK;
+        };
+        for (int l = 0; l < L && !s->fused_qkv; l++) {
+            const int mi[3] = {s->mq[l], s->mk[l], s->mv[l]};
+            for (int i = 0; i < 3; i++)
+                if ((rc = make(s->w_in[l], mi[i], &s->wia_in[l][i]))) return rc;
+        }
+        for (int l = 0; l < L && !s->fused_gu; l++) {
+            const int mi[2] = {s->mg[l], s->mu[l]};
+            for (int i = 0; i < 2; i++)
+                if ((rc = make(s->w_pn[l], mi[i], &s->wia_pn[l][i]))) return rc;
+        }
+    }
     IBH_HIP(hipStreamCreateWithFlags(&s->st, hipStreamNonBlocking), "ibh_v5_open: stream");
     return IBH_OK;
 }
@@ -1213,22 +1253,50 @@ int norm_threads(int) { return kNormThreads; }
 int forward_dev(ibh_v5_session* s, ibh_v5_kv* kv, bool want_logits) {
     const int H = s->hidden, KV = s->kv_dim, I = s->inter, hd = s->head_dim;
     int* dpos = kv->state;
+    float *xcur = s->x, *xalt = s->xalt;   // residual stream, ping-pong under the norm-fused launches
     if (s->embed_kind == 2) {
         const ibh_pq_tensor& t = s->mats[s->embed_mat].pq;
         const int n = t.C * t.G + t.n_outlier;
-        pq_row_kernel<<<(n + 255) / 256, 256, 0, s->st>>>(s->x, t, kv->tokens, dpos);
+        pq_row_kernel<<<(n + 255) / 256, 256, 0, s->st>>>(xcur, t, kv->tokens, dpos);
     } else {
-        embed_raw_kernel<<<(H + 255) / 256, 256, 0, s->st>>>(s->x, s->embed, s->embed_kind, kv->tokens, dpos,
+        embed_raw_kernel<<<(H + 255) / 256, 256, 0, s->st>>>(xcur, s->embed, s->embed_kind, kv->tokens, dpos,
                                                              s->embed_rows, H);
     }
+    // residual add + rmsnorm fused into a set of INT4 launches (1 = done)
+    auto norm_set = [&](const std::array<const float*, 3>& wia, const int* mi, float* const* o, int n,
+                        const float* dl) -> int {
+        if (s->no_group) return 0;
+        const ibh_int4g_tensor* t[3];
+        for (int i = 0; i < n; i++) {
+            if (!wia[i] || s->mats[mi[i]].kind != MAT_INT4) return 0;
+            t[i] = &s->mats[mi[i]].i4;
+        }
+        const int r = ibh_int4g_matmul_group_norm(t, wia.data(), o, n, xcur, dl, dl ? xalt : nullptr, s->eps,
+                                                  s->act_sparse_rel, s->st);
+        if (r < 0) return -1;
+        if (r == 1 && dl) std::swap(xcur, xalt);
+        return r;
+    };
     IBH_CHECK_LAUNCH("ibh_v5: embedding");
     int rc;
     const float* pending = nullptr;   // residual not yet added into x
     for (int l = 0; l < s->n_layers; l++) {
-        v5_rmsnorm_kernel<<<1, norm_threads(H), 0, s->st>>>(s->xb, s->x, pending, s->w_in[l], s->eps, H, nullptr);
-        IBH_CHECK_LAUNCH("ibh_v5: rmsnorm");
         float *q = s->q, *k = s->kn, *v = s->vn;
-        if (s->fused_qkv) {
+        int nf = 0;
+        if (!s->fused_qkv) {
+            const int mi[3] = {s->mq[l], s->mk[l], s->mv[l]};
+            float* const o[3] = {q, k, v};
+            if ((nf = norm_set(s->wia_in[l], mi, o, 3, pending)) < 0) {
+                ibh_set_error("ibh_v5: norm-fused q/k/v launch failed");
+                return IBH_ERROR_INTERNAL;
+            }
+        }
+        if (!nf) {
+            v5_rmsnorm_kernel<<<1, norm_threads(H), 0, s->st>>>(s->xb, xcur, pending, s->w_in[l], s->eps, H, nullptr);
+            IBH_CHECK_LAUNCH("ibh_v5: rmsnorm");
+        }
+        if (nf) {
+        } else if (s->fused_qkv) {
             if ((rc = matmul(s, s->mqkv[l], s->xb, s->qkv))) return rc;
             q = s->qkv;
             k = s->qkv + H;
@@ -1250,10 +1318,22 @@ int forward_dev(ibh_v5_session* s, ibh_v5_kv* kv, bool want_logits) {
                 return rc;
         }
         if ((rc = matmul(s, s->mo[l], s->xb2, s->delta))) return rc;
-        v5_rmsnorm_kernel<<<1, norm_threads(H), 0, s->st>>>(s->xb, s->x, s->delta, s->w_pn[l], s->eps, H, nullptr);
-        IBH_CHECK_LAUNCH("ibh_v5: rmsnorm");
         float *g = s->gate, *u = s->up;
-        if (s->fused_gu) {
+        nf = 0;
+        if (!s->fused_gu) {
+            const int mi[2] = {s->mg[l], s->mu[l]};
+            float* const o[2] = {g, u};
+            if ((nf = norm_set(s->wia_pn[l], mi, o, 2, s->delta)) < 0) {
+                ibh_set_error("ibh_v5: norm-fused gate/up launch failed");
+                return IBH_ERROR_INTERNAL;
+            }
+        }
+        if (!nf) {
+            v5_rmsnorm_kernel<<<1, norm_threads(H), 0, s->st>>>(s->xb, xcur, s->delta, s->w_pn[l], s->eps, H, nullptr);
+            IBH_CHECK_LAUNCH("ibh_v5: rmsnorm");
+        }
+        if (nf) {
+        } else if (s->fused_gu) {
             if ((rc = matmul(s, s->mgu[l], s->xb, s->gu))) return rc;
             g = s->gu;
             u = s->gu + I;
@@ -1278,7 +1358,7 @@ int forward_dev(ibh_v5_session* s, ibh_v5_kv* kv, bool want_logits) {
         }
         pending = s->delta;
     }
-    v5_rmsnorm_kernel<<<1, norm_threads(H), 0, s->st>>>(s->xb, s->x, pending, s->w_final, s->eps, H, dpos);
+    v5_rmsnorm_kernel<<<1, norm_threads(H), 0, s->st>>>(s->xb, xcur, pending, s->w_final, s->eps, H, dpos);
     IBH_CHECK_LAUNCH("ibh_v5: final rmsnorm");
     if (want_logits && (rc = matmul(s, s->m_head, s->xb, s->logits))) return rc;
     return IBH_OK;
