@@ -265,7 +265,7 @@ __global__ __launch_bounds__(kAttnThreads) void v5_attn_kernel(
     const float* __restrict__ cs, const int* __restrict__ dpos, int n_kv, int NS, float scale,
     float* __restrict__ part, int* __restrict__ counter) {
     constexpr int HALF = HD / 2, NW = kAttnThreads / 64, DPL = HD / 64, PPW = kAttnPos / NW;
-    constexpr int KPRE = HD == 64 ? HD / 4 : 1;   // key row held in registers (head_dim 64)
+    constexpr int KPRE = HD / 4;   // the lane's key row held in registers
     constexpr int SPAN = kAttnPos * kAttnTiles;
     __shared__ __align__(16) float qs[GRP][HD];
     __shared__ __align__(16) float kcur[HD], vcur[HD];
@@ -288,11 +288,9 @@ __global__ __launch_bounds__(kAttnThreads) void v5_attn_kernel(
         const int t1 = min(b1, t0 + kAttnPos), t = t0 + lane;
         const bool ok = t < t1 && t != pos;
         kst = (KVT == KV_I8 && ok) ? ksc[t] : 1.f;
-        if constexpr (HD == 64) {
-            if (ok) {
+        if (ok) {
 #pragma unroll
-                for (int i = 0; i < KPRE; i++) kreg[i] = kv_ld4<KVT>(kc, (size_t)t * kv_dim + hoff + 4 * i, kst);
-            }
+            for (int i = 0; i < KPRE; i++) kreg[i] = kv_ld4<KVT>(kc, (size_t)t * kv_dim + hoff + 4 * i, kst);
         }
 #pragma unroll
         for (int j = 0; j < PPW; j++) {
@@ -406,7 +404,6 @@ __global__ __launch_bounds__(kAttnThreads) void v5_attn_kernel(
         // this tile's registers; the next tile's reads go out now
         float4 kt[KPRE];
         float vt[PPW][DPL];
-        const float kstt = kst;
 #pragma unroll
         for (int i = 0; i < KPRE; i++) kt[i] = kreg[i];
 #pragma unroll
@@ -425,9 +422,7 @@ __global__ __launch_bounds__(kAttnThreads) void v5_attn_kernel(
 #pragma unroll
                 for (int d = 0; d < HD; d += 4) {
                     float4 kk;
-                    if (t == pos) kk = *(const float4*)(kcur + d);
-                    else if constexpr (HD == 64) kk = kt[d / 4];
-                    else kk = kv_ld4<KVT>(kc, (size_t)t * kv_dim + hoff + d, kstt);
+                    kk = t == pos ? *(const float4*)(kcur + d) : kt[d / 4];
 #pragma unroll
                     for (int h = 0; h < HPW; h++) {
                         const int g = wave + NW * h;
