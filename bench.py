@@ -203,9 +203,10 @@ def int4g_case(torch, L, M, N, G, K_out, steps, warmup, awq=True):
 
 
 def pq_policy_cases(torch, L, steps, warmup):
-    """The PQ session's policy variants (ibh_pq_matmul_policy) at the
-    config-5 FFN shape with two levels (K = K_l2 = 256) and the top-K LM
-    head (ibh_pq_lm_head_topk, K_top = 50) at a 32000 x 4096 head."""
+    """The PQ session's policy variants (ibh_pq_matmul_policy) and the
+    byte-quantised LUT (ibh_pq_matmul_q8lut) at the config-5 FFN shape with
+    two levels (K = K_l2 = 256), and the top-K LM head (ibh_pq_lm_head_topk,
+    K_top = 50 and the greedy 8) at a 32000 x 4096 head."""
     sys.path.insert(0, os.path.join(ROOT, "tests", "golden"))
     from gen_golden import make_pq
     rng = np.random.default_rng(21)
@@ -220,6 +221,10 @@ def pq_policy_cases(torch, L, steps, warmup):
         def launch(i, v=v, st=st, at=at):
             devs[i % 4].matmul_policy(x, y, v, st, at)
         out[name] = {"us": round(time_launches(torch, launch, steps, warmup) * 1e6, 2)}
+
+    def launch_q8(i):
+        devs[i % 4].matmul_q8lut(x, y)
+    out["q8lut"] = {"us": round(time_launches(torch, launch_q8, steps, warmup) * 1e6, 2)}
     th = make_pq(rng, 32000, 256, 16, 256, 2, 256, 0)
     dh = L.ops.PqDeviceTensor(th)
     xh = torch.randn(th["N"], generator=torch.Generator().manual_seed(6)).cuda()
@@ -231,6 +236,11 @@ def pq_policy_cases(torch, L, steps, warmup):
         dh.lm_head_topk(xh, 50)
     torch.cuda.synchronize()
     out["lm_head_topk_32000x4096_k50"] = {"us_per_call_host_clock": round((time.perf_counter() - t0) / 50 * 1e6, 1)}
+    t0 = time.perf_counter()
+    for _ in range(50):
+        dh.lm_head_topk(xh, 8)
+    torch.cuda.synchronize()
+    out["lm_head_topk_32000x4096_k8"] = {"us_per_call_host_clock": round((time.perf_counter() - t0) / 50 * 1e6, 1)}
     return out
 
 
