@@ -5,8 +5,8 @@
  * Plain C types only: pointers, sizes, ints.  Two layers:
  *
  *  1. Device entry points (ibh_*): operands are DEVICE pointers, launches go
- *     on `stream` (a hipStream_t passed as void*, NULL = the library's
- *     stream for the current device).  They return INFERBIT_* style codes
+ *     on `stream` (a hipStream_t passed as void*, NULL = the device's null
+ *     stream, ordered with every blocking stream of the process).  They return INFERBIT_* style codes
  *     (0 ok, negative error) and leave a message for ibh_last_error().
  *     They never allocate unless the comment says so.
  *
@@ -46,7 +46,7 @@ extern "C" {
 
 /* ── runtime ───────────────────────────────────────────────── */
 
-/* Selects `device`, creates the library stream for it.  Idempotent.
+/* Selects `device` and allocates the library workspace on it.  Idempotent.
  * Replaces nothing in the reference (it has no device); the reference's
  * ibf_load (src/ibf_loader.c:539-543) is where it would be called. */
 int         ibh_init(int device);
@@ -54,7 +54,7 @@ int         ibh_init(int device);
  * same convention as inferbit_last_error (src/error.c:17-21). */
 const char* ibh_last_error(void);
 const char* ibh_version(void);
-void*       ibh_default_stream(void);
+void*       ibh_default_stream(void);   /* the stream NULL stands for (the null stream) */
 int         ibh_synchronize(void* stream);
 int         ibh_device_malloc(void** dptr, size_t bytes);
 int         ibh_device_free(void* dptr);
@@ -74,6 +74,12 @@ int         ibh_memcpy_d2d(void* dst, const void* src, size_t bytes, void* strea
  * fp32 accumulation; summation order differs from the CPU's. */
 int ibh_matmul(float* out, const void* w, const void* scales, int scale_kind,
                const float* x, int M, int N, int bits, void* stream);
+
+/* Tuning hook for the tile matvec kernel behind ibh_matmul (no counterpart in
+ * the reference): R 16-row tiles x KS 64-byte steps per wavefront, WR row
+ * groups per block (0 = automatic); R = 0 restores the automatic choice,
+ * R = -1 switches the tile kernel off (the row kernels then serve). */
+int ibh_set_tile_config(int R, int KS, int WR);
 
 /* Per-128-group int8 activation quantization, bit-identical to
  * ib_quantize_input_int8_g128 (src/threading.c:401-432).  q[N], s[ceil(N/128)]. */

@@ -60,6 +60,36 @@ __device__ __forceinline__ int wave_isum(int v) {
     return v;
 }
 
+// Reductions over the 64 lanes with DPP row operations and four readlanes
+// (no LDS round trips): every lane gets the result.
+__device__ __forceinline__ float dpp_row_max(float v) {
+    int b = __builtin_bit_cast(int, v);
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(b, 0xB1, 0xF, 0xF, false)));   // quad_perm 1,0,3,2
+    b = __builtin_bit_cast(int, v);
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(b, 0x4E, 0xF, 0xF, false)));   // quad_perm 2,3,0,1
+    b = __builtin_bit_cast(int, v);
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(b, 0x124, 0xF, 0xF, false)));  // row_ror 4
+    b = __builtin_bit_cast(int, v);
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(b, 0x128, 0xF, 0xF, false)));  // row_ror 8
+    return v;
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    const int b = __builtin_bit_cast(int, dpp_row_max(v));
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+__device__ __forceinline__ int wave_isum_dpp(int v) {
+    v += __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);
+    v += __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);
+    v += __builtin_amdgcn_mov_dpp(v, 0x124, 0xF, 0xF, false);
+    v += __builtin_amdgcn_mov_dpp(v, 0x128, 0xF, 0xF, false);
+    return (__builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16)) +
+           (__builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48));
+}
+
 // 16-byte streaming load (weights are read exactly once per call).
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 ld_stream16(const void* p) {

@@ -828,7 +828,10 @@ int ibh_launch_rows_w4a8(float* out, const void* w, const void* sw, int kind, co
 
 // fp32 activations, int8 / int4 weights, rows of whole 1 KiB steps.  Returns 1
 // if launched, 0 if the shape is not eligible.
+int ibh_launch_tile_x_multi(const MatDesc* d, int n, int kind, const float* x, int N, int bits, hipStream_t st);
+
 int ibh_launch_rows_x_multi(const MatDesc* d, int n, int kind, const float* x, int N, int bits, hipStream_t st) {
+    if (ibh_launch_tile_x_multi(d, n, kind, x, N, bits, st)) return 1;
     if (bits != 8 && bits != 4) return 0;
     const size_t rb = (size_t)N * bits / 8;
     if (rb % 1024 != 0 || ((uintptr_t)x & 15) || N > 131072 || n < 1 || n > 3) return 0;

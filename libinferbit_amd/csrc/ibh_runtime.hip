@@ -34,7 +34,6 @@ namespace {
 constexpr int kMaxDev = 16;
 struct DevState {
     bool ready = false;
-    hipStream_t stream = nullptr;
     void* ws = nullptr;          // library workspace (activation operand staging)
     size_t ws_bytes = 0;
 };
@@ -60,7 +59,6 @@ extern "C" int ibh_init(int device) {
     IBH_HIP(hipSetDevice(device), "ibh_init: hipSetDevice");
     DevState& s = g_dev[device];
     if (!s.ready) {
-        IBH_HIP(hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking), "ibh_init: hipStreamCreate");
         if (hipMalloc(&s.ws, kDefaultWorkspace) != hipSuccess) {
             ibh_set_error("ibh_init: cannot allocate the %zu-byte workspace", kDefaultWorkspace);
             return IBH_ERROR_MEMORY;
@@ -81,12 +79,13 @@ void* ibh_workspace(size_t bytes) {
     return bytes <= g_dev[d].ws_bytes ? g_dev[d].ws : nullptr;
 }
 
+// NULL selects the device's null stream, which is ordered with every
+// blocking stream of the process (torch's default stream included).
 hipStream_t ibh_resolve_stream(void* s) {
     if (s) return (hipStream_t)s;
     const int d = current_device();
-    if (d < 0 || d >= kMaxDev) return nullptr;
-    if (!g_dev[d].ready) ibh_init(d);
-    return g_dev[d].stream;
+    if (d >= 0 && d < kMaxDev && !g_dev[d].ready) ibh_init(d);
+    return nullptr;
 }
 
 extern "C" void* ibh_default_stream(void) { return (void*)ibh_resolve_stream(nullptr); }

@@ -468,18 +468,23 @@ void or_rmsnorm(float* out, const float* x, const float* w, float eps, int N) {
     for (int j = 0; j < N; j++) out[j] = (x[j] * sc) * w[j];
 }
 
-/* scalar.c:140-157: pairs (2i, 2i+1) rotated by pos * theta^(-2i/hd). */
+/* avx2.c:256-273 (= scalar.c:140-157): pairs (2i, 2i+1) rotated by
+ * pos * theta^(-2i/hd).  The reference's x86 build (gcc -O3 -mfma, whose
+ * default -ffp-contract=fast fuses) evaluates q0*c - q1*s as
+ * fma(q0, c, -(q1*s)) and q0*s + q1*c as fma(q0, s, q1*c); this restatement
+ * writes those fused forms out (the reference-written fixture
+ * tests/golden/layer.npz fixes which operand is fused). */
 void or_rope(float* q, float* k, int hd, int pos, float theta) {
     for (int i = 0; i < hd; i += 2) {
         float freq = 1.0f / powf(theta, (float)i / (float)hd);
         float ang = (float)pos * freq;
         float c = cosf(ang), s = sinf(ang);
         float q0 = q[i], q1 = q[i + 1];
-        q[i] = q0 * c - q1 * s;
-        q[i + 1] = q0 * s + q1 * c;
+        q[i] = fmaf(q0, c, -(q1 * s));
+        q[i + 1] = fmaf(q0, s, q1 * c);
         float k0 = k[i], k1 = k[i + 1];
-        k[i] = k0 * c - k1 * s;
-        k[i + 1] = k0 * s + k1 * c;
+        k[i] = fmaf(k0, c, -(k1 * s));
+        k[i + 1] = fmaf(k0, s, k1 * c);
     }
 }
 

@@ -331,7 +331,41 @@ def gen_pqq8(out):
     np.savez_compressed(os.path.join(out, "pqq8.npz"), **d)
 
 
+# decode-layer helpers: the reference's own table entries (x86 AVX2 table,
+# src/kernels/avx2.c:153-273), odd lengths, several positions and thetas
+LAYER_N = [1, 7, 64, 2051]
+LAYER_ROPE = [(64, 0, 10000.0), (64, 5, 10000.0), (128, 4095, 10000.0), (128, 77, 1000000.0), (6, 3, 500.0)]
+
+
+def gen_layer(out):
+    tab = R.kernels(R.IB_SIMD_AVX2)
+    rng = np.random.default_rng(4242)
+    d = {}
+    for n in LAYER_N:
+        x = (rng.standard_normal(n) * 3).astype(np.float32)
+        w = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+        o = np.zeros(n, np.float32)
+        R.call_f32(tab, "rmsnorm", R._p(o), R._p(x), R._p(w), np.float32(1e-5), n)
+        d[f"rms{n}.x"], d[f"rms{n}.w"], d[f"rms{n}.y"] = x, w, o
+        g = (rng.standard_normal(n) * 4).astype(np.float32)
+        u = rng.standard_normal(n).astype(np.float32)
+        o2 = np.zeros(n, np.float32)
+        R.call_f32(tab, "silu_mul", R._p(o2), R._p(g), R._p(u), n)
+        d[f"silu{n}.g"], d[f"silu{n}.u"], d[f"silu{n}.y"] = g, u, o2
+    for i, (hd, pos, theta) in enumerate(LAYER_ROPE):
+        q = rng.standard_normal(hd).astype(np.float32)
+        k = rng.standard_normal(hd).astype(np.float32)
+        d[f"rope{i}.q"], d[f"rope{i}.k"] = q.copy(), k.copy()
+        R.call_f32(tab, "rope", R._p(q), R._p(k), hd, pos, np.float32(theta))
+        d[f"rope{i}.qo"], d[f"rope{i}.ko"] = q, k
+        d[f"rope{i}.arg"] = np.array([hd, pos, theta], np.float64)
+    np.savez_compressed(os.path.join(out, "layer.npz"), **d)
+
+
 def main():
+    if len(sys.argv) > 1 and sys.argv[1] == "layer":
+        gen_layer(HERE)
+        return
     if len(sys.argv) > 2 and sys.argv[1] == "int4g-skip-child":
         np.savez(sys.argv[2], **int4g_outputs(int4g_inputs()))
         return
@@ -360,6 +394,7 @@ def main():
     gen_pqtopk(HERE)
     gen_pqq8(HERE)
     gen_int4g(HERE)
+    gen_layer(HERE)
     for f in sorted(os.listdir(HERE)):
         if f.endswith(".npz"):
             print(f, os.path.getsize(os.path.join(HERE, f)))

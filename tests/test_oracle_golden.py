@@ -458,3 +458,63 @@ def test_pq_q8lut_error_bound(oracle_lib, name):
         os_ = np.asarray(t["oscale"]).view(np.float16).astype(np.float64)
         slack += np.abs(t["oside"]).max() * np.abs(x[oc] * os_).max() / 254.0 * t["n_outlier"]
     assert np.all(np.abs(y - exact) <= rs * bound + slack)
+
+
+# ── decode-layer helpers (or_rmsnorm, or_rope, or_silu_mul) ──────────────────
+LAYER_N = [1, 7, 64, 2051]
+
+
+@pytest.mark.parametrize("n", LAYER_N)
+def test_rmsnorm_matches_reference(oracle_lib, n):
+    """avx2_rmsnorm (src/kernels/avx2.c:153-188) wrote these: 8-lane FMA sum of
+    squares, fold, FMA tail, (x*scale)*w -- bit for bit, odd lengths too."""
+    d = load_golden("layer.npz")
+    same_bits(oracle_lib.rmsnorm(d[f"rms{n}.x"], d[f"rms{n}.w"], 1e-5), d[f"rms{n}.y"])
+
+
+@pytest.mark.parametrize("n", LAYER_N)
+def test_silu_mul_matches_reference(oracle_lib, n):
+    """avx2_silu_mul (src/kernels/avx2.c:233-251), bit for bit."""
+    d = load_golden("layer.npz")
+    same_bits(oracle_lib.silu_mul(d[f"silu{n}.g"], d[f"silu{n}.u"]), d[f"silu{n}.y"])
+
+
+@pytest.mark.parametrize("i", range(5))
+def test_rope_matches_reference(oracle_lib, i):
+    """avx2_rope (src/kernels/avx2.c:256-273): head dims 6..128, positions 0..4095,
+    theta 500..1e6, bit for bit."""
+    d = load_golden("layer.npz")
+    hd, pos, theta = d[f"rope{i}.arg"]
+    q, k = oracle_lib.rope(d[f"rope{i}.q"], d[f"rope{i}.k"], int(hd), int(pos), float(theta))
+    same_bits(q, d[f"rope{i}.qo"])
+    same_bits(k, d[f"rope{i}.ko"])
+
+
+def test_layer_helpers_closed_forms(oracle_lib):
+    """Properties fixed by the mathematics, independent of the reference:
+    rmsnorm of a constant vector is w * c / sqrt(c^2 + eps); RoPE at position
+    0 is the identity and at any position keeps each pair's norm and rotates
+    pair i by pos * theta^(-2i/hd); silu(0) = 0 and silu(g) -> g for large g."""
+    n = 33
+    x = np.full(n, 2.5, np.float32)
+    w = np.linspace(0.5, 1.5, n).astype(np.float32)
+    y = oracle_lib.rmsnorm(x, w, 1e-5)
+    np.testing.assert_allclose(y, w * 2.5 / np.sqrt(2.5 ** 2 + 1e-5), rtol=2e-7)
+    rng = np.random.default_rng(3)
+    q = rng.standard_normal(64).astype(np.float32)
+    k = rng.standard_normal(64).astype(np.float32)
+    q0, k0 = oracle_lib.rope(q, k, 64, 0, 10000.0)
+    same_bits(q0, q)
+    same_bits(k0, k)
+    pos = 37
+    q1, _ = oracle_lib.rope(q, k, 64, pos, 10000.0)
+    for i in range(0, 64, 2):
+        ang = pos * 10000.0 ** (-i / 64)
+        c, s = np.cos(ang), np.sin(ang)
+        want = (q[i] * c - q[i + 1] * s, q[i] * s + q[i + 1] * c)
+        np.testing.assert_allclose(q1[i:i + 2], want, rtol=0, atol=2e-5)
+        np.testing.assert_allclose(np.hypot(*q1[i:i + 2]), np.hypot(q[i], q[i + 1]), rtol=1e-5)
+    g = np.array([0.0, 30.0, -30.0, 1.0], np.float32)
+    y = oracle_lib.silu_mul(g, np.ones(4, np.float32))
+    assert y[0] == 0.0 and abs(y[1] - 30.0) < 1e-5 and abs(y[2]) < 1e-10
+    np.testing.assert_allclose(y[3], 1.0 / (1.0 + np.exp(-1.0)), rtol=1e-6)
