@@ -98,6 +98,17 @@ int ibh_matmul_w4a8(float* out, const void* w, const void* scales, int scale_kin
 int ibh_matmul_w4a8_x(float* out, const void* w, const void* scales, int scale_kind,
                       const float* x, int M, int N, int8_t* qx_ws, float* sa_ws, void* stream);
 
+/* No counterpart in the reference: ibh_matmul_w4a8_x for callers that cannot
+ * allocate (code under HIP graph capture, serving loops, harnesses that
+ * forbid hipMalloc).  The activation codes and scales go to a fixed device
+ * array of the library (N <= 65536; larger N returns IBH_ERROR_PARAM),
+ * located once per device by ibh_init, which must have run on the current
+ * device (else IBH_ERROR_CONTEXT).  The call allocates nothing.  Every call
+ * on one GPU shares that array: calls that overlap in time on one GPU
+ * (different streams) race; calls ordered on one stream do not. */
+int ibh_matmul_w4a8_x_noalloc(float* out, const void* w, const void* scales, int scale_kind,
+                              const float* x, int M, int N, void* stream);
+
 /* Batched forms, out[b*M_stride + i] (src/inferbit_internal.h:242-276).
  * ibh_matmul_w4a8_batch is bit-identical to the x86 build's scalar kernel
  * (src/kernels/scalar.c:86-124: per-group multiply and add rounded apart);

@@ -26,6 +26,7 @@ SIGNATURES = {
     "ibh_memcpy_d2d": (I, [P, P, SZ, P]),
     "ibh_matmul": (I, [P, P, P, I, P, I, I, I, P]),
     "ibh_set_tile_config": (I, [I, I, I]),
+    "ibh_matmul_w4a8_x_noalloc": (I, [P, P, P, I, P, I, I, P]),
     "ibh_quantize_act_g128": (I, [P, P, P, I, P]),
     "ibh_matmul_w4a8": (I, [P, P, P, I, P, P, I, I, P]),
     "ibh_matmul_w4a8_x": (I, [P, P, P, I, P, I, I, P, P, P]),

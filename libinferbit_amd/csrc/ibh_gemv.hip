@@ -544,6 +544,47 @@ extern "C" int ibh_matmul_w4a8_x(float* out, const void* w, const void* scales, 
     return ibh_matmul_w4a8(out, w, scales, scale_kind, qx_ws, sa_ws, M, N, stream);
 }
 
+// ── allocation-free W4A8 decode entry ────────────────────────────────────────
+// The activation codes and group scales of ibh_matmul_w4a8_x live in one
+// file-scope device array per GPU instead of caller workspace.  Its device
+// address is looked up once per device at ibh_init (hipGetSymbolAddress); the
+// host-side name is only a stand-in and is never passed to a kernel.
+namespace {
+constexpr int kNoAllocMaxN = 65536;                                  // activation length limit
+constexpr size_t kNoAllocSaOff = kNoAllocMaxN;                       // byte offset of the group scales
+constexpr size_t kNoAllocBytes = kNoAllocSaOff + 4 * (kNoAllocMaxN / 128);
+constexpr int kNoAllocDevs = 16;
+void* g_scratch_ptr[kNoAllocDevs];                                   // device address, per device
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
+
+// Called by ibh_init with `device` current (under its lock).
+int ibh_noalloc_setup(int device) {
+    if (device < 0 || device >= kNoAllocDevs) return IBH_OK;
+    if (g_scratch_ptr[device]) return IBH_OK;
+    void* p = nullptr;
+    IBH_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "ibh_init: hipGetSymbolAddress(scratch)");
+    g_scratch_ptr[device] = p;
+    return IBH_OK;
+}
+
+extern "C" int ibh_matmul_w4a8_x_noalloc(float* out, const void* w, const void* scales, int scale_kind,
+                                         const float* x, int M, int N, void* stream) {
+    if (N <= 0 || N > kNoAllocMaxN) {
+        ibh_set_error("ibh_matmul_w4a8_x_noalloc: N=%d outside 1..%d (the fixed scratch size)", N, kNoAllocMaxN);
+        return IBH_ERROR_PARAM;
+    }
+    int d = -1;
+    if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= kNoAllocDevs || !g_scratch_ptr[d]) {
+        ibh_set_error("ibh_matmul_w4a8_x_noalloc: call ibh_init on this device first");
+        return IBH_ERROR_CONTEXT;
+    }
+    unsigned char* base = (unsigned char*)g_scratch_ptr[d];
+    return ibh_matmul_w4a8_x(out, w, scales, scale_kind, x, M, N, (int8_t*)base, (float*)(base + kNoAllocSaOff),
+                             stream);
+}
+
 extern "C" int ibh_matmul_w4a8_batch(float* out, const void* w, const void* scales, int scale_kind,
                                      const int8_t* qx, const float* sa, int M, int N, int B,
                                      int M_stride, void* stream) {

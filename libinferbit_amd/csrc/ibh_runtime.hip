@@ -48,6 +48,8 @@ int current_device() {
 }
 }  // namespace
 
+int ibh_noalloc_setup(int device);   // ibh_gemv.hip
+
 extern "C" int ibh_init(int device) {
     std::lock_guard<std::mutex> lk(g_mu);
     int n = 0;
@@ -64,6 +66,8 @@ extern "C" int ibh_init(int device) {
             return IBH_ERROR_MEMORY;
         }
         s.ws_bytes = kDefaultWorkspace;
+        const int rc = ibh_noalloc_setup(device);
+        if (rc != IBH_OK) return rc;
         s.ready = true;
     }
     return IBH_OK;
