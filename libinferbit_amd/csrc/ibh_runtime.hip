@@ -49,6 +49,10 @@ int current_device() {
 }  // namespace
 
 int ibh_noalloc_setup(int device);   // ibh_gemv.hip
+int ibh_launch_matvec_exact(float* y, const void* w, const void* sc, int kind, const float* x, int M, int N, int bits,
+                            const uint8_t* mask, hipStream_t st);   // ibh_exact.hip
+int ibh_launch_int8_batch_exact(float* y, const void* w, const void* sc, int kind, const float* x, int M, int N,
+                                int B, int M_stride, hipStream_t st);
 
 extern "C" int ibh_init(int device) {
     std::lock_guard<std::mutex> lk(g_mu);
@@ -215,7 +219,14 @@ void tab_matmul(float* out, const void* w, const float* sc, const float* x, int 
     float* dsc = (float*)S.put(sc, 4 * (size_t)M, st);
     float* dx = (float*)S.put(x, 4 * (size_t)N, st);
     float* dout = (float*)S.put(nullptr, 4 * (size_t)M, st);
-    int rc = ibh_matmul(dout, dw, dsc, IBH_SCALE_F32, dx, M, N, bits, st);
+    // The x86 table's operation order (matvec_exact), so a reference build
+    // that swaps its table keeps its logits bit for bit; rows longer than the
+    // exact kernel's LDS tile (N > 15360 at 8/4 bits) take the tolerance kernel.
+    int rc = ibh_launch_matvec_exact(dout, dw, dsc, IBH_SCALE_F32, dx, M, N, bits, nullptr, st);
+    if (rc == IBH_ERROR_PARAM) {
+        (void)ibh_last_error();
+        rc = ibh_matmul(dout, dw, dsc, IBH_SCALE_F32, dx, M, N, bits, st);
+    }
     if (rc == IBH_OK && hipMemcpyAsync(out, dout, 4 * (size_t)M, hipMemcpyDeviceToHost, st) == hipSuccess &&
         hipStreamSynchronize(st) == hipSuccess)
         return;
@@ -282,7 +293,8 @@ void hip_int8_batch(float* out, const void* w, const float* sw, const float* x, 
     float* dsw = (float*)S.put(sw, 4 * (size_t)M, st);
     float* dx = (float*)S.put(x, 4 * (size_t)B * N, st);
     float* dout = (float*)S.put(out, ob, st);
-    int rc = ibh_matmul_int8_batch(dout, dw, dsw, IBH_SCALE_F32, dx, M, N, B, M_stride, st);
+    // scalar.c:70-84 (the x86 table's batched INT8 entry): serial sums
+    int rc = ibh_launch_int8_batch_exact(dout, dw, dsw, IBH_SCALE_F32, dx, M, N, B, M_stride, st);
     if (rc == IBH_OK && hipMemcpyAsync(out, dout, ob, hipMemcpyDeviceToHost, st) == hipSuccess &&
         hipStreamSynchronize(st) == hipSuccess)
         return;
