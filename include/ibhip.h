@@ -465,6 +465,24 @@ void ib_init_kernels_hip(ibh_kernels* kern);
 int  ibh_register_host_weights(const void* host_base, size_t bytes, void** dev_base);
 void ibh_unregister_host_weights(const void* host_base);
 
+/* Attention of one position over a HOST KV cache, for the head loop of
+ * forward_single_ex / forward_batch (src/forward.c:596-614, :768-783), which
+ * call ib_attn_head_task for heads 0..n_heads-1 after kv_cache_write has
+ * stored position `pos`.  `cache` identifies the host cache (the
+ * ib_kv_cache*); kdata/vdata/kscales/vscales/capacity/kv_bits are its fields
+ * (src/inferbit_internal.h:101-109).  A device mirror per cache receives the
+ * rows it lacks, as stored, and the heads run in the x86 order, so `out`
+ * (the head outputs, xb2) equals ib_attn_head_task's bit for bit.  A rewind
+ * (inferbit_kv_truncate/clear, src/kv_cache.c:5-20) needs no call: writing a
+ * position below the mirror's length shortens it.  head_dim 64/128/256,
+ * pos < 8192.  Returns IBH_OK, or an error with nothing written (the caller
+ * then runs its CPU loop). */
+int  ibh_host_attn(const void* cache, const void* kdata, const void* vdata, const float* kscales,
+                   const float* vscales, int capacity, int pos, int kv_bits, const float* q, float* out,
+                   int n_heads, int n_kv, int head_dim);
+/* Frees the device mirror of `cache` (from inferbit_free, src/model.c:42-107). */
+void ibh_host_kv_release(const void* cache);
+
 #ifdef __cplusplus
 }
 #endif

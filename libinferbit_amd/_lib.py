@@ -87,6 +87,8 @@ SIGNATURES = {
     "ib_init_kernels_hip": (None, [P]),
     "ibh_register_host_weights": (I, [P, SZ, C.POINTER(P)]),
     "ibh_unregister_host_weights": (None, [P]),
+    "ibh_host_attn": (I, [P, P, P, P, P, I, I, I, P, P, I, I, I]),
+    "ibh_host_kv_release": (None, [P]),
 }
 
 

@@ -4,6 +4,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <mutex>
 #include <vector>
 
@@ -345,6 +346,129 @@ extern "C" void ibh_unregister_host_weights(const void* host_base) {
         if (g_regions[i].host == host_base) {
             (void)hipFree(g_regions[i].dev);
             g_regions.erase(g_regions.begin() + (long)i);
+            return;
+        }
+}
+
+// ── attention hook on host pointers (forward.c's head loop) ─────────────────
+// The reference keeps its KV cache in host memory (ib_kv_cache,
+// src/inferbit_internal.h:101-109) and writes it with kv_cache_write
+// (src/forward.c:352-413) right before the head loop at every position.  The
+// hook keeps a device mirror per host cache: rows the device lacks (positions
+// from its length up to pos) are uploaded as the host stored them, then every
+// head runs on the device in the x86 order (attn_scores_exact +
+// attn_out_exact), so the head outputs are the reference's bit for bit.  A
+// rewind (inferbit_kv_truncate / _clear) needs no call: the next position the
+// host writes is below the mirror's length, which then drops to it.
+namespace {
+struct KvMirror {
+    const void* key;
+    int capacity, kv_bits, n_kv, head_dim;
+    uint8_t* k;
+    uint8_t* v;
+    float* ks;
+    float* vs;
+    int len;
+};
+std::vector<KvMirror> g_kv;
+
+size_t kv_row_bytes(int bits, int kv_dim) {
+    return bits >= 16 ? 4 * (size_t)kv_dim : bits == 8 ? (size_t)kv_dim : (size_t)(kv_dim + 1) / 2;
+}
+
+void kv_mirror_free(KvMirror& mm) {
+    (void)hipFree(mm.k);
+    (void)hipFree(mm.v);
+    (void)hipFree(mm.ks);
+    (void)hipFree(mm.vs);
+    mm.k = mm.v = nullptr;
+    mm.ks = mm.vs = nullptr;
+}
+}  // namespace
+
+size_t ibh_attn_exact_scratch(int n_heads, int max_pos);   // ibh_exact.hip
+int ibh_launch_attn_exact(float* out, const float* q, const void* kdata, const void* vdata, const float* ks,
+                          const float* vs, const int* dpos, int max_pos, int n_heads, int n_kv, int hd, int kv_bits,
+                          float* att, hipStream_t st);
+
+extern "C" int ibh_host_attn(const void* cache, const void* kdata, const void* vdata, const float* kscales,
+                             const float* vscales, int capacity, int pos, int kv_bits, const float* q, float* out,
+                             int n_heads, int n_kv, int head_dim) {
+    if (!cache || !kdata || !vdata || !q || !out || pos < 0 || pos >= capacity || n_kv <= 0 || n_heads % n_kv ||
+        (kv_bits <= 8 && (!kscales || !vscales))) {
+        ibh_set_error("ibh_host_attn: invalid arguments (pos %d, capacity %d)", pos, capacity);
+        return IBH_ERROR_PARAM;
+    }
+    std::lock_guard<std::mutex> lk(g_tab_mu);
+    hipStream_t st = ibh_resolve_stream(nullptr);
+    const int kv_dim = n_kv * head_dim;
+    const size_t rbytes = kv_row_bytes(kv_bits, kv_dim);
+    KvMirror* mm = nullptr;
+    for (KvMirror& e : g_kv)
+        if (e.key == cache) mm = &e;
+    if (mm && (mm->capacity != capacity || mm->kv_bits != kv_bits || mm->n_kv != n_kv || mm->head_dim != head_dim)) {
+        kv_mirror_free(*mm);                       // the host cache was re-shaped (a dynamic cache grew)
+        mm->len = 0;
+    }
+    if (!mm) {
+        g_kv.push_back({cache, capacity, kv_bits, n_kv, head_dim, nullptr, nullptr, nullptr, nullptr, 0});
+        mm = &g_kv.back();
+    }
+    if (!mm->k) {
+        mm->capacity = capacity;
+        mm->kv_bits = kv_bits;
+        mm->n_kv = n_kv;
+        mm->head_dim = head_dim;
+        const size_t sb = kv_bits <= 8 ? 4 * (size_t)capacity * n_kv : 0;
+        if (hipMalloc((void**)&mm->k, rbytes * capacity) != hipSuccess ||
+            hipMalloc((void**)&mm->v, rbytes * capacity) != hipSuccess ||
+            (sb && (hipMalloc((void**)&mm->ks, sb) != hipSuccess || hipMalloc((void**)&mm->vs, sb) != hipSuccess))) {
+            kv_mirror_free(*mm);
+            ibh_set_error("ibh_host_attn: out of device memory for the KV mirror");
+            return IBH_ERROR_MEMORY;
+        }
+        mm->len = 0;
+    }
+    // rows [len, pos] as the host stored them (a rewound position re-uploads)
+    const int from = std::min(mm->len, pos);
+    const size_t nrow = (size_t)(pos + 1 - from);
+    IBH_HIP(hipMemcpyAsync(mm->k + from * rbytes, (const uint8_t*)kdata + from * rbytes, nrow * rbytes,
+                           hipMemcpyHostToDevice, st), "ibh_host_attn: K upload");
+    IBH_HIP(hipMemcpyAsync(mm->v + from * rbytes, (const uint8_t*)vdata + from * rbytes, nrow * rbytes,
+                           hipMemcpyHostToDevice, st), "ibh_host_attn: V upload");
+    if (kv_bits <= 8) {
+        const size_t sr = 4 * (size_t)n_kv;
+        IBH_HIP(hipMemcpyAsync((uint8_t*)mm->ks + from * sr, (const uint8_t*)kscales + from * sr, nrow * sr,
+                               hipMemcpyHostToDevice, st), "ibh_host_attn: K scales upload");
+        IBH_HIP(hipMemcpyAsync((uint8_t*)mm->vs + from * sr, (const uint8_t*)vscales + from * sr, nrow * sr,
+                               hipMemcpyHostToDevice, st), "ibh_host_attn: V scales upload");
+    }
+    mm->len = pos + 1;
+    const size_t qb = 4 * (size_t)n_heads * head_dim;
+    Staged S;
+    S.base = workspace(al256(qb) * 2 + al256(16) + al256(ibh_attn_exact_scratch(n_heads, pos)));
+    if (!S.base) {
+        ibh_set_error("ibh_host_attn: out of device memory");
+        return IBH_ERROR_MEMORY;
+    }
+    float* dq = (float*)S.put(q, qb, st);
+    int* dpos = (int*)S.put(&pos, sizeof(int), st);
+    float* dout = (float*)S.put(nullptr, qb, st);
+    float* att = (float*)S.put(nullptr, ibh_attn_exact_scratch(n_heads, pos), st);
+    int rc = ibh_launch_attn_exact(dout, dq, mm->k, mm->v, mm->ks, mm->vs, dpos, pos, n_heads, n_kv, head_dim,
+                                   kv_bits, att, st);
+    if (rc != IBH_OK) return rc;
+    IBH_HIP(hipMemcpyAsync(out, dout, qb, hipMemcpyDeviceToHost, st), "ibh_host_attn: output copy");
+    IBH_HIP(hipStreamSynchronize(st), "ibh_host_attn: synchronize");
+    return IBH_OK;
+}
+
+extern "C" void ibh_host_kv_release(const void* cache) {
+    std::lock_guard<std::mutex> lk(g_tab_mu);
+    for (size_t i = 0; i < g_kv.size(); i++)
+        if (g_kv[i].key == cache) {
+            kv_mirror_free(g_kv[i]);
+            g_kv.erase(g_kv.begin() + (long)i);
             return;
         }
 }

@@ -21,7 +21,22 @@
  * compares the GPU pass with token streams the reference recorded earlier).  Prints one JSON line: the prompt's last-token logits compared
  * bit for bit (CPU table vs GPU table), both greedy token streams, and the
  * wall time of each generate call.  KEEP_CPU_TABLE=1 runs the second pass on
- * the CPU table too (the control: both passes must then agree trivially). */
+ * the CPU table too (the control: both passes must then agree trivially).
+ *
+ * Built a second time as dropin_attn (-DDROPIN_ATTN) against the reference's
+ * forward.c with its two head loops (src/forward.c:610-614, :779-783) routed
+ * through a hook -- the call the integration patch of INTEGRATION.md section
+ * 2 adds; oracle/Makefile derives that copy with sed into oracle/_ref.  The
+ * GPU pass then also runs every attention step on the device through
+ * ibh_host_attn (the device KV mirror), and frees the mirrors with
+ * ibh_host_kv_release before inferbit_free.  DROPIN_LOOKUP="ngram,k" turns on
+ * the reference's prompt-lookup speculation (inferbit_set_prompt_lookup), which
+ * verifies drafts through forward_batch and rewinds the cache with
+ * inferbit_kv_truncate. */
+#ifdef DROPIN_ATTN
+static int ibh_attn_hook(void* ctx, int n_heads);
+#include "forward_hip.c"
+#endif
 #include "inferbit_internal.h"
 
 #include <stdio.h>
@@ -32,6 +47,23 @@
 #include "../include/ibhip.h"
 
 extern ib_kernels ib_kern;   /* src/kernels/scalar.c:185 */
+
+static int g_gpu_attn = 0, g_attn_calls = 0, g_attn_fallbacks = 0;
+
+#ifdef DROPIN_ATTN
+/* 0: the heads ran on the device; nonzero: run the reference's CPU loop */
+static int ibh_attn_hook(void* p, int n_heads) {
+    ib_attn_ctx* c = (ib_attn_ctx*)p;
+    if (!g_gpu_attn) return 1;
+    const ib_kv_cache* kv = c->kv;
+    g_attn_calls++;
+    if (ibh_host_attn(kv, kv->key_data, kv->value_data, kv->key_scales, kv->value_scales, kv->capacity, c->pos,
+                      c->kv_bits, c->q, c->xb2, n_heads, c->n_kv_heads, c->head_dim) == IBH_OK)
+        return 0;
+    if (!g_attn_fallbacks++) fprintf(stderr, "device attention declined: %s\n", ibh_last_error());
+    return 1;
+}
+#endif
 
 static double now_s(void) {
     struct timespec ts;
@@ -77,6 +109,10 @@ int main(int argc, char** argv) {
     inferbit_config_set_context_length(cfg, atoi(argv[2]));
     inferbit_model* m = inferbit_load(argv[1], cfg);
     if (!m) { fprintf(stderr, "load failed: %s\n", inferbit_last_error()); return 1; }
+    int lk_ng = 0, lk_k = 0;
+    const char* lk = getenv("DROPIN_LOOKUP");
+    if (lk && sscanf(lk, "%d,%d", &lk_ng, &lk_k) != 2) { fprintf(stderr, "bad DROPIN_LOOKUP\n"); return 1; }
+    if (lk) inferbit_set_prompt_lookup(m, lk_ng, lk_k);
     const int n_out = atoi(argv[3]);
     size_t pn = 0;
     int32_t* prompt = (int32_t*)slurp(argv[4], &pn);
@@ -95,11 +131,15 @@ int main(int argc, char** argv) {
     inferbit_config_set_threads(cfg, 1);
     m = inferbit_load(argv[1], cfg);   /* ibf_load re-initialises the x86 table */
     if (!m) { fprintf(stderr, "reload failed: %s\n", inferbit_last_error()); return 1; }
+    if (lk) inferbit_set_prompt_lookup(m, lk_ng, lk_k);
 
     if (!keep_cpu) {
         void* dev = NULL;
         if (ibh_init(0) != IBH_OK) { fprintf(stderr, "ibh_init: %s\n", ibh_last_error()); return 1; }
         ib_init_kernels_hip((ibh_kernels*)&ib_kern);
+#ifdef DROPIN_ATTN
+        g_gpu_attn = 1;
+#endif
         if (ibh_register_host_weights(m->weight_data, m->weight_data_size, &dev) != IBH_OK) {
             fprintf(stderr, "upload: %s\n", ibh_last_error());
             return 1;
@@ -128,14 +168,18 @@ int main(int argc, char** argv) {
     printf("{\"vocab\": %d, \"prompt\": %d, \"logits_same_bits\": %d, \"logits_nan\": %d, "
            "\"logits_max_abs_diff\": %.9g, \"logits_max_abs\": %.9g, \"tokens_equal\": %d, "
            "\"n_cpu\": %d, \"n_gpu\": %d, \"cpu_seconds\": %.6f, \"gpu_seconds\": %.6f, \"gpu_table\": %d, "
-           "\"cpu_threads\": %d, \"tokens_cpu\": [", vocab, np, same_bits, n_nan, max_abs, max_ref, tokens_equal,
-           n_cpu, n_gpu, s_cpu, s_gpu, !keep_cpu, atoi(argv[5]));
+           "\"cpu_threads\": %d, \"attn_calls\": %d, \"attn_fallbacks\": %d, \"tokens_cpu\": [", vocab, np,
+           same_bits, n_nan, max_abs, max_ref, tokens_equal, n_cpu, n_gpu, s_cpu, s_gpu, !keep_cpu, atoi(argv[5]),
+           g_attn_calls, g_attn_fallbacks);
     for (int i = 0; i < n_cpu; i++) printf("%s%d", i ? ", " : "", out_cpu[i]);
     printf("], \"tokens_gpu\": [");
     for (int i = 0; i < n_gpu; i++) printf("%s%d", i ? ", " : "", out_gpu[i]);
     printf("]}\n");
 
-    if (!keep_cpu) ibh_unregister_host_weights(m->weight_data);
+    if (!keep_cpu) {
+        for (int l = 0; l < m->header.num_layers; l++) ibh_host_kv_release(&m->kv_caches[l]);
+        ibh_unregister_host_weights(m->weight_data);
+    }
     inferbit_free(m);
     inferbit_config_free(cfg);
     free(prompt);

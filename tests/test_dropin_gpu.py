@@ -28,6 +28,7 @@ from conftest import GOLDEN, ROOT
 pytestmark = pytest.mark.gpu
 
 DROPIN = os.path.join(ROOT, "oracle", "_ref", "dropin")
+DROPIN_ATTN = os.path.join(ROOT, "oracle", "_ref", "dropin_attn")
 MODEL_DIR = os.environ.get("IBH_MODEL_DIR", "/tmp/ibh_models")
 
 
@@ -46,13 +47,13 @@ def R():
     return R
 
 
-def run_dropin(path, prompt, n_out, tmp, cpu_threads=4, ctx=0):
-    if not os.path.exists(DROPIN):
-        pytest.skip("oracle/_ref/dropin not built (make -C oracle ref)")
+def run_dropin(path, prompt, n_out, tmp, cpu_threads=4, ctx=0, exe=DROPIN, env=None):
+    if not os.path.exists(exe):
+        pytest.skip(f"{exe} not built (make -C oracle ref)")
     pp = str(tmp / "p.i32")
     np.asarray(prompt, np.int32).tofile(pp)
-    r = subprocess.run([DROPIN, path, str(ctx), str(n_out), pp, str(cpu_threads)], capture_output=True, text=True,
-                       timeout=600)
+    r = subprocess.run([exe, path, str(ctx), str(n_out), pp, str(cpu_threads)], capture_output=True, text=True,
+                       timeout=600, env=dict(os.environ, **(env or {})))
     assert r.returncode == 0, r.stderr
     return json.loads(r.stdout.strip().splitlines()[-1])
 
@@ -108,6 +109,41 @@ def test_reference_generate_tinyllama_config(tmp_path):
     assert r["logits_nan"] == 0
     assert r["tokens_gpu"] == g["tokens"]
     print(f"dropin tinyllama: {g['n_out'] / r['gpu_seconds']:.1f} tok/s through the reference host loop", flush=True)
+
+
+ATTN = {
+    "fp32kv": dict(kv_bits=32),
+    "int8kv": dict(kv_bits=8),
+    "int4kv": dict(kv_bits=4),
+    "hd128": dict(kv_bits=8, hidden_size=512, num_heads=4, num_kv_heads=1, head_dim=128, intermediate_size=1024),
+}
+
+
+@pytest.mark.parametrize("lookup", [None, "2,4"])
+@pytest.mark.parametrize("name", list(ATTN))
+def test_reference_generate_with_device_attention(tmp_path, name, lookup):
+    """The reference's forward.c with its head loops offered to ibh_host_attn
+    (the device KV mirror): every attention step of the GPU pass runs on the
+    device, none falls back, and logits and tokens equal the x86 run.  With
+    prompt-lookup speculation the reference verifies drafts in forward_batch
+    and rewinds with inferbit_kv_truncate, which the mirror follows."""
+    from libinferbit_amd import ibf
+    path = str(tmp_path / "m.ibf")
+    ibf.write_synthetic(path, tiny_cfg(**ATTN[name]), seed=23)
+    prompt = [7, 7, 100, 7, 7, 100, 250, 3, 7, 7, 100, 9]
+    print(f"case dropin_attn {name} lookup={lookup}", flush=True)
+    r = run_dropin(path, prompt, 48, tmp_path, exe=DROPIN_ATTN, env={"DROPIN_LOOKUP": lookup} if lookup else None)
+    assert r["attn_calls"] > 0 and r["attn_fallbacks"] == 0, r
+    assert r["logits_same_bits"] == r["vocab"], r
+    assert r["tokens_equal"] == 1, (r["tokens_cpu"], r["tokens_gpu"])
+
+
+def test_host_attn_rejects_bad_arguments(L):
+    q = np.zeros(64, np.float32)
+    k = np.zeros((4, 64), np.float32)
+    assert L.lib().ibh_host_attn(_p(k), _p(k), _p(k), None, None, 4, 4, 32, _p(q), _p(q), 1, 1, 64) != 0
+    assert L.lib().ibh_host_attn(_p(k), _p(k), _p(k), None, None, 4, 0, 8, _p(q), _p(q), 1, 1, 64) != 0
+    assert L.lib().ibh_last_error()
 
 
 # ── the table entries, host pointers ─────────────────────────────────────────
