@@ -82,42 +82,40 @@ def matvec_bytes(M, N, bits, w4a8=False):
 
 
 def make_weights(oracle, bits, M, N, seed):
-    """Quantize N(0,0.02) rows with the quantize.c rules.  To keep host time
-    bounded, 256 distinct rows are quantized and tiled to M rows."""
-    rng = np.random.default_rng(seed)
-    base = (rng.standard_normal((min(256, M), N)) * 0.02).astype(np.float32)
-    w, s = oracle.quantize(bits, base)
-    reps = (M + w.shape[0] - 1) // w.shape[0]
-    return np.tile(w, (reps, 1))[:M], np.tile(s, reps)[:M]
+    """Every row distinct: W ~ N(0, 0.02) from the library's generator,
+    quantized with the quantize.c rules (ibh_quantize_rows, host threads)."""
+    from libinferbit_amd import ibf
+    W = ibf.fill_normal(M * N, 0x5EED0000 + 97 * seed + bits, std=0.02).reshape(M, N)
+    w, s = ibf.quantize(bits, W)
+    return (w.view(np.int8) if bits == 8 else w), s
 
 
 def time_launches(torch, launch, steps, warmup):
-    """Average device time per launch.  The launches are captured into a HIP
-    graph (one node per weight copy) and the graph is replayed, so the
-    timed region holds back-to-back kernels with no host launch gaps; HIP
-    events on the replay stream bracket the whole timed region."""
-    for i in range(COPIES):
+    """Average device time per launch over exactly `steps` launches.  The
+    launches (weight copy i % COPIES for launch i) are captured into one HIP
+    graph of `steps` nodes, so the timed region holds back-to-back kernels
+    with no host launch gaps; HIP events on the replay stream bracket it.
+    Before it: `warmup` eager launches and one untimed replay of the graph
+    (its first replay uploads the graph)."""
+    for i in range(max(1, warmup)):
         launch(i)                                   # eager warmup, also validates
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     cap = torch.cuda.Stream()
     with torch.cuda.stream(cap):
         with torch.cuda.graph(g, stream=cap):
-            for i in range(COPIES):
+            for i in range(steps):
                 launch(i)
     torch.cuda.synchronize()
-    reps = max(1, steps // COPIES)
-    for _ in range(max(1, warmup // COPIES)):
-        g.replay()
+    g.replay()
     torch.cuda.synchronize()
     st = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(st)
-    for _ in range(reps):
-        g.replay()
+    g.replay()
     e1.record(st)
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / (reps * COPIES) * 1e-3   # seconds per launch
+    return e0.elapsed_time(e1) / steps * 1e-3   # seconds per launch
 
 
 def gemv_case(torch, L, oracle, bits, M, N, steps, warmup, w4a8=False, seed=0):
@@ -356,26 +354,81 @@ def decode_case(name, steps, cpu):
                      "kv_positions": n_pos, "bytes_per_token": nbytes, "GBps": round(nbytes * tok_s / 1e9, 1),
                      "frac_hbm": round(nbytes * tok_s / 1e9 / HBM_PEAK_GBS, 4)}
     if cpu:
-        out["cpu_baseline"] = cpu_decode(path, case)
+        threads = host_cpu()[0]
+        if name == "tinyllama":
+            out["cpu_baseline"] = cpu_decode(path, case, 8, [threads])
+        else:
+            out["cpu_baseline"] = cpu_decode(path, case, 2, [threads])
     return out
 
 
-def cpu_decode(path, case, n_out=8):
-    """The reference CPU decode (oracle/_ref/ref_decode) on the same file, a
-    bounded sample of n_out tokens after a 1-token prompt (no KV prefill)."""
+def host_cpu():
+    """(threads to use, affinity count, model name).  The GPU box gives one
+    GPU a share of 16 host threads (OMP_NUM_THREADS there is 16), whatever the
+    affinity mask shows, so worker pools stop at 16."""
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except AttributeError:
+        aff = os.cpu_count() or 1
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    share = int(os.environ.get("OMP_NUM_THREADS", "16") or 16)
+    return max(1, min(aff, share, 16)), aff, model
+
+
+def _ref_decode(exe, path, threads, n_out, prompt_file, kv_file=None, n_pos=0):
+    cmd = [exe, path, str(threads), "0", str(n_out), prompt_file]
+    if kv_file:
+        cmd += [kv_file, str(n_pos)]
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=900)
+    if r.returncode != 0:
+        raise RuntimeError(r.stderr[-400:])
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
+def cpu_decode(path, case, n_tok, threads_list):
+    """The reference CPU decode (oracle/_ref/ref_decode: inferbit_generate,
+    greedy) on the benchmark configuration's own workload: its prompt, and for
+    the long-context case the KV cache prefilled to kv_pos positions (through
+    the reference's kv_cache_write).  A bounded sample: tok/s = n_tok / (time
+    of prompt + 1 + n_tok tokens - time of prompt + 1 token)."""
+    sys.path.insert(0, os.path.join(ROOT, "tests", "golden"))
+    import gen_decode_golden as G
     exe = os.path.join(ROOT, "oracle", "_ref", "ref_decode")
     if not os.path.exists(exe):
         return None
-    cores = max(1, min(len(os.sched_getaffinity(0)), 16))
     pp = path + ".cpu_prompt.i32"
-    np.array([1], np.int32).tofile(pp)
-    r = subprocess.run([exe, path, str(cores), "0", str(n_out), pp], capture_output=True, text=True, timeout=600)
-    if r.returncode != 0:
-        return None
-    d = json.loads(r.stdout.strip().splitlines()[-1])
-    return {"value": round(d["steps"] / d["seconds"], 3), "unit": "tok/s", "cores": cores, "kind": "reference",
-            "sample": f"inferbit_generate greedy, 1-token prompt + {n_out} tokens ({d['steps']} forward steps), "
-                      f"empty KV cache, {d['seconds']:.2f} s"}
+    G.prompt_of(case).tofile(pp)
+    kvp = None
+    if case["kv_pos"]:
+        kvp = path + ".cpu_kv.f32"
+        if not os.path.exists(kvp):
+            k, v = G.kv_of(case)
+            with open(kvp + ".tmp", "wb") as f:
+                f.write(k.tobytes())
+                f.write(v.tobytes())
+            del k, v
+            os.replace(kvp + ".tmp", kvp)
+    out = []
+    _, aff, model = host_cpu()
+    for threads in threads_list:
+        n = n_tok[threads] if isinstance(n_tok, dict) else n_tok
+        d1 = _ref_decode(exe, path, threads, 1, pp, kvp, case["kv_pos"])
+        d2 = _ref_decode(exe, path, threads, 1 + n, pp, kvp, case["kv_pos"])
+        dt = d2["seconds"] - d1["seconds"]
+        out.append({"value": round(n / dt, 3), "unit": "tok/s", "cores": threads, "kind": "reference",
+                    "sample": f"inferbit_generate greedy, the configuration's {case['n_prompt']}-token prompt"
+                              + (f" over a KV cache prefilled to {case['kv_pos']} positions" if case["kv_pos"] else "")
+                              + f", {n} decode steps timed ({dt:.2f} s) as the difference of two runs",
+                    "host": model, "affinity_cpus": aff})
+    return out
 
 
 V5_TINYLLAMA = dict(num_layers=22, hidden_size=2048, num_heads=32, num_kv_heads=4, head_dim=64,
@@ -438,7 +491,7 @@ def v5_decode_case(steps, cpu):
     if cpu:
         exe = os.path.join(ROOT, "oracle", "_ref", "ref_v5")
         if os.path.exists(exe):
-            cores = max(1, min(len(os.sched_getaffinity(0)), 16))
+            cores = host_cpu()[0]
             pp = path + ".prompt.i32"
             np.asarray(prompt, np.int32).tofile(pp)
             n_cpu = 8
@@ -457,26 +510,30 @@ def v5_decode_case(steps, cpu):
 def cpu_baseline():
     """The reference library compiled from its own sources (oracle/_ref),
     ib_parallel_matmul INT4 14336x4096 with the x86 AVX2 table, timed on
-    this host's cores over rotating weight copies."""
+    this host over rotating weight copies: with the box's thread share and
+    with one thread."""
     exe = os.path.join(ROOT, "oracle", "_ref", "ref_harness")
     if not os.path.exists(exe):
         return None
-    try:
-        cores = len(os.sched_getaffinity(0))
-    except AttributeError:
-        cores = os.cpu_count() or 1
-    cores = max(1, min(cores, 16))
-    iters, copies = 800, 8
-    r = subprocess.run([exe, "gemv", "4", "14336", "4096", str(cores), str(iters), str(copies)],
-                       capture_output=True, text=True, timeout=300)
-    if r.returncode != 0:
-        return None
-    d = json.loads(r.stdout.strip().splitlines()[-1])
+    threads, aff, model = host_cpu()
+    copies = 8
+    res = {}
+    for t, iters in ((threads, 800), (1, 60)):
+        r = subprocess.run([exe, "gemv", "4", "14336", "4096", str(t), str(iters), str(copies)],
+                           capture_output=True, text=True, timeout=300)
+        if r.returncode != 0:
+            return None
+        res[t] = json.loads(r.stdout.strip().splitlines()[-1])
+    d, d1 = res[threads], res[1]
     nbytes = matvec_bytes(14336, 4096, 4)
-    return {"value": round(nbytes / d["median_s"] / 1e9, 2), "unit": "GB/s", "cores": cores,
+    return {"value": round(nbytes / d["median_s"] / 1e9, 2), "unit": "GB/s", "cores": threads,
             "kind": "reference",
-            "sample": f"{iters} calls of ib_parallel_matmul(bits=4) 14336x4096 ({d['simd']}), "
-                      f"{copies} rotating weight copies, median per call {d['median_s'] * 1e6:.0f} us"}
+            "sample": f"{800} calls of ib_parallel_matmul(bits=4) 14336x4096 ({d['simd']}), "
+                      f"{copies} rotating weight copies, median per call {d['median_s'] * 1e6:.0f} us",
+            "one_thread": {"value": round(nbytes / d1["median_s"] / 1e9, 2), "unit": "GB/s",
+                           "median_us": round(d1["median_s"] * 1e6, 1), "calls": 60},
+            "host": model, "affinity_cpus": aff,
+            "threads_note": "worker pools stop at the GPU box's share of 16 host threads"}
 
 
 def main():
@@ -543,7 +600,7 @@ def main():
     if not a.no_decode and not a.quick:
         for name in ("tinyllama", "mistral"):
             print(f"bench: decode {name}", file=sys.stderr, flush=True)
-            decode[name] = decode_case(name, 128, cpu=not a.no_cpu and name == "tinyllama")
+            decode[name] = decode_case(name, 128, cpu=not a.no_cpu)
         print("bench: batched verify (forward_positions)", file=sys.stderr, flush=True)
         decode["tinyllama_forward_positions"] = verify_case(10)
         print("bench: v5 session decode", file=sys.stderr, flush=True)
@@ -556,17 +613,19 @@ def main():
         "n_gpus": 1,
         "steps": a.steps,
         "warmup": a.warmup,
+        "timing": f"{a.steps} launches in one HIP graph, timed by HIP events; {a.warmup} eager warmup launches "
+                  "and one untimed replay before",
         "ms_per_step": round(head["us"] / 1e3, 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int4xf32",
-        "data": "synthetic: W N(0,0.02) quantized with quantize.c rules (256 distinct rows tiled), x N(0,1)",
+        "data": "synthetic: W N(0,0.02), every row distinct, quantized with quantize.c rules, x N(0,1)",
         "config": {"workload": "INT4 matvec 14336x4096 batch 1 (matmul_int4), 16 rotating weight copies",
                    "M": 14336, "N": 4096, "batch": 1, "bits": 4},
         "roofline": {"bound": "hbm", "achieved": head["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": head["frac_hbm"], "traffic": measured_traffic(),
-                     "kernel": "gemv_rows_x<4,...>", "bytes_per_launch": head["bytes"],
+                     "kernel": "gemv_tile_x<4,...>", "bytes_per_launch": head["bytes"],
                      "us_per_launch": head["us"]},
         "cpu_baseline": cpu,
         "decode_tok_s": decode.get("mistral", {}).get("exact", {}).get("tok_s"),
