@@ -40,7 +40,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--quick", action="store_true", help="headline only (for profiling runs)")
     p.add_argument("--no-decode", action="store_true", help="skip the end-to-end decode legs")
-    p.add_argument("--only", choices=["headline", "gemm", "pq", "pqpol", "int4g", "verify", "v5", "decode-tinyllama",
+    p.add_argument("--only", choices=["headline", "floor", "gemm", "pq", "pqpol", "int4g", "verify", "v5", "decode-tinyllama",
                             "decode-mistral"],
                    help="run one case and print its JSON (for profiler runs)")
     p.add_argument("--calib-copy", action="store_true",
@@ -141,6 +141,23 @@ def gemv_case(torch, L, oracle, bits, M, N, steps, warmup, w4a8=False, seed=0):
     return {"M": M, "N": N, "bits": bits, "w4a8": w4a8, "us": round(t * 1e6, 3),
             "bytes": nbytes, "GBps": round(nbytes / t / 1e9, 1),
             "frac_hbm": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
+
+
+def floor_case(torch, L, steps, warmup):
+    """The per-launch floor (an empty kernel) and a plain streaming read of
+    the headline's 29,462,528 bytes (ibh_probe), timed like the matvecs."""
+    nbytes = matvec_bytes(14336, 4096, 4)
+    bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(i + 1) for i in range(COPIES)]
+    st = lambda: torch.cuda.current_stream().cuda_stream
+    out = {}
+    for mode, name in ((0, "empty_kernel"), (1, "read_29462528_bytes")):
+        def launch(i, mode=mode):
+            L._lib.check(L.lib().ibh_probe(mode, bufs[i % COPIES].data_ptr(), nbytes, st()), "ibh_probe")
+        t = time_launches(torch, launch, steps, warmup)
+        out[name] = {"us": round(t * 1e6, 3)}
+        if mode == 1:
+            out[name].update(GBps=round(nbytes / t / 1e9, 1), frac_hbm=round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4))
+    return out
 
 
 def batch_case(torch, L, oracle, B, steps, warmup):
@@ -552,6 +569,8 @@ def main():
     if a.only:
         if a.only == "headline":
             r = gemv_case(torch, L, oracle, 4, 14336, 4096, a.steps, a.warmup)
+        elif a.only == "floor":
+            r = floor_case(torch, L, a.steps, a.warmup)
         elif a.only == "gemm":
             r = prefill_gemm_case(torch, L, 64, 8)
         elif a.only == "pq":
@@ -573,7 +592,7 @@ def main():
         return
     print("bench: headline INT4 GEMV 14336x4096", file=sys.stderr, flush=True)
     head = gemv_case(torch, L, oracle, 4, 14336, 4096, a.steps, a.warmup)
-    extra = {}
+    extra = {"floor": floor_case(torch, L, a.steps, a.warmup)}
     if not a.quick:
         for name, (bits, M, N, w4a8) in {
             "int4_4096x14336": (4, 4096, 14336, False),

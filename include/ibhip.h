@@ -76,10 +76,18 @@ int ibh_matmul(float* out, const void* w, const void* scales, int scale_kind,
                const float* x, int M, int N, int bits, void* stream);
 
 /* Tuning hook for the tile matvec kernel behind ibh_matmul (no counterpart in
- * the reference): R 16-row tiles x KS 64-byte steps per wavefront, WR row
- * groups per block (0 = automatic); R = 0 restores the automatic choice,
- * R = -1 switches the tile kernel off (the row kernels then serve). */
-int ibh_set_tile_config(int R, int KS, int WR);
+ * the reference).  mode 1: KS 256-byte row steps per weight wavefront (4, 7,
+ * 8, 14 or 16; 0 = automatic), WR row quads per block (0 = automatic), delay
+ * units (~0.1 us each) that weight wavefronts wait before issuing their loads
+ * (-1 = automatic).  mode 0 restores every automatic choice; mode -1 switches
+ * the tile kernel off (the row kernels then serve). */
+int ibh_set_tile_config(int mode, int KS, int WR, int delay);
+
+/* Measurement probes (no counterpart in the reference): mode 0 launches an
+ * empty kernel on a 256 x 16-wavefront grid (the per-launch floor); mode 1
+ * reads `bytes` of `buf` once with 16-byte loads, 1 KB contiguous per
+ * instruction (the streaming rate a matvec of that size is judged against). */
+int ibh_probe(int mode, const void* buf, size_t bytes, void* stream);
 
 /* Per-128-group int8 activation quantization, bit-identical to
  * ib_quantize_input_int8_g128 (src/threading.c:401-432).  q[N], s[ceil(N/128)]. */

@@ -25,7 +25,8 @@ SIGNATURES = {
     "ibh_memcpy_d2h": (I, [P, P, SZ, P]),
     "ibh_memcpy_d2d": (I, [P, P, SZ, P]),
     "ibh_matmul": (I, [P, P, P, I, P, I, I, I, P]),
-    "ibh_set_tile_config": (I, [I, I, I]),
+    "ibh_set_tile_config": (I, [I, I, I, I]),
+    "ibh_probe": (I, [I, P, SZ, P]),
     "ibh_matmul_w4a8_x_noalloc": (I, [P, P, P, I, P, I, I, P]),
     "ibh_quantize_act_g128": (I, [P, P, P, I, P]),
     "ibh_matmul_w4a8": (I, [P, P, P, I, P, P, I, I, P]),

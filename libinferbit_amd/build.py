@@ -15,7 +15,7 @@ CSRC = os.path.join(HERE, "csrc")
 OUT_DIR = os.path.join(HERE, "_build")
 LIB = os.path.join(OUT_DIR, "libibhip.so")
 
-SOURCES = ["ibh_runtime.hip", "ibh_gemv.hip", "ibh_mfma.hip", "ibh_rows.hip", "ibh_tile.hip", "ibh_attn.hip", "ibh_pq.hip", "ibh_int4g.hip", "ibh_v5.hip", "ibh_decode.hip", "ibh_exact.hip", "ibh_gemm.hip", "ibh_host.cpp", "ibh_spec.cpp", "ibh_sample.cpp", "ibh_v5_sample.cpp"]
+SOURCES = ["ibh_runtime.hip", "ibh_gemv.hip", "ibh_mfma.hip", "ibh_rows.hip", "ibh_tile.hip", "ibh_probe.hip", "ibh_attn.hip", "ibh_pq.hip", "ibh_int4g.hip", "ibh_v5.hip", "ibh_decode.hip", "ibh_exact.hip", "ibh_gemm.hip", "ibh_host.cpp", "ibh_spec.cpp", "ibh_sample.cpp", "ibh_v5_sample.cpp"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

@@ -54,7 +54,28 @@ namespace {
 
 typedef int i4_t __attribute__((ext_vector_type(4)));
 
+// Timeline probes, compiled only with -DIBH_TILE_TRACE (a development build
+// outside the library): s_memrealtime at the phase boundaries of each block's
+// last weight wavefront (and of activation wavefront 0), kept in ibh_tile_tt.
+#ifdef IBH_TILE_TRACE
+__device__ unsigned long long ibh_tile_tt[8192][8];
+#define IBH_TT(i) (tt[(i)] = __builtin_amdgcn_s_memrealtime())
+#define IBH_TT_END(r)                                                                   \
+    do {                                                                                \
+        if (lane == 0 && (wave == 0 || wave == (int)(blockDim.x >> 6) - 1) && blockIdx.x < 8192) { \
+            unsigned long long* o = ibh_tile_tt[blockIdx.x];                              \
+            if (wave == 0) { o[0] = tt[0]; o[1] = tt[1]; o[2] = tt[2]; }                  \
+            else { o[3] = tt[3]; o[4] = tt[4]; o[5] = tt[5]; o[6] = tt[6];                \
+                   o[7] = __builtin_amdgcn_s_memrealtime(); }                             \
+        }                                                                               \
+    } while (0)
+#else
+#define IBH_TT(i) ((void)0)
+#define IBH_TT_END(r) ((void)0)
+#endif
+
 constexpr int kTileMaxWaves = 16;
+constexpr int kTileMaxChunks = 64;          // digit chunks (64 runs of x each) per block
 
 template <int BITS>
 struct TGeo {
@@ -117,108 +138,139 @@ __device__ __forceinline__ void lds_wait(int* c, int n) {
 }
 
 // Block = NXW activation wavefronts (waves 0..NXW-1) + WQ quads x KW K-ranges
-// of weight wavefronts.  The activation waves never touch the weights, so the
-// digit planes are ready soon after x arrives, however long the weight
-// wavefronts stay blocked issuing their loads; the weight waves wait on an LDS
-// counter only once their own loads are in flight.
+// of weight wavefronts.  The activation waves never touch the weights: they
+// load x first thing, stage it in LDS and post max|x|, so x is not queued
+// behind their own weight loads.  The digit planes are then made by every
+// wave of the block, one 64-run chunk at a time claimed from an LDS counter:
+// a weight wave joins as soon as its loads are issued (until then the memory
+// pipeline keeps it waiting anyway), so the planes are ready shortly after x
+// arrives.  A weight wave contracts once every chunk is written (a second
+// LDS counter), never at a block barrier.
 // x digits: Q = trunc(x * 2^14 / s) (|Q| < 2^21), d0 = Q >> 14 (signed),
 // d1 = (Q >> 7) & 127, d2 = Q & 127, so Q = 2^14 d0 + 2^7 d1 + d2 and
 // |x/s - Q/2^14| < 1.2 * 2^-14.  The bias term needs only sum(Q).
-template <int BITS, int KIND, int KS>
+template <int BITS>
+__device__ __forceinline__ void digit_chunk(unsigned char* smem, const float* xraw, int k, int lane, int N,
+                                            float kq, int* qpart) {
+    constexpr int NA = TGeo<BITS>::NA;
+    constexpr int RUN = 4 * NA;
+    const int c = RUN * (64 * k + lane);
+    int sd0 = 0, sq = 0;
+    if (c < N) {
+        // column c + e: step, chunk, k-group, slot t0 + e / NA, operand e % NA
+        const int st = c / TGeo<BITS>::kStepCols;
+        const int cs = c - st * TGeo<BITS>::kStepCols;
+        const int ch = cs / (64 * NA);
+        const int cg = (cs - ch * 64 * NA) / (16 * NA);
+        const int t0 = (cs - ch * 64 * NA - cg * 16 * NA) / NA;
+        float4 xv[NA];
+#pragma unroll
+        for (int h = 0; h < NA; h++) xv[h] = *(const float4*)(xraw + c + 4 * h);
+        uint32_t b0[RUN], b1[RUN], b2[RUN];
+#pragma unroll
+        for (int e = 0; e < RUN; e++) {
+            const float4 f = xv[e >> 2];
+            const float xe = (e & 3) == 0 ? f.x : (e & 3) == 1 ? f.y : (e & 3) == 2 ? f.z : f.w;
+            const int q = (int)(xe * kq);
+            b0[e] = (uint32_t)(q >> 14);
+            b1[e] = ((uint32_t)q >> 7) & 127u;
+            b2[e] = (uint32_t)q & 127u;
+            if constexpr (TGeo<BITS>::kBias != 0) {
+                sd0 += q >> 14;
+                sq += q & 0x3fff;
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < NA; h++) {
+            unsigned char* base = smem + b_off<BITS>(st, h, 4 * ch, cg) + t0;
+            *(uint32_t*)(base + 0 * 64) = pack_lo_bytes(b0[h], b0[h + NA], b0[h + 2 * NA], b0[h + 3 * NA]);
+            *(uint32_t*)(base + 1 * 64) = pack_lo_bytes(b1[h], b1[h + NA], b1[h + 2 * NA], b1[h + 3 * NA]);
+            *(uint32_t*)(base + 2 * 64) = pack_lo_bytes(b2[h], b2[h + NA], b2[h + 2 * NA], b2[h + 3 * NA]);
+        }
+    }
+    if constexpr (TGeo<BITS>::kBias != 0) {
+        sd0 = wave_isum_dpp(sd0);
+        sq = wave_isum_dpp(sq);
+        // chunk k's sums in its own slot (every lane writes the same value)
+        qpart[2 * k] = sd0;
+        qpart[2 * k + 1] = sq;
+    }
+}
+
+// Claims chunks of the digit planes until none is left.  Every lane adds 1
+// to both counters (a wave-uniform value, one LDS atomic of 64 per wave), so
+// a claim is (old >> 6) and a finished chunk counts 64 in *done (release:
+// its LDS writes are visible to whoever sees the count).  No branch in the
+// loop depends on the lane; it runs at most nchunks + 1 times.
+template <int BITS>
+__device__ __forceinline__ void digit_work(unsigned char* smem, const float* xraw, int* next, int* done, int nchunks,
+                                           int lane, int N, float kq, int* qpart) {
+    for (int it = 0; it <= nchunks; it++) {
+        const int got = __hip_atomic_fetch_add(next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        const int k = __builtin_amdgcn_readfirstlane(got) >> 6;
+        if (k >= nchunks) break;
+        digit_chunk<BITS>(smem, xraw, k, lane, N, kq, qpart);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __hip_atomic_fetch_add(done, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+}
+
+template <int BITS, int KIND, int KS, int CH>
 __global__ __launch_bounds__(1024) void gemv_tile_x(const RowSet rs, const float* __restrict__ x, int N, int S,
-                                                    int WQ, int KW, int NXW) {
+                                                    int WQ, int KW, int NXW, int delay) {
     constexpr int NA = TGeo<BITS>::NA;
     constexpr int RUN = 4 * NA;             // consecutive columns per x run
-    constexpr int XR = 32 / RUN;            // runs per activation lane (32 floats)
+    constexpr int XF = 8;                   // float4 of x per activation lane
     constexpr int kBias = TGeo<BITS>::kBias;
     const RowPick P = pick_rows(rs);
     extern __shared__ __align__(16) unsigned char smem[];
+    float* xraw = (float*)(smem + (size_t)S * NA * 1024);   // x as loaded
     __shared__ float red[kTileMaxWaves];
-    __shared__ int qsum[kTileMaxWaves][2];
-    __shared__ float xs_sh;
-    __shared__ int cnt[2];                  // activation waves that posted max|x| / finished the planes
+    __shared__ int qpart[2 * kTileMaxChunks];   // per digit chunk: sum of d0, sum of (Q & 0x3fff)
+    __shared__ int cnt[3];                  // waves that posted max|x|; digit chunks done; next chunk
     __shared__ int part[kTileMaxWaves][4][3];
     __shared__ __align__(16) int epi[kTileMaxWaves][48];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    if (threadIdx.x < 2) cnt[threadIdx.x] = 0;
+    const int nchunks = (N + 64 * RUN - 1) / (64 * RUN);
+#ifdef IBH_TILE_TRACE
+    unsigned long long tt[8];
+#endif
+    if (threadIdx.x < 3) cnt[threadIdx.x] = 0;
     __syncthreads();
+    IBH_TT(0);
 
     if (wave < NXW) {
-        // ── activation wavefront: x -> three digit planes in B-operand order
-        float4 xv[XR][NA];
+        // ── activation wavefront: x -> LDS, max|x|, then digit chunks
+        float4 xv[XF];
 #pragma unroll
-        for (int u = 0; u < XR; u++) {
-            const int c = RUN * (lane + 64 * (wave + NXW * u));
-#pragma unroll
-            for (int h = 0; h < NA; h++)
-                xv[u][h] = c < N ? *(const float4*)(x + c + 4 * h) : float4{0.f, 0.f, 0.f, 0.f};
+        for (int u = 0; u < XF; u++) {
+            const int c4 = lane + 64 * (wave + NXW * u);   // float4 index
+            xv[u] = 4 * c4 < N ? ((const float4*)x)[c4] : float4{0.f, 0.f, 0.f, 0.f};
         }
         float mx = 0.f;
 #pragma unroll
-        for (int u = 0; u < XR; u++)
-#pragma unroll
-            for (int h = 0; h < NA; h++)
-                mx = fmaxf(fmaxf(mx, fmaxf(fabsf(xv[u][h].x), fabsf(xv[u][h].y))),
-                           fmaxf(fabsf(xv[u][h].z), fabsf(xv[u][h].w)));
+        for (int u = 0; u < XF; u++) {
+            const int c4 = lane + 64 * (wave + NXW * u);
+            if (4 * c4 < N) ((float4*)xraw)[c4] = xv[u];
+            mx = fmaxf(fmaxf(mx, fmaxf(fabsf(xv[u].x), fabsf(xv[u].y))), fmaxf(fabsf(xv[u].z), fabsf(xv[u].w)));
+        }
         mx = wave_max_dpp(mx);
-        if (NXW > 1) {
-            if (lane == 0) {
-                red[wave] = mx;
-                lds_signal(&cnt[0]);
-            }
-            lds_wait(&cnt[0], NXW);
-            for (int w = 0; w < NXW; w++) mx = fmaxf(mx, red[w]);
-        }
-        const float xs = mx > 0.f ? mx / 127.0f : 1.0f;
-        const float kq = (1.0f / xs) * 16384.0f;
-        int sd0 = 0, sq = 0;
-#pragma unroll
-        for (int u = 0; u < XR; u++) {
-            const int c = RUN * (lane + 64 * (wave + NXW * u));
-            if (c < N) {
-                // column c + e: step, chunk, k-group, slot t0 + e / NA, operand e % NA
-                const int st = c / TGeo<BITS>::kStepCols;
-                const int cs = c - st * TGeo<BITS>::kStepCols;
-                const int ch = cs / (64 * NA);
-                const int cg = (cs - ch * 64 * NA) / (16 * NA);
-                const int t0 = (cs - ch * 64 * NA - cg * 16 * NA) / NA;
-                uint32_t b0[RUN], b1[RUN], b2[RUN];
-#pragma unroll
-                for (int e = 0; e < RUN; e++) {
-                    const float4 f = xv[u][e >> 2];
-                    const float xe = (e & 3) == 0 ? f.x : (e & 3) == 1 ? f.y : (e & 3) == 2 ? f.z : f.w;
-                    const int q = (int)(xe * kq);
-                    b0[e] = (uint32_t)(q >> 14);
-                    b1[e] = ((uint32_t)q >> 7) & 127u;
-                    b2[e] = (uint32_t)q & 127u;
-                    if constexpr (kBias != 0) {
-                        sd0 += q >> 14;
-                        sq += q & 0x3fff;
-                    }
-                }
-#pragma unroll
-                for (int h = 0; h < NA; h++) {
-                    unsigned char* base = smem + b_off<BITS>(st, h, 4 * ch, cg) + t0;
-                    *(uint32_t*)(base + 0 * 64) = pack_lo_bytes(b0[h], b0[h + NA], b0[h + 2 * NA], b0[h + 3 * NA]);
-                    *(uint32_t*)(base + 1 * 64) = pack_lo_bytes(b1[h], b1[h + NA], b1[h + 2 * NA], b1[h + 3 * NA]);
-                    *(uint32_t*)(base + 2 * 64) = pack_lo_bytes(b2[h], b2[h + NA], b2[h + 2 * NA], b2[h + 3 * NA]);
-                }
-            }
-        }
-        if constexpr (kBias != 0) {
-            sd0 = wave_isum_dpp(sd0);
-            sq = wave_isum_dpp(sq);
-        }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         if (lane == 0) {
-            qsum[wave][0] = sd0;
-            qsum[wave][1] = sq;
-            if (wave == 0) xs_sh = xs;
-            lds_signal(&cnt[1]);
+            red[wave] = mx;
+            lds_signal(&cnt[0]);
         }
+        lds_wait(&cnt[0], NXW);
+        IBH_TT(1);
+        float gm = 0.f;
+        for (int w = 0; w < NXW; w++) gm = fmaxf(gm, red[w]);
+        const float xs = gm > 0.f ? gm / 127.0f : 1.0f;
+        digit_work<BITS>(smem, xraw, &cnt[2], &cnt[1], nchunks, lane, N, (1.0f / xs) * 16384.0f, qpart);
+        IBH_TT(2);
+        IBH_TT_END(0);
         if (KW > 1) __syncthreads();   // pairs with the weight waves' K-range barrier
         return;
     }
@@ -238,6 +290,7 @@ __global__ __launch_bounds__(1024) void gemv_tile_x(const RowSet rs, const float
     uint32_t rsc_bits;
     if constexpr (KIND == IBH_SCALE_F16) rsc_bits = ((const uint16_t*)P.sc)[srow];
     else rsc_bits = ((const uint32_t*)P.sc)[srow];
+    for (int i = 0; i < delay; i++) __builtin_amdgcn_s_sleep(4);   // 256 clocks each
     uint4 wv[KS];
     const int s0 = wk * KS;
     {
@@ -245,22 +298,39 @@ __global__ __launch_bounds__(1024) void gemv_tile_x(const RowSet rs, const float
 #pragma unroll
         for (int j = 0; j < KS; j++) wv[j] = ld_stream16(base + j * 256);
     }
-    __builtin_amdgcn_sched_barrier(0);   // every load is issued before the wait below
-    lds_wait(&cnt[1], NXW);
+    __builtin_amdgcn_sched_barrier(0);   // every load is issued before the waits below
+    lds_wait(&cnt[0], NXW);
+    IBH_TT(3);
+    float gm = 0.f;
+    for (int w = 0; w < NXW; w++) gm = fmaxf(gm, red[w]);
+    const float xs = gm > 0.f ? gm / 127.0f : 1.0f;
+    digit_work<BITS>(smem, xraw, &cnt[2], &cnt[1], nchunks, lane, N, (1.0f / xs) * 16384.0f, qpart);
+    IBH_TT(4);
+    lds_wait(&cnt[1], 64 * nchunks);
+    IBH_TT(5);
 
     // contract: exact int32 per (chunk, row) x (chunk, plane) over this
     // wavefront's steps (S is a multiple of KS)
-    i4_t acc = {0, 0, 0, 0};
+    // two independent accumulator chains halve the dependent-MFMA tail that
+    // follows the last load's arrival
+    i4_t accs[CH];
+#pragma unroll
+    for (int c = 0; c < CH; c++) accs[c] = i4_t{0, 0, 0, 0};
     const unsigned char* bb = smem + b_off<BITS>(s0, 0, m, kg);
 #pragma unroll
     for (int j = 0; j < KS; j++) {
 #pragma unroll
         for (int h = 0; h < NA; h++) {
             const i4_t b = *(const i4_t*)(bb + (j * NA + h) * 1024);
-            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(tile_operand_h<BITS>(wv[j], h), b, acc, 0, 0, 0);
+            i4_t& a = accs[(j * NA + h) % CH];
+            a = __builtin_amdgcn_mfma_i32_16x16x64_i8(tile_operand_h<BITS>(wv[j], h), b, a, 0, 0, 0);
         }
     }
+    i4_t acc = accs[0];
+#pragma unroll
+    for (int c = 1; c < CH; c++) acc += accs[c];
 
+    IBH_TT(6);
     // chunk sums through LDS: lane 20c + p (register i) holds row i, plane p,
     // chunk c; lane i < 4 then sums row i's four chunks per plane
     int* ep = epi[wave];                                   // [row i][plane p][chunk c]
@@ -301,20 +371,27 @@ __global__ __launch_bounds__(1024) void gemv_tile_x(const RowSet rs, const float
         double v = (double)a0 * 16384.0 + (double)a1 * 128.0 + (double)a2;
         if constexpr (kBias != 0) {
             long long sQ = 0;
-            for (int w = 0; w < NXW; w++) sQ += (long long)qsum[w][0] * 16384 + qsum[w][1];
+            for (int c = 0; c < nchunks; c++) sQ += (long long)qpart[2 * c] * 16384 + qpart[2 * c + 1];
             v -= (double)kBias * (double)sQ;
         }
         const float rsc = KIND == IBH_SCALE_F16 ? f16_to_f32((uint16_t)rsc_bits) : __builtin_bit_cast(float, rsc_bits);
-        y[row0 + lane] = (float)(v * ((double)xs_sh * (1.0 / (16384.0 * TGeo<BITS>::kOpScale)))) * rsc;
+        y[row0 + lane] = (float)(v * ((double)xs * (1.0 / (16384.0 * TGeo<BITS>::kOpScale)))) * rsc;
+        IBH_TT_END(row0 + lane);
     }
 }
 
 // Geometry override (0 = automatic); set by ibh_set_tile_config.
-int g_tile_mode = 0, g_tile_KS = 0, g_tile_WR = 0;
+int g_tile_mode = 0, g_tile_KS = 0, g_tile_WR = 0, g_tile_delay = -1;
 
 }  // namespace
 
-extern "C" int ibh_set_tile_config(int mode, int KS, int WR) {
+#ifdef IBH_TILE_TRACE
+extern "C" int ibh_tile_trace_read(void* out) {
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(ibh_tile_tt), sizeof(ibh_tile_tt)) == hipSuccess ? 0 : -1;
+}
+#endif
+
+extern "C" int ibh_set_tile_config(int mode, int KS, int WR, int delay) {
     if (mode > 0 && KS != 4 && KS != 7 && KS != 8 && KS != 14 && KS != 16) {
         ibh_set_error("ibh_set_tile_config: unsupported KS=%d (4, 7, 8, 14 or 16)", KS);
         return IBH_ERROR_PARAM;
@@ -326,6 +403,7 @@ extern "C" int ibh_set_tile_config(int mode, int KS, int WR) {
     g_tile_mode = mode < 0 ? -1 : (mode > 0 ? 1 : 0);
     g_tile_KS = KS;
     g_tile_WR = WR;
+    g_tile_delay = mode > 0 ? std::min(delay, 64) : -1;
     return IBH_OK;
 }
 
@@ -344,7 +422,8 @@ int ibh_launch_tile_x_multi(const MatDesc* d, int n, int kind, const float* x, i
     const int S = (int)(rb / 256);
     // activation waves: 32 floats of x per lane
     const int nxw = (N + 2047) / 2048;
-    if (nxw > 8) return 0;
+    if (nxw > 8 || N % 4) return 0;
+    if ((N + 64 * 4 * (8 / bits) - 1) / (64 * 4 * (8 / bits)) > kTileMaxChunks) return 0;
     // KS steps per weight wavefront (<= 16 loads per lane), dividing S
     int KS = 0;
     for (int c : {16, 14, 8, 7, 4})
@@ -358,12 +437,20 @@ int ibh_launch_tile_x_multi(const MatDesc* d, int n, int kind, const float* x, i
     int WQ = std::min(wq_max, std::max(1, (quads + 255) / 256));
     if (g_tile_mode > 0 && g_tile_WR) WQ = std::min(g_tile_WR, wq_max);
     const int nthreads = 64 * (nxw + WQ * KW);
-    const size_t lds = (size_t)S * (8 / bits) * 1024;
+    // Weight wavefronts hold their loads back ~0.1 us per unit so that the
+    // activation loads of every block reach the memory queues first (x is
+    // needed before any contraction; behind the weight flood it arrives
+    // microseconds late).  Measured on MI355X: 3 units pays 0.6-1.7 us on
+    // long rows (4096 x 14336), on int2 and on small matrices; on tall int8 /
+    // int4 matrices with short rows (14336 x 4096) 1 unit is best.
+    int delay = (bits >= 4 && quads * 4 >= 2 * N) ? 1 : 3;
+    if (g_tile_mode > 0 && g_tile_delay >= 0) delay = g_tile_delay;
+    const size_t lds = (size_t)S * (8 / bits) * 1024 + 4 * (size_t)N;
     if (lds > 150 * 1024) return 0;
     const RowSet rs = make_rowset(d, n, 4 * WQ);
     const int blocks = rowset_blocks(d, n, 4 * WQ);
 #define IBH_TX(B_, K_, KS_) \
-    gemv_tile_x<B_, K_, KS_><<<blocks, nthreads, lds, st>>>(rs, x, N, S, WQ, KW, nxw)
+    gemv_tile_x<B_, K_, KS_, 2><<<blocks, nthreads, lds, st>>>(rs, x, N, S, WQ, KW, nxw, delay)
 #define IBH_TXC(B_, K_) do { switch (KS) { case 4: IBH_TX(B_, K_, 4); break; case 7: IBH_TX(B_, K_, 7); break; \
                                            case 8: IBH_TX(B_, K_, 8); break; case 14: IBH_TX(B_, K_, 14); break; \
                                            default: IBH_TX(B_, K_, 16); break; } } while (0)
