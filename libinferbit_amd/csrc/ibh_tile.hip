@@ -424,10 +424,11 @@ int ibh_launch_tile_x_multi(const MatDesc* d, int n, int kind, const float* x, i
     const int nxw = (N + 2047) / 2048;
     if (nxw > 8 || N % 4) return 0;
     if ((N + 64 * 4 * (8 / bits) - 1) / (64 * 4 * (8 / bits)) > kTileMaxChunks) return 0;
-    // KS steps per weight wavefront (<= 16 loads per lane), dividing S
+    // KS steps per weight wavefront (<= 16 loads per lane), dividing S; not 16
+    // for int2, whose 64 MFMA operands per wavefront would spill
     int KS = 0;
     for (int c : {16, 14, 8, 7, 4})
-        if (S % c == 0 && S / c + nxw <= kTileMaxWaves) { KS = c; break; }
+        if (S % c == 0 && S / c + nxw <= kTileMaxWaves && !(bits == 2 && c == 16)) { KS = c; break; }
     if (g_tile_mode > 0 && g_tile_KS) KS = g_tile_KS;
     if (KS == 0 || S % KS != 0) return 0;
     const int KW = S / KS;
