@@ -392,7 +392,7 @@ extern "C" int ibh_tile_trace_read(void* out) {
 #endif
 
 extern "C" int ibh_set_tile_config(int mode, int KS, int WR, int delay) {
-    if (mode > 0 && KS != 4 && KS != 7 && KS != 8 && KS != 14 && KS != 16) {
+    if (mode > 0 && KS != 0 && KS != 4 && KS != 7 && KS != 8 && KS != 14 && KS != 16) {
         ibh_set_error("ibh_set_tile_config: unsupported KS=%d (4, 7, 8, 14 or 16)", KS);
         return IBH_ERROR_PARAM;
     }
