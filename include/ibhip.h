@@ -199,7 +199,12 @@ typedef struct {
  * ib_pq_matmul_fp32_threaded (src/pq_decode.c:1684-1810): same chunk
  * skipping rule, tables, gather and outlier sidecar; fp32 summation order
  * differs.  Returns 0 / negative like the reference (plus a message).
- * `ws` >= ibh_pq_workspace_bytes(t) bytes, NULL = library workspace. */
+ * `ws` >= ibh_pq_workspace_bytes(t) bytes, NULL = library workspace.
+ * Single-level work (one level, or level 1 only) with G <= 16 and K <= 256
+ * runs in one launch whose blocks meet through per-row-tile arrival counters
+ * kept in device memory (they return to zero at the end of every call): PQ
+ * calls that overlap on one GPU (different streams) race, as calls sharing
+ * a workspace already do. */
 size_t ibh_pq_workspace_bytes(const ibh_pq_tensor* t);
 int    ibh_pq_matmul(const ibh_pq_tensor* t, const float* x, float* out, void* ws,
                      size_t ws_bytes, void* stream);
@@ -220,6 +225,10 @@ int    ibh_pq_matmul_streaming(const ibh_pq_tensor* t, const float* x, float* ou
  * fp32 rounding of its threshold may go the other way.  Same workspace. */
 int    ibh_pq_matmul_policy(const ibh_pq_tensor* t, const float* x, float* out, const ibh_pq_policy* policy,
                             void* ws, size_t ws_bytes, void* stream);
+/* Development switch (no counterpart in the reference): 0 sends every PQ
+ * matvec through the three-kernel path (tables, gather, reduce), 1 (the
+ * default) lets eligible tensors run in one launch. */
+int    ibh_pq_set_fused(int on);
 /* ib_pq_matmul_fp32_q8lut (src/pq_decode.c:2340-2561): every chunk's tables
  * (the matmul_impl entry order) quantised to int8 with one scale per
  * (chunk, side) -- max|T|/127, round half away, clamp [-128, 127] -- then

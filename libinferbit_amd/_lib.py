@@ -40,6 +40,7 @@ SIGNATURES = {
     "ibh_attn_decode": (I, [P, P, P, P, P, P, I, I, I, I, I, P, SZ, P]),
     "ibh_pq_workspace_bytes": (SZ, [P]),
     "ibh_pq_matmul": (I, [P, P, P, P, SZ, P]),
+    "ibh_pq_set_fused": (I, [I]),
     "ibh_pq_matmul_streaming": (I, [P, P, P, P, SZ, P]),
     "ibh_pq_matmul_policy": (I, [P, P, P, P, P, SZ, P]),
     "ibh_pq_matmul_q8lut": (I, [P, P, P, P, SZ, P]),

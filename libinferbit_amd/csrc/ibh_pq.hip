@@ -349,6 +349,340 @@ __global__ __launch_bounds__(kThreads) void pq_reduce(PqDev t, const float* __re
 }
 
 
+// ── one-launch PQ matvec (level 1, G <= 16, K <= 256) ──────────────────────
+// Block = (tile of 512 rows, slab of 32 chunks), 1024 threads: two per row,
+// thread q of a row owns chunks 16q..16q+15 of the slab on both sides.  The
+// two slabs that share the 64-byte index segments of a row run on one XCD,
+// back to back (its L2 serves the second).
+//  1. Global loads first: the slab's x, the codebooks, x for the max|x|
+//     scan, and last the row's index bytes (one 16-byte load per side), so
+//     the table phase does not wait for those HBM reads.
+//  2. The slab's tables T[c][side][k] = cb_side[k] . x[chunk c, side] on the
+//     matrix cores: per side, a 32-code x 32-chunk tile is one
+//     v_mfma_f32_32x32x16_f16 with A = [cb | cb] (the fp16 codewords, exact)
+//     and B = [x_hi ; x_lo], x scaled per (chunk, side) by a power of two
+//     (exact) and split into two fp16 parts; products are exact and sums
+//     fp32, so an entry carries ~2^-22 of its chunk's max|x| (the CPU's fp32
+//     table sum carries ~2^-24 per term).
+//  3. Max|x| over the inner columns (the skipping rule of
+//     pq_decode.c:1569-1616), the slab's chunk maxima, max|codeword|.
+//  4. Gather: 32 LDS lookups per thread, the row's two partials summed.
+//  5. Slabs meet per row in one 64-bit word: each slab adds
+//     2^58 + round(partial * 2^q) + 2^50 (an agent-scope atomic with return,
+//     performed where every XCD sees it).  2^q maps the largest sum the
+//     inputs allow (N * max|cb| * max|x|, doubled) to 2^50, so every term is
+//     an exact integer below 2^51 and the sum of at most 63 slabs stays
+//     below 2^58; the count sits above.  The slab whose add completes the
+//     count has the whole row in the returned value: it applies the row scale
+//     and the outliers, writes y and clears the word for the next call.
+//     Integer addition is associative: y does not depend on arrival order.
+constexpr int kFThreads = 1024;
+constexpr int kFRows = 512;
+constexpr int kFCS = 32;
+constexpr int kFMaxS = 63;
+constexpr int kFMaxRows = 131072;
+constexpr int kXS = 20;   // LDS floats per slab chunk: 8 per side (zero padded) + 4 (bank spread)
+__device__ unsigned long long pq_row_acc[kFMaxRows];   // zero at load; each row's last slab clears it
+
+// Phase probes, compiled only with -DIBH_PQ_TRACE (a development build
+// outside the library): s_memrealtime of thread 0 of each block.
+#ifdef IBH_PQ_TRACE
+__device__ unsigned long long ibh_pq_tt[4096][8];
+#define PQ_TT(i) do { if (tid == 0 && blockIdx.x < 4096) ibh_pq_tt[blockIdx.x][i] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#else
+#define PQ_TT(i) ((void)0)
+#endif
+
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f16x_t __attribute__((ext_vector_type(16)));
+
+// One table tile (side sd, codes 32*kt.., chunks 32*ct.. of the slab; the
+// item index is wave-uniform, so its decomposition is scalar work) from the
+// block's LDS copies of the codebooks (fp16, rows padded to 8) and of the
+// slab's x, scaled by 2^-e (e: exponent of max|x|, one per call, so the
+// entries are T * 2^-e and the row sums are rescaled once).  Tiles with
+// kt == 0 also record each (chunk, side)'s max|x|.
+template <bool KA, int CS>
+__device__ __forceinline__ void table_tile(const PqDev& t, const h8_t* cbs, const float* xsl, int it, int KT, int CT,
+                                           int cn, int lane, int TS, float xscale, float* T, float (*cmax_s)[CS]) {
+    const int K = t.K;
+    const int sd = it / (KT * CT), rest = it - sd * KT * CT, kt = rest / CT, ct = rest - kt * CT;
+    const int k = min(kt * 32 + (lane & 31), K - 1);
+    const int cc = ct * 32 + (lane & 31);
+    const int ccl = min(cc, cn - 1);
+    const h8_t a = cbs[sd * K + k];
+    const float4* xp = (const float4*)(xsl + ccl * kXS + sd * 8);
+    const float4 x0 = xp[0], x1 = xp[1];
+    const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    if (kt == 0) {
+        float m = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) m = fmaxf(m, fabsf(xv[i]));
+        if (lane < 32 && cc < cn) cmax_s[sd][cc] = m;        // this (chunk, side)'s max|x|
+    }
+    const bool lo = lane >= 32;
+    h8_t b;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float v = xv[i] * xscale;                       // exact: a power of two
+        const _Float16 h = (_Float16)v;
+        b[i] = lo ? (_Float16)(v - (float)h) : h;
+    }
+    const f16x_t d = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, f16x_t{}, 0, 0, 0);
+    // D[k][n]: lane (n = lane & 31), register r: row 8*(r>>2) + 4*(lane>>5) + (r&3)
+    if (cc < cn) {
+        float* dst = T + (size_t)cc * TS + sd * K + kt * 32 + 4 * (lane >> 5);
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const int kk = kt * 32 + 8 * g + 4 * (lane >> 5);
+            const float4 v = make_float4(d[4 * g], d[4 * g + 1], d[4 * g + 2], d[4 * g + 3]);
+            if (KA || kk + 3 < K) *(float4*)(dst + 8 * g) = v;
+            else {
+                const float vv[4] = {v.x, v.y, v.z, v.w};
+                for (int u = 0; u < 4; u++)
+                    if (kk + u < K) dst[8 * g + u] = vv[u];
+            }
+        }
+    }
+}
+
+template <bool KA>   // K % 32 == 0: every table row of a tile is stored
+__global__ __launch_bounds__(kFThreads) void pq_fused(PqDev t, const float* __restrict__ x, float* __restrict__ out,
+                                                      int S) {
+    constexpr int CS = kFCS;
+    extern __shared__ __align__(16) float T[];            // [CS][TS]
+    __shared__ float red[kFThreads / 64], redc[kFThreads / 64];
+    __shared__ float cmax_s[2][CS];
+    __shared__ int8_t qq_s[1024];
+    __shared__ float meta_s;
+    __shared__ h8_t cbs[2 * 256];                          // both codebooks, fp16 rows padded to 8
+    __shared__ __align__(16) float xsl[CS * kXS];          // the slab's x: [chunk][side][8], zero padded
+    const int K = t.K, C = t.C, G = t.G, M = t.M, hf = G / 2;
+    const int TS = 2 * K + 4;                              // padded chunk stride (bank spread)
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // XCD-aware order: dispatch puts block b on XCD b % 8, so logical block
+    // (b % 8) * (nb / 8) + b / 8 keeps consecutive slabs of a tile on one XCD
+    const int nb = gridDim.x, bx = blockIdx.x;
+    const int lb = (nb & 7) ? bx : (bx & 7) * (nb >> 3) + (bx >> 3);
+    const int rt = lb / S, sl = lb - rt * S;
+    const int c0 = sl * CS, cn = min(CS, C - c0);
+    const int q = tid & 1;
+    const int r = rt * kFRows + (tid >> 1);
+    const int row = min(r, M - 1);
+
+    // 1. loads: the slab's x, the codebooks, x for the max|x| scan, the index
+    // bytes (in the order they are needed; loads complete in issue order)
+    const int ninner = C * G;
+    const bool x4ok = !t.inner && (ninner & 3) == 0 && ninner <= 16 * kFThreads;
+    const bool slab4 = x4ok && G == 16;                    // the slab's x as float4s (c0 * 16 floats)
+    float4 xsv = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (slab4) xsv = ((const float4*)x)[(size_t)c0 * 4 + min(tid, cn * 4 - 1)];
+    const bool cb16 = hf == 8;
+    uint4 cbv = make_uint4(0, 0, 0, 0);
+    if (cb16) {
+        const int ci = min(tid, 2 * K - 1);
+        cbv = *(const uint4*)((ci < K ? t.cb1l : t.cb1r) + (size_t)(ci < K ? ci : ci - K) * 8);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float4 xs4[4];
+    if (x4ok) {
+        const float4* x4 = (const float4*)x;
+        const int n4 = ninner >> 2;
+#pragma unroll
+        for (int u = 0; u < 4; u++) xs4[u] = x4[min(u * kFThreads + tid, n4 - 1)];
+    }
+    // the index bytes last, unconditionally (from a safe address when the
+    // slab is ragged; a load under a branch is waited for where it joins)
+    __builtin_amdgcn_sched_barrier(0);
+    const bool vec = cn == CS && (C & 15) == 0;
+    const size_t io = vec ? (size_t)row * C + c0 + 16 * q : 0;
+    const uint4 ivl = *(const uint4*)(t.i1l + io);
+    const uint4 ivr = *(const uint4*)(t.i1r + io);
+    PQ_TT(0);
+
+    // codebooks and the slab's x into LDS; the slab's max|x| and max|codeword|
+    float mc = 0.f, ms = 0.f;
+    if (tid < 2 * K) {
+        h8_t h;
+        if (cb16) h = __builtin_bit_cast(h8_t, cbv);
+        else {
+            const uint16_t* cr = (tid < K ? t.cb1l : t.cb1r) + (size_t)(tid < K ? tid : tid - K) * hf;
+#pragma unroll
+            for (int i = 0; i < 8; i++) h[i] = i < hf ? __builtin_bit_cast(_Float16, cr[min(i, hf - 1)]) : (_Float16)0.f;
+        }
+        cbs[tid] = h;
+#pragma unroll
+        for (int i = 0; i < 8; i++) mc = fmaxf(mc, fabsf((float)h[i]));
+    }
+    if (slab4) {
+        if (tid < cn * 4) {
+            ((float4*)(xsl + (tid >> 2) * kXS))[tid & 3] = xsv;
+            ms = fmaxf(fmaxf(fabsf(xsv.x), fabsf(xsv.y)), fmaxf(fabsf(xsv.z), fabsf(xsv.w)));
+        }
+    } else {
+        for (int i = tid; i < cn * 16; i += kFThreads) {
+            const int cc = i >> 4, sd = (i >> 3) & 1, e = i & 7;
+            const float v = e < hf ? x[inner_col(t, (c0 + cc) * G + sd * hf + e)] : 0.f;
+            xsl[cc * kXS + sd * 8 + e] = v;
+            ms = fmaxf(ms, fabsf(v));
+        }
+    }
+    ms = wave_max_dpp(ms);
+    mc = wave_max_dpp(mc);
+    if (lane == 0) {
+        red[wave] = ms;
+        redc[wave] = mc;
+    }
+    __syncthreads();
+    float smax = 0.f, cbmax = 0.f;
+#pragma unroll
+    for (int w = 0; w < kFThreads / 64; w++) {
+        smax = fmaxf(smax, red[w]);
+        cbmax = fmaxf(cbmax, redc[w]);
+    }
+    // the tables carry 2^-ex, ex the exponent of the slab's max|x|
+    int ex = 0;
+    if (smax > 0.f) frexpf(smax, &ex);                     // smax < 2^ex
+    const float xscale = ldexpf(1.0f, -ex);
+
+    // 2. tables: items (side, 32-code tile, 32-chunk tile), <= 32
+    const int KT = (K + 31) / 32, CT = (cn + 31) / 32, items = 2 * KT * CT;
+    for (int it = wave; it < items; it += kFThreads / 64)
+        table_tile<KA, CS>(t, cbs, xsl, it, KT, CT, cn, lane, TS, xscale, T, cmax_s);
+    PQ_TT(1);
+    // max|x| over the inner columns (the skipping rule's reference)
+    float mx = 0.f;
+    if (x4ok) {
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(xs4[u].x), fabsf(xs4[u].y)), fmaxf(fabsf(xs4[u].z), fabsf(xs4[u].w))));
+    } else {
+        for (int j0 = 0; j0 < ninner; j0 += 16 * kFThreads) {
+            float v[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) v[u] = x[inner_col(t, min(j0 + u * kFThreads + tid, ninner - 1))];
+#pragma unroll
+            for (int u = 0; u < 16; u++) mx = fmaxf(mx, fabsf(v[u]));
+        }
+    }
+    mx = wave_max_dpp(mx);
+    __syncthreads();                                       // tables done; red[] read above
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    float gmax = 0.f;
+#pragma unroll
+    for (int w = 0; w < kFThreads / 64; w++) gmax = fmaxf(gmax, red[w]);
+    // the slab's kept chunks as a mask, made by every wavefront (lane = chunk)
+    bool keep = false;
+    if (lane < cn) {
+        const float cm = fmaxf(cmax_s[0][lane], cmax_s[1][lane]);
+        keep = t.skip_mode == 1 ? (gmax > 0.f ? cm >= gmax * t.skip_val : true)
+             : t.skip_mode == 2 ? (t.skip_val > 0.f ? cm > t.skip_val : true) : true;
+    }
+    const unsigned long long keepm = __ballot(keep);
+    const unsigned long long full = cn == 64 ? ~0ull : ((1ull << cn) - 1);
+    PQ_TT(2);
+
+    // 4. gather: the thread's 16 chunks, L then R per chunk (entries carry 2^-ex)
+    float acc = 0.f;
+    if (vec) {
+        const uint32_t wl[4] = {ivl.x, ivl.y, ivl.z, ivl.w}, wr[4] = {ivr.x, ivr.y, ivr.z, ivr.w};
+        const float* Tq = T + (size_t)(16 * q) * TS;
+        if (keepm == full) {
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const int il = (wl[j >> 2] >> (8 * (j & 3))) & 0xff, ir = (wr[j >> 2] >> (8 * (j & 3))) & 0xff;
+                acc = acc + (Tq[j * TS + il] + Tq[j * TS + K + ir]);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const int c = 16 * q + j;
+                const int il = (wl[j >> 2] >> (8 * (j & 3))) & 0xff, ir = (wr[j >> 2] >> (8 * (j & 3))) & 0xff;
+                const float val = Tq[j * TS + il] + Tq[j * TS + K + ir];
+                acc = acc + (((keepm >> c) & 1) ? val : 0.f);
+            }
+        }
+    } else if (r < M) {
+        const uint8_t* pl = t.i1l + (size_t)r * C + c0;
+        const uint8_t* pr = t.i1r + (size_t)r * C + c0;
+        for (int c = 16 * q; c < min(16 * q + 16, cn); c++) {
+            const float* Tc = T + (size_t)c * TS;
+            const float val = Tc[pl[c]] + Tc[K + pr[c]];
+            acc = acc + (((keepm >> c) & 1) ? val : 0.f);
+        }
+    }
+    // the row's two partials, lanes 2i, 2i+1
+    acc += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, acc), 0xB1, 0xF, 0xF, false));
+    PQ_TT(3);
+
+    // 5. the rows' words
+    const bool own = q == 0 && r < M;
+    bool fin = own;
+    float sum = ldexpf(acc, ex);
+    const uint16_t rs_bits = t.row_scale[row];   // in flight with the atomic below
+    if (S > 1 && own) {
+        // 2^qe maps 2 * N_inner * max|cb| * max|x| (a bound on |row sum|) to <= 2^50
+        const float bound = 2.0f * (float)ninner * cbmax * gmax;
+        int eb = 0;
+        if (bound > 0.f) frexpf(bound, &eb);               // bound < 2^eb
+        const int qe = 50 - eb;
+        const long long v = llrint((double)acc * ldexp(1.0, qe + ex));
+        const unsigned long long add = (1ull << 58) + (unsigned long long)(v + (1ll << 50));
+        const unsigned long long old =
+            __hip_atomic_fetch_add(&pq_row_acc[r], add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned long long tot = old + add;
+        fin = (tot >> 58) == (unsigned long long)S;
+        if (fin) {
+            const long long val = (long long)(tot & ((1ull << 58) - 1)) - (long long)S * (1ll << 50);
+            sum = (float)((double)val * ldexp(1.0, -qe));
+            __hip_atomic_store(&pq_row_acc[r], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    PQ_TT(4);
+    // outliers (pq_decode.c:1233-1421): int8-quantised dot for >= 32
+    // outliers, fp32 otherwise
+    const int no = t.n_outlier;
+    const bool quant = no >= 32;
+    if (no > 0) {
+        if (__syncthreads_or(fin) == 0) return;
+        if (quant) {
+            if (tid == 0) {
+                float m = 0.f;
+                for (int j = 0; j < no; j++) {
+                    const float v = x[t.ocols[j]] * f16_to_f32(t.oscale[j]);
+                    const float av = v < 0 ? -v : v;
+                    if (av > m) m = av;
+                }
+                meta_s = m > 0.f ? m / 127.0f : 1.0f;
+            }
+            __syncthreads();
+            const float inv = 1.0f / meta_s;
+            for (int j = tid; j < no; j += kFThreads) {
+                const float sv = (x[t.ocols[j]] * f16_to_f32(t.oscale[j])) * inv;
+                const int v = (int)(sv >= 0 ? sv + 0.5f : sv - 0.5f);
+                qq_s[j] = (int8_t)(v > 127 ? 127 : (v < -128 ? -128 : v));
+            }
+            __syncthreads();
+        }
+    }
+    if (!fin) return;
+    float y = sum * f16_to_f32(rs_bits);
+    if (no > 0) {
+        const int8_t* sdc = t.oside + (size_t)r * no;
+        if (quant) {
+            int32_t isum = 0;
+            for (int j = 0; j < no; j++) isum += (int32_t)sdc[j] * (int32_t)qq_s[j];
+            y = fmaf((float)isum, meta_s, y);
+        } else {
+            for (int j = 0; j < no; j++) y = fmaf((float)sdc[j] * f16_to_f32(t.oscale[j]), x[t.ocols[j]], y);
+        }
+    }
+    out[r] = y;
+    PQ_TT(5);
+}
+
 // ── top-K LM head (ib_pq_lm_head_topk, pq_decode.c:2259-2346) ─────────────
 // Order key of a float, descending: smaller key = larger value.
 __device__ __forceinline__ uint32_t desc_key(float v) {
@@ -739,6 +1073,22 @@ extern "C" int ibh_pq_matmul_policy(const ibh_pq_tensor_abi* t, const float* x, 
     return pq_run(t, x, out, ws, ws_bytes, stream, md, "ibh_pq_matmul_policy");
 }
 
+static int g_pq_fused = 1;
+
+// Development switch (no counterpart in the reference): 0 sends every PQ
+// matvec through the three-kernel path, 1 (default) lets eligible tensors
+// run in one launch.
+#ifdef IBH_PQ_TRACE
+extern "C" int ibh_pq_trace_read(void* out) {
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(ibh_pq_tt), sizeof(ibh_pq_tt)) == hipSuccess ? 0 : -1;
+}
+#endif
+
+extern "C" int ibh_pq_set_fused(int on) {
+    g_pq_fused = on != 0;
+    return IBH_OK;
+}
+
 static int pq_run(const ibh_pq_tensor_abi* t, const float* x, float* out, void* ws, size_t ws_bytes, void* stream,
                   const PqMode& md, const char* who) {
     if (!t || !x || !out || t->M <= 0 || t->C <= 0 || t->G <= 0 || t->G % 2 || t->G > 64 || t->K <= 0 || t->K > 65536 ||
@@ -792,6 +1142,18 @@ static int pq_run(const ibh_pq_tensor_abi* t, const float* x, float* out, void* 
     float* c2max = (float*)(base + w.c2max);
     d.cnorm = cnorm;
     d.c2max = c2max;
+    // one launch for level-1 work with half-chunks of <= 8 columns and <= 256
+    // codes (the scope of pq_fused); other tensors and policies take the
+    // three-kernel path below
+    const int tiles = (t->M + kFRows - 1) / kFRows;
+    const int S = (t->C + kFCS - 1) / kFCS;
+    if (!two && !md.q8 && !md.tq8 && t->G <= 16 && t->K <= 256 && S <= kFMaxS && t->M <= kFMaxRows && g_pq_fused) {
+        const size_t flds = (size_t)kFCS * (2 * t->K + 4) * sizeof(float);
+        if (t->K % 32 == 0) pq_fused<true><<<tiles * S, kFThreads, flds, st>>>(d, x, out, S);
+        else pq_fused<false><<<tiles * S, kFThreads, flds, st>>>(d, x, out, S);
+        IBH_CHECK_LAUNCH("ibh_pq_matmul (one launch)");
+        return IBH_OK;
+    }
     if (d.l2skip) {
         const int n_outer = d.pyramid ? t->K : 1;
         const int k_inner = d.pyramid ? d.K2 / t->K : d.K2;

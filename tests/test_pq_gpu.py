@@ -223,3 +223,30 @@ def test_pq_lm_head_topk_two_pass(ops, oracle_lib, k):
     # GPU row order; compare as sets per equal value and the values exactly
     assert sorted(got.tolist()) == sorted(want_ids2.tolist())
     assert float(np.abs(lg2.cpu().numpy().astype(np.float64) - want_lg2).max() / np.abs(want_lg2).max()) <= 1e-4
+
+
+@pytest.mark.parametrize("shape", [(4096, 896, 16, 256, 0), (300, 130, 16, 256, 0), (1000, 64, 8, 128, 40),
+                                   (257, 200, 4, 64, 8), (513, 97, 16, 256, 33)])
+def test_pq_one_launch_matches_three_kernels(ops, oracle_lib, shape):
+    """The one-launch kernel (tables on the matrix cores, per-tile arrival
+    counters) against the three-kernel path and the oracle, on ragged row
+    tiles and slabs, with and without outliers; each call twice, so the
+    counters' reset between calls is exercised."""
+    from gen_golden import make_pq
+    M, C, G, K, no = shape
+    print(f"case pq one-launch {shape}", flush=True)
+    rng = np.random.default_rng(M + C)
+    t = make_pq(rng, M, C, G, K, 1, 0, no)
+    x = rng.standard_normal(t["N"]).astype(np.float32)
+    ref = oracle_lib.pq_matmul(t, x)
+    lib = ops.lib()
+    try:
+        lib.ibh_pq_set_fused(0)
+        three = run(ops, t, x)
+    finally:
+        lib.ibh_pq_set_fused(1)
+    one = run(ops, t, x)
+    again = run(ops, t, x)
+    np.testing.assert_array_equal(one, again)
+    assert relerr(one, ref) <= 1e-4
+    assert relerr(one, three) <= 1e-5
