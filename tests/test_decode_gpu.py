@@ -241,3 +241,82 @@ def test_benchmark_config_tokens_match_reference(L, name):
     got = m.generate(np.asarray(g["prompt"], np.int32), g["n_out"])
     m.close()
     assert got.tolist() == g["tokens"]
+
+
+def _fast_vs_exact(name, n_steps=None):
+    """Fast-mode decode of a benchmark config, teacher-forced along the
+    reference's token stream next to the exact-mode model (whose logits are
+    bit-identical to the CPU's): per step the fast argmax, the exact top-2
+    gap and max|logit_fast - logit_exact|."""
+    import sys
+    sys.path.insert(0, GOLDEN)
+    import gen_decode_golden as G
+    from libinferbit_amd.model import Model
+    g = _golden_case(name)
+    os.makedirs(MODEL_DIR, exist_ok=True)
+    path = G.ensure_model(name, MODEL_DIR)
+    assert _sha256(path) == g["model_sha256"], "synthetic model bytes differ from the fixture's"
+    case = G.CASES[name]
+    me, mf = Model(path), Model(path)
+    mf.set_exact(False)
+    if case["kv_pos"]:
+        k, v = G.kv_of(case)
+        me.kv_prefill(k, v)
+        mf.kv_prefill(k, v)
+        del k, v
+    ref = g["tokens"][:n_steps] if n_steps else g["tokens"]
+    feed = list(g["prompt"])
+    rows = []
+    for i in range(len(ref)):
+        le, lf = me.forward(feed), mf.forward(feed)
+        top = np.argsort(-le.astype(np.float64), kind="stable")[:2]
+        rows.append(dict(step=i, exact=int(np.argmax(le)), fast=int(np.argmax(lf)), ref=ref[i],
+                         gap=float(le[top[0]] - le[top[1]]), err=float(np.abs(lf - le).max()),
+                         scale=float(np.abs(le).max())))
+        feed = [int(np.argmax(le))]
+    me.close()
+    mf.close()
+    return rows
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("name", ["tinyllama", "mistral"])
+def test_benchmark_config_fast_mode_tokens(L, name):
+    """Fast mode (fp32-tolerance kernels) on configs 3 and 4, teacher-forced
+    along the reference's recorded stream.  Reported: every step where the
+    fast argmax leaves the stream, with the CPU's (= exact mode's) top-2
+    logit gap there.  With INT4 layers in W4A8 form (the reference's default,
+    forward.c:14-21) the activations of o/gate/up/down are re-quantized to
+    int8 per 128-group with round-to-nearest: an fp32-rounding difference
+    upstream can move a value across a rounding boundary, which changes one
+    code by 1/127 of its group's max -- a step, not a drift, so fast and
+    exact logits differ by far more than 1e-4 (measured up to ~7 %) and the
+    streams part at near-ties.  Asserted: the exact model follows the
+    reference stream, and every fast departure sits where the CPU's top-2
+    gap is within twice the fast path's logit error at that step."""
+    print(f"case decode fast {name}", flush=True)
+    rows = _fast_vs_exact(name)
+    assert all(r["exact"] == r["ref"] for r in rows), "exact mode left the reference stream"
+    flips = [r for r in rows if r["fast"] != r["ref"]]
+    worst = max(r["err"] / r["scale"] for r in rows)
+    print(f"fast {name}: {len(rows)} steps, {len(flips)} argmax departures, max rel logit err {worst:.3g}",
+          flush=True)
+    for r in flips:
+        print(f"  step {r['step']}: fast {r['fast']} ref {r['ref']} top-2 gap {r['gap']:.6g} "
+              f"fast err {r['err']:.3g}", flush=True)
+    assert all(r["gap"] <= 2 * r["err"] for r in flips)
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("name", ["tinyllama", "mistral"])
+def test_benchmark_config_fast_mode_without_w4a8(L, name, monkeypatch):
+    """The same configs with IB_W4A8=0 (INT4 layers on fp32 activations, no
+    re-quantization step): fast logits within 1e-4 of the exact model's at
+    every step and the same greedy stream (32 steps)."""
+    print(f"case decode fast {name} IB_W4A8=0", flush=True)
+    monkeypatch.setenv("IB_W4A8", "0")
+    rows = _fast_vs_exact(name, 32)
+    worst = max(r["err"] / r["scale"] for r in rows)
+    print(f"fast {name} IB_W4A8=0: max rel logit err {worst:.3g}", flush=True)
+    assert worst <= 1e-4
+    assert all(r["fast"] == r["exact"] for r in rows)
