@@ -160,6 +160,13 @@ size_t ibh_attn_workspace_bytes(int n_heads, int head_dim, int n_pos);
 int ibh_attn_decode(float* out, const float* q, const void* kdata, const void* vdata,
                     const float* kscales, const float* vscales, int pos, int n_heads, int n_kv,
                     int head_dim, int kv_bits, void* ws, size_t ws_bytes, void* stream);
+/* head_dim 64 or 128, fp32 / int8 / int4 caches and <= 64 KV heads run in
+ * one launch whose chunk blocks meet through per-KV-head arrival counters in
+ * device memory (back to zero after every call): attention calls that
+ * overlap on one GPU (different streams) race, as calls sharing a workspace
+ * already do.  Development switch (no counterpart in the reference): 0 sends
+ * them through the chunk + merge kernels, 1 (default) the one launch. */
+int ibh_attn_set_split(int on);
 
 /* ── product-quantised LUT matvec, device pointers ─────────── */
 

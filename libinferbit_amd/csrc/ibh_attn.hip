@@ -533,6 +533,263 @@ int ibh_launch_kv_write(void* kdata, void* vdata, float* kscales, float* vscales
     return IBH_OK;
 }
 
+namespace {
+
+// ── split attention (fast path) ──────────────────────────────────────────────
+// Block = (kv head, chunk of CT positions), 1024 threads, every thread one
+// 16-dimension piece of one position's K and V row (PIECES = HD/16 threads
+// per position, CT = 1024 / PIECES positions: 256 at head_dim 64, 128 at
+// 128), so a chunk's K and V rows are in flight from every thread at once.
+//  scores  each thread dots its 8 dims with the GRP query heads (q in LDS),
+//          the PIECES partials of a position are summed across lanes;
+//  softmax wavefront g does head g over the chunk (max, exp, sum);
+//  P.V     V bytes in LDS, thread (t-range, head, 4 dims) accumulates, the
+//          t-ranges are summed through LDS;
+//  partial the chunk's (m, l, o) per head; a second kernel (one 1024-thread
+//          block per head, every load in flight at once) merges them.
+// (A merge by the last-arriving chunk block, through write-through stores
+// and an arrival counter, measured 4.5 us slower: three dependent round
+// trips to memory after the chunk's own work.)
+constexpr int kSplitThreads = 1024;
+constexpr int kSplitMaxChunks = 256;
+constexpr int kSplitMaxKv = 64;
+
+template <int BITS>
+struct SplitGeo {
+    static constexpr int PB = BITS == 32 ? 64 : (BITS == 8 ? 16 : 8);   // bytes of a 16-dim piece
+};
+
+// 16 dequantised values of a piece (without the row scale)
+template <int BITS>
+__device__ __forceinline__ void piece_vals(const uint4* r, float* v) {
+    if constexpr (BITS == 32) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            v[4 * j] = __uint_as_float(r[j].x); v[4 * j + 1] = __uint_as_float(r[j].y);
+            v[4 * j + 2] = __uint_as_float(r[j].z); v[4 * j + 3] = __uint_as_float(r[j].w);
+        }
+    } else if constexpr (BITS == 8) {
+        const uint32_t u[4] = {r[0].x, r[0].y, r[0].z, r[0].w};
+#pragma unroll
+        for (int i = 0; i < 16; i++) v[i] = (float)(int8_t)(u[i >> 2] >> (8 * (i & 3)));
+    } else {
+        const uint32_t u[2] = {r[0].x, r[0].y};
+#pragma unroll
+        for (int i = 0; i < 16; i++) v[i] = (float)((int)((u[i >> 3] >> (4 * (i & 7))) & 0xf) - 8);
+    }
+}
+
+template <int BITS>
+__device__ __forceinline__ void piece_load(const uint8_t* p, uint4* r) {
+    if constexpr (BITS == 32) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) r[j] = ((const uint4*)p)[j];
+    } else if constexpr (BITS == 8) {
+        r[0] = *(const uint4*)p;
+    } else {
+        const uint2 u = *(const uint2*)p;
+        r[0] = make_uint4(u.x, u.y, 0u, 0u);
+    }
+}
+
+template <int BITS, int GRP, int HD>
+__global__ __launch_bounds__(kSplitThreads) void attn_split(float* __restrict__ out, float* __restrict__ part,
+                                                           const float* __restrict__ q,
+                                                           const uint8_t* __restrict__ kd,
+                                                           const uint8_t* __restrict__ vd,
+                                                           const float* __restrict__ ks,
+                                                           const float* __restrict__ vs, int T,
+                                                           const int* __restrict__ dpos, int n_kv, float scale,
+                                                           int nstride) {
+    constexpr int PB = SplitGeo<BITS>::PB;
+    constexpr int NR = BITS == 32 ? 4 : 1;                // uint4 per piece register set
+    constexpr int PIECES = HD / 16;
+    constexpr int CT = kSplitThreads / PIECES;
+    constexpr int RB = HD * PB / 16;                      // bytes of one head's row
+    constexpr int NDQ = HD / 4;                           // 4-dim groups in P.V
+    constexpr int TR = kSplitThreads / (GRP * NDQ);       // t-ranges in P.V
+    constexpr int MB = 64;                                // chunks one merge pass loads per thread
+    static_assert(TR >= 1 && CT % TR == 0, "P.V split");
+    if (dpos) T = *dpos + 1;
+    const int kh = blockIdx.x, c = blockIdx.y, t0 = c * CT;
+    if (t0 >= T) return;
+    const int tn = min(CT, T - t0);
+    const int nch = (T + CT - 1) / CT;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const size_t row_bytes = (size_t)n_kv * RB;
+    __shared__ __align__(16) float qs[GRP][HD];
+    __shared__ float sc[GRP][CT];
+    __shared__ __align__(16) uint8_t vsh[CT][RB];
+    __shared__ float vsc[CT];
+    __shared__ float mlr[GRP][2];
+    __shared__ __align__(16) float ob[TR][GRP][HD];
+
+    // 1. this thread's K and V piece (position clamped to the last valid one)
+    const int t = tid / PIECES, pc = tid % PIECES;
+    const int pos = t0 + min(t, tn - 1);
+    uint4 kr[NR], vr[NR];
+    piece_load<BITS>(kd + (size_t)pos * row_bytes + (size_t)kh * RB + pc * PB, kr);
+    piece_load<BITS>(vd + (size_t)pos * row_bytes + (size_t)kh * RB + pc * PB, vr);
+    const float ksc = BITS == 32 ? 1.f : ks[(size_t)pos * n_kv + kh];
+    const float vsv = BITS == 32 ? 1.f : vs[(size_t)pos * n_kv + kh];
+    for (int i = tid; i < GRP * HD / 4; i += kSplitThreads)
+        ((float4*)&qs[0][0])[i] = ((const float4*)(q + (size_t)kh * GRP * HD))[i];
+    __syncthreads();
+
+    // 2. scores: the piece's dot with each head, summed over the position's lanes
+    float kv[16];
+    piece_vals<BITS>(kr, kv);
+    float s[GRP];
+#pragma unroll
+    for (int g = 0; g < GRP; g++) {
+        float a = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float4 qq = *(const float4*)&qs[g][pc * 16 + 4 * j];
+            a += qq.x * kv[4 * j] + qq.y * kv[4 * j + 1] + qq.z * kv[4 * j + 2] + qq.w * kv[4 * j + 3];
+        }
+        s[g] = a;
+    }
+#pragma unroll
+    for (int o = 1; o < PIECES; o <<= 1)
+#pragma unroll
+        for (int g = 0; g < GRP; g++) s[g] += __shfl_xor(s[g], o);
+    if (pc == 0) {
+#pragma unroll
+        for (int g = 0; g < GRP; g++) sc[g][t] = t < tn ? s[g] * ksc * scale : -INFINITY;
+    }
+    // V piece into LDS
+#pragma unroll
+    for (int j = 0; j < NR; j++) {
+        if constexpr (BITS == 4) *(uint2*)&vsh[t][pc * PB] = make_uint2(vr[0].x, vr[0].y);
+        else ((uint4*)&vsh[t][pc * PB])[j] = vr[j];
+    }
+    if (pc == 0) vsc[t] = vsv;
+    __syncthreads();
+
+    // 3. chunk softmax, wavefront g for head g
+    if (wave < GRP) {
+        const int g = wave;
+        float m = -INFINITY;
+        for (int i = lane; i < CT; i += 64) m = fmaxf(m, sc[g][i]);
+        m = wave_max(m);
+        float l = 0.f;
+        for (int i = lane; i < CT; i += 64) {
+            const float e = i < tn ? expf(sc[g][i] - m) : 0.f;
+            sc[g][i] = e;
+            l += e;
+        }
+        l = wave_sum(l);
+        if (lane == 0) { mlr[g][0] = m; mlr[g][1] = l; }
+    }
+    __syncthreads();
+
+    // 4. P.V: thread (t-range tr, head g, dims 4 dq .. 4 dq + 3)
+    {
+        const int dq = tid % NDQ, g = (tid / NDQ) % GRP, tr = tid / (NDQ * GRP);
+        float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+        for (int tt = tr; tt < tn; tt += TR) {
+            const float pw = sc[g][tt] * vsc[tt];
+            float v[4];
+            if constexpr (BITS == 32) {
+                const float4 f = *(const float4*)&vsh[tt][dq * 16];
+                v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+            } else if constexpr (BITS == 8) {
+                const uint32_t u = *(const uint32_t*)&vsh[tt][dq * 4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) v[i] = (float)(int8_t)(u >> (8 * i));
+            } else {
+                const uint16_t u = *(const uint16_t*)&vsh[tt][dq * 2];
+#pragma unroll
+                for (int i = 0; i < 4; i++) v[i] = (float)((int)((u >> (4 * i)) & 0xf) - 8);
+            }
+            a0 = fmaf(pw, v[0], a0);
+            a1 = fmaf(pw, v[1], a1);
+            a2 = fmaf(pw, v[2], a2);
+            a3 = fmaf(pw, v[3], a3);
+        }
+        *(float4*)&ob[tr][g][dq * 4] = make_float4(a0, a1, a2, a3);
+    }
+    __syncthreads();
+
+    // 5. the chunk's partial (m, l, o[HD]) per head
+    if (tid < GRP * HD) {
+        const int g = tid / HD, d = tid % HD;
+        float o = 0.f;
+#pragma unroll
+        for (int r = 0; r < TR; r++) o += ob[r][g][d];
+        float* pp = part + ((size_t)(kh * GRP + g) * nstride + c) * (HD + 2);
+        pp[2 + d] = o;
+        if (d < 2) pp[d] = mlr[g][d];
+    }
+}
+
+// Merge of one head's chunks: out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c.
+// 1024 threads: thread (chunk class cq, dim d) holds chunks c = cq (mod
+// 1024/HD), every load of the block issued at once.
+template <int HD>
+__global__ __launch_bounds__(1024) void attn_merge_wide(float* __restrict__ out, const float* __restrict__ part,
+                                                        int T, const int* __restrict__ dpos, int ct, int nstride) {
+    constexpr int NCQ = 1024 / HD;                        // chunk classes
+    constexpr int PER = kSplitMaxChunks / NCQ;            // chunks per thread at most
+    __shared__ float wm[kSplitMaxChunks], wl[kSplitMaxChunks];
+    __shared__ float osum[NCQ][HD];
+    __shared__ float tot;
+    if (dpos) T = *dpos + 1;
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nch = (T + ct - 1) / ct;
+    const float* ph = part + (size_t)h * nstride * (HD + 2);
+    const int cq = tid / HD, d = tid % HD;
+    const int per = (nch + NCQ - 1) / NCQ;
+    float v[PER];
+#pragma unroll
+    for (int u = 0; u < PER; u++)
+        if (u < per) v[u] = ph[(size_t)min(cq + NCQ * u, nch - 1) * (HD + 2) + 2 + d];
+    if (tid < nch) {
+        wm[tid] = ph[(size_t)tid * (HD + 2)];
+        wl[tid] = ph[(size_t)tid * (HD + 2) + 1];
+    }
+    __syncthreads();
+    if (wave == 0) {
+        float M = -INFINITY;
+        for (int cc = lane; cc < nch; cc += 64) M = fmaxf(M, wm[cc]);
+        M = wave_max(M);
+        float L = 0.f;
+        for (int cc = lane; cc < nch; cc += 64) {
+            const float e = expf(wm[cc] - M);
+            wm[cc] = e;
+            L = fmaf(e, wl[cc], L);
+        }
+        L = wave_sum(L);
+        if (lane == 0) tot = L;
+    }
+    __syncthreads();
+    float o = 0.f;
+#pragma unroll
+    for (int u = 0; u < PER; u++)
+        if (u < per && cq + NCQ * u < nch) o = fmaf(wm[cq + NCQ * u], v[u], o);
+    osum[cq][d] = o;
+    __syncthreads();
+    if (tid < HD) {
+        float r = 0.f;
+#pragma unroll
+        for (int k = 0; k < NCQ; k++) r += osum[k][tid];
+        out[(size_t)h * HD + tid] = r / tot;
+    }
+}
+
+}  // namespace
+
+static int g_attn_split = 1;
+
+// Development switch (no counterpart in the reference): 0 sends decode
+// attention through the chunk + merge kernels, 1 (default) lets eligible
+// shapes run in one launch.
+extern "C" int ibh_attn_set_split(int on) {
+    g_attn_split = on != 0;
+    return IBH_OK;
+}
+
 extern "C" size_t ibh_attn_workspace_bytes(int n_heads, int head_dim, int n_pos) {
     const int nchunks = (n_pos + kChunk - 1) / kChunk;
     return (size_t)n_heads * nchunks * (head_dim + 2) * sizeof(float);
@@ -567,6 +824,31 @@ int ibh_launch_attn(float* out, const float* q, const void* kdata, const void* v
     const float scale = 1.0f / sqrtf((float)head_dim);
     float* part = (float*)ws;
     const int grp = n_heads / n_kv;
+    if (g_attn_split && (kv_bits == 32 || kv_bits == 8 || kv_bits == 4) && (head_dim == 64 || head_dim == 128) &&
+        (grp == 1 || grp == 2 || grp == 4 || grp == 8) && n_kv <= kSplitMaxKv) {
+        const int ct = kSplitThreads / (head_dim / 16);
+        const int nstride = (max_pos + 1 + ct - 1) / ct;
+        if (nstride <= kSplitMaxChunks) {
+            const uint8_t* K = (const uint8_t*)kdata;
+            const uint8_t* V = (const uint8_t*)vdata;
+#define IBH_AS(B_, G_, H_) do { \
+                attn_split<B_, G_, H_><<<dim3(n_kv, nstride), kSplitThreads, 0, st>>>( \
+                    out, part, q, K, V, kscales, vscales, T, dpos, n_kv, scale, nstride); \
+                IBH_CHECK_LAUNCH("ibh_attn_decode (split)"); \
+                attn_merge_wide<H_><<<n_heads, 1024, 0, st>>>(out, part, T, dpos, ct, nstride); } while (0)
+#define IBH_ASG(B_, H_) do { if (grp == 1) IBH_AS(B_, 1, H_); else if (grp == 2) IBH_AS(B_, 2, H_); \
+                             else if (grp == 4) IBH_AS(B_, 4, H_); else IBH_AS(B_, 8, H_); } while (0)
+#define IBH_ASH(B_) do { if (head_dim == 64) IBH_ASG(B_, 64); else IBH_ASG(B_, 128); } while (0)
+            if (kv_bits == 32) IBH_ASH(32);
+            else if (kv_bits == 8) IBH_ASH(8);
+            else IBH_ASH(4);
+#undef IBH_AS
+#undef IBH_ASG
+#undef IBH_ASH
+            IBH_CHECK_LAUNCH("ibh_attn_decode (split)");
+            return IBH_OK;
+        }
+    }
     if (head_dim == 64 || head_dim == 128 || head_dim == 256) {
         const uint8_t* K = (const uint8_t*)kdata;
         const uint8_t* V = (const uint8_t*)vdata;

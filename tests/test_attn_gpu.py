@@ -97,3 +97,37 @@ def test_attention_bad_arguments(ops):
         ops.attn_decode(t, t, t, t, t, t, 0, 6, 4, 16, 8)       # heads not a multiple of kv heads
     with pytest.raises(L.IbhError):
         ops.attn_decode(t, t, t, t, None, None, 0, 4, 4, 16, 8)  # int8 cache needs scales
+
+
+@pytest.mark.parametrize("bits,n_heads,n_kv,hd,T", [(8, 32, 8, 128, 4096), (4, 32, 8, 128, 4000),
+                                                  (32, 32, 4, 64, 2048), (8, 32, 4, 64, 131), (32, 8, 8, 128, 65)])
+def test_attention_one_launch_matches_chunk_merge(ops, oracle_lib, bits, n_heads, n_kv, hd, T):
+    """The one-launch split kernel (per-KV-head arrival counters, merge by
+    the last chunk) against the chunk + merge kernels and the oracle; each
+    configuration twice in a row, bit-identical (the counters reset)."""
+    import libinferbit_amd as L
+    print(f"case attn-split bits={bits} heads={n_heads}/{n_kv} hd={hd} T={T}", flush=True)
+    rng = np.random.default_rng(T + hd + bits)
+    K = rng.standard_normal((T, n_kv * hd)).astype(np.float32)
+    V = rng.standard_normal((T, n_kv * hd)).astype(np.float32)
+    cache = oracle_lib.kv_alloc(bits, T, n_kv, hd)
+    for t in range(T):
+        oracle_lib.kv_write(cache, t, K[t], V[t], n_kv, hd, bits)
+    g = [torch.from_numpy(a).cuda() for a in cache]
+    q = torch.from_numpy(rng.standard_normal(n_heads * hd).astype(np.float32) * 2).cuda()
+
+    def run():
+        out = torch.empty(n_heads * hd, device="cuda")
+        ops.attn_decode(out, q, g[0], g[1], g[2], g[3], T - 1, n_heads, n_kv, hd, bits)
+        torch.cuda.synchronize()
+        return out.cpu().numpy()
+    a, b = run(), run()
+    try:
+        L.lib().ibh_attn_set_split(0)
+        c = run()
+    finally:
+        L.lib().ibh_attn_set_split(1)
+    np.testing.assert_array_equal(a, b)
+    ref = oracle_lib.attn_decode(q.cpu().numpy(), cache, T - 1, n_heads, n_kv, hd, bits)
+    assert np.abs(a - ref).max() / np.abs(ref).max() <= 1e-4
+    assert np.abs(a - c).max() / np.abs(c).max() <= 1e-5
