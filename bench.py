@@ -450,6 +450,11 @@ def cpu_decode(path, case, n_tok, threads_list):
 
 V5_TINYLLAMA = dict(num_layers=22, hidden_size=2048, num_heads=32, num_kv_heads=4, head_dim=64,
                     intermediate_size=5632, vocab_size=32000, rope_theta=10000.0)
+# head_dim 128 with four query heads per kv head
+V5_MISTRAL = dict(num_layers=32, hidden_size=4096, num_heads=32, num_kv_heads=8, head_dim=128,
+                  intermediate_size=14336, vocab_size=32000, rope_theta=1000000.0)
+V5_CASES = {"tinyllama": (V5_TINYLLAMA, "TinyLlama-1.1B shape", 8),
+            "mistral": (V5_MISTRAL, "Mistral-7B shape (head_dim 128)", 4)}
 
 
 def v5_bytes_per_token(cfg, n_pos, G=128, pq_G=16, pq_K=256):
@@ -469,22 +474,24 @@ def v5_bytes_per_token(cfg, n_pos, G=128, pq_G=16, pq_K=256):
     return L * per_layer + head + 2 * H
 
 
-def v5_decode_case(steps, cpu):
-    """IBF v5 session greedy decode (ib_pq_generate_greedy) on a TinyLlama-
-    1.1B-shaped synthetic v5 model: INT4 group-128 projections with AWQ
-    scales, PQ LM head (G 16, K 256), fp16 embedding.  tok/s = steps / (time
+def v5_decode_case(steps, cpu, shape="tinyllama"):
+    """IBF v5 session greedy decode (ib_pq_generate_greedy) on a synthetic v5
+    model of the named shape (TinyLlama-1.1B, or Mistral-7B for head_dim
+    128): INT4 group-128 projections with AWQ scales, PQ LM head (G 16,
+    K 256), fp16 embedding.  tok/s = steps / (time
     of prompt + steps - time of the prompt alone), each a full
     generate call (device-resident loop of captured steps)."""
     from libinferbit_amd import ibf5
     from libinferbit_amd.session import PqSession
     workdir = os.environ.get("IBH_MODEL_DIR", "/tmp/ibh_models")
     os.makedirs(workdir, exist_ok=True)
-    path = os.path.join(workdir, "v5_tinyllama_int4g_awq.ibf")
+    cfg, label, n_cpu = V5_CASES[shape]
+    path = os.path.join(workdir, f"v5_{shape}_int4g_awq.ibf")
     t = time.time()
     if not os.path.exists(path):
-        ibf5.write_synthetic_v5(path + ".tmp", V5_TINYLLAMA, seed=7, awq=True)
+        ibf5.write_synthetic_v5(path + ".tmp", cfg, seed=7, awq=True)
         os.replace(path + ".tmp", path)
-    out = {"config": "TinyLlama-1.1B shape, IBF v5 INT4 g128 + AWQ, PQ head", "model_write_s": round(time.time() - t, 1)}
+    out = {"config": f"{label}, IBF v5 INT4 g128 + AWQ, PQ head", "model_write_s": round(time.time() - t, 1)}
     S = PqSession(path)
     kv = S.kv_cache(1024)
     prompt = list(range(1, 9))
@@ -499,7 +506,7 @@ def v5_decode_case(steps, cpu):
     t_all = time.perf_counter() - t0
     dt = t_all - t_pre
     tok_s = steps / dt
-    nbytes = v5_bytes_per_token(V5_TINYLLAMA, len(prompt) + steps // 2)
+    nbytes = v5_bytes_per_token(cfg, len(prompt) + steps // 2)
     out["gpu"] = {"tok_s": round(tok_s, 2), "ms_per_token": round(dt / steps * 1e3, 4), "steps": steps,
                   "prefill_ms": round(t_pre * 1e3, 3), "bytes_per_token": nbytes,
                   "GBps": round(nbytes * tok_s / 1e9, 1), "frac_hbm": round(nbytes * tok_s / 1e9 / HBM_PEAK_GBS, 4)}
@@ -511,7 +518,6 @@ def v5_decode_case(steps, cpu):
             cores = host_cpu()[0]
             pp = path + ".prompt.i32"
             np.asarray(prompt, np.int32).tofile(pp)
-            n_cpu = 8
             r = subprocess.run([exe, path, "64", str(n_cpu), pp, "greedy"], capture_output=True, text=True,
                                timeout=900, env=dict(os.environ, IB_PQ_THREADS=str(cores)))
             if r.returncode == 0:
@@ -578,7 +584,7 @@ def main():
         elif a.only == "pqpol":
             r = pq_policy_cases(torch, L, max(200, a.steps // 4), 20)
         elif a.only == "v5":
-            r = v5_decode_case(256, cpu=not a.no_cpu)
+            r = {k: v5_decode_case(256, cpu=not a.no_cpu, shape=k) for k in V5_CASES}
         elif a.only == "verify":
             r = verify_case(10)
         elif a.only == "int4g":
@@ -624,6 +630,8 @@ def main():
         decode["tinyllama_forward_positions"] = verify_case(10)
         print("bench: v5 session decode", file=sys.stderr, flush=True)
         decode["v5_tinyllama_int4g"] = v5_decode_case(256, cpu=not a.no_cpu)
+        print("bench: v5 session decode, head_dim 128", file=sys.stderr, flush=True)
+        decode["v5_mistral_int4g"] = v5_decode_case(256, cpu=not a.no_cpu, shape="mistral")
     cpu = None if a.no_cpu else cpu_baseline()
     out = {
         "metric": "quantized GEMV HBM GB/s (% of peak) + decode tok/s, Mistral-7B-shape INT4, 1 GPU",

@@ -90,6 +90,33 @@ __device__ __forceinline__ int wave_isum_dpp(int v) {
            (__builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48));
 }
 
+// One 128-column group of the W4A8 activation quantizer (threading.c:401-432,
+// bit-identical): the wavefront holds the group as v0 = column j0 = base +
+// lane, v1 = column j1 = base + 64 + lane; scale = max|v| / 127 (1e-10 with
+// zero codes below 1e-10), codes = round-half-away(v * (1 / scale)) clamped
+// to [-127, 127].
+__device__ __forceinline__ void quant_group128(float v0, float v1, int j0, int j1, int end, int g,
+                                               int8_t* __restrict__ q, float* __restrict__ s) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const float mx = wave_max(fmaxf(v0 < 0 ? -v0 : v0, v1 < 0 ? -v1 : v1));
+    if (mx < 1e-10f) {
+        if (j0 < end) q[j0] = 0;
+        if (j1 < end) q[j1] = 0;
+        if (lane == 0) s[g] = 1e-10f;
+        return;
+    }
+    const float scale = mx / 127.0f;
+    const float inv = 1.0f / scale;
+    auto qz = [&](float v) {
+        const float t = v * inv;
+        int r = (int)(t + (v >= 0 ? 0.5f : -0.5f));
+        return (int8_t)(r < -127 ? -127 : (r > 127 ? 127 : r));
+    };
+    if (j0 < end) q[j0] = qz(v0);
+    if (j1 < end) q[j1] = qz(v1);
+    if (lane == 0) s[g] = scale;
+}
+
 // 16-byte streaming load (weights are read exactly once per call).
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 ld_stream16(const void* p) {

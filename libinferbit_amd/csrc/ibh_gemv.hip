@@ -274,24 +274,7 @@ __global__ __launch_bounds__(kBlock) void w4a8_generic(float* __restrict__ y,
 // Quantization of one 128-group held two elements per lane (threading.c:401-432).
 __device__ __forceinline__ void quant_group(float v0, float v1, int j0, int j1, int end, int g, int8_t* __restrict__ q,
                                             float* __restrict__ s) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const float mx = wave_max(fmaxf(v0 < 0 ? -v0 : v0, v1 < 0 ? -v1 : v1));
-    if (mx < 1e-10f) {
-        if (j0 < end) q[j0] = 0;
-        if (j1 < end) q[j1] = 0;
-        if (lane == 0) s[g] = 1e-10f;
-        return;
-    }
-    const float scale = mx / 127.0f;
-    const float inv = 1.0f / scale;
-    auto qz = [&](float v) {
-        const float t = v * inv;
-        int r = (int)(t + (v >= 0 ? 0.5f : -0.5f));
-        return (int8_t)(r < -127 ? -127 : (r > 127 ? 127 : r));
-    };
-    if (j0 < end) q[j0] = qz(v0);
-    if (j1 < end) q[j1] = qz(v1);
-    if (lane == 0) s[g] = scale;
+    quant_group128(v0, v1, j0, j1, end, g, q, s);
 }
 
 __global__ __launch_bounds__(kBlock) void quant_act_g128(const float* __restrict__ x,

@@ -178,6 +178,13 @@ __global__ __launch_bounds__(kNormThreads) void v5_rmsnorm_kernel(float* __restr
     if (bump && threadIdx.x == 0) *bump += 1;   // end of a step: position + 1
 }
 
+// ib_rope_f32's rotation of (a, b) = (x[i], x[i + half]) as the reference's
+// x86 build evaluates it (pq_decode.c is built with -mfma; gcc contracts the
+// first product of each line): a c - b s with a c fused, b c + a s with b c
+// fused.  The rounding matters once rows are stored as fp16 or int8.
+__device__ __forceinline__ float rope_lo(float a, float b, float c, float s) { return fmaf(a, c, -(b * s)); }
+__device__ __forceinline__ float rope_hi(float a, float b, float c, float s) { return fmaf(b, c, a * s); }
+
 // ib_rope_f32 (NEOX halves, src/pq_decode.c:4623-4642) of the query heads in
 // place and of the key heads into the cache row, plus the value copy.
 // Block b < n_heads: query head; < n_heads + n_kv: key head; else value head.
@@ -194,8 +201,8 @@ __global__ void v5_rope_kv_kernel(float* __restrict__ q, const float* __restrict
             float* dst = b < n_heads ? q + (size_t)b * hd : kc + (size_t)(b - n_heads) * hd;
             const float c = cs[2 * i], s = cs[2 * i + 1];
             const float a = src[i], e = src[i + half];
-            dst[i] = a * c - e * s;
-            dst[i + half] = e * c + a * s;
+            dst[i] = rope_lo(a, e, c, s);
+            dst[i + half] = rope_hi(a, e, c, s);
         } else {
             const int h = b - n_heads - n_kv;
             vc[(size_t)h * hd + i] = v[(size_t)h * hd + i];
@@ -308,8 +315,8 @@ __global__ __launch_bounds__(kAttnThreads) void v5_attn_kernel(
         const int g = e / HALF, i = e - g * HALF;
         const float* qh = q + (size_t)(kvh * GRP + g) * HD;
         const float c = csp[2 * i], sn = csp[2 * i + 1], a = qh[i], b = qh[i + HALF];
-        qs[g][i] = a * c - b * sn;
-        qs[g][i + HALF] = b * c + a * sn;
+        qs[g][i] = rope_lo(a, b, c, sn);
+        qs[g][i + HALF] = rope_hi(a, b, c, sn);
     }
     if (tid < GRP) {
         gmax[tid] = -INFINITY;
@@ -328,7 +335,7 @@ __global__ __launch_bounds__(kAttnThreads) void v5_attn_kernel(
                 const int h = e / HALF, i = e - h * HALF;
                 const float* kk = k + (size_t)h * HD;
                 const float c = csp[2 * i], sn = csp[2 * i + 1], a = kk[i], b = kk[i + HALF];
-                km = fmaxf(km, fmaxf(fabsf(a * c - b * sn), fabsf(b * c + a * sn)));
+                km = fmaxf(km, fmaxf(fabsf(rope_lo(a, b, c, sn)), fabsf(rope_hi(a, b, c, sn))));
             }
             for (int e = tid; e < kv_dim; e += kAttnThreads) vm = fmaxf(vm, fabsf(v[e]));
             km = wave_max(km);
@@ -352,7 +359,7 @@ __global__ __launch_bounds__(kAttnThreads) void v5_attn_kernel(
             int8_t* vrow = (int8_t*)vc + rowo;
             for (int i = tid; i < HALF; i += kAttnThreads) {
                 const float c = csp[2 * i], sn = csp[2 * i + 1], a = kh[i], b = kh[i + HALF];
-                const int q0 = kv_q8(a * c - b * sn, ki), q1 = kv_q8(b * c + a * sn, ki);
+                const int q0 = kv_q8(rope_lo(a, b, c, sn), ki), q1 = kv_q8(rope_hi(a, b, c, sn), ki);
                 krow[i] = (int8_t)q0;
                 krow[i + HALF] = (int8_t)q1;
                 kcur[i] = (float)q0 * ks;
@@ -366,7 +373,7 @@ __global__ __launch_bounds__(kAttnThreads) void v5_attn_kernel(
         } else {
             for (int i = tid; i < HALF; i += kAttnThreads) {
                 const float c = csp[2 * i], sn = csp[2 * i + 1], a = kh[i], b = kh[i + HALF];
-                const float r0 = a * c - b * sn, r1 = b * c + a * sn;
+                const float r0 = rope_lo(a, b, c, sn), r1 = rope_hi(a, b, c, sn);
                 if constexpr (KVT == KV_F16) {
                     const _Float16 h0 = (_Float16)r0, h1 = (_Float16)r1;
                     ((_Float16*)kc)[rowo + i] = h0;
