@@ -351,9 +351,18 @@ typedef struct {
 /* ib_pq_generate_sample (src/pq_decode.c:5480-5561): candidates from the
  * device (top-K PQ head, or the full logits), the pick on the host with the
  * reference's xorshift64 stream and softmax / top-p / inverse-CDF rule.
- * Equal full-vocabulary logits are ordered by token id. */
+ * Equal full-vocabulary logits are ordered as the reference's selection sort
+ * leaves them. */
 int  ibh_v5_generate_sample(ibh_v5_session* s, ibh_v5_kv* kv, const int* prompt_ids, int n_prompt, int max_new,
                             int eos_token_id, const ibh_pq_sample_params* params, int* out_ids, int* n_out);
+/* sample_from_logits (src/pq_decode.c:5363-5436), the full-vocabulary pick
+ * of ibh_v5_generate_sample, on host logits: descending selection-sort order
+ * (ties as the reference's swaps leave them), softmax / T, top-k (top_k > 0
+ * and < vocab), top-p, inverse CDF with one draw from the xorshift64 state
+ * *rng_state (advanced).  Host only; returns the token id, or < 0 on invalid
+ * arguments. */
+int  ibh_v5_sample_from_logits(const float* logits, int vocab, const ibh_pq_sample_params* params,
+                               uint64_t* rng_state);
 
 /* ── device-resident decode (forward_single_ex + greedy generate) ── */
 

@@ -65,6 +65,7 @@ SIGNATURES = {
     "ibh_v5_forward_step_to_hidden": (I, [P, P, I, I, P]),
     "ibh_v5_generate_greedy": (I, [P, P, P, I, I, I, P, P]),
     "ibh_v5_generate_sample": (I, [P, P, P, I, I, I, P, P, P]),
+    "ibh_v5_sample_from_logits": (I, [P, I, P, P]),
     "ibh_model_load": (I, [C.c_char_p, I, P]),
     "ibh_model_free": (None, [P]),
     "ibh_model_dims": (I, [P, P]),

@@ -8,8 +8,10 @@
 //            sorted candidates, top-p prefix, inverse CDF;
 //   full     sample_from_logits (5362-5436): descending order (top_k == 0
 //            or > 256: the whole vocabulary), softmax / T, top-p, inverse
-//            CDF.  Equal logits take the lower token id first here; the
-//            reference's selection sort orders ties by its swap sequence.
+//            CDF.  The order is the one the reference's selection sort
+//            with swaps (5380-5397) leaves, ties included: equal logits end
+//            up in the order its swaps displace them (logits [5,5,9] give
+//            ids 2,1,0), found here in O(V log V) by following the swaps.
 //   T <= 0   argmax (first maximum) / the first candidate.
 #include <math.h>
 #include <stdint.h>
@@ -89,6 +91,48 @@ int pick_topk(const float* lg, const int32_t* ids, int K, const ibh_pq_sample_pa
     return picked;
 }
 
+// The first k positions of the order the reference's selection sort leaves
+// (pq_decode.c:5380-5397): step i takes the lowest position >= i holding the
+// largest value not yet placed (strict >, so the first such position) and
+// swaps it with position i, which moves position i's element to where the
+// taken one was.  Only that displacement differs from a plain stable sort,
+// so this follows it: each distinct value keeps the positions its elements
+// occupy, sorted descending (the lowest at the back); a step pops the lowest
+// position of the current value and, when that is not i, moves the element
+// at i (of a smaller value) into the vacated position.  Comparisons are by
+// float ==/>, as the reference's; NaN logits are not ordered the same way.
+void selection_order(const float* logits, int vocab, int k, std::vector<int>& idx) {
+    std::vector<int> by_val(vocab);
+    std::iota(by_val.begin(), by_val.end(), 0);
+    std::sort(by_val.begin(), by_val.end(),
+              [&](int a, int b) { return logits[a] > logits[b] || (logits[a] == logits[b] && a < b); });
+    std::vector<int> grp(vocab);
+    std::vector<std::vector<int>> where;   // per value, descending positions
+    for (int r = 0; r < vocab; r++) {
+        const int e = by_val[r];
+        if (r == 0 || logits[e] != logits[by_val[r - 1]]) where.emplace_back();
+        grp[e] = (int)where.size() - 1;
+    }
+    // initially position = id; ids run ascending within a value, so the
+    // reversed walk leaves each list descending
+    for (int r = vocab - 1; r >= 0; r--) where[grp[by_val[r]]].push_back(by_val[r]);
+    idx.resize(vocab);
+    std::iota(idx.begin(), idx.end(), 0);   // element at each position
+    int g = 0;
+    for (int i = 0; i < k; i++) {
+        while (where[g].empty()) g++;
+        const int j = where[g].back();
+        where[g].pop_back();
+        if (j != i) {
+            const int e = idx[i];   // a smaller value: moves from i to j
+            auto& w = where[grp[e]];
+            w.erase(std::find(w.begin(), w.end(), i));
+            w.insert(std::upper_bound(w.begin(), w.end(), j, std::greater<int>()), j);
+            std::swap(idx[i], idx[j]);
+        }
+    }
+}
+
 int pick_full(const float* logits, int vocab, const ibh_pq_sample_params& p, Rng& rng) {
     if (p.temperature <= 0.0f) {
         int best = 0;
@@ -102,11 +146,8 @@ int pick_full(const float* logits, int vocab, const ibh_pq_sample_params& p, Rng
     }
     const float invT = 1.0f / p.temperature;
     const int k = (p.top_k > 0 && p.top_k < vocab) ? p.top_k : vocab;
-    std::vector<int> idx(vocab);
-    std::iota(idx.begin(), idx.end(), 0);
-    auto desc = [&](int a, int b) { return logits[a] > logits[b] || (logits[a] == logits[b] && a < b); };
-    if (k < vocab) std::partial_sort(idx.begin(), idx.begin() + k, idx.end(), desc);
-    else std::sort(idx.begin(), idx.end(), desc);
+    std::vector<int> idx;
+    selection_order(logits, vocab, k, idx);
     std::vector<float> sc(k);
     int n_keep = k;
     const float m = logits[idx[0]] * invT;
@@ -147,6 +188,18 @@ int pick_full(const float* logits, int vocab, const ibh_pq_sample_params& p, Rng
 }
 
 }  // namespace
+
+extern "C" int ibh_v5_sample_from_logits(const float* logits, int vocab, const ibh_pq_sample_params* params,
+                                         uint64_t* rng_state) {
+    if (!logits || vocab <= 0 || !params || !rng_state) {
+        ibh_set_error("ibh_v5_sample_from_logits: invalid arguments");
+        return IBH_ERROR_PARAM;
+    }
+    Rng rng{*rng_state};
+    const int tok = pick_full(logits, vocab, *params, rng);
+    *rng_state = rng.s;
+    return tok;
+}
 
 extern "C" int ibh_v5_generate_sample(ibh_v5_session* s, ibh_v5_kv* kv, const int* prompt, int n_prompt, int max_new,
                                       int eos, const ibh_pq_sample_params* params, int* out_ids, int* n_out) {

@@ -31,3 +31,17 @@ int ref_int4g_matmul(const uint8_t* q, const uint16_t* s, const float* inv_act, 
     free(xs);
     return rc;
 }
+
+/* sample_from_logits (src/pq_decode.c:5363-5436) with the caller's
+ * xorshift64 state, which it advances. */
+int ref_sample_from_logits(const float* logits, int vocab, float temperature, int top_k, float top_p,
+                           uint64_t* state) {
+    ib_pq_sample_params p;
+    memset(&p, 0, sizeof(p));
+    p.temperature = temperature; p.top_k = top_k; p.top_p = top_p;
+    pq_rng r;
+    r.s = *state;
+    int tok = sample_from_logits(logits, vocab, p, &r);
+    *state = r.s;
+    return tok;
+}

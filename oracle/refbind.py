@@ -274,15 +274,31 @@ def pq_reconstruct(t: dict):
 _i4 = None
 
 
-def int4g_matmul(t: dict, x):
-    """The reference's INT4 group-scale session matmul (oracle/ref_int4g.c).
-    IB_ACT_SPARSE_REL is read by the reference once per process, so a caller
-    that wants the skip mask sets it before the first call (in a subprocess)."""
+def _int4g_lib():
     global _i4
     if _i4 is None:
         _i4 = C.CDLL(REF_INT4G)
         _i4.ref_int4g_matmul.argtypes = [P, P, P, P, P, I, I, I, I, P, P]
         _i4.ref_int4g_matmul.restype = I
+        _i4.ref_sample_from_logits.argtypes = [P, I, C.c_float, I, C.c_float, P]
+        _i4.ref_sample_from_logits.restype = I
+    return _i4
+
+
+def sample_from_logits(logits, temperature, top_k, top_p, state: int):
+    """The reference's full-vocabulary pick (src/pq_decode.c:5363-5436) from
+    xorshift64 state ``state``; returns (token, advanced state)."""
+    lg = np.ascontiguousarray(logits, np.float32)
+    st = np.array([state], np.uint64)
+    tok = _int4g_lib().ref_sample_from_logits(_p(lg), lg.size, temperature, top_k, top_p, _p(st))
+    return tok, int(st[0])
+
+
+def int4g_matmul(t: dict, x):
+    """The reference's INT4 group-scale session matmul (oracle/ref_int4g.c).
+    IB_ACT_SPARSE_REL is read by the reference once per process, so a caller
+    that wants the skip mask sets it before the first call (in a subprocess)."""
+    _int4g_lib()
     q, s = np.ascontiguousarray(t["q"], np.uint8), np.ascontiguousarray(t["s"], np.uint16)
     M, N = q.shape[0], q.shape[1] * 2
     G = N // s.shape[1]

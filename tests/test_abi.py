@@ -71,3 +71,45 @@ def test_prompt_lookup_search_matches_reference():
         assert na == nb and (a == b).all()
         hits += na > 0
     assert hits > 100
+
+
+def test_full_vocab_sample_matches_reference_with_ties():
+    """ibh_v5_sample_from_logits (host code, no GPU) against the compiled
+    reference's sample_from_logits (src/pq_decode.c:5363-5436) on logits
+    with many equal values: its selection sort with swaps orders ties by the
+    displacement its swaps cause (logits [5,5,9] give ids 2,1,0), which a
+    stable sort does not, so top-k / top-p truncation and the inverse-CDF
+    pick see the same order only if that order is reproduced.  The same
+    xorshift64 state is carried through every draw on both sides."""
+    import ctypes
+    import numpy as np
+    from oracle import refbind as R
+    if not os.path.exists(R.REF_INT4G):
+        pytest.skip("reference library not built")
+    from libinferbit_amd import _lib
+    ours = _lib.lib()
+    rng = np.random.default_rng(3)
+    cases = [np.array([5, 5, 5.1], np.float32), np.array([5, 5, 9], np.float32), np.array([1, 1, 1, 1], np.float32),
+             np.array([9, 2, 2, 9, 2, 9, 0], np.float32)]
+    for _ in range(40):
+        n = int(rng.integers(2, 400))
+        cases.append(rng.integers(0, int(rng.integers(1, 6)), n).astype(np.float32) * 0.5)
+    cases.append(rng.integers(-3, 4, 3000).astype(np.float32))
+    picked_1 = 0
+    for lg in cases:
+        for T, k, p in ((1.0, 0, 0.0), (0.7, 0, 0.9), (1.5, 2, 0.0), (1.0, 5, 0.5), (2.0, 0, 0.3),
+                        (1.0, len(lg) - 1, 0.0), (0.0, 0, 0.0)):
+            prm = _lib.PqSampleParams(T, k, p, 0)
+            st_ours = st_ref = 0x9E3779B97F4A7C15
+            for _ in range(12):
+                s = np.array([st_ours], np.uint64)
+                a = ours.ibh_v5_sample_from_logits(lg.ctypes.data_as(ctypes.c_void_p), len(lg), ctypes.byref(prm),
+                                                   s.ctypes.data_as(ctypes.c_void_p))
+                st_ours = int(s[0])
+                b, st_ref = R.sample_from_logits(lg, T, k, p, st_ref)
+                assert a == b, (lg[:16], T, k, p)
+                assert st_ours == st_ref
+                # [5, 5, 5.1] with top_k 2: the reference keeps ids 2 and 1; a
+                # stable order would keep 2 and 0 and never return 1
+                picked_1 += lg.size == 3 and lg[2] == np.float32(5.1) and k == 2 and b == 1
+    assert picked_1 > 0

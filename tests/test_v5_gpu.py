@@ -29,6 +29,9 @@ ALLPQ = {p: "pq" for p in ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", 
 CASES = {
     "int4": dict(),
     "int4_awq_outl": dict(awq=True, outliers=3),
+    # 40 outliers per row: 4 rows x 40 > 128 sidecar slots, so the fused
+    # rmsnorm (q/k/v, gate/up) and silu (down) launches take the per-row loop
+    "int4_awq_outl40": dict(awq=True, outliers=40),
     "mixed": dict(backend=dict(gate_proj="pq", up_proj="pq", down_proj="pq", o_proj="fp16"), awq=True),
     "pq_l2_actscale_pqembed": dict(backend=ALLPQ, levels=2, pq_act_scale=True, embed="pq"),
     "pq_outl_k16_f32embed": dict(backend=ALLPQ, levels=2, k2=16, pq_outliers=16, embed="f32"),
@@ -97,6 +100,7 @@ def test_forward_step_and_greedy(L, tmp_path_factory, tmp_path, name):
     S = PqSession(path)
     gt, gl = gpu_steps(S, PROMPT, N_NEW)
     errs = [relerr(gl[i], rl[i]) for i in range(len(PROMPT))]
+    print(f"v5 {name}: max rel logit err {max(errs):.3g}", flush=True)
     assert max(errs) <= TOL, (name, errs)
     assert gt == rt, (name, gt, rt)
     rg, _ = ref_run(path, PROMPT, N_NEW, "greedy", tmp_path)
