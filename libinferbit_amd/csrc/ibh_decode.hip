@@ -53,6 +53,13 @@ int ibh_launch_silu_quant(float* out, const float* gate, const float* up, const 
                           int N, bool exact, hipStream_t st);
 int ibh_launch_rows_w4a8_multi(const MatDesc* d, int n, int kind, const int8_t* qx, const float* sa, int N,
                                hipStream_t st);
+int ibh_launch_rows_w4a8_norm_multi(const MatDesc* d, int n, int kind, const float* x, const float* dl,
+                                    const uint16_t* w_norm, float* xr, float eps, int N, hipStream_t st,
+                                    bool accy);
+int ibh_launch_rows_w4a8(float* out, const void* w, const void* sw, int kind, const int8_t* qx, const float* sa,
+                         int M, int N, hipStream_t st, bool accy);
+int ibh_launch_tile_x_multi(const MatDesc* d, int n, int kind, const float* x, int N, int bits, hipStream_t st,
+                            bool accy, const float* dl, const uint16_t* nw, float* xr, float eps);
 int ibh_launch_rows_x_multi(const MatDesc* d, int n, int kind, const float* x, int N, int bits, hipStream_t st);
 int ibh_launch_matvec_exact_multi(const MatDesc* d, int n, int kind, const float* x, int N, int bits,
                                   hipStream_t st);
@@ -234,6 +241,7 @@ struct ibh_model {
     float theta = 10000.f, eps = 1e-5f;
     bool w4a8 = true;
     bool exact = true;               // bit-identical to the x86 reference (default)
+    bool no_norm_fuse = false;       // IBH_NO_NORM_FUSE=1: separate norm / quantize kernels in fast mode
     float* att = nullptr;            // exact attention scores [n_heads][max_pos + 1]
     uint8_t* dweights = nullptr;
     size_t wbytes = 0;
@@ -242,6 +250,7 @@ struct ibh_model {
     const uint16_t* out_norm = nullptr;
     float *x = nullptr, *xb = nullptr, *xb2 = nullptr, *q = nullptr, *k = nullptr, *v = nullptr;
     float *hb = nullptr, *hb2 = nullptr, *logits = nullptr, *ones = nullptr, *rope = nullptr, *sa = nullptr;
+    float* xalt = nullptr;   // second residual buffer (norm-fused launches that add a delta)
     int8_t* qx = nullptr;
     void* attn_ws = nullptr;
     size_t attn_ws_bytes = 0;
@@ -345,6 +354,8 @@ int qkv(ibh_model* m, const DLayer& L, bool exact) {
 // (the reference quantizes the same vector for each, with identical codes);
 // when down is, silu_mul and the quantization of its result run as one
 // kernel.  `exact` selects the x86-order kernels.
+int mlp_down(ibh_model* m, const DLayer& L, bool exact, float* resid = nullptr, bool* acc = nullptr);
+
 int mlp(ibh_model* m, const DLayer& L, bool exact) {
     const int H = m->hidden, I = m->inter;
     void* st = (void*)m->st;
@@ -366,11 +377,25 @@ int mlp(ibh_model* m, const DLayer& L, bool exact) {
     } else if ((rc = mm(m, L.gate, m->hb, m->xb2, I, H)) || (rc = mm(m, L.up, m->hb2, m->xb2, I, H))) {
         return rc;
     }
+    return mlp_down(m, L, exact);
+}
+
+// silu(gate) * up and the down projection, m->hb / m->hb2 -> m->xb, or,
+// when resid is not null and the W4A8 kernel takes it, added into resid (the
+// layer's residual add; *acc set).
+int mlp_down(ibh_model* m, const DLayer& L, bool exact, float* resid, bool* acc) {
+    const int H = m->hidden, I = m->inter;
+    void* st = (void*)m->st;
+    int rc;
+    if (acc) *acc = false;
     if (m->w4a8 && L.down.bits == 4) {
-        if ((rc = ibh_launch_silu_quant(m->hb, m->hb, m->hb2, L.mask, m->qx, m->sa, I, exact, m->st)) ||
-            (rc = ibh_matmul_w4a8(m->xb, L.down.w, L.down.s, L.down.skind, m->qx, m->sa, H, I, st)))
-            return rc;
-        return IBH_OK;
+        if ((rc = ibh_launch_silu_quant(m->hb, m->hb, m->hb2, L.mask, m->qx, m->sa, I, exact, m->st))) return rc;
+        if (resid && ibh_launch_rows_w4a8(resid, L.down.w, L.down.s, L.down.skind, m->qx, m->sa, H, I, m->st, true)) {
+            IBH_CHECK_LAUNCH("ibh_model: down (w4a8) + residual");
+            *acc = true;
+            return IBH_OK;
+        }
+        return ibh_matmul_w4a8(m->xb, L.down.w, L.down.s, L.down.skind, m->qx, m->sa, H, I, st);
     }
     if (exact) {
         if ((rc = ibh_launch_silu_mul_exact(m->hb, m->hb, m->hb2, L.mask, I, m->st))) return rc;
@@ -379,6 +404,68 @@ int mlp(ibh_model* m, const DLayer& L, bool exact) {
     silu_mul_kernel<<<(I + 255) / 256, 256, 0, m->st>>>(m->hb, m->hb, m->hb2, L.mask, I);
     IBH_CHECK_LAUNCH("ibh_model: silu_mul");
     return mm(m, L.down, m->xb, m->hb, H, I);
+}
+
+// Fast path: the o projection added into the residual stream by the
+// kernel's epilogue (resid += W_o x): the W4A8 launch quantizing x in its
+// prologue, or the fp32-activation tile kernel.  Returns 1 if launched, 0 if
+// the tensor or shape is not eligible (the caller writes m->xb and adds it
+// later).
+int o_acc(ibh_model* m, const DLayer& L, float* resid) {
+    const int H = m->hidden;
+    const MatDesc d{resid, L.o.w, L.o.s, H};
+    if (L.o.bits == 4 && m->w4a8) {
+        if (!ibh_launch_rows_w4a8_norm_multi(&d, 1, L.o.skind, m->xb2, nullptr, nullptr, nullptr, 0.f, H, m->st, true))
+            return 0;
+    } else if (L.o.bits == 8 || L.o.bits == 4 || L.o.bits == 2) {
+        if (!ibh_launch_tile_x_multi(&d, 1, L.o.skind, m->xb2, H, L.o.bits, m->st, true, nullptr, nullptr, nullptr, 0.f))
+            return 0;
+    } else {
+        return 0;
+    }
+    IBH_CHECK_LAUNCH("ibh_model: o + residual");
+    return 1;
+}
+
+// Fast path: rmsnorm + activation quantization (and, with a pending delta
+// dl, the residual add) fused into the W4A8 q/k/v (qkv = true) or gate/up
+// launch.  With dl the residual stream moves from *xc to *xa (swapped on
+// return).  Returns 1 if launched, 0 if the layer's tensors are not all W4A8
+// of one scale kind (the caller runs the separate kernels then).
+int norm_fused(ibh_model* m, const DLayer& L, bool qkv, float*& xc, float*& xa, const float* dl) {
+    if (m->no_norm_fuse) return 0;
+    const int H = m->hidden, KV = m->n_kv * m->head_dim, I = m->inter;
+    int n, kind, bits;
+    MatDesc d[3];
+    if (qkv) {
+        if (L.q.bits != L.k.bits || L.k.bits != L.v.bits || L.q.skind != L.k.skind || L.k.skind != L.v.skind)
+            return 0;
+        d[0] = {m->q, L.q.w, L.q.s, H};
+        d[1] = {m->k, L.k.w, L.k.s, KV};
+        d[2] = {m->v, L.v.w, L.v.s, KV};
+        n = 3;
+        kind = L.q.skind;
+        bits = L.q.bits;
+    } else {
+        if (L.gate.bits != L.up.bits || L.gate.skind != L.up.skind || (L.mask && L.mask_sparse)) return 0;
+        d[0] = {m->hb, L.gate.w, L.gate.s, I};
+        d[1] = {m->hb2, L.up.w, L.up.s, I};
+        n = 2;
+        kind = L.gate.skind;
+        bits = L.gate.bits;
+    }
+    const uint16_t* nw = qkv ? L.in_norm : L.post_norm;
+    float* xr = dl ? xa : nullptr;
+    if (bits == 4 && m->w4a8) {
+        if (!ibh_launch_rows_w4a8_norm_multi(d, n, kind, xc, dl, nw, xr, m->eps, H, m->st, false)) return 0;
+    } else if (bits == 8 || bits == 4 || bits == 2) {
+        if (!ibh_launch_tile_x_multi(d, n, kind, xc, H, bits, m->st, false, dl, nw, xr, m->eps)) return 0;
+    } else {
+        return 0;
+    }
+    IBH_CHECK_LAUNCH(qkv ? "ibh_model: norm + qkv (w4a8)" : "ibh_model: norm + gate/up (w4a8)");
+    if (dl) std::swap(xc, xa);
+    return 1;
 }
 
 // forward_single_ex(compute_logits=1) + greedy pick, bit-identical to the CPU.
@@ -418,24 +505,46 @@ int step(ibh_model* m) {
     embed_kernel<<<(H + 255) / 256, 256, 0, m->st>>>(m->x, m->emb.w, (const uint16_t*)(m->emb.skind == IBH_SCALE_F16 ? m->emb.s : nullptr),
                                                      m->emb.bits, H, m->dtokens(), m->dpos());
     IBH_CHECK_LAUNCH("ibh_model: embedding");
+    // The residual stream (ping-ponged by norm-fused launches that add a
+    // delta) and the delta not yet added to it (null: none pending).  The o
+    // and down projections add into the stream in their epilogue where the
+    // kernels allow; otherwise they write m->xb and the next norm adds it.
+    float *xc = m->x, *xa = m->xalt;
+    const float* dl = nullptr;
     for (int l = 0; l < m->n_layers; l++) {
         DLayer& L = m->layers[l];
-        // residual of the previous layer's MLP folded into this norm
-        add_rmsnorm_kernel<<<1, kNormThreads, 0, m->st>>>(m->xb, m->x, l ? m->xb : nullptr, L.in_norm, m->eps, H);
-        IBH_CHECK_LAUNCH("ibh_model: rmsnorm");
-        if ((rc = qkv(m, L, false))) return rc;
+        int f = norm_fused(m, L, true, xc, xa, dl);
+        if (f < 0) return f;
+        if (!f) {
+            add_rmsnorm_kernel<<<1, kNormThreads, 0, m->st>>>(m->xb, xc, dl, L.in_norm, m->eps, H);
+            IBH_CHECK_LAUNCH("ibh_model: rmsnorm");
+            if ((rc = qkv(m, L, false))) return rc;
+        }
         if ((rc = ibh_launch_rope_kv_write(L.kd, L.vd, L.ks, L.vs, m->q, m->k, m->v, m->rope, m->dpos(), m->n_heads,
                                            m->n_kv, m->head_dim, m->kv_bits, false, m->st)))
             return rc;
         if ((rc = ibh_launch_attn(m->xb2, m->q, L.kd, L.vd, L.ks, L.vs, 0, m->dpos(), m->max_pos, m->n_heads,
                                   m->n_kv, m->head_dim, m->kv_bits, m->attn_ws, m->attn_ws_bytes, m->st)))
             return rc;
-        if ((rc = mm(m, L.o, m->xb, m->xb2, H, H))) return rc;
-        add_rmsnorm_kernel<<<1, kNormThreads, 0, m->st>>>(m->xb2, m->x, m->xb, L.post_norm, m->eps, H);
-        IBH_CHECK_LAUNCH("ibh_model: rmsnorm");
-        if ((rc = mlp(m, L, false))) return rc;
+        if (!m->no_norm_fuse && o_acc(m, L, xc)) {
+            dl = nullptr;
+        } else {
+            if ((rc = mm(m, L.o, m->xb, m->xb2, H, H))) return rc;
+            dl = m->xb;
+        }
+        if ((f = norm_fused(m, L, false, xc, xa, dl)) < 0) return f;
+        if (!f) {
+            add_rmsnorm_kernel<<<1, kNormThreads, 0, m->st>>>(m->xb2, xc, dl, L.post_norm, m->eps, H);
+            IBH_CHECK_LAUNCH("ibh_model: rmsnorm");
+            if ((rc = mlp(m, L, false))) return rc;
+            dl = m->xb;
+        } else {
+            bool acc = false;
+            if ((rc = mlp_down(m, L, false, m->no_norm_fuse ? nullptr : xc, &acc))) return rc;
+            dl = acc ? nullptr : m->xb;
+        }
     }
-    add_rmsnorm_kernel<<<1, kNormThreads, 0, m->st>>>(m->x, m->x, m->xb, m->out_norm, m->eps, H);
+    add_rmsnorm_kernel<<<1, kNormThreads, 0, m->st>>>(m->x, xc, dl, m->out_norm, m->eps, H);
     IBH_CHECK_LAUNCH("ibh_model: final rmsnorm");
     if ((rc = mm(m, m->head, m->logits, m->x, m->vocab, H))) return rc;
     argmax_advance_kernel<<<1, 1024, 0, m->st>>>(m->logits, m->vocab, m->dtokens(), m->dpos(), m->dprompt_end());
@@ -746,6 +855,10 @@ int load(ibh_model* m, const char* path, int context_length) {
     }
     m->w4a8 = w4a8_enabled();
     {
+        const char* e = getenv("IBH_NO_NORM_FUSE");
+        m->no_norm_fuse = e && e[0] == '1';
+    }
+    {
         const char* f = getenv("IBH_DECODE_FAST");
         m->exact = !(f && f[0] == '1');
         if (m->hidden % 8 || m->hidden > 12288) m->exact = false;   // no x86-order rmsnorm: fast kernels
@@ -807,12 +920,21 @@ int load(ibh_model* m, const char* path, int context_length) {
         }
         return IBH_OK;
     };
+    // norm weights: copied out of the weight blob into 16-byte-aligned rows
+    // (the norm-fused launches read them as 16-byte vectors)
+    const size_t nrow = ((size_t)m->hidden * 2 + 15) & ~(size_t)15;
+    uint16_t* norms = nullptr;
+    if ((rc = dalloc(m, (void**)&norms, nrow * (2 * (size_t)m->n_layers + 1)))) return rc;
+    int nnorm = 0;
     auto norm = [&](const TMeta& t, const uint16_t** d, const char* name) -> int {
         if (!t.present || t.offset + (size_t)m->hidden * 2 > wsize) {
             ibh_set_error("ibh_model_load: norm %s missing or out of range", name);
             return IBH_ERROR_FORMAT;
         }
-        *d = (const uint16_t*)(m->dweights + t.offset);
+        uint16_t* dst = (uint16_t*)((uint8_t*)norms + nrow * nnorm++);
+        IBH_HIP(hipMemcpy(dst, m->dweights + t.offset, (size_t)m->hidden * 2, hipMemcpyDeviceToDevice),
+                "ibh_model_load: norm weights");
+        *d = dst;
         return IBH_OK;
     };
     const size_t H = m->hidden, KV = (size_t)m->n_kv * m->head_dim, I = m->inter, V = m->vocab;
@@ -870,6 +992,7 @@ int load(ibh_model* m, const char* path, int context_length) {
 
     // activations and state
     if ((rc = dalloc(m, (void**)&m->x, H * 4)) || (rc = dalloc(m, (void**)&m->xb, H * 4)) ||
+        (rc = dalloc(m, (void**)&m->xalt, H * 4)) ||
         (rc = dalloc(m, (void**)&m->xb2, H * 4)) || (rc = dalloc(m, (void**)&m->q, H * 4)) ||
         (rc = dalloc(m, (void**)&m->k, KV * 4)) || (rc = dalloc(m, (void**)&m->v, KV * 4)) ||
         (rc = dalloc(m, (void**)&m->hb, I * 4)) || (rc = dalloc(m, (void**)&m->hb2, I * 4)) ||

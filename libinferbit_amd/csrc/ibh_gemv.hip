@@ -385,7 +385,7 @@ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 }  // namespace
 
 int ibh_launch_rows_w4a8(float* out, const void* w, const void* sw, int kind, const int8_t* qx, const float* sa,
-                         int M, int N, hipStream_t st);
+                         int M, int N, hipStream_t st, bool accy = false);
 int ibh_launch_rows_x(float* out, const void* w, const void* scales, int kind, const float* x, int M, int N,
                       int bits, hipStream_t st);
 int ibh_launch_gemv_mfma(float* out, const void* w, const void* scales, int kind, const float* x, int M,

@@ -113,7 +113,7 @@ template <int KIND, int R, int SPW, bool SAREG>
 __global__ __launch_bounds__(512) void gemv_rows_w4a8(float* __restrict__ y, const uint8_t* __restrict__ W,
                                                       const void* __restrict__ sc, const int8_t* __restrict__ qx,
                                                       const float* __restrict__ sa, int M, int N, int S, int WR,
-                                                      int KW) {
+                                                      int KW, int accy) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -195,7 +195,8 @@ __global__ __launch_bounds__(512) void gemv_rows_w4a8(float* __restrict__ y, con
                 if (4 * q + 2 < G) f = fmaf(a4.z, s4.z, f);
                 if (4 * q + 3 < G) f = fmaf(a4.w, s4.w, f);
             }
-            y[row] = f * load_scale<KIND>(sc, row);
+            const float yv = f * load_scale<KIND>(sc, row);
+            y[row] = accy ? y[row] + yv : yv;
         }
     } else {
         if (threadIdx.x < G) sa_s[threadIdx.x] = sa_mine;
@@ -212,7 +213,8 @@ __global__ __launch_bounds__(512) void gemv_rows_w4a8(float* __restrict__ y, con
                 f = fmaf(a4.x, s4.x, f); f = fmaf(a4.y, s4.y, f); f = fmaf(a4.z, s4.z, f); f = fmaf(a4.w, s4.w, f);
             }
             for (; g < G; g++) f = fmaf(gp[g], sa_s[g], f);
-            y[row] = f * load_scale<KIND>(sc, row);
+            const float yv = f * load_scale<KIND>(sc, row);
+            y[row] = accy ? y[row] + yv : yv;
         }
     }
 }
@@ -220,31 +222,143 @@ __global__ __launch_bounds__(512) void gemv_rows_w4a8(float* __restrict__ y, con
 // W4A8 with the row length fixed at compile time: N = 128*GS (GS = 16 or 32
 // groups, one or two 1 KiB steps), whole rows per wavefront.  sa lives in
 // registers from the start, group sums pass through LDS once.
-template <int KIND, int R, int GS>
-__global__ __launch_bounds__(256) void gemv_rows_w4a8_k(const RowSet rs, const int8_t* __restrict__ qx,
-                                                        const float* __restrict__ sa) {
+//
+// NORM (1, or 2 with a residual delta): the layer's rmsnorm and activation
+// quantization (NORM 2: and the residual add) run in the prologue of every
+// block instead of separate kernels before it; NORM 3: the quantization
+// alone (xn = x).  Each thread takes CPT =
+// N/256 consecutive columns: xin = x (+ dl), ss = sum of fmaf(xin, xin) (wave sums, then the
+// four waves in order), xn = (xin * (1/sqrtf(ss/N + eps))) * w_norm (the
+// add_rmsnorm_kernel rule), then each 128-column group (128/CPT adjacent
+// lanes) is quantized by the quant_group128 rule into LDS, which the
+// contraction reads in place of qx / sa.  NORM 2: block 0 writes xin to
+// xr, the next residual stream.  x, dl and w_norm are loaded before the weights and
+// used after them are issued, so no wait for them waits on a weight load.
+// WPB: wavefronts per block (4 rows each).
+template <int KIND, int R, int GS, int NORM, int WPB = 4>
+__global__ __launch_bounds__(64 * WPB) void gemv_rows_w4a8_k(const RowSet rs, const int8_t* __restrict__ qx,
+                                                        const float* __restrict__ sa, const float* __restrict__ x,
+                                                        const float* __restrict__ dl, const uint16_t* __restrict__ nw,
+                                                        float* __restrict__ xr, float eps, int accy) {
     constexpr int SPW = GS / 16;
     constexpr size_t rb = (size_t)GS * 64;
-    __shared__ __align__(16) float gsum[4 * R][GS];
+    constexpr int N = 128 * GS, CPT = N / (64 * WPB), TPG = 128 / CPT;
+    static_assert(CPT == 8 || CPT == 16, "8 or 16 columns per thread");
+    __shared__ __align__(16) float gsum[WPB * R][GS];
+    __shared__ __align__(16) int8_t qs[NORM ? N : 16];
+    __shared__ __align__(16) float ss_s[NORM ? GS : 4];
+    __shared__ float red[WPB];
     const RowPick P = pick_rows(rs);
     const uint8_t* __restrict__ W = P.W;
     const void* __restrict__ sc = P.sc;
     float* __restrict__ y = P.y;
     const int M = P.M;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int row0 = (P.bid * 4 + wave) * R;
+    const int row0 = (P.bid * WPB + wave) * R;
     const int segl = seg_of<true>(lane);
+    const int c0 = (int)threadIdx.x * CPT;
+    float4 xv[NORM ? CPT / 4 : 1], dv[NORM == 2 ? CPT / 4 : 1];
+    uint4 wn[NORM ? CPT / 8 : 1];
     float4 sav[GS / 4];
+    if constexpr (NORM) {
 #pragma unroll
-    for (int q = 0; q < GS / 4; q++) sav[q] = ((const float4*)sa)[q];
+        for (int q = 0; q < CPT / 4; q++) {
+            xv[q] = *(const float4*)(x + c0 + 4 * q);
+            if constexpr (NORM == 2) dv[q] = *(const float4*)(dl + c0 + 4 * q);
+        }
+#pragma unroll
+        for (int q = 0; q < CPT / 8; q++) wn[q] = NORM == 3 ? uint4{0u, 0u, 0u, 0u} : *(const uint4*)(nw + c0 + 8 * q);
+    } else {
+#pragma unroll
+        for (int q = 0; q < GS / 4; q++) sav[q] = ((const float4*)sa)[q];
+    }
     uint4 bv[SPW][2];
     uint4 wv[SPW][R];
 #pragma unroll
     for (int j = 0; j < SPW; j++) {
+        if constexpr (!NORM) {
 #pragma unroll
-        for (int a = 0; a < 2; a++) bv[j][a] = *(const uint4*)(qx + j * 2048 + segl * 32 + 16 * a);
+            for (int a = 0; a < 2; a++) bv[j][a] = *(const uint4*)(qx + j * 2048 + segl * 32 + 16 * a);
+        }
 #pragma unroll
         for (int r = 0; r < R; r++) wv[j][r] = ld_stream16(W + (size_t)min(row0 + r, M - 1) * rb + j * 1024 + 16 * segl);
+    }
+    if constexpr (NORM) {
+        float v[CPT];
+        float ss = 0.f;
+#pragma unroll
+        for (int q = 0; q < CPT / 4; q++) {
+            if constexpr (NORM == 2) {
+                v[4 * q] = xv[q].x + dv[q].x;
+                v[4 * q + 1] = xv[q].y + dv[q].y;
+                v[4 * q + 2] = xv[q].z + dv[q].z;
+                v[4 * q + 3] = xv[q].w + dv[q].w;
+            } else {
+                v[4 * q] = xv[q].x;
+                v[4 * q + 1] = xv[q].y;
+                v[4 * q + 2] = xv[q].z;
+                v[4 * q + 3] = xv[q].w;
+            }
+        }
+        float mx = 0.f;
+        if constexpr (NORM != 3) {
+#pragma unroll
+            for (int e = 0; e < CPT; e++) ss = fmaf(v[e], v[e], ss);
+            ss = wave_sum(ss);
+            if (lane == 0) red[wave] = ss;
+            if (NORM == 2 && blockIdx.x == 0) {
+#pragma unroll
+                for (int q = 0; q < CPT / 4; q++)
+                    *(float4*)(xr + c0 + 4 * q) = float4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+            }
+            __syncthreads();
+            float tot = 0.f;
+#pragma unroll
+            for (int w = 0; w < WPB; w++) tot += red[w];
+            const float scale = 1.0f / sqrtf(tot / (float)N + eps);
+#pragma unroll
+            for (int e = 0; e < CPT; e++) {
+                const uint32_t h2 = (&wn[e / 8].x)[(e % 8) / 2];
+                v[e] = (v[e] * scale) * f16_to_f32((uint16_t)((e & 1) ? h2 >> 16 : h2 & 0xffff));
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < CPT; e++) mx = fmaxf(mx, fabsf(v[e]));
+#pragma unroll
+        for (int o = 1; o < TPG; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        uint32_t pk[CPT / 4];
+        float sg;
+        if (mx < 1e-10f) {
+            sg = 1e-10f;
+#pragma unroll
+            for (int q = 0; q < CPT / 4; q++) pk[q] = 0u;
+        } else {
+            sg = mx / 127.0f;
+            const float inv = 1.0f / sg;
+#pragma unroll
+            for (int q = 0; q < CPT / 4; q++) {
+                uint32_t w = 0u;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float xe = v[4 * q + e];
+                    const float t = xe * inv;
+                    int r = (int)(t + (xe >= 0 ? 0.5f : -0.5f));
+                    r = r < -127 ? -127 : (r > 127 ? 127 : r);
+                    w |= ((uint32_t)r & 0xffu) << (8 * e);
+                }
+                pk[q] = w;
+            }
+        }
+        if constexpr (CPT == 16) *(uint4*)(qs + c0) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        else *(uint2*)(qs + c0) = make_uint2(pk[0], pk[1]);
+        if ((threadIdx.x & (TPG - 1)) == 0) ss_s[threadIdx.x / TPG] = sg;
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < SPW; j++)
+#pragma unroll
+            for (int a = 0; a < 2; a++) bv[j][a] = *(const uint4*)(qs + j * 2048 + segl * 32 + 16 * a);
+#pragma unroll
+        for (int q = 0; q < GS / 4; q++) sav[q] = ((const float4*)ss_s)[q];
     }
     const i4_t zero4 = {0, 0, 0, 0};
     int isum[SPW][R];
@@ -282,7 +396,8 @@ __global__ __launch_bounds__(256) void gemv_rows_w4a8_k(const RowSet rs, const i
             const float4 a4 = gp[q], s4 = sav[q];
             f = fmaf(a4.x, s4.x, f); f = fmaf(a4.y, s4.y, f); f = fmaf(a4.z, s4.z, f); f = fmaf(a4.w, s4.w, f);
         }
-        y[row] = f * load_scale<KIND>(sc, row);
+        const float yv = f * load_scale<KIND>(sc, row);
+        y[row] = accy ? y[row] + yv : yv;
     }
 }
 
@@ -784,19 +899,57 @@ int ibh_launch_rows_w4a8_multi(const MatDesc* d, int n, int kind, const int8_t* 
     constexpr int R = 4;
     const RowSet rs = make_rowset(d, n, 4 * R);
     const int blocks = rowset_blocks(d, n, 4 * R);
-#define IBH_RWK(K_, G_) gemv_rows_w4a8_k<K_, R, G_><<<blocks, 256, 0, st>>>(rs, qx, sa)
+#define IBH_RWK(K_, G_) gemv_rows_w4a8_k<K_, R, G_, 0> \
+    <<<blocks, 256, 0, st>>>(rs, qx, sa, nullptr, nullptr, nullptr, nullptr, 0.f, 0)
     if (kind == IBH_SCALE_F16) { if (N == 4096) IBH_RWK(IBH_SCALE_F16, 32); else IBH_RWK(IBH_SCALE_F16, 16); }
     else { if (N == 4096) IBH_RWK(IBH_SCALE_F32, 32); else IBH_RWK(IBH_SCALE_F32, 16); }
 #undef IBH_RWK
     return 1;
 }
 
+// The same launch with the rmsnorm and activation quantization in every
+// block's prologue (decode's q/k/v and gate/up): x (+ dl when dl is not
+// null: the residual add, block 0 writing x + dl to xr, a buffer no block
+// reads) normed with the fp16 weight w_norm; with w_norm null, x quantized
+// as it is (dl must be null then).  accy: out += W x.  Returns 1 if
+// launched, 0 if not eligible.
+int ibh_launch_rows_w4a8_norm_multi(const MatDesc* d, int n, int kind, const float* x, const float* dl,
+                                    const uint16_t* w_norm, float* xr, float eps, int N, hipStream_t st,
+                                    bool accy) {
+    if ((N != 2048 && N != 4096) || n < 1 || n > 3 || !x || (dl && (!xr || !w_norm))) return 0;
+    if (((uintptr_t)x & 15) || ((uintptr_t)dl & 15) || ((uintptr_t)w_norm & 15) || ((uintptr_t)xr & 15)) return 0;
+    for (int i = 0; i < n; i++)
+        if (((uintptr_t)d[i].w & 15) || d[i].M <= 0) return 0;
+    constexpr int R = 4;
+    int Mt = 0;
+    for (int i = 0; i < n; i++) Mt += d[i].M;
+    // 8 wavefronts (32 rows) per block where that still leaves >= 512 blocks:
+    // every block repeats the prologue's reads of x (16 KB at N = 4096)
+    const int wpb = (N == 4096 && Mt / (8 * R) >= 512) ? 8 : 4;
+    const RowSet rs = make_rowset(d, n, wpb * R);
+    const int blocks = rowset_blocks(d, n, wpb * R);
+    const int ac = accy ? 1 : 0;
+#define IBH_RWK1(K_, G_, W_) do { \
+        if (!w_norm) gemv_rows_w4a8_k<K_, R, G_, 3, W_><<<blocks, 64 * W_, 0, st>>>(rs, nullptr, nullptr, x, nullptr, nullptr, nullptr, 0.f, ac); \
+        else if (dl) gemv_rows_w4a8_k<K_, R, G_, 2, W_><<<blocks, 64 * W_, 0, st>>>(rs, nullptr, nullptr, x, dl, w_norm, xr, eps, ac); \
+        else gemv_rows_w4a8_k<K_, R, G_, 1, W_><<<blocks, 64 * W_, 0, st>>>(rs, nullptr, nullptr, x, nullptr, w_norm, nullptr, eps, ac); } while (0)
+#define IBH_RWK(K_, G_) do { if (wpb == 8) IBH_RWK1(K_, G_, 8); else IBH_RWK1(K_, G_, 4); } while (0)
+    if (kind == IBH_SCALE_F16) { if (N == 4096) IBH_RWK(IBH_SCALE_F16, 32); else IBH_RWK1(IBH_SCALE_F16, 16, 4); }
+    else { if (N == 4096) IBH_RWK(IBH_SCALE_F32, 32); else IBH_RWK1(IBH_SCALE_F32, 16, 4); }
+#undef IBH_RWK1
+#undef IBH_RWK
+    return 1;
+}
+
 // W4A8, batch 1.  Returns 1 if launched, 0 if the shape is not eligible.
+// accy: out += W x (the residual add folded into the epilogue; N of 2048 or
+// 4096 columns is not eligible then).
 int ibh_launch_rows_w4a8(float* out, const void* w, const void* sw, int kind, const int8_t* qx, const float* sa,
-                         int M, int N, hipStream_t st) {
+                         int M, int N, hipStream_t st, bool accy) {
     const size_t rb = (size_t)N / 2;
     if (N % 32 != 0 || N < 32 || ((uintptr_t)w & 15) || ((uintptr_t)qx & 15)) return 0;
     if ((N == 2048 || N == 4096) && ((uintptr_t)sa & 15) == 0) {
+        if (accy) return 0;
         const MatDesc d{out, w, sw, M};
         return ibh_launch_rows_w4a8_multi(&d, 1, kind, qx, sa, N, st);
     }
@@ -817,7 +970,7 @@ int ibh_launch_rows_w4a8(float* out, const void* w, const void* sw, int kind, co
     const int blocks = (M + WR * R - 1) / (WR * R);
     const uint8_t* W = (const uint8_t*)w;
 #define IBH_RW(K_, SP_, SR_) \
-    gemv_rows_w4a8<K_, R, SP_, SR_><<<blocks, nthreads, lds, st>>>(out, W, sw, qx, sa, M, N, S, WR, KW)
+    gemv_rows_w4a8<K_, R, SP_, SR_><<<blocks, nthreads, lds, st>>>(out, W, sw, qx, sa, M, N, S, WR, KW, accy ? 1 : 0)
 #define IBH_RWK(K_) do { if (sareg) { if (spw == 2) IBH_RW(K_, 2, true); else IBH_RW(K_, 1, true); } \
                          else { if (spw == 2) IBH_RW(K_, 2, false); else IBH_RW(K_, 1, false); } } while (0)
     if (kind == IBH_SCALE_F16) IBH_RWK(IBH_SCALE_F16); else IBH_RWK(IBH_SCALE_F32);
@@ -828,7 +981,9 @@ int ibh_launch_rows_w4a8(float* out, const void* w, const void* sw, int kind, co
 
 // fp32 activations, int8 / int4 weights, rows of whole 1 KiB steps.  Returns 1
 // if launched, 0 if the shape is not eligible.
-int ibh_launch_tile_x_multi(const MatDesc* d, int n, int kind, const float* x, int N, int bits, hipStream_t st);
+int ibh_launch_tile_x_multi(const MatDesc* d, int n, int kind, const float* x, int N, int bits, hipStream_t st,
+                            bool accy = false, const float* dl = nullptr, const uint16_t* nw = nullptr,
+                            float* xr = nullptr, float eps = 0.f);
 
 int ibh_launch_rows_x_multi(const MatDesc* d, int n, int kind, const float* x, int N, int bits, hipStream_t st) {
     if (ibh_launch_tile_x_multi(d, n, kind, x, N, bits, st)) return 1;

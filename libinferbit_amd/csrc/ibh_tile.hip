@@ -216,9 +216,13 @@ __device__ __forceinline__ void digit_work(unsigned char* smem, const float* xra
     }
 }
 
-template <int BITS, int KIND, int KS, int CH>
+// NRM: the activation is the rmsnorm of x (+ dl) with weight nw (see the
+// launcher); the plain launch keeps the activation path as lean as it is.
+template <int BITS, int KIND, int KS, int CH, bool NRM>
 __global__ __launch_bounds__(1024) void gemv_tile_x(const RowSet rs, const float* __restrict__ x, int N, int S,
-                                                    int WQ, int KW, int NXW, int delay) {
+                                                    int WQ, int KW, int NXW, int delay, int accy,
+                                                    const float* __restrict__ dl, const uint16_t* __restrict__ nw,
+                                                    float* __restrict__ xr, float eps) {
     constexpr int NA = TGeo<BITS>::NA;
     constexpr int RUN = 4 * NA;             // consecutive columns per x run
     constexpr int XF = 8;                   // float4 of x per activation lane
@@ -228,7 +232,8 @@ __global__ __launch_bounds__(1024) void gemv_tile_x(const RowSet rs, const float
     float* xraw = (float*)(smem + (size_t)S * NA * 1024);   // x as loaded
     __shared__ float red[kTileMaxWaves];
     __shared__ int qpart[2 * kTileMaxChunks];   // per digit chunk: sum of d0, sum of (Q & 0x3fff)
-    __shared__ int cnt[3];                  // waves that posted max|x|; digit chunks done; next chunk
+    __shared__ int cnt[4];                  // waves that posted max|x|; digit chunks done; next chunk; ss posted
+    __shared__ float red_ss[kTileMaxWaves];
     __shared__ int part[kTileMaxWaves][4][3];
     __shared__ __align__(16) int epi[kTileMaxWaves][48];
     const int lane = threadIdx.x & 63;
@@ -237,17 +242,70 @@ __global__ __launch_bounds__(1024) void gemv_tile_x(const RowSet rs, const float
 #ifdef IBH_TILE_TRACE
     unsigned long long tt[8];
 #endif
-    if (threadIdx.x < 3) cnt[threadIdx.x] = 0;
+    if (threadIdx.x < 4) cnt[threadIdx.x] = 0;
     __syncthreads();
     IBH_TT(0);
 
     if (wave < NXW) {
         // ── activation wavefront: x -> LDS, max|x|, then digit chunks
-        float4 xv[XF];
+        // x, and for the norm dl and the norm weight, all issued before any
+        // is used: unconditional loads (an absent operand reads x again)
+        float4 xv[XF], dv[NRM ? XF : 1];
+        uint2 hv[NRM ? XF : 1];
+        if constexpr (NRM) {
+            const float4* dsrc = (const float4*)(dl ? dl : x);
+            const uint2* hsrc = (const uint2*)nw;
 #pragma unroll
-        for (int u = 0; u < XF; u++) {
-            const int c4 = lane + 64 * (wave + NXW * u);   // float4 index
-            xv[u] = 4 * c4 < N ? ((const float4*)x)[c4] : float4{0.f, 0.f, 0.f, 0.f};
+            for (int u = 0; u < XF; u++) {
+                const int c4 = lane + 64 * (wave + NXW * u);   // float4 index
+                const int cc = 4 * c4 < N ? c4 : 0;
+                xv[u] = ((const float4*)x)[cc];
+                dv[u] = dsrc[cc];
+                hv[u] = hsrc[cc];
+                if (4 * c4 >= N) xv[u] = float4{0.f, 0.f, 0.f, 0.f};
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < XF; u++) {
+                const int c4 = lane + 64 * (wave + NXW * u);   // float4 index
+                xv[u] = 4 * c4 < N ? ((const float4*)x)[c4] : float4{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+        if constexpr (NRM) {
+            // the layer's rmsnorm in front (and with dl its residual add,
+            // block 0 writing x + dl to xr): x <- ((x + dl) * inv) * w_norm,
+            // inv = 1/sqrtf(sum(x^2)/N + eps), the sum over the activation
+            // waves in wave order
+            float ss = 0.f;
+#pragma unroll
+            for (int u = 0; u < XF; u++) {
+                const int c4 = lane + 64 * (wave + NXW * u);
+                if (dl && 4 * c4 < N) {
+                    xv[u].x += dv[u].x; xv[u].y += dv[u].y; xv[u].z += dv[u].z; xv[u].w += dv[u].w;
+                    if (xr && blockIdx.x == 0) ((float4*)xr)[c4] = xv[u];
+                }
+                ss = fmaf(xv[u].x, xv[u].x, ss);
+                ss = fmaf(xv[u].y, xv[u].y, ss);
+                ss = fmaf(xv[u].z, xv[u].z, ss);
+                ss = fmaf(xv[u].w, xv[u].w, ss);
+            }
+            ss = wave_sum(ss);
+            if (lane == 0) {
+                red_ss[wave] = ss;
+                lds_signal(&cnt[3]);
+            }
+            lds_wait(&cnt[3], NXW);
+            float tot = 0.f;
+            for (int w = 0; w < NXW; w++) tot += red_ss[w];
+            const float inv = 1.0f / sqrtf(tot / (float)N + eps);
+#pragma unroll
+            for (int u = 0; u < XF; u++) {
+                const uint2 h = hv[u];
+                xv[u].x = (xv[u].x * inv) * f16_to_f32((uint16_t)(h.x & 0xffff));
+                xv[u].y = (xv[u].y * inv) * f16_to_f32((uint16_t)(h.x >> 16));
+                xv[u].z = (xv[u].z * inv) * f16_to_f32((uint16_t)(h.y & 0xffff));
+                xv[u].w = (xv[u].w * inv) * f16_to_f32((uint16_t)(h.y >> 16));
+            }
         }
         float mx = 0.f;
 #pragma unroll
@@ -375,7 +433,8 @@ __global__ __launch_bounds__(1024) void gemv_tile_x(const RowSet rs, const float
             v -= (double)kBias * (double)sQ;
         }
         const float rsc = KIND == IBH_SCALE_F16 ? f16_to_f32((uint16_t)rsc_bits) : __builtin_bit_cast(float, rsc_bits);
-        y[row0 + lane] = (float)(v * ((double)xs * (1.0 / (16384.0 * TGeo<BITS>::kOpScale)))) * rsc;
+        const float yv = (float)(v * ((double)xs * (1.0 / (16384.0 * TGeo<BITS>::kOpScale)))) * rsc;
+        y[row0 + lane] = accy ? y[row0 + lane] + yv : yv;   // accy: a residual stream takes the product
         IBH_TT_END(row0 + lane);
     }
 }
@@ -410,7 +469,13 @@ extern "C" int ibh_set_tile_config(int mode, int KS, int WR, int delay) {
 // fp32 activations, int8 / int4 / int2 weights whose rows are whole 256-byte
 // steps, 1-3 matrices sharing x (one launch).  Returns 1 if launched, 0 if the
 // shape is not eligible (the caller then runs another kernel).
-int ibh_launch_tile_x_multi(const MatDesc* d, int n, int kind, const float* x, int N, int bits, hipStream_t st) {
+// accy: y += W x (the residual add of the layer folded into the epilogue).
+// nw (fp16, N values, 8-byte aligned): the activation is the rmsnorm of x
+// (plus dl when not null; block 0 then writes x + dl to xr) with weight nw,
+// formed by the activation wavefronts of every block.
+int ibh_launch_tile_x_multi(const MatDesc* d, int n, int kind, const float* x, int N, int bits, hipStream_t st,
+                            bool accy, const float* dl, const uint16_t* nw, float* xr, float eps) {
+    if (nw && (((uintptr_t)nw & 7) || (dl && (((uintptr_t)dl & 15) || !xr || ((uintptr_t)xr & 15))))) return 0;
     if ((bits != 8 && bits != 4 && bits != 2) || g_tile_mode < 0) return 0;
     const size_t rb = (size_t)N * bits / 8;
     if (N <= 0 || rb % 256 != 0 || ((uintptr_t)x & 15) || n < 1 || n > 3) return 0;
@@ -450,8 +515,9 @@ int ibh_launch_tile_x_multi(const MatDesc* d, int n, int kind, const float* x, i
     if (lds > 150 * 1024) return 0;
     const RowSet rs = make_rowset(d, n, 4 * WQ);
     const int blocks = rowset_blocks(d, n, 4 * WQ);
-#define IBH_TX(B_, K_, KS_) \
-    gemv_tile_x<B_, K_, KS_, 2><<<blocks, nthreads, lds, st>>>(rs, x, N, S, WQ, KW, nxw, delay)
+#define IBH_TX(B_, K_, KS_) do { \
+        if (nw) gemv_tile_x<B_, K_, KS_, 2, true><<<blocks, nthreads, lds, st>>>(rs, x, N, S, WQ, KW, nxw, delay, accy ? 1 : 0, dl, nw, xr, eps); \
+        else gemv_tile_x<B_, K_, KS_, 2, false><<<blocks, nthreads, lds, st>>>(rs, x, N, S, WQ, KW, nxw, delay, accy ? 1 : 0, dl, nw, xr, eps); } while (0)
 #define IBH_TXC(B_, K_) do { switch (KS) { case 4: IBH_TX(B_, K_, 4); break; case 7: IBH_TX(B_, K_, 7); break; \
                                            case 8: IBH_TX(B_, K_, 8); break; case 14: IBH_TX(B_, K_, 14); break; \
                                            default: IBH_TX(B_, K_, 16); break; } } while (0)
