@@ -592,7 +592,20 @@ __device__ __forceinline__ void piece_load(const uint8_t* p, uint4* r) {
     }
 }
 
-template <int BITS, int GRP, int HD>
+// The position's rotary embedding and cache write, done by the attention
+// launch itself (ROPE): k / v are the projections of position *dpos, q is
+// rotated into LDS only.  The rule is rope_kv_write_kernel<false>'s.
+struct SplitRope {
+    const float* k;
+    const float* v;
+    const float* table;   // (cos, sin) per (position, pair)
+    uint8_t* kd;          // the caches, written at *dpos
+    uint8_t* vd;
+    float* ks;
+    float* vs;
+};
+
+template <int BITS, int GRP, int HD, bool ROPE = false>
 __global__ __launch_bounds__(kSplitThreads) void attn_split(float* __restrict__ out, float* __restrict__ part,
                                                            const float* __restrict__ q,
                                                            const uint8_t* __restrict__ kd,
@@ -600,7 +613,7 @@ __global__ __launch_bounds__(kSplitThreads) void attn_split(float* __restrict__ 
                                                            const float* __restrict__ ks,
                                                            const float* __restrict__ vs, int T,
                                                            const int* __restrict__ dpos, int n_kv, float scale,
-                                                           int nstride) {
+                                                           int nstride, SplitRope rp) {
     constexpr int PB = SplitGeo<BITS>::PB;
     constexpr int NR = BITS == 32 ? 4 : 1;                // uint4 per piece register set
     constexpr int PIECES = HD / 16;
@@ -630,11 +643,92 @@ __global__ __launch_bounds__(kSplitThreads) void attn_split(float* __restrict__ 
     uint4 kr[NR], vr[NR];
     piece_load<BITS>(kd + (size_t)pos * row_bytes + (size_t)kh * RB + pc * PB, kr);
     piece_load<BITS>(vd + (size_t)pos * row_bytes + (size_t)kh * RB + pc * PB, vr);
-    const float ksc = BITS == 32 ? 1.f : ks[(size_t)pos * n_kv + kh];
-    const float vsv = BITS == 32 ? 1.f : vs[(size_t)pos * n_kv + kh];
-    for (int i = tid; i < GRP * HD / 4; i += kSplitThreads)
-        ((float4*)&qs[0][0])[i] = ((const float4*)(q + (size_t)kh * GRP * HD))[i];
-    __syncthreads();
+    float ksc = BITS == 32 ? 1.f : ks[(size_t)pos * n_kv + kh];
+    float vsv = BITS == 32 ? 1.f : vs[(size_t)pos * n_kv + kh];
+    if constexpr (ROPE) {
+        // q of the group rotated into LDS; the block holding position T - 1
+        // rotates k, quantizes the k and v rows of head kh into the caches
+        // (wavefront 0: k, 1: v; lane j: pair (2j, 2j+1)) and keeps them in LDS
+        __shared__ __align__(16) uint8_t nrow[2][RB];
+        __shared__ float nsc[2];
+        constexpr int HALF = HD / 2;
+        const int pcur = T - 1;
+        const float* tb = rp.table + (size_t)pcur * HALF * 2;
+        for (int i = tid; i < GRP * HALF; i += kSplitThreads) {
+            const int g = i / HALF, j = i - g * HALF;
+            const float* qh = q + (size_t)(kh * GRP + g) * HD;
+            const float x0 = qh[2 * j], x1 = qh[2 * j + 1], cc = tb[2 * j], sn = tb[2 * j + 1];
+            qs[g][2 * j] = x0 * cc - x1 * sn;
+            qs[g][2 * j + 1] = x0 * sn + x1 * cc;
+        }
+        if (c == nch - 1 && wave < 2) {
+            const int side = wave, j = lane;
+            const float* src = (side ? rp.v : rp.k) + (size_t)kh * HD;
+            float x0 = 0.f, x1 = 0.f;
+            if (j < HALF) {
+                x0 = src[2 * j];
+                x1 = src[2 * j + 1];
+                if (side == 0) {
+                    const float cc = tb[2 * j], sn = tb[2 * j + 1], a = x0, b = x1;
+                    x0 = a * cc - b * sn;
+                    x1 = a * sn + b * cc;
+                }
+            }
+            uint8_t* grow = (side ? rp.vd : rp.kd) + (size_t)pcur * row_bytes + (size_t)kh * RB;
+            if constexpr (BITS == 32) {
+                if (j < HALF) {
+                    ((float2*)grow)[j] = make_float2(x0, x1);
+                    ((float2*)nrow[side])[j] = make_float2(x0, x1);
+                }
+                if (lane == 0) nsc[side] = 1.f;
+            } else {
+                const float mx = wave_max(fmaxf(fabsf(x0), fabsf(x1)));
+                float sc = mx / (BITS == 8 ? 127.0f : 7.0f);
+                if (sc < 1e-8f) sc = 1e-8f;
+                const float inv = 1.0f / sc;
+                int q0 = (int)roundf(x0 * inv), q1 = (int)roundf(x1 * inv);
+                if (j < HALF) {
+                    if constexpr (BITS == 8) {
+                        q0 = q0 < -127 ? -127 : (q0 > 127 ? 127 : q0);
+                        q1 = q1 < -127 ? -127 : (q1 > 127 ? 127 : q1);
+                        const uint16_t b2 = (uint16_t)((q0 & 0xff) | ((q1 & 0xff) << 8));
+                        ((uint16_t*)grow)[j] = b2;
+                        ((uint16_t*)nrow[side])[j] = b2;
+                    } else {
+                        q0 = q0 < -7 ? -7 : (q0 > 7 ? 7 : q0);
+                        q1 = q1 < -7 ? -7 : (q1 > 7 ? 7 : q1);
+                        const uint8_t b1 = (uint8_t)(((q0 + 8) & 0xf) | (((q1 + 8) & 0xf) << 4));
+                        grow[j] = b1;
+                        nrow[side][j] = b1;
+                    }
+                }
+                if (lane == 0) {
+                    (side ? rp.vs : rp.ks)[(size_t)pcur * n_kv + kh] = sc;
+                    nsc[side] = sc;
+                }
+            }
+        }
+        __syncthreads();
+        if (c == nch - 1 && pos == pcur) {   // the pieces of position T - 1, as just written
+            if constexpr (BITS == 4) {
+                const uint2 a = *(const uint2*)&nrow[0][pc * PB], b = *(const uint2*)&nrow[1][pc * PB];
+                kr[0] = make_uint4(a.x, a.y, 0u, 0u);
+                vr[0] = make_uint4(b.x, b.y, 0u, 0u);
+            } else {
+#pragma unroll
+                for (int j = 0; j < NR; j++) {
+                    kr[j] = ((const uint4*)&nrow[0][pc * PB])[j];
+                    vr[j] = ((const uint4*)&nrow[1][pc * PB])[j];
+                }
+            }
+            ksc = nsc[0];
+            vsv = nsc[1];
+        }
+    } else {
+        for (int i = tid; i < GRP * HD / 4; i += kSplitThreads)
+            ((float4*)&qs[0][0])[i] = ((const float4*)(q + (size_t)kh * GRP * HD))[i];
+        __syncthreads();
+    }
 
     // 2. scores: the piece's dot with each head, summed over the position's lanes
     float kv[16];
@@ -782,6 +876,47 @@ __global__ __launch_bounds__(1024) void attn_merge_wide(float* __restrict__ out,
 
 static int g_attn_split = 1;
 
+namespace {
+
+// The one-launch split attention + merge where the shape allows it (1 if
+// launched).  rope: the position's rotary embedding and cache write done by
+// the same launch (dpos required).
+int launch_split(float* out, float* part, const float* q, const void* kdata, const void* vdata,
+                 const float* kscales, const float* vscales, int T, const int* dpos, int max_pos, int n_heads,
+                 int n_kv, int head_dim, int kv_bits, float scale, const SplitRope* rope, hipStream_t st) {
+    const int grp = n_heads / n_kv;
+    if (!(g_attn_split && (kv_bits == 32 || kv_bits == 8 || kv_bits == 4) && (head_dim == 64 || head_dim == 128) &&
+          (grp == 1 || grp == 2 || grp == 4 || grp == 8) && n_kv <= kSplitMaxKv))
+        return 0;
+    if (rope && !dpos) return 0;
+    const int ct = kSplitThreads / (head_dim / 16);
+    const int nstride = (max_pos + 1 + ct - 1) / ct;
+    if (nstride > kSplitMaxChunks) return 0;
+    const uint8_t* K = (const uint8_t*)kdata;
+    const uint8_t* V = (const uint8_t*)vdata;
+    const SplitRope rp = rope ? *rope : SplitRope{};
+#define IBH_AS(B_, G_, H_) do { \
+        if (rope) attn_split<B_, G_, H_, true><<<dim3(n_kv, nstride), kSplitThreads, 0, st>>>( \
+                      out, part, q, K, V, kscales, vscales, T, dpos, n_kv, scale, nstride, rp); \
+        else attn_split<B_, G_, H_, false><<<dim3(n_kv, nstride), kSplitThreads, 0, st>>>( \
+                 out, part, q, K, V, kscales, vscales, T, dpos, n_kv, scale, nstride, rp); \
+        IBH_CHECK_LAUNCH("ibh_attn_decode (split)"); \
+        attn_merge_wide<H_><<<n_heads, 1024, 0, st>>>(out, part, T, dpos, ct, nstride); } while (0)
+#define IBH_ASG(B_, H_) do { if (grp == 1) IBH_AS(B_, 1, H_); else if (grp == 2) IBH_AS(B_, 2, H_); \
+                         else if (grp == 4) IBH_AS(B_, 4, H_); else IBH_AS(B_, 8, H_); } while (0)
+#define IBH_ASH(B_) do { if (head_dim == 64) IBH_ASG(B_, 64); else IBH_ASG(B_, 128); } while (0)
+    if (kv_bits == 32) IBH_ASH(32);
+    else if (kv_bits == 8) IBH_ASH(8);
+    else IBH_ASH(4);
+#undef IBH_AS
+#undef IBH_ASG
+#undef IBH_ASH
+    IBH_CHECK_LAUNCH("ibh_attn_decode (split)");
+    return 1;
+}
+
+}  // namespace
+
 // Development switch (no counterpart in the reference): 0 sends decode
 // attention through the chunk + merge kernels, 1 (default) lets eligible
 // shapes run in one launch.
@@ -824,31 +959,9 @@ int ibh_launch_attn(float* out, const float* q, const void* kdata, const void* v
     const float scale = 1.0f / sqrtf((float)head_dim);
     float* part = (float*)ws;
     const int grp = n_heads / n_kv;
-    if (g_attn_split && (kv_bits == 32 || kv_bits == 8 || kv_bits == 4) && (head_dim == 64 || head_dim == 128) &&
-        (grp == 1 || grp == 2 || grp == 4 || grp == 8) && n_kv <= kSplitMaxKv) {
-        const int ct = kSplitThreads / (head_dim / 16);
-        const int nstride = (max_pos + 1 + ct - 1) / ct;
-        if (nstride <= kSplitMaxChunks) {
-            const uint8_t* K = (const uint8_t*)kdata;
-            const uint8_t* V = (const uint8_t*)vdata;
-#define IBH_AS(B_, G_, H_) do { \
-                attn_split<B_, G_, H_><<<dim3(n_kv, nstride), kSplitThreads, 0, st>>>( \
-                    out, part, q, K, V, kscales, vscales, T, dpos, n_kv, scale, nstride); \
-                IBH_CHECK_LAUNCH("ibh_attn_decode (split)"); \
-                attn_merge_wide<H_><<<n_heads, 1024, 0, st>>>(out, part, T, dpos, ct, nstride); } while (0)
-#define IBH_ASG(B_, H_) do { if (grp == 1) IBH_AS(B_, 1, H_); else if (grp == 2) IBH_AS(B_, 2, H_); \
-                             else if (grp == 4) IBH_AS(B_, 4, H_); else IBH_AS(B_, 8, H_); } while (0)
-#define IBH_ASH(B_) do { if (head_dim == 64) IBH_ASG(B_, 64); else IBH_ASG(B_, 128); } while (0)
-            if (kv_bits == 32) IBH_ASH(32);
-            else if (kv_bits == 8) IBH_ASH(8);
-            else IBH_ASH(4);
-#undef IBH_AS
-#undef IBH_ASG
-#undef IBH_ASH
-            IBH_CHECK_LAUNCH("ibh_attn_decode (split)");
-            return IBH_OK;
-        }
-    }
+    if (launch_split(out, part, q, kdata, vdata, kscales, vscales, T, dpos, max_pos, n_heads, n_kv, head_dim,
+                     kv_bits, scale, nullptr, st))
+        return IBH_OK;
     if (head_dim == 64 || head_dim == 128 || head_dim == 256) {
         const uint8_t* K = (const uint8_t*)kdata;
         const uint8_t* V = (const uint8_t*)vdata;
@@ -888,6 +1001,23 @@ generic:
     attn_combine<<<n_heads, 256, 0, st>>>(out, part, T, dpos, n_heads, head_dim, nchunks);
     IBH_CHECK_LAUNCH("ibh_attn_decode (combine)");
     return IBH_OK;
+}
+
+// Decode attention at position *dpos with that position's rotary embedding
+// and cache write (the non-exact rule of ibh_launch_rope_kv_write) done by
+// the split attention launch itself.  Returns 1 if launched, 0 if the shape
+// is not eligible (the caller runs ibh_launch_rope_kv_write, then
+// ibh_launch_attn), < 0 on an error.
+int ibh_launch_attn_rope(float* out, const float* q, const float* k, const float* v, const float* table, void* kdata,
+                         void* vdata, float* kscales, float* vscales, const int* dpos, int max_pos, int n_heads,
+                         int n_kv, int head_dim, int kv_bits, void* ws, size_t ws_bytes, hipStream_t st) {
+    if (!out || !q || !k || !v || !table || !kdata || !vdata || !dpos || n_heads <= 0 || n_kv <= 0 ||
+        n_heads % n_kv || max_pos < 0 || (kv_bits < 16 && (!kscales || !vscales)))
+        return 0;
+    if (!ws || ws_bytes < ibh_attn_workspace_bytes(n_heads, head_dim, max_pos + 1)) return 0;
+    const SplitRope rp{k, v, table, (uint8_t*)kdata, (uint8_t*)vdata, kscales, vscales};
+    return launch_split(out, (float*)ws, q, kdata, vdata, kscales, vscales, 1, dpos, max_pos, n_heads, n_kv, head_dim,
+                        kv_bits, 1.0f / sqrtf((float)head_dim), &rp, st);
 }
 
 // Rotary embedding of q and k at position *dpos plus the cache write of the

@@ -53,6 +53,9 @@ int ibh_launch_silu_quant(float* out, const float* gate, const float* up, const 
                           int N, bool exact, hipStream_t st);
 int ibh_launch_rows_w4a8_multi(const MatDesc* d, int n, int kind, const int8_t* qx, const float* sa, int N,
                                hipStream_t st);
+int ibh_launch_attn_rope(float* out, const float* q, const float* k, const float* v, const float* table, void* kdata,
+                         void* vdata, float* kscales, float* vscales, const int* dpos, int max_pos, int n_heads,
+                         int n_kv, int head_dim, int kv_bits, void* ws, size_t ws_bytes, hipStream_t st);
 int ibh_launch_rows_w4a8_norm_multi(const MatDesc* d, int n, int kind, const float* x, const float* dl,
                                     const uint16_t* w_norm, float* xr, float eps, int N, hipStream_t st,
                                     bool accy);
@@ -520,11 +523,16 @@ int step(ibh_model* m) {
             IBH_CHECK_LAUNCH("ibh_model: rmsnorm");
             if ((rc = qkv(m, L, false))) return rc;
         }
-        if ((rc = ibh_launch_rope_kv_write(L.kd, L.vd, L.ks, L.vs, m->q, m->k, m->v, m->rope, m->dpos(), m->n_heads,
-                                           m->n_kv, m->head_dim, m->kv_bits, false, m->st)))
-            return rc;
-        if ((rc = ibh_launch_attn(m->xb2, m->q, L.kd, L.vd, L.ks, L.vs, 0, m->dpos(), m->max_pos, m->n_heads,
-                                  m->n_kv, m->head_dim, m->kv_bits, m->attn_ws, m->attn_ws_bytes, m->st)))
+        // rope + cache write inside the attention launch where it allows
+        f = m->no_norm_fuse ? 0
+                            : ibh_launch_attn_rope(m->xb2, m->q, m->k, m->v, m->rope, L.kd, L.vd, L.ks, L.vs,
+                                                   m->dpos(), m->max_pos, m->n_heads, m->n_kv, m->head_dim,
+                                                   m->kv_bits, m->attn_ws, m->attn_ws_bytes, m->st);
+        if (f < 0) return f;
+        if (!f && ((rc = ibh_launch_rope_kv_write(L.kd, L.vd, L.ks, L.vs, m->q, m->k, m->v, m->rope, m->dpos(),
+                                                  m->n_heads, m->n_kv, m->head_dim, m->kv_bits, false, m->st)) ||
+                   (rc = ibh_launch_attn(m->xb2, m->q, L.kd, L.vd, L.ks, L.vs, 0, m->dpos(), m->max_pos, m->n_heads,
+                                         m->n_kv, m->head_dim, m->kv_bits, m->attn_ws, m->attn_ws_bytes, m->st))))
             return rc;
         if (!m->no_norm_fuse && o_acc(m, L, xc)) {
             dl = nullptr;
