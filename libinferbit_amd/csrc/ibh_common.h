@@ -54,6 +54,31 @@ __device__ __forceinline__ float wave_max(float v) {
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
     return v;
 }
+// One rmsnorm chain of the x86 order: acc = fmaf(c[k], c[k], acc) for
+// k = 0 .. N8-1 in order (c in LDS, 16-byte aligned, N8 % 4 == 0), the
+// reads kept 32 elements ahead of the dependent fused adds.
+template <int N8>
+__device__ __forceinline__ float chain_sumsq(const float* c) {
+    static_assert(N8 % 32 == 0, "chain length");
+    float acc = 0.f;
+    float4 cur[8], nxt[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) cur[u] = *(const float4*)(c + 4 * u);
+    for (int k = 0; k < N8; k += 32) {
+        const int kn = k + 32 < N8 ? k + 32 : k;
+#pragma unroll
+        for (int u = 0; u < 8; u++) nxt[u] = *(const float4*)(c + kn + 4 * u);
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            acc = fmaf(cur[u].x, cur[u].x, acc); acc = fmaf(cur[u].y, cur[u].y, acc);
+            acc = fmaf(cur[u].z, cur[u].z, acc); acc = fmaf(cur[u].w, cur[u].w, acc);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) cur[u] = nxt[u];
+    }
+    return acc;
+}
+
 __device__ __forceinline__ int wave_isum(int v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);

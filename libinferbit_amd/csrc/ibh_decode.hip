@@ -58,15 +58,17 @@ int ibh_launch_attn_rope(float* out, const float* q, const float* k, const float
                          int n_kv, int head_dim, int kv_bits, void* ws, size_t ws_bytes, hipStream_t st);
 int ibh_launch_rows_w4a8_norm_multi(const MatDesc* d, int n, int kind, const float* x, const float* dl,
                                     const uint16_t* w_norm, float* xr, float eps, int N, hipStream_t st,
-                                    bool accy);
+                                    bool accy, bool xord = false);
 int ibh_launch_rows_w4a8(float* out, const void* w, const void* sw, int kind, const int8_t* qx, const float* sa,
                          int M, int N, hipStream_t st, bool accy);
 int ibh_launch_tile_x_multi(const MatDesc* d, int n, int kind, const float* x, int N, int bits, hipStream_t st,
                             bool accy, const float* dl, const uint16_t* nw, float* xr, float eps);
 int ibh_launch_rows_x_multi(const MatDesc* d, int n, int kind, const float* x, int N, int bits, hipStream_t st);
 int ibh_launch_matvec_exact_multi(const MatDesc* d, int n, int kind, const float* x, int N, int bits,
-                                  hipStream_t st);
+                                  hipStream_t st, const float* dl = nullptr, const uint16_t* nw = nullptr,
+                                  float* xr = nullptr, float eps = 0.f);
 size_t ibh_attn_exact_scratch(int n_heads, int max_pos);
+size_t ibh_exact_matvec_lds(int N, bool norm);
 int ibh_launch_int8_batch_exact(float* y, const void* w, const void* sc, int kind, const float* x, int M, int N,
                                 int B, int M_stride, hipStream_t st);
 int ibh_launch_attn_exact(float* out, const float* q, const void* kdata, const void* vdata, const float* ks,
@@ -471,27 +473,96 @@ int norm_fused(ibh_model* m, const DLayer& L, bool qkv, float*& xc, float*& xa, 
     return 1;
 }
 
+// Exact mode: rmsnorm (x86 order) fused into the q/k/v launch (INT8 x86-order
+// matvec, or W4A8 with the norm and quantizer in its prologue), or into the
+// gate/up launch.  With a pending delta dl the residual add runs in the same
+// launch and the stream moves from *xc to *xa (swapped on return).  Returns 1
+// if launched, 0 if the layer's tensors do not allow it.
+int norm_fused_exact(ibh_model* m, const DLayer& L, bool qkv, float*& xc, float*& xa, const float* dl) {
+    if (m->no_norm_fuse) return 0;
+    const int H = m->hidden, KV = m->n_kv * m->head_dim, I = m->inter;
+    int n, kind, bits;
+    MatDesc d[3];
+    if (qkv) {
+        if (L.q.bits != L.k.bits || L.k.bits != L.v.bits || L.q.skind != L.k.skind || L.k.skind != L.v.skind)
+            return 0;
+        d[0] = {m->q, L.q.w, L.q.s, H};
+        d[1] = {m->k, L.k.w, L.k.s, KV};
+        d[2] = {m->v, L.v.w, L.v.s, KV};
+        n = 3;
+        kind = L.q.skind;
+        bits = L.q.bits;
+    } else {
+        if (L.gate.bits != L.up.bits || L.gate.skind != L.up.skind || (L.mask && L.mask_sparse)) return 0;
+        d[0] = {m->hb, L.gate.w, L.gate.s, I};
+        d[1] = {m->hb2, L.up.w, L.up.s, I};
+        n = 2;
+        kind = L.gate.skind;
+        bits = L.gate.bits;
+    }
+    const uint16_t* nw = qkv ? L.in_norm : L.post_norm;
+    float* xr = dl ? xa : nullptr;
+    if (bits == 4 && m->w4a8) {
+        if (!ibh_launch_rows_w4a8_norm_multi(d, n, kind, xc, dl, nw, xr, m->eps, H, m->st, false, true)) return 0;
+    } else if (bits == 8 && H % 256 == 0 && ibh_exact_matvec_lds(H, true) <= 64 * 1024) {
+        int rc = ibh_launch_matvec_exact_multi(d, n, kind, xc, H, 8, m->st, dl, nw, xr, m->eps);
+        if (rc) return rc;
+    } else {
+        return 0;
+    }
+    IBH_CHECK_LAUNCH(qkv ? "ibh_model: exact norm + qkv" : "ibh_model: exact norm + gate/up");
+    if (dl) std::swap(xc, xa);
+    return 1;
+}
+
 // forward_single_ex(compute_logits=1) + greedy pick, bit-identical to the CPU.
+// The residual adds run inside the launches that produce or consume the
+// delta where the kernels allow (same operands, same single fp32 add).
 int step_exact(ibh_model* m) {
-    const int H = m->hidden, kv_dim = m->n_kv * m->head_dim;
+    const int H = m->hidden;
     int rc;
     embed_kernel<<<(H + 255) / 256, 256, 0, m->st>>>(m->x, m->emb.w, (const uint16_t*)(m->emb.skind == IBH_SCALE_F16 ? m->emb.s : nullptr),
                                                      m->emb.bits, H, m->dtokens(), m->dpos());
     IBH_CHECK_LAUNCH("ibh_model: embedding");
+    float *xc = m->x, *xa = m->xalt;
+    const float* dl = nullptr;
     for (int l = 0; l < m->n_layers; l++) {
         DLayer& L = m->layers[l];
-        if ((rc = ibh_launch_rmsnorm_exact(m->xb, m->x, l ? m->xb : nullptr, L.in_norm, m->eps, H, m->st)) ||
-            (rc = qkv(m, L, true)) ||
-            (rc = ibh_launch_rope_kv_write(L.kd, L.vd, L.ks, L.vs, m->q, m->k, m->v, m->rope, m->dpos(),
+        int f = norm_fused_exact(m, L, true, xc, xa, dl);
+        if (f < 0) return f;
+        if (!f && ((rc = ibh_launch_rmsnorm_exact(m->xb, xc, dl, L.in_norm, m->eps, H, m->st)) ||
+                   (rc = qkv(m, L, true))))
+            return rc;
+        if ((rc = ibh_launch_rope_kv_write(L.kd, L.vd, L.ks, L.vs, m->q, m->k, m->v, m->rope, m->dpos(),
                                            m->n_heads, m->n_kv, m->head_dim, m->kv_bits, true, m->st)) ||
             (rc = ibh_launch_attn_exact(m->xb2, m->q, L.kd, L.vd, L.ks, L.vs, m->dpos(), m->max_pos, m->n_heads,
-                                        m->n_kv, m->head_dim, m->kv_bits, m->att, m->st)) ||
-            (rc = mm_exact(m, L.o, m->xb, m->xb2, H, H, nullptr, false)) ||
-            (rc = ibh_launch_rmsnorm_exact(m->xb2, m->x, m->xb, L.post_norm, m->eps, H, m->st)) ||
-            (rc = mlp(m, L, true)))
+                                        m->n_kv, m->head_dim, m->kv_bits, m->att, m->st)))
             return rc;
+        // o: W4A8 with the activation quantized in the prologue and the
+        // product added into the residual stream in the epilogue
+        const MatDesc od{xc, L.o.w, L.o.s, H};
+        if (!m->no_norm_fuse && L.o.bits == 4 && m->w4a8 &&
+            ibh_launch_rows_w4a8_norm_multi(&od, 1, L.o.skind, m->xb2, nullptr, nullptr, nullptr, 0.f, H, m->st,
+                                            true)) {
+            IBH_CHECK_LAUNCH("ibh_model: exact o + residual");
+            dl = nullptr;
+        } else {
+            if ((rc = mm_exact(m, L.o, m->xb, m->xb2, H, H, nullptr, false))) return rc;
+            dl = m->xb;
+        }
+        if ((f = norm_fused_exact(m, L, false, xc, xa, dl)) < 0) return f;
+        if (!f) {
+            if ((rc = ibh_launch_rmsnorm_exact(m->xb2, xc, dl, L.post_norm, m->eps, H, m->st)) ||
+                (rc = mlp(m, L, true)))
+                return rc;
+            dl = m->xb;
+        } else {
+            bool acc = false;
+            if ((rc = mlp_down(m, L, true, m->no_norm_fuse ? nullptr : xc, &acc))) return rc;
+            dl = acc ? nullptr : m->xb;
+        }
     }
-    if ((rc = ibh_launch_rmsnorm_exact(m->x, m->x, m->xb, m->out_norm, m->eps, H, m->st)) ||
+    if ((rc = ibh_launch_rmsnorm_exact(m->x, xc, dl, m->out_norm, m->eps, H, m->st)) ||
         (rc = mm_exact(m, m->head, m->logits, m->x, m->vocab, H, nullptr, false)))
         return rc;
     argmax_advance_kernel<<<1, 1024, 0, m->st>>>(m->logits, m->vocab, m->dtokens(), m->dpos(), m->dprompt_end());

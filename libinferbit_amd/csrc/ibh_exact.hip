@@ -117,9 +117,16 @@ __global__ __launch_bounds__(256) void rmsnorm_exact(float* out, float* x, const
 // 4 rows; lane (r, c) of a wavefront runs chain c of row r.  Per tile of 256
 // columns each lane loads the 16 weights of block c (one 16-column block)
 // into a per-wavefront LDS tile as int8, then reads back column c of the 16
-// blocks; x is staged in LDS once per block.
-template <int BITS, int KIND, bool ALIGNED>
-__global__ __launch_bounds__(256) void matvec_exact(const RowSet rs, const float* __restrict__ x, int N) {
+// blocks; x is staged in LDS once per block.  The first 16 tiles' weight
+// loads are issued before x is read.
+//
+// NORM 1: x is first put through the x86 rmsnorm (rmsnorm_exact's
+// arithmetic, every block computing it); NORM 2: the residual add x + dl
+// before it, block 0 writing the sum to xr (the next residual stream).
+template <int BITS, int KIND, bool ALIGNED, int NORM = 0>
+__global__ __launch_bounds__(256) void matvec_exact(const RowSet rs, const float* __restrict__ x, int N,
+                                                    const float* __restrict__ dl, const uint16_t* __restrict__ nw,
+                                                    float* __restrict__ xr, float eps) {
     const RowPick P = pick_rows(rs);
     const uint8_t* __restrict__ W = P.W;
     const void* __restrict__ sc = P.sc;
@@ -128,19 +135,8 @@ __global__ __launch_bounds__(256) void matvec_exact(const RowSet rs, const float
     extern __shared__ __align__(16) unsigned char smem[];
     float* xs = (float*)smem;                                         // [N]
     int8_t* tile = (int8_t*)(smem + (((size_t)N * 4 + 15) & ~(size_t)15));   // [4 waves][4 rows][256]
-    {
-        constexpr int NQ = 16;                                        // N <= 16384
-        const int n4 = N >> 2;
-        float4 v[NQ];
-#pragma unroll
-        for (int u = 0; u < NQ; u++) v[u] = n4 > 0 ? ((const float4*)x)[max(min((int)threadIdx.x + 256 * u, n4 - 1), 0)]
-                                                   : float4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int u = 0; u < NQ; u++)
-            if ((int)threadIdx.x + 256 * u < n4) ((float4*)xs)[threadIdx.x + 256 * u] = v[u];
-        for (int i = 4 * n4 + (int)threadIdx.x; i < N; i += 256) xs[i] = x[i];
-    }
-    __syncthreads();
+    float* xt = (float*)(tile + 4 * 4 * 256);                         // NORM: [8][N/8] chain-major
+    __shared__ float part[8];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane >> 4, c = lane & 15;
     const int row = (P.bid * 4 + wave) * 4 + r;
@@ -150,12 +146,11 @@ __global__ __launch_bounds__(256) void matvec_exact(const RowSet rs, const float
     int8_t* mytile = tile + (size_t)(wave * 4 + r) * 256;
     const int nb = N / 16;                                            // whole 16-column blocks
     const int nt = (nb + 15) / 16;                                    // tiles of 16 blocks
-    float acc = 0.f;
-    for (int g0 = 0; g0 < nt; g0 += 16) {
-        // all of this group's weight loads first (one 16-column block per tile)
-        // (a native vector array and no early exit from the unrolled loop
-        // below keep buf in registers: all 16 loads are in flight together)
-        u32x4_t buf[16];
+    // all of a group's weight loads at once (one 16-column block per tile)
+    // (a native vector array and no early exit from the unrolled loops keep
+    // buf in registers: all 16 loads are in flight together)
+    u32x4_t buf[16];
+    auto issue = [&](int g0) {
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             const int b = min(16 * (g0 + k) + c, nb - 1);             // clamped: unused blocks are never read
@@ -180,6 +175,82 @@ __global__ __launch_bounds__(256) void matvec_exact(const RowSet rs, const float
                 }
             }
         }
+    };
+    issue(0);
+    {
+        constexpr int NQ = 16;                                        // N <= 16384
+        const int n4 = N >> 2;
+        float4 v[NQ];
+#pragma unroll
+        for (int u = 0; u < NQ; u++) {
+            const int i4 = (int)threadIdx.x + 256 * u;
+            v[u] = i4 < n4 ? ((const float4*)x)[i4] : float4{0.f, 0.f, 0.f, 0.f};
+            if constexpr (NORM == 2) {
+                if (i4 < n4) {
+                    const float4 d = ((const float4*)dl)[i4];
+                    v[u].x = v[u].x + d.x; v[u].y = v[u].y + d.y; v[u].z = v[u].z + d.z; v[u].w = v[u].w + d.w;
+                }
+            }
+        }
+        if constexpr (NORM) {
+            // N % 256 == 0 (checked by the launcher): no tail
+            const int n8 = N >> 3;
+#pragma unroll
+            for (int u = 0; u < NQ; u++) {
+                const int i4 = (int)threadIdx.x + 256 * u;
+                if (i4 < n4) {
+                    const int i = 4 * i4;
+                    xt[((i + 0) & 7) * n8 + ((i + 0) >> 3)] = v[u].x;
+                    xt[((i + 1) & 7) * n8 + ((i + 1) >> 3)] = v[u].y;
+                    xt[((i + 2) & 7) * n8 + ((i + 2) >> 3)] = v[u].z;
+                    xt[((i + 3) & 7) * n8 + ((i + 3) >> 3)] = v[u].w;
+                    if (NORM == 2 && blockIdx.x == 0) ((float4*)xr)[i4] = v[u];
+                }
+            }
+            __syncthreads();
+            if (threadIdx.x < 8) {
+                const float* ch = xt + threadIdx.x * n8;
+                float acc = 0.f;
+                for (int k = 0; k < n8; k += 32) {                    // n8 % 32 == 0
+                    float4 q[8];
+#pragma unroll
+                    for (int e = 0; e < 8; e++) q[e] = *(const float4*)(ch + k + 4 * e);
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        acc = fmaf(q[e].x, q[e].x, acc); acc = fmaf(q[e].y, q[e].y, acc);
+                        acc = fmaf(q[e].z, q[e].z, acc); acc = fmaf(q[e].w, q[e].w, acc);
+                    }
+                }
+                part[threadIdx.x] = acc;
+            }
+            __syncthreads();
+            const float q0 = part[0] + part[4], q1 = part[1] + part[5], q2 = part[2] + part[6], q3 = part[3] + part[7];
+            const float ss = (q0 + q1) + (q2 + q3);
+            const float scale = 1.0f / sqrtf(ss / (float)N + eps);
+#pragma unroll
+            for (int u = 0; u < NQ; u++) {
+                const int i4 = (int)threadIdx.x + 256 * u;
+                if (i4 < n4) {
+                    const uint2 wq = ((const uint2*)nw)[i4];
+                    float4 o;
+                    o.x = (v[u].x * scale) * f16_to_f32((uint16_t)(wq.x & 0xffff));
+                    o.y = (v[u].y * scale) * f16_to_f32((uint16_t)(wq.x >> 16));
+                    o.z = (v[u].z * scale) * f16_to_f32((uint16_t)(wq.y & 0xffff));
+                    o.w = (v[u].w * scale) * f16_to_f32((uint16_t)(wq.y >> 16));
+                    ((float4*)xs)[i4] = o;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < NQ; u++)
+                if ((int)threadIdx.x + 256 * u < n4) ((float4*)xs)[threadIdx.x + 256 * u] = v[u];
+            for (int i = 4 * n4 + (int)threadIdx.x; i < N; i += 256) xs[i] = x[i];
+        }
+    }
+    __syncthreads();
+    float acc = 0.f;
+    for (int g0 = 0; g0 < nt; g0 += 16) {
+        if (g0) issue(g0);
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             const int tile = g0 + k;
@@ -484,15 +555,21 @@ __global__ __launch_bounds__(64) void attn_scores_exact(float* __restrict__ att,
     const int T = *dpos + 1;
     const int t = blockIdx.y * 64 + threadIdx.x;
     if ((int)blockIdx.y * 64 >= T) return;
+    const int kh = h / (n_heads / n_kv);
+    const int tc = min(t, T - 1);
+    // the first 128 columns of the key row are loaded before q is staged
+    float kv[8][16];
+#pragma unroll
+    for (int u = 0; u < 8; u++) kv_row16<BITS>(kv[u], kd, ks, tc, kh, min(16 * u, hd - 16), hd, n_kv);
     for (int d = threadIdx.x; d < hd; d += 64) qs[d] = q[(size_t)h * hd + d];
     __syncthreads();
     if (t >= T) return;
-    const int kh = h / (n_heads / n_kv);
     float score = 0.f;
     for (int c0 = 0; c0 < hd; c0 += 128) {                 // up to 8 chunks of 16 loaded at once
-        float kv[8][16];
+        if (c0) {
 #pragma unroll
-        for (int u = 0; u < 8; u++) kv_row16<BITS>(kv[u], kd, ks, t, kh, min(c0 + 16 * u, hd - 16), hd, n_kv);
+            for (int u = 0; u < 8; u++) kv_row16<BITS>(kv[u], kd, ks, t, kh, min(c0 + 16 * u, hd - 16), hd, n_kv);
+        }
 #pragma unroll
         for (int u = 0; u < 8; u++) {
             if (c0 + 16 * u >= hd) break;
@@ -728,9 +805,12 @@ int ibh_launch_rmsnorm_exact(float* out, float* x, const float* delta, const uin
 }
 
 int ibh_launch_matvec_exact_multi(const MatDesc* d, int n, int kind, const float* x, int N, int bits,
-                                  hipStream_t st);
+                                  hipStream_t st, const float* dl = nullptr, const uint16_t* nw = nullptr,
+                                  float* xr = nullptr, float eps = 0.f);
 
-size_t ibh_exact_matvec_lds(int N) { return (((size_t)N * 4 + 15) & ~(size_t)15) + 4 * 4 * 256; }
+size_t ibh_exact_matvec_lds(int N, bool norm) {
+    return (((size_t)N * 4 + 15) & ~(size_t)15) + 4 * 4 * 256 + (norm ? (size_t)N * 4 : 0);
+}
 
 int ibh_launch_matvec_exact(float* y, const void* w, const void* sc, int kind, const float* x, int M, int N, int bits,
                             const uint8_t* mask, hipStream_t st) {
@@ -750,11 +830,18 @@ int ibh_launch_matvec_exact(float* y, const void* w, const void* sc, int kind, c
 }
 
 // 1-3 matrices with the same N, bits and scale kind sharing x, one launch.
+// With nw: x is first normed (and, with dl, x + dl is normed and written to
+// xr) by the rmsnorm_exact rule; N % 256 == 0 and 16-byte aligned vectors.
 int ibh_launch_matvec_exact_multi(const MatDesc* d, int n, int kind, const float* x, int N, int bits,
-                                  hipStream_t st) {
-    const size_t lds = ibh_exact_matvec_lds(N);
+                                  hipStream_t st, const float* dl, const uint16_t* nw, float* xr, float eps) {
+    const size_t lds = ibh_exact_matvec_lds(N, nw != nullptr);
     if ((bits != 8 && bits != 4) || lds > 64 * 1024 || (bits == 4 && N % 2) || n < 1 || n > 3) {
         ibh_set_error("exact matvec: bits=%d N=%d unsupported", bits, N);
+        return IBH_ERROR_PARAM;
+    }
+    if (nw && (N % 256 || ((uintptr_t)x & 15) || ((uintptr_t)nw & 7) || (dl && (!xr || ((uintptr_t)dl & 15) ||
+                                                                               ((uintptr_t)xr & 15))))) {
+        ibh_set_error("exact matvec: fused norm needs N %% 256 == 0 and aligned vectors (N=%d)", N);
         return IBH_ERROR_PARAM;
     }
     const size_t rb = (size_t)N * bits / 8;
@@ -764,7 +851,10 @@ int ibh_launch_matvec_exact_multi(const MatDesc* d, int n, int kind, const float
                               : (((uintptr_t)d[i].w & 7) == 0 && rb % 8 == 0));
     const RowSet rs = make_rowset(d, n, 16);
     const int blocks = rowset_blocks(d, n, 16);
-#define IBH_MX(B_, K_, A_) matvec_exact<B_, K_, A_><<<blocks, 256, lds, st>>>(rs, x, N)
+#define IBH_MX(B_, K_, A_) do { \
+        if (!nw) matvec_exact<B_, K_, A_, 0><<<blocks, 256, lds, st>>>(rs, x, N, nullptr, nullptr, nullptr, 0.f); \
+        else if (!dl) matvec_exact<B_, K_, A_, 1><<<blocks, 256, lds, st>>>(rs, x, N, nullptr, nw, nullptr, eps); \
+        else matvec_exact<B_, K_, A_, 2><<<blocks, 256, lds, st>>>(rs, x, N, dl, nw, xr, eps); } while (0)
 #define IBH_MXA(B_, K_) do { if (al) IBH_MX(B_, K_, true); else IBH_MX(B_, K_, false); } while (0)
     if (kind == IBH_SCALE_F16) { if (bits == 8) IBH_MXA(8, IBH_SCALE_F16); else IBH_MXA(4, IBH_SCALE_F16); }
     else { if (bits == 8) IBH_MXA(8, IBH_SCALE_F32); else IBH_MXA(4, IBH_SCALE_F32); }

@@ -234,8 +234,12 @@ __global__ __launch_bounds__(512) void gemv_rows_w4a8(float* __restrict__ y, con
 // contraction reads in place of qx / sa.  NORM 2: block 0 writes xin to
 // xr, the next residual stream.  x, dl and w_norm are loaded before the weights and
 // used after them are issued, so no wait for them waits on a weight load.
-// WPB: wavefronts per block (4 rows each).
-template <int KIND, int R, int GS, int NORM, int WPB = 4>
+// WPB: wavefronts per block (4 rows each).  XORD (NORM 1/2): ss in the
+// x86 order of rmsnorm (kernels/avx2.c:155-190): xin staged chain-major in
+// LDS, 8 lanes run the fma chains over i = l (mod 8) serially, folded as
+// ((s0 + s4) + (s1 + s5)) + ((s2 + s6) + (s3 + s7)); the normed vector and its
+// codes are then bit-identical to the x86 rmsnorm + quantizer.
+template <int KIND, int R, int GS, int NORM, int WPB = 4, bool XORD = false>
 __global__ __launch_bounds__(64 * WPB) void gemv_rows_w4a8_k(const RowSet rs, const int8_t* __restrict__ qx,
                                                         const float* __restrict__ sa, const float* __restrict__ x,
                                                         const float* __restrict__ dl, const uint16_t* __restrict__ nw,
@@ -247,7 +251,8 @@ __global__ __launch_bounds__(64 * WPB) void gemv_rows_w4a8_k(const RowSet rs, co
     __shared__ __align__(16) float gsum[WPB * R][GS];
     __shared__ __align__(16) int8_t qs[NORM ? N : 16];
     __shared__ __align__(16) float ss_s[NORM ? GS : 4];
-    __shared__ float red[WPB];
+    __shared__ float red[XORD ? 8 : WPB];
+    __shared__ __align__(16) float xts[XORD ? N : 4];
     const RowPick P = pick_rows(rs);
     const uint8_t* __restrict__ W = P.W;
     const void* __restrict__ sc = P.sc;
@@ -302,19 +307,34 @@ __global__ __launch_bounds__(64 * WPB) void gemv_rows_w4a8_k(const RowSet rs, co
         }
         float mx = 0.f;
         if constexpr (NORM != 3) {
-#pragma unroll
-            for (int e = 0; e < CPT; e++) ss = fmaf(v[e], v[e], ss);
-            ss = wave_sum(ss);
-            if (lane == 0) red[wave] = ss;
-            if (NORM == 2 && blockIdx.x == 0) {
-#pragma unroll
-                for (int q = 0; q < CPT / 4; q++)
-                    *(float4*)(xr + c0 + 4 * q) = float4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
-            }
-            __syncthreads();
             float tot = 0.f;
+            if constexpr (XORD) {
+                constexpr int N8 = N / 8;
 #pragma unroll
-            for (int w = 0; w < WPB; w++) tot += red[w];
+                for (int e = 0; e < CPT; e++) xts[((c0 + e) & 7) * N8 + ((c0 + e) >> 3)] = v[e];
+                if (NORM == 2 && blockIdx.x == 0) {
+#pragma unroll
+                    for (int q = 0; q < CPT / 4; q++)
+                        *(float4*)(xr + c0 + 4 * q) = float4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+                }
+                __syncthreads();
+                if (threadIdx.x < 8) red[threadIdx.x] = chain_sumsq<N8>(xts + threadIdx.x * N8);
+                __syncthreads();
+                tot = ((red[0] + red[4]) + (red[1] + red[5])) + ((red[2] + red[6]) + (red[3] + red[7]));
+            } else {
+#pragma unroll
+                for (int e = 0; e < CPT; e++) ss = fmaf(v[e], v[e], ss);
+                ss = wave_sum(ss);
+                if (lane == 0) red[wave] = ss;
+                if (NORM == 2 && blockIdx.x == 0) {
+#pragma unroll
+                    for (int q = 0; q < CPT / 4; q++)
+                        *(float4*)(xr + c0 + 4 * q) = float4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+                }
+                __syncthreads();
+#pragma unroll
+                for (int w = 0; w < WPB; w++) tot += red[w];
+            }
             const float scale = 1.0f / sqrtf(tot / (float)N + eps);
 #pragma unroll
             for (int e = 0; e < CPT; e++) {
@@ -915,7 +935,7 @@ int ibh_launch_rows_w4a8_multi(const MatDesc* d, int n, int kind, const int8_t* 
 // launched, 0 if not eligible.
 int ibh_launch_rows_w4a8_norm_multi(const MatDesc* d, int n, int kind, const float* x, const float* dl,
                                     const uint16_t* w_norm, float* xr, float eps, int N, hipStream_t st,
-                                    bool accy) {
+                                    bool accy, bool xord) {
     if ((N != 2048 && N != 4096) || n < 1 || n > 3 || !x || (dl && (!xr || !w_norm))) return 0;
     if (((uintptr_t)x & 15) || ((uintptr_t)dl & 15) || ((uintptr_t)w_norm & 15) || ((uintptr_t)xr & 15)) return 0;
     for (int i = 0; i < n; i++)
@@ -929,13 +949,15 @@ int ibh_launch_rows_w4a8_norm_multi(const MatDesc* d, int n, int kind, const flo
     const RowSet rs = make_rowset(d, n, wpb * R);
     const int blocks = rowset_blocks(d, n, wpb * R);
     const int ac = accy ? 1 : 0;
-#define IBH_RWK1(K_, G_, W_) do { \
+#define IBH_RWK2(K_, G_, W_, X_) do { \
         if (!w_norm) gemv_rows_w4a8_k<K_, R, G_, 3, W_><<<blocks, 64 * W_, 0, st>>>(rs, nullptr, nullptr, x, nullptr, nullptr, nullptr, 0.f, ac); \
-        else if (dl) gemv_rows_w4a8_k<K_, R, G_, 2, W_><<<blocks, 64 * W_, 0, st>>>(rs, nullptr, nullptr, x, dl, w_norm, xr, eps, ac); \
-        else gemv_rows_w4a8_k<K_, R, G_, 1, W_><<<blocks, 64 * W_, 0, st>>>(rs, nullptr, nullptr, x, nullptr, w_norm, nullptr, eps, ac); } while (0)
+        else if (dl) gemv_rows_w4a8_k<K_, R, G_, 2, W_, X_><<<blocks, 64 * W_, 0, st>>>(rs, nullptr, nullptr, x, dl, w_norm, xr, eps, ac); \
+        else gemv_rows_w4a8_k<K_, R, G_, 1, W_, X_><<<blocks, 64 * W_, 0, st>>>(rs, nullptr, nullptr, x, nullptr, w_norm, nullptr, eps, ac); } while (0)
+#define IBH_RWK1(K_, G_, W_) do { if (xord) IBH_RWK2(K_, G_, W_, true); else IBH_RWK2(K_, G_, W_, false); } while (0)
 #define IBH_RWK(K_, G_) do { if (wpb == 8) IBH_RWK1(K_, G_, 8); else IBH_RWK1(K_, G_, 4); } while (0)
     if (kind == IBH_SCALE_F16) { if (N == 4096) IBH_RWK(IBH_SCALE_F16, 32); else IBH_RWK1(IBH_SCALE_F16, 16, 4); }
     else { if (N == 4096) IBH_RWK(IBH_SCALE_F32, 32); else IBH_RWK1(IBH_SCALE_F32, 16, 4); }
+#undef IBH_RWK2
 #undef IBH_RWK1
 #undef IBH_RWK
     return 1;

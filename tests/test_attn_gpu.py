@@ -131,3 +131,4 @@ def test_attention_one_launch_matches_chunk_merge(ops, oracle_lib, bits, n_heads
     ref = oracle_lib.attn_decode(q.cpu().numpy(), cache, T - 1, n_heads, n_kv, hd, bits)
     assert np.abs(a - ref).max() / np.abs(ref).max() <= 1e-4
     assert np.abs(a - c).max() / np.abs(c).max() <= 1e-5
+
