@@ -590,9 +590,13 @@ __global__ __launch_bounds__(64) void attn_scores_exact(float* __restrict__ att,
 //  the first chunks are issued before the serial sum).  Every barrier after
 //  those loads orders LDS only, so the prefetched loads stay in flight.
 constexpr int kAoThreads = 512;                           // wave 0 consumer, waves 1-7 producers
-constexpr int kAoD = 64;                                  // d per block = consumer lanes
+constexpr int kAoD = 16;                                  // d per block = active consumer lanes (a narrow slice
+                                                          // halves each block's producer work: the producers,
+                                                          // not the consumer's add chain, set the pace at 64)
 constexpr int kAoProd = kAoThreads - 64;
-constexpr int kAoCH = 56;                                 // positions per chunk: 56*64/4 = 2 float4 per producer
+constexpr int kAoCH = 112;                                // positions per chunk: 112*64/4 = 4 float4 per producer
+constexpr int kAoH = kAoCH / 4;                           // the consumer reads a chunk in quarters (14 LDS reads:
+                                                          // within the 4-bit LDS wait counter)
 constexpr int kAoNG = kAoCH * kAoD / 4 / kAoProd;         // float4 groups per producer per chunk
 static_assert(kAoNG * kAoProd * 4 == kAoCH * kAoD, "chunk split");
 constexpr int kAoP = 4;                                   // chunks of V rows in flight per producer
@@ -605,6 +609,15 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_s_waitcnt(0xC07F);                   // lgkmcnt(0), vmcnt/expcnt untouched
     __builtin_amdgcn_s_barrier();
 }
+
+// Phase probes, compiled only with -DIBH_AO_TRACE (a development build
+// outside the library): s_memrealtime of thread 0 of each block.
+#ifdef IBH_AO_TRACE
+__device__ unsigned long long ibh_ao_tt[256][8];
+#define AO_TT(i) do { if (tid == 0 && blockIdx.x < 256) ibh_ao_tt[blockIdx.x][i] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#else
+#define AO_TT(i) ((void)0)
+#endif
 
 template <int BITS, int HD, int NB>
 __global__ __launch_bounds__(kAoThreads) void attn_out_exact(float* __restrict__ out, const float* __restrict__ att,
@@ -623,6 +636,7 @@ __global__ __launch_bounds__(kAoThreads) void attn_out_exact(float* __restrict__
     const int T = *dpos + 1;
     const int kh = h / (n_heads / n_kv);
     const float* a = att + (size_t)h * tstride;
+    AO_TT(0);
 
     // Scores to LDS: every load of the row is issued before any is used (the
     // scores were just written by another kernel and arrive from a far
@@ -643,6 +657,7 @@ __global__ __launch_bounds__(kAoThreads) void attn_out_exact(float* __restrict__
         }
     }
     __syncthreads();
+    AO_TT(1);
     float mx = -INFINITY;
     for (int t = tid; t < T; t += kAoThreads) mx = fmaxf(mx, es[t]);
     mx = wave_max(mx);
@@ -653,9 +668,10 @@ __global__ __launch_bounds__(kAoThreads) void attn_out_exact(float* __restrict__
     for (int w = 1; w < kAoThreads / 64; w++) m = fmaxf(m, red[w]);
     for (int t = tid; t < T; t += kAoThreads) es[t] = ib_expf(es[t] - m);
     __syncthreads();
+    AO_TT(2);
 
     // producer geometry: float4 f = u * kAoProd + pid of a chunk tile is row
-    // f / 16, columns 4 (f % 16) .. +3 of the slice
+    // f / (kAoD / 4), columns 4 (f % (kAoD / 4)) .. +3 of the slice
     const int nch = (T + kAoCH - 1) / kAoCH;
     const int nsteps = (nch + kAoP - 1) / kAoP * kAoP;    // barrier steps, the same for every wave
     const int pid = tid - 64;
@@ -663,8 +679,8 @@ __global__ __launch_bounds__(kAoThreads) void attn_out_exact(float* __restrict__
 #pragma unroll
     for (int u = 0; u < kAoNG; u++) {
         const int f = u * kAoProd + (pid < 0 ? 0 : pid);
-        gtt[u] = f >> 4;
-        gd[u] = d0 + 4 * (f & 15);
+        gtt[u] = f / (kAoD / 4);
+        gd[u] = d0 + 4 * (f % (kAoD / 4));
     }
     Kv4x4<BITS, kAoNG> ring[kAoP];
     auto fetch = [&](int k, Kv4x4<BITS, kAoNG>& r) {
@@ -691,84 +707,101 @@ __global__ __launch_bounds__(kAoThreads) void attn_out_exact(float* __restrict__
     if (tid == 0) {
         float sum = 0.f;
         int t = 0;
-        const int T32 = T & ~31;
-        float4 cur[8], nxt[8];
-        if (T32 > 0) {
+        const int T64 = T & ~63;
+        float4 cur[16], nxt[16];
+        if (T64 > 0) {
 #pragma unroll
-            for (int u = 0; u < 8; u++) cur[u] = *(const float4*)(es + 4 * u);
+            for (int u = 0; u < 16; u++) cur[u] = *(const float4*)(es + 4 * u);
         }
-        for (; t < T32; t += 32) {
-            const int tn = min(t + 32, T32 - 32);
+        for (; t < T64; t += 64) {
+            const int tn = min(t + 64, T64 - 64);
 #pragma unroll
-            for (int u = 0; u < 8; u++) nxt[u] = *(const float4*)(es + tn + 4 * u);
+            for (int u = 0; u < 16; u++) nxt[u] = *(const float4*)(es + tn + 4 * u);
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
+            for (int u = 0; u < 16; u++) {
                 sum = sum + cur[u].x; sum = sum + cur[u].y; sum = sum + cur[u].z; sum = sum + cur[u].w;
             }
 #pragma unroll
-            for (int u = 0; u < 8; u++) cur[u] = nxt[u];
+            for (int u = 0; u < 16; u++) cur[u] = nxt[u];
         }
         for (; t < T; t++) sum = sum + es[t];
         inv_s = 1.0f / sum;
     }
     lds_barrier();
+    AO_TT(3);
     const float inv = inv_s;
     for (int t = tid; t < T; t += kAoThreads) es[t] = es[t] * inv;
     lds_barrier();
+    AO_TT(4);
 
     if (wave == 0) {
-        // consumer: lane d of the slice; chunk k lives in buffer k % NB
+        // consumer: lane d of the slice; chunk k lives in buffer k % NB.  Its
+        // issue slots come first on the SIMD it shares with producers.
+        __builtin_amdgcn_s_setprio(3);
         float o = 0.f;
         lds_barrier();                                    // chunks 0 .. NB-2 produced
+        auto add_part = [&](int k) {                      // the last, partial chunk, from its buffer
+            const int tn = T - k * kAoCH;
+            const float* src = pbuf + (k % NB) * kAoTile + tid;
+            for (int e = 0; e < tn; e++) o = o + src[e * kAoD];
+        };
+        float va[kAoH], vb[kAoH];
+        auto rd = [&](int k, int half, float (&v)[kAoH]) {
+            const float* src = pbuf + (k % NB) * kAoTile + half * kAoH * kAoD + tid;
+#pragma unroll
+            for (int e = 0; e < kAoH; e++) v[e] = src[e * kAoD];   // immediate LDS offsets
+        };
+        auto add = [&](const float (&v)[kAoH]) {
+#pragma unroll
+            for (int e = 0; e < kAoH; e++) o = o + v[e];
+        };
         if constexpr (NB == 2) {
             for (int k = 0; k < nsteps; k++) {
                 if (k < nch) {
-                    const float* src = pbuf + (k & 1) * kAoTile + tid;
                     if (T - k * kAoCH >= kAoCH) {
-                        float v[kAoCH];
 #pragma unroll
-                        for (int e = 0; e < kAoCH; e++) v[e] = src[e * kAoD];   // immediate LDS offsets
-#pragma unroll
-                        for (int e = 0; e < kAoCH; e++) o = o + v[e];
+                        for (int q = 0; q < 4; q += 2) {
+                            rd(k, q, va);
+                            rd(k, q + 1, vb);
+                            add(va);
+                            add(vb);
+                        }
                     } else {
-                        const int tn = T - k * kAoCH;
-                        for (int e = 0; e < tn; e++) o = o + src[e * kAoD];
+                        add_part(k);
                     }
                 }
                 lds_barrier();
             }
         } else {
-            // chunk k+1 is read into registers while chunk k is added, so
-            // only the dependent adds are on this wave's path
-            float va[kAoCH], vb[kAoCH];
-            auto rd = [&](int k, float (&v)[kAoCH]) {
-                const float* src = pbuf + (k % NB) * kAoTile + tid;
+            // each quarter of a chunk (the last one: the next chunk's first) is
+            // read into registers while the quarter before it is added, so
+            // only the dependent adds are on this wave's path (chunk k + 1 is
+            // complete during step k; the producers write chunk k + 2).
+            // sched_barrier keeps the compiler from sinking the reads below
+            // the adds they are meant to overlap.
+            rd(0, 0, va);
+            for (int k = 0; k < nsteps; k++) {
+                if (T - k * kAoCH >= kAoCH) {
 #pragma unroll
-                for (int e = 0; e < kAoCH; e++) v[e] = src[e * kAoD];
-            };
-            // full chunks add from registers; the last, partial one is read
-            // again from its buffer (untouched during its own step)
-            auto add = [&](int k, const float (&v)[kAoCH]) {
-                const int tn = T - k * kAoCH;
-                if (tn >= kAoCH) {
-#pragma unroll
-                    for (int e = 0; e < kAoCH; e++) o = o + v[e];
-                } else if (tn > 0) {
-                    const float* src = pbuf + (k % NB) * kAoTile + tid;
-                    for (int e = 0; e < tn; e++) o = o + src[e * kAoD];
+                    for (int q = 1; q <= 4; q += 2) {
+                        rd(k, q, vb);
+                        __builtin_amdgcn_sched_barrier(0);
+                        add(va);
+                        __builtin_amdgcn_sched_barrier(0);
+                        if (q + 1 < 4) rd(k, q + 1, va);
+                        else rd(k + 1, 0, va);
+                        __builtin_amdgcn_sched_barrier(0);
+                        add(vb);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                } else if (k < nch) {
+                    add_part(k);
                 }
-            };
-            rd(0, va);
-            for (int k = 0; k < nsteps; k += 2) {
-                rd(k + 1, vb);
-                add(k, va);
-                lds_barrier();
-                rd(k + 2, va);
-                add(k + 1, vb);
                 lds_barrier();
             }
         }
-        out[(size_t)h * HD + d0 + tid] = o;
+        AO_TT(5);
+        if (tid < kAoD) out[(size_t)h * HD + d0 + tid] = o;
         return;
     }
     // producers: branch-free; rows past T are clamped and their products land
@@ -906,7 +939,7 @@ int ibh_launch_attn_exact(float* out, const float* q, const void* kdata, const v
     const uint8_t* K = (const uint8_t*)kdata;
     const uint8_t* V = (const uint8_t*)vdata;
     const int tcap = (max_pos + 1 + 3) & ~3;
-    const bool nb3 = (size_t)(tcap + 3 * kAoTile) * sizeof(float) <= 64 * 1024;
+    const bool nb3 = (size_t)(tcap + 3 * kAoTile) * sizeof(float) <= 160 * 1024;
     const size_t lds = (size_t)(tcap + (nb3 ? 3 : 2) * kAoTile) * sizeof(float);
 #define IBH_AO(B_, H_) do { \
         if (nb3) attn_out_exact<B_, H_, 3><<<n_heads * (H_ / kAoD), kAoThreads, lds, st>>>(out, att, V, vs, dpos, n_heads, n_kv, tstride, tcap); \
@@ -922,6 +955,12 @@ int ibh_launch_attn_exact(float* out, const float* q, const void* kdata, const v
     IBH_CHECK_LAUNCH("exact attention");
     return IBH_OK;
 }
+
+#ifdef IBH_AO_TRACE
+extern "C" int ibh_ao_trace(void* host) {
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(ibh_ao_tt), sizeof(ibh_ao_tt)) == hipSuccess ? 0 : -1;
+}
+#endif
 
 // Host copy of the device expf (checks of the restatement).
 extern "C" void ibh_expf_host(const float* x, float* y, size_t n) {
