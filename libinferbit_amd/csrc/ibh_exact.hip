@@ -118,12 +118,12 @@ __global__ __launch_bounds__(256) void rmsnorm_exact(float* out, float* x, const
 // columns each lane loads the 16 weights of block c (one 16-column block)
 // into a per-wavefront LDS tile as int8, then reads back column c of the 16
 // blocks; x is staged in LDS once per block.  The first 16 tiles' weight
-// loads are issued before x is read.
+// loads are issued right after x's, before x is used.
 //
 // NORM 1: x is first put through the x86 rmsnorm (rmsnorm_exact's
 // arithmetic, every block computing it); NORM 2: the residual add x + dl
 // before it, block 0 writing the sum to xr (the next residual stream).
-template <int BITS, int KIND, bool ALIGNED, int NORM = 0>
+template <int BITS, int KIND, bool ALIGNED, int NORM = 0, int NQ = 16>
 __global__ __launch_bounds__(256) void matvec_exact(const RowSet rs, const float* __restrict__ x, int N,
                                                     const float* __restrict__ dl, const uint16_t* __restrict__ nw,
                                                     float* __restrict__ xr, float eps) {
@@ -176,20 +176,23 @@ __global__ __launch_bounds__(256) void matvec_exact(const RowSet rs, const float
             }
         }
     };
-    issue(0);
     {
-        constexpr int NQ = 16;                                        // N <= 16384
-        const int n4 = N >> 2;
-        float4 v[NQ];
+        // x (and dl) first: loads return in issue order, and the weight loads
+        // issued right after them must not delay the x chain
+        const int n4 = N >> 2;                                        // N <= 1024 * NQ
+        float4 v[NQ], dv[NORM == 2 ? NQ : 1];
 #pragma unroll
         for (int u = 0; u < NQ; u++) {
             const int i4 = (int)threadIdx.x + 256 * u;
             v[u] = i4 < n4 ? ((const float4*)x)[i4] : float4{0.f, 0.f, 0.f, 0.f};
-            if constexpr (NORM == 2) {
-                if (i4 < n4) {
-                    const float4 d = ((const float4*)dl)[i4];
-                    v[u].x = v[u].x + d.x; v[u].y = v[u].y + d.y; v[u].z = v[u].z + d.z; v[u].w = v[u].w + d.w;
-                }
+            if constexpr (NORM == 2) dv[u] = i4 < n4 ? ((const float4*)dl)[i4] : float4{0.f, 0.f, 0.f, 0.f};
+        }
+        issue(0);
+        if constexpr (NORM == 2) {
+#pragma unroll
+            for (int u = 0; u < NQ; u++) {
+                v[u].x = v[u].x + dv[u].x; v[u].y = v[u].y + dv[u].y; v[u].z = v[u].z + dv[u].z;
+                v[u].w = v[u].w + dv[u].w;
             }
         }
         if constexpr (NORM) {
@@ -884,14 +887,16 @@ int ibh_launch_matvec_exact_multi(const MatDesc* d, int n, int kind, const float
                               : (((uintptr_t)d[i].w & 7) == 0 && rb % 8 == 0));
     const RowSet rs = make_rowset(d, n, 16);
     const int blocks = rowset_blocks(d, n, 16);
-#define IBH_MX(B_, K_, A_) do { \
-        if (!nw) matvec_exact<B_, K_, A_, 0><<<blocks, 256, lds, st>>>(rs, x, N, nullptr, nullptr, nullptr, 0.f); \
-        else if (!dl) matvec_exact<B_, K_, A_, 1><<<blocks, 256, lds, st>>>(rs, x, N, nullptr, nw, nullptr, eps); \
-        else matvec_exact<B_, K_, A_, 2><<<blocks, 256, lds, st>>>(rs, x, N, dl, nw, xr, eps); } while (0)
+#define IBH_MX2(B_, K_, A_, Q_) do { \
+        if (!nw) matvec_exact<B_, K_, A_, 0, Q_><<<blocks, 256, lds, st>>>(rs, x, N, nullptr, nullptr, nullptr, 0.f); \
+        else if (!dl) matvec_exact<B_, K_, A_, 1, Q_><<<blocks, 256, lds, st>>>(rs, x, N, nullptr, nw, nullptr, eps); \
+        else matvec_exact<B_, K_, A_, 2, Q_><<<blocks, 256, lds, st>>>(rs, x, N, dl, nw, xr, eps); } while (0)
+#define IBH_MX(B_, K_, A_) do { if (N <= 4096) IBH_MX2(B_, K_, A_, 4); else IBH_MX2(B_, K_, A_, 16); } while (0)
 #define IBH_MXA(B_, K_) do { if (al) IBH_MX(B_, K_, true); else IBH_MX(B_, K_, false); } while (0)
     if (kind == IBH_SCALE_F16) { if (bits == 8) IBH_MXA(8, IBH_SCALE_F16); else IBH_MXA(4, IBH_SCALE_F16); }
     else { if (bits == 8) IBH_MXA(8, IBH_SCALE_F32); else IBH_MXA(4, IBH_SCALE_F32); }
 #undef IBH_MX
+#undef IBH_MX2
 #undef IBH_MXA
     IBH_CHECK_LAUNCH("exact matvec");
     return IBH_OK;
