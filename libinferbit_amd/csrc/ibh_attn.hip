@@ -605,6 +605,16 @@ struct SplitRope {
     float* vs;
 };
 
+// Phase probes, compiled only with -DIBH_AS_TRACE (a development build
+// outside the library): s_memrealtime of thread 0 of each block.
+#ifdef IBH_AS_TRACE
+__device__ unsigned long long ibh_as_tt[512][8];
+#define AS_TT(i) do { if (threadIdx.x == 0 && blockIdx.x + gridDim.x * blockIdx.y < 512) \
+    ibh_as_tt[blockIdx.x + gridDim.x * blockIdx.y][i] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#else
+#define AS_TT(i) ((void)0)
+#endif
+
 template <int BITS, int GRP, int HD, bool ROPE = false>
 __global__ __launch_bounds__(kSplitThreads) void attn_split(float* __restrict__ out, float* __restrict__ part,
                                                            const float* __restrict__ q,
@@ -623,11 +633,20 @@ __global__ __launch_bounds__(kSplitThreads) void attn_split(float* __restrict__ 
     constexpr int TR = kSplitThreads / (GRP * NDQ);       // t-ranges in P.V
     constexpr int MB = 64;                                // chunks one merge pass loads per thread
     static_assert(TR >= 1 && CT % TR == 0, "P.V split");
+    AS_TT(0);
     if (dpos) T = *dpos + 1;
-    const int kh = blockIdx.x, c = blockIdx.y, t0 = c * CT;
-    if (t0 >= T) return;
-    const int tn = min(CT, T - t0);
-    const int nch = (T + CT - 1) / CT;
+    // ROPE: the chunks cover positions 0 .. T-2 and the last row of blocks
+    // (blockIdx.y == gridDim.y - 1) takes position T-1 alone, with its rotary
+    // embedding and cache write, as one more partial (slot nmain), so that
+    // extra work runs beside the chunks instead of after one of them
+    const int kh = blockIdx.x;
+    const bool cur = ROPE && blockIdx.y == gridDim.y - 1;
+    const int Tc = ROPE ? T - 1 : T;                      // positions the chunks cover
+    const int c = blockIdx.y, t0 = cur ? T - 1 : c * CT;
+    if (!cur && t0 >= Tc) return;
+    const int tn = cur ? 1 : min(CT, Tc - t0);
+    const int nmain = (Tc + CT - 1) / CT;
+    const int slot = cur ? nmain : c;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const size_t row_bytes = (size_t)n_kv * RB;
     __shared__ __align__(16) float qs[GRP][HD];
@@ -661,7 +680,7 @@ __global__ __launch_bounds__(kSplitThreads) void attn_split(float* __restrict__ 
             qs[g][2 * j] = x0 * cc - x1 * sn;
             qs[g][2 * j + 1] = x0 * sn + x1 * cc;
         }
-        if (c == nch - 1 && wave < 2) {
+        if (cur && wave < 2) {
             const int side = wave, j = lane;
             const float* src = (side ? rp.v : rp.k) + (size_t)kh * HD;
             float x0 = 0.f, x1 = 0.f;
@@ -709,7 +728,7 @@ __global__ __launch_bounds__(kSplitThreads) void attn_split(float* __restrict__ 
             }
         }
         __syncthreads();
-        if (c == nch - 1 && pos == pcur) {   // the pieces of position T - 1, as just written
+        if (cur && pos == pcur) {            // the pieces of position T - 1, as just written
             if constexpr (BITS == 4) {
                 const uint2 a = *(const uint2*)&nrow[0][pc * PB], b = *(const uint2*)&nrow[1][pc * PB];
                 kr[0] = make_uint4(a.x, a.y, 0u, 0u);
@@ -730,6 +749,7 @@ __global__ __launch_bounds__(kSplitThreads) void attn_split(float* __restrict__ 
         __syncthreads();
     }
 
+    AS_TT(1);
     // 2. scores: the piece's dot with each head, summed over the position's lanes
     float kv[16];
     piece_vals<BITS>(kr, kv);
@@ -745,9 +765,7 @@ __global__ __launch_bounds__(kSplitThreads) void attn_split(float* __restrict__ 
         s[g] = a;
     }
 #pragma unroll
-    for (int o = 1; o < PIECES; o <<= 1)
-#pragma unroll
-        for (int g = 0; g < GRP; g++) s[g] += __shfl_xor(s[g], o);
+    for (int g = 0; g < GRP; g++) s[g] = group_sum_dpp<PIECES>(s[g]);
     if (pc == 0) {
 #pragma unroll
         for (int g = 0; g < GRP; g++) sc[g][t] = t < tn ? s[g] * ksc * scale : -INFINITY;
@@ -760,23 +778,25 @@ __global__ __launch_bounds__(kSplitThreads) void attn_split(float* __restrict__ 
     }
     if (pc == 0) vsc[t] = vsv;
     __syncthreads();
+    AS_TT(2);
 
     // 3. chunk softmax, wavefront g for head g
     if (wave < GRP) {
         const int g = wave;
         float m = -INFINITY;
         for (int i = lane; i < CT; i += 64) m = fmaxf(m, sc[g][i]);
-        m = wave_max(m);
+        m = wave_max_dpp(m);
         float l = 0.f;
         for (int i = lane; i < CT; i += 64) {
             const float e = i < tn ? expf(sc[g][i] - m) : 0.f;
             sc[g][i] = e;
             l += e;
         }
-        l = wave_sum(l);
+        l = wave_sum_dpp(l);
         if (lane == 0) { mlr[g][0] = m; mlr[g][1] = l; }
     }
     __syncthreads();
+    AS_TT(3);
 
     // 4. P.V: thread (t-range tr, head g, dims 4 dq .. 4 dq + 3)
     {
@@ -805,6 +825,7 @@ __global__ __launch_bounds__(kSplitThreads) void attn_split(float* __restrict__ 
         *(float4*)&ob[tr][g][dq * 4] = make_float4(a0, a1, a2, a3);
     }
     __syncthreads();
+    AS_TT(4);
 
     // 5. the chunk's partial (m, l, o[HD]) per head
     if (tid < GRP * HD) {
@@ -812,10 +833,11 @@ __global__ __launch_bounds__(kSplitThreads) void attn_split(float* __restrict__ 
         float o = 0.f;
 #pragma unroll
         for (int r = 0; r < TR; r++) o += ob[r][g][d];
-        float* pp = part + ((size_t)(kh * GRP + g) * nstride + c) * (HD + 2);
+        float* pp = part + ((size_t)(kh * GRP + g) * nstride + slot) * (HD + 2);
         pp[2 + d] = o;
         if (d < 2) pp[d] = mlr[g][d];
     }
+    AS_TT(5);
 }
 
 // Merge of one head's chunks: out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c.
@@ -823,38 +845,47 @@ __global__ __launch_bounds__(kSplitThreads) void attn_split(float* __restrict__ 
 // 1024/HD), every load of the block issued at once.
 template <int HD>
 __global__ __launch_bounds__(1024) void attn_merge_wide(float* __restrict__ out, const float* __restrict__ part,
-                                                        int T, const int* __restrict__ dpos, int ct, int nstride) {
+                                                        int T, const int* __restrict__ dpos, int ct, int nstride,
+                                                        int rope) {
     constexpr int NCQ = 1024 / HD;                        // chunk classes
     constexpr int PER = kSplitMaxChunks / NCQ;            // chunks per thread at most
     __shared__ float wm[kSplitMaxChunks], wl[kSplitMaxChunks];
     __shared__ float osum[NCQ][HD];
     __shared__ float tot;
-    if (dpos) T = *dpos + 1;
     const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int nch = (T + ct - 1) / ct;
     const float* ph = part + (size_t)h * nstride * (HD + 2);
     const int cq = tid / HD, d = tid % HD;
-    const int per = (nch + NCQ - 1) / NCQ;
+    // every slot of the head is loaded before the position is known (slots
+    // past the last chunk hold stale values that are never used), so the
+    // partials' loads do not wait for dpos
+    const int per = (nstride + NCQ - 1) / NCQ;
     float v[PER];
 #pragma unroll
     for (int u = 0; u < PER; u++)
-        if (u < per) v[u] = ph[(size_t)min(cq + NCQ * u, nch - 1) * (HD + 2) + 2 + d];
+        if (u < per) v[u] = ph[(size_t)min(cq + NCQ * u, nstride - 1) * (HD + 2) + 2 + d];
+    float wmv = 0.f, wlv = 0.f;
+    if (tid < nstride) {
+        wmv = ph[(size_t)tid * (HD + 2)];
+        wlv = ph[(size_t)tid * (HD + 2) + 1];
+    }
+    if (dpos) T = *dpos + 1;
+    const int nch = rope ? (T - 1 + ct - 1) / ct + 1 : (T + ct - 1) / ct;   // rope: one more partial, position T-1
     if (tid < nch) {
-        wm[tid] = ph[(size_t)tid * (HD + 2)];
-        wl[tid] = ph[(size_t)tid * (HD + 2) + 1];
+        wm[tid] = wmv;
+        wl[tid] = wlv;
     }
     __syncthreads();
     if (wave == 0) {
         float M = -INFINITY;
         for (int cc = lane; cc < nch; cc += 64) M = fmaxf(M, wm[cc]);
-        M = wave_max(M);
+        M = wave_max_dpp(M);
         float L = 0.f;
         for (int cc = lane; cc < nch; cc += 64) {
             const float e = expf(wm[cc] - M);
             wm[cc] = e;
             L = fmaf(e, wl[cc], L);
         }
-        L = wave_sum(L);
+        L = wave_sum_dpp(L);
         if (lane == 0) tot = L;
     }
     __syncthreads();
@@ -890,18 +921,19 @@ int launch_split(float* out, float* part, const float* q, const void* kdata, con
         return 0;
     if (rope && !dpos) return 0;
     const int ct = kSplitThreads / (head_dim / 16);
-    const int nstride = (max_pos + 1 + ct - 1) / ct;
+    const int nchunk = (max_pos + 1 + ct - 1) / ct;       // chunk blocks
+    const int nstride = nchunk + (rope ? 1 : 0);          // partial slots per head
     if (nstride > kSplitMaxChunks) return 0;
     const uint8_t* K = (const uint8_t*)kdata;
     const uint8_t* V = (const uint8_t*)vdata;
     const SplitRope rp = rope ? *rope : SplitRope{};
 #define IBH_AS(B_, G_, H_) do { \
-        if (rope) attn_split<B_, G_, H_, true><<<dim3(n_kv, nstride), kSplitThreads, 0, st>>>( \
+        if (rope) attn_split<B_, G_, H_, true><<<dim3(n_kv, nchunk + 1), kSplitThreads, 0, st>>>( \
                       out, part, q, K, V, kscales, vscales, T, dpos, n_kv, scale, nstride, rp); \
-        else attn_split<B_, G_, H_, false><<<dim3(n_kv, nstride), kSplitThreads, 0, st>>>( \
+        else attn_split<B_, G_, H_, false><<<dim3(n_kv, nchunk), kSplitThreads, 0, st>>>( \
                  out, part, q, K, V, kscales, vscales, T, dpos, n_kv, scale, nstride, rp); \
         IBH_CHECK_LAUNCH("ibh_attn_decode (split)"); \
-        attn_merge_wide<H_><<<n_heads, 1024, 0, st>>>(out, part, T, dpos, ct, nstride); } while (0)
+        attn_merge_wide<H_><<<n_heads, 1024, 0, st>>>(out, part, T, dpos, ct, nstride, rope ? 1 : 0); } while (0)
 #define IBH_ASG(B_, H_) do { if (grp == 1) IBH_AS(B_, 1, H_); else if (grp == 2) IBH_AS(B_, 2, H_); \
                          else if (grp == 4) IBH_AS(B_, 4, H_); else IBH_AS(B_, 8, H_); } while (0)
 #define IBH_ASH(B_) do { if (head_dim == 64) IBH_ASG(B_, 64); else IBH_ASG(B_, 128); } while (0)
@@ -917,6 +949,12 @@ int launch_split(float* out, float* part, const float* q, const void* kdata, con
 
 }  // namespace
 
+#ifdef IBH_AS_TRACE
+extern "C" int ibh_as_trace(void* host) {
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(ibh_as_tt), sizeof(ibh_as_tt)) == hipSuccess ? 0 : -1;
+}
+#endif
+
 // Development switch (no counterpart in the reference): 0 sends decode
 // attention through the chunk + merge kernels, 1 (default) lets eligible
 // shapes run in one launch.
@@ -926,7 +964,7 @@ extern "C" int ibh_attn_set_split(int on) {
 }
 
 extern "C" size_t ibh_attn_workspace_bytes(int n_heads, int head_dim, int n_pos) {
-    const int nchunks = (n_pos + kChunk - 1) / kChunk;
+    const int nchunks = (n_pos + kChunk - 1) / kChunk + 1;   // + 1: the split launch's own-position partial
     return (size_t)n_heads * nchunks * (head_dim + 2) * sizeof(float);
 }
 

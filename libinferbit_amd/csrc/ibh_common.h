@@ -106,6 +106,32 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
     const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
     return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    int b = __builtin_bit_cast(int, v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(b, 0xB1, 0xF, 0xF, false));
+    b = __builtin_bit_cast(int, v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(b, 0x4E, 0xF, 0xF, false));
+    b = __builtin_bit_cast(int, v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(b, 0x124, 0xF, 0xF, false));
+    b = __builtin_bit_cast(int, v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(b, 0x128, 0xF, 0xF, false));
+    b = __builtin_bit_cast(int, v);
+    return (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)) + __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))) +
+           (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)) + __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48)));
+}
+// Sum over aligned groups of L = 2, 4 or 8 lanes, every lane of a group
+// getting it: the butterfly of __shfl_xor(v, 1), (v, 2), (v, 4) (the same
+// operands at every step, so the same bits) as DPP moves.
+template <int L>
+__device__ __forceinline__ float group_sum_dpp(float v) {
+    static_assert(L == 2 || L == 4 || L == 8, "group size");
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));  // lane ^ 1
+    if constexpr (L >= 4)
+        v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));  // lane ^ 2
+    if constexpr (L >= 8)
+        v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false)); // half-row mirror
+    return v;
+}
 __device__ __forceinline__ int wave_isum_dpp(int v) {
     v += __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);
     v += __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);
