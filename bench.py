@@ -96,7 +96,10 @@ def time_launches(torch, launch, steps, warmup):
     graph of `steps` nodes, so the timed region holds back-to-back kernels
     with no host launch gaps; HIP events on the replay stream bracket it.
     Before it: `warmup` eager launches and one untimed replay of the graph
-    (its first replay uploads the graph)."""
+    (its first replay uploads the graph); a second untimed replay is queued
+    just ahead of the timed one, so the start event is stamped when the
+    device reaches it rather than while the host is still submitting the
+    timed graph."""
     for i in range(max(1, warmup)):
         launch(i)                                   # eager warmup, also validates
     torch.cuda.synchronize()
@@ -111,6 +114,7 @@ def time_launches(torch, launch, steps, warmup):
     torch.cuda.synchronize()
     st = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    g.replay()                                      # untimed, keeps the device busy while the timed one is queued
     e0.record(st)
     g.replay()
     e1.record(st)
