@@ -43,6 +43,16 @@ __device__ __forceinline__ float load_scale(const void* s, int i) {
     else return ((const float*)s)[i];
 }
 
+// Workgroup barrier that orders LDS only: LDS operations issued before it are
+// complete (lgkmcnt 0) but global loads stay in flight.  __syncthreads() is a
+// release fence that also waits for every outstanding global load (vmcnt 0),
+// which in a prologue running while the weight loads are in flight would wait
+// for all of them.
+__device__ __forceinline__ void lds_only_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);                   // lgkmcnt(0), vmcnt/expcnt untouched
+    __builtin_amdgcn_s_barrier();
+}
+
 // Butterfly sum over the 64 lanes of a wavefront (every lane gets the total).
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

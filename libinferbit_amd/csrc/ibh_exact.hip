@@ -123,18 +123,40 @@ __global__ __launch_bounds__(256) void rmsnorm_exact(float* out, float* x, const
 // NORM 1: x is first put through the x86 rmsnorm (rmsnorm_exact's
 // arithmetic, every block computing it); NORM 2: the residual add x + dl
 // before it, block 0 writing the sum to xr (the next residual stream).
+// LDS layout of matvec_exact's x: 16 chain rows of ceil(N/16) floats, the
+// row stride rounded up to 4 mod 32 floats, 16 floats of slack at the end
+// (the last tile's 16-byte reads may run past its row).
+__host__ __device__ inline int exact_xstride(int N) {
+    const int nbc = (N + 15) / 16;
+    return ((nbc + 27) / 32) * 32 + 4;
+}
+__host__ __device__ inline size_t exact_xs_bytes(int N) { return ((size_t)16 * exact_xstride(N) + 16) * 4; }
+
+// Phase probes, compiled only with -DIBH_MX_TRACE (a development build
+// outside the library): s_memrealtime of thread 0 of each block.
+#ifdef IBH_MX_TRACE
+__device__ unsigned long long ibh_mx_tt[1024][8];
+#define MX_TT(i) do { if (NORM && threadIdx.x == 0 && blockIdx.x < 1024) ibh_mx_tt[blockIdx.x][i] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#else
+#define MX_TT(i) ((void)0)
+#endif
+
 template <int BITS, int KIND, bool ALIGNED, int NORM = 0, int NQ = 16>
 __global__ __launch_bounds__(256) void matvec_exact(const RowSet rs, const float* __restrict__ x, int N,
                                                     const float* __restrict__ dl, const uint16_t* __restrict__ nw,
                                                     float* __restrict__ xr, float eps) {
+    MX_TT(0);
     const RowPick P = pick_rows(rs);
     const uint8_t* __restrict__ W = P.W;
     const void* __restrict__ sc = P.sc;
     float* __restrict__ y = P.y;
     const int M = P.M;
     extern __shared__ __align__(16) unsigned char smem[];
-    float* xs = (float*)smem;                                         // [N]
-    int8_t* tile = (int8_t*)(smem + (((size_t)N * 4 + 15) & ~(size_t)15));   // [4 waves][4 rows][256]
+    // x chain-major: xs[c][k] = x[16k + c], rows of XSTR floats (a multiple
+    // of 4, and 4 mod 32 so the 16 chains' 16-byte reads fall in distinct banks)
+    const int XSTR = exact_xstride(N);
+    float* xs = (float*)smem;                                         // [16][XSTR] (+ 16 slack)
+    int8_t* tile = (int8_t*)(smem + exact_xs_bytes(N));               // [4 waves][4 rows][256]
     float* xt = (float*)(tile + 4 * 4 * 256);                         // NORM: [8][N/8] chain-major
     __shared__ float part[8];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -181,13 +203,16 @@ __global__ __launch_bounds__(256) void matvec_exact(const RowSet rs, const float
         // issued right after them must not delay the x chain
         const int n4 = N >> 2;                                        // N <= 1024 * NQ
         float4 v[NQ], dv[NORM == 2 ? NQ : 1];
+        uint2 wq[NORM ? NQ : 1];
 #pragma unroll
         for (int u = 0; u < NQ; u++) {
             const int i4 = (int)threadIdx.x + 256 * u;
             v[u] = i4 < n4 ? ((const float4*)x)[i4] : float4{0.f, 0.f, 0.f, 0.f};
             if constexpr (NORM == 2) dv[u] = i4 < n4 ? ((const float4*)dl)[i4] : float4{0.f, 0.f, 0.f, 0.f};
+            if constexpr (NORM != 0) wq[u] = i4 < n4 ? ((const uint2*)nw)[i4] : uint2{0u, 0u};
         }
         issue(0);
+        MX_TT(1);
         if constexpr (NORM == 2) {
 #pragma unroll
             for (int u = 0; u < NQ; u++) {
@@ -210,7 +235,7 @@ __global__ __launch_bounds__(256) void matvec_exact(const RowSet rs, const float
                     if (NORM == 2 && blockIdx.x == 0) ((float4*)xr)[i4] = v[u];
                 }
             }
-            __syncthreads();
+            lds_only_barrier();
             if (threadIdx.x < 8) {
                 const float* ch = xt + threadIdx.x * n8;
                 float acc = 0.f;
@@ -226,31 +251,35 @@ __global__ __launch_bounds__(256) void matvec_exact(const RowSet rs, const float
                 }
                 part[threadIdx.x] = acc;
             }
-            __syncthreads();
+            lds_only_barrier();
             const float q0 = part[0] + part[4], q1 = part[1] + part[5], q2 = part[2] + part[6], q3 = part[3] + part[7];
             const float ss = (q0 + q1) + (q2 + q3);
             const float scale = 1.0f / sqrtf(ss / (float)N + eps);
+            MX_TT(2);
 #pragma unroll
             for (int u = 0; u < NQ; u++) {
                 const int i4 = (int)threadIdx.x + 256 * u;
                 if (i4 < n4) {
-                    const uint2 wq = ((const uint2*)nw)[i4];
-                    float4 o;
-                    o.x = (v[u].x * scale) * f16_to_f32((uint16_t)(wq.x & 0xffff));
-                    o.y = (v[u].y * scale) * f16_to_f32((uint16_t)(wq.x >> 16));
-                    o.z = (v[u].z * scale) * f16_to_f32((uint16_t)(wq.y & 0xffff));
-                    o.w = (v[u].w * scale) * f16_to_f32((uint16_t)(wq.y >> 16));
-                    ((float4*)xs)[i4] = o;
+                    v[u].x = (v[u].x * scale) * f16_to_f32((uint16_t)(wq[u].x & 0xffff));
+                    v[u].y = (v[u].y * scale) * f16_to_f32((uint16_t)(wq[u].x >> 16));
+                    v[u].z = (v[u].z * scale) * f16_to_f32((uint16_t)(wq[u].y & 0xffff));
+                    v[u].w = (v[u].w * scale) * f16_to_f32((uint16_t)(wq[u].y >> 16));
                 }
             }
-        } else {
-#pragma unroll
-            for (int u = 0; u < NQ; u++)
-                if ((int)threadIdx.x + 256 * u < n4) ((float4*)xs)[threadIdx.x + 256 * u] = v[u];
-            for (int i = 4 * n4 + (int)threadIdx.x; i < N; i += 256) xs[i] = x[i];
         }
+#pragma unroll
+        for (int u = 0; u < NQ; u++) {
+            const int i4 = (int)threadIdx.x + 256 * u;
+            if (i4 < n4) {
+                const int i = 4 * i4;                                 // columns i .. i+3: chains c0 .. c0+3
+                float* d = xs + (i & 15) * XSTR + (i >> 4);
+                d[0] = v[u].x; d[XSTR] = v[u].y; d[2 * XSTR] = v[u].z; d[3 * XSTR] = v[u].w;
+            }
+        }
+        for (int i = 4 * n4 + (int)threadIdx.x; i < N; i += 256) xs[(i & 15) * XSTR + (i >> 4)] = x[i];
     }
-    __syncthreads();
+    lds_only_barrier();
+    MX_TT(3);
     float acc = 0.f;
     for (int g0 = 0; g0 < nt; g0 += 16) {
         if (g0) issue(g0);
@@ -279,20 +308,30 @@ __global__ __launch_bounds__(256) void matvec_exact(const RowSet rs, const float
             const int b0 = 16 * tile;
             const int nj = min(16, nb - b0);
             float wv[16], xv[16];
+            const float4* xc = (const float4*)(xs + c * XSTR + b0);    // chain c's x, blocks b0 ..
 #pragma unroll
-            for (int j = 0; j < 16; j++) {
-                wv[j] = (float)mytile[16 * j + c];
-                xv[j] = xs[16 * min(b0 + j, nb - 1) + c];
+            for (int q = 0; q < 4; q++) {
+                const float4 f = xc[q];
+                xv[4 * q] = f.x; xv[4 * q + 1] = f.y; xv[4 * q + 2] = f.z; xv[4 * q + 3] = f.w;
             }
 #pragma unroll
-            for (int j = 0; j < 16; j++)
-                if (j < nj) acc = fmaf(wv[j], xv[j], acc);
+            for (int j = 0; j < 16; j++) wv[j] = (float)mytile[16 * j + c];
+            if (nj == 16) {                                        // whole tile: no select in the fma chain
+#pragma unroll
+                for (int j = 0; j < 16; j++) acc = fmaf(wv[j], xv[j], acc);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 16; j++)
+                    if (j < nj) acc = fmaf(wv[j], xv[j], acc);
+            }
+            if (tile == 0) MX_TT(4);
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
             }
         }
     }
+    MX_TT(5);
     // acc0 + acc1 (lane c < 8 gets chain c + 8), then lo + hi, hadd, hadd
     const float s = acc + __shfl_down(acc, 8, 16);
     const float q = s + __shfl_down(s, 4, 16);                        // q_k = s_k + s_(k+4), k < 4
@@ -306,7 +345,7 @@ __global__ __launch_bounds__(256) void matvec_exact(const RowSet rs, const float
                 const uint8_t byte = wr[j / 2];
                 wv = (float)((int)((j & 1) ? (byte >> 4) : (byte & 0xf)) - 8);
             }
-            res = fmaf(wv, xs[j], res);
+            res = fmaf(wv, xs[(j & 15) * XSTR + (j >> 4)], res);
         }
         y[row] = res * load_scale<KIND>(sc, row);
     }
@@ -845,7 +884,7 @@ int ibh_launch_matvec_exact_multi(const MatDesc* d, int n, int kind, const float
                                   float* xr = nullptr, float eps = 0.f);
 
 size_t ibh_exact_matvec_lds(int N, bool norm) {
-    return (((size_t)N * 4 + 15) & ~(size_t)15) + 4 * 4 * 256 + (norm ? (size_t)N * 4 : 0);
+    return exact_xs_bytes(N) + 4 * 4 * 256 + (norm ? (size_t)N * 4 : 0);
 }
 
 int ibh_launch_matvec_exact(float* y, const void* w, const void* sc, int kind, const float* x, int M, int N, int bits,
@@ -964,6 +1003,12 @@ int ibh_launch_attn_exact(float* out, const float* q, const void* kdata, const v
 #ifdef IBH_AO_TRACE
 extern "C" int ibh_ao_trace(void* host) {
     return hipMemcpyFromSymbol(host, HIP_SYMBOL(ibh_ao_tt), sizeof(ibh_ao_tt)) == hipSuccess ? 0 : -1;
+}
+#endif
+
+#ifdef IBH_MX_TRACE
+extern "C" int ibh_mx_trace(void* host) {
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(ibh_mx_tt), sizeof(ibh_mx_tt)) == hipSuccess ? 0 : -1;
 }
 #endif
 

@@ -317,9 +317,9 @@ __global__ __launch_bounds__(64 * WPB) void gemv_rows_w4a8_k(const RowSet rs, co
                     for (int q = 0; q < CPT / 4; q++)
                         *(float4*)(xr + c0 + 4 * q) = float4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
                 }
-                __syncthreads();
+                lds_only_barrier();
                 if (threadIdx.x < 8) red[threadIdx.x] = chain_sumsq<N8>(xts + threadIdx.x * N8);
-                __syncthreads();
+                lds_only_barrier();
                 tot = ((red[0] + red[4]) + (red[1] + red[5])) + ((red[2] + red[6]) + (red[3] + red[7]));
             } else {
 #pragma unroll
@@ -331,7 +331,7 @@ __global__ __launch_bounds__(64 * WPB) void gemv_rows_w4a8_k(const RowSet rs, co
                     for (int q = 0; q < CPT / 4; q++)
                         *(float4*)(xr + c0 + 4 * q) = float4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
                 }
-                __syncthreads();
+                lds_only_barrier();
 #pragma unroll
                 for (int w = 0; w < WPB; w++) tot += red[w];
             }
@@ -372,7 +372,7 @@ __global__ __launch_bounds__(64 * WPB) void gemv_rows_w4a8_k(const RowSet rs, co
         if constexpr (CPT == 16) *(uint4*)(qs + c0) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
         else *(uint2*)(qs + c0) = make_uint2(pk[0], pk[1]);
         if ((threadIdx.x & (TPG - 1)) == 0) ss_s[threadIdx.x / TPG] = sg;
-        __syncthreads();
+        lds_only_barrier();
 #pragma unroll
         for (int j = 0; j < SPW; j++)
 #pragma unroll
