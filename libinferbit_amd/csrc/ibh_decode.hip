@@ -68,6 +68,9 @@ int ibh_launch_matvec_exact_multi(const MatDesc* d, int n, int kind, const float
                                   hipStream_t st, const float* dl = nullptr, const uint16_t* nw = nullptr,
                                   float* xr = nullptr, float eps = 0.f);
 size_t ibh_attn_exact_scratch(int n_heads, int max_pos);
+int ibh_launch_attn_exact_rope(float* out, const float* q, const float* k, const float* v, const float* table,
+                               void* kdata, void* vdata, float* ks, float* vs, const int* dpos, int max_pos,
+                               int n_heads, int n_kv, int hd, int kv_bits, float* att, hipStream_t st);
 size_t ibh_exact_matvec_lds(int N, bool norm);
 int ibh_launch_int8_batch_exact(float* y, const void* w, const void* sc, int kind, const float* x, int M, int N,
                                 int B, int M_stride, hipStream_t st);
@@ -533,11 +536,18 @@ int step_exact(ibh_model* m) {
         if (!f && ((rc = ibh_launch_rmsnorm_exact(m->xb, xc, dl, L.in_norm, m->eps, H, m->st)) ||
                    (rc = qkv(m, L, true))))
             return rc;
-        if ((rc = ibh_launch_rope_kv_write(L.kd, L.vd, L.ks, L.vs, m->q, m->k, m->v, m->rope, m->dpos(),
-                                           m->n_heads, m->n_kv, m->head_dim, m->kv_bits, true, m->st)) ||
-            (rc = ibh_launch_attn_exact(m->xb2, m->q, L.kd, L.vd, L.ks, L.vs, m->dpos(), m->max_pos, m->n_heads,
-                                        m->n_kv, m->head_dim, m->kv_bits, m->att, m->st)))
+        if (!m->no_norm_fuse) {
+            // rotary embedding and cache write inside the scores launch
+            if ((rc = ibh_launch_attn_exact_rope(m->xb2, m->q, m->k, m->v, m->rope, L.kd, L.vd, L.ks, L.vs, m->dpos(),
+                                                 m->max_pos, m->n_heads, m->n_kv, m->head_dim, m->kv_bits, m->att,
+                                                 m->st)))
+                return rc;
+        } else if ((rc = ibh_launch_rope_kv_write(L.kd, L.vd, L.ks, L.vs, m->q, m->k, m->v, m->rope, m->dpos(),
+                                                  m->n_heads, m->n_kv, m->head_dim, m->kv_bits, true, m->st)) ||
+                   (rc = ibh_launch_attn_exact(m->xb2, m->q, L.kd, L.vd, L.ks, L.vs, m->dpos(), m->max_pos,
+                                               m->n_heads, m->n_kv, m->head_dim, m->kv_bits, m->att, m->st))) {
             return rc;
+        }
         // o: W4A8 with the activation quantized in the prologue and the
         // product added into the residual stream in the epilogue
         const MatDesc od{xc, L.o.w, L.o.s, H};

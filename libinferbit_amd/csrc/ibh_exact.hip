@@ -586,24 +586,119 @@ __device__ __forceinline__ float4 kv_deq4(const Kv4x4<BITS, NG>& r, int u) {
     }
 }
 
+// The position's rotary embedding and cache write done by the exact scores
+// launch (ROPE): q of each head rotated into LDS by the block itself, and the
+// block holding position T-1 rotates k, quantizes k and v by the cache rule
+// and (the group's first head) writes both rows; rope_kv_write_kernel<true>'s
+// arithmetic: a' = fma(a, c, -(b*s)), b' = fma(a, s, b*c); scale =
+// max|row|/127 (int4: /7), at least 1e-8; code = roundf(v * (1/scale)),
+// clamped.  The score of position T-1 uses code * scale, as read back.
+struct ExRope {
+    const float* k;       // projections of position *dpos (k unrotated)
+    const float* v;
+    const float* table;   // (cos, sin) per (position, pair)
+    uint8_t* kd;          // the caches, written at *dpos
+    uint8_t* vd;
+    float* ks;
+    float* vs;
+};
+
 // Scores of one head for positions t (one thread each), serial over d.
-template <int BITS>
+template <int BITS, bool ROPE = false>
 __global__ __launch_bounds__(64) void attn_scores_exact(float* __restrict__ att, const float* __restrict__ q,
                                                         const uint8_t* __restrict__ kd, const float* __restrict__ ks,
                                                         const int* __restrict__ dpos, int n_heads, int n_kv, int hd,
-                                                        float scale, int tstride) {
+                                                        float scale, int tstride, ExRope rp = ExRope{}) {
     __shared__ float qs[256];
+    __shared__ float knew[ROPE ? 256 : 1];
     const int h = blockIdx.x;
     const int T = *dpos + 1;
     const int t = blockIdx.y * 64 + threadIdx.x;
     if ((int)blockIdx.y * 64 >= T) return;
-    const int kh = h / (n_heads / n_kv);
+    const int grp = n_heads / n_kv;
+    const int kh = h / grp;
     const int tc = min(t, T - 1);
+    const int lane = threadIdx.x;
     // the first 128 columns of the key row are loaded before q is staged
     float kv[8][16];
 #pragma unroll
     for (int u = 0; u < 8; u++) kv_row16<BITS>(kv[u], kd, ks, tc, kh, min(16 * u, hd - 16), hd, n_kv);
-    for (int d = threadIdx.x; d < hd; d += 64) qs[d] = q[(size_t)h * hd + d];
+    const int pcur = T - 1;
+    bool own = false;                                      // this lane scores position T-1 from knew
+    if constexpr (ROPE) {
+        const int half = hd / 2;
+        const float* tb = rp.table + (size_t)pcur * half * 2;
+        for (int j = lane; j < half; j += 64) {
+            const float x0 = q[(size_t)h * hd + 2 * j], x1 = q[(size_t)h * hd + 2 * j + 1];
+            const float c = tb[2 * j], sn = tb[2 * j + 1];
+            qs[2 * j] = fmaf(x0, c, -(x1 * sn));
+            qs[2 * j + 1] = fmaf(x0, sn, x1 * c);
+        }
+        if ((int)blockIdx.y == pcur / 64) {
+            const int kv_dim = n_kv * hd;
+            const bool writer = h % grp == 0;
+            float a[2][2], b[2][2];                        // [side][pair i]: side 0 k (rotated), 1 v
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const int j = lane + 64 * i;
+                const bool on = j < half;
+                const float k0 = on ? rp.k[(size_t)kh * hd + 2 * j] : 0.f, k1 = on ? rp.k[(size_t)kh * hd + 2 * j + 1] : 0.f;
+                const float c = on ? tb[2 * j] : 0.f, sn = on ? tb[2 * j + 1] : 0.f;
+                a[0][i] = on ? fmaf(k0, c, -(k1 * sn)) : 0.f;
+                b[0][i] = on ? fmaf(k0, sn, k1 * c) : 0.f;
+                a[1][i] = on ? rp.v[(size_t)kh * hd + 2 * j] : 0.f;
+                b[1][i] = on ? rp.v[(size_t)kh * hd + 2 * j + 1] : 0.f;
+            }
+#pragma unroll
+            for (int side = 0; side < 2; side++) {
+                uint8_t* dst = side ? rp.vd : rp.kd;
+                if constexpr (BITS >= 16) {
+                    float* row = (float*)dst + (size_t)pcur * kv_dim + (size_t)kh * hd;
+#pragma unroll
+                    for (int i = 0; i < 2; i++) {
+                        const int j = lane + 64 * i;
+                        if (j < half) {
+                            if (writer) { row[2 * j] = a[side][i]; row[2 * j + 1] = b[side][i]; }
+                            if (side == 0) { knew[2 * j] = a[0][i]; knew[2 * j + 1] = b[0][i]; }
+                        }
+                    }
+                } else {
+                    float mx = fmaxf(fmaxf(fabsf(a[side][0]), fabsf(b[side][0])), fmaxf(fabsf(a[side][1]), fabsf(b[side][1])));
+                    mx = wave_max(mx);
+                    float sc = mx / (BITS == 8 ? 127.0f : 7.0f);
+                    if (sc < 1e-8f) sc = 1e-8f;
+                    const float inv = 1.0f / sc;
+                    if (writer && lane == 0) (side ? rp.vs : rp.ks)[(size_t)pcur * n_kv + kh] = sc;
+#pragma unroll
+                    for (int i = 0; i < 2; i++) {
+                        const int j = lane + 64 * i;
+                        if (j >= half) continue;
+                        int q0 = (int)roundf(a[side][i] * inv), q1 = (int)roundf(b[side][i] * inv);
+                        if constexpr (BITS == 8) {
+                            q0 = q0 < -127 ? -127 : (q0 > 127 ? 127 : q0);
+                            q1 = q1 < -127 ? -127 : (q1 > 127 ? 127 : q1);
+                            if (writer) {
+                                int8_t* row = (int8_t*)dst + (size_t)pcur * kv_dim + (size_t)kh * hd;
+                                row[2 * j] = (int8_t)q0;
+                                row[2 * j + 1] = (int8_t)q1;
+                            }
+                        } else {
+                            q0 = q0 < -7 ? -7 : (q0 > 7 ? 7 : q0);
+                            q1 = q1 < -7 ? -7 : (q1 > 7 ? 7 : q1);
+                            if (writer) {
+                                uint8_t* row = dst + (size_t)pcur * ((kv_dim + 1) / 2) + (size_t)kh * ((hd + 1) / 2);
+                                row[j] = (uint8_t)(((q0 + 8) & 0xf) | (((q1 + 8) & 0xf) << 4));
+                            }
+                        }
+                        if (side == 0) { knew[2 * j] = (float)q0 * sc; knew[2 * j + 1] = (float)q1 * sc; }
+                    }
+                }
+            }
+            own = t == pcur;
+        }
+    } else {
+        for (int d = lane; d < hd; d += 64) qs[d] = q[(size_t)h * hd + d];
+    }
     __syncthreads();
     if (t >= T) return;
     float score = 0.f;
@@ -611,6 +706,12 @@ __global__ __launch_bounds__(64) void attn_scores_exact(float* __restrict__ att,
         if (c0) {
 #pragma unroll
             for (int u = 0; u < 8; u++) kv_row16<BITS>(kv[u], kd, ks, t, kh, min(c0 + 16 * u, hd - 16), hd, n_kv);
+        }
+        if (ROPE && own) {
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) kv[u][e] = knew[min(c0 + 16 * u, hd - 16) + e];
         }
 #pragma unroll
         for (int u = 0; u < 8; u++) {
@@ -969,9 +1070,34 @@ size_t ibh_attn_exact_scratch(int n_heads, int max_pos) { return (size_t)n_heads
 // Attention of the current position (read from dpos) over cache rows 0..pos;
 // `att` >= ibh_attn_exact_scratch(n_heads, max_pos) bytes.  head_dim 64, 128
 // or 256; up to 8192 positions.
+static int launch_attn_exact(float* out, const float* q, const void* kdata, const void* vdata, const float* ks,
+                             const float* vs, const int* dpos, int max_pos, int n_heads, int n_kv, int hd, int kv_bits,
+                             float* att, const ExRope* rope, hipStream_t st);
+
 int ibh_launch_attn_exact(float* out, const float* q, const void* kdata, const void* vdata, const float* ks,
                           const float* vs, const int* dpos, int max_pos, int n_heads, int n_kv, int hd, int kv_bits,
                           float* att, hipStream_t st) {
+    return launch_attn_exact(out, q, kdata, vdata, ks, vs, dpos, max_pos, n_heads, n_kv, hd, kv_bits, att, nullptr,
+                             st);
+}
+
+// The same with the position's rotary embedding and KV-cache write done by
+// the scores launch (q, k unrotated; k, v the projections of position
+// *dpos): replaces ibh_launch_rope_kv_write(exact) + ibh_launch_attn_exact.
+int ibh_launch_attn_exact_rope(float* out, const float* q, const float* k, const float* v, const float* table,
+                               void* kdata, void* vdata, float* ks, float* vs, const int* dpos, int max_pos,
+                               int n_heads, int n_kv, int hd, int kv_bits, float* att, hipStream_t st) {
+    if (!k || !v || !table || (kv_bits < 16 && (!ks || !vs))) {
+        ibh_set_error("exact attention + rope: null operand");
+        return IBH_ERROR_PARAM;
+    }
+    const ExRope rp{k, v, table, (uint8_t*)kdata, (uint8_t*)vdata, ks, vs};
+    return launch_attn_exact(out, q, kdata, vdata, ks, vs, dpos, max_pos, n_heads, n_kv, hd, kv_bits, att, &rp, st);
+}
+
+static int launch_attn_exact(float* out, const float* q, const void* kdata, const void* vdata, const float* ks,
+                             const float* vs, const int* dpos, int max_pos, int n_heads, int n_kv, int hd, int kv_bits,
+                             float* att, const ExRope* rope, hipStream_t st) {
     if ((hd != 64 && hd != 128 && hd != 256) || n_heads % n_kv || max_pos + 1 > 8192 ||
         (kv_bits != 32 && kv_bits != 16 && kv_bits != 8 && kv_bits != 4)) {
         ibh_set_error("exact attention: unsupported geometry (head_dim %d, %d positions)", hd, max_pos + 1);
@@ -990,7 +1116,8 @@ int ibh_launch_attn_exact(float* out, const float* q, const void* kdata, const v
         else attn_out_exact<B_, H_, 2><<<n_heads * (H_ / kAoD), kAoThreads, lds, st>>>(out, att, V, vs, dpos, n_heads, n_kv, tstride, tcap); \
     } while (0)
 #define IBH_AE(B_) do { \
-        attn_scores_exact<B_><<<g1, 64, 0, st>>>(att, q, K, ks, dpos, n_heads, n_kv, hd, scale, tstride); \
+        if (rope) attn_scores_exact<B_, true><<<g1, 64, 0, st>>>(att, q, K, ks, dpos, n_heads, n_kv, hd, scale, tstride, *rope); \
+        else attn_scores_exact<B_, false><<<g1, 64, 0, st>>>(att, q, K, ks, dpos, n_heads, n_kv, hd, scale, tstride); \
         if (hd == 64) IBH_AO(B_, 64); else if (hd == 128) IBH_AO(B_, 128); else IBH_AO(B_, 256); \
     } while (0)
     if (kv_bits >= 16) IBH_AE(32); else if (kv_bits == 8) IBH_AE(8); else IBH_AE(4);
