@@ -70,20 +70,31 @@ __global__ __launch_bounds__(256) void prefill_digits(const float* __restrict__ 
         return;
     }
     const float* xr = x + (size_t)b * N;
+    // the row is read once: up to kDR float4 per thread stay in registers
+    // between the max and the digits (longer rows read again from L2)
+    constexpr int kDR = 8;
+    float4 xv[kDR];
     float mx = 0.f;
-    for (int j = threadIdx.x * 4; j < N; j += 1024) {
+#pragma unroll
+    for (int u = 0; u < kDR; u++) {
+        const int j = threadIdx.x * 4 + 1024 * u;
+        xv[u] = j < N ? *(const float4*)(xr + j) : float4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int u = 0; u < kDR; u++)
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(xv[u].x), fabsf(xv[u].y)), fmaxf(fabsf(xv[u].z), fabsf(xv[u].w))));
+    for (int j = threadIdx.x * 4 + 1024 * kDR; j < N; j += 1024) {
         const float4 v = *(const float4*)(xr + j);
         mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     }
-    mx = wave_max(mx);
+    mx = wave_max_dpp(mx);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
     __syncthreads();
     const float gm = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     const float xs = gm > 0.f ? gm / 127.0f : 1.0f;
     const float inv = 1.0f / xs;
     if (threadIdx.x == 0) s[b] = xs;
-    for (int j = threadIdx.x * 4; j < N; j += 1024) {
-        const float4 v = *(const float4*)(xr + j);
+    auto digits = [&](int j, const float4 v) {
         const float e[4] = {v.x, v.y, v.z, v.w};
         uint32_t p0 = 0, p1 = 0, p2 = 0;
 #pragma unroll
@@ -98,7 +109,13 @@ __global__ __launch_bounds__(256) void prefill_digits(const float* __restrict__ 
             p2 |= ((uint32_t)(int)k2 & 0xffu) << (8 * q);
         }
         put(j, p0, p1, p2);
+    };
+#pragma unroll
+    for (int u = 0; u < kDR; u++) {
+        const int j = threadIdx.x * 4 + 1024 * u;
+        if (j < N) digits(j, xv[u]);
     }
+    for (int j = threadIdx.x * 4 + 1024 * kDR; j < N; j += 1024) digits(j, *(const float4*)(xr + j));
 }
 
 template <int KIND>
