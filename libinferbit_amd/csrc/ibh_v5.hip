@@ -449,10 +449,10 @@ __global__ __launch_bounds__(kAttnThreads) void v5_attn_kernel(
                 if (g < GRP) {
                     const float x = act ? sc[h] * scale : -INFINITY;
                     const float mold = gmax[g];
-                    const float mnew = fmaxf(mold, wave_max(x));
+                    const float mnew = fmaxf(mold, wave_max_dpp(x));
                     const float p = act ? __expf(x - mnew) : 0.f;
                     pr[g][lane] = p;
-                    const float sm = wave_sum(p);
+                    const float sm = wave_sum_dpp(p);
                     if (lane == 0) {
                         const float al = __expf(mold - mnew);   // 0 on the first tile
                         galpha[g] = al;
@@ -502,39 +502,44 @@ __global__ __launch_bounds__(kAttnThreads) void v5_attn_kernel(
         }
         return;
     }
+    // the split's partial, stored and later read at agent scope (performed
+    // past the XCD's L2, where every XCD sees it): no L2 writeback or
+    // invalidate is needed, only that this block's stores have completed
+    // (vmcnt 0) before its arrival is counted
     float* pp = part + ((size_t)kvh * NS + sp) * GRP * (HD + 2);
     for (int e = tid; e < GRP * HD; e += kAttnThreads) {
         const int g = e / HD, d = e - g * HD;
         float a = 0.f;
 #pragma unroll
         for (int w = 0; w < NW; w++) a += vred[w][g][d];
-        pp[g * (HD + 2) + 2 + d] = a;
+        __hip_atomic_store(pp + g * (HD + 2) + 2 + d, a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (tid < GRP) {
-        pp[tid * (HD + 2)] = gmax[tid];
-        pp[tid * (HD + 2) + 1] = gsum[tid];
+        __hip_atomic_store(pp + tid * (HD + 2), gmax[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(pp + tid * (HD + 2) + 1, gsum[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    __threadfence();
+    __builtin_amdgcn_s_waitcnt(0x0070);                    // vmcnt(0), lgkmcnt(0)
     __syncthreads();
-    if (tid == 0) last = atomicAdd(&counter[kvh], 1) == nact - 1;
+    if (tid == 0)
+        last = __hip_atomic_fetch_add(&counter[kvh], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nact - 1;
     __syncthreads();
     if (!last) return;
-    __threadfence();   // acquire: the other splits' partials are visible to plain loads
     const float* pk = part + (size_t)kvh * NS * GRP * (HD + 2);
+    auto ld = [](const float* a) { return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
     for (int e = tid; e < GRP * HD; e += kAttnThreads) {
         const int g = e / HD, d = e - g * HD;
         float M = -INFINITY;
-        for (int s2 = 0; s2 < nact; s2++) M = fmaxf(M, pk[((size_t)s2 * GRP + g) * (HD + 2)]);
+        for (int s2 = 0; s2 < nact; s2++) M = fmaxf(M, ld(pk + ((size_t)s2 * GRP + g) * (HD + 2)));
         float L = 0.f, A = 0.f;
         for (int s2 = 0; s2 < nact; s2++) {
             const float* ps = pk + ((size_t)s2 * GRP + g) * (HD + 2);
-            const float w = __expf(ps[0] - M);
-            L = fmaf(ps[1], w, L);
-            A = fmaf(ps[2 + d], w, A);
+            const float w = __expf(ld(ps) - M);
+            L = fmaf(ld(ps + 1), w, L);
+            A = fmaf(ld(ps + 2 + d), w, A);
         }
         out[(size_t)(kvh * GRP + g) * HD + d] = A / L;
     }
-    if (tid == 0) counter[kvh] = 0;
+    if (tid == 0) __hip_atomic_store(&counter[kvh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ib_silu_gate_f32 (src/pq_decode.c:4610-4616).
