@@ -11,10 +11,10 @@
 // rows), C[i][(p, b)], and the epilogue folds
 // y = s_b * (C0 + C1/128 + C2/16384) * scale[i].
 //
-// Block tile 256 rows x 128 tokens (x 3 planes = 384 digit rows), K steps of
-// 64, eight wavefronts in 2 (rows) x 4 (tokens): each owns 128 rows x 32
-// tokens x 3 planes = 8 x 6 tiles of v_mfma_i32_16x16x64_i8, accumulated in
-// VGPRs.  A and B go straight from global memory to a 3-stage LDS ring
+// Block tile 256 (or 224) rows x 128 tokens (x 3 planes = 384 digit rows), K
+// steps of 64, eight wavefronts in 2 (rows) x 4 (tokens): each owns 128 (112)
+// rows x 32 tokens x 3 planes = 8 (7) x 6 tiles of v_mfma_i32_16x16x64_i8,
+// accumulated in VGPRs.  A and B go straight from global memory to a 3-stage LDS ring
 // (global_load_lds_dwordx4, no register staging): the loads for steps s+1 and
 // s+2 are in flight while step s is multiplied.  The digit planes are written
 // tile-contiguous in the LDS layout, so each B stage is one contiguous 24 KB
@@ -118,7 +118,11 @@ __global__ __launch_bounds__(256) void prefill_digits(const float* __restrict__ 
     for (int j = threadIdx.x * 4 + 1024 * kDR; j < N; j += 1024) digits(j, *(const float4*)(xr + j));
 }
 
-template <int KIND>
+// NA = A tiles per wavefront: the block covers 32 NA rows (NA = 8: 256 rows;
+// NA = 7: 224 rows, so 14336 rows x 4 token tiles make exactly 256 blocks).
+// The LDS A region is always 256 rows; with NA = 7 its last two groups are
+// filled (to keep every wave's load count uniform) but never read.
+template <int KIND, int NA>
 __global__ __launch_bounds__(kGemmThreads) void gemm_i8_digits(float* __restrict__ y, const int8_t* __restrict__ W,
                                                                const void* __restrict__ sc,
                                                                const int8_t* __restrict__ dig,
@@ -133,7 +137,8 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_i8_digits(float* __restrict
     const int L = blockIdx.x;
     const int xcd = L & 7, q = L >> 3;
     const int rt = (q / NT) * 8 + xcd, tt = q % NT;
-    const int row0 = rt * kBM, tok0 = tt * kBT;
+    constexpr int TM = 32 * NA;
+    const int row0 = rt * TM, tok0 = tt * kBT;
     if (row0 >= M) return;
     const int nsteps = N / kBK;
 
@@ -155,12 +160,12 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_i8_digits(float* __restrict
     }
     // Operand reads: A tile a is rows wm*128 + 16a + l % 16 at chunk l / 16;
     // B tile (p, h) is digit row group p*8 + wn*2 + h, lane l at 16 l.
-    const int ao = (wm * 128 + (lane & 15)) * kBK + 16 * (lane >> 4);
+    const int ao = (wm * 16 * NA + (lane & 15)) * kBK + 16 * (lane >> 4);
     const int bo = kBM * kBK + wn * 2 * 1024 + 16 * lane;
 
-    i4_t acc[8][6];
+    i4_t acc[NA][6];
 #pragma unroll
-    for (int a = 0; a < 8; a++)
+    for (int a = 0; a < NA; a++)
 #pragma unroll
         for (int c = 0; c < 6; c++) acc[a][c] = i4_t{0, 0, 0, 0};
 
@@ -196,11 +201,11 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_i8_digits(float* __restrict
         for (int c = 0; c < 6; c++) bv[c] = *(const i4_t*)(sb + bo + ((c >> 1) * 8 + (c & 1)) * 1024);
         i4_t av = *(const i4_t*)(sb + ao);
 #pragma unroll
-        for (int a = 0; a < 8; a++) {
+        for (int a = 0; a < NA; a++) {
             acc[a][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv[0], acc[a][0], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
             i4_t an = av;
-            if (a < 7) an = *(const i4_t*)(sb + ao + (a + 1) * 16 * kBK);
+            if (a < NA - 1) an = *(const i4_t*)(sb + ao + (a + 1) * 16 * kBK);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int c = 1; c < 6; c++) acc[a][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv[c], acc[a][c], 0, 0, 0);
@@ -220,9 +225,9 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_i8_digits(float* __restrict
         if (b >= B) continue;
         const float sb = s[b];
 #pragma unroll
-        for (int a = 0; a < 8; a++) {
+        for (int a = 0; a < NA; a++) {
             const i4_t c0 = acc[a][h], c1 = acc[a][2 + h], c2 = acc[a][4 + h];
-            const int i0 = row0 + wm * 128 + a * 16 + 4 * g;
+            const int i0 = row0 + wm * 16 * NA + a * 16 + 4 * g;
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int i = i0 + r;
@@ -272,13 +277,20 @@ extern "C" int ibh_gemm_int8(float* out, const void* w, const void* scales, int 
     const int NT = (B + kBT - 1) / kBT;
     prefill_digits<<<NT * kBT, 256, 0, st>>>(x, dig, s, B, N);
     IBH_CHECK_LAUNCH("ibh_gemm_int8 (digits)");
-    const int RT = ((M + kBM - 1) / kBM + 7) / 8 * 8;        // row tiles, padded to the 8 XCDs
-    const int grid = RT * NT;
+    // Row tile of 256 or 224 rows: whichever finishes in fewer rows of work
+    // per CU (rounds of 256 blocks x rows per block), 256 on a tie.
+    auto rtiles = [&](int tm) { return ((M + tm - 1) / tm + 7) / 8 * 8; };  // padded to the 8 XCDs
+    auto cost = [&](int tm) { return (long)((rtiles(tm) * NT + 255) / 256) * tm; };
+    const bool narrow = cost(224) < cost(256);
+    const int grid = rtiles(narrow ? 224 : 256) * NT;
     const int8_t* W = (const int8_t*)w;
-    if (scale_kind == IBH_SCALE_F16)
-        gemm_i8_digits<IBH_SCALE_F16><<<grid, kGemmThreads, 0, st>>>(out, W, scales, dig, s, M, N, B, M_stride, NT);
-    else
-        gemm_i8_digits<IBH_SCALE_F32><<<grid, kGemmThreads, 0, st>>>(out, W, scales, dig, s, M, N, B, M_stride, NT);
+#define IBH_GEMM_LAUNCH(K, NA) gemm_i8_digits<K, NA><<<grid, kGemmThreads, 0, st>>>(out, W, scales, dig, s, M, N, B, M_stride, NT)
+    if (scale_kind == IBH_SCALE_F16) {
+        if (narrow) IBH_GEMM_LAUNCH(IBH_SCALE_F16, 7); else IBH_GEMM_LAUNCH(IBH_SCALE_F16, 8);
+    } else {
+        if (narrow) IBH_GEMM_LAUNCH(IBH_SCALE_F32, 7); else IBH_GEMM_LAUNCH(IBH_SCALE_F32, 8);
+    }
+#undef IBH_GEMM_LAUNCH
     IBH_CHECK_LAUNCH("ibh_gemm_int8");
     return IBH_OK;
 }

@@ -34,7 +34,10 @@ def run(ops, w, s, x, M_stride=None):
     return out.cpu().numpy()
 
 
-@pytest.mark.parametrize("M,N,B", [(128, 64, 64), (300, 256, 70), (37, 192, 5), (1000, 2048, 130), (256, 4096, 1)])
+# (16384, 64, 400) takes the 256-row tile (more than 256 blocks at 224 rows),
+# every other case the 224-row tile.
+@pytest.mark.parametrize("M,N,B", [(128, 64, 64), (300, 256, 70), (37, 192, 5), (1000, 2048, 130), (256, 4096, 1),
+                                   (16384, 64, 400)])
 def test_gemm_small_vs_oracle(ops, oracle_lib, M, N, B):
     print(f"case gemm M={M} N={N} B={B}", flush=True)
     rng = np.random.default_rng(M + N + B)
