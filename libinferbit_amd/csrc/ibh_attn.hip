@@ -841,20 +841,22 @@ __global__ __launch_bounds__(kSplitThreads) void attn_split(float* __restrict__ 
 }
 
 // Merge of one head's chunks: out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c.
-// 1024 threads: thread (chunk class cq, dim d) holds chunks c = cq (mod
-// 1024/HD), every load of the block issued at once.
-template <int HD>
+// Block (head, slice of DS dims), 1024 threads: thread (chunk class cq, dim
+// d) holds chunks c = cq (mod 1024/DS), every load of the block issued at
+// once.  Slicing the dims spreads a head's partials over HD/DS blocks (the
+// weights e^(m_c - M) are recomputed by each).
+template <int HD, int DS = 32>
 __global__ __launch_bounds__(1024) void attn_merge_wide(float* __restrict__ out, const float* __restrict__ part,
                                                         int T, const int* __restrict__ dpos, int ct, int nstride,
                                                         int rope) {
-    constexpr int NCQ = 1024 / HD;                        // chunk classes
+    constexpr int NCQ = 1024 / DS;                        // chunk classes
     constexpr int PER = kSplitMaxChunks / NCQ;            // chunks per thread at most
     __shared__ float wm[kSplitMaxChunks], wl[kSplitMaxChunks];
-    __shared__ float osum[NCQ][HD];
+    __shared__ float osum[NCQ][DS];
     __shared__ float tot;
     const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float* ph = part + (size_t)h * nstride * (HD + 2);
-    const int cq = tid / HD, d = tid % HD;
+    const int cq = tid / DS, d = blockIdx.y * DS + tid % DS;
     // every slot of the head is loaded before the position is known (slots
     // past the last chunk hold stale values that are never used), so the
     // partials' loads do not wait for dpos
@@ -893,13 +895,13 @@ __global__ __launch_bounds__(1024) void attn_merge_wide(float* __restrict__ out,
 #pragma unroll
     for (int u = 0; u < PER; u++)
         if (u < per && cq + NCQ * u < nch) o = fmaf(wm[cq + NCQ * u], v[u], o);
-    osum[cq][d] = o;
+    osum[cq][tid % DS] = o;
     __syncthreads();
-    if (tid < HD) {
+    if (tid < DS) {
         float r = 0.f;
 #pragma unroll
         for (int k = 0; k < NCQ; k++) r += osum[k][tid];
-        out[(size_t)h * HD + tid] = r / tot;
+        out[(size_t)h * HD + blockIdx.y * DS + tid] = r / tot;
     }
 }
 
@@ -933,7 +935,7 @@ int launch_split(float* out, float* part, const float* q, const void* kdata, con
         else attn_split<B_, G_, H_, false><<<dim3(n_kv, nchunk), kSplitThreads, 0, st>>>( \
                  out, part, q, K, V, kscales, vscales, T, dpos, n_kv, scale, nstride, rp); \
         IBH_CHECK_LAUNCH("ibh_attn_decode (split)"); \
-        attn_merge_wide<H_><<<n_heads, 1024, 0, st>>>(out, part, T, dpos, ct, nstride, rope ? 1 : 0); } while (0)
+        attn_merge_wide<H_><<<dim3(n_heads, H_ / 32), 1024, 0, st>>>(out, part, T, dpos, ct, nstride, rope ? 1 : 0); } while (0)
 #define IBH_ASG(B_, H_) do { if (grp == 1) IBH_AS(B_, 1, H_); else if (grp == 2) IBH_AS(B_, 2, H_); \
                          else if (grp == 4) IBH_AS(B_, 4, H_); else IBH_AS(B_, 8, H_); } while (0)
 #define IBH_ASH(B_) do { if (head_dim == 64) IBH_ASG(B_, 64); else IBH_ASG(B_, 128); } while (0)
