@@ -802,7 +802,12 @@ __global__ __launch_bounds__(kSplitThreads) void attn_split(float* __restrict__ 
     {
         const int dq = tid % NDQ, g = (tid / NDQ) % GRP, tr = tid / (NDQ * GRP);
         float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-        for (int tt = tr; tt < tn; tt += TR) {
+        // fixed trip count (CT / TR), so the LDS reads of every position
+        // are issued ahead of the fma chain; same order as a tt < tn loop
+#pragma unroll
+        for (int i = 0; i < CT / TR; i++) {
+            const int tt = tr + TR * i;
+            if (tt >= tn) break;
             const float pw = sc[g][tt] * vsc[tt];
             float v[4];
             if constexpr (BITS == 32) {
