@@ -500,7 +500,19 @@ int ibh_launch_tile_x_multi(const MatDesc* d, int n, int kind, const float* x, i
     // quads per block: about one block per CU (256), within 16 wavefronts
     const int wq_max = (kTileMaxWaves - nxw) / KW;
     if (wq_max < 1) return 0;
-    int WQ = std::min(wq_max, std::max(1, (quads + 255) / 256));
+    // Start from ~one block per CU, then take the WQ (from half of that up)
+    // with the least rows per CU: rounds of 256 blocks x rows per block.
+    // Several matrices of one launch each round their own block count up,
+    // which can spill one block past 256 (q/k/v at 6144 rows: 257 blocks at
+    // WQ 6, 221 at WQ 7); a long row set can also balance its last round
+    // better with smaller blocks (32000 rows: WQ 8 before WQ 14).
+    const int wq0 = std::min(wq_max, std::max(1, (quads + 255) / 256));
+    int WQ = wq0;
+    long best = -1;
+    for (int wq = wq_max; wq >= std::max(1, wq0 / 2 + 1); wq--) {
+        const long cost = (long)((rowset_blocks(d, n, 4 * wq) + 255) / 256) * wq;
+        if (best < 0 || cost < best) { best = cost; WQ = wq; }
+    }
     if (g_tile_mode > 0 && g_tile_WR) WQ = std::min(g_tile_WR, wq_max);
     const int nthreads = 64 * (nxw + WQ * KW);
     // Weight wavefronts hold their loads back ~0.1 us per unit so that the
