@@ -208,9 +208,18 @@ __global__ __launch_bounds__(1024) void argmax_advance_kernel(const float* __res
     __shared__ int bi[16];
     float best = -INFINITY;
     int idx = 0x7fffffff;
-    for (int i = threadIdx.x; i < n; i += 1024) {
-        const float v = logits[i];   // NaN never wins, like `>` in the reference
-        if ((idx == 0x7fffffff && !(v != v)) || v > best) { best = v; idx = i; }
+    // 32 loads per thread issued together, then compared in index order
+    // (one memory round trip per 32768 logits instead of one per 1024)
+    for (int i0 = threadIdx.x; i0 < n; i0 += 32 * 1024) {
+        float v[32];
+#pragma unroll
+        for (int u = 0; u < 32; u++) v[u] = i0 + 1024 * u < n ? logits[i0 + 1024 * u] : 0.f;
+#pragma unroll
+        for (int u = 0; u < 32; u++) {
+            const int i = i0 + 1024 * u;
+            // NaN never wins, like `>` in the reference
+            if (i < n && ((idx == 0x7fffffff && !(v[u] != v[u])) || v[u] > best)) { best = v[u]; idx = i; }
+        }
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
