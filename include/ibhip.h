@@ -61,6 +61,14 @@ int         ibh_device_free(void* dptr);
 int         ibh_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream);
 int         ibh_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream);
 int         ibh_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
+/* Device-side errors raised since the last clear, on the current device:
+ * a bitmask of IBH_DEVERR_* (0 = none), negative if it cannot be read.  A
+ * kernel that raises one has written NaN into the outputs it could not
+ * vouch for.  Waits for the device; clear != 0 resets the bits.  No
+ * reference counterpart (the CPU kernels have no such failure). */
+#define IBH_DEVERR_TILE_WAIT 1   /* a bounded wait inside the tile GEMV expired */
+#define IBH_DEVERR_PQ_WS     2   /* a PQ workspace that ibh_pq_workspace_init did not prepare */
+int         ibh_device_errors(int clear);
 
 /* ── quantized matvec, device pointers ─────────────────────── */
 
@@ -88,6 +96,12 @@ int ibh_set_tile_config(int mode, int KS, int WR, int delay);
  * reads `bytes` of `buf` once with 16-byte loads, 1 KB contiguous per
  * instruction (the streaming rate a matvec of that size is judged against). */
 int ibh_probe(int mode, const void* buf, size_t bytes, void* stream);
+/* The read of mode 1 with the launch shape as parameters: `blocks` blocks of
+ * `threads` threads (64..1024), each block reading a contiguous share,
+ * `per_lane` 16-byte loads (1/2/4/8/16) in flight per lane, nontemporal or
+ * ordinary loads.  bytes a multiple of 16.  No reference counterpart. */
+int ibh_probe_read(int blocks, int threads, int per_lane, int nontemporal, const void* buf, size_t bytes,
+                   void* stream);
 
 /* Per-128-group int8 activation quantization, bit-identical to
  * ib_quantize_input_int8_g128 (src/threading.c:401-432).  q[N], s[ceil(N/128)]. */
@@ -160,21 +174,24 @@ size_t ibh_attn_workspace_bytes(int n_heads, int head_dim, int n_pos);
 int ibh_attn_decode(float* out, const float* q, const void* kdata, const void* vdata,
                     const float* kscales, const float* vscales, int pos, int n_heads, int n_kv,
                     int head_dim, int kv_bits, void* ws, size_t ws_bytes, void* stream);
-/* head_dim 64 or 128, fp32 / int8 / int4 caches and <= 64 KV heads run in
- * one launch whose chunk blocks meet through per-KV-head arrival counters in
- * device memory (back to zero after every call): attention calls that
- * overlap on one GPU (different streams) race, as calls sharing a workspace
- * already do.  Development switch (no counterpart in the reference): 0 sends
- * them through the chunk + merge kernels, 1 (default) the one launch. */
+/* head_dim 64 or 128, fp32 / int8 / int4 caches and <= 64 KV heads run as
+ * a 1024-thread split kernel (all chunks of a KV head group in flight) and a
+ * wide merge; calls sharing a workspace must not overlap in time.
+ * Development switch (no counterpart in the reference): 0 sends them through
+ * the 256-thread chunk + merge kernels, 1 (default) the split kernels. */
 int ibh_attn_set_split(int on);
 
 /* ── product-quantised LUT matvec, device pointers ─────────── */
 
-/* Device-resident mirror of ib_pq_tensor (src/pq_decode.h:39-87): same
- * fields and array layouts, pointers into device memory.  inner_cols (the
- * N - n_outlier non-outlier columns in increasing order, which
- * matmul_impl rebuilds on every call at src/pq_decode.c:1538-1546) is
- * computed once at upload; it may be NULL when n_outlier == 0. */
+/* Device-side description of a PQ tensor: the arrays of ib_pq_tensor
+ * (src/pq_decode.h:39-87) with the same array layouts, pointers into device
+ * memory, but NOT the same struct layout (no rotate, l2_packed_bits or
+ * backing-storage fields; format and C sit elsewhere).  A caller holding a
+ * reference ib_pq_tensor uses ibh_pq_matmul_fp32_host below, which takes
+ * that struct as it is.  inner_cols (the N - n_outlier non-outlier columns
+ * in increasing order, which matmul_impl rebuilds on every call at
+ * src/pq_decode.c:1538-1546) is computed once at upload; it may be NULL when
+ * n_outlier == 0. */
 typedef struct {
     int M, N, G, K, K_l2, n_levels, n_outlier, C, l2_idx_bytes;
     const uint16_t *codebook_l1_l, *codebook_l1_r, *codebook_l2_l, *codebook_l2_r;
@@ -208,11 +225,20 @@ typedef struct {
  * differs.  Returns 0 / negative like the reference (plus a message).
  * `ws` >= ibh_pq_workspace_bytes(t) bytes, NULL = library workspace.
  * Single-level work (one level, or level 1 only) with G <= 16 and K <= 256
- * runs in one launch whose blocks meet through per-row-tile arrival counters
- * kept in device memory (they return to zero at the end of every call): PQ
- * calls that overlap on one GPU (different streams) race, as calls sharing
- * a workspace already do. */
+ * runs in one launch whose blocks meet through one 64-bit word per row kept
+ * at the front of the workspace (they return to zero at the end of every
+ * call).  A caller workspace must be prepared ONCE, before its first use,
+ * by ibh_pq_workspace_init; it then stays usable by every PQ call of any
+ * tensor on that stream, but must not hold other data in between.  An
+ * unprepared one gives NaN rows and IBH_DEVERR_PQ_WS (ibh_device_errors).
+ * Calls that share a workspace must not overlap in time; different
+ * workspaces are independent.  A non-finite x gives NaN rows on this path
+ * (the CPU gives +-Inf or NaN). */
 size_t ibh_pq_workspace_bytes(const ibh_pq_tensor* t);
+/* Stamps a caller PQ workspace and zeroes its row words (a kernel on
+ * `stream`, so it may sit in a captured graph).  ws 256-byte aligned,
+ * ws_bytes >= 1 MB + 256.  No reference counterpart. */
+int    ibh_pq_workspace_init(void* ws, size_t ws_bytes, void* stream);
 int    ibh_pq_matmul(const ibh_pq_tensor* t, const float* x, float* out, void* ws,
                      size_t ws_bytes, void* stream);
 /* The PQ session's default variant: ib_pq_matmul_fp32_streaming_cached
@@ -515,6 +541,40 @@ int  ibh_host_attn(const void* cache, const void* kdata, const void* vdata, cons
                    int n_heads, int n_kv, int head_dim);
 /* Frees the device mirror of `cache` (from inferbit_free, src/model.c:42-107). */
 void ibh_host_kv_release(const void* cache);
+
+/* Layout-identical mirror of the reference's ib_pq_tensor
+ * (src/pq_decode.h:39-87; `format` is the ib_pq_format enum, an int): a
+ * reference build passes its own ib_pq_tensor* where this is expected. */
+typedef struct {
+    int M, N, G, K, K_l2, n_levels, rotate, n_outlier;
+    int format;
+    uint16_t *codebook_l1_l, *codebook_l1_r, *codebook_l2_l, *codebook_l2_r;
+    uint8_t *indices_l1_l, *indices_l1_r, *indices_l2_l, *indices_l2_r;
+    int C, l2_idx_bytes, l2_packed_bits;
+    uint16_t* row_scale;
+    int32_t* outlier_cols;
+    int8_t* outlier_sidecar;
+    uint16_t* outlier_scale;
+    void* _arena;
+    size_t _arena_size;
+    void* _mmap_base;
+    size_t _mmap_size;
+    int _owns_mmap;
+} ibh_ref_pq_tensor;
+
+/* Twin of int ib_pq_matmul_fp32(const ib_pq_tensor* t, const float* x,
+ * float* out) (src/pq_decode.h:197, src/pq_decode.c:1684-1686 ->
+ * matmul_impl 1504-1682), same signature and host pointers: out[M] = W x
+ * with the reference's chunk-skipping rule, tables, gather, row scale and
+ * outlier sidecar (fp32 summation order differs, rel-err <= 1e-4).  x is in
+ * the rotated basis when t->rotate, as for the reference.  The first call
+ * on a tensor builds its device copy (arrays inside a region registered
+ * with ibh_register_host_weights are used in place, the rest uploaded
+ * once); later calls stage only x and out.  Returns 0, or -1 with a message
+ * in ibh_last_error (the reference returns -1 without one). */
+int  ibh_pq_matmul_fp32_host(const ibh_ref_pq_tensor* t, const float* x, float* out);
+/* Frees the device copy of `t` (called from ib_pq_free, src/pq_decode.c:376-387). */
+void ibh_pq_host_release(const ibh_ref_pq_tensor* t);
 
 #ifdef __cplusplus
 }

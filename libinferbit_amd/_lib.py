@@ -27,6 +27,7 @@ SIGNATURES = {
     "ibh_matmul": (I, [P, P, P, I, P, I, I, I, P]),
     "ibh_set_tile_config": (I, [I, I, I, I]),
     "ibh_probe": (I, [I, P, SZ, P]),
+    "ibh_probe_read": (I, [I, I, I, I, P, SZ, P]),
     "ibh_matmul_w4a8_x_noalloc": (I, [P, P, P, I, P, I, I, P]),
     "ibh_quantize_act_g128": (I, [P, P, P, I, P]),
     "ibh_matmul_w4a8": (I, [P, P, P, I, P, P, I, I, P]),
@@ -40,6 +41,10 @@ SIGNATURES = {
     "ibh_attn_decode": (I, [P, P, P, P, P, P, I, I, I, I, I, P, SZ, P]),
     "ibh_attn_set_split": (I, [I]),
     "ibh_pq_workspace_bytes": (SZ, [P]),
+    "ibh_pq_workspace_init": (I, [P, SZ, P]),
+    "ibh_pq_matmul_fp32_host": (I, [P, P, P]),
+    "ibh_pq_host_release": (None, [P]),
+    "ibh_device_errors": (I, [I]),
     "ibh_pq_matmul": (I, [P, P, P, P, SZ, P]),
     "ibh_pq_set_fused": (I, [I]),
     "ibh_pq_matmul_streaming": (I, [P, P, P, P, SZ, P]),

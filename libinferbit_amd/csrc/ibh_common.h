@@ -6,6 +6,17 @@
 
 #include "../../include/ibhip.h"
 
+// Every kernel here is written for gfx950 (MI355X).  Some cross-block
+// hand-offs rely on its memory system rather than on the C++ memory model:
+// a relaxed agent-scope store or atomic is performed at the device-coherent
+// level (past the XCD's L2), and s_waitcnt vmcnt(0) before a later atomic
+// means those stores are done, so a block that sees the atomic's result and
+// reads with agent-scope loads sees them.  Another target must re-check
+// that (or use release/acquire): refuse to build for one.
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "libinferbit_amd kernels target gfx950 only"
+#endif
+
 // ── host-side error plumbing (ibh_runtime.hip) ─────────────────────────────
 extern "C" void ibh_set_error(const char* fmt, ...);
 hipStream_t ibh_resolve_stream(void* s);
@@ -27,6 +38,13 @@ hipStream_t ibh_resolve_stream(void* s);
             return IBH_ERROR_INTERNAL;                                          \
         }                                                                       \
     } while (0)
+
+// Device-side error bits: kernels that can give up on a bounded wait, or
+// that find a workspace they cannot trust, write NaN outputs and OR a bit
+// into their file's error word (bits IBH_DEVERR_*); ibh_device_errors
+// collects them.
+int ibh_tile_errors(bool clear);
+int ibh_pq_errors(bool clear);
 
 // ── device helpers ─────────────────────────────────────────────────────────
 namespace ibh {

@@ -362,8 +362,9 @@ __global__ __launch_bounds__(kThreads) void pq_reduce(PqDev t, const float* __re
 //     v_mfma_f32_32x32x16_f16 with A = [cb | cb] (the fp16 codewords, exact)
 //     and B = [x_hi ; x_lo], x scaled per (chunk, side) by a power of two
 //     (exact) and split into two fp16 parts; products are exact and sums
-//     fp32, so an entry carries ~2^-22 of its chunk's max|x| (the CPU's fp32
-//     table sum carries ~2^-24 per term).
+//     fp32.  x is scaled by one power of two per slab (2^-e, e the exponent
+//     of the slab's max|x|), so an entry carries ~2^-22 of the SLAB's max|x|
+//     (the CPU's fp32 table sum carries ~2^-24 per term).
 //  3. Max|x| over the inner columns (the skipping rule of
 //     pq_decode.c:1569-1616), the slab's chunk maxima, max|codeword|.
 //  4. Gather: 32 LDS lookups per thread, the row's two partials summed.
@@ -376,13 +377,24 @@ __global__ __launch_bounds__(kThreads) void pq_reduce(PqDev t, const float* __re
 //     count has the whole row in the returned value: it applies the row scale
 //     and the outliers, writes y and clears the word for the next call.
 //     Integer addition is associative: y does not depend on arrival order.
+//     The words belong to the caller's workspace (its first 1 MB + 256 B),
+//     zeroed once by ibh_pq_workspace_init, which also writes a stamp the
+//     kernel checks: a workspace without it gives NaN rows and raises
+//     IBH_DEVERR_PQ_WS instead of adding into unknown words.  Calls on the
+//     library workspace (ws == NULL) use a library array of words.
+//     A non-finite x (or a bound that overflows) would make the fixed-point
+//     terms meaningless: every slab then writes NaN to its rows (the CPU
+//     gives +-Inf or NaN there).
 constexpr int kFThreads = 1024;
 constexpr int kFRows = 512;
 constexpr int kFCS = 32;
 constexpr int kFMaxS = 63;
 constexpr int kFMaxRows = 131072;
 constexpr int kXS = 20;   // LDS floats per slab chunk: 8 per side (zero padded) + 4 (bank spread)
-__device__ unsigned long long pq_row_acc[kFMaxRows];   // zero at load; each row's last slab clears it
+__device__ unsigned long long pq_row_acc[kFMaxRows];   // ws == NULL calls: zero at load, each row's last slab clears it
+__device__ unsigned int ibh_pq_err;                    // IBH_DEVERR_* bits of this file's kernels
+constexpr unsigned long long kPqStamp = 0x49424850515753ull;   // "IBHPQWS"
+constexpr size_t kPqFront = 256 + (size_t)kFMaxRows * 8;       // stamp + row words at the front of a caller workspace
 
 // Phase probes, compiled only with -DIBH_PQ_TRACE (a development build
 // outside the library): s_memrealtime of thread 0 of each block.
@@ -448,7 +460,8 @@ __device__ __forceinline__ void table_tile(const PqDev& t, const h8_t* cbs, cons
 
 template <bool KA>   // K % 32 == 0: every table row of a tile is stored
 __global__ __launch_bounds__(kFThreads) void pq_fused(PqDev t, const float* __restrict__ x, float* __restrict__ out,
-                                                      int S) {
+                                                      int S, unsigned long long* __restrict__ racc,
+                                                      const unsigned long long* __restrict__ hdr) {
     constexpr int CS = kFCS;
     extern __shared__ __align__(16) float T[];            // [CS][TS]
     __shared__ float red[kFThreads / 64], redc[kFThreads / 64];
@@ -470,6 +483,14 @@ __global__ __launch_bounds__(kFThreads) void pq_fused(PqDev t, const float* __re
     const int q = tid & 1;
     const int r = rt * kFRows + (tid >> 1);
     const int row = min(r, M - 1);
+    // the workspace stamp (caller workspaces): its address, and the magic
+    const bool wsok = !hdr || (hdr[0] == kPqStamp && hdr[1] == (unsigned long long)(uintptr_t)hdr);
+    if (S > 1 && !wsok) {
+        if (q == 0 && r < M) out[r] = __builtin_nanf("");
+        if (tid == 0) __hip_atomic_fetch_or(&ibh_pq_err, (unsigned)IBH_DEVERR_PQ_WS, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    unsigned long long* const words = racc ? racc : pq_row_acc;
 
     // 1. loads: the slab's x, the codebooks, x for the max|x| scan, the index
     // bytes (in the order they are needed; loads complete in issue order)
@@ -552,24 +573,33 @@ __global__ __launch_bounds__(kFThreads) void pq_fused(PqDev t, const float* __re
         table_tile<KA, CS>(t, cbs, xsl, it, KT, CT, cn, lane, TS, xscale, T, cmax_s);
     PQ_TT(1);
     // max|x| over the inner columns (the skipping rule's reference)
+    // (fmaxf drops NaN, so non-finite inputs are flagged on their own)
     float mx = 0.f;
+    bool nonfin = false;
     if (x4ok) {
 #pragma unroll
-        for (int u = 0; u < 4; u++)
-            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(xs4[u].x), fabsf(xs4[u].y)), fmaxf(fabsf(xs4[u].z), fabsf(xs4[u].w))));
+        for (int u = 0; u < 4; u++) {
+            const float a = fmaxf(fmaxf(fabsf(xs4[u].x), fabsf(xs4[u].y)), fmaxf(fabsf(xs4[u].z), fabsf(xs4[u].w)));
+            mx = fmaxf(mx, a);
+            nonfin |= !(fabsf(xs4[u].x) <= 3.4e38f && fabsf(xs4[u].y) <= 3.4e38f && fabsf(xs4[u].z) <= 3.4e38f &&
+                        fabsf(xs4[u].w) <= 3.4e38f);
+        }
     } else {
         for (int j0 = 0; j0 < ninner; j0 += 16 * kFThreads) {
             float v[16];
 #pragma unroll
             for (int u = 0; u < 16; u++) v[u] = x[inner_col(t, min(j0 + u * kFThreads + tid, ninner - 1))];
 #pragma unroll
-            for (int u = 0; u < 16; u++) mx = fmaxf(mx, fabsf(v[u]));
+            for (int u = 0; u < 16; u++) {
+                mx = fmaxf(mx, fabsf(v[u]));
+                nonfin |= !(fabsf(v[u]) <= 3.4e38f);
+            }
         }
     }
     mx = wave_max_dpp(mx);
     __syncthreads();                                       // tables done; red[] read above
     if (lane == 0) red[wave] = mx;
-    __syncthreads();
+    const bool x_nonfinite = __syncthreads_or(nonfin) != 0;
     float gmax = 0.f;
 #pragma unroll
     for (int w = 0; w < kFThreads / 64; w++) gmax = fmaxf(gmax, red[w]);
@@ -622,8 +652,17 @@ __global__ __launch_bounds__(kFThreads) void pq_fused(PqDev t, const float* __re
     bool fin = own;
     float sum = ldexpf(acc, ex);
     const uint16_t rs_bits = t.row_scale[row];   // in flight with the atomic below
+    if (S > 1) {
+        // 2^qe maps 2 * N_inner * max|cb| * max|x| (a bound on |row sum|) to
+        // <= 2^50; the same on every slab (cbmax, gmax and the flag are over
+        // the whole tensor), so either every slab adds or none does
+        const float bound = 2.0f * (float)ninner * cbmax * gmax;
+        if (x_nonfinite || !(bound <= 3.4e38f)) {
+            if (own) out[r] = __builtin_nanf("");
+            return;
+        }
+    }
     if (S > 1 && own) {
-        // 2^qe maps 2 * N_inner * max|cb| * max|x| (a bound on |row sum|) to <= 2^50
         const float bound = 2.0f * (float)ninner * cbmax * gmax;
         int eb = 0;
         if (bound > 0.f) frexpf(bound, &eb);               // bound < 2^eb
@@ -631,13 +670,13 @@ __global__ __launch_bounds__(kFThreads) void pq_fused(PqDev t, const float* __re
         const long long v = llrint((double)acc * ldexp(1.0, qe + ex));
         const unsigned long long add = (1ull << 58) + (unsigned long long)(v + (1ll << 50));
         const unsigned long long old =
-            __hip_atomic_fetch_add(&pq_row_acc[r], add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(&words[r], add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const unsigned long long tot = old + add;
         fin = (tot >> 58) == (unsigned long long)S;
         if (fin) {
             const long long val = (long long)(tot & ((1ull << 58) - 1)) - (long long)S * (1ll << 50);
             sum = (float)((double)val * ldexp(1.0, -qe));
-            __hip_atomic_store(&pq_row_acc[r], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&words[r], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
     PQ_TT(4);
@@ -930,7 +969,8 @@ struct PqWs {
     size_t tab1, tab2, part, cmax, cnorm, c2max, need;
 };
 
-static int pq_geometry(const ibh_pq_tensor_abi* t, int* CS, int* nslabs, size_t* lds, PqWs* w) {
+// front: the stamp and row words of a caller workspace come first
+static int pq_geometry(const ibh_pq_tensor_abi* t, int* CS, int* nslabs, size_t* lds, PqWs* w, bool front = true) {
     const bool two = t->n_levels == 2;
     const int K2 = t->K_l2 > 0 ? t->K_l2 : t->K;
     int cs = 16;
@@ -941,8 +981,8 @@ static int pq_geometry(const ibh_pq_tensor_abi* t, int* CS, int* nslabs, size_t*
     *nslabs = (t->C + cs - 1) / cs;
     *lds = need(cs);
     auto al = [](size_t v) { return (v + 255) / 256 * 256; };
-    w->tab1 = 0;
-    w->tab2 = al((size_t)t->C * 2 * t->K * 4);
+    w->tab1 = front ? kPqFront : 0;
+    w->tab2 = w->tab1 + al((size_t)t->C * 2 * t->K * 4);
     w->part = w->tab2 + (two ? al((size_t)t->C * 2 * K2 * 4) : 0);
     w->cmax = w->part + al((size_t)(*nslabs) * t->M * sizeof(float));
     w->cnorm = w->cmax + al((size_t)t->C * sizeof(float));
@@ -951,12 +991,44 @@ static int pq_geometry(const ibh_pq_tensor_abi* t, int* CS, int* nslabs, size_t*
     return IBH_OK;
 }
 
-extern "C" size_t ibh_pq_workspace_bytes(const ibh_pq_tensor_abi* t) {
+namespace {
+// The stamp of a caller workspace and zero row words (a fill kernel, not a
+// memset, so that a captured graph may hold it).
+__global__ void pq_ws_init(unsigned long long* __restrict__ w) {
+    const size_t n = kPqFront / 8;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        w[i] = i == 0 ? kPqStamp : (i == 1 ? (unsigned long long)(uintptr_t)w : 0ull);
+}
+}  // namespace
+
+extern "C" int ibh_pq_workspace_init(void* ws, size_t ws_bytes, void* stream) {
+    if (!ws || ws_bytes < kPqFront || ((uintptr_t)ws & 255)) {
+        ibh_set_error("ibh_pq_workspace_init: need a 256-byte aligned workspace of >= %zu bytes", kPqFront);
+        return IBH_ERROR_PARAM;
+    }
+    pq_ws_init<<<256, 256, 0, ibh_resolve_stream(stream)>>>((unsigned long long*)ws);
+    IBH_CHECK_LAUNCH("ibh_pq_workspace_init");
+    return IBH_OK;
+}
+
+int ibh_pq_errors(bool clear) {
+    unsigned int v = 0;
+    if (hipMemcpyFromSymbol(&v, HIP_SYMBOL(ibh_pq_err), sizeof(v)) != hipSuccess) return -1;
+    if (clear && v) {
+        const unsigned int z = 0;
+        if (hipMemcpyToSymbol(HIP_SYMBOL(ibh_pq_err), &z, sizeof(z)) != hipSuccess) return -1;
+    }
+    return (int)v;
+}
+
+static size_t pq_ws_need(const ibh_pq_tensor_abi* t, bool front) {
     int cs, ns;
     size_t lds;
     PqWs w;
-    return t && pq_geometry(t, &cs, &ns, &lds, &w) == IBH_OK ? w.need : 0;
+    return t && pq_geometry(t, &cs, &ns, &lds, &w, front) == IBH_OK ? w.need : 0;
 }
+
+extern "C" size_t ibh_pq_workspace_bytes(const ibh_pq_tensor_abi* t) { return pq_ws_need(t, true); }
 
 namespace {
 struct PqMode {
@@ -1004,8 +1076,9 @@ __global__ __launch_bounds__(kThreads) void pq_tq8(float* __restrict__ tab1, flo
 }
 }  // namespace
 
+// lib_ws: `ws` is the library workspace (no stamp; the library's row words)
 static int pq_run(const ibh_pq_tensor_abi* t, const float* x, float* out, void* ws, size_t ws_bytes, void* stream,
-                  const PqMode& md, const char* who);
+                  const PqMode& md, const char* who, bool lib_ws = false);
 
 extern "C" int ibh_pq_matmul(const ibh_pq_tensor_abi* t, const float* x, float* out, void* ws, size_t ws_bytes,
                              void* stream) {
@@ -1090,7 +1163,7 @@ extern "C" int ibh_pq_set_fused(int on) {
 }
 
 static int pq_run(const ibh_pq_tensor_abi* t, const float* x, float* out, void* ws, size_t ws_bytes, void* stream,
-                  const PqMode& md, const char* who) {
+                  const PqMode& md, const char* who, bool lib_ws) {
     if (!t || !x || !out || t->M <= 0 || t->C <= 0 || t->G <= 0 || t->G % 2 || t->G > 64 || t->K <= 0 || t->K > 65536 ||
         !t->codebook_l1_l || !t->codebook_l1_r || !t->indices_l1_l || !t->indices_l1_r || !t->row_scale ||
         t->N != t->C * t->G + t->n_outlier || t->n_outlier < 0 || t->n_outlier > 1024 ||
@@ -1108,7 +1181,8 @@ static int pq_run(const ibh_pq_tensor_abi* t, const float* x, float* out, void* 
     int CS, nslabs;
     size_t lds;
     PqWs w;
-    if (pq_geometry(t, &CS, &nslabs, &lds, &w) != IBH_OK) {
+    const bool own_ws = ws != nullptr && !lib_ws;
+    if (pq_geometry(t, &CS, &nslabs, &lds, &w, own_ws) != IBH_OK) {
         ibh_set_error("%s: codebooks too large for the LDS tables", who);
         return IBH_ERROR_PARAM;
     }
@@ -1149,8 +1223,10 @@ static int pq_run(const ibh_pq_tensor_abi* t, const float* x, float* out, void* 
     const int S = (t->C + kFCS - 1) / kFCS;
     if (!two && !md.q8 && !md.tq8 && t->G <= 16 && t->K <= 256 && S <= kFMaxS && t->M <= kFMaxRows && g_pq_fused) {
         const size_t flds = (size_t)kFCS * (2 * t->K + 4) * sizeof(float);
-        if (t->K % 32 == 0) pq_fused<true><<<tiles * S, kFThreads, flds, st>>>(d, x, out, S);
-        else pq_fused<false><<<tiles * S, kFThreads, flds, st>>>(d, x, out, S);
+        unsigned long long* hdr = own_ws ? (unsigned long long*)ws : nullptr;
+        unsigned long long* racc = own_ws ? hdr + 32 : nullptr;
+        if (t->K % 32 == 0) pq_fused<true><<<tiles * S, kFThreads, flds, st>>>(d, x, out, S, racc, hdr);
+        else pq_fused<false><<<tiles * S, kFThreads, flds, st>>>(d, x, out, S, racc, hdr);
         IBH_CHECK_LAUNCH("ibh_pq_matmul (one launch)");
         return IBH_OK;
     }
@@ -1178,12 +1254,16 @@ static int pq_run(const ibh_pq_tensor_abi* t, const float* x, float* out, void* 
 
 // Workspace of ibh_pq_lm_head_topk: the matvec's, then the coarse logits,
 // the selected rows and their refined logits.
-extern "C" size_t ibh_pq_topk_workspace_bytes(const ibh_pq_tensor_abi* t, int k_top) {
-    const size_t base = ibh_pq_workspace_bytes(t);
+static size_t pq_topk_need(const ibh_pq_tensor_abi* t, int k_top, bool front) {
+    const size_t base = pq_ws_need(t, front);
     if (!base || k_top <= 0) return 0;
     auto al = [](size_t v) { return (v + 255) / 256 * 256; };
     const size_t nb = ((size_t)t->M + kLocalSpan - 1) / kLocalSpan;   // two-pass select candidates
     return base + al((size_t)t->M * 4) + 3 * al((size_t)k_top * 4) + 2 * al(nb * kLocalMaxK * 4);
+}
+
+extern "C" size_t ibh_pq_topk_workspace_bytes(const ibh_pq_tensor_abi* t, int k_top) {
+    return pq_topk_need(t, k_top, true);
 }
 
 extern "C" int ibh_pq_lm_head_topk(const ibh_pq_tensor_abi* t, const float* x, int k_top, float* out_logits,
@@ -1192,7 +1272,8 @@ extern "C" int ibh_pq_lm_head_topk(const ibh_pq_tensor_abi* t, const float* x, i
         ibh_set_error("ibh_pq_lm_head_topk: invalid arguments (K_top=%d, M=%d; K_top <= 1024)", k_top, t ? t->M : 0);
         return IBH_ERROR_PARAM;
     }
-    const size_t need = ibh_pq_topk_workspace_bytes(t, k_top);
+    const bool lib_ws = ws == nullptr;
+    const size_t need = pq_topk_need(t, k_top, !lib_ws);
     if (!need) {
         ibh_set_error("ibh_pq_lm_head_topk: invalid tensor");
         return IBH_ERROR_PARAM;
@@ -1206,7 +1287,7 @@ extern "C" int ibh_pq_lm_head_topk(const ibh_pq_tensor_abi* t, const float* x, i
         return IBH_ERROR_MEMORY;
     }
     auto al = [](size_t v) { return (v + 255) / 256 * 256; };
-    const size_t base = ibh_pq_workspace_bytes(t);
+    const size_t base = pq_ws_need(t, !lib_ws);
     float* coarse = (float*)((char*)ws + base);
     int32_t* sel = (int32_t*)((char*)coarse + al((size_t)t->M * 4));
     float* refined = (float*)((char*)sel + al((size_t)k_top * 4));
@@ -1215,7 +1296,7 @@ extern "C" int ibh_pq_lm_head_topk(const ibh_pq_tensor_abi* t, const float* x, i
     PqMode md;
     md.skip_mode = 0;
     md.level2 = false;
-    int rc = pq_run(t, x, coarse, ws, base, stream, md, "ibh_pq_lm_head_topk");
+    int rc = pq_run(t, x, coarse, ws, base, stream, md, "ibh_pq_lm_head_topk", lib_ws);
     if (rc) return rc;
     // 2. the K largest, 3. their full-pyramid logits, 4. sorted
     const int nb = (t->M + kLocalSpan - 1) / kLocalSpan;

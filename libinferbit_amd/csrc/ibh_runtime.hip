@@ -28,6 +28,19 @@ extern "C" const char* ibh_last_error(void) {
     return g_err;
 }
 
+extern "C" int ibh_device_errors(int clear) {
+    if (hipDeviceSynchronize() != hipSuccess) {
+        ibh_set_error("ibh_device_errors: device synchronisation failed");
+        return IBH_ERROR_INTERNAL;
+    }
+    const int a = ibh_tile_errors(clear != 0), b = ibh_pq_errors(clear != 0);
+    if (a < 0 || b < 0) {
+        ibh_set_error("ibh_device_errors: cannot read the device error words");
+        return IBH_ERROR_INTERNAL;
+    }
+    return a | b;
+}
+
 extern "C" const char* ibh_version(void) { return "libinferbit_amd 0.1.0 (gfx950)"; }
 
 // ── per-device state ───────────────────────────────────────────────────────
@@ -469,6 +482,221 @@ extern "C" void ibh_host_kv_release(const void* cache) {
         if (g_kv[i].key == cache) {
             kv_mirror_free(g_kv[i]);
             g_kv.erase(g_kv.begin() + (long)i);
+            return;
+        }
+}
+
+// ── PQ matvec on a host ib_pq_tensor (ib_pq_matmul_fp32's twin) ─────────────
+// The reference's PQ entries take an ib_pq_tensor whose arrays are host
+// memory (an arena from the fread loaders or the file mmap,
+// src/pq_decode.c:391-555, 685-744).  The first call on a tensor builds its
+// device description: arrays inside a region registered with
+// ibh_register_host_weights map to that device copy, the others are uploaded
+// once into an allocation of the entry; inner_cols and a stamped PQ workspace
+// come with it.  Entries are keyed by the tensor's array addresses and
+// checked against a fingerprint of its shape and of the first and last bytes
+// of every array, so a tensor freed and another loaded at the same addresses
+// is uploaded anew; ibh_pq_host_release (from ib_pq_free) frees an entry.
+namespace {
+struct PqHostEntry {
+    const void* key;          // codebook_l1_l
+    const void* key2;         // indices_l1_l
+    uint64_t fp;
+    uint8_t* blob;            // uploaded arrays + inner_cols
+    void* ws;                 // stamped PQ workspace
+    size_t ws_bytes;
+    ibh_pq_tensor d;          // device description
+};
+std::vector<PqHostEntry> g_pqh;
+
+struct PqArr {
+    const void* h;
+    size_t n;
+};
+
+// The reference tensor's arrays with their byte sizes (src/pq_decode.c:470-489).
+int pq_host_arrays(const ibh_ref_pq_tensor* t, PqArr* a) {
+    const int K2 = t->K_l2 > 0 ? t->K_l2 : t->K;
+    const int hf = t->G / 2;
+    const size_t l2s = K2 == 16 ? (size_t)(t->C + 1) / 2 : (size_t)t->C * (t->l2_idx_bytes == 2 ? 2 : 1);
+    const size_t M = (size_t)t->M, no = (size_t)(t->n_outlier > 0 ? t->n_outlier : 0);
+    const bool two = t->n_levels == 2;
+    a[0] = {t->codebook_l1_l, (size_t)t->K * hf * 2};
+    a[1] = {t->codebook_l1_r, (size_t)t->K * hf * 2};
+    a[2] = {two ? t->codebook_l2_l : nullptr, two ? (size_t)K2 * hf * 2 : 0};
+    a[3] = {two ? t->codebook_l2_r : nullptr, two ? (size_t)K2 * hf * 2 : 0};
+    a[4] = {t->indices_l1_l, M * t->C};
+    a[5] = {t->indices_l1_r, M * t->C};
+    a[6] = {two ? t->indices_l2_l : nullptr, two ? M * l2s : 0};
+    a[7] = {two ? t->indices_l2_r : nullptr, two ? M * l2s : 0};
+    a[8] = {t->row_scale, M * 2};
+    a[9] = {no ? t->outlier_cols : nullptr, no * 4};
+    a[10] = {no ? t->outlier_sidecar : nullptr, M * no};
+    a[11] = {no ? t->outlier_scale : nullptr, no * 2};
+    return 12;
+}
+
+uint64_t fnv(uint64_t h, const void* p, size_t n) {
+    const uint8_t* b = (const uint8_t*)p;
+    for (size_t i = 0; i < n; i++) h = (h ^ b[i]) * 0x100000001b3ull;
+    return h;
+}
+
+uint64_t pq_host_fp(const ibh_ref_pq_tensor* t, const PqArr* a, int na) {
+    const int dims[] = {t->M, t->N, t->G, t->K, t->K_l2, t->n_levels, t->n_outlier, t->format, t->C, t->l2_idx_bytes};
+    uint64_t h = fnv(0xcbf29ce484222325ull, dims, sizeof(dims));
+    for (int i = 0; i < na; i++) {
+        if (!a[i].h) continue;
+        const size_t k = std::min<size_t>(a[i].n, 512);
+        h = fnv(h, a[i].h, k);
+        h = fnv(h, (const uint8_t*)a[i].h + a[i].n - k, k);
+    }
+    return h;
+}
+
+void pq_host_free(PqHostEntry& e) {
+    (void)hipFree(e.blob);
+    (void)hipFree(e.ws);
+    e.blob = nullptr;
+    e.ws = nullptr;
+}
+
+int pq_host_entry(const ibh_ref_pq_tensor* t, PqHostEntry** out) {
+    PqArr a[12];
+    const int na = pq_host_arrays(t, a);
+    const uint64_t fp = pq_host_fp(t, a, na);
+    for (PqHostEntry& e : g_pqh)
+        if (e.key == t->codebook_l1_l && e.key2 == t->indices_l1_l) {
+            if (e.fp == fp) {
+                *out = &e;
+                return IBH_OK;
+            }
+            pq_host_free(e);          // another tensor at the same addresses
+            e = g_pqh.back();
+            g_pqh.pop_back();
+            break;
+        }
+    // arrays not resident in a registered region go to one allocation
+    const uint8_t* dev[12];
+    size_t up = 0;
+    for (int i = 0; i < na; i++) {
+        dev[i] = a[i].h ? lookup(a[i].h, a[i].n) : nullptr;
+        if (a[i].h && !dev[i]) up += al256(a[i].n);
+    }
+    const int ninner = t->N - t->n_outlier;
+    std::vector<int32_t> inner;
+    if (t->n_outlier > 0) {
+        std::vector<char> is_out((size_t)t->N, 0);
+        for (int j = 0; j < t->n_outlier; j++) {
+            const int c = t->outlier_cols[j];
+            if (c < 0 || c >= t->N) {
+                ibh_set_error("ibh_pq_matmul_fp32_host: outlier column %d outside [0, %d)", c, t->N);
+                return IBH_ERROR_PARAM;
+            }
+            is_out[(size_t)c] = 1;
+        }
+        for (int c = 0; c < t->N; c++)
+            if (!is_out[(size_t)c]) inner.push_back(c);
+        if ((int)inner.size() != ninner) {
+            ibh_set_error("ibh_pq_matmul_fp32_host: repeated outlier columns");
+            return IBH_ERROR_PARAM;
+        }
+        up += al256(inner.size() * 4);
+    }
+    PqHostEntry e{};
+    e.key = t->codebook_l1_l;
+    e.key2 = t->indices_l1_l;
+    e.fp = fp;
+    if (up && hipMalloc((void**)&e.blob, up) != hipSuccess) {
+        ibh_set_error("ibh_pq_matmul_fp32_host: out of device memory (%zu bytes)", up);
+        return IBH_ERROR_MEMORY;
+    }
+    size_t off = 0;
+    for (int i = 0; i < na; i++) {
+        if (!a[i].h || dev[i]) continue;
+        if (hipMemcpy(e.blob + off, a[i].h, a[i].n, hipMemcpyHostToDevice) != hipSuccess) {
+            pq_host_free(e);
+            ibh_set_error("ibh_pq_matmul_fp32_host: upload failed");
+            return IBH_ERROR_INTERNAL;
+        }
+        dev[i] = e.blob + off;
+        off += al256(a[i].n);
+    }
+    const int32_t* dinner = nullptr;
+    if (!inner.empty()) {
+        if (hipMemcpy(e.blob + off, inner.data(), inner.size() * 4, hipMemcpyHostToDevice) != hipSuccess) {
+            pq_host_free(e);
+            ibh_set_error("ibh_pq_matmul_fp32_host: upload failed");
+            return IBH_ERROR_INTERNAL;
+        }
+        dinner = (const int32_t*)(e.blob + off);
+    }
+    ibh_pq_tensor& d = e.d;
+    d.M = t->M; d.N = t->N; d.G = t->G; d.K = t->K; d.K_l2 = t->K_l2; d.n_levels = t->n_levels;
+    d.n_outlier = t->n_outlier; d.C = t->C; d.l2_idx_bytes = t->l2_idx_bytes; d.format = t->format;
+    d.codebook_l1_l = (const uint16_t*)dev[0]; d.codebook_l1_r = (const uint16_t*)dev[1];
+    d.codebook_l2_l = (const uint16_t*)dev[2]; d.codebook_l2_r = (const uint16_t*)dev[3];
+    d.indices_l1_l = dev[4]; d.indices_l1_r = dev[5]; d.indices_l2_l = dev[6]; d.indices_l2_r = dev[7];
+    d.row_scale = (const uint16_t*)dev[8];
+    d.outlier_cols = (const int32_t*)dev[9]; d.outlier_sidecar = (const int8_t*)dev[10];
+    d.outlier_scale = (const uint16_t*)dev[11];
+    d.inner_cols = dinner;
+    e.ws_bytes = ibh_pq_workspace_bytes(&d);
+    if (!e.ws_bytes) {
+        pq_host_free(e);
+        ibh_set_error("ibh_pq_matmul_fp32_host: unsupported tensor geometry");
+        return IBH_ERROR_PARAM;
+    }
+    if (hipMalloc(&e.ws, e.ws_bytes) != hipSuccess) {
+        pq_host_free(e);
+        ibh_set_error("ibh_pq_matmul_fp32_host: out of device memory for the workspace");
+        return IBH_ERROR_MEMORY;
+    }
+    const int rc = ibh_pq_workspace_init(e.ws, e.ws_bytes, nullptr);
+    if (rc != IBH_OK) {
+        pq_host_free(e);
+        return rc;
+    }
+    g_pqh.push_back(e);
+    *out = &g_pqh.back();
+    return IBH_OK;
+}
+}  // namespace
+
+extern "C" int ibh_pq_matmul_fp32_host(const ibh_ref_pq_tensor* t, const float* x, float* out) {
+    if (!t || !x || !out || t->M <= 0 || t->N <= 0 || t->C <= 0 || t->G <= 0 || t->K <= 0 || !t->codebook_l1_l ||
+        !t->indices_l1_l) {
+        ibh_set_error("ibh_pq_matmul_fp32_host: invalid arguments");
+        return -1;
+    }
+    std::lock_guard<std::mutex> lk(g_tab_mu);
+    PqHostEntry* e = nullptr;
+    if (pq_host_entry(t, &e) != IBH_OK) return -1;
+    hipStream_t st = ibh_resolve_stream(nullptr);
+    Staged S;
+    S.base = workspace(al256(4 * (size_t)t->N) + al256(4 * (size_t)t->M));
+    if (!S.base) {
+        ibh_set_error("ibh_pq_matmul_fp32_host: out of device memory");
+        return -1;
+    }
+    float* dx = (float*)S.put(x, 4 * (size_t)t->N, st);
+    float* dout = (float*)S.put(nullptr, 4 * (size_t)t->M, st);
+    if (ibh_pq_matmul(&e->d, dx, dout, e->ws, e->ws_bytes, st) != IBH_OK) return -1;
+    if (hipMemcpyAsync(out, dout, 4 * (size_t)t->M, hipMemcpyDeviceToHost, st) != hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess) {
+        ibh_set_error("ibh_pq_matmul_fp32_host: device copy failed");
+        return -1;
+    }
+    return 0;
+}
+
+extern "C" void ibh_pq_host_release(const ibh_ref_pq_tensor* t) {
+    if (!t) return;
+    std::lock_guard<std::mutex> lk(g_tab_mu);
+    for (size_t i = 0; i < g_pqh.size(); i++)
+        if (g_pqh[i].key == t->codebook_l1_l && g_pqh[i].key2 == t->indices_l1_l) {
+            pq_host_free(g_pqh[i]);
+            g_pqh.erase(g_pqh.begin() + (long)i);
             return;
         }
 }

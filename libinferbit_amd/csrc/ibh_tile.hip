@@ -128,13 +128,21 @@ __device__ __forceinline__ int b_off(int s, int h, int n, int kg) {
 __device__ __forceinline__ void lds_signal(int* c) {
     __hip_atomic_fetch_add(c, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
-// Waits until *c >= n.  Bounded: after ~2^20 polls the wave goes on (it
-// cannot happen unless a wave of the block died; the grid still drains).
-__device__ __forceinline__ void lds_wait(int* c, int n) {
+// Device error word of this file's kernels (IBH_DEVERR_* bits), read and
+// cleared by ibh_device_errors.
+__device__ unsigned int ibh_tile_err;
+
+// Waits until *c >= n.  Bounded: after ~2^20 polls the wave gives up, marks
+// the block bad (*bad, an LDS flag whose outputs then become NaN) and raises
+// IBH_DEVERR_TILE_WAIT, so an expired wait is never a silent wrong answer;
+// the grid still drains.  It cannot expire unless a wave of the block died.
+__device__ __forceinline__ void lds_wait(int* c, int n, int* bad) {
     for (int it = 0; it < (1 << 20); it++) {
         if (__hip_atomic_load(c, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= n) return;
         __builtin_amdgcn_s_sleep(1);
     }
+    __hip_atomic_store(bad, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    __hip_atomic_fetch_or(&ibh_tile_err, IBH_DEVERR_TILE_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Block = NXW activation wavefronts (waves 0..NXW-1) + WQ quads x KW K-ranges
@@ -233,6 +241,7 @@ __global__ __launch_bounds__(1024) void gemv_tile_x(const RowSet rs, const float
     __shared__ float red[kTileMaxWaves];
     __shared__ int qpart[2 * kTileMaxChunks];   // per digit chunk: sum of d0, sum of (Q & 0x3fff)
     __shared__ int cnt[4];                  // waves that posted max|x|; digit chunks done; next chunk; ss posted
+    __shared__ int bad;                     // a wait of the block expired: outputs NaN
     __shared__ float red_ss[kTileMaxWaves];
     __shared__ int part[kTileMaxWaves][4][3];
     __shared__ __align__(16) int epi[kTileMaxWaves][48];
@@ -243,6 +252,7 @@ __global__ __launch_bounds__(1024) void gemv_tile_x(const RowSet rs, const float
     unsigned long long tt[8];
 #endif
     if (threadIdx.x < 4) cnt[threadIdx.x] = 0;
+    if (threadIdx.x == 0) bad = 0;
     __syncthreads();
     IBH_TT(0);
 
@@ -294,7 +304,7 @@ __global__ __launch_bounds__(1024) void gemv_tile_x(const RowSet rs, const float
                 red_ss[wave] = ss;
                 lds_signal(&cnt[3]);
             }
-            lds_wait(&cnt[3], NXW);
+            lds_wait(&cnt[3], NXW, &bad);
             float tot = 0.f;
             for (int w = 0; w < NXW; w++) tot += red_ss[w];
             const float inv = 1.0f / sqrtf(tot / (float)N + eps);
@@ -321,7 +331,7 @@ __global__ __launch_bounds__(1024) void gemv_tile_x(const RowSet rs, const float
             red[wave] = mx;
             lds_signal(&cnt[0]);
         }
-        lds_wait(&cnt[0], NXW);
+        lds_wait(&cnt[0], NXW, &bad);
         IBH_TT(1);
         float gm = 0.f;
         for (int w = 0; w < NXW; w++) gm = fmaxf(gm, red[w]);
@@ -357,14 +367,14 @@ __global__ __launch_bounds__(1024) void gemv_tile_x(const RowSet rs, const float
         for (int j = 0; j < KS; j++) wv[j] = ld_stream16(base + j * 256);
     }
     __builtin_amdgcn_sched_barrier(0);   // every load is issued before the waits below
-    lds_wait(&cnt[0], NXW);
+    lds_wait(&cnt[0], NXW, &bad);
     IBH_TT(3);
     float gm = 0.f;
     for (int w = 0; w < NXW; w++) gm = fmaxf(gm, red[w]);
     const float xs = gm > 0.f ? gm / 127.0f : 1.0f;
     digit_work<BITS>(smem, xraw, &cnt[2], &cnt[1], nchunks, lane, N, (1.0f / xs) * 16384.0f, qpart);
     IBH_TT(4);
-    lds_wait(&cnt[1], 64 * nchunks);
+    lds_wait(&cnt[1], 64 * nchunks, &bad);
     IBH_TT(5);
 
     // contract: exact int32 per (chunk, row) x (chunk, plane) over this
@@ -433,7 +443,8 @@ __global__ __launch_bounds__(1024) void gemv_tile_x(const RowSet rs, const float
             v -= (double)kBias * (double)sQ;
         }
         const float rsc = KIND == IBH_SCALE_F16 ? f16_to_f32((uint16_t)rsc_bits) : __builtin_bit_cast(float, rsc_bits);
-        const float yv = (float)(v * ((double)xs * (1.0 / (16384.0 * TGeo<BITS>::kOpScale)))) * rsc;
+        float yv = (float)(v * ((double)xs * (1.0 / (16384.0 * TGeo<BITS>::kOpScale)))) * rsc;
+        if (__hip_atomic_load(&bad, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) yv = __builtin_nanf("");
         y[row0 + lane] = accy ? y[row0 + lane] + yv : yv;   // accy: a residual stream takes the product
         IBH_TT_END(row0 + lane);
     }
@@ -449,6 +460,16 @@ extern "C" int ibh_tile_trace_read(void* out) {
     return hipMemcpyFromSymbol(out, HIP_SYMBOL(ibh_tile_tt), sizeof(ibh_tile_tt)) == hipSuccess ? 0 : -1;
 }
 #endif
+
+int ibh_tile_errors(bool clear) {
+    unsigned int v = 0;
+    if (hipMemcpyFromSymbol(&v, HIP_SYMBOL(ibh_tile_err), sizeof(v)) != hipSuccess) return -1;
+    if (clear && v) {
+        const unsigned int z = 0;
+        if (hipMemcpyToSymbol(HIP_SYMBOL(ibh_tile_err), &z, sizeof(z)) != hipSuccess) return -1;
+    }
+    return (int)v;
+}
 
 extern "C" int ibh_set_tile_config(int mode, int KS, int WR, int delay) {
     if (mode > 0 && KS != 0 && KS != 4 && KS != 7 && KS != 8 && KS != 14 && KS != 16) {

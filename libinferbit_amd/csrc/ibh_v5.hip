@@ -624,8 +624,10 @@ struct ibh_v5_session {
     float *gate = nullptr, *up = nullptr, *gu = nullptr, *delta = nullptr, *xs = nullptr, *logits = nullptr;
     float* top_val = nullptr;
     int32_t* top_ids = nullptr;
-    void* ws = nullptr;
+    void* ws = nullptr;      // INT4 matvec workspace
     size_t ws_bytes = 0;
+    void* pq_ws = nullptr;   // PQ workspace (stamped, its row words kept zero by the PQ kernels)
+    size_t pq_ws_bytes = 0;
     unsigned epoch = 1;   // bumped by policy changes: captured steps are stale
     bool no_group = false;   // IBH_V5_NO_GROUP=1: one launch per matrix, silu separate
 };
@@ -1131,14 +1133,20 @@ int open_session(ibh_v5_session* s, const char* path) {
         (rc = salloc(s, (void**)&s->logits, (size_t)s->vocab * 4)) ||
         (rc = salloc(s, (void**)&s->top_val, 1024 * 4)) || (rc = salloc(s, (void**)&s->top_ids, 1024 * 4)))
         return rc;
-    size_t ws = 0;
+    size_t ws = 256, pws = 0;
     for (auto& m : s->mats) {
-        if (m.kind == MAT_PQ) ws = std::max(ws, ibh_pq_workspace_bytes(&m.pq));
+        if (m.kind == MAT_PQ) pws = std::max(pws, ibh_pq_workspace_bytes(&m.pq));
         if (m.kind == MAT_INT4) ws = std::max(ws, ibh_int4g_workspace_bytes(&m.i4));
     }
-    if (s->mats[s->m_head].kind == MAT_PQ) ws = std::max(ws, ibh_pq_topk_workspace_bytes(&s->mats[s->m_head].pq, 256));
+    if (s->mats[s->m_head].kind == MAT_PQ) pws = std::max(pws, ibh_pq_topk_workspace_bytes(&s->mats[s->m_head].pq, 256));
     s->ws_bytes = ws;
     if ((rc = salloc(s, &s->ws, ws))) return rc;
+    if (pws) {
+        s->pq_ws_bytes = pws;
+        if ((rc = salloc(s, &s->pq_ws, pws))) return rc;
+        if ((rc = ibh_pq_workspace_init(s->pq_ws, pws, nullptr))) return rc;
+        IBH_HIP(hipDeviceSynchronize(), "ibh_v5_open: PQ workspace");
+    }
     // inputs of the norm-fused INT4 launches: norm weight (* AWQ vector)
     s->wia_in.assign(L, {nullptr, nullptr, nullptr});
     s->wia_pn.assign(L, {nullptr, nullptr, nullptr});
@@ -1191,7 +1199,7 @@ int matmul(ibh_v5_session* s, int mi, const float* x, float* out) {
         xk = s->xs;
     }
     const ibh_pq_policy& p = m.has_policy ? m.policy : s->default_policy;
-    return ibh_pq_matmul_policy(&m.pq, xk, out, &p, s->ws, s->ws_bytes, s->st);
+    return ibh_pq_matmul_policy(&m.pq, xk, out, &p, s->pq_ws, s->pq_ws_bytes, s->st);
 }
 
 constexpr int kAttnMaxSplits = 1024;
@@ -1375,7 +1383,7 @@ int forward_dev(ibh_v5_session* s, ibh_v5_kv* kv, bool want_logits) {
 // ids[0] recorded and placed at tokens[*pos].
 int pick_dev(ibh_v5_session* s, ibh_v5_kv* kv) {
     int rc;
-    if ((rc = ibh_pq_lm_head_topk(&s->mats[s->m_head].pq, s->xb, 8, s->top_val, s->top_ids, s->ws, s->ws_bytes,
+    if ((rc = ibh_pq_lm_head_topk(&s->mats[s->m_head].pq, s->xb, 8, s->top_val, s->top_ids, s->pq_ws, s->pq_ws_bytes,
                                   s->st)))
         return rc;
     v5_advance_kernel<<<1, 1, 0, s->st>>>(s->top_ids, kv->tokens, kv->state, kv->outs);
@@ -1761,7 +1769,7 @@ int ibh_v5_step_hidden_topk(ibh_v5_session* s, ibh_v5_kv* kv, int first, const i
             (rc = set_token_pos(s, kv, token, pos)) || (rc = run_graph(s, kv, 0)))
             return rc;
     }
-    if ((rc = ibh_pq_lm_head_topk(&s->mats[s->m_head].pq, s->xb, k_top, s->top_val, s->top_ids, s->ws, s->ws_bytes,
+    if ((rc = ibh_pq_lm_head_topk(&s->mats[s->m_head].pq, s->xb, k_top, s->top_val, s->top_ids, s->pq_ws, s->pq_ws_bytes,
                                   s->st)))
         return rc;
     IBH_HIP(hipMemcpyAsync(top_logits, s->top_val, (size_t)k_top * 4, hipMemcpyDeviceToHost, s->st),

@@ -49,12 +49,24 @@ class V5Writer:
         d.update(dtype=dtype, shape=list(np.asarray(arr).shape))
         self.raw[name] = d
 
-    def pq_tensor(self, name: str, t: dict):
+    def pq_tensor(self, name: str, t: dict, rotate: bool = False, l2_packed_bits: int = 0):
         """t: the oracle's PQ dict (M, N, G, K, n_levels, K_l2, n_outlier,
-        cb1l, cb1r, i1l, i1r, row_scale[, cb2l, cb2r, i2l, i2r, ocols, oside, oscale])."""
-        fmt = "pq2d_v1_l1" if t["n_levels"] == 1 else "pq2d_v1_l1_l2"
+        cb1l, cb1r, i1l, i1r, row_scale[, cb2l, cb2r, i2l, i2r, ocols, oside, oscale]).
+        Two-byte level-2 indices (l2_idx_bytes 2), or a K_l2 outside {16, 64,
+        K} (which pq2d_v1_l1_l2 refuses, src/pq_decode.c:425-426), make a
+        pyramid tensor (pq2d_v1_pyramid).  l2_packed_bits > 0 stores those indices
+        bit-packed LSB-first per row, ceil(C * bits / 8) bytes a row, which
+        the loader unpacks to uint16 (src/pq_decode.c:431-446, 504-528)."""
+        K2 = int(t.get("K_l2") or t["K"])
+        pyramid = t["n_levels"] == 2 and (int(t.get("l2_idx_bytes", 1)) == 2 or K2 not in (16, 64, int(t["K"])))
+        fmt = "pq2d_v1_l1" if t["n_levels"] == 1 else ("pq2d_v1_pyramid" if pyramid else "pq2d_v1_l1_l2")
         m = {"format": fmt, "shape": [int(t["M"]), int(t["N"])], "G": int(t["G"]), "K": int(t["K"]),
              "n_levels": int(t["n_levels"])}
+        if rotate:
+            m["rotate"] = True
+        if l2_packed_bits:
+            assert pyramid, "bit-packed level-2 indices are a pyramid-format option"
+            m["l2_packed_bits"] = int(l2_packed_bits)
         if t.get("K_l2"):
             m["K_l2"] = int(t["K_l2"])
         if t.get("n_outlier"):
@@ -67,7 +79,11 @@ class V5Writer:
         if t.get("n_outlier"):
             blocks += [("outlier_cols", "ocols"), ("outlier_sidecar", "oside"), ("outlier_scale", "oscale")]
         for key, k in blocks:
-            m[key] = self._blob(t[k])
+            a = t[k]
+            if l2_packed_bits and k in ("i2l", "i2r"):
+                a = _pack_bits(np.ascontiguousarray(a).view(np.uint16).reshape(int(t["M"]), int(t["C"])),
+                               l2_packed_bits)
+            m[key] = self._blob(a)
         self.tensors[name] = m
 
     def write(self, path: str):
@@ -87,6 +103,17 @@ class V5Writer:
             f.write(b"\0" * (start - PREAMBLE - reserve))
             for b in self.blobs:
                 f.write(b)
+
+
+def _pack_bits(v: np.ndarray, bits: int) -> np.ndarray:
+    """Rows of values < 2^bits packed LSB-first, each row ceil(C*bits/8) bytes."""
+    M, C = v.shape
+    per = (C * bits + 7) // 8
+    bitsarr = ((v[:, :, None].astype(np.uint32) >> np.arange(bits, dtype=np.uint32)) & 1).astype(np.uint8)
+    flat = bitsarr.reshape(M, C * bits)
+    pad = np.zeros((M, per * 8), np.uint8)
+    pad[:, :C * bits] = flat
+    return np.packbits(pad.reshape(M, per, 8), axis=2, bitorder="little").reshape(M, per)
 
 
 def _pq(rng, M, N, G=16, K=256, levels=1, K2=0, n_outlier=0, cb_std=0.05):

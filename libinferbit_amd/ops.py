@@ -144,6 +144,8 @@ class PqDeviceTensor:
         # a workspace of its own (tables, slab partials), allocated once
         self.ws = torch.empty(max(1, lib().ibh_pq_workspace_bytes(ctypes.byref(s))), dtype=torch.uint8,
                               device="cuda")
+        check(lib().ibh_pq_workspace_init(_ptr(self.ws), self.ws.numel(), _stream()), "ibh_pq_workspace_init")
+        self._topk_ws = {}
 
     def matmul(self, x, out) -> None:
         """ib_pq_matmul_fp32 (src/pq_decode.c:1684)."""
@@ -164,7 +166,12 @@ class PqDeviceTensor:
     def lm_head_topk(self, x, k_top: int):
         """ib_pq_lm_head_topk (src/pq_decode.c:2259-2346): (logits [k], ids [k]) on the GPU."""
         need = lib().ibh_pq_topk_workspace_bytes(ctypes.byref(self.s), k_top)
-        ws = torch.empty(max(1, need), dtype=torch.uint8, device="cuda")
+        ws = self._topk_ws.get(k_top)
+        if ws is None:
+            # prepared once, kept for later calls with the same K_top
+            ws = torch.empty(max(1, need), dtype=torch.uint8, device="cuda")
+            check(lib().ibh_pq_workspace_init(_ptr(ws), ws.numel(), _stream()), "ibh_pq_workspace_init")
+            self._topk_ws[k_top] = ws
         lg = torch.empty(k_top, device="cuda")
         ids = torch.empty(k_top, dtype=torch.int32, device="cuda")
         check(lib().ibh_pq_lm_head_topk(ctypes.byref(self.s), _ptr(x), k_top, _ptr(lg), _ptr(ids), _ptr(ws), need,

@@ -12,7 +12,7 @@
  *   before inferbit_free (src/model.c:42-107):
  *       ibh_unregister_host_weights(model->weight_data);
  *
- *   dropin MODEL.ibf CONTEXT N_OUT PROMPT.i32 CPU_THREADS [KEEP_CPU_TABLE]
+ *   dropin MODEL.ibf CONTEXT N_OUT PROMPT.i32 CPU_THREADS [KEEP_CPU_TABLE [KV.f32 N_POS]]
  *
  * The CPU pass loads the model with CPU_THREADS pool threads (the pool splits
  * rows, so the results do not depend on the count); the GPU pass loads it
@@ -32,7 +32,11 @@
  * ibh_host_kv_release before inferbit_free.  DROPIN_LOOKUP="ngram,k" turns on
  * the reference's prompt-lookup speculation (inferbit_set_prompt_lookup), which
  * verifies drafts through forward_batch and rewinds the cache with
- * inferbit_kv_truncate. */
+ * inferbit_kv_truncate.  KV.f32 N_POS (dropin_attn only) prefills every
+ * layer's cache with N_POS positions before each pass, through forward.c's
+ * own kv_cache_write (the file holds fp32 K [layers][N_POS][kv_dim], then V
+ * in the same layout), as ref_decode does; each pass then rewinds to N_POS
+ * instead of clearing. */
 #ifdef DROPIN_ATTN
 static int ibh_attn_hook(void* ctx, int n_heads);
 #include "forward_hip.c"
@@ -83,12 +87,48 @@ static void* slurp(const char* path, size_t* n) {
     return b;
 }
 
-/* logits of the prompt's last token, then greedy generation from a clean cache */
+static int g_kv0 = 0;   /* prefilled positions each pass starts from */
+
+static void rewind_kv(inferbit_model* m) {
+    if (g_kv0 > 0) inferbit_kv_truncate(m, g_kv0);
+    else inferbit_kv_clear(m);
+}
+
+#ifdef DROPIN_ATTN
+/* every layer's cache holds positions 0..npos-1 of the file's K/V, written by
+ * forward.c's kv_cache_write (src/forward.c:352-413) */
+static int prefill(inferbit_model* m, const char* path, int npos) {
+    const int L = m->header.num_layers, n_kv = m->header.num_kv_heads, hd = m->header.head_dim;
+    const size_t kv_dim = (size_t)n_kv * hd;
+    FILE* f = fopen(path, "rb");
+    float* k = malloc(kv_dim * sizeof(float));
+    float* v = malloc(kv_dim * sizeof(float));
+    if (!f || !k || !v) return -1;
+    const long vbase = (long)((size_t)L * npos * kv_dim * sizeof(float));
+    for (int l = 0; l < L; l++) {
+        for (int p = 0; p < npos; p++) {
+            const long off = (long)(((size_t)l * npos + p) * kv_dim * sizeof(float));
+            if (fseek(f, off, SEEK_SET) || fread(k, sizeof(float), kv_dim, f) != kv_dim ||
+                fseek(f, vbase + off, SEEK_SET) || fread(v, sizeof(float), kv_dim, f) != kv_dim)
+                return -1;
+            kv_cache_write(&m->kv_caches[l], p, k, v, (int)kv_dim, n_kv, hd, m->header.kv_bits);
+        }
+        m->kv_caches[l].length = npos;
+    }
+    fclose(f);
+    free(k);
+    free(v);
+    return 0;
+}
+#endif
+
+/* logits of the prompt's last token, then greedy generation from the same
+ * cache state (empty, or the prefilled positions) */
 static int pass(inferbit_model* m, const int32_t* prompt, int np, int n_out, float* lg, int32_t* out,
                 double* secs) {
-    inferbit_kv_clear(m);
+    rewind_kv(m);
     if (inferbit_forward(m, prompt, np, lg, m->header.vocab_size) != INFERBIT_OK) return -1;
-    inferbit_kv_clear(m);
+    rewind_kv(m);
     inferbit_sample_params sp = inferbit_default_sample_params();
     sp.temperature = 0.0f;
     const double t0 = now_s();
@@ -103,6 +143,10 @@ int main(int argc, char** argv) {
         return 2;
     }
     const int keep_cpu = argc > 6 && atoi(argv[6]) != 0;
+    const char* kv_path = argc > 8 ? argv[7] : NULL;
+#ifndef DROPIN_ATTN
+    if (kv_path) { fprintf(stderr, "KV prefill needs the dropin_attn build\n"); return 2; }
+#endif
     inferbit_config* cfg = inferbit_config_create();
     const int cpu_threads = atoi(argv[5]);
     inferbit_config_set_threads(cfg, cpu_threads > 0 ? cpu_threads : 1);
@@ -113,6 +157,12 @@ int main(int argc, char** argv) {
     const char* lk = getenv("DROPIN_LOOKUP");
     if (lk && sscanf(lk, "%d,%d", &lk_ng, &lk_k) != 2) { fprintf(stderr, "bad DROPIN_LOOKUP\n"); return 1; }
     if (lk) inferbit_set_prompt_lookup(m, lk_ng, lk_k);
+#ifdef DROPIN_ATTN
+    if (kv_path) {
+        g_kv0 = atoi(argv[8]);
+        if (cpu_threads > 0 && prefill(m, kv_path, g_kv0)) { fprintf(stderr, "bad KV file\n"); return 1; }
+    }
+#endif
     const int n_out = atoi(argv[3]);
     size_t pn = 0;
     int32_t* prompt = (int32_t*)slurp(argv[4], &pn);
@@ -132,6 +182,9 @@ int main(int argc, char** argv) {
     m = inferbit_load(argv[1], cfg);   /* ibf_load re-initialises the x86 table */
     if (!m) { fprintf(stderr, "reload failed: %s\n", inferbit_last_error()); return 1; }
     if (lk) inferbit_set_prompt_lookup(m, lk_ng, lk_k);
+#ifdef DROPIN_ATTN
+    if (kv_path && prefill(m, kv_path, g_kv0)) { fprintf(stderr, "bad KV file\n"); return 1; }
+#endif
 
     if (!keep_cpu) {
         void* dev = NULL;

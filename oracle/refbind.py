@@ -90,7 +90,33 @@ def lib():
         _lib.ib_pq_matmul_fp32_streaming_int8_cached.argtypes = [P, P, P, P]
         _lib.ib_pq_matmul_fp32_subset.argtypes = [P, P, P, I, P]
         _lib.ib_pq_lm_head_topk.argtypes = [P, P, I, P, P]
+        _lib.ib_pq_load_single.argtypes = [C.c_char_p, P]
+        _lib.ib_pq_load_single.restype = I
+        _lib.ib_pq_free.argtypes = [P]
+        _lib.ib_pq_free.restype = None
     return _lib
+
+
+def pq_load_single(path: str) -> IbPqTensor:
+    """ib_pq_load_single (src/pq_decode.c:726-744): the reference's own
+    loader fills an ib_pq_tensor whose arrays live in its arena."""
+    s = IbPqTensor()
+    rc = lib().ib_pq_load_single(path.encode(), C.byref(s))
+    if rc != 0:
+        raise RuntimeError(f"ib_pq_load_single({path}) = {rc}")
+    return s
+
+
+def pq_free(s: IbPqTensor) -> None:
+    lib().ib_pq_free(C.byref(s))
+
+
+def pq_matmul_struct(s: IbPqTensor, x):
+    """ib_pq_matmul_fp32 on a loaded tensor."""
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.zeros(s.M, np.float32)
+    assert lib().ib_pq_matmul_fp32(C.byref(s), _p(x), _p(out)) == 0
+    return out
 
 
 def kernels(level: int) -> IbKernels:

@@ -281,3 +281,42 @@ def test_unregister_releases_and_restages(L, tabs, R):
     cpu.matmul_int8(_p(yc), _p(w), _p(sc), _p(x), 64, 512)
     _same(y2, yc)
     assert np.all(np.sign(y1[y1 != 0]) == -np.sign(y2[y1 != 0]))
+
+
+@pytest.mark.timeout(900)
+def test_reference_generate_mistral_config_with_device_attention(tmp_path):
+    """Config 4 through the reference's own host loop: Mistral-7B shape, INT8
+    KV prefilled to 4096 positions by forward.c's kv_cache_write, then greedy
+    steps whose matvecs run on the GPU table and whose head loops
+    (src/forward.c:596-614) go to ibh_host_attn (head_dim 128, T = 4097 ...).
+    The tokens must be the prefix of the stream the reference recorded on its
+    own x86 table (tests/golden/decode.json), every attention step on the
+    device."""
+    import sys
+    sys.path.insert(0, GOLDEN)
+    import gen_decode_golden as G
+    g = json.load(open(os.path.join(GOLDEN, "decode.json")))["mistral"]
+    n_out = 8
+    os.makedirs(MODEL_DIR, exist_ok=True)
+    print("case dropin_attn mistral: writing model and KV", flush=True)
+    path = G.ensure_model("mistral", MODEL_DIR)
+    case = G.CASES["mistral"]
+    kp = str(tmp_path / "kv.f32")
+    k, v = G.kv_of(case)
+    with open(kp, "wb") as f:
+        f.write(k.tobytes())
+        f.write(v.tobytes())
+    del k, v
+    print("case dropin_attn mistral: generating", flush=True)
+    if not os.path.exists(DROPIN_ATTN):
+        pytest.skip(f"{DROPIN_ATTN} not built (make -C oracle ref)")
+    pp = str(tmp_path / "p.i32")
+    np.asarray(g["prompt"], np.int32).tofile(pp)
+    r = subprocess.run([DROPIN_ATTN, path, "0", str(n_out), pp, "0", "0", kp, str(g["kv_pos"])],
+                       capture_output=True, text=True, timeout=800)
+    assert r.returncode == 0, r.stderr
+    r = json.loads(r.stdout.strip().splitlines()[-1])
+    assert r["logits_nan"] == 0
+    assert r["attn_calls"] > 0 and r["attn_fallbacks"] == 0, r
+    assert r["tokens_gpu"] == g["tokens"][:n_out]
+    print(f"dropin_attn mistral: {n_out / r['gpu_seconds']:.2f} tok/s through the reference host loop", flush=True)

@@ -225,19 +225,21 @@ def test_pq_lm_head_topk_two_pass(ops, oracle_lib, k):
     assert float(np.abs(lg2.cpu().numpy().astype(np.float64) - want_lg2).max() / np.abs(want_lg2).max()) <= 1e-4
 
 
+@pytest.mark.parametrize("heavy", [False, True])
 @pytest.mark.parametrize("shape", [(4096, 896, 16, 256, 0), (300, 130, 16, 256, 0), (1000, 64, 8, 128, 40),
                                    (257, 200, 4, 64, 8), (513, 97, 16, 256, 33)])
-def test_pq_one_launch_matches_three_kernels(ops, oracle_lib, shape):
-    """The one-launch kernel (tables on the matrix cores, per-tile arrival
-    counters) against the three-kernel path and the oracle, on ragged row
-    tiles and slabs, with and without outliers; each call twice, so the
-    counters' reset between calls is exercised."""
+def test_pq_one_launch_matches_three_kernels(ops, oracle_lib, shape, heavy):
+    """The one-launch kernel (tables on the matrix cores, per-row fixed-point
+    words) against the three-kernel path and the oracle, on ragged row
+    tiles and slabs, with and without outliers, x N(0,1) and heavy-tailed
+    (Student t, 1.5 dof: the fixed-point scale follows max|x|); each call
+    twice, so the words' reset between calls is exercised."""
     from gen_golden import make_pq
     M, C, G, K, no = shape
-    print(f"case pq one-launch {shape}", flush=True)
+    print(f"case pq one-launch {shape} heavy={heavy}", flush=True)
     rng = np.random.default_rng(M + C)
     t = make_pq(rng, M, C, G, K, 1, 0, no)
-    x = rng.standard_normal(t["N"]).astype(np.float32)
+    x = (rng.standard_t(1.5, t["N"]) if heavy else rng.standard_normal(t["N"])).astype(np.float32)
     ref = oracle_lib.pq_matmul(t, x)
     lib = ops.lib()
     try:
@@ -250,3 +252,46 @@ def test_pq_one_launch_matches_three_kernels(ops, oracle_lib, shape):
     np.testing.assert_array_equal(one, again)
     assert relerr(one, ref) <= 1e-4
     assert relerr(one, three) <= 1e-5
+
+
+def test_pq_one_launch_nonfinite_x(ops, oracle_lib):
+    """A non-finite x on the one-launch path: every row NaN (the CPU gives
+    +-Inf or NaN there), and the next finite call is right again."""
+    from gen_golden import make_pq
+    rng = np.random.default_rng(11)
+    t = make_pq(rng, 4096, 896, 16, 256, 1, 0, 0)
+    x = rng.standard_normal(t["N"]).astype(np.float32)
+    for bad in (np.inf, np.nan):
+        xb = x.copy()
+        xb[123] = bad
+        y = run(ops, t, xb)
+        assert np.isnan(y).all()
+        assert not np.isfinite(oracle_lib.pq_matmul(t, xb)).all()
+    assert relerr(run(ops, t, x), oracle_lib.pq_matmul(t, x)) <= 1e-4
+
+
+def test_pq_workspace_needs_stamp(ops, oracle_lib):
+    """A caller workspace that ibh_pq_workspace_init did not prepare: NaN rows
+    and IBH_DEVERR_PQ_WS, never a silent sum into unknown words; prepared,
+    the same memory gives the right result."""
+    import ctypes
+    from gen_golden import make_pq
+    rng = np.random.default_rng(12)
+    t = make_pq(rng, 4096, 896, 16, 256, 1, 0, 0)
+    x = rng.standard_normal(t["N"]).astype(np.float32)
+    d = ops.PqDeviceTensor(t)
+    lib = ops.lib()
+    assert lib.ibh_device_errors(1) == 0
+    ws = torch.full((d.ws.numel(),), 7, dtype=torch.uint8, device="cuda")   # garbage, no stamp
+    xd = torch.from_numpy(x).cuda()
+    out = torch.empty(t["M"], device="cuda")
+    assert lib.ibh_pq_matmul(ctypes.byref(d.s), xd.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(), None) == 0
+    torch.cuda.synchronize()
+    assert torch.isnan(out).all()
+    assert lib.ibh_device_errors(1) == 2
+    assert lib.ibh_device_errors(0) == 0
+    assert lib.ibh_pq_workspace_init(ws.data_ptr(), ws.numel(), None) == 0
+    assert lib.ibh_pq_matmul(ctypes.byref(d.s), xd.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(), None) == 0
+    torch.cuda.synchronize()
+    assert relerr(out.cpu().numpy(), oracle_lib.pq_matmul(t, x)) <= 1e-4
+    assert lib.ibh_device_errors(0) == 0
