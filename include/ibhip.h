@@ -575,6 +575,33 @@ typedef struct {
 int  ibh_pq_matmul_fp32_host(const ibh_ref_pq_tensor* t, const float* x, float* out);
 /* Frees the device copy of `t` (called from ib_pq_free, src/pq_decode.c:376-387). */
 void ibh_pq_host_release(const ibh_ref_pq_tensor* t);
+/* The PQ branch of ib_pq_session_matmul (src/pq_decode.c:4457-4490) on the
+ * same host tensor: the policy's kernel (STREAMING -> streaming_cached,
+ * L1_ONLY, L2SKIP, SPARSE, INT8; ib_pq_policy has ibh_pq_policy's layout)
+ * on x as the session passes it (after its act-scale pre-multiply).  Same
+ * device copy, return convention and tolerance as ibh_pq_matmul_fp32_host. */
+int  ibh_pq_matmul_policy_host(const ibh_ref_pq_tensor* t, const ibh_pq_policy* p, const float* x, float* out);
+
+/* Layout-identical mirror of the PQ session's INT4 tensor, struct
+ * ib_int4_tensor (src/pq_decode.c:3474-3482, private to that file). */
+typedef struct {
+    char* name;
+    const uint8_t* q;
+    const uint16_t* s;
+    const float* inv_act;
+    const uint16_t* outl_idx;
+    const uint16_t* outl_val;
+    int M, N, G, K_out;
+} ibh_ref_int4_tensor;
+/* The INT4 branch of ib_pq_session_matmul (src/pq_decode.c:4441-4453) on the
+ * session's own tensor: out[M] = W (x * inv_act) with the group scales and
+ * the fp16 outliers, x raw (the pre-scale runs on the device), the
+ * IB_ACT_SPARSE_REL rule read once as the reference does.  First call
+ * builds the device copy (registered regions in place); returns 0 or -1
+ * with a message; rel-err <= 1e-4 against int4_matmul_fp32_threaded. */
+int  ibh_int4g_matmul_host(const ibh_ref_int4_tensor* t, const float* x, float* out);
+/* Frees the device copy of `t` (from ib_pq_session_close, src/pq_decode.c:4333-4372). */
+void ibh_int4g_host_release(const ibh_ref_int4_tensor* t);
 
 #ifdef __cplusplus
 }

@@ -44,6 +44,9 @@ SIGNATURES = {
     "ibh_pq_workspace_init": (I, [P, SZ, P]),
     "ibh_pq_matmul_fp32_host": (I, [P, P, P]),
     "ibh_pq_host_release": (None, [P]),
+    "ibh_pq_matmul_policy_host": (I, [P, P, P, P]),
+    "ibh_int4g_matmul_host": (I, [P, P, P]),
+    "ibh_int4g_host_release": (None, [P]),
     "ibh_device_errors": (I, [I]),
     "ibh_pq_matmul": (I, [P, P, P, P, SZ, P]),
     "ibh_pq_set_fused": (I, [I]),

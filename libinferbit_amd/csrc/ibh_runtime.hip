@@ -663,10 +663,12 @@ int pq_host_entry(const ibh_ref_pq_tensor* t, PqHostEntry** out) {
 }
 }  // namespace
 
-extern "C" int ibh_pq_matmul_fp32_host(const ibh_ref_pq_tensor* t, const float* x, float* out) {
+// policy: NULL = ib_pq_matmul_fp32 (matmul_impl), else the session's dispatch
+static int pq_host_run(const ibh_ref_pq_tensor* t, const ibh_pq_policy* policy, const float* x, float* out,
+                       const char* who) {
     if (!t || !x || !out || t->M <= 0 || t->N <= 0 || t->C <= 0 || t->G <= 0 || t->K <= 0 || !t->codebook_l1_l ||
         !t->indices_l1_l) {
-        ibh_set_error("ibh_pq_matmul_fp32_host: invalid arguments");
+        ibh_set_error("%s: invalid arguments", who);
         return -1;
     }
     std::lock_guard<std::mutex> lk(g_tab_mu);
@@ -676,18 +678,33 @@ extern "C" int ibh_pq_matmul_fp32_host(const ibh_ref_pq_tensor* t, const float* 
     Staged S;
     S.base = workspace(al256(4 * (size_t)t->N) + al256(4 * (size_t)t->M));
     if (!S.base) {
-        ibh_set_error("ibh_pq_matmul_fp32_host: out of device memory");
+        ibh_set_error("%s: out of device memory", who);
         return -1;
     }
     float* dx = (float*)S.put(x, 4 * (size_t)t->N, st);
     float* dout = (float*)S.put(nullptr, 4 * (size_t)t->M, st);
-    if (ibh_pq_matmul(&e->d, dx, dout, e->ws, e->ws_bytes, st) != IBH_OK) return -1;
+    const int rc = policy ? ibh_pq_matmul_policy(&e->d, dx, dout, policy, e->ws, e->ws_bytes, st)
+                          : ibh_pq_matmul(&e->d, dx, dout, e->ws, e->ws_bytes, st);
+    if (rc != IBH_OK) return -1;
     if (hipMemcpyAsync(out, dout, 4 * (size_t)t->M, hipMemcpyDeviceToHost, st) != hipSuccess ||
         hipStreamSynchronize(st) != hipSuccess) {
-        ibh_set_error("ibh_pq_matmul_fp32_host: device copy failed");
+        ibh_set_error("%s: device copy failed", who);
         return -1;
     }
     return 0;
+}
+
+extern "C" int ibh_pq_matmul_fp32_host(const ibh_ref_pq_tensor* t, const float* x, float* out) {
+    return pq_host_run(t, nullptr, x, out, "ibh_pq_matmul_fp32_host");
+}
+
+extern "C" int ibh_pq_matmul_policy_host(const ibh_ref_pq_tensor* t, const ibh_pq_policy* p, const float* x,
+                                         float* out) {
+    if (!p) {
+        ibh_set_error("ibh_pq_matmul_policy_host: null policy");
+        return -1;
+    }
+    return pq_host_run(t, p, x, out, "ibh_pq_matmul_policy_host");
 }
 
 extern "C" void ibh_pq_host_release(const ibh_ref_pq_tensor* t) {
@@ -697,6 +714,183 @@ extern "C" void ibh_pq_host_release(const ibh_ref_pq_tensor* t) {
         if (g_pqh[i].key == t->codebook_l1_l && g_pqh[i].key2 == t->indices_l1_l) {
             pq_host_free(g_pqh[i]);
             g_pqh.erase(g_pqh.begin() + (long)i);
+            return;
+        }
+}
+
+// ── INT4 group-scale matvec on a host ib_int4_tensor (the session's branch) ──
+// The PQ session's INT4 tensors (struct ib_int4_tensor, src/pq_decode.c:
+// 3474-3482) point into the session's mmap or arena.  As for PQ tensors, the
+// first call builds a device copy (registered regions used in place), keyed
+// by the q array and checked by a fingerprint; x goes in raw (the AWQ
+// pre-scale and the outliers run on the device).
+namespace {
+struct I4HostEntry {
+    const void* key;
+    uint64_t fp;
+    uint8_t* blob;
+    void* ws;
+    size_t ws_bytes;
+    ibh_int4g_tensor d;       // inv_act: the device copy of ia_host (or null)
+    const float* ia_host;     // the host AWQ vector last uploaded
+    uint64_t fp_ia;
+    float* ia_dev;
+};
+std::vector<I4HostEntry> g_i4h;
+
+float act_sparse_rel_env() {
+    // read once, as build_skip_mask does (src/pq_decode.c:3855-3863)
+    static float rel = -2.0f;
+    if (rel < -1.0f) {
+        const char* e = getenv("IB_ACT_SPARSE_REL");
+        rel = (e && atof(e) >= 0.0) ? (float)atof(e) : 0.0f;
+    }
+    return rel;
+}
+
+void i4_host_free(I4HostEntry& e) {
+    (void)hipFree(e.blob);
+    (void)hipFree(e.ws);
+    (void)hipFree(e.ia_dev);
+    e.blob = nullptr;
+    e.ws = nullptr;
+    e.ia_dev = nullptr;
+}
+
+// The call's AWQ vector on the device (re-uploaded when the host pointer or
+// its first and last bytes change); d.inv_act follows the call.
+int i4_host_act(I4HostEntry& e, const ibh_ref_int4_tensor* t) {
+    if (!t->inv_act) {
+        e.d.inv_act = nullptr;
+        return IBH_OK;
+    }
+    const size_t n = (size_t)t->N * 4, k = std::min<size_t>(n, 512);
+    const uint64_t fp = fnv(fnv(0xcbf29ce484222325ull, t->inv_act, k), (const uint8_t*)t->inv_act + n - k, k);
+    const uint8_t* res = lookup(t->inv_act, n);
+    if (res) {
+        e.d.inv_act = (const float*)res;
+        return IBH_OK;
+    }
+    if (!e.ia_dev || e.ia_host != t->inv_act || e.fp_ia != fp) {
+        if (!e.ia_dev && hipMalloc((void**)&e.ia_dev, n) != hipSuccess) {
+            ibh_set_error("ibh_int4g_matmul_host: out of device memory");
+            return IBH_ERROR_MEMORY;
+        }
+        if (hipMemcpy(e.ia_dev, t->inv_act, n, hipMemcpyHostToDevice) != hipSuccess) {
+            ibh_set_error("ibh_int4g_matmul_host: upload failed");
+            return IBH_ERROR_INTERNAL;
+        }
+        e.ia_host = t->inv_act;
+        e.fp_ia = fp;
+    }
+    e.d.inv_act = e.ia_dev;
+    return IBH_OK;
+}
+
+int i4_host_entry(const ibh_ref_int4_tensor* t, I4HostEntry** out) {
+    // the AWQ vector is not part of the entry's identity: a caller may pass
+    // the tensor with and without it (the session applies it only when the
+    // row fits its scratch, src/pq_decode.c:4444); it is uploaded on demand
+    const size_t M = (size_t)t->M, N = (size_t)t->N, ko = (size_t)(t->K_out > 0 ? t->K_out : 0);
+    const PqArr a[5] = {{t->q, M * (N / 2)},
+                        {t->s, M * (N / (size_t)t->G) * 2},
+                        {nullptr, 0},
+                        {ko ? t->outl_idx : nullptr, M * ko * 2},
+                        {ko ? t->outl_val : nullptr, M * ko * 2}};
+    const int dims[] = {t->M, t->N, t->G, t->K_out};
+    uint64_t fp = fnv(0xcbf29ce484222325ull, dims, sizeof(dims));
+    for (const PqArr& r : a) {
+        if (!r.h || !r.n) continue;
+        const size_t k = std::min<size_t>(r.n, 512);
+        fp = fnv(fnv(fp, r.h, k), (const uint8_t*)r.h + r.n - k, k);
+    }
+    for (I4HostEntry& e : g_i4h)
+        if (e.key == t->q) {
+            if (e.fp == fp) {
+                *out = &e;
+                return i4_host_act(e, t);
+            }
+            i4_host_free(e);
+            e = g_i4h.back();
+            g_i4h.pop_back();
+            break;
+        }
+    const uint8_t* dev[5];
+    size_t up = 0;
+    for (int i = 0; i < 5; i++) {
+        dev[i] = a[i].h && a[i].n ? lookup(a[i].h, a[i].n) : nullptr;
+        if (a[i].h && a[i].n && !dev[i]) up += al256(a[i].n);
+    }
+    I4HostEntry e{};
+    e.key = t->q;
+    e.fp = fp;
+    if (up && hipMalloc((void**)&e.blob, up) != hipSuccess) {
+        ibh_set_error("ibh_int4g_matmul_host: out of device memory (%zu bytes)", up);
+        return IBH_ERROR_MEMORY;
+    }
+    size_t off = 0;
+    for (int i = 0; i < 5; i++) {
+        if (!a[i].h || !a[i].n || dev[i]) continue;
+        if (hipMemcpy(e.blob + off, a[i].h, a[i].n, hipMemcpyHostToDevice) != hipSuccess) {
+            i4_host_free(e);
+            ibh_set_error("ibh_int4g_matmul_host: upload failed");
+            return IBH_ERROR_INTERNAL;
+        }
+        dev[i] = e.blob + off;
+        off += al256(a[i].n);
+    }
+    e.d.q = dev[0];
+    e.d.s = (const uint16_t*)dev[1];
+    e.d.inv_act = nullptr;
+    e.d.outl_idx = (const uint16_t*)dev[3];
+    e.d.outl_val = (const uint16_t*)dev[4];
+    e.d.M = t->M; e.d.N = t->N; e.d.G = t->G; e.d.K_out = (int)ko;
+    e.ws_bytes = ibh_int4g_workspace_bytes(&e.d);
+    if (e.ws_bytes && hipMalloc(&e.ws, e.ws_bytes) != hipSuccess) {
+        i4_host_free(e);
+        ibh_set_error("ibh_int4g_matmul_host: out of device memory for the workspace");
+        return IBH_ERROR_MEMORY;
+    }
+    g_i4h.push_back(e);
+    *out = &g_i4h.back();
+    return i4_host_act(**out, t);
+}
+}  // namespace
+
+extern "C" int ibh_int4g_matmul_host(const ibh_ref_int4_tensor* t, const float* x, float* out) {
+    if (!t || !x || !out || !t->q || !t->s || t->M <= 0 || t->N <= 0 || t->G <= 0 || t->N % t->G ||
+        (t->K_out > 0 && (!t->outl_idx || !t->outl_val))) {
+        ibh_set_error("ibh_int4g_matmul_host: invalid arguments");
+        return -1;
+    }
+    std::lock_guard<std::mutex> lk(g_tab_mu);
+    I4HostEntry* e = nullptr;
+    if (i4_host_entry(t, &e) != IBH_OK) return -1;
+    hipStream_t st = ibh_resolve_stream(nullptr);
+    Staged S;
+    S.base = workspace(al256(4 * (size_t)t->N) + al256(4 * (size_t)t->M));
+    if (!S.base) {
+        ibh_set_error("ibh_int4g_matmul_host: out of device memory");
+        return -1;
+    }
+    float* dx = (float*)S.put(x, 4 * (size_t)t->N, st);
+    float* dout = (float*)S.put(nullptr, 4 * (size_t)t->M, st);
+    if (ibh_int4g_matmul(&e->d, dx, dout, act_sparse_rel_env(), e->ws, e->ws_bytes, st) != IBH_OK) return -1;
+    if (hipMemcpyAsync(out, dout, 4 * (size_t)t->M, hipMemcpyDeviceToHost, st) != hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess) {
+        ibh_set_error("ibh_int4g_matmul_host: device copy failed");
+        return -1;
+    }
+    return 0;
+}
+
+extern "C" void ibh_int4g_host_release(const ibh_ref_int4_tensor* t) {
+    if (!t) return;
+    std::lock_guard<std::mutex> lk(g_tab_mu);
+    for (size_t i = 0; i < g_i4h.size(); i++)
+        if (g_i4h[i].key == t->q) {
+            i4_host_free(g_i4h[i]);
+            g_i4h.erase(g_i4h.begin() + (long)i);
             return;
         }
 }
