@@ -102,6 +102,16 @@ int ibh_probe(int mode, const void* buf, size_t bytes, void* stream);
  * ordinary loads.  bytes a multiple of 16.  No reference counterpart. */
 int ibh_probe_read(int blocks, int threads, int per_lane, int nontemporal, const void* buf, size_t bytes,
                    void* stream);
+/* The same read, then `nout` floats written to `out` (one per thread of the
+ * first blocks), as a matvec writes its output. */
+int ibh_probe_read_write(int blocks, int threads, int per_lane, int nontemporal, const void* buf, size_t bytes,
+                         float* out, int nout, void* stream);
+/* One wavefront runs a dependent fp32 chain of n steps (n a multiple of 16):
+ * mode 0 adds of register operands, 1 adds of LDS operands read ahead, 2 four
+ * interleaved add chains, 3 fused multiply-adds.  *ns from s_memrealtime
+ * (100 MHz), *clocks from s_memtime.  Synchronous; allocates.  No reference
+ * counterpart: the floor of the exact-mode serial sums. */
+int ibh_probe_chain(int mode, int n, double* ns, double* clocks);
 
 /* Per-128-group int8 activation quantization, bit-identical to
  * ib_quantize_input_int8_g128 (src/threading.c:401-432).  q[N], s[ceil(N/128)]. */

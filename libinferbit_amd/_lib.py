@@ -28,6 +28,8 @@ SIGNATURES = {
     "ibh_set_tile_config": (I, [I, I, I, I]),
     "ibh_probe": (I, [I, P, SZ, P]),
     "ibh_probe_read": (I, [I, I, I, I, P, SZ, P]),
+    "ibh_probe_read_write": (I, [I, I, I, I, P, SZ, P, I, P]),
+    "ibh_probe_chain": (I, [I, I, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "ibh_matmul_w4a8_x_noalloc": (I, [P, P, P, I, P, I, I, P]),
     "ibh_quantize_act_g128": (I, [P, P, P, I, P]),
     "ibh_matmul_w4a8": (I, [P, P, P, I, P, P, I, I, P]),

@@ -14,6 +14,12 @@
 //           share, each wavefront 1 KB per load instruction, U instructions
 //           issued before any result is used, then the next U.  Gives the
 //           one-launch read ceiling the GEMV kernels are held against.
+//   ibh_probe_chain: one wavefront runs a dependent fp32 chain of n steps
+//           (the shape of the exact-mode serial softmax sum and P.V sums) and
+//           reports its duration from the shader's own clocks: mode 0 adds
+//           of register operands, 1 adds of LDS operands read 16 ahead (as
+//           the exact attention's consumer reads them), 2 four independent
+//           add chains interleaved (issue rate), 3 fused multiply-adds.
 #include "ibh_common.h"
 
 using namespace ibh;
@@ -38,7 +44,7 @@ __global__ __launch_bounds__(64) void probe_read(const uint8_t* __restrict__ buf
 
 template <int U, bool NT>
 __global__ __launch_bounds__(1024) void probe_read_shaped(const uint8_t* __restrict__ buf, size_t bytes, size_t share,
-                                                          uint32_t* sink) {
+                                                          uint32_t* sink, float* out, int nout) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const size_t b0 = (size_t)blockIdx.x * share;
     const size_t b1 = b0 + share < bytes ? b0 + share : bytes;
@@ -55,22 +61,115 @@ __global__ __launch_bounds__(1024) void probe_read_shaped(const uint8_t* __restr
         for (int i = 0; i < U; i++) a ^= v[i].x + 3u * v[i].y + 5u * v[i].z + 7u * v[i].w;
     }
     if (a == 0x9e3779b9u && sink) sink[0] = a;
+    // the output a matvec writes: nout floats, one per thread of the first
+    // blocks, after the block's reads
+    const int o = blockIdx.x * blockDim.x + threadIdx.x;
+    if (o < nout) out[o] = (float)(a & 1);
+}
+
+__device__ float probe_chain_sink[64];
+
+template <int MODE>
+__global__ __launch_bounds__(64) void probe_chain(const float* __restrict__ in, int n, unsigned long long* __restrict__ t) {
+    __shared__ __align__(16) float buf[8192];
+    const int lane = threadIdx.x;
+    for (int i = lane; i < 8192; i += 64) buf[i] = in[i & 1023] * (1.0f + (float)(i >> 10) * 1e-3f);
+    __syncthreads();
+    float v[16];
+#pragma unroll
+    for (int u = 0; u < 16; u++) v[u] = buf[lane * 16 + u];
+    float s0 = (float)lane, s1 = 1.f, s2 = 2.f, s3 = 3.f;
+    unsigned long long c0, r0, c1, r1;
+    // the clocks as volatile asm, ordered against the chain's operands and result
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_memtime %0\n\ts_memrealtime %1\n\ts_waitcnt lgkmcnt(0)"
+                 : "=s"(c0), "=s"(r0) : "v"(v[0]), "v"(v[15]) : "memory");
+    if constexpr (MODE == 0 || MODE == 3) {
+        for (int i = 0; i < n; i += 16) {
+#pragma unroll
+            for (int u = 0; u < 16; u++) s0 = MODE == 0 ? s0 + v[u] : fmaf(v[u], v[(u + 1) & 15], s0);
+        }
+    } else if constexpr (MODE == 2) {
+        for (int i = 0; i < n; i += 16) {
+#pragma unroll
+            for (int u = 0; u < 16; u++) {
+                s0 = s0 + v[u]; s1 = s1 + v[(u + 4) & 15]; s2 = s2 + v[(u + 8) & 15]; s3 = s3 + v[(u + 12) & 15];
+            }
+        }
+    } else {
+        float4 cur[4], nxt[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) cur[u] = *(const float4*)(buf + 4 * u);
+        for (int i = 0; i < n; i += 16) {
+            const int j = (i + 16) & 8191;
+#pragma unroll
+            for (int u = 0; u < 4; u++) nxt[u] = *(const float4*)(buf + j + 4 * u);
+#pragma unroll
+            for (int u = 0; u < 4; u++) { s0 = s0 + cur[u].x; s0 = s0 + cur[u].y; s0 = s0 + cur[u].z; s0 = s0 + cur[u].w; }
+#pragma unroll
+            for (int u = 0; u < 4; u++) cur[u] = nxt[u];
+        }
+    }
+    asm volatile("s_memtime %0\n\ts_memrealtime %1\n\ts_waitcnt lgkmcnt(0)"
+                 : "=s"(c1), "=s"(r1) : "v"(s0), "v"(s1), "v"(s2), "v"(s3) : "memory");
+    probe_chain_sink[lane] = s0 + s1 + s2 + s3;
+    if (lane == 0) {
+        t[0] = c1 - c0;
+        t[1] = r1 - r0;
+    }
 }
 
 }  // namespace
 
-extern "C" int ibh_probe_read(int blocks, int threads, int per_lane, int nontemporal, const void* buf, size_t bytes,
-                              void* stream) {
+extern "C" int ibh_probe_chain(int mode, int n, double* ns, double* clocks) {
+    if (mode < 0 || mode > 3 || n < 16 || n % 16 || !ns || !clocks) {
+        ibh_set_error("ibh_probe_chain: mode 0..3, n a positive multiple of 16");
+        return IBH_ERROR_PARAM;
+    }
+    float* in = nullptr;
+    unsigned long long* t = nullptr;
+    IBH_HIP(hipMalloc((void**)&in, 1024 * sizeof(float)), "ibh_probe_chain");
+    if (hipMalloc((void**)&t, 2 * sizeof(unsigned long long)) != hipSuccess) {
+        (void)hipFree(in);
+        ibh_set_error("ibh_probe_chain: out of device memory");
+        return IBH_ERROR_MEMORY;
+    }
+    float h[1024];
+    for (int i = 0; i < 1024; i++) h[i] = 1e-3f * (float)((i * 37) % 101);
+    int rc = IBH_OK;
+    unsigned long long ht[2] = {0, 0};
+    if (hipMemcpy(in, h, sizeof(h), hipMemcpyHostToDevice) != hipSuccess) rc = IBH_ERROR_INTERNAL;
+    for (int rep = 0; rc == IBH_OK && rep < 2; rep++) {   // the first launch warms the code and caches
+        if (mode == 0) probe_chain<0><<<1, 64>>>(in, n, t);
+        else if (mode == 1) probe_chain<1><<<1, 64>>>(in, n, t);
+        else if (mode == 2) probe_chain<2><<<1, 64>>>(in, n, t);
+        else probe_chain<3><<<1, 64>>>(in, n, t);
+        if (hipGetLastError() != hipSuccess || hipMemcpy(ht, t, sizeof(ht), hipMemcpyDeviceToHost) != hipSuccess)
+            rc = IBH_ERROR_INTERNAL;
+    }
+    (void)hipFree(in);
+    (void)hipFree(t);
+    if (rc != IBH_OK) {
+        ibh_set_error("ibh_probe_chain: launch failed");
+        return rc;
+    }
+    *clocks = (double)ht[0];
+    *ns = (double)ht[1] * 10.0;   // s_memrealtime counts at 100 MHz
+    return IBH_OK;
+}
+
+extern "C" int ibh_probe_read_write(int blocks, int threads, int per_lane, int nontemporal, const void* buf,
+                                    size_t bytes, float* out, int nout, void* stream) {
     if (!buf || bytes < 16 || bytes % 16 || blocks < 1 || threads < 64 || threads > 1024 || threads % 64 ||
-        (per_lane != 1 && per_lane != 2 && per_lane != 4 && per_lane != 8 && per_lane != 16)) {
+        (per_lane != 1 && per_lane != 2 && per_lane != 4 && per_lane != 8 && per_lane != 16) || nout < 0 ||
+        (nout > 0 && !out)) {
         ibh_set_error("ibh_probe_read: bytes a multiple of 16 (>= 16), threads 64..1024 by 64, per_lane 1/2/4/8/16");
         return IBH_ERROR_PARAM;
     }
     hipStream_t st = ibh_resolve_stream(stream);
     const size_t share = ((bytes + blocks - 1) / blocks + 1023) / 1024 * 1024;
     const unsigned nb = (unsigned)((bytes + share - 1) / share);
-#define IBH_PR(U_) do { if (nontemporal) probe_read_shaped<U_, true><<<nb, threads, 0, st>>>((const uint8_t*)buf, bytes, share, nullptr); \
-                        else probe_read_shaped<U_, false><<<nb, threads, 0, st>>>((const uint8_t*)buf, bytes, share, nullptr); } while (0)
+#define IBH_PR(U_) do { if (nontemporal) probe_read_shaped<U_, true><<<nb, threads, 0, st>>>((const uint8_t*)buf, bytes, share, nullptr, out, nout); \
+                        else probe_read_shaped<U_, false><<<nb, threads, 0, st>>>((const uint8_t*)buf, bytes, share, nullptr, out, nout); } while (0)
     switch (per_lane) {
     case 1: IBH_PR(1); break;
     case 2: IBH_PR(2); break;
@@ -81,6 +180,11 @@ extern "C" int ibh_probe_read(int blocks, int threads, int per_lane, int nontemp
 #undef IBH_PR
     IBH_CHECK_LAUNCH("ibh_probe_read");
     return IBH_OK;
+}
+
+extern "C" int ibh_probe_read(int blocks, int threads, int per_lane, int nontemporal, const void* buf, size_t bytes,
+                              void* stream) {
+    return ibh_probe_read_write(blocks, threads, per_lane, nontemporal, buf, bytes, nullptr, 0, stream);
 }
 
 extern "C" int ibh_probe(int mode, const void* buf, size_t bytes, void* stream) {
