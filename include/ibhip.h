@@ -190,6 +190,11 @@ int ibh_attn_decode(float* out, const float* q, const void* kdata, const void* v
  * Development switch (no counterpart in the reference): 0 sends them through
  * the 256-thread chunk + merge kernels, 1 (default) the split kernels. */
 int ibh_attn_set_split(int on);
+/* Development switch (no counterpart in the reference) of the exact-order
+ * attention used by the exact decode and ibh_host_attn: 1 (default) scores
+ * the query heads of a KV head together from one coalesced key tile in LDS
+ * (head_dim 64 or 128), 0 one head per launch row.  Same bits either way. */
+int ibh_attn_exact_set_grouped(int on);
 
 /* ── product-quantised LUT matvec, device pointers ─────────── */
 

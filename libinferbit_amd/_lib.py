@@ -41,6 +41,7 @@ SIGNATURES = {
     "ibh_kv_write": (I, [P, P, P, P, I, P, P, I, I, I, P]),
     "ibh_attn_workspace_bytes": (SZ, [I, I, I]),
     "ibh_attn_decode": (I, [P, P, P, P, P, P, I, I, I, I, I, P, SZ, P]),
+    "ibh_attn_exact_set_grouped": (I, [I]),
     "ibh_attn_set_split": (I, [I]),
     "ibh_pq_workspace_bytes": (SZ, [P]),
     "ibh_pq_workspace_init": (I, [P, SZ, P]),

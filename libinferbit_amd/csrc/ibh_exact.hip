@@ -723,6 +723,176 @@ __global__ __launch_bounds__(64) void attn_scores_exact(float* __restrict__ att,
     att[(size_t)h * tstride + t] = score * scale;
 }
 
+// Scores of the GRP query heads that share KV head blockIdx.x, for 64
+// positions per block (one thread each), serial over d as
+// ib_attn_head_task does it (forward.c:474-484: score += q[d] * k[d], the
+// product rounded, then the add; k dequantised as (float)code * scale).  The
+// block's key rows are loaded once, coalesced (each 16-byte segment of a row
+// by a different lane), into LDS, and serve all GRP heads: the per-head form
+// above reads every row GRP times with one row per lane.  ROPE: the block
+// holding position *dpos also rotates k (the fmaf form of
+// rope_kv_write_kernel<true>), writes the position's K and V rows of its KV
+// head, and scores that position from the new key.
+template <int BITS, int GRP, int HD, bool ROPE>
+__global__ __launch_bounds__(64 * GRP) void attn_scores_grp(float* __restrict__ att, const float* __restrict__ q,
+                                                      const uint8_t* __restrict__ kd, const float* __restrict__ ks,
+                                                      const int* __restrict__ dpos, int n_kv, float scale,
+                                                      int tstride, ExRope rp) {
+    constexpr int RB = BITS >= 16 ? 4 * HD : (BITS == 8 ? HD : HD / 2);   // bytes of a key row
+    constexpr int NSEG = RB / 16;
+    constexpr int RS = RB + 16;                                           // LDS row stride (bank spread)
+    constexpr int NT = 64 * GRP;                                          // threads
+    constexpr int PER = (64 * NSEG + NT - 1) / NT;                        // segments per thread
+    constexpr int BATCH = PER < 8 ? PER : 8;                              // segments in flight per thread
+    __shared__ __align__(16) unsigned char kt[64 * RS];
+    __shared__ __align__(16) float qs[GRP][HD];
+    __shared__ __align__(16) float knew[ROPE ? HD : 4];
+    const int kh = blockIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;   // wave g scores query head kh * GRP + g
+    const int T = *dpos + 1;
+    const int c0 = blockIdx.y * 64;
+    if (c0 >= T) return;
+    const int kv_dim = n_kv * HD;
+    const size_t grs = BITS >= 16 ? (size_t)kv_dim * 4 : (BITS == 8 ? (size_t)kv_dim : (size_t)(kv_dim + 1) / 2);
+    const size_t hoff = BITS >= 16 ? (size_t)kh * HD * 4 : (BITS == 8 ? (size_t)kh * HD : (size_t)kh * ((HD + 1) / 2));
+    const int t = c0 + lane;
+    const int tc = min(t, T - 1);
+    // this thread's row scale, then the tile: segment f = i * 64 + lane is
+    // row f / NSEG, bytes 16 (f % NSEG) .. +15
+    float sc = 1.f;
+    if constexpr (BITS < 16) sc = ks[(size_t)tc * n_kv + kh];
+#pragma unroll
+    for (int b0 = 0; b0 < PER; b0 += BATCH) {
+        uint4 v[BATCH];
+#pragma unroll
+        for (int i = 0; i < BATCH; i++) {
+            const int f = min((b0 + i) * NT + (int)threadIdx.x, 64 * NSEG - 1), r = f / NSEG, sg = f - r * NSEG;
+            v[i] = *(const uint4*)(kd + (size_t)min(c0 + r, T - 1) * grs + hoff + 16 * sg);
+        }
+#pragma unroll
+        for (int i = 0; i < BATCH; i++) {
+            const int f = (b0 + i) * NT + (int)threadIdx.x, r = f / NSEG, sg = f - r * NSEG;
+            if (f < 64 * NSEG) *(uint4*)(kt + r * RS + 16 * sg) = v[i];
+        }
+    }
+    const int pcur = T - 1;
+    bool own = false;
+    if constexpr (ROPE) {
+        const int half = HD / 2;
+        const float* tb = rp.table + (size_t)pcur * half * 2;
+        {
+            const float* qh = q + (size_t)(kh * GRP + wave) * HD;
+            for (int j = lane; j < half; j += 64) {
+                const float x0 = qh[2 * j], x1 = qh[2 * j + 1];
+                const float c = tb[2 * j], sn = tb[2 * j + 1];
+                qs[wave][2 * j] = fmaf(x0, c, -(x1 * sn));
+                qs[wave][2 * j + 1] = fmaf(x0, sn, x1 * c);
+            }
+        }
+        if ((int)blockIdx.y == pcur / 64 && wave == 0) {
+            float a[2][2], b[2][2];                        // [side][pair i]: side 0 k (rotated), 1 v
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const int j = lane + 64 * i;
+                const bool on = j < half;
+                const float k0 = on ? rp.k[(size_t)kh * HD + 2 * j] : 0.f, k1 = on ? rp.k[(size_t)kh * HD + 2 * j + 1] : 0.f;
+                const float c = on ? tb[2 * j] : 0.f, sn = on ? tb[2 * j + 1] : 0.f;
+                a[0][i] = on ? fmaf(k0, c, -(k1 * sn)) : 0.f;
+                b[0][i] = on ? fmaf(k0, sn, k1 * c) : 0.f;
+                a[1][i] = on ? rp.v[(size_t)kh * HD + 2 * j] : 0.f;
+                b[1][i] = on ? rp.v[(size_t)kh * HD + 2 * j + 1] : 0.f;
+            }
+#pragma unroll
+            for (int side = 0; side < 2; side++) {
+                uint8_t* dst = side ? rp.vd : rp.kd;
+                if constexpr (BITS >= 16) {
+                    float* row = (float*)dst + (size_t)pcur * kv_dim + (size_t)kh * HD;
+#pragma unroll
+                    for (int i = 0; i < 2; i++) {
+                        const int j = lane + 64 * i;
+                        if (j < half) {
+                            row[2 * j] = a[side][i];
+                            row[2 * j + 1] = b[side][i];
+                            if (side == 0) { knew[2 * j] = a[0][i]; knew[2 * j + 1] = b[0][i]; }
+                        }
+                    }
+                } else {
+                    float mx = fmaxf(fmaxf(fabsf(a[side][0]), fabsf(b[side][0])), fmaxf(fabsf(a[side][1]), fabsf(b[side][1])));
+                    mx = wave_max(mx);
+                    float s2 = mx / (BITS == 8 ? 127.0f : 7.0f);
+                    if (s2 < 1e-8f) s2 = 1e-8f;
+                    const float inv = 1.0f / s2;
+                    if (lane == 0) (side ? rp.vs : rp.ks)[(size_t)pcur * n_kv + kh] = s2;
+#pragma unroll
+                    for (int i = 0; i < 2; i++) {
+                        const int j = lane + 64 * i;
+                        if (j >= half) continue;
+                        int q0 = (int)roundf(a[side][i] * inv), q1 = (int)roundf(b[side][i] * inv);
+                        if constexpr (BITS == 8) {
+                            q0 = q0 < -127 ? -127 : (q0 > 127 ? 127 : q0);
+                            q1 = q1 < -127 ? -127 : (q1 > 127 ? 127 : q1);
+                            int8_t* row = (int8_t*)dst + (size_t)pcur * kv_dim + (size_t)kh * HD;
+                            row[2 * j] = (int8_t)q0;
+                            row[2 * j + 1] = (int8_t)q1;
+                        } else {
+                            q0 = q0 < -7 ? -7 : (q0 > 7 ? 7 : q0);
+                            q1 = q1 < -7 ? -7 : (q1 > 7 ? 7 : q1);
+                            uint8_t* row = dst + (size_t)pcur * ((kv_dim + 1) / 2) + (size_t)kh * ((HD + 1) / 2);
+                            row[j] = (uint8_t)(((q0 + 8) & 0xf) | (((q1 + 8) & 0xf) << 4));
+                        }
+                        if (side == 0) { knew[2 * j] = (float)q0 * s2; knew[2 * j + 1] = (float)q1 * s2; }
+                    }
+                }
+            }
+        }
+        own = (int)blockIdx.y == pcur / 64 && t == pcur;
+    } else {
+        for (int d = lane; d < HD; d += 64) qs[wave][d] = q[(size_t)(kh * GRP + wave) * HD + d];
+    }
+    __syncthreads();
+    if (t >= T) return;
+    float acc = 0.f;
+    const unsigned char* row = kt + lane * RS;
+#pragma unroll 4
+    for (int d0 = 0; d0 < HD; d0 += 16) {
+        float kv[16];
+        if constexpr (BITS >= 16) {
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const float4 v = *(const float4*)(row + 4 * d0 + 16 * u);
+                kv[4 * u] = v.x; kv[4 * u + 1] = v.y; kv[4 * u + 2] = v.z; kv[4 * u + 3] = v.w;
+            }
+        } else if constexpr (BITS == 8) {
+            const uint4 qv = *(const uint4*)(row + d0);
+            const uint32_t w[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+            for (int e = 0; e < 16; e++) kv[e] = (float)(int8_t)(w[e >> 2] >> (8 * (e & 3))) * sc;
+        } else {
+            const uint2 qv = *(const uint2*)(row + d0 / 2);
+            const uint32_t w[2] = {qv.x, qv.y};
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const uint32_t bb = (w[e >> 2] >> (8 * (e & 3))) & 0xffu;
+                kv[2 * e] = (float)((int)(bb & 0xf) - 8) * sc;
+                kv[2 * e + 1] = (float)((int)(bb >> 4) - 8) * sc;
+            }
+        }
+        if (ROPE && own) {
+#pragma unroll
+            for (int e = 0; e < 16; e++) kv[e] = knew[d0 + e];
+        }
+#pragma unroll
+        for (int e4 = 0; e4 < 16; e4 += 4) {
+            const float4 qv = *(const float4*)(&qs[wave][d0 + e4]);
+            acc = acc + qv.x * kv[e4];
+            acc = acc + qv.y * kv[e4 + 1];
+            acc = acc + qv.z * kv[e4 + 2];
+            acc = acc + qv.w * kv[e4 + 3];
+        }
+    }
+    att[(size_t)(kh * GRP + wave) * tstride + t] = acc * scale;
+}
+
 // Softmax over one head's scores and the serial output sum (forward.c:480-502,
 // kernels/avx2.c:192-229).  Block per (head, slice of 64 d), 512 threads:
 //  max (any order is exact); e_t = expf(s_t - max) into LDS; thread 0 sums
@@ -1065,6 +1235,15 @@ int ibh_launch_silu_mul_exact(float* out, const float* g, const float* u, const 
     return IBH_OK;
 }
 
+// Development switch (no counterpart in the reference): 0 scores every head
+// in its own launch grid (attn_scores_exact), 1 (default) the KV-head groups
+// with shared key tiles (attn_scores_grp) where head_dim is 64 or 128.
+static int g_scores_grp = 1;
+extern "C" int ibh_attn_exact_set_grouped(int on) {
+    g_scores_grp = on != 0;
+    return IBH_OK;
+}
+
 size_t ibh_attn_exact_scratch(int n_heads, int max_pos) { return (size_t)n_heads * ((max_pos + 1 + 3) & ~3) * sizeof(float); }
 
 // Attention of the current position (read from dpos) over cache rows 0..pos;
@@ -1115,14 +1294,27 @@ static int launch_attn_exact(float* out, const float* q, const void* kdata, cons
         if (nb3) attn_out_exact<B_, H_, 3><<<n_heads * (H_ / kAoD), kAoThreads, lds, st>>>(out, att, V, vs, dpos, n_heads, n_kv, tstride, tcap); \
         else attn_out_exact<B_, H_, 2><<<n_heads * (H_ / kAoD), kAoThreads, lds, st>>>(out, att, V, vs, dpos, n_heads, n_kv, tstride, tcap); \
     } while (0)
+    const int grp = n_heads / n_kv;
+    const bool grouped = g_scores_grp && (hd == 64 || hd == 128) && (grp == 1 || grp == 2 || grp == 4 || grp == 8);
+    const dim3 g2(n_kv, (max_pos + 1 + 63) / 64);
+    const ExRope rz{};
+#define IBH_AG(B_, G_, H_) do { \
+        if (rope) attn_scores_grp<B_, G_, H_, true><<<g2, 64 * G_, 0, st>>>(att, q, K, ks, dpos, n_kv, scale, tstride, *rope); \
+        else attn_scores_grp<B_, G_, H_, false><<<g2, 64 * G_, 0, st>>>(att, q, K, ks, dpos, n_kv, scale, tstride, rz); \
+    } while (0)
+#define IBH_AGG(B_, H_) do { if (grp == 1) IBH_AG(B_, 1, H_); else if (grp == 2) IBH_AG(B_, 2, H_); \
+                             else if (grp == 4) IBH_AG(B_, 4, H_); else IBH_AG(B_, 8, H_); } while (0)
 #define IBH_AE(B_) do { \
-        if (rope) attn_scores_exact<B_, true><<<g1, 64, 0, st>>>(att, q, K, ks, dpos, n_heads, n_kv, hd, scale, tstride, *rope); \
+        if (grouped) { if (hd == 64) IBH_AGG(B_, 64); else IBH_AGG(B_, 128); } \
+        else if (rope) attn_scores_exact<B_, true><<<g1, 64, 0, st>>>(att, q, K, ks, dpos, n_heads, n_kv, hd, scale, tstride, *rope); \
         else attn_scores_exact<B_, false><<<g1, 64, 0, st>>>(att, q, K, ks, dpos, n_heads, n_kv, hd, scale, tstride); \
         if (hd == 64) IBH_AO(B_, 64); else if (hd == 128) IBH_AO(B_, 128); else IBH_AO(B_, 256); \
     } while (0)
     if (kv_bits >= 16) IBH_AE(32); else if (kv_bits == 8) IBH_AE(8); else IBH_AE(4);
 #undef IBH_AE
 #undef IBH_AO
+#undef IBH_AG
+#undef IBH_AGG
     IBH_CHECK_LAUNCH("exact attention");
     return IBH_OK;
 }

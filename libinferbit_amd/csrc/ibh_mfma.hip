@@ -223,9 +223,9 @@ __global__ __launch_bounds__(512) void gemv_mfma_f32(float* __restrict__ y,
 }
 
 // ── W4A8 ───────────────────────────────────────────────────────────────────
-constexpr int kW4a8Cols = 4;      // batch columns per launch
-
-template <int KIND, bool FUSED, int MAXC>
+// NC batch columns per launch (4, 8 or 16 of the MFMA's 16 B columns),
+// chosen by the launcher from B and what the LDS holds.
+template <int KIND, bool FUSED, int MAXC, int NC>
 __global__ __launch_bounds__(512) void w4a8_mfma(float* __restrict__ y,
                                                  const uint8_t* __restrict__ W,
                                                  const void* __restrict__ sw,
@@ -242,13 +242,102 @@ __global__ __launch_bounds__(512) void w4a8_mfma(float* __restrict__ y,
     const int g0 = wave * CPW;
     const int gn = max(0, min(CPW, G - g0));
     const size_t rb = (size_t)N / 2;
-    float* gs = (float*)smem;                                      // [G][16 rows][kW4a8Cols]
-    uint4* qs = (uint4*)(smem + (size_t)G * kRows * kW4a8Cols * 4) // [wave][chunk][col][8 x 16B]
-                + (size_t)wave * CPW * kW4a8Cols * 8;
+    float* gs = (float*)smem;                                      // [G][16 rows][NC]
+
+    // (a) the B operand straight from global memory (issued before the
+    // weights): lane (i, q) holds column i's codes of its k-quarter, 32
+    // bytes of each chunk of this wavefront
+    uint4 bq[MAXC][2];
+    const bool col = i < B;
+    const int8_t* qrow = qx + (size_t)(col ? i : 0) * N;
+#pragma unroll
+    for (int c = 0; c < MAXC; c++) {
+        const size_t off = min((size_t)(g0 + min(c, gn - 1 < 0 ? 0 : gn - 1)) * 128 + 32 * q, (size_t)N - 32);
+        bq[c][0] = *(const uint4*)(qrow + off);
+        bq[c][1] = *(const uint4*)(qrow + off + 16);
+    }
+    // (b) weights
+    const uint8_t* wrow = W + (size_t)min(row0 + i, M - 1) * rb;
+    uint4 seg[MAXC];
+#pragma unroll
+    for (int c = 0; c < MAXC; c++) {
+        const size_t off = min((size_t)(g0 + c) * 64 + 16 * q, rb - 16);
+        seg[c] = ld_stream16(wrow + off);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // (c) exact int32 group sums on the matrix cores
+    const i4_t zero4 = {0, 0, 0, 0};
+#pragma unroll
+    for (int c = 0; c < MAXC; c++) {
+        if (c >= gn) continue;
+        const uint32_t q8[8] = {col ? bq[c][0].x : 0u, col ? bq[c][0].y : 0u, col ? bq[c][0].z : 0u,
+                                col ? bq[c][0].w : 0u, col ? bq[c][1].x : 0u, col ? bq[c][1].y : 0u,
+                                col ? bq[c][1].z : 0u, col ? bq[c][1].w : 0u};
+        const uint32_t w[4] = {seg[c].x, seg[c].y, seg[c].z, seg[c].w};
+        uint32_t av[8], bv[8];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const uint32_t s = w[e] ^ 0x88888888u;
+            av[2 * e] = (s << 4) & 0xf0f0f0f0u;
+            av[2 * e + 1] = s & 0xf0f0f0f0u;
+            bv[2 * e] = __builtin_amdgcn_perm(q8[2 * e + 1], q8[2 * e], 0x06040200u);
+            bv[2 * e + 1] = __builtin_amdgcn_perm(q8[2 * e + 1], q8[2 * e], 0x07050301u);
+        }
+        i4_t d = __builtin_amdgcn_mfma_i32_16x16x64_i8(i4_t{(int)av[0], (int)av[1], (int)av[2], (int)av[3]},
+                                                       i4_t{(int)bv[0], (int)bv[1], (int)bv[2], (int)bv[3]},
+                                                       zero4, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_i32_16x16x64_i8(i4_t{(int)av[4], (int)av[5], (int)av[6], (int)av[7]},
+                                                  i4_t{(int)bv[4], (int)bv[5], (int)bv[6], (int)bv[7]},
+                                                  d, 0, 0, 0);
+        if (i < B) {
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                gs[((size_t)(g0 + c) * kRows + 4 * q + r) * NC + i] = (float)(d[r] >> 4);
+        }
+    }
+    __syncthreads();
+
+    // (d) serial fold, one thread per (row, column), groups in order
+    const int fr = threadIdx.x / NC, fb = threadIdx.x % NC;
+    if (fr < kRows && fb < B && row0 + fr < M) {
+        const float* sab = sa + (size_t)fb * G_sa;
+        float acc = 0.f;
+        for (int g = 0; g < G; g++) {
+            const float f = gs[((size_t)g * kRows + fr) * NC + fb];
+            if constexpr (FUSED) acc = fmaf(f, sab[g], acc);
+            else acc = acc + f * sab[g];
+        }
+        y[(size_t)fb * M_stride + row0 + fr] = acc * load_scale<KIND>(sw, row0 + fr);
+    }
+}
+
+// The same with the activation codes staged through LDS in load order (fewer,
+// coalesced loads ahead of the weights: the faster form for up to 4 columns).
+template <int KIND, bool FUSED, int MAXC, int NC>
+__global__ __launch_bounds__(512) void w4a8_mfma_lds(float* __restrict__ y,
+                                                 const uint8_t* __restrict__ W,
+                                                 const void* __restrict__ sw,
+                                                 const int8_t* __restrict__ qx,
+                                                 const float* __restrict__ sa,
+                                                 int M, int N, int B, int M_stride, int G_sa,
+                                                 int KW, int CPW) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int i = lane & 15, q = lane >> 4;
+    const int row0 = blockIdx.x * kRows;
+    const int G = (N + 127) / 128;
+    const int g0 = wave * CPW;
+    const int gn = max(0, min(CPW, G - g0));
+    const size_t rb = (size_t)N / 2;
+    float* gs = (float*)smem;                                      // [G][16 rows][NC]
+    uint4* qs = (uint4*)(smem + (size_t)G * kRows * NC * 4) // [wave][chunk][col][8 x 16B]
+                + (size_t)wave * CPW * NC * 8;
 
     // (a) this wavefront's activation codes -> LDS (issued before the weights)
     const int nq = gn * B * 8;                                     // 16-byte pieces
-    constexpr int NQ = (MAXC * kW4a8Cols * 8 + 63) / 64;
+    constexpr int NQ = (MAXC * NC * 8 + 63) / 64;
     uint4 qv[NQ];
 #pragma unroll
     for (int k = 0; k < NQ; k++) {
@@ -273,7 +362,7 @@ __global__ __launch_bounds__(512) void w4a8_mfma(float* __restrict__ y,
         const int u = lane + 64 * k;
         if (u < nq) {
             const int c = u / (B * 8), b = (u / 8) % B, piece = u & 7;
-            qs[(c * kW4a8Cols + b) * 8 + piece] = qv[k];
+            qs[(c * NC + b) * 8 + piece] = qv[k];
         }
     }
     __syncthreads();
@@ -285,8 +374,8 @@ __global__ __launch_bounds__(512) void w4a8_mfma(float* __restrict__ y,
         if (c >= gn) continue;
         uint32_t q8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
         if (i < B) {
-            const uint4 a = qs[(c * kW4a8Cols + i) * 8 + 2 * q];
-            const uint4 b = qs[(c * kW4a8Cols + i) * 8 + 2 * q + 1];
+            const uint4 a = qs[(c * NC + i) * 8 + 2 * q];
+            const uint4 b = qs[(c * NC + i) * 8 + 2 * q + 1];
             q8[0] = a.x; q8[1] = a.y; q8[2] = a.z; q8[3] = a.w;
             q8[4] = b.x; q8[5] = b.y; q8[6] = b.z; q8[7] = b.w;
         }
@@ -309,18 +398,18 @@ __global__ __launch_bounds__(512) void w4a8_mfma(float* __restrict__ y,
         if (i < B) {
 #pragma unroll
             for (int r = 0; r < 4; r++)
-                gs[((size_t)(g0 + c) * kRows + 4 * q + r) * kW4a8Cols + i] = (float)(d[r] >> 4);
+                gs[((size_t)(g0 + c) * kRows + 4 * q + r) * NC + i] = (float)(d[r] >> 4);
         }
     }
     __syncthreads();
 
     // (d) serial fold, one thread per (row, column), groups in order
-    const int fr = threadIdx.x / kW4a8Cols, fb = threadIdx.x % kW4a8Cols;
+    const int fr = threadIdx.x / NC, fb = threadIdx.x % NC;
     if (fr < kRows && fb < B && row0 + fr < M) {
         const float* sab = sa + (size_t)fb * G_sa;
         float acc = 0.f;
         for (int g = 0; g < G; g++) {
-            const float f = gs[((size_t)g * kRows + fr) * kW4a8Cols + fb];
+            const float f = gs[((size_t)g * kRows + fr) * NC + fb];
             if constexpr (FUSED) acc = fmaf(f, sab[g], acc);
             else acc = acc + f * sab[g];
         }
@@ -387,26 +476,38 @@ int ibh_launch_w4a8_mfma(float* out, const void* w, const void* sw, int kind, co
     const int KW = pick_kw(M, G);
     const int CPW = (G + KW - 1) / KW;
     if (CPW > kMaxChunks) return 0;
-    const size_t lds = (size_t)G * kRows * kW4a8Cols * 4 + (size_t)KW * CPW * kW4a8Cols * 8 * 16;
+    auto lds_of = [&](int nc) { return (size_t)G * kRows * nc * 4; };
+    auto lds_st = [&](int nc) { return lds_of(nc) + (size_t)KW * CPW * nc * 8 * 16; };   // w4a8_mfma_lds
+    // batch columns per pass: as many of B as one launch's LDS holds (a
+    // pass reads every weight once)
+    // (the fold takes 16 * NC threads)
+    int NC = 4;
+    if (B > 8 && 16 * 16 <= 64 * KW && lds_of(16) <= 160 * 1024) NC = 16;
+    else if (B > 4 && 16 * 8 <= 64 * KW && lds_of(8) <= 160 * 1024) NC = 8;
+    const size_t lds = NC == 4 ? lds_st(NC) : lds_of(NC);
     const int blocks = (M + kRows - 1) / kRows;
     const uint8_t* W = (const uint8_t*)w;
-    for (int b0 = 0; b0 < B; b0 += kW4a8Cols) {
-        const int nb = min(kW4a8Cols, B - b0);
+    for (int b0 = 0; b0 < B; b0 += NC) {
+        const int nb = min(NC, B - b0);
         float* o = out + (size_t)b0 * M_stride;
         const int8_t* q = qx + (size_t)b0 * N;
         const float* s = sa + (size_t)b0 * G;
-#define IBH_WM3(K_, F_, C_)                                                                                 \
+#define IBH_WM3(KN_, K_, F_, C_, N_)                                                                        \
     do {                                                                                                    \
-        if (!set_lds((const void*)w4a8_mfma<K_, F_, C_>, lds)) return 0;                                   \
-        w4a8_mfma<K_, F_, C_><<<blocks, 64 * KW, lds, st>>>(o, W, sw, q, s, M, N, nb, M_stride, G, KW, CPW); \
+        if (!set_lds((const void*)KN_<K_, F_, C_, N_>, lds)) return 0;                                     \
+        KN_<K_, F_, C_, N_><<<blocks, 64 * KW, lds, st>>>(o, W, sw, q, s, M, N, nb, M_stride, G, KW, CPW);  \
     } while (0)
+#define IBH_WMN(K_, F_, C_) do { if (NC == 16) IBH_WM3(w4a8_mfma, K_, F_, C_, 16); \
+                                 else if (NC == 8) IBH_WM3(w4a8_mfma, K_, F_, C_, 8); \
+                                 else IBH_WM3(w4a8_mfma_lds, K_, F_, C_, 4); } while (0)
 #define IBH_WM(K_, F_)                                                                                      \
     do {                                                                                                    \
-        if (CPW <= 4) IBH_WM3(K_, F_, 4); else if (CPW <= 8) IBH_WM3(K_, F_, 8); else IBH_WM3(K_, F_, 16); \
+        if (CPW <= 4) IBH_WMN(K_, F_, 4); else if (CPW <= 8) IBH_WMN(K_, F_, 8); else IBH_WMN(K_, F_, 16); \
     } while (0)
         if (kind == IBH_SCALE_F16) { if (fused) IBH_WM(IBH_SCALE_F16, true); else IBH_WM(IBH_SCALE_F16, false); }
         else { if (fused) IBH_WM(IBH_SCALE_F32, true); else IBH_WM(IBH_SCALE_F32, false); }
 #undef IBH_WM
+#undef IBH_WMN
 #undef IBH_WM3
     }
     return 1;
