@@ -43,6 +43,8 @@ def parse():
     p.add_argument("--only", choices=["headline", "floor", "gemm", "pq", "pqpol", "int4g", "verify", "v5", "decode-tinyllama",
                             "decode-mistral"],
                    help="run one case and print its JSON (for profiler runs)")
+    p.add_argument("--decode-steps", type=int, default=128,
+                   help="timed decode steps of --only decode-* (fewer for profiler runs)")
     p.add_argument("--calib-copy", action="store_true",
                    help="first copy a 64 MiB buffer 8 times (the known-size kernel that scales the "
                         "FETCH_SIZE / WRITE_SIZE counters in the traffic passes)")
@@ -597,7 +599,7 @@ def main():
                  "14336x4096_plain": int4g_case(torch, L, 14336, 4096, 128, 0, a.steps, a.warmup, awq=False),
                  "4096x14336_plain": int4g_case(torch, L, 4096, 14336, 128, 0, a.steps, a.warmup, awq=False)}
         else:
-            r = decode_case(a.only.split("-", 1)[1], 128, cpu=False)
+            r = decode_case(a.only.split("-", 1)[1], a.decode_steps, cpu=False)
         print(json.dumps({"only": a.only, "result": r}), flush=True)
         return
     print("bench: headline INT4 GEMV 14336x4096", file=sys.stderr, flush=True)
