@@ -382,6 +382,10 @@ def decode_case(name, steps, cpu):
             out["cpu_baseline"] = cpu_decode(path, case, 8, [threads])
         else:
             out["cpu_baseline"] = cpu_decode(path, case, 2, [threads])
+        try:
+            out["dropin"] = dropin_decode(path, case, 32 if name == "tinyllama" else 8)
+        except (RuntimeError, subprocess.TimeoutExpired) as e:
+            out["dropin"] = {"error": str(e)[-300:]}
     return out
 
 
@@ -452,6 +456,52 @@ def cpu_decode(path, case, n_tok, threads_list):
                               + f", {n} decode steps timed ({dt:.2f} s) as the difference of two runs",
                     "host": model, "affinity_cpus": aff})
     return out
+
+
+def dropin_decode(path, case, n_tok):
+    """The drop-in path's decode rate: the reference's own inferbit_generate
+    (oracle/_ref/dropin_attn: the reference's host code compiled from its
+    sources, test infrastructure) with libibhip's dispatch-table entries and
+    attention hook swapped in, weights registered once, threads = 1; the
+    configuration's prompt (and prefilled KV cache).  Reported beside the
+    CPU baseline, not as a product figure: every matvec stages x and y
+    through host memory.  tok/s = n_tok / (generate(1 + n_tok) -
+    generate(1)), the GPU pass only."""
+    sys.path.insert(0, os.path.join(ROOT, "tests", "golden"))
+    import gen_decode_golden as G
+    exe = os.path.join(ROOT, "oracle", "_ref", "dropin_attn")
+    if not os.path.exists(exe):
+        return None
+    pp = path + ".cpu_prompt.i32"
+    G.prompt_of(case).tofile(pp)
+    extra = []
+    if case["kv_pos"]:
+        kvp = path + ".cpu_kv.f32"
+        if not os.path.exists(kvp):
+            k, v = G.kv_of(case)
+            with open(kvp + ".tmp", "wb") as f:
+                f.write(k.tobytes())
+                f.write(v.tobytes())
+            del k, v
+            os.replace(kvp + ".tmp", kvp)
+        extra = [kvp, str(case["kv_pos"])]
+
+    def run(n_out):
+        r = subprocess.run([exe, path, "0", str(n_out), pp, "0", "0"] + extra, capture_output=True, text=True,
+                           timeout=900)
+        if r.returncode != 0:
+            raise RuntimeError(r.stderr[-400:])
+        d = json.loads(r.stdout.strip().splitlines()[-1])
+        if d["attn_fallbacks"] or d["logits_nan"]:
+            raise RuntimeError(f"drop-in pass fell back to the CPU: {d}")
+        return d
+
+    d1, d2 = run(1), run(1 + n_tok)
+    dt = d2["gpu_seconds"] - d1["gpu_seconds"]
+    return {"value": round(n_tok / dt, 2), "unit": "tok/s", "kind": "reference host loop on the GPU table",
+            "sample": f"inferbit_generate greedy (threads 1) with ib_init_kernels_hip + ibh_register_host_weights "
+                      f"+ the ibh_host_attn head-loop hook, {n_tok} decode steps timed ({dt:.2f} s) as the "
+                      f"difference of two runs", "attn_calls": d2["attn_calls"]}
 
 
 V5_TINYLLAMA = dict(num_layers=22, hidden_size=2048, num_heads=32, num_kv_heads=4, head_dim=64,
