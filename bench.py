@@ -40,7 +40,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--quick", action="store_true", help="headline only (for profiling runs)")
     p.add_argument("--no-decode", action="store_true", help="skip the end-to-end decode legs")
-    p.add_argument("--only", choices=["headline", "floor", "gemm", "pq", "pqpol", "int4g", "verify", "v5", "decode-tinyllama",
+    p.add_argument("--only", choices=["headline", "steps", "floor", "gemm", "pq", "pqpol", "int4g", "verify", "v5", "decode-tinyllama",
                             "decode-mistral"],
                    help="run one case and print its JSON (for profiler runs)")
     p.add_argument("--decode-steps", type=int, default=128,
@@ -147,6 +147,30 @@ def gemv_case(torch, L, oracle, bits, M, N, steps, warmup, w4a8=False, seed=0):
     return {"M": M, "N": N, "bits": bits, "w4a8": w4a8, "us": round(t * 1e6, 3),
             "bytes": nbytes, "GBps": round(nbytes / t / 1e9, 1),
             "frac_hbm": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
+
+
+def steps_case(torch, L, oracle, warmup):
+    """The headline kernel timed as in the bench line at several step counts
+    K; a least-squares line through (K, total time) separates the per-launch
+    time (slope) from what one timed graph window adds once (intercept:
+    the gap before a graph's first kernel and the two event markers)."""
+    M, N = 14336, 4096
+    w, s = make_weights(oracle, 4, M, N, 0)
+    wd = torch.from_numpy(w.view(np.uint8).copy()).cuda()
+    copies = [wd] + [wd.clone() for _ in range(COPIES - 1)]
+    sd = torch.from_numpy(s.view(np.int16).copy()).cuda()
+    x = torch.randn(N, generator=torch.Generator().manual_seed(1)).cuda()
+    y = torch.empty(M, device="cuda")
+
+    def launch(i):
+        L.ops.parallel_matmul(y, copies[i % COPIES], sd, x, M, N, 4)
+    ks = (20, 40, 80, 160, 640, 2000)
+    per = {k: time_launches(torch, launch, k, warmup) * 1e6 for k in ks}
+    slope, icpt = np.polyfit(np.array(ks, dtype=float), np.array([per[k] * k for k in ks]), 1)
+    nbytes = matvec_bytes(M, N, 4)
+    return {"us_per_launch": {k: round(v, 3) for k, v in per.items()},
+            "slope_us": round(float(slope), 3), "intercept_us": round(float(icpt), 2),
+            "frac_hbm_at_slope": round(nbytes / (slope * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
 def floor_case(torch, L, steps, warmup):
@@ -631,6 +655,8 @@ def main():
     if a.only:
         if a.only == "headline":
             r = gemv_case(torch, L, oracle, 4, 14336, 4096, a.steps, a.warmup)
+        elif a.only == "steps":
+            r = steps_case(torch, L, oracle, a.warmup)
         elif a.only == "floor":
             r = floor_case(torch, L, a.steps, a.warmup)
         elif a.only == "gemm":

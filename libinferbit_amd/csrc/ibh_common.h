@@ -227,7 +227,8 @@ constexpr uint64_t kExp2fTab[32] = {
     0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
 
-__host__ __device__ inline float ib_expf(float x) {
+// tab: the 32-entry table (kExp2fTab, or a copy of it in LDS)
+__host__ __device__ inline float ib_expf_tab(float x, const uint64_t* tab) {
     constexpr double kN = 32.0;
     constexpr double C0 = 0x1.c6af84b912394p-5 / kN / kN / kN, C1 = 0x1.ebfce50fac4f3p-3 / kN / kN,
                      C2 = 0x1.62e42ff0c52d6p-1 / kN;
@@ -246,7 +247,7 @@ __host__ __device__ inline float ib_expf(float x) {
     const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
     kd -= kShift;
     const double r = __builtin_fma(kInvLn2N, xd, -kd);
-    uint64_t t = kExp2fTab[ki % 32];
+    uint64_t t = tab[ki % 32];
     t += ki << 47;
     const double s = __builtin_bit_cast(double, t);
     const double p = __builtin_fma(C0, r, C1);
@@ -255,6 +256,41 @@ __host__ __device__ inline float ib_expf(float x) {
     y = __builtin_fma(p, r2, y);
     y = y * s;
     return (float)y;
+}
+__host__ __device__ inline float ib_expf(float x) { return ib_expf_tab(x, kExp2fTab); }
+
+// ib_expf_tab without branches: the main path for every input, then the
+// special cases by selection (same results), so several exponentials in a
+// row interleave instead of each one branching.
+__host__ __device__ inline float ib_expf_sel(float x, const uint64_t* tab) {
+    constexpr double kN = 32.0;
+    constexpr double C0 = 0x1.c6af84b912394p-5 / kN / kN / kN, C1 = 0x1.ebfce50fac4f3p-3 / kN / kN,
+                     C2 = 0x1.62e42ff0c52d6p-1 / kN;
+    constexpr double kInvLn2N = 0x1.71547652b82fep+0 * kN, kShift = 0x1.8p+52;
+    const uint32_t ux = __builtin_bit_cast(uint32_t, x);
+    const uint32_t abstop = (ux >> 20) & 0x7ff;
+    const double xd = (double)x;
+    const double z = kInvLn2N * xd;
+    double kd = z + kShift;
+    const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
+    kd -= kShift;
+    const double r = __builtin_fma(kInvLn2N, xd, -kd);
+    uint64_t t = tab[ki % 32];
+    t += ki << 47;
+    const double s = __builtin_bit_cast(double, t);
+    const double p = __builtin_fma(C0, r, C1);
+    const double r2 = r * r;
+    double y = __builtin_fma(C2, r, 1.0);
+    y = __builtin_fma(p, r2, y);
+    y = y * s;
+    const float main = (float)y;
+    // the special cases in rising priority, each a plain select
+    float big = main;
+    big = x < -0x1.9fe368p6f ? 0.0f : big;                  // underflow
+    big = x > 0x1.62e42ep6f ? __builtin_inff() : big;       // overflow
+    big = abstop >= (0x7f800000u >> 20) ? x + x : big;      // inf, nan
+    big = ux == 0xff800000u ? 0.0f : big;                   // -inf
+    return abstop >= (0x42b00000u >> 20) ? big : main;
 }
 
 // Up to three matrices with the same input length (and activation) in one

@@ -898,7 +898,7 @@ __global__ __launch_bounds__(64 * GRP) void attn_scores_grp(float* __restrict__ 
 //  max (any order is exact); e_t = expf(s_t - max) into LDS; thread 0 sums
 //  e_t in position order; a_t = e_t * (1/sum).  Output: wave 0 (one lane per
 //  d of the slice) adds p_t[d] = a_t * v_t[d] in position order; waves 1-7
-//  produce p for the chunks of kAoCH positions ahead into a ring of LDS
+//  produce p for the chunks of CH positions ahead into a ring of LDS
 //  tiles, with their V rows held kAoP chunks ahead in registers (the loads of
 //  the first chunks are issued before the serial sum).  Every barrier after
 //  those loads orders LDS only, so the prefetched loads stay in flight.
@@ -907,13 +907,26 @@ constexpr int kAoD = 16;                                  // d per block = activ
                                                           // halves each block's producer work: the producers,
                                                           // not the consumer's add chain, set the pace at 64)
 constexpr int kAoProd = kAoThreads - 64;
-constexpr int kAoCH = 112;                                // positions per chunk: 112*64/4 = 4 float4 per producer
-constexpr int kAoH = kAoCH / 4;                           // the consumer reads a chunk in quarters (14 LDS reads:
-                                                          // within the 4-bit LDS wait counter)
-constexpr int kAoNG = kAoCH * kAoD / 4 / kAoProd;         // float4 groups per producer per chunk
-static_assert(kAoNG * kAoProd * 4 == kAoCH * kAoD, "chunk split");
+constexpr int kAoH = 56;                                  // the consumer reads a chunk in parts of 56 positions
+                                                          // (14 LDS reads: within the 4-bit LDS wait counter)
 constexpr int kAoP = 4;                                   // chunks of V rows in flight per producer
-constexpr int kAoTile = kAoCH * kAoD;                     // floats per LDS chunk tile
+// Chunk geometry for CH positions per chunk (one barrier step each): 224
+// for long rows (fewer barriers on the consumer's chain), 112 for short ones
+// (half the producer work before the first chunk).  Tiles are column-major
+// [kAoD][TS], so the consumer lane of column d reads 4 positions per 16-byte
+// read; TS = 20 mod 32 spreads 8 lanes' reads over all 32 banks.
+template <int CH>
+struct AoGeo {
+    static constexpr int NP = CH / kAoH;                  // parts per chunk
+    static constexpr int NG = CH * kAoD / 4 / kAoProd;    // float4 groups per producer per chunk
+    static constexpr int TS = CH == 112 ? 116 : 244;      // floats per column of a tile
+    static constexpr int Tile = TS * kAoD;                // floats per LDS chunk tile
+    static_assert(NP * kAoH == CH && NP % 2 == 0, "chunk parts");
+    static_assert(NG * kAoProd * 4 == CH * kAoD, "chunk split");
+    static_assert(TS >= CH && TS % 4 == 0, "tile column");
+};
+constexpr int kAoTileMax = AoGeo<224>::Tile;
+constexpr int kAoShortT = 1024;                           // rows of at most this many positions take CH = 112
 
 // Workgroup barrier that orders LDS only: the LDS stores issued before it are
 // complete (lgkmcnt 0) but outstanding global loads stay in flight, which
@@ -932,54 +945,70 @@ __device__ unsigned long long ibh_ao_tt[256][8];
 #define AO_TT(i) ((void)0)
 #endif
 
-template <int BITS, int HD, int NB>
-__global__ __launch_bounds__(kAoThreads) void attn_out_exact(float* __restrict__ out, const float* __restrict__ att,
-                                                            const uint8_t* __restrict__ vd,
-                                                            const float* __restrict__ vs,
-                                                            const int* __restrict__ dpos, int n_heads, int n_kv,
-                                                            int tstride, int tcap) {
-    extern __shared__ __align__(16) float sm[];
-    __shared__ float red[kAoThreads / 64];
-    __shared__ float inv_s;
+template <int BITS, int HD, int NB, int CH>
+__device__ __forceinline__ void attn_out_body(float* __restrict__ out, const float* __restrict__ att,
+                                              const uint8_t* __restrict__ vd, const float* __restrict__ vs,
+                                              int T, int n_heads, int n_kv, int tstride, int tcap, float* sm,
+                                              float* red, float* inv_sp, uint64_t* etab) {
+    using G = AoGeo<CH>;
+    constexpr int kAoCH = CH, kAoNP = G::NP, kAoNG = G::NG, kAoTS = G::TS, kAoTile = G::Tile;
+    float& inv_s = *inv_sp;
     constexpr int NS = HD / kAoD;
     float* es = sm;                                       // [tcap]
-    float* pbuf = sm + tcap;                              // [NB][kAoCH][kAoD]
+    float* pbuf = sm + tcap;                              // [NB][kAoD][TS]
     const int h = blockIdx.x / NS, d0 = (blockIdx.x % NS) * kAoD;
     const int tid = threadIdx.x, wave = tid >> 6;
-    const int T = *dpos + 1;
     const int kh = h / (n_heads / n_kv);
     const float* a = att + (size_t)h * tstride;
     AO_TT(0);
 
-    // Scores to LDS: every load of the row is issued before any is used (the
-    // scores were just written by another kernel and arrive from a far
-    // cache); then max (any order is exact) and the exponentials in place.
+    // Scores: every load of the row is issued before any is used (the scores
+    // were just written by another kernel and arrive from a far cache).  A
+    // thread keeps its float4s in registers for the max (any order is exact)
+    // and the exponentials, which it writes to LDS.  The launcher caps T at
+    // 8192, so 8 float4 per thread cover the row (n4 <= 2048 < 8 * 512).
     // tstride and the row base are multiples of 4 floats.
     {
         const float4* a4 = (const float4*)a;
         const int n4 = (T + 3) >> 2;
-        for (int f0 = 0; f0 < n4; f0 += 8 * kAoThreads) {
-            float4 v[8];
+        float4 v[8];
 #pragma unroll
-            for (int u = 0; u < 8; u++) v[u] = a4[min(f0 + u * kAoThreads + tid, n4 - 1)];
+        for (int u = 0; u < 8; u++) v[u] = a4[min(u * kAoThreads + tid, n4 - 1)];
+        // ib_expf's table in LDS, from immediates by selection (no global
+        // load, no branch), while the score loads are in flight
+        if (tid < 32) {
+            uint64_t e = 0;
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const int f = f0 + u * kAoThreads + tid;
-                if (f < n4) ((float4*)es)[f] = v[u];
-            }
+            for (int i = 0; i < 32; i++) e = tid == i ? kExp2fTab[i] : e;
+            etab[tid] = e;
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int t0 = 4 * (u * kAoThreads + tid);
+            if (t0 < T) mx = fmaxf(mx, v[u].x);
+            if (t0 + 1 < T) mx = fmaxf(mx, v[u].y);
+            if (t0 + 2 < T) mx = fmaxf(mx, v[u].z);
+            if (t0 + 3 < T) mx = fmaxf(mx, v[u].w);
+        }
+        AO_TT(7);
+        mx = wave_max_dpp(mx);
+        if ((tid & 63) == 0) red[wave] = mx;
+        __syncthreads();
+        AO_TT(1);
+        AO_TT(6);
+        float m = red[0];
+#pragma unroll
+        for (int w = 1; w < kAoThreads / 64; w++) m = fmaxf(m, red[w]);
+        // positions past T in the last float4 get values nobody reads
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int f = u * kAoThreads + tid;
+            if (f < n4)
+                ((float4*)es)[f] = float4{ib_expf_sel(v[u].x - m, etab), ib_expf_sel(v[u].y - m, etab),
+                                          ib_expf_sel(v[u].z - m, etab), ib_expf_sel(v[u].w - m, etab)};
         }
     }
-    __syncthreads();
-    AO_TT(1);
-    float mx = -INFINITY;
-    for (int t = tid; t < T; t += kAoThreads) mx = fmaxf(mx, es[t]);
-    mx = wave_max(mx);
-    if ((tid & 63) == 0) red[wave] = mx;
-    __syncthreads();
-    float m = red[0];
-#pragma unroll
-    for (int w = 1; w < kAoThreads / 64; w++) m = fmaxf(m, red[w]);
-    for (int t = tid; t < T; t += kAoThreads) es[t] = ib_expf(es[t] - m);
     __syncthreads();
     AO_TT(2);
 
@@ -1002,13 +1031,18 @@ __global__ __launch_bounds__(kAoThreads) void attn_out_exact(float* __restrict__
         for (int u = 0; u < kAoNG; u++) t[u] = min(k * kAoCH + gtt[u], T - 1);
         kv_raw4x4<BITS, kAoNG>(r, vd, vs, t, gd, kh, HD, n_kv);
     };
+    float inv = 1.f;                                      // 1 / sum, known after the serial sum
     auto produce = [&](int k, const Kv4x4<BITS, kAoNG>& r) {
-        float4* dst = (float4*)(pbuf + (k % NB) * kAoTile);
+        float* dst = pbuf + (k % NB) * kAoTile;
 #pragma unroll
         for (int u = 0; u < kAoNG; u++) {
-            const float at = es[min(k * kAoCH + gtt[u], T - 1)];
+            const float at = es[min(k * kAoCH + gtt[u], T - 1)] * inv;
             const float4 v = kv_deq4<BITS, kAoNG>(r, u);
-            dst[u * kAoProd + pid] = float4{at * v.x, at * v.y, at * v.z, at * v.w};
+            float* col = dst + (gd[u] - d0) * kAoTS + gtt[u];
+            col[0] = at * v.x;
+            col[kAoTS] = at * v.y;
+            col[2 * kAoTS] = at * v.z;
+            col[3 * kAoTS] = at * v.w;
         }
     };
     if (wave > 0) {
@@ -1016,36 +1050,58 @@ __global__ __launch_bounds__(kAoThreads) void attn_out_exact(float* __restrict__
         for (int k = 0; k < kAoP; k++) fetch(k, ring[k]);
     }
 
-    // serial sum in position order, the next 32 values read while these are added
+    // serial sum in position order.  Two register buffers of 28 values in
+    // turn, B read while A is added and A while B is (no copies between them
+    // on the chain's path; 7 + 7 reads stay within the 4-bit LDS wait
+    // counter, so a wait never covers the reads just issued); sched_barrier
+    // keeps the compiler from sinking each read next to its first use.  The
+    // last < 56 values are read at once and added under a position check.
     if (tid == 0) {
+        constexpr int kC = 64;
         float sum = 0.f;
-        int t = 0;
-        const int T64 = T & ~63;
-        float4 cur[16], nxt[16];
-        if (T64 > 0) {
+        float4 A[kC / 4], B[kC / 4];
+        auto ld = [&](float4 (&v)[kC / 4], int t0) {
 #pragma unroll
-            for (int u = 0; u < 16; u++) cur[u] = *(const float4*)(es + 4 * u);
-        }
-        for (; t < T64; t += 64) {
-            const int tn = min(t + 64, T64 - 64);
+            for (int u = 0; u < kC / 4; u++) v[u] = *(const float4*)(es + t0 + 4 * u);
+        };
+        auto add = [&](const float4 (&v)[kC / 4]) {
 #pragma unroll
-            for (int u = 0; u < 16; u++) nxt[u] = *(const float4*)(es + tn + 4 * u);
-#pragma unroll
-            for (int u = 0; u < 16; u++) {
-                sum = sum + cur[u].x; sum = sum + cur[u].y; sum = sum + cur[u].z; sum = sum + cur[u].w;
+            for (int u = 0; u < kC / 4; u++) {
+                sum = sum + v[u].x; sum = sum + v[u].y; sum = sum + v[u].z; sum = sum + v[u].w;
             }
-#pragma unroll
-            for (int u = 0; u < 16; u++) cur[u] = nxt[u];
+        };
+        const int T2 = T / (2 * kC) * (2 * kC);
+        // nothing else outstanding on the LDS/scalar counter, so the waits in
+        // the loop can be partial
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        if (T2 > 0) ld(A, 0);
+        for (int t = 0; t < T2; t += 2 * kC) {
+            ld(B, t + kC);
+            __builtin_amdgcn_sched_barrier(0);
+            add(A);
+            __builtin_amdgcn_sched_barrier(0);
+            ld(A, min(t + 2 * kC, T2 - kC));
+            __builtin_amdgcn_sched_barrier(0);
+            add(B);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        for (; t < T; t++) sum = sum + es[t];
+        float4 R[2 * kC / 4];
+#pragma unroll
+        for (int u = 0; u < 2 * kC / 4; u++) R[u] = *(const float4*)(es + min(T2 + 4 * u, tcap - 4));
+#pragma unroll
+        for (int u = 0; u < 2 * kC / 4; u++) {
+            const int t = T2 + 4 * u;
+            if (t < T) sum = sum + R[u].x;
+            if (t + 1 < T) sum = sum + R[u].y;
+            if (t + 2 < T) sum = sum + R[u].z;
+            if (t + 3 < T) sum = sum + R[u].w;
+        }
         inv_s = 1.0f / sum;
     }
     lds_barrier();
     AO_TT(3);
-    const float inv = inv_s;
-    for (int t = tid; t < T; t += kAoThreads) es[t] = es[t] * inv;
-    lds_barrier();
     AO_TT(4);
+    inv = inv_s;                                          // a_t = e_t * inv, formed where p_t is
 
     if (wave == 0) {
         // consumer: lane d of the slice; chunk k lives in buffer k % NB.  Its
@@ -1055,25 +1111,27 @@ __global__ __launch_bounds__(kAoThreads) void attn_out_exact(float* __restrict__
         lds_barrier();                                    // chunks 0 .. NB-2 produced
         auto add_part = [&](int k) {                      // the last, partial chunk, from its buffer
             const int tn = T - k * kAoCH;
-            const float* src = pbuf + (k % NB) * kAoTile + tid;
-            for (int e = 0; e < tn; e++) o = o + src[e * kAoD];
+            const float* src = pbuf + (k % NB) * kAoTile + tid * kAoTS;
+            for (int e = 0; e < tn; e++) o = o + src[e];
         };
-        float va[kAoH], vb[kAoH];
-        auto rd = [&](int k, int half, float (&v)[kAoH]) {
-            const float* src = pbuf + (k % NB) * kAoTile + half * kAoH * kAoD + tid;
+        float4 va[kAoH / 4], vb[kAoH / 4];
+        auto rd = [&](int k, int half, float4 (&v)[kAoH / 4]) {
+            const float4* src = (const float4*)(pbuf + (k % NB) * kAoTile + tid * kAoTS + half * kAoH);
 #pragma unroll
-            for (int e = 0; e < kAoH; e++) v[e] = src[e * kAoD];   // immediate LDS offsets
+            for (int e = 0; e < kAoH / 4; e++) v[e] = src[e];   // immediate LDS offsets
         };
-        auto add = [&](const float (&v)[kAoH]) {
+        auto add = [&](const float4 (&v)[kAoH / 4]) {
 #pragma unroll
-            for (int e = 0; e < kAoH; e++) o = o + v[e];
+            for (int e = 0; e < kAoH / 4; e++) {
+                o = o + v[e].x; o = o + v[e].y; o = o + v[e].z; o = o + v[e].w;
+            }
         };
         if constexpr (NB == 2) {
             for (int k = 0; k < nsteps; k++) {
                 if (k < nch) {
                     if (T - k * kAoCH >= kAoCH) {
 #pragma unroll
-                        for (int q = 0; q < 4; q += 2) {
+                        for (int q = 0; q < kAoNP; q += 2) {
                             rd(k, q, va);
                             rd(k, q + 1, vb);
                             add(va);
@@ -1096,12 +1154,12 @@ __global__ __launch_bounds__(kAoThreads) void attn_out_exact(float* __restrict__
             for (int k = 0; k < nsteps; k++) {
                 if (T - k * kAoCH >= kAoCH) {
 #pragma unroll
-                    for (int q = 1; q <= 4; q += 2) {
+                    for (int q = 1; q <= kAoNP; q += 2) {
                         rd(k, q, vb);
                         __builtin_amdgcn_sched_barrier(0);
                         add(va);
                         __builtin_amdgcn_sched_barrier(0);
-                        if (q + 1 < 4) rd(k, q + 1, va);
+                        if (q + 1 < kAoNP) rd(k, q + 1, va);
                         else rd(k + 1, 0, va);
                         __builtin_amdgcn_sched_barrier(0);
                         add(vb);
@@ -1135,6 +1193,23 @@ __global__ __launch_bounds__(kAoThreads) void attn_out_exact(float* __restrict__
             lds_barrier();
         }
     }
+}
+
+template <int BITS, int HD, int NB>
+__global__ __launch_bounds__(kAoThreads) void attn_out_exact(float* __restrict__ out, const float* __restrict__ att,
+                                                            const uint8_t* __restrict__ vd,
+                                                            const float* __restrict__ vs,
+                                                            const int* __restrict__ dpos, int n_heads, int n_kv,
+                                                            int tstride, int tcap) {
+    extern __shared__ __align__(16) float sm[];
+    __shared__ float red[kAoThreads / 64];
+    __shared__ float inv_s;
+    __shared__ uint64_t etab[32];
+    const int T = *dpos + 1;
+    if (T <= kAoShortT)
+        attn_out_body<BITS, HD, NB, 112>(out, att, vd, vs, T, n_heads, n_kv, tstride, tcap, sm, red, &inv_s, etab);
+    else
+        attn_out_body<BITS, HD, NB, 224>(out, att, vd, vs, T, n_heads, n_kv, tstride, tcap, sm, red, &inv_s, etab);
 }
 
 }  // namespace
@@ -1288,8 +1363,8 @@ static int launch_attn_exact(float* out, const float* q, const void* kdata, cons
     const uint8_t* K = (const uint8_t*)kdata;
     const uint8_t* V = (const uint8_t*)vdata;
     const int tcap = (max_pos + 1 + 3) & ~3;
-    const bool nb3 = (size_t)(tcap + 3 * kAoTile) * sizeof(float) <= 160 * 1024;
-    const size_t lds = (size_t)(tcap + (nb3 ? 3 : 2) * kAoTile) * sizeof(float);
+    const bool nb3 = (size_t)(tcap + 3 * kAoTileMax) * sizeof(float) <= 160 * 1024;
+    const size_t lds = (size_t)(tcap + (nb3 ? 3 : 2) * kAoTileMax) * sizeof(float);
 #define IBH_AO(B_, H_) do { \
         if (nb3) attn_out_exact<B_, H_, 3><<<n_heads * (H_ / kAoD), kAoThreads, lds, st>>>(out, att, V, vs, dpos, n_heads, n_kv, tstride, tcap); \
         else attn_out_exact<B_, H_, 2><<<n_heads * (H_ / kAoD), kAoThreads, lds, st>>>(out, att, V, vs, dpos, n_heads, n_kv, tstride, tcap); \
