@@ -156,8 +156,8 @@ __global__ __launch_bounds__(256) void matvec_exact(const RowSet rs, const float
     // of 4, and 4 mod 32 so the 16 chains' 16-byte reads fall in distinct banks)
     const int XSTR = exact_xstride(N);
     float* xs = (float*)smem;                                         // [16][XSTR] (+ 16 slack)
-    int8_t* tile = (int8_t*)(smem + exact_xs_bytes(N));               // [4 waves][4 rows][256]
-    float* xt = (float*)(tile + 4 * 4 * 256);                         // NORM: [8][N/8] chain-major
+    int8_t* tile = (int8_t*)(smem + exact_xs_bytes(N));               // [4 waves][4 rows][2][256]
+    float* xt = (float*)(tile + 4 * 4 * 512);                         // NORM: [8][N/8] chain-major
     __shared__ float part[8];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane >> 4, c = lane & 15;
@@ -165,7 +165,7 @@ __global__ __launch_bounds__(256) void matvec_exact(const RowSet rs, const float
     const int rowc = min(row, M - 1);
     const size_t rb = (size_t)N * BITS / 8;
     const uint8_t* wr = W + (size_t)rowc * rb;
-    int8_t* mytile = tile + (size_t)(wave * 4 + r) * 256;
+    int8_t* mytile = tile + (size_t)(wave * 4 + r) * 512;
     const int nb = N / 16;                                            // whole 16-column blocks
     const int nt = (nb + 15) / 16;                                    // tiles of 16 blocks
     // all of a group's weight loads at once (one 16-column block per tile)
@@ -281,53 +281,73 @@ __global__ __launch_bounds__(256) void matvec_exact(const RowSet rs, const float
     lds_only_barrier();
     MX_TT(3);
     float acc = 0.f;
+    // Tile k of a group: this lane's block (16 columns, one per chain) goes to
+    // the row's LDS buffer, and two transposing reads (ds_read_b64_tr_b8: in
+    // each 16-lane group, lane L receives byte L % 8 of the 8-byte rows that
+    // lanes 2i + L / 8 address, i = 0..7) return byte c of blocks 0..7 and
+    // 8..15, i.e. chain c's 16 weights in order.  Lane L addresses 8L (block
+    // L / 2, half L % 2) for blocks 0..7 and 128 + 8L for blocks 8..15.  The
+    // next tile is staged (its bytes written and read back, and its x read)
+    // before this tile's fma chain, into the other of two buffers; LDS
+    // operations of one wavefront complete in order, so no wait is needed
+    // between a write and the reads of it.
+    typedef int v2i_t __attribute__((ext_vector_type(2)));
+    typedef __attribute__((address_space(3))) v2i_t lds_v2i;
+    auto stage = [&](int k, int8_t* tb, v2i_t& lo, v2i_t& hi, float (&xv)[16], int tile) {
+        int8_t v[16];
+        if constexpr (BITS == 8) {
+            __builtin_memcpy(v, &buf[k], 16);
+        } else {
+            const uint32_t d[2] = {buf[k].x, buf[k].y};
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const uint32_t byte = (d[e >> 2] >> (8 * (e & 3))) & 0xffu;
+                v[2 * e] = (int8_t)((int)(byte & 0xf) - 8);
+                v[2 * e + 1] = (int8_t)((int)(byte >> 4) - 8);
+            }
+        }
+        uint4 pk;
+        __builtin_memcpy(&pk, v, 16);
+        *(uint4*)(tb + 16 * c) = pk;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(tb + 8 * c));
+        hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(tb + 128 + 8 * c));
+        const float4* xc = (const float4*)(xs + c * XSTR + 16 * tile);    // chain c's x, blocks 16 tile ..
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float4 f = xc[q];
+            xv[4 * q] = f.x; xv[4 * q + 1] = f.y; xv[4 * q + 2] = f.z; xv[4 * q + 3] = f.w;
+        }
+    };
+    v2i_t lo[2], hi[2];
+    float xv[2][16];
     for (int g0 = 0; g0 < nt; g0 += 16) {
         if (g0) issue(g0);
+        stage(0, mytile, lo[0], hi[0], xv[0], g0);
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             const int tile = g0 + k;
             if (tile < nt) {
-            int8_t v[16];
-            if constexpr (BITS == 8) {
-                __builtin_memcpy(v, &buf[k], 16);
-            } else {
-                const uint32_t d[2] = {buf[k].x, buf[k].y};
+                if (k + 1 < 16 && tile + 1 < nt)
+                    stage(k + 1 < 16 ? k + 1 : 15, mytile + ((k + 1) & 1) * 256, lo[(k + 1) & 1], hi[(k + 1) & 1],
+                          xv[(k + 1) & 1], tile + 1);
+                const v2i_t L = lo[k & 1], H = hi[k & 1];
+                const uint32_t wd[4] = {(uint32_t)L.x, (uint32_t)L.y, (uint32_t)H.x, (uint32_t)H.y};
+                float wv[16];
 #pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const uint32_t byte = (d[e >> 2] >> (8 * (e & 3))) & 0xffu;
-                    v[2 * e] = (int8_t)((int)(byte & 0xf) - 8);
-                    v[2 * e + 1] = (int8_t)((int)(byte >> 4) - 8);
+                for (int j = 0; j < 16; j++) wv[j] = (float)(int8_t)(wd[j >> 2] >> (8 * (j & 3)));
+                const int nj = min(16, nb - 16 * tile);
+                if (nj == 16) {                                    // whole tile: no select in the fma chain
+#pragma unroll
+                    for (int j = 0; j < 16; j++) acc = fmaf(wv[j], xv[k & 1][j], acc);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 16; j++)
+                        if (j < nj) acc = fmaf(wv[j], xv[k & 1][j], acc);
                 }
-            }
-            uint4 pk;
-            __builtin_memcpy(&pk, v, 16);
-            *(uint4*)(mytile + 16 * c) = pk;
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            const int b0 = 16 * tile;
-            const int nj = min(16, nb - b0);
-            float wv[16], xv[16];
-            const float4* xc = (const float4*)(xs + c * XSTR + b0);    // chain c's x, blocks b0 ..
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const float4 f = xc[q];
-                xv[4 * q] = f.x; xv[4 * q + 1] = f.y; xv[4 * q + 2] = f.z; xv[4 * q + 3] = f.w;
-            }
-#pragma unroll
-            for (int j = 0; j < 16; j++) wv[j] = (float)mytile[16 * j + c];
-            if (nj == 16) {                                        // whole tile: no select in the fma chain
-#pragma unroll
-                for (int j = 0; j < 16; j++) acc = fmaf(wv[j], xv[j], acc);
-            } else {
-#pragma unroll
-                for (int j = 0; j < 16; j++)
-                    if (j < nj) acc = fmaf(wv[j], xv[j], acc);
-            }
-            if (tile == 0) MX_TT(4);
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                if (tile == 0) MX_TT(4);
             }
         }
     }
@@ -1230,7 +1250,7 @@ int ibh_launch_matvec_exact_multi(const MatDesc* d, int n, int kind, const float
                                   float* xr = nullptr, float eps = 0.f);
 
 size_t ibh_exact_matvec_lds(int N, bool norm) {
-    return exact_xs_bytes(N) + 4 * 4 * 256 + (norm ? (size_t)N * 4 : 0);
+    return exact_xs_bytes(N) + 4 * 4 * 512 + (norm ? (size_t)N * 4 : 0);
 }
 
 int ibh_launch_matvec_exact(float* y, const void* w, const void* sc, int kind, const float* x, int M, int N, int bits,
@@ -1256,7 +1276,7 @@ int ibh_launch_matvec_exact(float* y, const void* w, const void* sc, int kind, c
 int ibh_launch_matvec_exact_multi(const MatDesc* d, int n, int kind, const float* x, int N, int bits,
                                   hipStream_t st, const float* dl, const uint16_t* nw, float* xr, float eps) {
     const size_t lds = ibh_exact_matvec_lds(N, nw != nullptr);
-    if ((bits != 8 && bits != 4) || lds > 64 * 1024 || (bits == 4 && N % 2) || n < 1 || n > 3) {
+    if ((bits != 8 && bits != 4) || lds > 160 * 1024 || (bits == 4 && N % 2) || n < 1 || n > 3) {
         ibh_set_error("exact matvec: bits=%d N=%d unsupported", bits, N);
         return IBH_ERROR_PARAM;
     }
