@@ -60,3 +60,45 @@ def test_grouped_scores_bit_identical(lib, bits, hd, n_heads, n_kv, T):
         lib.ibh_host_kv_release(C.c_void_p(key))
     assert np.isfinite(a).all()
     np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def scores_case(rng, kind, T, n_kv, hd):
+    """fp32 K/V rows whose scores stress the exact softmax sum: random,
+    flat (every e_t = 1: the sum is an integer), few distinct values (long
+    runs of equal terms: many round-to-even ties), peaky (terms spanning
+    many binades, underflow to 0), and a sum that crosses many binades."""
+    kv_dim = n_kv * hd
+    v = rng.standard_normal((T, kv_dim)).astype(np.float32)
+    if kind == "random":
+        k = rng.standard_normal((T, kv_dim)).astype(np.float32)
+    elif kind == "flat":
+        k = np.zeros((T, kv_dim), np.float32)
+    elif kind == "few":
+        k = rng.choice(np.array([-1.0, -0.5, 0.0, 0.25], np.float32), (T, kv_dim))
+    elif kind == "peaky":
+        k = (rng.standard_normal((T, kv_dim)) * 6).astype(np.float32)
+    else:  # "ramp": scores rise along t, so the partial sums climb through many binades
+        k = np.outer(np.linspace(-4, 0.5, T), np.ones(kv_dim)).astype(np.float32)
+    return [k, v, None, None]
+
+
+@pytest.mark.parametrize("kind", ["random", "flat", "few", "peaky", "ramp"])
+@pytest.mark.parametrize("hd,n_heads,n_kv,T", [(128, 32, 8, 4176), (64, 32, 4, 111), (128, 8, 8, 8000), (64, 8, 2, 1)])
+def test_exact_attention_matches_oracle_bits(lib, oracle_lib, kind, hd, n_heads, n_kv, T):
+    """Same bits as the oracle's restatement of the x86 head loop (serial
+    dot, max, expf, serial sum, serial P.V): the device sums the softmax
+    denominator by binade jumps and must still equal the serial sum."""
+    print(f"case exact attention vs oracle kind={kind} hd={hd} heads={n_heads}/{n_kv} T={T}", flush=True)
+    rng = np.random.default_rng([len(kind), ord(kind[0]), hd, T])
+    arrs = scores_case(rng, kind, T, n_kv, hd)
+    q = rng.standard_normal(n_heads * hd).astype(np.float32)
+    if kind == "few":
+        q = np.abs(q).round(1).astype(np.float32)
+    key = 0x2000 + hd + T
+    try:
+        got = run(lib, key, arrs, T, 32, q, n_heads, n_kv, hd)
+    finally:
+        lib.ibh_host_kv_release(C.c_void_p(key))
+    ref = oracle_lib.attn_decode(q, [arrs[0], arrs[1], np.zeros(1, np.float32), np.zeros(1, np.float32)], T - 1,
+                                 n_heads, n_kv, hd, 32)
+    np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
