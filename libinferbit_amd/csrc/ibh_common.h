@@ -60,6 +60,19 @@ __device__ __forceinline__ float load_scale(const void* s, int i) {
     if constexpr (KIND == IBH_SCALE_F16) return f16_to_f32(((const uint16_t*)s)[i]);
     else return ((const float*)s)[i];
 }
+// The scale's raw bits, fetched early (a kernel's first loads) and widened
+// where it is used: an epilogue that loaded it there would wait a memory
+// round trip after its last MFMA.
+template <int KIND>
+__device__ __forceinline__ uint32_t scale_bits(const void* s, int i) {
+    if constexpr (KIND == IBH_SCALE_F16) return ((const uint16_t*)s)[i];
+    else return ((const uint32_t*)s)[i];
+}
+template <int KIND>
+__device__ __forceinline__ float scale_from_bits(uint32_t b) {
+    if constexpr (KIND == IBH_SCALE_F16) return f16_to_f32((uint16_t)b);
+    else return __builtin_bit_cast(float, b);
+}
 
 // Workgroup barrier that orders LDS only: LDS operations issued before it are
 // complete (lgkmcnt 0) but global loads stay in flight.  __syncthreads() is a

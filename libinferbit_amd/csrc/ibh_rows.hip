@@ -122,10 +122,15 @@ __global__ __launch_bounds__(512) void gemv_rows_w4a8(float* __restrict__ y, con
     const int row0 = blockIdx.x * RB + wr * R;
     const size_t rb = (size_t)N / 2;
     const int G = (N + 127) / 128;
-    const int Gp = (G + 3) & ~3;                           // padded LDS row stride
+    const int Gp = (G + 15) & ~15;                         // padded LDS row stride (whole batches of 4 float4)
     float* gsum = (float*)smem;                            // [RB][Gp]
     float* sa_s = gsum + (size_t)RB * Gp;                  // [Gp]  (!SAREG)
     const int segl = seg_of<true>(lane);
+    // the row this thread folds at the end (if any): its scale and, for a
+    // residual add, its old value, fetched before the weights
+    const int frc = min(SAREG ? row0 + lane : (int)(blockIdx.x * RB + threadIdx.x), M - 1);
+    const uint32_t scb = scale_bits<KIND>(sc, frc);
+    const float yold = y[frc];
 
     // small operands first (their waits then cover no weight load)
     float4 sav[SAREG ? 8 : 1];
@@ -195,26 +200,54 @@ __global__ __launch_bounds__(512) void gemv_rows_w4a8(float* __restrict__ y, con
                 if (4 * q + 2 < G) f = fmaf(a4.z, s4.z, f);
                 if (4 * q + 3 < G) f = fmaf(a4.w, s4.w, f);
             }
-            const float yv = f * load_scale<KIND>(sc, row);
-            y[row] = accy ? y[row] + yv : yv;
+            const float yv = f * scale_from_bits<KIND>(scb);
+            y[row] = accy ? yold + yv : yv;
         }
     } else {
         if (threadIdx.x < G) sa_s[threadIdx.x] = sa_mine;
         for (int g = G + (int)threadIdx.x; g < Gp; g += blockDim.x) sa_s[g] = 0.f;
+        for (int e = (int)threadIdx.x; e < RB * (Gp - G); e += blockDim.x)        // gsum padding
+            gsum[(size_t)(e / (Gp - G)) * Gp + G + e % (Gp - G)] = 0.f;
         __syncthreads();
         const int fr = threadIdx.x;
         const int row = blockIdx.x * RB + fr;
         if (fr < RB && row < M) {
-            const float* gp = gsum + (size_t)fr * Gp;
+            // the serial fold over Gp groups (the padding holds 0 in both
+            // operands: fmaf(0, 0, f) = f, f never being -0), 16 groups per
+            // batch, the next batch read while this one is folded, in two
+            // register buffers taken in turn (no copies on the chain's path)
+            const float4* g4 = (const float4*)(gsum + (size_t)fr * Gp);
+            const float4* s4 = (const float4*)sa_s;
+            const int nb = Gp >> 4;
             float f = 0.f;
-            int g = 0;
-            for (; g + 4 <= G; g += 4) {
-                const float4 a4 = *(const float4*)(gp + g), s4 = *(const float4*)(sa_s + g);
-                f = fmaf(a4.x, s4.x, f); f = fmaf(a4.y, s4.y, f); f = fmaf(a4.z, s4.z, f); f = fmaf(a4.w, s4.w, f);
+            float4 ga[4], sa[4], gb[4], sb[4];
+            auto ld = [&](float4 (&gv)[4], float4 (&sv)[4], int bi) {
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    gv[u] = g4[4 * bi + u];
+                    sv[u] = s4[4 * bi + u];
+                }
+            };
+            auto fold = [&](const float4 (&gv)[4], const float4 (&sv)[4]) {
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    f = fmaf(gv[u].x, sv[u].x, f); f = fmaf(gv[u].y, sv[u].y, f);
+                    f = fmaf(gv[u].z, sv[u].z, f); f = fmaf(gv[u].w, sv[u].w, f);
+                }
+            };
+            ld(ga, sa, 0);
+            for (int bi = 0; bi < nb; bi += 2) {
+                ld(gb, sb, min(bi + 1, nb - 1));
+                __builtin_amdgcn_sched_barrier(0);
+                fold(ga, sa);
+                __builtin_amdgcn_sched_barrier(0);
+                ld(ga, sa, min(bi + 2, nb - 1));
+                __builtin_amdgcn_sched_barrier(0);
+                if (bi + 1 < nb) fold(gb, sb);
+                __builtin_amdgcn_sched_barrier(0);
             }
-            for (; g < G; g++) f = fmaf(gp[g], sa_s[g], f);
-            const float yv = f * load_scale<KIND>(sc, row);
-            y[row] = accy ? y[row] + yv : yv;
+            const float yv = f * scale_from_bits<KIND>(scb);
+            y[row] = accy ? yold + yv : yv;
         }
     }
 }
@@ -984,7 +1017,7 @@ int ibh_launch_rows_w4a8(float* out, const void* w, const void* sw, int kind, co
     if (WR * KW > 8) return 0;
     const int nthreads = 64 * WR * KW;
     const int G = (N + 127) / 128;
-    const int Gp = (G + 3) & ~3;
+    const int Gp = (G + 15) & ~15;
     const bool sareg = KW == 1 && G <= 32;
     if (!sareg && G > nthreads) return 0;
     const size_t lds = (size_t)(WR * R * Gp + (sareg ? 0 : Gp)) * 4;
