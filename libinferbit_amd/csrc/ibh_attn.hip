@@ -656,14 +656,25 @@ __global__ __launch_bounds__(kSplitThreads) void attn_split(float* __restrict__ 
     __shared__ float mlr[GRP][2];
     __shared__ __align__(16) float ob[TR][GRP][HD];
 
-    // 1. this thread's K and V piece (position clamped to the last valid one)
+    // 1. this thread's K and V piece (position clamped to the last valid one).
+    // A wavefront whose positions all lie past the chunk's end (a short
+    // chunk: the last one, or every one while the context is short) loads
+    // nothing and scores nothing (its scores are -inf).
     const int t = tid / PIECES, pc = tid % PIECES;
+    const bool wact = (tid & ~63) / PIECES < tn;          // wave-uniform
     const int pos = t0 + min(t, tn - 1);
     uint4 kr[NR], vr[NR];
-    piece_load<BITS>(kd + (size_t)pos * row_bytes + (size_t)kh * RB + pc * PB, kr);
-    piece_load<BITS>(vd + (size_t)pos * row_bytes + (size_t)kh * RB + pc * PB, vr);
-    float ksc = BITS == 32 ? 1.f : ks[(size_t)pos * n_kv + kh];
-    float vsv = BITS == 32 ? 1.f : vs[(size_t)pos * n_kv + kh];
+#pragma unroll
+    for (int j = 0; j < NR; j++) kr[j] = vr[j] = make_uint4(0u, 0u, 0u, 0u);
+    float ksc = 1.f, vsv = 1.f;
+    if (wact) {
+        piece_load<BITS>(kd + (size_t)pos * row_bytes + (size_t)kh * RB + pc * PB, kr);
+        piece_load<BITS>(vd + (size_t)pos * row_bytes + (size_t)kh * RB + pc * PB, vr);
+        if constexpr (BITS != 32) {
+            ksc = ks[(size_t)pos * n_kv + kh];
+            vsv = vs[(size_t)pos * n_kv + kh];
+        }
+    }
     if constexpr (ROPE) {
         // q of the group rotated into LDS; the block holding position T - 1
         // rotates k, quantizes the k and v rows of head kh into the caches
@@ -751,32 +762,37 @@ __global__ __launch_bounds__(kSplitThreads) void attn_split(float* __restrict__ 
 
     AS_TT(1);
     // 2. scores: the piece's dot with each head, summed over the position's lanes
-    float kv[16];
-    piece_vals<BITS>(kr, kv);
-    float s[GRP];
+    if (wact) {
+        float kv[16];
+        piece_vals<BITS>(kr, kv);
+        float s[GRP];
 #pragma unroll
-    for (int g = 0; g < GRP; g++) {
-        float a = 0.f;
+        for (int g = 0; g < GRP; g++) {
+            float a = 0.f;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const float4 qq = *(const float4*)&qs[g][pc * 16 + 4 * j];
-            a += qq.x * kv[4 * j] + qq.y * kv[4 * j + 1] + qq.z * kv[4 * j + 2] + qq.w * kv[4 * j + 3];
+            for (int j = 0; j < 4; j++) {
+                const float4 qq = *(const float4*)&qs[g][pc * 16 + 4 * j];
+                a += qq.x * kv[4 * j] + qq.y * kv[4 * j + 1] + qq.z * kv[4 * j + 2] + qq.w * kv[4 * j + 3];
+            }
+            s[g] = a;
         }
-        s[g] = a;
-    }
 #pragma unroll
-    for (int g = 0; g < GRP; g++) s[g] = group_sum_dpp<PIECES>(s[g]);
-    if (pc == 0) {
+        for (int g = 0; g < GRP; g++) s[g] = group_sum_dpp<PIECES>(s[g]);
+        if (pc == 0) {
 #pragma unroll
-        for (int g = 0; g < GRP; g++) sc[g][t] = t < tn ? s[g] * ksc * scale : -INFINITY;
-    }
-    // V piece into LDS
+            for (int g = 0; g < GRP; g++) sc[g][t] = t < tn ? s[g] * ksc * scale : -INFINITY;
+        }
+        // V piece into LDS
 #pragma unroll
-    for (int j = 0; j < NR; j++) {
-        if constexpr (BITS == 4) *(uint2*)&vsh[t][pc * PB] = make_uint2(vr[0].x, vr[0].y);
-        else ((uint4*)&vsh[t][pc * PB])[j] = vr[j];
+        for (int j = 0; j < NR; j++) {
+            if constexpr (BITS == 4) *(uint2*)&vsh[t][pc * PB] = make_uint2(vr[0].x, vr[0].y);
+            else ((uint4*)&vsh[t][pc * PB])[j] = vr[j];
+        }
+        if (pc == 0) vsc[t] = vsv;
+    } else if (pc == 0) {
+#pragma unroll
+        for (int g = 0; g < GRP; g++) sc[g][t] = -INFINITY;
     }
-    if (pc == 0) vsc[t] = vsv;
     __syncthreads();
     AS_TT(2);
 
