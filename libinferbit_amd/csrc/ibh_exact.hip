@@ -1108,13 +1108,19 @@ __device__ __forceinline__ void attn_out_body(float* __restrict__ out, const flo
         float4 R[2 * kC / 4];
 #pragma unroll
         for (int u = 0; u < 2 * kC / 4; u++) R[u] = *(const float4*)(es + min(T2 + 4 * u, tcap - 4));
+        // whole float4s without a check on the chain, then the last partial one
+        const int nf = (T - T2) >> 2, nr = (T - T2) & 3;
 #pragma unroll
         for (int u = 0; u < 2 * kC / 4; u++) {
-            const int t = T2 + 4 * u;
-            if (t < T) sum = sum + R[u].x;
-            if (t + 1 < T) sum = sum + R[u].y;
-            if (t + 2 < T) sum = sum + R[u].z;
-            if (t + 3 < T) sum = sum + R[u].w;
+            if (u < nf) {
+                sum = sum + R[u].x; sum = sum + R[u].y; sum = sum + R[u].z; sum = sum + R[u].w;
+            }
+        }
+        if (nr) {
+            const float4 p = *(const float4*)(es + T2 + 4 * nf);
+            sum = sum + p.x;
+            if (nr > 1) sum = sum + p.y;
+            if (nr > 2) sum = sum + p.z;
         }
         inv_s = 1.0f / sum;
     }
@@ -1132,7 +1138,14 @@ __device__ __forceinline__ void attn_out_body(float* __restrict__ out, const flo
         auto add_part = [&](int k) {                      // the last, partial chunk, from its buffer
             const int tn = T - k * kAoCH;
             const float* src = pbuf + (k % NB) * kAoTile + tid * kAoTS;
-            for (int e = 0; e < tn; e++) o = o + src[e];
+            const float4* s4 = (const float4*)src;
+            const int nf = tn >> 2;
+#pragma unroll 4
+            for (int e = 0; e < nf; e++) {
+                const float4 v = s4[e];
+                o = o + v.x; o = o + v.y; o = o + v.z; o = o + v.w;
+            }
+            for (int e = 4 * nf; e < tn; e++) o = o + src[e];
         };
         float4 va[kAoH / 4], vb[kAoH / 4];
         auto rd = [&](int k, int half, float4 (&v)[kAoH / 4]) {
