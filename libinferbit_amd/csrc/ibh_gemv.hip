@@ -305,18 +305,19 @@ __global__ __launch_bounds__(kBlock) void silu_quant_g128(float* __restrict__ ou
     if (base >= N) return;
     const int end = min(N, base + 128);
     const int j0 = base + lane, j1 = base + lane + 64;
+    // all four loads first (clamped addresses), one memory round trip
+    const int c0 = min(j0, end - 1), c1 = min(j1, end - 1);
+    const float g0 = gate[c0], g1 = gate[c1], u0 = up[c0], u1 = up[c1];
+    const bool on0 = j0 < end && (!mask || mask[c0]), on1 = j1 < end && (!mask || mask[c1]);
     float h[2];
 #pragma unroll
     for (int e = 0; e < 2; e++) {
-        const int j = e ? j1 : j0;
-        h[e] = 0.f;
-        if (j < end) {
-            const bool on = !mask || mask[j];
-            const float gv = on ? gate[j] : 0.f, uv = on ? up[j] : 0.f;
-            h[e] = (gv / (1.0f + (EXACT ? ib_expf(-gv) : expf(-gv)))) * uv;
-            out[j] = h[e];
-        }
+        const bool on = e ? on1 : on0;
+        const float gv = on ? (e ? g1 : g0) : 0.f, uv = on ? (e ? u1 : u0) : 0.f;
+        h[e] = (gv / (1.0f + (EXACT ? ib_expf_sel(-gv, kExp2fTab) : expf(-gv)))) * uv;
     }
+    if (j0 < end) out[j0] = h[0];
+    if (j1 < end) out[j1] = h[1];
     quant_group(h[0], h[1], j0, j1, end, g, q, s);
 }
 
