@@ -172,6 +172,7 @@ __global__ __launch_bounds__(256) void matvec_exact(const RowSet rs, const float
     // (a native vector array and no early exit from the unrolled loops keep
     // buf in registers: all 16 loads are in flight together)
     u32x4_t buf[16];
+    uint32_t scb = 0;
     auto issue = [&](int g0) {
 #pragma unroll
         for (int k = 0; k < 16; k++) {
@@ -213,6 +214,8 @@ __global__ __launch_bounds__(256) void matvec_exact(const RowSet rs, const float
         }
         issue(0);
         MX_TT(1);
+        // the row's scale, needed last, loaded behind the weights
+        scb = scale_bits<KIND>(sc, rowc);
         if constexpr (NORM == 2) {
 #pragma unroll
             for (int u = 0; u < NQ; u++) {
@@ -367,7 +370,7 @@ __global__ __launch_bounds__(256) void matvec_exact(const RowSet rs, const float
             }
             res = fmaf(wv, xs[(j & 15) * XSTR + (j >> 4)], res);
         }
-        y[row] = res * load_scale<KIND>(sc, row);
+        y[row] = res * scale_from_bits<KIND>(scb);
     }
 }
 
