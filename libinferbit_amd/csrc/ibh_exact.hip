@@ -773,13 +773,50 @@ __global__ __launch_bounds__(64 * GRP) void attn_scores_grp(float* __restrict__ 
     const int kh = blockIdx.x;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;   // wave g scores query head kh * GRP + g
     const int T = *dpos + 1;
-    const int c0 = blockIdx.y * 64;
+    // position tiles in reverse launch order: the tile of the current
+    // position (the block with the cache write) is dispatched first instead of
+    // last, onto a CU not yet shared with two other tiles
+    const int ty = (int)gridDim.y - 1 - (int)blockIdx.y;
+    const int c0 = ty * 64;
     if (c0 >= T) return;
     const int kv_dim = n_kv * HD;
     const size_t grs = BITS >= 16 ? (size_t)kv_dim * 4 : (BITS == 8 ? (size_t)kv_dim : (size_t)(kv_dim + 1) / 2);
     const size_t hoff = BITS >= 16 ? (size_t)kh * HD * 4 : (BITS == 8 ? (size_t)kh * HD : (size_t)kh * ((HD + 1) / 2));
     const int t = c0 + lane;
     const int tc = min(t, T - 1);
+    // ROPE: q's pairs (and, in the block of the current position, the new
+    // k and v pairs) are loaded before the key tile, so the rotation and the
+    // cache write do not wait behind it; pair j = lane + 64 i, i < 2
+    const int pcur = T - 1;
+    // the current position's k is written by wavefront 0 and its v by
+    // wavefront 1 (wavefront 0 both when the group is one head)
+    constexpr bool kSides2 = GRP >= 2;
+    const bool pblk = ROPE && ty == pcur / 64 && wave < (kSides2 ? 2 : 1);
+    const int side0 = kSides2 ? wave : 0, side1 = kSides2 ? wave : 1;
+    float rq[2][2] = {}, rt[2][2] = {}, rk[2][2] = {}, rv[2][2] = {};
+    if constexpr (ROPE) {
+        const int half = HD / 2;
+        const float* tb = rp.table + (size_t)pcur * half * 2;
+        const float* qh = q + (size_t)(kh * GRP + wave) * HD;
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int j = lane + 64 * i;
+            if (j < half) {
+                rq[i][0] = qh[2 * j];
+                rq[i][1] = qh[2 * j + 1];
+                rt[i][0] = tb[2 * j];
+                rt[i][1] = tb[2 * j + 1];
+                if (pblk && side0 == 0) {
+                    rk[i][0] = rp.k[(size_t)kh * HD + 2 * j];
+                    rk[i][1] = rp.k[(size_t)kh * HD + 2 * j + 1];
+                }
+                if (pblk && side1 == 1) {
+                    rv[i][0] = rp.v[(size_t)kh * HD + 2 * j];
+                    rv[i][1] = rp.v[(size_t)kh * HD + 2 * j + 1];
+                }
+            }
+        }
+    }
     // this thread's row scale, then the tile: segment f = i * 64 + lane is
     // row f / NSEG, bytes 16 (f % NSEG) .. +15
     float sc = 1.f;
@@ -798,35 +835,31 @@ __global__ __launch_bounds__(64 * GRP) void attn_scores_grp(float* __restrict__ 
             if (f < 64 * NSEG) *(uint4*)(kt + r * RS + 16 * sg) = v[i];
         }
     }
-    const int pcur = T - 1;
     bool own = false;
     if constexpr (ROPE) {
         const int half = HD / 2;
-        const float* tb = rp.table + (size_t)pcur * half * 2;
-        {
-            const float* qh = q + (size_t)(kh * GRP + wave) * HD;
-            for (int j = lane; j < half; j += 64) {
-                const float x0 = qh[2 * j], x1 = qh[2 * j + 1];
-                const float c = tb[2 * j], sn = tb[2 * j + 1];
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int j = lane + 64 * i;
+            if (j < half) {
+                const float x0 = rq[i][0], x1 = rq[i][1], c = rt[i][0], sn = rt[i][1];
                 qs[wave][2 * j] = fmaf(x0, c, -(x1 * sn));
                 qs[wave][2 * j + 1] = fmaf(x0, sn, x1 * c);
             }
         }
-        if ((int)blockIdx.y == pcur / 64 && wave == 0) {
+        if (pblk) {
             float a[2][2], b[2][2];                        // [side][pair i]: side 0 k (rotated), 1 v
 #pragma unroll
             for (int i = 0; i < 2; i++) {
                 const int j = lane + 64 * i;
                 const bool on = j < half;
-                const float k0 = on ? rp.k[(size_t)kh * HD + 2 * j] : 0.f, k1 = on ? rp.k[(size_t)kh * HD + 2 * j + 1] : 0.f;
-                const float c = on ? tb[2 * j] : 0.f, sn = on ? tb[2 * j + 1] : 0.f;
+                const float k0 = rk[i][0], k1 = rk[i][1], c = rt[i][0], sn = rt[i][1];
                 a[0][i] = on ? fmaf(k0, c, -(k1 * sn)) : 0.f;
                 b[0][i] = on ? fmaf(k0, sn, k1 * c) : 0.f;
-                a[1][i] = on ? rp.v[(size_t)kh * HD + 2 * j] : 0.f;
-                b[1][i] = on ? rp.v[(size_t)kh * HD + 2 * j + 1] : 0.f;
+                a[1][i] = on ? rv[i][0] : 0.f;
+                b[1][i] = on ? rv[i][1] : 0.f;
             }
-#pragma unroll
-            for (int side = 0; side < 2; side++) {
+            for (int side = side0; side <= side1; side++) {
                 uint8_t* dst = side ? rp.vd : rp.kd;
                 if constexpr (BITS >= 16) {
                     float* row = (float*)dst + (size_t)pcur * kv_dim + (size_t)kh * HD;
@@ -841,7 +874,7 @@ __global__ __launch_bounds__(64 * GRP) void attn_scores_grp(float* __restrict__ 
                     }
                 } else {
                     float mx = fmaxf(fmaxf(fabsf(a[side][0]), fabsf(b[side][0])), fmaxf(fabsf(a[side][1]), fabsf(b[side][1])));
-                    mx = wave_max(mx);
+                    mx = wave_max_dpp(mx);
                     float s2 = mx / (BITS == 8 ? 127.0f : 7.0f);
                     if (s2 < 1e-8f) s2 = 1e-8f;
                     const float inv = 1.0f / s2;
@@ -868,7 +901,7 @@ __global__ __launch_bounds__(64 * GRP) void attn_scores_grp(float* __restrict__ 
                 }
             }
         }
-        own = (int)blockIdx.y == pcur / 64 && t == pcur;
+        own = ty == pcur / 64 && t == pcur;
     } else {
         for (int d = lane; d < HD; d += 64) qs[wave][d] = q[(size_t)(kh * GRP + wave) * HD + d];
     }
