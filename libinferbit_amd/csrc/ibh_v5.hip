@@ -526,16 +526,40 @@ __global__ __launch_bounds__(kAttnThreads) void v5_attn_kernel(
     if (!last) return;
     const float* pk = part + (size_t)kvh * NS * GRP * (HD + 2);
     auto ld = [](const float* a) { return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+    constexpr int kMB = 8;                                 // splits merged from registers
     for (int e = tid; e < GRP * HD; e += kAttnThreads) {
         const int g = e / HD, d = e - g * HD;
-        float M = -INFINITY;
-        for (int s2 = 0; s2 < nact; s2++) M = fmaxf(M, ld(pk + ((size_t)s2 * GRP + g) * (HD + 2)));
-        float L = 0.f, A = 0.f;
-        for (int s2 = 0; s2 < nact; s2++) {
-            const float* ps = pk + ((size_t)s2 * GRP + g) * (HD + 2);
-            const float w = __expf(ld(ps) - M);
-            L = fmaf(ld(ps + 1), w, L);
-            A = fmaf(ld(ps + 2 + d), w, A);
+        float M = -INFINITY, L = 0.f, A = 0.f;
+        if (nact <= kMB) {
+            // every split's (m, l, o[d]) loaded at once (each load is a
+            // round trip to the memory side), then combined in split order
+            float mv[kMB], lv[kMB], av[kMB];
+#pragma unroll
+            for (int s2 = 0; s2 < kMB; s2++) {
+                const float* ps = pk + ((size_t)min(s2, nact - 1) * GRP + g) * (HD + 2);
+                mv[s2] = ld(ps);
+                lv[s2] = ld(ps + 1);
+                av[s2] = ld(ps + 2 + d);
+            }
+#pragma unroll
+            for (int s2 = 0; s2 < kMB; s2++)
+                if (s2 < nact) M = fmaxf(M, mv[s2]);
+#pragma unroll
+            for (int s2 = 0; s2 < kMB; s2++) {
+                if (s2 < nact) {
+                    const float w = __expf(mv[s2] - M);
+                    L = fmaf(lv[s2], w, L);
+                    A = fmaf(av[s2], w, A);
+                }
+            }
+        } else {
+            for (int s2 = 0; s2 < nact; s2++) M = fmaxf(M, ld(pk + ((size_t)s2 * GRP + g) * (HD + 2)));
+            for (int s2 = 0; s2 < nact; s2++) {
+                const float* ps = pk + ((size_t)s2 * GRP + g) * (HD + 2);
+                const float w = __expf(ld(ps) - M);
+                L = fmaf(ld(ps + 1), w, L);
+                A = fmaf(ld(ps + 2 + d), w, A);
+            }
         }
         out[(size_t)(kvh * GRP + g) * HD + d] = A / L;
     }
