@@ -1086,8 +1086,13 @@ int ibh_launch_rows_x(float* out, const void* w, const void* scales, int kind, c
 // outlier sidecar reads (xk[j] = xo[j] * ia[j], or xo[j] when ia is NULL).
 // up: x is the MLP gate and xk = silu(x) * up (xo = x then; no AWQ).
 // Returns 1 if launched, 0 if not eligible (the caller runs its own path).
+int ibh_launch_tile_grp_multi(const IbhGrpMat* m, int n, int mode, const float* x, const float* x2, int N, int G,
+                              const IbhGrpNorm* nrm, hipStream_t st);
+
 int ibh_launch_rows_grp_multi(const IbhGrpMat* m, int n, const float* x, bool awq, const float* xo, int N, int G,
                               hipStream_t st, const float* up, const IbhGrpNorm* nrm) {
+    // shapes the quad-layout kernel takes (outliers reading xk itself) go there
+    if (xo == x && ibh_launch_tile_grp_multi(m, n, nrm ? 3 : up ? 2 : awq ? 1 : 0, x, up, N, G, nrm, st)) return 1;
     // up != null: x is the MLP gate, xk = silu(x) * up (no inv_act then);
     // nrm != null: residual add + rmsnorm in front (each matrix's ia = its
     // norm weight, times its AWQ vector)

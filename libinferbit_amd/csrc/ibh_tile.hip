@@ -157,7 +157,8 @@ __device__ __forceinline__ void lds_wait(int* c, int n, int* bad) {
 // x digits: Q = trunc(x * 2^14 / s) (|Q| < 2^21), d0 = Q >> 14 (signed),
 // d1 = (Q >> 7) & 127, d2 = Q & 127, so Q = 2^14 d0 + 2^7 d1 + d2 and
 // |x/s - Q/2^14| < 1.2 * 2^-14.  The bias term needs only sum(Q).
-template <int BITS>
+// RNE: Q = rint(x * 2^14 / s) instead of trunc (unbiased, half the error).
+template <int BITS, bool RNE = false>
 __device__ __forceinline__ void digit_chunk(unsigned char* smem, const float* xraw, int k, int lane, int N,
                                             float kq, int* qpart) {
     constexpr int NA = TGeo<BITS>::NA;
@@ -179,7 +180,7 @@ __device__ __forceinline__ void digit_chunk(unsigned char* smem, const float* xr
         for (int e = 0; e < RUN; e++) {
             const float4 f = xv[e >> 2];
             const float xe = (e & 3) == 0 ? f.x : (e & 3) == 1 ? f.y : (e & 3) == 2 ? f.z : f.w;
-            const int q = (int)(xe * kq);
+            const int q = RNE ? (int)__builtin_rintf(xe * kq) : (int)(xe * kq);
             b0[e] = (uint32_t)(q >> 14);
             b1[e] = ((uint32_t)q >> 7) & 127u;
             b2[e] = (uint32_t)q & 127u;
@@ -210,14 +211,14 @@ __device__ __forceinline__ void digit_chunk(unsigned char* smem, const float* xr
 // a claim is (old >> 6) and a finished chunk counts 64 in *done (release:
 // its LDS writes are visible to whoever sees the count).  No branch in the
 // loop depends on the lane; it runs at most nchunks + 1 times.
-template <int BITS>
+template <int BITS, bool RNE = false>
 __device__ __forceinline__ void digit_work(unsigned char* smem, const float* xraw, int* next, int* done, int nchunks,
                                            int lane, int N, float kq, int* qpart) {
     for (int it = 0; it <= nchunks; it++) {
         const int got = __hip_atomic_fetch_add(next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         const int k = __builtin_amdgcn_readfirstlane(got) >> 6;
         if (k >= nchunks) break;
-        digit_chunk<BITS>(smem, xraw, k, lane, N, kq, qpart);
+        digit_chunk<BITS, RNE>(smem, xraw, k, lane, N, kq, qpart);
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __hip_atomic_fetch_add(done, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -450,6 +451,295 @@ __global__ __launch_bounds__(1024) void gemv_tile_x(const RowSet rs, const float
     }
 }
 
+// ── group-scaled INT4 rows (IBF v5 __i4_q / __i4_s) on the quad layout ───
+// y[m] = sum_g fp16(s[m][g]) * sum_{j in g} (nibble - 8) * xk[j]
+//        + sum_k fp16(outl_val[m][k]) * xk[outl_idx[m][k]]
+// (int4_matmul_rows_skip, src/pq_decode.c:3565-3644).  Same block as
+// gemv_tile_x: activation wavefronts form xk (x, x * inv_act, silu(gate) * up
+// or the residual add + rmsnorm), stage it in LDS and post max|xk|; every
+// wavefront then writes digit chunks; weight wavefronts stream their quad's
+// 256-byte steps.  The digits round to nearest, Q = rint(xk * 2^14 / s): a
+// truncated Q is biased toward zero, and through a model's layers that bias
+// (up to 2^-14 s per element, the same sign as xk) adds up where rows align
+// with xk.  With G % 128 == 0, chunk c of a step (128 columns) lies in
+// one scale group, so the contraction starts a fresh int32 accumulator per
+// step and its diagonal lane 20c + p folds it into an fp32 per-plane sum
+// with that group's scale: F_p[i] += s[i][g(step, c)] * A_p(step, c, i).
+// A step's block sum is below 2^24 (128 x 128 x 127), so the conversion is
+// exact.  The wavefront's scales are staged in LDS as [group][row] halves
+// (one 8-byte read per step).  Outliers read xk from the LDS copy.
+struct GrpTileSet {
+    const uint8_t* W[3];
+    const uint16_t* sg[3];
+    const float* ia[3];
+    const uint16_t* oi[3];
+    const uint16_t* ov[3];
+    float* y[3];
+    int M[3];
+    int K_out[3];
+    int b1, b2;
+};
+
+// silu(g) = g / (1 + e^-g) (ib_silu_gate_f32, pq_decode.c:4610-4616; the
+// hardware exp, as the row kernel of the same path)
+__device__ __forceinline__ float grp_silu(float g) { return g / (1.0f + __expf(-g)); }
+
+constexpr int kGrpScaleHalves = 256;   // per weight wavefront: 64 groups x 4 rows
+
+// MODE 0: xk = x; 1: xk = x * ia (AWQ); 2: xk = silu(x) * x2 (the MLP's gate
+// and up); 3: xin = x + dl (dl may be null; block 0 writes xin to xr when xr
+// is not null), inv = 1 / sqrtf((float)(sum_double xin^2 / N) + eps),
+// xk = (xin * inv) * ia (ia = norm weight, times the AWQ vector if any).
+template <int KS, int MODE>
+__global__ __launch_bounds__(1024) void gemv_tile_grp(const GrpTileSet gs, const float* __restrict__ x,
+                                                      const float* __restrict__ x2, int N, int G, int S, int WQ,
+                                                      int KW, int NXW, int delay, const float* __restrict__ dl,
+                                                      float* __restrict__ xr, float eps) {
+    constexpr int NA = 2;                   // int4: two operands per 16-byte segment
+    constexpr int XF = MODE == 3 ? 4 : 8;   // float4 of x per activation lane
+    const int seg = (int)blockIdx.x >= gs.b2 ? 2 : (int)blockIdx.x >= gs.b1 ? 1 : 0;
+    const int bid = (int)blockIdx.x - (seg == 2 ? gs.b2 : seg == 1 ? gs.b1 : 0);
+    const float* __restrict__ ia = gs.ia[seg];
+    extern __shared__ __align__(16) unsigned char smem[];
+    float* xraw = (float*)(smem + (size_t)S * NA * 1024);
+    uint16_t* scl = (uint16_t*)(xraw + N);
+    __shared__ float red[kTileMaxWaves];
+    __shared__ double red_ss[kTileMaxWaves];
+    __shared__ int cnt[4];
+    __shared__ int bad;
+    __shared__ float part[kTileMaxWaves][4][3];
+    __shared__ __align__(16) float epi[kTileMaxWaves][48];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int nchunks = (N + 64 * 4 * NA - 1) / (64 * 4 * NA);
+    if (threadIdx.x < 4) cnt[threadIdx.x] = 0;
+    if (threadIdx.x == 0) bad = 0;
+    __syncthreads();
+
+    if (wave < NXW) {
+        // ── activation wavefront: every load issued before any is used
+        // (unconditional: an absent operand reads x again)
+        float4 xv[XF], av[MODE != 0 ? XF : 1], dv[MODE == 3 ? XF : 1];
+        const float4* asrc = (const float4*)(MODE == 2 ? x2 : MODE != 0 ? ia : x);
+        const float4* dsrc = (const float4*)(dl ? dl : x);
+#pragma unroll
+        for (int u = 0; u < XF; u++) {
+            const int c4 = lane + 64 * (wave + NXW * u);
+            const int cc = 4 * c4 < N ? c4 : 0;
+            xv[u] = ((const float4*)x)[cc];
+            if constexpr (MODE != 0) av[u] = asrc[cc];
+            if constexpr (MODE == 3) dv[u] = dsrc[cc];
+        }
+#pragma unroll
+        for (int u = 0; u < XF; u++) {
+            const int c4 = lane + 64 * (wave + NXW * u);
+            if constexpr (MODE == 1) {
+                xv[u].x *= av[u].x; xv[u].y *= av[u].y; xv[u].z *= av[u].z; xv[u].w *= av[u].w;
+            }
+            if constexpr (MODE == 2) {
+                xv[u].x = grp_silu(xv[u].x) * av[u].x; xv[u].y = grp_silu(xv[u].y) * av[u].y;
+                xv[u].z = grp_silu(xv[u].z) * av[u].z; xv[u].w = grp_silu(xv[u].w) * av[u].w;
+            }
+            if constexpr (MODE == 3) {
+                if (dl) {
+                    xv[u].x += dv[u].x; xv[u].y += dv[u].y; xv[u].z += dv[u].z; xv[u].w += dv[u].w;
+                }
+                if (xr && blockIdx.x == 0 && 4 * c4 < N) ((float4*)xr)[c4] = xv[u];
+            }
+            if (4 * c4 >= N) xv[u] = float4{0.f, 0.f, 0.f, 0.f};
+        }
+        if constexpr (MODE == 3) {
+            double ss = 0.0;
+#pragma unroll
+            for (int u = 0; u < XF; u++)
+                ss += ((double)xv[u].x * (double)xv[u].x + (double)xv[u].y * (double)xv[u].y) +
+                      ((double)xv[u].z * (double)xv[u].z + (double)xv[u].w * (double)xv[u].w);
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+            if (lane == 0) {
+                red_ss[wave] = ss;
+                lds_signal(&cnt[3]);
+            }
+            lds_wait(&cnt[3], NXW, &bad);
+            double tot = 0.0;
+            for (int w = 0; w < NXW; w++) tot += red_ss[w];
+            const float ninv = 1.0f / sqrtf((float)(tot / (double)N) + eps);
+#pragma unroll
+            for (int u = 0; u < XF; u++) {
+                xv[u].x = (xv[u].x * ninv) * av[u].x; xv[u].y = (xv[u].y * ninv) * av[u].y;
+                xv[u].z = (xv[u].z * ninv) * av[u].z; xv[u].w = (xv[u].w * ninv) * av[u].w;
+            }
+        }
+        float mx = 0.f;
+#pragma unroll
+        for (int u = 0; u < XF; u++) {
+            const int c4 = lane + 64 * (wave + NXW * u);
+            if (4 * c4 < N) ((float4*)xraw)[c4] = xv[u];
+            mx = fmaxf(fmaxf(mx, fmaxf(fabsf(xv[u].x), fabsf(xv[u].y))), fmaxf(fabsf(xv[u].z), fabsf(xv[u].w)));
+        }
+        mx = wave_max_dpp(mx);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        if (lane == 0) {
+            red[wave] = mx;
+            lds_signal(&cnt[0]);
+        }
+        lds_wait(&cnt[0], NXW, &bad);
+        float gm = 0.f;
+        for (int w = 0; w < NXW; w++) gm = fmaxf(gm, red[w]);
+        const float xs = gm > 0.f ? gm / 127.0f : 1.0f;
+        digit_work<4, true>(smem, xraw, &cnt[2], &cnt[1], nchunks, lane, N, (1.0f / xs) * 16384.0f, nullptr);
+        if (KW > 1) __syncthreads();   // pairs with the weight waves' K-range barrier
+        return;
+    }
+
+    // ── weight wavefront: 4 rows (a quad) x KS 256-byte steps
+    const uint8_t* __restrict__ W = gs.W[seg];
+    const uint16_t* __restrict__ sg = gs.sg[seg];
+    const uint16_t* __restrict__ oi = gs.oi[seg];
+    const uint16_t* __restrict__ ov = gs.ov[seg];
+    float* __restrict__ y = gs.y[seg];
+    const int M = gs.M[seg], K_out = gs.K_out[seg];
+    const int ww = wave - NXW;
+    const int wq = ww / KW, wk = ww - wq * KW;
+    const int row0 = bid * 4 * WQ + 4 * wq;
+    const size_t rb = (size_t)N / 2;
+    const int m = lane & 15, kg = lane >> 4;
+    const int ng = N / G;
+    const int s0 = wk * KS;
+    const int g0 = s0 * 512 / G;                        // the K-range's first group
+    const int ngw = ((s0 + KS) * 512 - 1) / G - g0 + 1;   // groups it touches (<= 4 KS)
+    // 1. the group scales of the quad's K-range (lane: row lane >> 4, groups
+    // (lane & 15) + 16 t) and the outlier sidecar, unconditional clamped loads
+    // consumed only after the weight loads are issued
+    constexpr int NT = (4 * KS + 15) / 16;
+    uint32_t scb[NT];
+    {
+        const uint16_t* sr = sg + (size_t)min(row0 + (lane >> 4), M - 1) * ng;
+#pragma unroll
+        for (int t = 0; t < NT; t++) scb[t] = sr[min(g0 + (lane & 15) + 16 * t, ng - 1)];
+    }
+    const bool osc = wk == 0 && K_out > 0 && 4 * K_out <= 128;
+    int ojx[2] = {0, 0}, orr[2] = {-1, -1};
+    uint32_t ovh[2] = {0u, 0u};
+    if (osc) {
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int idx = min(lane + 64 * u, 4 * K_out - 1);
+            const int r = idx / K_out;
+            const size_t e = (size_t)min(row0 + r, M - 1) * K_out + (idx - r * K_out);
+            ojx[u] = oi[e];
+            ovh[u] = ov[e];
+            orr[u] = lane + 64 * u < 4 * K_out ? r : -1;
+        }
+    }
+    for (int i = 0; i < delay; i++) __builtin_amdgcn_s_sleep(4);
+    // 2. weights
+    uint4 wv[KS];
+    {
+        const uint8_t* base = W + (size_t)min(row0 + (m & 3), M - 1) * rb + (size_t)s0 * 256 + 64 * (m >> 2) + 16 * kg;
+#pragma unroll
+        for (int j = 0; j < KS; j++) wv[j] = ld_stream16(base + j * 256);
+    }
+    __builtin_amdgcn_sched_barrier(0);   // every load is issued before the waits below
+    // 3. scales -> LDS [group][row] halves
+    uint16_t* sl = scl + ww * kGrpScaleHalves;
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        const int gl = (lane & 15) + 16 * t;
+        if (gl < ngw) sl[gl * 4 + (lane >> 4)] = (uint16_t)scb[t];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");   // the scale writes stay ahead of their reads
+    __builtin_amdgcn_wave_barrier();
+    lds_wait(&cnt[0], NXW, &bad);
+    float gm = 0.f;
+    for (int w = 0; w < NXW; w++) gm = fmaxf(gm, red[w]);
+    const float xs = gm > 0.f ? gm / 127.0f : 1.0f;
+    digit_work<4, true>(smem, xraw, &cnt[2], &cnt[1], nchunks, lane, N, (1.0f / xs) * 16384.0f, nullptr);
+    lds_wait(&cnt[1], 64 * nchunks, &bad);   // acquire: also orders this wave's scale writes
+
+    // 4. contract: per step a fresh exact int32 block sum, folded with its
+    // group scale into fp32 per-plane sums
+    const i4_t zero4 = {0, 0, 0, 0};
+    float F[4] = {0.f, 0.f, 0.f, 0.f};
+    const unsigned char* bb = smem + b_off<4>(s0, 0, m, kg);
+#pragma unroll
+    for (int j = 0; j < KS; j++) {
+        const i4_t b0 = *(const i4_t*)(bb + (j * NA + 0) * 1024);
+        const i4_t b1 = *(const i4_t*)(bb + (j * NA + 1) * 1024);
+        i4_t a = __builtin_amdgcn_mfma_i32_16x16x64_i8(tile_operand<4, 0>(wv[j]), b0, zero4, 0, 0, 0);
+        a = __builtin_amdgcn_mfma_i32_16x16x64_i8(tile_operand<4, 1>(wv[j]), b1, a, 0, 0, 0);
+        const int gl = ((s0 + j) * 512 + 128 * kg) / G - g0;   // chunk kg's group
+        const uint2 sv = *(const uint2*)(sl + 4 * gl);
+        F[0] = fmaf((float)a[0], f16_to_f32((uint16_t)(sv.x & 0xffff)), F[0]);
+        F[1] = fmaf((float)a[1], f16_to_f32((uint16_t)(sv.x >> 16)), F[1]);
+        F[2] = fmaf((float)a[2], f16_to_f32((uint16_t)(sv.y & 0xffff)), F[2]);
+        F[3] = fmaf((float)a[3], f16_to_f32((uint16_t)(sv.y >> 16)), F[3]);
+    }
+
+    // 5. chunk sums through LDS: lane 20c + p (register i) holds row i, plane
+    // p, chunk c; lane i < 4 sums row i's four chunks per plane
+    float* ep = epi[wave];
+    const int pl = m & 3;
+    if ((m >> 2) == kg && pl < 3) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) ep[(i * 3 + pl) * 4 + kg] = F[i];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float f0 = 0.f, f1 = 0.f, f2 = 0.f;
+    if (lane < 4) {
+        const float4 q0 = *(const float4*)(ep + (lane * 3 + 0) * 4);
+        const float4 q1 = *(const float4*)(ep + (lane * 3 + 1) * 4);
+        const float4 q2 = *(const float4*)(ep + (lane * 3 + 2) * 4);
+        f0 = (q0.x + q0.y) + (q0.z + q0.w);
+        f1 = (q1.x + q1.y) + (q1.z + q1.w);
+        f2 = (q2.x + q2.y) + (q2.z + q2.w);
+    }
+    if (KW > 1) {
+        if (lane < 4) {
+            part[wave][lane][0] = f0;
+            part[wave][lane][1] = f1;
+            part[wave][lane][2] = f2;
+        }
+        __syncthreads();
+        if (wk != 0) return;
+        if (lane < 4) {
+            for (int k = 1; k < KW; k++) {
+                f0 += part[wave + k][lane][0];
+                f1 += part[wave + k][lane][1];
+                f2 += part[wave + k][lane][2];
+            }
+        }
+    }
+    // 6. outliers: sum_k val_k * xk[idx_k] per row, xk from the LDS copy
+    float osum[4] = {0.f, 0.f, 0.f, 0.f};
+    if (osc) {
+        float op[2];
+#pragma unroll
+        for (int u = 0; u < 2; u++) op[u] = orr[u] >= 0 ? f16_to_f32((uint16_t)ovh[u]) * xraw[ojx[u]] : 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; r++) osum[r] = wave_sum((orr[0] == r ? op[0] : 0.f) + (orr[1] == r ? op[1] : 0.f));
+    }
+    if (lane < 4 && row0 + lane < M) {
+        float o = osum[0];
+#pragma unroll
+        for (int r = 1; r < 4; r++) o = lane == r ? osum[r] : o;
+        if (K_out > 0 && 4 * K_out > 128) {
+            o = 0.f;
+            for (int k = 0; k < K_out; k++) {
+                const size_t e = (size_t)(row0 + lane) * K_out + k;
+                o = fmaf(f16_to_f32(ov[e]), xraw[oi[e]], o);
+            }
+        }
+        const float v = (f0 + f1 * (1.f / 128.f)) + f2 * (1.f / 16384.f);
+        float yv = v * (xs * (1.f / 16.f)) + o;
+        if (__hip_atomic_load(&bad, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) yv = __builtin_nanf("");
+        y[row0 + lane] = yv;
+    }
+}
+
 // Geometry override (0 = automatic); set by ibh_set_tile_config.
 int g_tile_mode = 0, g_tile_KS = 0, g_tile_WR = 0, g_tile_delay = -1;
 
@@ -561,5 +851,96 @@ int ibh_launch_tile_x_multi(const MatDesc* d, int n, int kind, const float* x, i
 #undef IBH_TX
 #undef IBH_TXC
 #undef IBH_TXB
+    return 1;
+}
+
+// Group-scaled INT4 matrices (IBF v5 __i4_q / __i4_s), one to three sharing
+// x, N and G, on the quad layout.  mode: 0 xk = x; 1 xk = x * inv_act (each
+// matrix's ia); 2 xk = silu(x) * x2; 3 residual add + rmsnorm in front (nrm,
+// each matrix's ia = its norm weight times its AWQ vector).  Outliers read
+// xk itself.  Returns 1 if launched, 0 if the shape is not eligible (nothing
+// launched; the caller runs the row kernel).
+int ibh_launch_tile_grp_multi(const IbhGrpMat* m, int n, int mode, const float* x, const float* x2, int N, int G,
+                              const IbhGrpNorm* nrm, hipStream_t st) {
+    if (g_tile_mode < 0 || n < 1 || n > 3 || mode < 0 || mode > 3) return 0;
+    if (N <= 0 || N % 512 || G <= 0 || G % 128 || N % G || ((uintptr_t)x & 15)) return 0;
+    if (mode == 2 && (!x2 || ((uintptr_t)x2 & 15))) return 0;
+    if (mode == 3 && (!nrm || ((uintptr_t)nrm->dl & 15) || ((uintptr_t)nrm->xr & 15))) return 0;
+    const bool need_ia = mode == 1 || mode == 3;
+    int quads = 0;
+    for (int i = 0; i < n; i++) {
+        if (((uintptr_t)m[i].q & 15) || m[i].M <= 0 || !m[i].s) return 0;
+        if (need_ia != (m[i].ia != nullptr) || ((uintptr_t)m[i].ia & 15)) return 0;
+        if (m[i].K_out < 0 || (m[i].K_out > 0 && (!m[i].oi || !m[i].ov))) return 0;
+        quads += (m[i].M + 3) / 4;
+    }
+    const int S = N / 512;
+    const int xf = mode == 3 ? 4 : 8;
+    const int nxw = (N + 256 * xf - 1) / (256 * xf);
+    if (nxw > 8 || S > kTileMaxChunks) return 0;
+    int KS = 0;
+    // (one step per wavefront, e.g. 11 K-ranges of a 5632-column row, leaves
+    // blocks of 4 rows; the row kernel is faster there)
+    for (int c : {16, 14, 8, 7, 4, 2})
+        if (S % c == 0 && S / c + nxw <= kTileMaxWaves) { KS = c; break; }
+    if (g_tile_mode > 0 && g_tile_KS) KS = g_tile_KS;
+    if (KS == 0 || S % KS != 0) return 0;
+    const int KW = S / KS;
+    const int wq_max = (kTileMaxWaves - nxw) / KW;
+    if (wq_max < 1) return 0;
+    auto nblocks = [&](int wq) {
+        int b = 0;
+        for (int i = 0; i < n; i++) b += (m[i].M + 4 * wq - 1) / (4 * wq);
+        return b;
+    };
+    // the tile kernel's choice: about one block per CU, then the WQ with the
+    // least rows per CU over rounds of 256 blocks
+    const int wq0 = std::min(wq_max, std::max(1, (quads + 255) / 256));
+    int WQ = wq0;
+    long best = -1;
+    for (int wq = wq_max; wq >= std::max(1, wq0 / 2 + 1); wq--) {
+        const long cost = (long)((nblocks(wq) + 255) / 256) * wq;
+        if (best < 0 || cost < best) { best = cost; WQ = wq; }
+    }
+    if (g_tile_mode > 0 && g_tile_WR) WQ = std::min(g_tile_WR, wq_max);
+    const int nthreads = 64 * (nxw + WQ * KW);
+    int delay = quads * 4 >= 2 * N ? 1 : 3;
+    if (g_tile_mode > 0 && g_tile_delay >= 0) delay = g_tile_delay;
+    const size_t lds = (size_t)S * 2 * 1024 + 4 * (size_t)N + 2 * (size_t)kGrpScaleHalves * WQ * KW;
+    if (lds > 150 * 1024) return 0;
+    GrpTileSet gs{};
+    int b = 0;
+    for (int i = 0; i < 3; i++) {
+        const IbhGrpMat& g = m[i < n ? i : 0];
+        gs.W[i] = g.q;
+        gs.sg[i] = g.s;
+        gs.ia[i] = g.ia;
+        gs.oi[i] = g.oi;
+        gs.ov[i] = g.ov;
+        gs.y[i] = g.out;
+        gs.M[i] = g.M;
+        gs.K_out[i] = g.K_out;
+    }
+    b += (m[0].M + 4 * WQ - 1) / (4 * WQ);
+    gs.b1 = n > 1 ? b : 0x7fffffff;
+    if (n > 1) b += (m[1].M + 4 * WQ - 1) / (4 * WQ);
+    gs.b2 = n > 2 ? b : 0x7fffffff;
+    const int blocks = nblocks(WQ);
+    const float* dl = nrm ? nrm->dl : nullptr;
+    float* xr = nrm ? nrm->xr : nullptr;
+    const float eps = nrm ? nrm->eps : 0.f;
+#define IBH_TG(KS_, M_) gemv_tile_grp<KS_, M_><<<blocks, nthreads, lds, st>>>(gs, x, x2, N, G, S, WQ, KW, nxw, delay, dl, xr, eps)
+#define IBH_TGK(M_) do { switch (KS) { case 2: IBH_TG(2, M_); break; \
+                                       case 4: IBH_TG(4, M_); break; case 7: IBH_TG(7, M_); break; \
+                                       case 8: IBH_TG(8, M_); break; case 14: IBH_TG(14, M_); break; \
+                                       default: IBH_TG(16, M_); break; } } while (0)
+    switch (mode) {
+    case 0: IBH_TGK(0); break;
+    case 1: IBH_TGK(1); break;
+    case 2: IBH_TGK(2); break;
+    default: IBH_TGK(3); break;
+    }
+#undef IBH_TG
+#undef IBH_TGK
     return 1;
 }

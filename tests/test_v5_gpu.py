@@ -108,6 +108,37 @@ def test_forward_step_and_greedy(L, tmp_path_factory, tmp_path, name):
     assert gg == rg, (name, gg, rg)
 
 
+# Rows of whole 256-byte steps: every INT4 launch of this shape runs the
+# quad-layout group kernel (q/k/v and gate/up with the residual add and
+# rmsnorm in front, down with silu * up formed in its prologue).
+WIDE = dict(CFG, hidden_size=1024, num_heads=8, num_kv_heads=2, head_dim=128, intermediate_size=2048)
+
+
+@pytest.mark.parametrize("name", ["int4", "int4_awq_outl", "int4_awq_outl40", "fused"])
+def test_quad_layout_group_kernel(L, tmp_path_factory, tmp_path, name):
+    """AWQ, outliers through the per-wavefront sidecar (3 per row) and the
+    per-row loop (40 per row), and the fused q/k/v + gate/up tensors, on the
+    quad-layout group kernel: logits within TOL of the reference's and the
+    same tokens; with that kernel switched off (the row kernel runs) the
+    same holds."""
+    from libinferbit_amd import _lib
+    from libinferbit_amd.session import PqSession
+    path = model(tmp_path_factory, f"wide_{name}", cfg=WIDE, **CASES[name])
+    print(f"case v5 wide {name}", flush=True)
+    rt, rl = ref_run(path, PROMPT, 6, "steps", tmp_path)
+    for mode in (0, -1):
+        assert _lib.lib().ibh_set_tile_config(mode, 0, 0, -1) == 0
+        try:
+            S = PqSession(path)
+            gt, gl = gpu_steps(S, PROMPT, 6)
+        finally:
+            _lib.lib().ibh_set_tile_config(0, 0, 0, -1)
+        errs = [relerr(gl[i], rl[i]) for i in range(len(PROMPT))]
+        print(f"v5 wide {name} tile_mode={mode}: max rel logit err {max(errs):.3g}", flush=True)
+        assert max(errs) <= TOL, (name, mode, errs)
+        assert gt == rt, (name, mode, gt, rt)
+
+
 POLICIES = {
     "l1_only": (1, 0.0, 0.0),
     "l2skip": (2, 0.5, 0.0),
