@@ -466,8 +466,9 @@ __global__ __launch_bounds__(1024) void gemv_tile_x(const RowSet rs, const float
 // step and its diagonal lane 20c + p folds it into an fp32 per-plane sum
 // with that group's scale: F_p[i] += s[i][g(step, c)] * A_p(step, c, i).
 // A step's block sum is below 2^24 (128 x 128 x 127), so the conversion is
-// exact.  The wavefront's scales are staged in LDS as [group][row] halves
-// (one 8-byte read per step).  Outliers read xk from the LDS copy.
+// exact.  G / 128 is a power of two, 2^gsh; the wavefront's scales are
+// staged in LDS once per (chunk, row), [chunk][row] halves, so a step reads
+// its four rows' scales with one 8-byte read at a fixed offset.  Outliers read xk from the LDS copy.
 struct GrpTileSet {
     const uint8_t* W[3];
     const uint16_t* sg[3];
@@ -484,7 +485,7 @@ struct GrpTileSet {
 // hardware exp, as the row kernel of the same path)
 __device__ __forceinline__ float grp_silu(float g) { return g / (1.0f + __expf(-g)); }
 
-constexpr int kGrpScaleHalves = 256;   // per weight wavefront: 64 groups x 4 rows
+constexpr int kGrpScaleHalves = 256;   // per weight wavefront: 64 chunks x 4 rows
 
 // MODE 0: xk = x; 1: xk = x * ia (AWQ); 2: xk = silu(x) * x2 (the MLP's gate
 // and up); 3: xin = x + dl (dl may be null; block 0 writes xin to xr when xr
@@ -492,7 +493,7 @@ constexpr int kGrpScaleHalves = 256;   // per weight wavefront: 64 groups x 4 ro
 // xk = (xin * inv) * ia (ia = norm weight, times the AWQ vector if any).
 template <int KS, int MODE>
 __global__ __launch_bounds__(1024) void gemv_tile_grp(const GrpTileSet gs, const float* __restrict__ x,
-                                                      const float* __restrict__ x2, int N, int G, int S, int WQ,
+                                                      const float* __restrict__ x2, int N, int gsh, int S, int WQ,
                                                       int KW, int NXW, int delay, const float* __restrict__ dl,
                                                       float* __restrict__ xr, float eps) {
     constexpr int NA = 2;                   // int4: two operands per 16-byte segment
@@ -605,19 +606,18 @@ __global__ __launch_bounds__(1024) void gemv_tile_grp(const GrpTileSet gs, const
     const int row0 = bid * 4 * WQ + 4 * wq;
     const size_t rb = (size_t)N / 2;
     const int m = lane & 15, kg = lane >> 4;
-    const int ng = N / G;
+    const int ng = N >> (7 + gsh);   // groups per row
     const int s0 = wk * KS;
-    const int g0 = s0 * 512 / G;                        // the K-range's first group
-    const int ngw = ((s0 + KS) * 512 - 1) / G - g0 + 1;   // groups it touches (<= 4 KS)
-    // 1. the group scales of the quad's K-range (lane: row lane >> 4, groups
-    // (lane & 15) + 16 t) and the outlier sidecar, unconditional clamped loads
+    const int ch0 = 4 * s0;   // the K-range's first 128-column chunk; its group is chunk >> gsh
+    // 1. the group scales of the quad's K-range (lane: row lane >> 4, the
+    // groups of chunks (lane & 15) + 16 t) and the outlier sidecar, unconditional clamped loads
     // consumed only after the weight loads are issued
     constexpr int NT = (4 * KS + 15) / 16;
     uint32_t scb[NT];
     {
         const uint16_t* sr = sg + (size_t)min(row0 + (lane >> 4), M - 1) * ng;
 #pragma unroll
-        for (int t = 0; t < NT; t++) scb[t] = sr[min(g0 + (lane & 15) + 16 * t, ng - 1)];
+        for (int t = 0; t < NT; t++) scb[t] = sr[min((ch0 + (lane & 15) + 16 * t) >> gsh, ng - 1)];
     }
     const bool osc = wk == 0 && K_out > 0 && 4 * K_out <= 128;
     int ojx[2] = {0, 0}, orr[2] = {-1, -1};
@@ -642,12 +642,12 @@ __global__ __launch_bounds__(1024) void gemv_tile_grp(const GrpTileSet gs, const
         for (int j = 0; j < KS; j++) wv[j] = ld_stream16(base + j * 256);
     }
     __builtin_amdgcn_sched_barrier(0);   // every load is issued before the waits below
-    // 3. scales -> LDS [group][row] halves
+    // 3. scales -> LDS, [chunk][row] halves
     uint16_t* sl = scl + ww * kGrpScaleHalves;
 #pragma unroll
     for (int t = 0; t < NT; t++) {
-        const int gl = (lane & 15) + 16 * t;
-        if (gl < ngw) sl[gl * 4 + (lane >> 4)] = (uint16_t)scb[t];
+        const int ci = (lane & 15) + 16 * t;
+        if (ci < 4 * KS) sl[ci * 4 + (lane >> 4)] = (uint16_t)scb[t];
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");   // the scale writes stay ahead of their reads
     __builtin_amdgcn_wave_barrier();
@@ -669,8 +669,7 @@ __global__ __launch_bounds__(1024) void gemv_tile_grp(const GrpTileSet gs, const
         const i4_t b1 = *(const i4_t*)(bb + (j * NA + 1) * 1024);
         i4_t a = __builtin_amdgcn_mfma_i32_16x16x64_i8(tile_operand<4, 0>(wv[j]), b0, zero4, 0, 0, 0);
         a = __builtin_amdgcn_mfma_i32_16x16x64_i8(tile_operand<4, 1>(wv[j]), b1, a, 0, 0, 0);
-        const int gl = ((s0 + j) * 512 + 128 * kg) / G - g0;   // chunk kg's group
-        const uint2 sv = *(const uint2*)(sl + 4 * gl);
+        const uint2 sv = *(const uint2*)(sl + 4 * (4 * j + kg));   // chunk kg's scales, rows 0..3
         F[0] = fmaf((float)a[0], f16_to_f32((uint16_t)(sv.x & 0xffff)), F[0]);
         F[1] = fmaf((float)a[1], f16_to_f32((uint16_t)(sv.x >> 16)), F[1]);
         F[2] = fmaf((float)a[2], f16_to_f32((uint16_t)(sv.y & 0xffff)), F[2]);
@@ -863,7 +862,9 @@ int ibh_launch_tile_x_multi(const MatDesc* d, int n, int kind, const float* x, i
 int ibh_launch_tile_grp_multi(const IbhGrpMat* m, int n, int mode, const float* x, const float* x2, int N, int G,
                               const IbhGrpNorm* nrm, hipStream_t st) {
     if (g_tile_mode < 0 || n < 1 || n > 3 || mode < 0 || mode > 3) return 0;
-    if (N <= 0 || N % 512 || G <= 0 || G % 128 || N % G || ((uintptr_t)x & 15)) return 0;
+    if (N <= 0 || N % 512 || G <= 0 || G % 128 || N % G || ((G / 128) & (G / 128 - 1)) || ((uintptr_t)x & 15))
+        return 0;
+    const int gsh = __builtin_ctz((unsigned)(G / 128));
     if (mode == 2 && (!x2 || ((uintptr_t)x2 & 15))) return 0;
     if (mode == 3 && (!nrm || ((uintptr_t)nrm->dl & 15) || ((uintptr_t)nrm->xr & 15))) return 0;
     const bool need_ia = mode == 1 || mode == 3;
@@ -929,7 +930,7 @@ int ibh_launch_tile_grp_multi(const IbhGrpMat* m, int n, int mode, const float* 
     const float* dl = nrm ? nrm->dl : nullptr;
     float* xr = nrm ? nrm->xr : nullptr;
     const float eps = nrm ? nrm->eps : 0.f;
-#define IBH_TG(KS_, M_) gemv_tile_grp<KS_, M_><<<blocks, nthreads, lds, st>>>(gs, x, x2, N, G, S, WQ, KW, nxw, delay, dl, xr, eps)
+#define IBH_TG(KS_, M_) gemv_tile_grp<KS_, M_><<<blocks, nthreads, lds, st>>>(gs, x, x2, N, gsh, S, WQ, KW, nxw, delay, dl, xr, eps)
 #define IBH_TGK(M_) do { switch (KS) { case 2: IBH_TG(2, M_); break; \
                                        case 4: IBH_TG(4, M_); break; case 7: IBH_TG(7, M_); break; \
                                        case 8: IBH_TG(8, M_); break; case 14: IBH_TG(14, M_); break; \
