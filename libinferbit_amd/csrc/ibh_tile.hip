@@ -491,7 +491,9 @@ constexpr int kGrpScaleHalves = 256;   // per weight wavefront: 64 chunks x 4 ro
 // and up); 3: xin = x + dl (dl may be null; block 0 writes xin to xr when xr
 // is not null), inv = 1 / sqrtf((float)(sum_double xin^2 / N) + eps),
 // xk = (xin * inv) * ia (ia = norm weight, times the AWQ vector if any).
-template <int KS, int MODE>
+// RAG: S is not a multiple of KS; the last K-range has S % KS steps (its
+// missing steps re-read its last one, unused).
+template <int KS, int MODE, bool RAG>
 __global__ __launch_bounds__(1024) void gemv_tile_grp(const GrpTileSet gs, const float* __restrict__ x,
                                                       const float* __restrict__ x2, int N, int gsh, int S, int WQ,
                                                       int KW, int NXW, int delay, const float* __restrict__ dl,
@@ -635,11 +637,12 @@ __global__ __launch_bounds__(1024) void gemv_tile_grp(const GrpTileSet gs, const
     }
     for (int i = 0; i < delay; i++) __builtin_amdgcn_s_sleep(4);
     // 2. weights
+    const int ns = RAG ? min(KS, S - s0) : KS;   // this K-range's steps
     uint4 wv[KS];
     {
         const uint8_t* base = W + (size_t)min(row0 + (m & 3), M - 1) * rb + (size_t)s0 * 256 + 64 * (m >> 2) + 16 * kg;
 #pragma unroll
-        for (int j = 0; j < KS; j++) wv[j] = ld_stream16(base + j * 256);
+        for (int j = 0; j < KS; j++) wv[j] = ld_stream16(base + (RAG ? min(j, ns - 1) : j) * 256);
     }
     __builtin_amdgcn_sched_barrier(0);   // every load is issued before the waits below
     // 3. scales -> LDS, [chunk][row] halves
@@ -665,6 +668,7 @@ __global__ __launch_bounds__(1024) void gemv_tile_grp(const GrpTileSet gs, const
     const unsigned char* bb = smem + b_off<4>(s0, 0, m, kg);
 #pragma unroll
     for (int j = 0; j < KS; j++) {
+        if (RAG && j >= ns) break;
         const i4_t b0 = *(const i4_t*)(bb + (j * NA + 0) * 1024);
         const i4_t b1 = *(const i4_t*)(bb + (j * NA + 1) * 1024);
         i4_t a = __builtin_amdgcn_mfma_i32_16x16x64_i8(tile_operand<4, 0>(wv[j]), b0, zero4, 0, 0, 0);
@@ -880,13 +884,16 @@ int ibh_launch_tile_grp_multi(const IbhGrpMat* m, int n, int mode, const float* 
     const int nxw = (N + 256 * xf - 1) / (256 * xf);
     if (nxw > 8 || S > kTileMaxChunks) return 0;
     int KS = 0;
-    // (one step per wavefront, e.g. 11 K-ranges of a 5632-column row, leaves
-    // blocks of 4 rows; the row kernel is faster there)
     for (int c : {16, 14, 8, 7, 4, 2})
         if (S % c == 0 && S / c + nxw <= kTileMaxWaves) { KS = c; break; }
+    // no divisor of S: K-ranges of 4 steps, the last one shorter (a
+    // 5632-column row: 4 + 4 + 3)
+    if (KS == 0 && S > 4 && (S + 3) / 4 + nxw <= kTileMaxWaves) KS = 4;
     if (g_tile_mode > 0 && g_tile_KS) KS = g_tile_KS;
-    if (KS == 0 || S % KS != 0) return 0;
-    const int KW = S / KS;
+    if (KS == 0) return 0;
+    const bool rag = S % KS != 0;
+    if (rag && KS != 4 && KS != 8) return 0;
+    const int KW = (S + KS - 1) / KS;
     const int wq_max = (kTileMaxWaves - nxw) / KW;
     if (wq_max < 1) return 0;
     auto nblocks = [&](int wq) {
@@ -933,8 +940,10 @@ int ibh_launch_tile_grp_multi(const IbhGrpMat* m, int n, int mode, const float* 
     const float* dl = nrm ? nrm->dl : nullptr;
     float* xr = nrm ? nrm->xr : nullptr;
     const float eps = nrm ? nrm->eps : 0.f;
-#define IBH_TG(KS_, M_) gemv_tile_grp<KS_, M_><<<blocks, nthreads, lds, st>>>(gs, x, x2, N, gsh, S, WQ, KW, nxw, delay, dl, xr, eps)
-#define IBH_TGK(M_) do { switch (KS) { case 2: IBH_TG(2, M_); break; \
+#define IBH_TG(KS_, M_) gemv_tile_grp<KS_, M_, false><<<blocks, nthreads, lds, st>>>(gs, x, x2, N, gsh, S, WQ, KW, nxw, delay, dl, xr, eps)
+#define IBH_TGR(KS_, M_) gemv_tile_grp<KS_, M_, true><<<blocks, nthreads, lds, st>>>(gs, x, x2, N, gsh, S, WQ, KW, nxw, delay, dl, xr, eps)
+#define IBH_TGK(M_) do { if (rag) { if (KS == 4) IBH_TGR(4, M_); else IBH_TGR(8, M_); break; } \
+                         switch (KS) { case 2: IBH_TG(2, M_); break; \
                                        case 4: IBH_TG(4, M_); break; case 7: IBH_TG(7, M_); break; \
                                        case 8: IBH_TG(8, M_); break; case 14: IBH_TG(14, M_); break; \
                                        default: IBH_TG(16, M_); break; } } while (0)
@@ -945,6 +954,7 @@ int ibh_launch_tile_grp_multi(const IbhGrpMat* m, int n, int mode, const float* 
     default: IBH_TGK(3); break;
     }
 #undef IBH_TG
+#undef IBH_TGR
 #undef IBH_TGK
     return 1;
 }

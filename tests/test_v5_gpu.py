@@ -114,16 +114,18 @@ def test_forward_step_and_greedy(L, tmp_path_factory, tmp_path, name):
 WIDE = dict(CFG, hidden_size=1024, num_heads=8, num_kv_heads=2, head_dim=128, intermediate_size=2048)
 
 
-@pytest.mark.parametrize("name", ["int4", "int4_awq_outl", "int4_awq_outl40", "fused"])
-def test_quad_layout_group_kernel(L, tmp_path_factory, tmp_path, name):
+@pytest.mark.parametrize("name,inter", [("int4", 2048), ("int4_awq_outl", 2048), ("int4_awq_outl40", 2048),
+                                        ("fused", 2048), ("int4_awq_outl", 5632)])
+def test_quad_layout_group_kernel(L, tmp_path_factory, tmp_path, name, inter):
     """AWQ, outliers through the per-wavefront sidecar (3 per row) and the
     per-row loop (40 per row), and the fused q/k/v + gate/up tensors, on the
-    quad-layout group kernel: logits within TOL of the reference's and the
-    same tokens; with that kernel switched off (the row kernel runs) the
-    same holds."""
+    quad-layout group kernel; intermediate 5632 (11 steps of 256 bytes)
+    takes K-ranges of 4 + 4 + 3 steps in the down projection.  Logits within
+    TOL of the reference's and the same tokens; with that kernel switched
+    off (the row kernel runs) the same holds."""
     from libinferbit_amd import _lib
     from libinferbit_amd.session import PqSession
-    path = model(tmp_path_factory, f"wide_{name}", cfg=WIDE, **CASES[name])
+    path = model(tmp_path_factory, f"wide_{name}_{inter}", cfg=dict(WIDE, intermediate_size=inter), **CASES[name])
     print(f"case v5 wide {name}", flush=True)
     rt, rl = ref_run(path, PROMPT, 6, "steps", tmp_path)
     for mode in (0, -1):
