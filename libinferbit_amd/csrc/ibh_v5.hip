@@ -272,9 +272,14 @@ __global__ __launch_bounds__(kAttnThreads) void v5_attn_kernel(
     const float* __restrict__ cs, const int* __restrict__ dpos, int n_kv, int NS, float scale,
     float* __restrict__ part, int* __restrict__ counter) {
     constexpr int HALF = HD / 2, NW = kAttnThreads / 64, DPL = HD / 64, PPW = kAttnPos / NW;
-    constexpr int KPRE = HD / 4;   // the lane's key row held in registers
+    // key rows: each wavefront loads PPW rows coalesced (E4 lanes of 4
+    // elements per row, RPI rows per load instruction) and stages them in
+    // LDS, where lane t of the scores reads row t (rows padded by 4 floats)
+    constexpr int E4 = HD / 4, RPI = 64 / E4, KI = PPW / RPI, KST = HD + 4;
     constexpr int SPAN = kAttnPos * kAttnTiles;
+    static_assert(kAttnTiles == 1, "one tile per split: the key rows are staged once");
     __shared__ __align__(16) float qs[GRP][HD];
+    __shared__ __align__(16) float ksm[kAttnPos * KST];
     __shared__ __align__(16) float kcur[HD], vcur[HD];
     __shared__ float pr[GRP][kAttnPos];
     __shared__ float gmax[GRP], gsum[GRP], galpha[GRP];
@@ -287,17 +292,18 @@ __global__ __launch_bounds__(kAttnThreads) void v5_attn_kernel(
     const int nact = (T + SPAN - 1) / SPAN;
     const int kv_dim = n_kv * HD;
     const size_t hoff = (size_t)kvh * HD;
-    // this lane's key row and this wavefront's value elements of one tile
-    float4 kreg[KPRE];
-    float kst = 1.f;
+    // this wavefront's key rows and value elements of the tile
+    float4 kld[KI];
     float vpre[PPW][DPL];
     auto fetch = [&](int t0) {
-        const int t1 = min(b1, t0 + kAttnPos), t = t0 + lane;
-        const bool ok = t < t1 && t != pos;
-        kst = (KVT == KV_I8 && ok) ? ksc[t] : 1.f;
-        if (ok) {
+        const int t1 = min(b1, t0 + kAttnPos);
 #pragma unroll
-            for (int i = 0; i < KPRE; i++) kreg[i] = kv_ld4<KVT>(kc, (size_t)t * kv_dim + hoff + 4 * i, kst);
+        for (int i = 0; i < KI; i++) {
+            const int tt = t0 + wave * PPW + i * RPI + lane / E4;
+            const bool ok = tt < t1 && tt != pos;
+            const float kst = (KVT == KV_I8 && ok) ? ksc[tt] : 1.f;
+            kld[i] = ok ? kv_ld4<KVT>(kc, (size_t)tt * kv_dim + hoff + 4 * (lane % E4), kst)
+                        : float4{0.f, 0.f, 0.f, 0.f};
         }
 #pragma unroll
         for (int j = 0; j < PPW; j++) {
@@ -399,6 +405,9 @@ __global__ __launch_bounds__(kAttnThreads) void v5_attn_kernel(
             }
         }
     }
+#pragma unroll
+    for (int i = 0; i < KI; i++)
+        *(float4*)(ksm + (wave * PPW + i * RPI + lane / E4) * KST + 4 * (lane % E4)) = kld[i];
     __syncthreads();
     float acc[GRP][DPL];
 #pragma unroll
@@ -408,16 +417,13 @@ __global__ __launch_bounds__(kAttnThreads) void v5_attn_kernel(
     for (int t0 = b0; t0 < b1; t0 += kAttnPos) {
         const int t1 = min(b1, t0 + kAttnPos), np = t1 - t0, t = t0 + lane;
         const bool act = t < t1;
-        // this tile's registers; the next tile's reads go out now
-        float4 kt[KPRE];
+        // this tile's value registers
         float vt[PPW][DPL];
-#pragma unroll
-        for (int i = 0; i < KPRE; i++) kt[i] = kreg[i];
 #pragma unroll
         for (int j = 0; j < PPW; j++)
 #pragma unroll
             for (int jj = 0; jj < DPL; jj++) vt[j][jj] = vpre[j][jj];
-        if (t0 + kAttnPos < b1) fetch(t0 + kAttnPos);
+        const float* krow = ksm + lane * KST;
         // scores: lane = position, wavefront = heads w, w + 4, ...; running
         // max / exp-sum per head kept by its wavefront
         if (wave < GRP) {
@@ -429,7 +435,7 @@ __global__ __launch_bounds__(kAttnThreads) void v5_attn_kernel(
 #pragma unroll
                 for (int d = 0; d < HD; d += 4) {
                     float4 kk;
-                    kk = t == pos ? *(const float4*)(kcur + d) : kt[d / 4];
+                    kk = t == pos ? *(const float4*)(kcur + d) : *(const float4*)(krow + d);
 #pragma unroll
                     for (int h = 0; h < HPW; h++) {
                         const int g = wave + NW * h;
