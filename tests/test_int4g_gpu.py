@@ -49,7 +49,12 @@ def test_int4g_golden(ops, name):
 # rows wide enough that a plain launch needs more waves per row (N = 5632).
 SHAPES = [(14336, 4096, 128, 1, 4), (4096, 14336, 128, 1, 0), (2048, 5632, 128, 1, 2), (5632, 2048, 128, 0, 0),
           (1024, 4096, 256, 1, 3), (512, 20480, 128, 0, 1), (300, 4096, 64, 1, 3), (77, 2048, 32, 0, 0),
-          (64, 24576, 128, 1, 2), (3, 96, 32, 1, 1), (2048, 5632, 128, 0, 0), (256, 5632, 128, 0, 3)]
+          (64, 24576, 128, 1, 2), (3, 96, 32, 1, 1), (2048, 5632, 128, 0, 0), (256, 5632, 128, 0, 3),
+          # the quad-layout kernel with row counts that are not whole quads or
+          # blocks, ragged K-ranges (5632 columns) with G = 256, and the
+          # outlier sidecar at its limit (32 per row) and one past it
+          (1001, 4096, 128, 1, 3), (13, 2048, 128, 0, 2), (333, 5632, 128, 1, 5), (100, 5632, 256, 1, 1),
+          (64, 4096, 128, 1, 32), (64, 4096, 128, 1, 33)]
 
 
 @pytest.mark.parametrize("M,N,G,awq,K", SHAPES)
