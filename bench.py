@@ -402,10 +402,12 @@ def decode_case(name, steps, cpu):
                      "frac_hbm": round(nbytes * tok_s / 1e9 / HBM_PEAK_GBS, 4)}
     if cpu:
         threads = host_cpu()[0]
+        # bounded samples of a few seconds each (TinyLlama ~15 tok/s, Mistral
+        # ~2 tok/s on the box's host threads)
         if name == "tinyllama":
-            out["cpu_baseline"] = cpu_decode(path, case, 8, [threads])
+            out["cpu_baseline"] = cpu_decode(path, case, 48, [threads])
         else:
-            out["cpu_baseline"] = cpu_decode(path, case, 2, [threads])
+            out["cpu_baseline"] = cpu_decode(path, case, 8, [threads])
         try:
             out["dropin"] = dropin_decode(path, case, 32 if name == "tinyllama" else 8)
         except (RuntimeError, subprocess.TimeoutExpired) as e:
