@@ -214,22 +214,26 @@ __global__ void v5_rope_kv_kernel(float* __restrict__ q, const float* __restrict
 // Decode attention of one position with the rope and the cache write fused
 // in (ib_rope_f32 + the fp32 cache write + the per-head loop of
 // forward_step_internal_sc, src/pq_decode.c:4623-4642, 5011-5251).
-// Grid (kv head, split): split sp owns positions [64 sp, 64 sp + 64) of
-// T = pos + 1 (splits past T exit at once).  Each block rotates its GRP
-// query heads into LDS; the block owning pos rotates the new key, writes key
-// and value rows to the cache and uses them from LDS.  Scores: wavefront w
-// takes the heads g = w mod 4, lane = position; softmax pieces per head in
+// Grid (kv head, split): split sp owns positions [256 sp, 256 sp + 256) of
+// T = pos + 1 (splits past T exit at once).  A block is four groups of four
+// wavefronts, group j the tile of 64 positions [256 sp + 64 j, + 64), all in
+// parallel.  Each block rotates its GRP query heads into LDS; the block
+// owning pos rotates the new key, writes key and value rows to the cache and
+// uses them from LDS.  A group's key rows are loaded coalesced (whole rows
+// per load instruction) into LDS.  Scores: wavefront w of a group takes the
+// heads g = w mod 4, lane = position; the tile's max and exp-sum per head in
 // that wavefront.  Value sums: lane = dimension, wavefront w the positions
-// = w mod 4, all heads, then the four wavefronts add up in LDS.  The split's
-// max / exp-sum / value sums go to `part`; the last active block of a kv
-// head to arrive merges the splits (log-sum-exp) into out and re-arms the
-// counter for the next call.  With one active split the block normalises
-// directly.  Exponentials use the hardware exp2 (__expf, a few ulp): the
-// softmax only needs fp32 accuracy here.
-constexpr int kAttnThreads = 256;
-constexpr int kAttnPos = 64;   // positions per tile (one per lane)
-constexpr int kAttnTiles = 1;  // tiles per split, online softmax across them (more
-                               // than one measured slower than split + merge)
+// = w mod 4, all heads.  The block then combines its four tiles by
+// log-sum-exp: with one active split (T <= 256) that is the output;
+// otherwise the split's max / exp-sum / value sums go to `part` and the last
+// active block of a kv head to arrive merges the splits the same way into
+// out and re-arms the counter for the next call.  Exponentials use the
+// hardware exp2 (__expf, a few ulp): the softmax only needs fp32 accuracy
+// here.
+constexpr int kAttnGroups = 4;                      // tiles per block, in parallel
+constexpr int kAttnThreads = 256 * kAttnGroups;
+constexpr int kAttnPos = 64;                        // positions per tile (one per lane)
+constexpr int kAttnSpan = kAttnPos * kAttnGroups;   // positions per split
 
 // Cache storage (ib_pq_kv_cache_create, pq_decode.c:4752-4833): fp32, fp16
 // (IB_PQ_KV_FP16; ib_fp32_to_fp16 rounds to nearest even) or int8
@@ -271,51 +275,48 @@ __global__ __launch_bounds__(kAttnThreads) void v5_attn_kernel(
     void* __restrict__ kc, void* __restrict__ vc, float* __restrict__ ksc, float* __restrict__ vsc,
     const float* __restrict__ cs, const int* __restrict__ dpos, int n_kv, int NS, float scale,
     float* __restrict__ part, int* __restrict__ counter) {
-    constexpr int HALF = HD / 2, NW = kAttnThreads / 64, DPL = HD / 64, PPW = kAttnPos / NW;
-    // key rows: each wavefront loads PPW rows coalesced (E4 lanes of 4
-    // elements per row, RPI rows per load instruction) and stages them in
-    // LDS, where lane t of the scores reads row t (rows padded by 4 floats)
+    constexpr int HALF = HD / 2, NW = kAttnThreads / 64, NWG = 4, DPL = HD / 64, PPW = kAttnPos / NWG;
+    // key rows: each wavefront loads PPW rows of its group's tile coalesced
+    // (E4 lanes of 4 elements per row, RPI rows per load instruction) and
+    // stages them in LDS, where lane t of the scores reads row t (rows padded
+    // by 4 floats); after the scores the same words hold the value sums
     constexpr int E4 = HD / 4, RPI = 64 / E4, KI = PPW / RPI, KST = HD + 4;
-    constexpr int SPAN = kAttnPos * kAttnTiles;
-    static_assert(kAttnTiles == 1, "one tile per split: the key rows are staged once");
+    constexpr int KSZ = kAttnPos * KST, VSZ = NWG * GRP * HD, USZ = KSZ > VSZ ? KSZ : VSZ;
     __shared__ __align__(16) float qs[GRP][HD];
-    __shared__ __align__(16) float ksm[kAttnPos * KST];
     __shared__ __align__(16) float kcur[HD], vcur[HD];
-    __shared__ float pr[GRP][kAttnPos];
-    __shared__ float gmax[GRP], gsum[GRP], galpha[GRP];
-    __shared__ float vred[NW][GRP][HD];
+    __shared__ __align__(16) float uni[kAttnGroups][USZ];
+    __shared__ float pr[kAttnGroups][GRP][kAttnPos];
+    __shared__ float gmx[kAttnGroups][GRP], gsm[kAttnGroups][GRP];
     __shared__ int last;
     const int kvh = blockIdx.x, sp = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tg = wave / NWG, gw = wave % NWG;           // group (tile) and wavefront in it
     const int pos = *dpos, T = pos + 1;
-    const int b0 = sp * SPAN, b1 = min(T, b0 + SPAN);
+    const int b0 = sp * kAttnSpan, b1 = min(T, b0 + kAttnSpan);
     if (b0 >= b1) return;                       // split past T: nothing to do
-    const int nact = (T + SPAN - 1) / SPAN;
+    const int nact = (T + kAttnSpan - 1) / kAttnSpan;
     const int kv_dim = n_kv * HD;
     const size_t hoff = (size_t)kvh * HD;
-    // this wavefront's key rows and value elements of the tile
+    const int t0 = b0 + tg * kAttnPos, t1 = min(b1, t0 + kAttnPos), np = max(0, t1 - t0);
+    float* ksm = uni[tg];
+    // this wavefront's key rows and value elements of the group's tile
     float4 kld[KI];
     float vpre[PPW][DPL];
-    auto fetch = [&](int t0) {
-        const int t1 = min(b1, t0 + kAttnPos);
 #pragma unroll
-        for (int i = 0; i < KI; i++) {
-            const int tt = t0 + wave * PPW + i * RPI + lane / E4;
-            const bool ok = tt < t1 && tt != pos;
-            const float kst = (KVT == KV_I8 && ok) ? ksc[tt] : 1.f;
-            kld[i] = ok ? kv_ld4<KVT>(kc, (size_t)tt * kv_dim + hoff + 4 * (lane % E4), kst)
-                        : float4{0.f, 0.f, 0.f, 0.f};
-        }
+    for (int i = 0; i < KI; i++) {
+        const int tt = t0 + gw * PPW + i * RPI + lane / E4;
+        const bool ok = tt < t1 && tt != pos;
+        const float kst = (KVT == KV_I8 && ok) ? ksc[tt] : 1.f;
+        kld[i] = ok ? kv_ld4<KVT>(kc, (size_t)tt * kv_dim + hoff + 4 * (lane % E4), kst) : float4{0.f, 0.f, 0.f, 0.f};
+    }
 #pragma unroll
-        for (int j = 0; j < PPW; j++) {
-            const int tt = t0 + wave + NW * j;
-            const bool vok = tt < t1 && tt != pos;
-            const float vst = (KVT == KV_I8 && vok) ? vsc[tt] : 1.f;
+    for (int j = 0; j < PPW; j++) {
+        const int tt = t0 + gw + NWG * j;
+        const bool vok = tt < t1 && tt != pos;
+        const float vst = (KVT == KV_I8 && vok) ? vsc[tt] : 1.f;
 #pragma unroll
-            for (int jj = 0; jj < DPL; jj++)
-                vpre[j][jj] = vok ? kv_ld<KVT>(vc, (size_t)tt * kv_dim + hoff + lane + 64 * jj, vst) : 0.f;
-        }
-    };
-    fetch(b0);   // the first tile's reads overlap the rope below
+        for (int jj = 0; jj < DPL; jj++)
+            vpre[j][jj] = vok ? kv_ld<KVT>(vc, (size_t)tt * kv_dim + hoff + lane + 64 * jj, vst) : 0.f;
+    }
     const float* csp = cs + (size_t)pos * HD;
     for (int e = tid; e < GRP * HALF; e += kAttnThreads) {
         const int g = e / HALF, i = e - g * HALF;
@@ -323,10 +324,6 @@ __global__ __launch_bounds__(kAttnThreads) void v5_attn_kernel(
         const float c = csp[2 * i], sn = csp[2 * i + 1], a = qh[i], b = qh[i + HALF];
         qs[g][i] = rope_lo(a, b, c, sn);
         qs[g][i + HALF] = rope_hi(a, b, c, sn);
-    }
-    if (tid < GRP) {
-        gmax[tid] = -INFINITY;
-        gsum[tid] = 0.f;
     }
     if (b0 <= pos && pos < b1) {
         const float* kh = k + hoff;
@@ -407,104 +404,108 @@ __global__ __launch_bounds__(kAttnThreads) void v5_attn_kernel(
     }
 #pragma unroll
     for (int i = 0; i < KI; i++)
-        *(float4*)(ksm + (wave * PPW + i * RPI + lane / E4) * KST + 4 * (lane % E4)) = kld[i];
+        *(float4*)(ksm + (gw * PPW + i * RPI + lane / E4) * KST + 4 * (lane % E4)) = kld[i];
     __syncthreads();
-    float acc[GRP][DPL];
-#pragma unroll
-    for (int g = 0; g < GRP; g++)
-#pragma unroll
-        for (int jj = 0; jj < DPL; jj++) acc[g][jj] = 0.f;
-    for (int t0 = b0; t0 < b1; t0 += kAttnPos) {
-        const int t1 = min(b1, t0 + kAttnPos), np = t1 - t0, t = t0 + lane;
+    // scores: lane = position, wavefront gw = heads gw, gw + 4, ...; the
+    // tile's max and exp-sum per head (a group past T: -inf and 0)
+    if (gw < GRP) {
+        constexpr int HPW = (GRP + NWG - 1) / NWG;
+        const int t = t0 + lane;
         const bool act = t < t1;
-        // this tile's value registers
-        float vt[PPW][DPL];
-#pragma unroll
-        for (int j = 0; j < PPW; j++)
-#pragma unroll
-            for (int jj = 0; jj < DPL; jj++) vt[j][jj] = vpre[j][jj];
         const float* krow = ksm + lane * KST;
-        // scores: lane = position, wavefront = heads w, w + 4, ...; running
-        // max / exp-sum per head kept by its wavefront
-        if (wave < GRP) {
-            constexpr int HPW = (GRP + NW - 1) / NW;
-            float sc[HPW];
+        float sc[HPW];
 #pragma unroll
-            for (int h = 0; h < HPW; h++) sc[h] = 0.f;
-            if (act) {
+        for (int h = 0; h < HPW; h++) sc[h] = 0.f;
+        if (act) {
 #pragma unroll
-                for (int d = 0; d < HD; d += 4) {
-                    float4 kk;
-                    kk = t == pos ? *(const float4*)(kcur + d) : *(const float4*)(krow + d);
+            for (int d = 0; d < HD; d += 4) {
+                const float4 kk = t == pos ? *(const float4*)(kcur + d) : *(const float4*)(krow + d);
 #pragma unroll
-                    for (int h = 0; h < HPW; h++) {
-                        const int g = wave + NW * h;
-                        if (g < GRP) {
-                            const float4 qq = *(const float4*)(&qs[g][d]);
-                            sc[h] = fmaf(qq.x, kk.x, sc[h]);
-                            sc[h] = fmaf(qq.y, kk.y, sc[h]);
-                            sc[h] = fmaf(qq.z, kk.z, sc[h]);
-                            sc[h] = fmaf(qq.w, kk.w, sc[h]);
-                        }
-                    }
-                }
-            }
-#pragma unroll
-            for (int h = 0; h < HPW; h++) {
-                const int g = wave + NW * h;
-                if (g < GRP) {
-                    const float x = act ? sc[h] * scale : -INFINITY;
-                    const float mold = gmax[g];
-                    const float mnew = fmaxf(mold, wave_max_dpp(x));
-                    const float p = act ? __expf(x - mnew) : 0.f;
-                    pr[g][lane] = p;
-                    const float sm = wave_sum_dpp(p);
-                    if (lane == 0) {
-                        const float al = __expf(mold - mnew);   // 0 on the first tile
-                        galpha[g] = al;
-                        gsum[g] = fmaf(gsum[g], al, sm);
-                        gmax[g] = mnew;
+                for (int h = 0; h < HPW; h++) {
+                    const int g = gw + NWG * h;
+                    if (g < GRP) {
+                        const float4 qq = *(const float4*)(&qs[g][d]);
+                        sc[h] = fmaf(qq.x, kk.x, sc[h]);
+                        sc[h] = fmaf(qq.y, kk.y, sc[h]);
+                        sc[h] = fmaf(qq.z, kk.z, sc[h]);
+                        sc[h] = fmaf(qq.w, kk.w, sc[h]);
                     }
                 }
             }
         }
-        __syncthreads();
-        // value sums: lane = dimension(s), wavefront w = positions w, w + 4, ...
 #pragma unroll
-        for (int g = 0; g < GRP; g++) {
-            const float al = galpha[g];
-#pragma unroll
-            for (int jj = 0; jj < DPL; jj++) acc[g][jj] *= al;
+        for (int h = 0; h < HPW; h++) {
+            const int g = gw + NWG * h;
+            if (g < GRP) {
+                const float x = act ? sc[h] * scale : -INFINITY;
+                const float m = wave_max_dpp(x);
+                const float p = act ? __expf(x - m) : 0.f;
+                pr[tg][g][lane] = p;
+                const float sm = wave_sum_dpp(p);
+                if (lane == 0) {
+                    gmx[tg][g] = m;
+                    gsm[tg][g] = sm;
+                }
+            }
         }
+    }
+    __syncthreads();
+    // value sums: lane = dimension(s), wavefront gw = positions gw, gw + 4, ...
+    // (into the group's LDS words: every key read is behind the barrier)
+    {
+        float acc[GRP][DPL];
+#pragma unroll
+        for (int g = 0; g < GRP; g++)
+#pragma unroll
+            for (int jj = 0; jj < DPL; jj++) acc[g][jj] = 0.f;
 #pragma unroll
         for (int j = 0; j < PPW; j++) {
-            const int pi = wave + NW * j;
+            const int pi = gw + NWG * j;
             if (pi < np) {
                 float vv[DPL];
 #pragma unroll
-                for (int jj = 0; jj < DPL; jj++) vv[jj] = t0 + pi == pos ? vcur[lane + 64 * jj] : vt[j][jj];
+                for (int jj = 0; jj < DPL; jj++) vv[jj] = t0 + pi == pos ? vcur[lane + 64 * jj] : vpre[j][jj];
 #pragma unroll
                 for (int g = 0; g < GRP; g++) {
-                    const float p = pr[g][pi];
+                    const float p = pr[tg][g][pi];
 #pragma unroll
                     for (int jj = 0; jj < DPL; jj++) acc[g][jj] = fmaf(p, vv[jj], acc[g][jj]);
                 }
             }
         }
-        __syncthreads();   // pr / galpha are rewritten by the next tile
+        float* vr = ksm + gw * GRP * HD;
+#pragma unroll
+        for (int g = 0; g < GRP; g++)
+#pragma unroll
+            for (int jj = 0; jj < DPL; jj++) vr[g * HD + lane + 64 * jj] = acc[g][jj];
     }
-#pragma unroll
-    for (int g = 0; g < GRP; g++)
-#pragma unroll
-        for (int jj = 0; jj < DPL; jj++) vred[wave][g][lane + 64 * jj] = acc[g][jj];
     __syncthreads();
+    // the block's tiles combined: M = max m_j, L = sum l_j e^(m_j - M),
+    // O[d] = sum_j o_j[d] e^(m_j - M), tiles and wavefronts in order
+    auto combine = [&](int g, int d, float& M, float& L, float& O) {
+        M = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < kAttnGroups; j++) M = fmaxf(M, gmx[j][g]);
+        L = 0.f;
+        O = 0.f;
+#pragma unroll
+        for (int j = 0; j < kAttnGroups; j++) {
+            if (gsm[j][g] > 0.f) {
+                const float w = __expf(gmx[j][g] - M);
+                float o = 0.f;
+#pragma unroll
+                for (int w2 = 0; w2 < NWG; w2++) o += uni[j][(w2 * GRP + g) * HD + d];
+                L = fmaf(gsm[j][g], w, L);
+                O = fmaf(o, w, O);
+            }
+        }
+    };
     if (nact == 1) {   // one split: normalise here
         for (int e = tid; e < GRP * HD; e += kAttnThreads) {
             const int g = e / HD, d = e - g * HD;
-            float a = 0.f;
-#pragma unroll
-            for (int w = 0; w < NW; w++) a += vred[w][g][d];
-            out[(size_t)(kvh * GRP + g) * HD + d] = a / gsum[g];
+            float M, L, O;
+            combine(g, d, M, L, O);
+            out[(size_t)(kvh * GRP + g) * HD + d] = O / L;
         }
         return;
     }
@@ -515,14 +516,13 @@ __global__ __launch_bounds__(kAttnThreads) void v5_attn_kernel(
     float* pp = part + ((size_t)kvh * NS + sp) * GRP * (HD + 2);
     for (int e = tid; e < GRP * HD; e += kAttnThreads) {
         const int g = e / HD, d = e - g * HD;
-        float a = 0.f;
-#pragma unroll
-        for (int w = 0; w < NW; w++) a += vred[w][g][d];
-        __hip_atomic_store(pp + g * (HD + 2) + 2 + d, a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    if (tid < GRP) {
-        __hip_atomic_store(pp + tid * (HD + 2), gmax[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(pp + tid * (HD + 2) + 1, gsum[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        float M, L, O;
+        combine(g, d, M, L, O);
+        __hip_atomic_store(pp + g * (HD + 2) + 2 + d, O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (d == 0) {
+            __hip_atomic_store(pp + g * (HD + 2), M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(pp + g * (HD + 2) + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
     __builtin_amdgcn_s_waitcnt(0x0070);                    // vmcnt(0), lgkmcnt(0)
     __syncthreads();
@@ -1237,7 +1237,7 @@ constexpr int kAttnMaxSplits = 1024;
 bool attn_fused_ok(const ibh_v5_session* s, int max_seq) {
     const int grp = s->n_heads / s->n_kv;
     return (s->head_dim == 64 || s->head_dim == 128) && (grp == 1 || grp == 2 || grp == 4 || grp == 8) &&
-           (max_seq + kAttnPos * kAttnTiles - 1) / (kAttnPos * kAttnTiles) <= kAttnMaxSplits && !getenv("IBH_V5_SPLIT_ATTN");
+           (max_seq + kAttnSpan - 1) / kAttnSpan <= kAttnMaxSplits && !getenv("IBH_V5_SPLIT_ATTN");
 }
 
 int launch_attn_fused(ibh_v5_session* s, ibh_v5_kv* kv, const float* q, const float* k, const float* v, int layer) {
@@ -1615,7 +1615,7 @@ extern "C" int ibh_v5_kv_create(ibh_v5_session* s, int max_seq, ibh_v5_kv** out)
               hipMalloc((void**)&kv->tokens, (size_t)max_seq * 4 + 4) == hipSuccess &&
               hipMalloc((void**)&kv->outs, (size_t)max_seq * 4 + 8) == hipSuccess;
     if (ok && attn_fused_ok(s, max_seq)) {
-        kv->ns = (max_seq + kAttnPos * kAttnTiles - 1) / (kAttnPos * kAttnTiles);
+        kv->ns = (max_seq + kAttnSpan - 1) / kAttnSpan;
         const size_t pb = (size_t)s->n_kv * kv->ns * (s->n_heads / s->n_kv) * (s->head_dim + 2) * 4;
         ok = hipMalloc((void**)&kv->apart, pb) == hipSuccess && hipMalloc((void**)&kv->acnt, 4 * s->n_kv) == hipSuccess &&
              hipMemset(kv->acnt, 0, 4 * s->n_kv) == hipSuccess;
