@@ -341,7 +341,8 @@ def prefill_gemm_case(torch, L, steps, warmup):
     flops = 2.0 * B * M * N
     return {"M": M, "N": N, "B": B, "us": round(t * 1e6, 2), "TFLOPs_algorithmic": round(flops / t / 1e12, 1),
             "TOPs_int8_executed": round(3 * flops / t / 1e12, 1),
-            "frac_int8_mfma_peak": round(3 * flops / t / 1e12 / 5000.0, 4)}
+            "frac_int8_mfma_peak": round(3 * flops / t / 1e12 / 5000.0, 4),
+            "frac_int8_peak_algorithmic": round(flops / t / 1e12 / 5000.0, 4)}
 
 
 def decode_bytes_per_token(cfg, bits, n_pos):
